@@ -1,0 +1,165 @@
+#pragma once
+#ifndef JIMOTONO_HIP_MOE_H
+#define JIMOTONO_HIP_MOE_H
+/*
+ * Device-resident quantised MoE path for the AMD Instinct MI355X (gfx950).
+ *
+ * This header has no single counterpart in the reference: it is the
+ * prepared-weight, HBM-resident form of the reference's quantised MoE
+ * forward (src/moe_layer.c:980-1614 with the W8A8 helpers
+ * src/moe_layer.c:164-274 and the low-bit driver src/lowbit.c:158-267).
+ * The host-pointer prototypes in w8a8.h / lowbit.h / moe_layer.h are the
+ * drop-in; this API is what a caller that keeps activations on the GPU uses.
+ *
+ * All pointers named d* are device (HBM) pointers; `stream` is a hipStream_t
+ * passed as void* (NULL = the library's own stream). Calls are asynchronous
+ * on that stream. Arguments are validated on the host before anything is
+ * enqueued (JT_ERR_INVAL, nothing written). Data-dependent failures found by
+ * the kernels (a non-finite activation, an overflowing epilogue) raise bits in
+ * a per-stream device error word instead of a partial result being trusted;
+ * jt_hip_sync_errors() waits for the stream and returns them.
+ *
+ * Formats of a prepared layer (built on the GPU from fp32 weights):
+ *  - shared experts: int8 codes, one fp32 scale per output channel (the
+ *    reference's jt_w8a8_quant_per_channel formula), gate/up rows interleaved
+ *    in blocks of 16 so a SwiGLU pair lands in one wavefront;
+ *  - routed experts: gate/up INT2 and down INT4 level codes li (the
+ *    reference's odd-symmetric grid, src/lowbit.c:42-45, 77-88) with one
+ *    fp16 scale maxabs_g/(2^bits-1) per `group` (64) weights along K;
+ *  - weights are stored in 16-channel x 64-K panels whose byte order equals
+ *    the operand layout of v_mfma_i32_16x16x64_i8, so a panel is one
+ *    coalesced 1 KiB (int8), 512 B (INT4) or 256 B (INT2) wavefront load.
+ * Activations are quantised per token (one fp32 scale per row).
+ */
+#include <stddef.h>
+#include <stdint.h>
+
+#include "jimotono/common.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- runtime ---- */
+
+/* Bind the calling thread's HIP device (idempotent; called implicitly by
+ * every other entry point with device 0). */
+int jt_hip_init(int device);
+/* Wait for `stream`, then read and clear its device error word.
+ * *out_flags gets the raised JT_HIP_EF_* bits (0 = clean). Returns JT_OK, or
+ * JT_ERR_IO on a HIP failure. */
+int jt_hip_sync_errors(void *stream, uint32_t *out_flags);
+
+#define JT_HIP_EF_NONFINITE_INPUT 0x1u /* NaN/Inf in an activation row */
+#define JT_HIP_EF_RANGE 0x2u           /* epilogue value overflowed fp32 */
+#define JT_HIP_EF_NONFINITE_MID 0x4u   /* non-finite SwiGLU / logits / Y */
+#define JT_HIP_EF_BAD_ID 0x8u          /* routed expert id out of range */
+
+/* ---- per-token activation quantisation ----
+ * dX [rows][cols] fp32 -> dXq [rows][cols] int8, dscale [rows] fp32, same
+ * formula as jt_w8a8_quant_per_channel (reference src/w8a8.c:812-851). */
+int jt_hip_quant_rows(const float *dX, int rows, int cols, int8_t *dXq,
+                      float *dscale, void *stream);
+
+/* ---- W8A8 GEMM with prepared weights ---- */
+typedef struct jt_hip_w8a8 jt_hip_w8a8;
+/* Quantise dW [N][K] fp32 per output row on the GPU and pack it. */
+int jt_hip_w8a8_prepare(const float *dW, int N, int K, jt_hip_w8a8 **out);
+/* Pack already-quantised codes given in the reference layout dBq [K][N]
+ * with column scales dsB [N] (no requantisation). */
+int jt_hip_w8a8_prepare_kn(const int8_t *dBq, const float *dsB, int N, int K,
+                           jt_hip_w8a8 **out);
+/* dC [M][N] = (float)((double)acc * ((double)dsA[m] * (double)sB[n])),
+ * acc = sum_k dAq[m][k] * B[n][k] in int32. M <= 16 uses the streaming GEMV
+ * kernel, larger M the MFMA kernel; both give identical bits. */
+int jt_hip_w8a8_gemm(const jt_hip_w8a8 *W, const int8_t *dAq,
+                     const float *dsA, float *dC, int M, void *stream);
+/* Copy out the quantised weights in the reference layout: Bq [K][N] int8
+ * and sB [N] fp32 (host pointers; for tests). */
+int jt_hip_w8a8_export(const jt_hip_w8a8 *W, int8_t *Bq_kn, float *sB);
+void jt_hip_w8a8_free(jt_hip_w8a8 *W);
+
+/* ---- one W8A8 SwiGLU expert (the shared-expert block) ----
+ * dWg, dWu [h][n], dWd [h][n] (reference shared-expert layout,
+ * moe_layer.h:59-61): Y = down(silu(X Wg^T) * (X Wu^T)) with per-token
+ * int8 activations on both GEMMs. */
+typedef struct jt_hip_ffn jt_hip_ffn;
+int jt_hip_ffn_prepare(const float *dWg, const float *dWu, const float *dWd,
+                       int n, int h, jt_hip_ffn **out);
+/* dY [T][n] = the expert output for dX [T][n] (fp32). */
+int jt_hip_ffn_fwd(jt_hip_ffn *F, const float *dX, float *dY, int T,
+                   void *stream);
+void jt_hip_ffn_free(jt_hip_ffn *F);
+
+/* ---- quantised MoE layer ---- */
+typedef struct jt_hip_moe_desc {
+    int n;          /* model width: K of gate/up, N of down */
+    int h;          /* routed expert hidden width */
+    int n_experts;  /* routed experts E (1..JT_MOE_MAX_EXPERTS) */
+    int topk;       /* k (1..min(E, 64)) */
+    int n_shared;   /* shared experts S (0..8) */
+    int h_shared;   /* shared expert hidden width (the reference ties it to h) */
+    int group;      /* low-bit scale group along K: 64 */
+    int max_tokens; /* largest T a forward may be called with */
+} jt_hip_moe_desc;
+
+typedef struct jt_hip_moe jt_hip_moe;
+
+/* Build a layer from fp32 device weights in the reference layouts:
+ * dWgate [E][n]; dWg, dWu, dWd [E][h][n]; dWg_s, dWu_s, dWd_s
+ * [S][h_shared][n] (NULL when S == 0). dWgate may be NULL for a layer that is
+ * only driven through jt_hip_moe_fwd_routed. */
+int jt_hip_moe_prepare(const jt_hip_moe_desc *desc, const float *dWgate,
+                       const float *dWg, const float *dWu, const float *dWd,
+                       const float *dWg_s, const float *dWu_s,
+                       const float *dWd_s, jt_hip_moe **out);
+
+/* Full forward: fp64 gate logits, top-k softmax, dropless expert sort,
+ * routed INT2/INT4 grouped GEMMs, shared W8A8 experts, fp64 combine.
+ * dX, dY [T][n] fp32, T <= max_tokens. */
+int jt_hip_moe_fwd(jt_hip_moe *L, const float *dX, float *dY, int T,
+                   void *stream);
+
+/* Forward with caller-supplied routing: d_ids [T][k] int32 (distinct per
+ * token, < E) and d_weights [T][k] fp32 replace the router. */
+int jt_hip_moe_fwd_routed(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
+                          const float *d_weights, float *dY, int T,
+                          void *stream);
+
+/* Device buffers of the last forward, for inspection. */
+enum jt_hip_moe_buf {
+    JT_HIP_BUF_IDS = 0,     /* int32 [T][k] */
+    JT_HIP_BUF_WEIGHTS = 1, /* fp32 [T][k] */
+    JT_HIP_BUF_PERM = 2,    /* int32 [T*k], flattened q grouped by expert */
+    JT_HIP_BUF_OFF = 3,     /* int32 [E+1] */
+    JT_HIP_BUF_XQ = 4,      /* int8 [T][n] */
+    JT_HIP_BUF_XSCALE = 5,  /* fp32 [T] */
+    JT_HIP_BUF_YE = 6,      /* fp32 [T*k][n], routed expert output per pair */
+    JT_HIP_BUF_YS = 7,      /* fp32 [S][T][n], shared expert outputs */
+    JT_HIP_BUF_LOGITS = 8,  /* fp32 [T][E] */
+};
+int jt_hip_moe_buffer(const jt_hip_moe *L, int which, void **dptr,
+                      size_t *bytes);
+
+/* Quantised routed weights of expert e in plain layouts (host pointers):
+ * gate/up codes li [2][h][n] uint8 and fp16 scales [2][h][n/group] (uint16
+ * bits); down codes [n][h] uint8 and scales [n][h/group]. */
+int jt_hip_moe_export_routed(const jt_hip_moe *L, int e, uint8_t *gu_codes,
+                             uint16_t *gu_scales, uint8_t *d_codes,
+                             uint16_t *d_scales);
+
+/* Per-stage device time of the most recent forwards, recorded with HIP
+ * events on the forward's stream while profiling is on. */
+int jt_hip_moe_set_profiling(jt_hip_moe *L, int on);
+/* Fills names[i] (static strings) and total milliseconds ms[i] summed over
+ * the profiled forwards since the last reset, plus the number of forwards in
+ * *count; returns the number of stages in *n (at most cap). */
+int jt_hip_moe_stage_times(jt_hip_moe *L, const char **names, double *ms,
+                           int cap, int *n, int *count);
+void jt_hip_moe_free(jt_hip_moe *L);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* JIMOTONO_HIP_MOE_H */
