@@ -1,0 +1,372 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantised MoE layer on one MI355X.
+
+Workload (the metric's configuration, "MoE-layer tokens/s"): full MoE layer
+forward, prefill, T=4096 tokens of fp32 N(0,1) hidden states, d_model=1024,
+router [1024 -> 256] with softmax top-8, 2 shared INT8 SwiGLU experts
+(ffn 2816) and 256 routed experts (ffn 256) with INT2 gate/up and INT4
+down weights, fp16 group-64 scales, dropless expert sort, fp64 combine.
+Weights are random (seeded), data synthetic. A step is one layer forward.
+
+The JSON line carries, beside the contract fields:
+  roofline     -- the dominant kernel's achieved rate from HIP events on the
+                  forward's stream (algorithmic ops per launch / average
+                  launch time) against MI355X's dense int8 MFMA peak;
+  cpu_baseline -- the reference CPU kernels (oracle/_ref, built from the
+                  reference sources) timed on a bounded token sample on this
+                  host, or the oracle restatement when _ref is absent;
+  sub          -- the other BASELINE shapes: W8A8 GEMM 64x1024x1024,
+                  shared-expert decode M in {1,4,16}, routed decode T=16,
+                  and the E=512 stress grouped GEMM.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+INT8_PEAK = 5.0e15  # MI355X dense int8 MFMA, ops/s
+HBM_PEAK = 8.0e12   # bytes/s
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-sub", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=15.0)
+    return p.parse_args()
+
+
+def make_layer(torch, api, n, h, E, k, S, hs, T, seed, router=True):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    rn = lambda *s: torch.randn(*s, generator=g, device="cuda", dtype=torch.float32)  # noqa
+    W = dict(Wgate=rn(E, n) / n ** 0.5 if router else None,
+             Wg=rn(E, h, n) / n ** 0.5, Wu=rn(E, h, n) / n ** 0.5, Wd=rn(E, h, n) / h ** 0.5)
+    if S:
+        W.update(Wg_s=rn(S, hs, n) / n ** 0.5, Wu_s=rn(S, hs, n) / n ** 0.5,
+                 Wd_s=rn(S, hs, n) / hs ** 0.5)
+    else:
+        W.update(Wg_s=None, Wu_s=None, Wd_s=None)
+    L = api.MoE(n, h, E, k, S, hs, T, W["Wgate"], W["Wg"], W["Wu"], W["Wd"], W["Wg_s"],
+                W["Wu_s"], W["Wd_s"])
+    return L, W
+
+
+def time_fn(torch, fn, steps, warmup, stream):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    return wall, e0.elapsed_time(e1) / steps
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path "
+              "(see the sharding notes in DESIGN.md); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    import jimotono_amd.api as api
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    torch.cuda.set_device(0)
+    assert api.lib().jt_hip_init(0) == 0
+    # a dedicated stream: the library treats a NULL stream as its own stream,
+    # so torch's default stream (handle 0) cannot carry the timing events
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
+
+    # ---------------- main workload: full layer prefill ----------------
+    n, h, E, k, S, hs, T = 1024, 256, 256, 8, 2, 2816, 4096
+    L, W = make_layer(torch, api, n, h, E, k, S, hs, T, seed=1234)
+    g = torch.Generator(device="cuda").manual_seed(99)
+    X = torch.randn(T, n, generator=g, device="cuda", dtype=torch.float32)
+    Y = torch.empty(T, n, device="cuda", dtype=torch.float32)
+
+    def step():
+        rc = L.fwd(X, Y, stream)
+        if rc != 0:
+            raise RuntimeError(f"jt_hip_moe_fwd rc={rc}")
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    assert api.sync_errors(stream) == 0
+    L.set_profiling(True)
+    stage_before, _ = L.stage_times()  # reset
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    ev_ms = e0.elapsed_time(e1) / args.steps
+    stages, count = L.stage_times()
+    L.set_profiling(False)
+    assert api.sync_errors(stream) == 0
+    ms_per_step = wall_ms
+    tokens_per_s = T / (ms_per_step / 1e3)
+
+    # algorithmic work per stage launch
+    ops = {
+        "shared_gateup": 2.0 * T * (2 * hs) * n,   # per shared expert launch
+        "shared_down": 2.0 * T * n * hs,
+        "routed_gateup": 2.0 * T * k * (2 * h) * n,
+        "routed_down": 2.0 * T * k * n * h,
+    }
+    launches = {"shared_gateup": S, "shared_down": S, "routed_gateup": 1, "routed_down": 1}
+    per_launch = {s: stages[s] / (count * launches.get(s, 1)) for s in stages}
+    dom = max(ops, key=lambda s: stages[s])
+    dom_ms = per_launch[dom]
+    achieved = ops[dom] / (dom_ms / 1e3)
+    total_ops = 2.0 * T * (S * (2 * hs * n + n * hs) + k * (2 * h * n + n * h))
+    roofline = {"bound": "mfma", "kernel": dom, "achieved": achieved / 1e12,
+                "peak": INT8_PEAK / 1e12, "unit": "TFLOP/s",
+                "frac": achieved / INT8_PEAK, "traffic": None,
+                "ops_per_launch": ops[dom], "avg_launch_ms": dom_ms}
+
+    out = {
+        "metric": "MoE-layer tokens/s; int8 TOPS (prefill) and HBM GB/s (decode) vs roofline",
+        "value": tokens_per_s, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic (seeded N(0,1) activations, random-init weights)",
+        "config": {"workload": "moe_layer_prefill", "tokens": T, "d_model": n,
+                   "routed_experts": E, "expert_ffn": h, "topk": k, "shared_experts": S,
+                   "shared_ffn": hs, "routed_quant": "INT2 gate/up, INT4 down, fp16 g64",
+                   "shared_quant": "W8A8 per-channel", "router": "fp64 top-8",
+                   "parallelism": "single GPU"},
+        "roofline": roofline,
+        "layer_int8_tops": total_ops / (ms_per_step / 1e3) / 1e12,
+        "layer_mfma_frac": total_ops / (ms_per_step / 1e3) / INT8_PEAK,
+        "event_ms_per_step": ev_ms,
+        "stages_ms_per_step": {s: v / count for s, v in stages.items()},
+    }
+
+    # ---------------- CPU baseline ----------------
+    if not args.no_cpu_baseline:
+        try:
+            out["cpu_baseline"] = cpu_baseline(np, torch, W, X, n, h, E, k, S, hs,
+                                               args.cpu_seconds)
+        except Exception as ex:  # reported, never fatal
+            out["cpu_baseline"] = {"error": repr(ex)}
+    del L
+    torch.cuda.empty_cache()
+
+    if not args.no_sub:
+        out["sub"] = sub_benchmarks(np, torch, api, stream)
+    print(json.dumps(out), flush=True)
+
+
+def cpu_baseline(np, torch, W, X, n, h, E, k, S, hs, seconds):
+    """Reference CPU path on a bounded token sample, single core.
+
+    Routed experts: jt_lowbit_gemm_lut (gate/up bits 2, down bits 4) per
+    touched expert on the dropless permutation of the sample; shared experts:
+    jt_w8a8_quant_per_channel of the token rows then jt_w8a8_gemm_per_channel
+    row by row (one activation scale per call); routing: the reference's
+    jt_routing_topk on the layer's own logits. Sample grows until `seconds`.
+    """
+    from oracle.pyoracle import RefLib, ref_available
+    Xh = X[:256].cpu().numpy()
+    Wg = W["Wg"].cpu().numpy()
+    Wu = W["Wu"].cpu().numpy()
+    Wd = W["Wd"].cpu().numpy()
+    Wgate = W["Wgate"].cpu().numpy()
+    Wgs, Wus, Wds = (W[x].cpu().numpy() for x in ("Wg_s", "Wu_s", "Wd_s"))
+    if not ref_available():
+        return cpu_baseline_port(np, Xh, Wgate, Wg, Wu, Wd, Wgs, Wus, Wds, n, h, E, k, S, hs,
+                                 seconds)
+    R = RefLib()
+    # weights pre-transposed the way the reference driver hands them to
+    # jt_lowbit_gemm_lut (src/moe_layer.c:1302-1331): gate/up [n][h]
+    WgT = np.ascontiguousarray(np.transpose(Wg, (0, 2, 1)))
+    WuT = np.ascontiguousarray(np.transpose(Wu, (0, 2, 1)))
+    # shared experts: weights quantised once per output channel, laid out as
+    # the reference's B[K][N] (src/moe_layer.c:164-274 quantises per call;
+    # that cost is left out here in the CPU's favour)
+    shared = []
+    for sidx in range(S):
+        _, qg, sg = R.quant_rows(np.ascontiguousarray(Wgs[sidx]))
+        _, qu, su = R.quant_rows(np.ascontiguousarray(Wus[sidx]))
+        _, qd, sdn = R.quant_rows(np.ascontiguousarray(Wds[sidx].T))
+        shared.append((np.ascontiguousarray(qg.T), sg, np.ascontiguousarray(qu.T), su,
+                       np.ascontiguousarray(qd.T), sdn))
+
+    def run(tok):
+        Xs = Xh[:tok]
+        logits = (Xs.astype(np.float64) @ Wgate.T.astype(np.float64)).astype(np.float32)
+        ids = np.zeros((tok, k), np.int64)
+        for t in range(tok):
+            _, ids[t], _ = R.topk(logits[t], k)
+        for e in np.unique(ids):
+            rows = np.nonzero((ids == e).any(axis=1))[0]
+            Xe = np.ascontiguousarray(Xs[rows])
+            _, G = R.lowbit_gemm_lut(Xe, WgT[e], 2)
+            _, U = R.lowbit_gemm_lut(Xe, WuT[e], 2)
+            Sg = (G / (1 + np.exp(-G.astype(np.float64))) * U).astype(np.float32)
+            R.lowbit_gemm_lut(Sg, Wd[e], 4)
+        _, Xq, sx = R.quant_rows(Xs)
+        for Bg, sg, Bu, su, Bd, sdn in shared:
+            Ss = np.zeros((tok, hs), np.float32)
+            for t in range(tok):
+                _, G = R.gemm_per_channel(Xq[t:t + 1], Bg, sx[t], sg)
+                _, U = R.gemm_per_channel(Xq[t:t + 1], Bu, sx[t], su)
+                Ss[t] = (G / (1 + np.exp(-G.astype(np.float64))) * U)[0]
+            _, Sq, ss = R.quant_rows(Ss)
+            for t in range(tok):
+                R.gemm_per_channel(Sq[t:t + 1], Bd, ss[t], sdn)
+
+    tok, el = 2, 0.0
+    while True:
+        t0 = time.perf_counter()
+        run(tok)
+        el = time.perf_counter() - t0
+        if el >= seconds or tok >= 256:
+            break
+        tok = min(256, max(tok * 2, int(tok * seconds / max(el, 1e-3) * 0.9)))
+    return {"value": tok / el, "unit": "tokens/s", "cores": 1, "kind": "reference",
+            "sample": f"{tok} tokens of the same layer (routed: reference "
+                      "jt_lowbit_gemm_lut T-MAC per touched expert; shared: reference "
+                      "W8A8 quant + gemm_per_channel per token row; top-k: reference "
+                      f"jt_routing_topk), {el:.1f} s single-threaded",
+            "seconds": el}
+
+
+def cpu_baseline_port(np, Xh, Wgate, Wg, Wu, Wd, Wgs, Wus, Wds, n, h, E, k, S, hs, seconds):
+    from oracle.pyoracle import Oracle
+    O = Oracle()
+    OL = O.moe_q(n, h, E, k, S, hs, Wgate, Wg, Wu, Wd, Wgs, Wus, Wds)
+    tok, el = 2, 0.0
+    while True:
+        t0 = time.perf_counter()
+        OL.fwd(Xh[:tok])
+        el = time.perf_counter() - t0
+        if el >= seconds or tok >= 256:
+            break
+        tok = min(256, max(tok * 2, int(tok * seconds / max(el, 1e-3) * 0.9)))
+    return {"value": tok / el, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"{tok} tokens of the same layer through the oracle's C "
+                      f"restatement, {el:.1f} s single-threaded", "seconds": el}
+
+
+def sub_benchmarks(np, torch, api, stream):
+    res = {}
+    # --- W8A8 GEMM 64x1024x1024 (per-row activation scales) ---
+    M, N, K = 64, 1024, 1024
+    g = torch.Generator(device="cuda").manual_seed(5)
+    Bq = torch.randint(-127, 128, (K, N), generator=g, device="cuda", dtype=torch.int8)
+    sB = torch.rand(N, generator=g, device="cuda") * 9e-3 + 1e-3
+    Wq = api.W8A8(Bq_kn=Bq, sB=sB)
+    Aq = torch.randint(-127, 128, (M, K), generator=g, device="cuda", dtype=torch.int8)
+    sA = torch.rand(M, generator=g, device="cuda") * 9e-3 + 1e-3
+    Cc = torch.empty(M, N, device="cuda")
+    _, ev = time_fn(torch, lambda: Wq.gemm(Aq, sA, Cc, stream), 200, 20, stream)
+    res["w8a8_gemm_64x1024x1024"] = {"us_per_call": ev * 1e3,
+                                     "tops": 2 * M * N * K / (ev / 1e3) / 1e12,
+                                     "gbps": (M * K + N * K + 4 * (M + N) + 4 * M * N)
+                                     / (ev / 1e3) / 1e9}
+    del Wq
+    # --- shared-expert decode, M in {1,4,16}; 40 rotating weight copies
+    # (> 256 MB MALL) so every call streams its weights from HBM ---
+    n, hs = 1024, 2816
+    copies = 40
+    Fs = []
+    for c in range(copies):
+        gw = torch.Generator(device="cuda").manual_seed(100 + c)
+        Fs.append(api.FFN(torch.randn(hs, n, generator=gw, device="cuda") / 32,
+                          torch.randn(hs, n, generator=gw, device="cuda") / 32,
+                          torch.randn(hs, n, generator=gw, device="cuda") / 53))
+    wbytes = 3 * hs * n + 4 * (2 * hs + n)
+    for m in (1, 4, 16):
+        Xd = torch.randn(m, n, device="cuda")
+        Yd = torch.empty(m, n, device="cuda")
+        it = [0]
+
+        def fstep():
+            Fs[it[0] % copies].fwd(Xd, Yd, stream)
+            it[0] += 1
+        _, ev = time_fn(torch, fstep, 4 * copies, copies, stream)
+        res[f"shared_decode_M{m}"] = {"us_per_expert": ev * 1e3,
+                                      "gbps": (wbytes + 8 * m * n) / (ev / 1e3) / 1e9,
+                                      "hbm_frac": (wbytes + 8 * m * n) / (ev / 1e3) / HBM_PEAK}
+    del Fs
+    torch.cuda.empty_cache()
+    # --- routed decode: T=16, E=256, d=1024, f=256, k=8, Zipf(1.1) ---
+    n, h, E, k, T = 1024, 256, 256, 8, 16
+    rng = np.random.default_rng(16)
+    p = 1.0 / np.arange(1, E + 1) ** 1.1
+    p /= p.sum()
+    ids = np.stack([rng.choice(E, k, replace=False, p=p) for _ in range(T)]).astype(np.int32)
+    w = rng.uniform(0, 1, (T, k)).astype(np.float32)
+    w /= w.sum(1, keepdims=True)
+    touched = len(np.unique(ids))
+    layers = []
+    for c in range(8):  # 8 layers x 73 MB of routed weights rotate past the MALL
+        Lr, _ = make_layer(torch, api, n, h, E, k, 0, 0, T, seed=500 + c, router=False)
+        layers.append(Lr)
+    dids = torch.from_numpy(ids).cuda()
+    dw = torch.from_numpy(w).cuda()
+    Xr = torch.randn(T, n, device="cuda")
+    Yr = torch.empty(T, n, device="cuda")
+    it = [0]
+
+    def rstep():
+        rc = layers[it[0] % len(layers)].fwd_routed(Xr, dids, dw, Yr, stream)
+        assert rc == 0
+        it[0] += 1
+    _, ev = time_fn(torch, rstep, 40, 8, stream)
+    rbytes = touched * (2 * h * n // 4 + n * h // 2 + 2 * (2 * h * n // 64 + n * h // 64))
+    res["routed_decode_T16"] = {"us_per_layer": ev * 1e3, "touched_experts": touched,
+                                "weight_bytes": rbytes,
+                                "gbps": rbytes / (ev / 1e3) / 1e9,
+                                "hbm_frac": rbytes / (ev / 1e3) / HBM_PEAK}
+    del layers
+    torch.cuda.empty_cache()
+    # --- stress prefill: T=16384, d=2048, E=512, f=512, k=8, Zipf(1.1) ---
+    n, h, E, k, T = 2048, 512, 512, 8, 16384
+    ids = np.stack([rng.choice(E, k, replace=False, p=(1.0 / np.arange(1, E + 1) ** 1.1)
+                               / (1.0 / np.arange(1, E + 1) ** 1.1).sum())
+                    for _ in range(T)]).astype(np.int32)
+    w = rng.uniform(0, 1, (T, k)).astype(np.float32)
+    w /= w.sum(1, keepdims=True)
+    Ls, _ = make_layer(torch, api, n, h, E, k, 0, 0, T, seed=777, router=False)
+    dids = torch.from_numpy(ids).cuda()
+    dw = torch.from_numpy(w).cuda()
+    Xs = torch.randn(T, n, device="cuda")
+    Ys = torch.empty(T, n, device="cuda")
+    Ls.set_profiling(True)
+    Ls.stage_times()
+    _, ev = time_fn(torch, lambda: Ls.fwd_routed(Xs, dids, dw, Ys, stream), 5, 2, stream)
+    st, cnt = Ls.stage_times()
+    Ls.set_profiling(False)
+    gops = 2.0 * T * k * (2 * h * n + n * h)
+    gemm_ms = (st["routed_gateup"] + st["routed_down"]) / cnt
+    res["stress_prefill_E512"] = {"ms_per_layer": ev, "grouped_gemm_ms": gemm_ms,
+                                  "grouped_gemm_tops": gops / (gemm_ms / 1e3) / 1e12,
+                                  "mfma_frac": gops / (gemm_ms / 1e3) / INT8_PEAK,
+                                  "stages_ms": {s: v / cnt for s, v in st.items()}}
+    return res
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,542 @@
+/*
+ * hip_moe.c -- device-resident quantised MoE layer and W8A8 SwiGLU expert
+ * (C11 host orchestration of the gfx950 kernels).
+ *
+ * Forward of the layer (jimotono/hip_moe.h), all on one stream:
+ *   1 quant_x        per-token int8 activations            (src/w8a8.c:787-855)
+ *   2 router         fp64 gate logits, lane order          (src/moe_layer.c:67-86)
+ *   3 topk           top-k + softmax                       (src/routing.c:16-76)
+ *   4 sort           dropless stable expert sort           (src/moe_layer.c:895-978)
+ *   5 tiles          64-row work list of the sorted pairs
+ *   6 routed_gateup  INT2 grouped GEMM + SwiGLU            (src/moe_layer.c:1301-1365)
+ *   7 routed_quant   per-row int8 requantisation of SwiGLU output
+ *   8 routed_down    INT4 grouped GEMM, rows scattered to their (token, slot)
+ *   9 shared_gateup  W8A8 GEMM + SwiGLU per shared expert  (src/moe_layer.c:1468-1540)
+ *  10 shared_quant
+ *  11 shared_down
+ *  12 combine        fp64 weighted sum, slot then shared order
+ *                                                          (src/moe_layer.c:1443-1574)
+ */
+#include <errno.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "jimotono/hip_moe.h"
+#include "jimotono/moe_layer.h"
+#include "jt_rt.h"
+
+#define FAIL(code, e) \
+    do {              \
+        errno = (e);  \
+        return (code); \
+    } while (0)
+
+/* ======================= W8A8 SwiGLU expert ======================= */
+
+struct jt_hip_ffn {
+    int n, h, Kpn, Kph, Np_gu, Np_d;
+    int8_t *gu_P; /* gate/up interleaved panels, N = 2h */
+    float *gu_s;
+    int8_t *d_P; /* down panels, N = n, K = h */
+    float *d_s;
+    /* workspace */
+    int cap_T;
+    int8_t *Xq;
+    float *sx;
+    float *S;
+    int8_t *Sq;
+    float *ss;
+};
+
+void jt_hip_ffn_free(jt_hip_ffn *F) {
+    if (!F) return;
+    void *p[] = {F->gu_P, F->gu_s, F->d_P, F->d_s, F->Xq, F->sx, F->S, F->Sq, F->ss};
+    for (size_t i = 0; i < sizeof(p) / sizeof(p[0]); i++) (void)hipFree(p[i]);
+    free(F);
+}
+
+static int ffn_prepare_on(jt_rt *rt, const float *dWg, const float *dWu, const float *dWd,
+                          int n, int h, jt_hip_ffn **out) {
+    jt_hip_ffn *F = calloc(1, sizeof(*F));
+    if (!F) FAIL(JT_ERR_NOMEM, ENOMEM);
+    F->n = n;
+    F->h = h;
+    F->Kpn = (int)jt_round_up((size_t)n, 64);
+    F->Kph = (int)jt_round_up((size_t)h, 64);
+    F->Np_gu = (int)jt_round_up((size_t)2 * h, 128);
+    F->Np_d = (int)jt_round_up((size_t)n, 128);
+    int8_t *qg = NULL, *qu = NULL, *qgu = NULL, *qd = NULL;
+    float *sg = NULL, *su = NULL;
+    hipError_t e = hipSuccess;
+#define ALLOC(p, bytes) \
+    if (e == hipSuccess) e = hipMalloc((void **)&(p), (size_t)(bytes))
+    ALLOC(F->gu_P, (size_t)F->Np_gu * F->Kpn);
+    ALLOC(F->gu_s, (size_t)F->Np_gu * sizeof(float));
+    ALLOC(F->d_P, (size_t)F->Np_d * F->Kph);
+    ALLOC(F->d_s, (size_t)F->Np_d * sizeof(float));
+    ALLOC(qg, (size_t)h * n);
+    ALLOC(qu, (size_t)h * n);
+    ALLOC(qgu, (size_t)2 * h * n);
+    ALLOC(qd, (size_t)n * h);
+    ALLOC(sg, (size_t)h * sizeof(float));
+    ALLOC(su, (size_t)h * sizeof(float));
+#undef ALLOC
+    if (e == hipSuccess) e = hipMemsetAsync(F->gu_s, 0, (size_t)F->Np_gu * sizeof(float), rt->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(F->d_s, 0, (size_t)F->Np_d * sizeof(float), rt->stream);
+    int rc = jt_rt_err(e);
+    if (rc == JT_OK) {
+        /* gate/up rows are output channels, K = n contiguous */
+        jtk_quant_weight_rows(dWg, n, 1, h, n, qg, sg, rt->d_err, rt->stream);
+        jtk_quant_weight_rows(dWu, n, 1, h, n, qu, su, rt->d_err, rt->stream);
+        jtk_interleave_rows(qg, qu, h, n, qgu, rt->stream);
+        jtk_interleave_rows(sg, su, h, (int64_t)sizeof(float), F->gu_s, rt->stream);
+        jtk_pack_i8(qgu, 2 * h, n, 0, F->Np_gu, F->Kpn, F->gu_P, rt->stream);
+        /* down: Wd [h][n] is B[K=h][N=n]; output channel j is column j */
+        jtk_quant_weight_rows(dWd, 1, n, n, h, qd, F->d_s, rt->d_err, rt->stream);
+        jtk_pack_i8(qd, n, h, 0, F->Np_d, F->Kph, F->d_P, rt->stream);
+        uint32_t f = 0;
+        rc = jt_rt_flags(rt, rt->stream, &f);
+        if (rc == JT_OK) rc = jt_rt_flags_to_rc(f);
+    }
+    (void)hipFree(qg);
+    (void)hipFree(qu);
+    (void)hipFree(qgu);
+    (void)hipFree(qd);
+    (void)hipFree(sg);
+    (void)hipFree(su);
+    if (rc != JT_OK) {
+        jt_hip_ffn_free(F);
+        return rc;
+    }
+    *out = F;
+    return JT_OK;
+}
+
+int jt_hip_ffn_prepare(const float *dWg, const float *dWu, const float *dWd, int n, int h,
+                       jt_hip_ffn **out) {
+    if (!dWg || !dWu || !dWd || !out || n <= 0 || h <= 0 || h % 16 != 0 ||
+        n > JT_BWD_MAX_WIDE || h > JT_BWD_MAX_WIDE)
+        FAIL(JT_ERR_INVAL, EINVAL);
+    jt_rt *rt = jt_rt_get();
+    if (!rt) return JT_ERR_IO;
+    return ffn_prepare_on(rt, dWg, dWu, dWd, n, h, out);
+}
+
+static int ffn_reserve(jt_hip_ffn *F, int T, int with_x) {
+    if (T <= F->cap_T && (!with_x || F->Xq)) return JT_OK;
+    int cap = T > F->cap_T ? T : F->cap_T;
+    (void)hipDeviceSynchronize();
+    void *olds[] = {F->Xq, F->sx, F->S, F->Sq, F->ss};
+    for (size_t i = 0; i < 5; i++) (void)hipFree(olds[i]);
+    F->Xq = NULL;
+    F->sx = NULL;
+    F->S = F->ss = NULL;
+    F->Sq = NULL;
+    hipError_t e = hipSuccess;
+    if (with_x) {
+        e = hipMalloc((void **)&F->Xq, (size_t)cap * F->Kpn);
+        if (e == hipSuccess) e = hipMemset(F->Xq, 0, (size_t)cap * F->Kpn);
+        if (e == hipSuccess) e = hipMalloc((void **)&F->sx, (size_t)cap * sizeof(float));
+    }
+    if (e == hipSuccess) e = hipMalloc((void **)&F->S, (size_t)cap * F->h * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc((void **)&F->Sq, (size_t)cap * F->Kph);
+    if (e == hipSuccess) e = hipMemset(F->Sq, 0, (size_t)cap * F->Kph);
+    if (e == hipSuccess) e = hipMalloc((void **)&F->ss, (size_t)cap * sizeof(float));
+    if (e != hipSuccess) {
+        F->cap_T = 0;
+        return jt_rt_err(e);
+    }
+    F->cap_T = cap;
+    return JT_OK;
+}
+
+/* Expert on already-quantised activations Xq [T][Kpn] (zero K padding). */
+static int ffn_run_q(jt_rt *rt, jt_hip_ffn *F, const int8_t *Xq, const float *sx, int T,
+                     float *dY, hipStream_t s, hipEvent_t *ev) {
+    if (ev) (void)hipEventRecord(ev[0], s);
+    int e = jtk_w8a8_gemm(Xq, F->Kpn, sx, F->gu_P, F->gu_s, T, 2 * F->h, F->Np_gu, F->Kpn,
+                          F->S, F->h, 1, rt->d_err, s);
+    if (ev) (void)hipEventRecord(ev[1], s);
+    e |= jtk_quant_rows(F->S, T, F->h, F->Sq, F->Kph, F->ss, NULL, rt->d_err, s);
+    if (ev) (void)hipEventRecord(ev[2], s);
+    e |= jtk_w8a8_gemm(F->Sq, F->Kph, F->ss, F->d_P, F->d_s, T, F->n, F->Np_d, F->Kph, dY,
+                       F->n, 0, rt->d_err, s);
+    return e ? jt_rt_err(hipErrorLaunchFailure) : JT_OK;
+}
+
+int jt_hip_ffn_fwd(jt_hip_ffn *F, const float *dX, float *dY, int T, void *stream) {
+    if (!F || !dX || !dY || T < 0) FAIL(JT_ERR_INVAL, EINVAL);
+    jt_rt *rt = jt_rt_get();
+    if (!rt) return JT_ERR_IO;
+    if (T == 0) return JT_OK;
+    int rc = ffn_reserve(F, T, 1);
+    if (rc != JT_OK) return rc;
+    hipStream_t s = stream ? (hipStream_t)stream : rt->stream;
+    if (jtk_quant_rows(dX, T, F->n, F->Xq, F->Kpn, F->sx, NULL, rt->d_err, s))
+        return jt_rt_err(hipErrorLaunchFailure);
+    return ffn_run_q(rt, F, F->Xq, F->sx, T, dY, s, NULL);
+}
+
+/* ======================= MoE layer ======================= */
+
+enum {
+    ST_QUANT_X = 0,
+    ST_ROUTER,
+    ST_TOPK,
+    ST_SORT,
+    ST_TILES,
+    ST_R_GATEUP,
+    ST_R_QUANT,
+    ST_R_DOWN,
+    ST_S_GATEUP,
+    ST_S_QUANT,
+    ST_S_DOWN,
+    ST_COMBINE,
+    ST_N
+};
+static const char *const k_stage_names[ST_N] = {
+    "quant_x",       "router_logits", "topk",         "sort",
+    "tiles",         "routed_gateup", "routed_quant", "routed_down",
+    "shared_gateup", "shared_quant",  "shared_down",  "combine"};
+
+#define PROF_RING 16
+
+struct jt_hip_moe {
+    jt_hip_moe_desc d;
+    float *Wgate;
+    uint8_t *gu_P;
+    uint16_t *gu_S;
+    uint8_t *dn_P;
+    uint16_t *dn_S;
+    int64_t gu_pstride, gu_sstride, dn_pstride, dn_sstride;
+    jt_hip_ffn *sh[JT_MOE_MAX_SHARED];
+    /* workspace (max_tokens) */
+    int8_t *Xq;
+    float *sx, *logits, *w, *Sr, *ssr, *Ye, *Ys;
+    int32_t *ids, *rank, *cnt, *tot, *off, *perm, *tiles, *ntiles;
+    int8_t *Sqr;
+    int last_T;
+    /* profiling: ring of per-forward event sets */
+    int prof;
+    hipEvent_t ev[PROF_RING][ST_N + 1 + 3 * JT_MOE_MAX_SHARED];
+    int ev_ready;
+    int ring_head, ring_count;
+    double acc_ms[ST_N];
+    int acc_count;
+};
+
+void jt_hip_moe_free(jt_hip_moe *L) {
+    if (!L) return;
+    void *p[] = {L->Wgate, L->gu_P, L->gu_S, L->dn_P,  L->dn_S, L->Xq,   L->sx,
+                 L->logits, L->w,  L->Sr,   L->ssr,  L->Ye,   L->Ys,   L->ids,
+                 L->rank,  L->cnt, L->tot,  L->off,  L->perm, L->tiles, L->ntiles,
+                 L->Sqr};
+    (void)hipDeviceSynchronize();
+    for (size_t i = 0; i < sizeof(p) / sizeof(p[0]); i++) (void)hipFree(p[i]);
+    for (int s = 0; s < JT_MOE_MAX_SHARED; s++) jt_hip_ffn_free(L->sh[s]);
+    if (L->ev_ready)
+        for (int r = 0; r < PROF_RING; r++)
+            for (int i = 0; i < ST_N + 1 + 3 * JT_MOE_MAX_SHARED; i++)
+                (void)hipEventDestroy(L->ev[r][i]);
+    free(L);
+}
+
+int jt_hip_moe_prepare(const jt_hip_moe_desc *desc, const float *dWgate, const float *dWg,
+                       const float *dWu, const float *dWd, const float *dWg_s,
+                       const float *dWu_s, const float *dWd_s, jt_hip_moe **out) {
+    if (!desc || !dWg || !dWu || !dWd || !out) FAIL(JT_ERR_INVAL, EINVAL);
+    const jt_hip_moe_desc d = *desc;
+    if (d.n <= 0 || d.n % 128 != 0 || d.n > JT_BWD_MAX_WIDE || d.h <= 0 || d.h % 64 != 0 ||
+        d.h > JT_BWD_MAX_WIDE || d.n_experts <= 0 || d.n_experts > JT_MOE_MAX_EXPERTS ||
+        d.topk <= 0 || d.topk > d.n_experts || d.topk > JT_MOE_MAX_TOPK || d.n_shared < 0 ||
+        d.n_shared > JT_MOE_MAX_SHARED || d.group != 64 || d.max_tokens <= 0)
+        FAIL(JT_ERR_INVAL, EINVAL);
+    if (d.n_shared > 0 && (!dWg_s || !dWu_s || !dWd_s || d.h_shared <= 0 ||
+                           d.h_shared % 16 != 0 || d.h_shared > JT_BWD_MAX_WIDE))
+        FAIL(JT_ERR_INVAL, EINVAL);
+    if ((int64_t)d.max_tokens * d.topk > (int64_t)64 * 65535) FAIL(JT_ERR_INVAL, EINVAL);
+    jt_rt *rt = jt_rt_get();
+    if (!rt) return JT_ERR_IO;
+    jt_hip_moe *L = calloc(1, sizeof(*L));
+    if (!L) FAIL(JT_ERR_NOMEM, ENOMEM);
+    L->d = d;
+    const int n = d.n, h = d.h, E = d.n_experts, T = d.max_tokens;
+    const int64_t Tk = (int64_t)T * d.topk;
+    const int NB = (int)((Tk + 255) / 256);
+    L->gu_pstride = (int64_t)(2 * h / 16) * (n / 64) * 256;
+    L->gu_sstride = (int64_t)(2 * h / 16) * (n / 64) * 16;
+    L->dn_pstride = (int64_t)(n / 16) * (h / 64) * 512;
+    L->dn_sstride = (int64_t)(n / 16) * (h / 64) * 16;
+    hipError_t e = hipSuccess;
+#define ALLOC(p, bytes) \
+    if (e == hipSuccess) e = hipMalloc((void **)&(p), (size_t)(bytes))
+    if (dWgate) ALLOC(L->Wgate, (size_t)E * n * sizeof(float));
+    ALLOC(L->gu_P, L->gu_pstride * E);
+    ALLOC(L->gu_S, L->gu_sstride * E * 2);
+    ALLOC(L->dn_P, L->dn_pstride * E);
+    ALLOC(L->dn_S, L->dn_sstride * E * 2);
+    ALLOC(L->Xq, (size_t)T * n);
+    ALLOC(L->sx, (size_t)T * 4);
+    ALLOC(L->logits, (size_t)T * E * 4);
+    ALLOC(L->ids, (size_t)Tk * 4);
+    ALLOC(L->w, (size_t)Tk * 4);
+    ALLOC(L->rank, (size_t)Tk * 4);
+    ALLOC(L->cnt, (size_t)NB * E * 4);
+    ALLOC(L->tot, (size_t)E * 4);
+    ALLOC(L->off, (size_t)(E + 1) * 4);
+    ALLOC(L->perm, (size_t)Tk * 4);
+    ALLOC(L->tiles, (size_t)(Tk / 64 + E + 1) * 4);
+    ALLOC(L->ntiles, 4);
+    ALLOC(L->Sr, (size_t)Tk * h * 4);
+    ALLOC(L->Sqr, (size_t)Tk * h);
+    ALLOC(L->ssr, (size_t)Tk * 4);
+    ALLOC(L->Ye, (size_t)Tk * n * 4);
+    ALLOC(L->Ys, (size_t)(d.n_shared > 0 ? d.n_shared : 1) * T * n * 4);
+#undef ALLOC
+    if (e == hipSuccess && dWgate)
+        e = hipMemcpyAsync(L->Wgate, dWgate, (size_t)E * n * sizeof(float),
+                           hipMemcpyDeviceToDevice, rt->stream);
+    int rc = jt_rt_err(e);
+    if (rc == JT_OK) {
+        jtk_check_finite(dWgate ? L->Wgate : NULL, dWgate ? (int64_t)E * n : 0, rt->d_err,
+                         rt->stream);
+        /* routed gate/up: rows of Wg/Wu [E][h][n] are channels, K = n */
+        jtk_pack_lowbit(dWg, dWu, (int64_t)h * n, n, 1, E, 2 * h, n, 2, L->gu_P, L->gu_S,
+                        NULL, NULL, rt->d_err, rt->stream);
+        /* routed down: Wd [E][h][n] is B[K=h][N=n]; channel j = column j */
+        jtk_pack_lowbit(dWd, NULL, (int64_t)h * n, 1, n, E, n, h, 4, L->dn_P, L->dn_S, NULL,
+                        NULL, rt->d_err, rt->stream);
+        uint32_t f = 0;
+        rc = jt_rt_flags(rt, rt->stream, &f);
+        if (rc == JT_OK) rc = jt_rt_flags_to_rc(f);
+    }
+    const int hs = d.h_shared;
+    for (int s = 0; s < d.n_shared && rc == JT_OK; s++) {
+        const int64_t so = (int64_t)s * hs * n;
+        rc = ffn_prepare_on(rt, dWg_s + so, dWu_s + so, dWd_s + so, n, hs, &L->sh[s]);
+        if (rc == JT_OK) rc = ffn_reserve(L->sh[s], T, 0);
+    }
+    if (rc != JT_OK) {
+        jt_hip_moe_free(L);
+        return rc;
+    }
+    *out = L;
+    return JT_OK;
+}
+
+static void prof_mark(jt_hip_moe *L, int slot, int i, hipStream_t s) {
+    if (L->prof) (void)hipEventRecord(L->ev[slot][i], s);
+}
+
+/* Accumulate the stage times of the oldest recorded forward. Event i < ST_N
+ * marks the start of stage i (ST_N = end of combine); shared expert e has
+ * its own three marks at ST_N + 1 + 3e (gate/up, quant, down). */
+static void prof_drain_one(jt_hip_moe *L) {
+    const int S = L->d.n_shared;
+    const int slot = (L->ring_head - L->ring_count + PROF_RING) % PROF_RING;
+    hipEvent_t *ev = L->ev[slot];
+    (void)hipEventSynchronize(ev[ST_N]);
+    float ms = 0.0f;
+#define ADD(st, a, b) \
+    if (hipEventElapsedTime(&ms, (a), (b)) == hipSuccess) L->acc_ms[st] += ms
+    for (int i = ST_QUANT_X; i < ST_R_DOWN; i++) ADD(i, ev[i], ev[i + 1]);
+    ADD(ST_R_DOWN, ev[ST_R_DOWN], S > 0 ? ev[ST_N + 1] : ev[ST_COMBINE]);
+    for (int e = 0; e < S; e++) {
+        hipEvent_t *x = &ev[ST_N + 1 + 3 * e];
+        hipEvent_t end = (e + 1 < S) ? ev[ST_N + 1 + 3 * (e + 1)] : ev[ST_COMBINE];
+        ADD(ST_S_GATEUP, x[0], x[1]);
+        ADD(ST_S_QUANT, x[1], x[2]);
+        ADD(ST_S_DOWN, x[2], end);
+    }
+    ADD(ST_COMBINE, ev[ST_COMBINE], ev[ST_N]);
+#undef ADD
+    L->acc_count++;
+    L->ring_count--;
+}
+
+static int prof_begin(jt_hip_moe *L, int *slot) {
+    if (!L->prof) return JT_OK;
+    if (!L->ev_ready) {
+        for (int r = 0; r < PROF_RING; r++)
+            for (int i = 0; i < ST_N + 1 + 3 * JT_MOE_MAX_SHARED; i++)
+                if (hipEventCreate(&L->ev[r][i]) != hipSuccess) return JT_ERR_IO;
+        L->ev_ready = 1;
+    }
+    if (L->ring_count == PROF_RING) prof_drain_one(L);
+    *slot = L->ring_head;
+    L->ring_head = (L->ring_head + 1) % PROF_RING;
+    L->ring_count++;
+    return JT_OK;
+}
+
+static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
+                       const float *d_w, float *dY, int T, void *stream) {
+    const jt_hip_moe_desc *d = &L->d;
+    if (!dX || !dY || T < 0 || T > d->max_tokens) FAIL(JT_ERR_INVAL, EINVAL);
+    if (!d_ids && !L->Wgate) FAIL(JT_ERR_INVAL, EINVAL);
+    jt_rt *rt = jt_rt_get();
+    if (!rt) return JT_ERR_IO;
+    if (T == 0) return JT_OK;
+    hipStream_t s = stream ? (hipStream_t)stream : rt->stream;
+    const int n = d->n, h = d->h, E = d->n_experts, k = d->topk, S = d->n_shared;
+    const int Tk = T * k;
+    const int max_tiles = Tk / 64 + E;
+    uint32_t *err = rt->d_err;
+    int slot = 0, rc = prof_begin(L, &slot);
+    if (rc != JT_OK) return rc;
+    int le = 0;
+    L->last_T = T;
+
+    prof_mark(L, slot, ST_QUANT_X, s);
+    le |= jtk_quant_rows(dX, T, n, L->Xq, n, L->sx, NULL, err, s);
+    prof_mark(L, slot, ST_ROUTER, s);
+    if (d_ids) {
+        le |= (int)hipMemcpyAsync(L->ids, d_ids, (size_t)Tk * 4, hipMemcpyDeviceToDevice, s);
+        le |= (int)hipMemcpyAsync(L->w, d_w, (size_t)Tk * 4, hipMemcpyDeviceToDevice, s);
+        prof_mark(L, slot, ST_TOPK, s);
+    } else {
+        le |= jtk_router_logits(dX, L->Wgate, T, E, n, L->logits, err, s);
+        prof_mark(L, slot, ST_TOPK, s);
+        le |= jtk_topk(L->logits, T, E, k, L->ids, NULL, L->w, err, s);
+    }
+    prof_mark(L, slot, ST_SORT, s);
+    le |= jtk_sort(L->ids, Tk, E, (int64_t)Tk, L->rank, L->cnt, L->tot, L->off, NULL, L->perm,
+                   NULL, NULL, err, s);
+    prof_mark(L, slot, ST_TILES, s);
+    le |= jtk_make_tiles(L->off, E, L->tiles, L->ntiles, s);
+    prof_mark(L, slot, ST_R_GATEUP, s);
+    le |= jtk_lowbit_grouped(2, L->Xq, n, L->sx, L->perm, L->off, k, L->tiles, L->ntiles,
+                             max_tiles, L->gu_P, L->gu_S, L->gu_pstride, L->gu_sstride, 2 * h,
+                             n, L->Sr, h, err, s);
+    prof_mark(L, slot, ST_R_QUANT, s);
+    le |= jtk_quant_rows(L->Sr, Tk, h, L->Sqr, h, L->ssr, NULL, err, s);
+    prof_mark(L, slot, ST_R_DOWN, s);
+    le |= jtk_lowbit_grouped(4, L->Sqr, h, L->ssr, L->perm, L->off, k, L->tiles, L->ntiles,
+                             max_tiles, L->dn_P, L->dn_S, L->dn_pstride, L->dn_sstride, n, h,
+                             L->Ye, n, err, s);
+    for (int e = 0; e < S; e++) {
+        hipEvent_t *ev = L->prof ? &L->ev[slot][ST_N + 1 + 3 * e] : NULL;
+        rc = ffn_run_q(rt, L->sh[e], L->Xq, L->sx, T, L->Ys + (size_t)e * T * n, s, ev);
+        if (rc != JT_OK) return rc;
+    }
+    prof_mark(L, slot, ST_COMBINE, s);
+    le |= jtk_combine(L->w, L->Ye, NULL, L->Ys, S, T, k, n, dY, err, s);
+    prof_mark(L, slot, ST_N, s);
+    return le ? jt_rt_err(hipErrorLaunchFailure) : JT_OK;
+}
+
+int jt_hip_moe_fwd(jt_hip_moe *L, const float *dX, float *dY, int T, void *stream) {
+    if (!L) FAIL(JT_ERR_INVAL, EINVAL);
+    return moe_forward(L, dX, NULL, NULL, dY, T, stream);
+}
+
+int jt_hip_moe_fwd_routed(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
+                          const float *d_weights, float *dY, int T, void *stream) {
+    if (!L || !d_ids || !d_weights) FAIL(JT_ERR_INVAL, EINVAL);
+    return moe_forward(L, dX, d_ids, d_weights, dY, T, stream);
+}
+
+int jt_hip_moe_buffer(const jt_hip_moe *L, int which, void **dptr, size_t *bytes) {
+    if (!L || !dptr || !bytes) FAIL(JT_ERR_INVAL, EINVAL);
+    const size_t T = (size_t)L->last_T, k = (size_t)L->d.topk, n = (size_t)L->d.n;
+    const size_t E = (size_t)L->d.n_experts, S = (size_t)L->d.n_shared;
+    switch (which) {
+    case JT_HIP_BUF_IDS: *dptr = L->ids; *bytes = T * k * 4; break;
+    case JT_HIP_BUF_WEIGHTS: *dptr = L->w; *bytes = T * k * 4; break;
+    case JT_HIP_BUF_PERM: *dptr = L->perm; *bytes = T * k * 4; break;
+    case JT_HIP_BUF_OFF: *dptr = L->off; *bytes = (E + 1) * 4; break;
+    case JT_HIP_BUF_XQ: *dptr = L->Xq; *bytes = T * n; break;
+    case JT_HIP_BUF_XSCALE: *dptr = L->sx; *bytes = T * 4; break;
+    case JT_HIP_BUF_YE: *dptr = L->Ye; *bytes = T * k * n * 4; break;
+    case JT_HIP_BUF_YS: *dptr = L->Ys; *bytes = S * T * n * 4; break;
+    case JT_HIP_BUF_LOGITS: *dptr = L->logits; *bytes = T * E * 4; break;
+    default: FAIL(JT_ERR_INVAL, EINVAL);
+    }
+    return JT_OK;
+}
+
+/* Decode one expert's panels back into plain code / scale arrays. */
+static void decode_panels(const uint8_t *P, const uint16_t *Sc, int N, int K, int bits,
+                          int inter, uint8_t *codes, uint16_t *scales) {
+    const int G = K / 64, PB = bits == 2 ? 256 : 512;
+    for (int nn = 0; nn < N; nn++) {
+        int row = nn, src = 0;
+        if (inter) {
+            src = (nn >> 4) & 1;
+            row = (nn >> 5) * 16 + (nn & 15);
+        }
+        const int64_t prow = (int64_t)src * (inter ? N / 2 : N) + row;
+        const int p = nn / 16, c = nn % 16;
+        for (int g = 0; g < G; g++) {
+            scales[prow * G + g] = Sc[((int64_t)p * G + g) * 16 + c];
+            for (int kk = 0; kk < 64; kk++) {
+                const int kc = kk >> 4, kap = kk & 15, o = kap >> 2, j = kap & 3;
+                const int plane = kc * 16 + c;
+                uint32_t dw;
+                int sh;
+                if (bits == 2) {
+                    memcpy(&dw, P + ((int64_t)p * G + g) * PB + plane * 4, 4);
+                    sh = 8 * j + 2 * o;
+                    codes[prow * K + g * 64 + kk] = (uint8_t)((dw >> sh) & 3u);
+                } else {
+                    memcpy(&dw, P + ((int64_t)p * G + g) * PB + plane * 8 + (o >> 1) * 4, 4);
+                    sh = 8 * j + 4 * (o & 1);
+                    codes[prow * K + g * 64 + kk] = (uint8_t)((dw >> sh) & 15u);
+                }
+            }
+        }
+    }
+}
+
+int jt_hip_moe_export_routed(const jt_hip_moe *L, int e, uint8_t *gu_codes,
+                             uint16_t *gu_scales, uint8_t *d_codes, uint16_t *d_scales) {
+    if (!L || e < 0 || e >= L->d.n_experts || !gu_codes || !gu_scales || !d_codes ||
+        !d_scales)
+        FAIL(JT_ERR_INVAL, EINVAL);
+    jt_rt *rt = jt_rt_get();
+    if (!rt) return JT_ERR_IO;
+    const int n = L->d.n, h = L->d.h;
+    uint8_t *hp = malloc((size_t)(L->gu_pstride > L->dn_pstride ? L->gu_pstride : L->dn_pstride));
+    uint16_t *hs = malloc((size_t)(L->gu_sstride > L->dn_sstride ? L->gu_sstride : L->dn_sstride) * 2);
+    if (!hp || !hs) {
+        free(hp);
+        free(hs);
+        FAIL(JT_ERR_NOMEM, ENOMEM);
+    }
+    int rc = jt_rt_d2h(rt, hp, L->gu_P + (int64_t)e * L->gu_pstride, (size_t)L->gu_pstride);
+    if (rc == JT_OK)
+        rc = jt_rt_d2h(rt, hs, L->gu_S + (int64_t)e * L->gu_sstride, (size_t)L->gu_sstride * 2);
+    if (rc == JT_OK) decode_panels(hp, hs, 2 * h, n, 2, 1, gu_codes, gu_scales);
+    if (rc == JT_OK)
+        rc = jt_rt_d2h(rt, hp, L->dn_P + (int64_t)e * L->dn_pstride, (size_t)L->dn_pstride);
+    if (rc == JT_OK)
+        rc = jt_rt_d2h(rt, hs, L->dn_S + (int64_t)e * L->dn_sstride, (size_t)L->dn_sstride * 2);
+    if (rc == JT_OK) decode_panels(hp, hs, n, h, 4, 0, d_codes, d_scales);
+    free(hp);
+    free(hs);
+    return rc;
+}
+
+int jt_hip_moe_set_profiling(jt_hip_moe *L, int on) {
+    if (!L) FAIL(JT_ERR_INVAL, EINVAL);
+    while (L->ring_count > 0) prof_drain_one(L);
+    L->prof = on ? 1 : 0;
+    return JT_OK;
+}
+
+int jt_hip_moe_stage_times(jt_hip_moe *L, const char **names, double *ms, int cap, int *n,
+                           int *count) {
+    if (!L || !ms || !n || !count) FAIL(JT_ERR_INVAL, EINVAL);
+    while (L->ring_count > 0) prof_drain_one(L);
+    int m = cap < ST_N ? cap : ST_N;
+    for (int i = 0; i < m; i++) {
+        if (names) names[i] = k_stage_names[i];
+        ms[i] = L->acc_ms[i];
+        L->acc_ms[i] = 0.0;
+    }
+    *n = m;
+    *count = L->acc_count;
+    L->acc_count = 0;
+    return JT_OK;
+}

@@ -1,0 +1,347 @@
+/*
+ * moe_layer.c -- the reference's batched MoE forward (jt_moe_fwd_batch,
+ * src/moe_layer.c:980-1663) on the MI355X, host orchestration in C11.
+ *
+ * Same stages, same order, same arithmetic as the reference:
+ *   gate logits (fp64, AVX2 lane order) -> top-k softmax -> capacity sort ->
+ *   renormalisation of tokens with drops -> per expert: gather, gate/up GEMM
+ *   (fp32 k-ordered / W8A8 per-tensor x per-channel with per-call weight
+ *   quantisation / low-bit fake-quant / T-MAC LUT), SwiGLU, down GEMM
+ *   (fp32 / W8A8 per-tensor / low-bit), scatter -> fp64 combine in slot
+ *   order -> shared experts (fp32 or W8A8) added in fp64 -> Y.
+ * The flag reads and their precedence (low-bit before W8A8) are those of
+ * src/moe_layer.c:1068-1071, 1301-1396. Everything runs as kernels on the
+ * library stream; Y, ids, weights and the sort outputs are copied back only
+ * when the whole forward raised no error bit.
+ */
+#include <errno.h>
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "jimotono/lowbit.h"
+#include "jimotono/moe_layer.h"
+#include "jimotono/w8a8.h"
+#include "jt_rt.h"
+
+#define FAIL(code, e) \
+    do {              \
+        errno = (e);  \
+        return (code); \
+    } while (0)
+
+int jt_dev_lowbit_gemm_lut(jt_rt *rt, const float *dX, const float *dW, float *dY, int me,
+                           int h, int k, int bits);
+
+/* allocation list freed at the end of a forward */
+typedef struct {
+    void *p[64];
+    int n;
+    hipError_t e;
+} arena_t;
+
+static void *aalloc(arena_t *a, size_t bytes) {
+    void *p = NULL;
+    if (a->e != hipSuccess || a->n >= 64) {
+        if (a->e == hipSuccess) a->e = hipErrorOutOfMemory;
+        return NULL;
+    }
+    a->e = hipMalloc(&p, bytes ? bytes : 16);
+    if (a->e != hipSuccess) return NULL;
+    a->p[a->n++] = p;
+    return p;
+}
+
+static void afree(arena_t *a) {
+    for (int i = 0; i < a->n; i++) (void)hipFree(a->p[i]);
+    a->n = 0;
+}
+
+/* W8A8 expert GEMM scratch, sized for the largest call of one forward */
+typedef struct {
+    int8_t *Aq, *Bq, *P;
+    float *sA1, *sA, *sB1, *sB;
+} w8_ws;
+
+/* C[M][N] = A[M][K] x Brow[N][K]^T: A per tensor, B per output row
+ * (src/moe_layer.c:228-274). */
+static int w8a8_pc(jt_rt *rt, w8_ws *w, const float *A, const float *Brow, float *C, int M,
+                   int N, int K) {
+    const int Kp = (int)jt_round_up((size_t)K, 64), Np = (int)jt_round_up((size_t)N, 128);
+    hipStream_t s = rt->stream;
+    int le = jtk_quant_tensor(A, (int64_t)M * K, w->Bq, w->sA1, rt->d_scratch, rt->d_err, s);
+    /* re-stride the activation codes to the padded GEMM layout */
+    le |= (int)hipMemsetAsync(w->Aq, 0, (size_t)M * Kp, s);
+    le |= (int)hipMemcpy2DAsync(w->Aq, (size_t)Kp, w->Bq, (size_t)K, (size_t)K, (size_t)M,
+                                hipMemcpyDeviceToDevice, s);
+    le |= jtk_bcast_f32(w->sA, M, w->sA1, s);
+    le |= jtk_quant_weight_rows(Brow, K, 1, N, K, w->Bq, w->sB, rt->d_err, s);
+    le |= jtk_pack_i8(w->Bq, N, K, 0, Np, Kp, w->P, s);
+    le |= jtk_w8a8_gemm(w->Aq, Kp, w->sA, w->P, w->sB, M, N, Np, Kp, C, N, 0, rt->d_err, s);
+    return le ? jt_rt_err(hipErrorLaunchFailure) : JT_OK;
+}
+
+/* C[M][N] = A[M][K] x Bkn[K][N], both per tensor (src/moe_layer.c:185-223). */
+static int w8a8_pt(jt_rt *rt, w8_ws *w, const float *A, const float *Bkn, float *C, int M,
+                   int N, int K) {
+    const int Kp = (int)jt_round_up((size_t)K, 64), Np = (int)jt_round_up((size_t)N, 128);
+    hipStream_t s = rt->stream;
+    int le = jtk_quant_tensor(A, (int64_t)M * K, w->Bq, w->sA1, rt->d_scratch, rt->d_err, s);
+    le |= (int)hipMemsetAsync(w->Aq, 0, (size_t)M * Kp, s);
+    le |= (int)hipMemcpy2DAsync(w->Aq, (size_t)Kp, w->Bq, (size_t)K, (size_t)K, (size_t)M,
+                                hipMemcpyDeviceToDevice, s);
+    le |= jtk_bcast_f32(w->sA, M, w->sA1, s);
+    le |= jtk_quant_tensor(Bkn, (int64_t)K * N, w->Bq, w->sB1, rt->d_scratch + 1, rt->d_err, s);
+    le |= jtk_bcast_f32(w->sB, Np, w->sB1, s);
+    le |= jtk_pack_i8(w->Bq, N, K, 1, Np, Kp, w->P, s);
+    le |= jtk_w8a8_gemm(w->Aq, Kp, w->sA, w->P, w->sB, M, N, Np, Kp, C, N, 0, rt->d_err, s);
+    return le ? jt_rt_err(hipErrorLaunchFailure) : JT_OK;
+}
+
+static int valid_dims(int n, int h, int e, int k, int s) {
+    if (n <= 0 || h <= 0 || n > JT_BWD_MAX_WIDE || h > JT_BWD_MAX_WIDE) return 0;
+    if (e <= 0 || e > JT_MOE_MAX_EXPERTS) return 0;
+    if (k <= 0 || k > e || k > JT_MOE_MAX_TOPK) return 0;
+    if (s < 0 || s > JT_MOE_MAX_SHARED) return 0;
+    return 1;
+}
+
+static int fwd_batch(const float *X, const float *Wgate, const float *Wg, const float *Wu,
+                     const float *Wd, const float *Wg_s, const float *Wu_s, const float *Wd_s,
+                     float *Y, int T, int n, int h, int E, int k, int S, size_t *out_ids,
+                     float *out_weights, float *cache_Gsel, float *cache_Usel,
+                     float *cache_Ysel, float *cache_Gs, float *cache_Us, float cap_factor,
+                     size_t *out_perm, size_t *out_off, unsigned char *out_drop,
+                     size_t *out_kept, size_t *out_dropped, int validate) {
+    if (!X || !Wgate || !Wg || !Wu || !Wd || !Y || !out_ids || !out_weights)
+        FAIL(JT_ERR_INVAL, EINVAL);
+    if (T <= 0 || !valid_dims(n, h, E, k, S)) FAIL(JT_ERR_INVAL, EINVAL);
+    if (S > 0 && (!Wg_s || !Wu_s || !Wd_s)) FAIL(JT_ERR_INVAL, EINVAL);
+    if (!(cap_factor >= 1.0f) || !(cap_factor <= 1.5f) || !isfinite((double)cap_factor))
+        FAIL(JT_ERR_INVAL, EINVAL);
+    if ((int64_t)T * k > INT32_MAX / 2 || (int64_t)T * k * n > ((int64_t)1 << 40))
+        FAIL(JT_ERR_INVAL, EINVAL);
+    if (sizeof(size_t) != 8) FAIL(JT_ERR_NOSUP, EINVAL);
+    const int w8a8_on = jt_w8a8_is_enabled();
+    const int lbmode = jt_lowbit_get_mode();
+    jt_rt *rt = jt_rt_get();
+    if (!rt) return JT_ERR_IO;
+    hipStream_t s = rt->stream;
+    uint32_t *err = rt->d_err;
+    const size_t Tk = (size_t)T * k, nh = (size_t)n * h, Tn = (size_t)T * n;
+    const size_t NB = (Tk + 255) / 256;
+    const int Kpmax = (int)jt_round_up((size_t)(n > h ? n : h), 64);
+    const int Npmax = (int)jt_round_up((size_t)(n > h ? n : h), 128);
+    const size_t Mmax = Tk > (size_t)T ? Tk : (size_t)T;
+    arena_t a = {.n = 0, .e = hipSuccess};
+    float *dX = aalloc(&a, Tn * 4), *dWgate = aalloc(&a, (size_t)E * n * 4);
+    float *dWg = aalloc(&a, E * nh * 4), *dWu = aalloc(&a, E * nh * 4);
+    float *dWd = aalloc(&a, E * nh * 4);
+    float *dWgs = S ? aalloc(&a, S * nh * 4) : NULL, *dWus = S ? aalloc(&a, S * nh * 4) : NULL;
+    float *dWds = S ? aalloc(&a, S * nh * 4) : NULL;
+    float *logits = aalloc(&a, (size_t)T * E * 4);
+    int32_t *ids = aalloc(&a, Tk * 4);
+    int64_t *ids64 = aalloc(&a, Tk * 8);
+    float *w = aalloc(&a, Tk * 4);
+    int32_t *rank = aalloc(&a, Tk * 4), *cnt = aalloc(&a, NB * E * 4);
+    int32_t *tot = aalloc(&a, (size_t)E * 4), *off = aalloc(&a, ((size_t)E + 1) * 4);
+    int64_t *off64 = aalloc(&a, ((size_t)E + 1) * 8);
+    int32_t *perm = aalloc(&a, Tk * 4);
+    int64_t *perm64 = aalloc(&a, Tk * 8);
+    uint8_t *drop = aalloc(&a, Tk);
+    float *Xe = aalloc(&a, Mmax * n * 4), *Ge = aalloc(&a, Mmax * h * 4);
+    float *Ue = aalloc(&a, Mmax * h * 4), *Se = aalloc(&a, Mmax * h * 4);
+    float *Ye = aalloc(&a, Mmax * n * 4);
+    float *Ysel = aalloc(&a, Tk * n * 4);
+    float *Gsel = cache_Gsel ? aalloc(&a, Tk * h * 4) : NULL;
+    float *Usel = cache_Usel ? aalloc(&a, Tk * h * 4) : NULL;
+    float *Ys = aalloc(&a, (size_t)(S ? S : 1) * Tn * 4);
+    float *Gs = (S && cache_Gs) ? aalloc(&a, (size_t)T * S * h * 4) : NULL;
+    float *Us = (S && cache_Us) ? aalloc(&a, (size_t)T * S * h * 4) : NULL;
+    float *Wt1 = aalloc(&a, nh * 4), *Wt2 = aalloc(&a, nh * 4);
+    float *dY = aalloc(&a, Tn * 4), *wsbuf = aalloc(&a, (size_t)(n > h ? n : h) * 4);
+    w8_ws w8 = {0};
+    w8.Aq = aalloc(&a, Mmax * Kpmax);
+    w8.Bq = aalloc(&a, (Mmax > (size_t)Npmax ? Mmax : (size_t)Npmax) * Kpmax);
+    w8.P = aalloc(&a, (size_t)Npmax * Kpmax);
+    w8.sA1 = aalloc(&a, 16);
+    w8.sB1 = aalloc(&a, 16);
+    w8.sA = aalloc(&a, Mmax * 4);
+    w8.sB = aalloc(&a, (size_t)Npmax * 4);
+    int rc = jt_rt_err(a.e);
+    int64_t *hoff = malloc(((size_t)E + 1) * 8);
+    if (rc == JT_OK && !hoff) rc = JT_ERR_NOMEM, errno = ENOMEM;
+    if (rc != JT_OK) goto out;
+#define H2D(d, h_, b) \
+    if (rc == JT_OK) rc = jt_rt_h2d(rt, (d), (h_), (b))
+    H2D(dX, X, Tn * 4);
+    H2D(dWgate, Wgate, (size_t)E * n * 4);
+    H2D(dWg, Wg, E * nh * 4);
+    H2D(dWu, Wu, E * nh * 4);
+    H2D(dWd, Wd, E * nh * 4);
+    if (S) {
+        H2D(dWgs, Wg_s, S * nh * 4);
+        H2D(dWus, Wu_s, S * nh * 4);
+        H2D(dWds, Wd_s, S * nh * 4);
+    }
+#undef H2D
+    if (rc != JT_OK) goto out;
+    int le = 0;
+    if (validate) { /* src/moe_layer.c:1074-1096 */
+        le |= jtk_check_finite(dX, (int64_t)Tn, err, s);
+        le |= jtk_check_finite(dWgate, (int64_t)E * n, err, s);
+        le |= jtk_check_finite(dWg, (int64_t)(E * nh), err, s);
+        le |= jtk_check_finite(dWu, (int64_t)(E * nh), err, s);
+        le |= jtk_check_finite(dWd, (int64_t)(E * nh), err, s);
+        if (S) {
+            le |= jtk_check_finite(dWgs, (int64_t)(S * nh), err, s);
+            le |= jtk_check_finite(dWus, (int64_t)(S * nh), err, s);
+            le |= jtk_check_finite(dWds, (int64_t)(S * nh), err, s);
+        }
+    }
+    /* gate logits + top-k (src/moe_layer.c:1114-1156) */
+    le |= jtk_router_logits(dX, dWgate, T, E, n, logits, err, s);
+    le |= jtk_topk(logits, T, E, k, ids, ids64, w, err, s);
+    /* capacity sort + renormalisation (src/moe_layer.c:1158-1201) */
+    const double capd = ceil((double)cap_factor * (double)Tk / (double)E);
+    le |= jtk_sort(ids, (int)Tk, E, (int64_t)capd, rank, cnt, tot, off, off64, perm, perm64,
+                   drop, err, s);
+    le |= jtk_renorm(w, drop, T, k, err, s);
+    if (le) {
+        rc = jt_rt_err(hipErrorLaunchFailure);
+        goto out;
+    }
+    uint32_t f = 0;
+    if ((rc = jt_rt_flags(rt, s, &f)) != JT_OK) goto out;
+    if ((rc = jt_rt_flags_to_rc(f)) != JT_OK) goto out;
+    if ((rc = jt_rt_d2h(rt, hoff, off64, ((size_t)E + 1) * 8)) != JT_OK) goto out;
+    if (cache_Ysel) le |= (int)hipMemsetAsync(Ysel, 0, Tk * n * 4, s);
+    if (Gsel) le |= (int)hipMemsetAsync(Gsel, 0, Tk * h * 4, s);
+    if (Usel) le |= (int)hipMemsetAsync(Usel, 0, Tk * h * 4, s);
+    /* per-expert forward (src/moe_layer.c:1265-1420) */
+    for (int e = 0; e < E && rc == JT_OK; e++) {
+        const int b0 = (int)hoff[e], Me = (int)(hoff[e + 1] - hoff[e]);
+        if (Me == 0) continue;
+        const float *wg = dWg + e * nh, *wu = dWu + e * nh, *wd = dWd + e * nh;
+        le |= jtk_gather_rows(dX, n, perm, b0, k, Me, Xe, s);
+        if (lbmode != 0) {
+            le |= jtk_transpose_f32(wg, Wt1, h, n, s);
+            le |= jtk_transpose_f32(wu, Wt2, h, n, s);
+            if (lbmode == 1) {
+                le |= jtk_lowbit_fq_cols(Wt1, n, h, 2, wsbuf, err, s);
+                le |= jtk_lowbit_fq_cols(Wt2, n, h, 2, wsbuf, err, s);
+                le |= jtk_gemm_f32(Xe, Wt1, Ge, Me, h, n, err, s);
+                le |= jtk_gemm_f32(Xe, Wt2, Ue, Me, h, n, err, s);
+            } else {
+                rc = jt_dev_lowbit_gemm_lut(rt, Xe, Wt1, Ge, Me, h, n, 2);
+                if (rc == JT_OK) rc = jt_dev_lowbit_gemm_lut(rt, Xe, Wt2, Ue, Me, h, n, 2);
+            }
+        } else if (w8a8_on) {
+            rc = w8a8_pc(rt, &w8, Xe, wg, Ge, Me, h, n);
+            if (rc == JT_OK) rc = w8a8_pc(rt, &w8, Xe, wu, Ue, Me, h, n);
+        } else {
+            le |= jtk_transpose_f32(wg, Wt1, h, n, s);
+            le |= jtk_transpose_f32(wu, Wt2, h, n, s);
+            le |= jtk_gemm_f32(Xe, Wt1, Ge, Me, h, n, err, s);
+            le |= jtk_gemm_f32(Xe, Wt2, Ue, Me, h, n, err, s);
+        }
+        le |= jtk_silu_tile(Ge, Ue, (int64_t)Me * h, Se, err, s);
+        if (lbmode != 0) {
+            if (lbmode == 1) {
+                le |= (int)hipMemcpyAsync(Wt1, wd, nh * 4, hipMemcpyDeviceToDevice, s);
+                le |= jtk_lowbit_fq_cols(Wt1, h, n, 4, wsbuf, err, s);
+                le |= jtk_gemm_f32(Se, Wt1, Ye, Me, n, h, err, s);
+            } else if (rc == JT_OK) {
+                rc = jt_dev_lowbit_gemm_lut(rt, Se, wd, Ye, Me, n, h, 4);
+            }
+        } else if (w8a8_on) {
+            if (rc == JT_OK) rc = w8a8_pt(rt, &w8, Se, wd, Ye, Me, n, h);
+        } else {
+            le |= jtk_gemm_f32(Se, wd, Ye, Me, n, h, err, s);
+        }
+        le |= jtk_scatter_rows(Ye, n, perm, b0, Me, Ysel, s);
+        if (Gsel) le |= jtk_scatter_rows(Ge, h, perm, b0, Me, Gsel, s);
+        if (Usel) le |= jtk_scatter_rows(Ue, h, perm, b0, Me, Usel, s);
+    }
+    if (rc == JT_OK && le) rc = jt_rt_err(hipErrorLaunchFailure);
+    /* shared experts (src/moe_layer.c:1468-1560) */
+    for (int sx = 0; sx < S && rc == JT_OK; sx++) {
+        const float *wg = dWgs + sx * nh, *wu = dWus + sx * nh, *wd = dWds + sx * nh;
+        float *ys = Ys + (size_t)sx * Tn;
+        if (w8a8_on) {
+            rc = w8a8_pc(rt, &w8, dX, wg, Ge, T, h, n);
+            if (rc == JT_OK) rc = w8a8_pc(rt, &w8, dX, wu, Ue, T, h, n);
+        } else {
+            le |= jtk_transpose_f32(wg, Wt1, h, n, s);
+            le |= jtk_transpose_f32(wu, Wt2, h, n, s);
+            le |= jtk_gemm_f32(dX, Wt1, Ge, T, h, n, err, s);
+            le |= jtk_gemm_f32(dX, Wt2, Ue, T, h, n, err, s);
+        }
+        if (Gs) le |= (int)hipMemcpy2DAsync(Gs + (size_t)sx * h, (size_t)S * h * 4, Ge,
+                                           (size_t)h * 4, (size_t)h * 4, (size_t)T,
+                                           hipMemcpyDeviceToDevice, s);
+        if (Us) le |= (int)hipMemcpy2DAsync(Us + (size_t)sx * h, (size_t)S * h * 4, Ue,
+                                           (size_t)h * 4, (size_t)h * 4, (size_t)T,
+                                           hipMemcpyDeviceToDevice, s);
+        le |= jtk_silu_tile(Ge, Ue, (int64_t)T * h, Se, err, s);
+        if (rc == JT_OK) {
+            if (w8a8_on) rc = w8a8_pt(rt, &w8, Se, wd, ys, T, n, h);
+            else le |= jtk_gemm_f32(Se, wd, ys, T, n, h, err, s);
+        }
+    }
+    /* combine (src/moe_layer.c:1443-1463, 1549-1574) */
+    le |= jtk_combine(w, Ysel, drop, Ys, S, T, k, n, dY, err, s);
+    if (rc == JT_OK && le) rc = jt_rt_err(hipErrorLaunchFailure);
+    if (rc != JT_OK) goto out;
+    if ((rc = jt_rt_flags(rt, s, &f)) != JT_OK) goto out;
+    if ((rc = jt_rt_flags_to_rc(f)) != JT_OK) goto out;
+    /* commit (fail-closed: nothing above wrote a host output) */
+    const size_t kept = (size_t)hoff[E];
+    rc = jt_rt_d2h(rt, Y, dY, Tn * 4);
+    if (rc == JT_OK) rc = jt_rt_d2h(rt, out_ids, ids64, Tk * 8);
+    if (rc == JT_OK) rc = jt_rt_d2h(rt, out_weights, w, Tk * 4);
+    if (rc == JT_OK && out_perm) rc = jt_rt_d2h(rt, out_perm, perm64, kept * 8);
+    if (rc == JT_OK && out_off) memcpy(out_off, hoff, ((size_t)E + 1) * 8);
+    if (rc == JT_OK && out_drop) rc = jt_rt_d2h(rt, out_drop, drop, Tk);
+    if (rc == JT_OK && cache_Ysel) rc = jt_rt_d2h(rt, cache_Ysel, Ysel, Tk * n * 4);
+    if (rc == JT_OK && cache_Gsel) rc = jt_rt_d2h(rt, cache_Gsel, Gsel, Tk * h * 4);
+    if (rc == JT_OK && cache_Usel) rc = jt_rt_d2h(rt, cache_Usel, Usel, Tk * h * 4);
+    if (rc == JT_OK && cache_Gs && Gs) rc = jt_rt_d2h(rt, cache_Gs, Gs, (size_t)T * S * h * 4);
+    if (rc == JT_OK && cache_Us && Us) rc = jt_rt_d2h(rt, cache_Us, Us, (size_t)T * S * h * 4);
+    if (rc == JT_OK) {
+        if (out_kept) *out_kept = kept;
+        if (out_dropped) *out_dropped = Tk - kept;
+    }
+out:
+    (void)hipStreamSynchronize(s);
+    afree(&a);
+    free(hoff);
+    return rc;
+}
+
+int jt_moe_fwd_batch(const float *X, const float *Wgate, const float *Wg, const float *Wu,
+                     const float *Wd, const float *Wg_s, const float *Wu_s, const float *Wd_s,
+                     float *Y, int T, int n, int h, int n_experts, int topk, int n_shared,
+                     size_t *out_ids, float *out_weights, float *cache_Gsel, float *cache_Usel,
+                     float *cache_Ysel, float *cache_Gs, float *cache_Us, float cap_factor,
+                     size_t *out_perm, size_t *out_off, unsigned char *out_drop,
+                     size_t *out_kept, size_t *out_dropped) {
+    return fwd_batch(X, Wgate, Wg, Wu, Wd, Wg_s, Wu_s, Wd_s, Y, T, n, h, n_experts, topk,
+                     n_shared, out_ids, out_weights, cache_Gsel, cache_Usel, cache_Ysel,
+                     cache_Gs, cache_Us, cap_factor, out_perm, out_off, out_drop, out_kept,
+                     out_dropped, 1);
+}
+
+int jt_moe_fwd_batch_unchecked(
+    const float *X, const float *Wgate, const float *Wg, const float *Wu, const float *Wd,
+    const float *Wg_s, const float *Wu_s, const float *Wd_s, float *Y, int T, int n, int h,
+    int n_experts, int topk, int n_shared, size_t *out_ids, float *out_weights,
+    float *cache_Gsel, float *cache_Usel, float *cache_Ysel, float *cache_Gs, float *cache_Us,
+    float cap_factor, size_t *out_perm, size_t *out_off, unsigned char *out_drop,
+    size_t *out_kept, size_t *out_dropped) {
+    return fwd_batch(X, Wgate, Wg, Wu, Wd, Wg_s, Wu_s, Wd_s, Y, T, n, h, n_experts, topk,
+                     n_shared, out_ids, out_weights, cache_Gsel, cache_Usel, cache_Ysel,
+                     cache_Gs, cache_Us, cap_factor, out_perm, out_off, out_drop, out_kept,
+                     out_dropped, 0);
+}

@@ -1,0 +1,135 @@
+/*
+ * runtime.c -- device binding, library stream, error word and staging
+ * buffers of libjimotono_hip. C11 over the HIP runtime C API.
+ *
+ * Threading: like the reference (src/w8a8.c:53, src/lowbit.c:16) the
+ * host-pointer entry points are not reentrant: they share the staging
+ * buffers and the error word of one process-wide runtime.
+ */
+#include "jt_rt.h"
+
+#include <errno.h>
+#include <string.h>
+
+#include "jimotono/hip_moe.h"
+
+static jt_rt g_rt;
+static int g_req_device = 0;
+
+int jt_rt_err(hipError_t e) {
+    if (e == hipSuccess) return JT_OK;
+    if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) {
+        errno = ENOMEM;
+        return JT_ERR_NOMEM;
+    }
+    errno = EIO;
+    return JT_ERR_IO;
+}
+
+jt_rt *jt_rt_get(void) {
+    if (g_rt.ready) return &g_rt;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0 || g_req_device >= n) {
+        errno = ENODEV;
+        return NULL;
+    }
+    if (hipSetDevice(g_req_device) != hipSuccess) {
+        errno = EIO;
+        return NULL;
+    }
+    memset(&g_rt, 0, sizeof(g_rt));
+    g_rt.device = g_req_device;
+    if (hipStreamCreateWithFlags(&g_rt.stream, hipStreamNonBlocking) != hipSuccess ||
+        hipMalloc((void **)&g_rt.d_err, 256) != hipSuccess ||
+        hipMalloc((void **)&g_rt.d_scratch, 4096) != hipSuccess ||
+        hipMemset(g_rt.d_err, 0, 256) != hipSuccess) {
+        errno = EIO;
+        return NULL;
+    }
+    g_rt.ready = 1;
+    return &g_rt;
+}
+
+int jt_hip_init(int device) {
+    if (device < 0) {
+        errno = EINVAL;
+        return JT_ERR_INVAL;
+    }
+    if (g_rt.ready) {
+        if (device != g_rt.device) {
+            errno = EINVAL; /* one device per process */
+            return JT_ERR_INVAL;
+        }
+        return hipSetDevice(device) == hipSuccess ? JT_OK : jt_rt_err(hipErrorUnknown);
+    }
+    g_req_device = device;
+    return jt_rt_get() ? JT_OK : JT_ERR_IO;
+}
+
+void *jt_rt_buf(jt_rt *rt, int s, size_t bytes, int *rc) {
+    if (bytes == 0) bytes = 16;
+    if (rt->slot_bytes[s] >= bytes) return rt->slot[s];
+    if (rt->slot[s]) {
+        (void)hipStreamSynchronize(rt->stream);
+        (void)hipFree(rt->slot[s]);
+        rt->slot[s] = NULL;
+        rt->slot_bytes[s] = 0;
+    }
+    size_t want = jt_round_up(bytes, 1u << 16);
+    hipError_t e = hipMalloc(&rt->slot[s], want);
+    if (e != hipSuccess) {
+        rt->slot[s] = NULL;
+        *rc = jt_rt_err(e);
+        return NULL;
+    }
+    rt->slot_bytes[s] = want;
+    return rt->slot[s];
+}
+
+int jt_rt_flags(jt_rt *rt, hipStream_t stream, uint32_t *flags) {
+    uint32_t f = 0;
+    hipError_t e = hipStreamSynchronize(stream);
+    if (e == hipSuccess) e = hipMemcpy(&f, rt->d_err, sizeof(f), hipMemcpyDeviceToHost);
+    if (e == hipSuccess && f != 0) e = hipMemset(rt->d_err, 0, sizeof(uint32_t));
+    if (e != hipSuccess) return jt_rt_err(e);
+    *flags = f;
+    return JT_OK;
+}
+
+int jt_rt_flags_to_rc(uint32_t flags) {
+    if (flags == 0) return JT_OK;
+    if (flags & (JT_EF_NONFINITE_INPUT | JT_EF_QRANGE | JT_EF_BAD_ID)) {
+        errno = EINVAL;
+        return JT_ERR_INVAL;
+    }
+    if (flags & JT_EF_RANGE) {
+        errno = ERANGE;
+        return JT_ERR_INVAL;
+    }
+    errno = EINVAL; /* non-finite intermediate */
+    return JT_ERR_INVAL;
+}
+
+int jt_rt_h2d(jt_rt *rt, void *dst, const void *src, size_t bytes) {
+    if (bytes == 0) return JT_OK;
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, rt->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(rt->stream);
+    return jt_rt_err(e);
+}
+
+int jt_rt_d2h(jt_rt *rt, void *dst, const void *src, size_t bytes) {
+    if (bytes == 0) return JT_OK;
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, rt->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(rt->stream);
+    return jt_rt_err(e);
+}
+
+int jt_hip_sync_errors(void *stream, uint32_t *out_flags) {
+    jt_rt *rt = jt_rt_get();
+    if (!rt) return JT_ERR_IO;
+    if (!out_flags) {
+        errno = EINVAL;
+        return JT_ERR_INVAL;
+    }
+    return jt_rt_flags(rt, stream ? (hipStream_t)stream : rt->stream, out_flags);
+}

@@ -1,0 +1,95 @@
+/*
+ * Launchers of the gfx950 kernels, callable from the C11 host layer.
+ * Each returns the hipError_t of the launch (0 = success). Pointers are
+ * device pointers; `err` is the library's device error word (EF_* bits).
+ */
+#ifndef JT_LAUNCH_H
+#define JT_LAUNCH_H
+
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* quant.hip */
+int jtk_quant_rows(const float *X, int64_t rows, int cols, int8_t *Q, int64_t ldq,
+                   float *scale, const int32_t *row_count, uint32_t *err, hipStream_t s);
+int jtk_quant_tensor(const float *x, int64_t n, int8_t *q, float *scale,
+                     uint32_t *amax_scratch, uint32_t *err, hipStream_t s);
+int jtk_fakequant(const float *x, int64_t rows, int64_t cols, float *d,
+                  uint32_t *amax_scratch, uint32_t *err, hipStream_t s);
+int jtk_dequant(const int8_t *q, const float *scale, int64_t rows, int64_t cols,
+                int per_row, float *d, uint32_t *err, hipStream_t s);
+int jtk_check_q(const int8_t *q, int64_t n, uint32_t *err, hipStream_t s);
+int jtk_check_finite(const float *x, int64_t n, uint32_t *err, hipStream_t s);
+int jtk_pack_i8(const int8_t *Q, int N, int K, int kn, int Np, int Kp, int8_t *P,
+                hipStream_t s);
+int jtk_unpack_i8_kn(const int8_t *P, int N, int K, int Kp, int8_t *Q, hipStream_t s);
+int jtk_pack_lowbit(const float *W0, const float *W1, int64_t w_estride, int64_t ld_n,
+                    int64_t ld_k, int E, int N, int K, int bits, uint8_t *P, uint16_t *S,
+                    uint8_t *codes_out, uint16_t *scales_out, uint32_t *err, hipStream_t s);
+int jtk_interleave_rows(const void *A, const void *B, int h, int64_t row_bytes, void *D,
+                        hipStream_t s);
+int jtk_quant_weight_rows(const float *W, int64_t ld_n, int64_t ld_k, int N, int K,
+                          int8_t *Q, float *scale, uint32_t *err, hipStream_t s);
+
+/* gemm_i8.hip */
+int jtk_w8a8_gemm(const int8_t *A, int lda, const float *sA, const int8_t *Wp,
+                  const float *sB, int M, int N, int Np, int Kp, float *C, int ldc,
+                  int swiglu, uint32_t *err, hipStream_t s);
+int jtk_lowbit_grouped(int bits, const int8_t *A, int lda, const float *sA,
+                       const int32_t *perm, const int32_t *off, int topk,
+                       const int32_t *tiles, const int32_t *ntiles, int max_tiles,
+                       const uint8_t *Wp, const uint16_t *Ws, int64_t wp_stride,
+                       int64_t ws_stride, int N, int K, float *out, int ldo,
+                       uint32_t *err, hipStream_t s);
+
+/* route.hip */
+int jtk_router_logits(const float *X, const float *Wg, int T, int E, int n, float *logits,
+                      uint32_t *err, hipStream_t s);
+int jtk_topk(const float *logits, int rows, int E, int k, int32_t *ids, int64_t *ids64,
+             float *w, uint32_t *err, hipStream_t s);
+int jtk_sort(const int32_t *ids, int Tk, int E, int64_t cap, int32_t *rank, int32_t *cnt,
+             int32_t *tot, int32_t *off, int64_t *off64, int32_t *perm, int64_t *perm64,
+             uint8_t *drop, uint32_t *err, hipStream_t s);
+int jtk_make_tiles(const int32_t *off, int E, int32_t *tiles, int32_t *ntiles,
+                   hipStream_t s);
+int jtk_combine(const float *w, const float *Ye, const uint8_t *drop, const float *Ys,
+                int S, int T, int k, int n, float *Y, uint32_t *err, hipStream_t s);
+int jtk_renorm(float *w, const uint8_t *drop, int T, int k, uint32_t *err, hipStream_t s);
+int jtk_gather_rows(const float *src, int n, const int32_t *perm, int base, int div,
+                    int rows, float *dst, hipStream_t s);
+int jtk_scatter_rows(const float *src, int n, const int32_t *perm, int base, int rows,
+                     float *dst, hipStream_t s);
+int jtk_silu_tile(const float *G, const float *U, int64_t n, float *S, uint32_t *err,
+                  hipStream_t s);
+int jtk_zero_u32(uint32_t *p, int64_t n, hipStream_t s);
+int jtk_bcast_f32(float *dst, int64_t n, const float *src, hipStream_t s);
+
+/* legacy.hip */
+int jtk_gemm_f32(const float *A, const float *B, float *C, int M, int N, int K,
+                 uint32_t *err, hipStream_t s);
+int jtk_transpose_f32(const float *src, float *dst, int rows, int cols, hipStream_t s);
+int jtk_tmac_ctor(const float *act, int64_t n, int64_t k, int8_t *qlut, float *scales,
+                  float *biases, uint32_t *err, hipStream_t s);
+int jtk_col_to_idx(const float *W, int k, int h, int bits, float *ws, uint8_t *idx,
+                   uint32_t *err, hipStream_t s);
+int jtk_tmac_gemm(const int8_t *qlut, const float *sc, const float *bi, const double *rowsum,
+                  const uint8_t *idx, const float *ws, int me, int h, int k, int bits,
+                  float *Y, uint32_t *err, hipStream_t s);
+int jtk_rowsum_f64(const float *X, int me, int k, double *rs, hipStream_t s);
+int jtk_tmac_lookup1(const int8_t *qlut, const uint8_t *idx, const float *sc,
+                     const float *bi, int64_t ng, int64_t nb, int bits, float w_scale,
+                     float *out, uint32_t *err, hipStream_t s);
+int jtk_gemm_f64acc(const float *A, const float *B, float *C, int M, int N, int K,
+                    hipStream_t s);
+int jtk_lowbit_fq_cols(float *W, int k, int h, int bits, float *ws, uint32_t *err,
+                       hipStream_t s);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* JT_LAUNCH_H */

@@ -1,0 +1,526 @@
+// Routing, expert sort, work lists and combine (gfx950).
+//
+//  k_router_logits : logits[t][e] = (float)dot(X[t], Wgate[e]) in fp64 with
+//                    the reference's four lane partials over j % 4, combined
+//                    as (l0+l1)+(l2+l3), then the tail (src/moe_layer.c:67-86,
+//                    1118-1137). Products of two floats are exact in fp64, so
+//                    fma(x, w, l) rounds exactly like the reference's
+//                    separate multiply and add.
+//  k_topk          : top-k by value with ties to the lower index, softmax
+//                    over the selected k in fp64 (src/routing.c:16-76).
+//  k_sort_*        : stable counting sort of the (token, slot) pairs by
+//                    expert, optional capacity (src/moe_layer.c:895-978).
+//  k_combine       : Y[t] = (float)(sum_p w_p*Ye[t,p] + sum_s Ys[s][t]) in
+//                    fp64, slot order then shared order
+//                    (src/moe_layer.c:1443-1463, 1549-1574).
+#include "jt_dev.h"
+#include "jt_launch.h"
+
+// ---------------- router logits ----------------
+// Block: 64 tokens x 64 experts, 256 threads, each a 4 x 4 (token, expert)
+// micro-tile with 4 lane partials per output. K streamed in chunks of 32
+// through LDS (stored transposed, k-major, so each thread reads float4s).
+#define RT_T 64
+#define RT_E 64
+#define RT_KC 32
+__global__ __launch_bounds__(256) void k_router_logits(const float *__restrict__ X,
+                                                       const float *__restrict__ Wg, int T,
+                                                       int E, int n,
+                                                       float *__restrict__ logits,
+                                                       uint32_t *err) {
+    __shared__ float xs[RT_KC][RT_T + 4];
+    __shared__ float ws[RT_KC][RT_E + 4];
+    const int tid = threadIdx.x;
+    const int t0 = blockIdx.x * RT_T, e0 = blockIdx.y * RT_E;
+    const int ty = tid >> 4, tx = tid & 15;  // tokens ty*4.., experts tx*4..
+    double part[4][4][4];
+#pragma unroll
+    for (int a = 0; a < 4; a++)
+#pragma unroll
+        for (int b = 0; b < 4; b++)
+#pragma unroll
+            for (int p = 0; p < 4; p++) part[a][b][p] = 0.0;
+    const int n4 = n & ~3;
+    for (int k0 = 0; k0 < n4; k0 += RT_KC) {
+        // load 64 x 32 floats of X and of Wgate: 2048 floats each, 8/thread
+        for (int i = tid; i < RT_T * RT_KC; i += 256) {
+            const int r = i / RT_KC, c = i % RT_KC;
+            const int t = min(t0 + r, T - 1), e = min(e0 + r, E - 1);
+            const int k = k0 + c;
+            xs[c][r] = k < n4 ? X[(int64_t)t * n + k] : 0.0f;
+            ws[c][r] = k < n4 ? Wg[(int64_t)e * n + k] : 0.0f;
+        }
+        __syncthreads();
+        const int kend = min(RT_KC, n4 - k0);
+        for (int c = 0; c < kend; c += 4) {
+#pragma unroll
+            for (int p = 0; p < 4; p++) {
+                const float4 xv = *(const float4 *)(&xs[c + p][ty * 4]);
+                const float4 wv = *(const float4 *)(&ws[c + p][tx * 4]);
+                const double xa[4] = {xv.x, xv.y, xv.z, xv.w};
+                const double wa[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+                for (int a = 0; a < 4; a++)
+#pragma unroll
+                    for (int b = 0; b < 4; b++) part[a][b][p] = fma(xa[a], wa[b], part[a][b][p]);
+            }
+        }
+        __syncthreads();
+    }
+    uint32_t bad = 0;
+#pragma unroll
+    for (int a = 0; a < 4; a++) {
+        const int t = t0 + ty * 4 + a;
+        if (t >= T) continue;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const int e = e0 + tx * 4 + b;
+            if (e >= E) continue;
+            double s = (part[a][b][0] + part[a][b][1]) + (part[a][b][2] + part[a][b][3]);
+            for (int j = n4; j < n; j++)
+                s = s + (double)X[(int64_t)t * n + j] * (double)Wg[(int64_t)e * n + j];
+            const float f = (float)s;
+            bad |= (!isfinite(s)) || (!isfinite(f));
+            logits[(int64_t)t * E + e] = f;
+        }
+    }
+    if (bad) raise_err(err, EF_NONFINITE_MID);
+}
+
+extern "C" int jtk_router_logits(const float *X, const float *Wg, int T, int E, int n,
+                                 float *logits, uint32_t *err, hipStream_t s) {
+    dim3 grid((unsigned)((T + RT_T - 1) / RT_T), (unsigned)((E + RT_E - 1) / RT_E));
+    hipLaunchKernelGGL(k_router_logits, grid, dim3(256), 0, s, X, Wg, T, E, n, logits, err);
+    return (int)hipGetLastError();
+}
+
+// ---------------- top-k + softmax ----------------
+// One wavefront per row of logits [rows][E]. Selection is an argmax by
+// (value desc, index asc) with already-selected entries treated as -INF,
+// which is exactly the reference's strict-greater linear scan. NaN logits
+// are rejected (EF_NONFINITE_MID). ids are written as int32 and, when ids64
+// is non-NULL, also as 64-bit values (the reference's size_t).
+__global__ __launch_bounds__(256) void k_topk(const float *__restrict__ logits, int rows,
+                                              int E, int k, int32_t *__restrict__ ids,
+                                              int64_t *__restrict__ ids64,
+                                              float *__restrict__ w, uint32_t *err) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float *l = logits + (int64_t)row * E;
+    int nan = 0;
+    for (int i = lane; i < E; i += 64) nan |= isnan(l[i]);
+    nan = wave_or_i(nan);
+    if (nan) {
+        if (lane == 0) raise_err(err, EF_NONFINITE_MID);
+        return;
+    }
+    // Lane l owns elements i = l + 64*j (j < 64, E <= 4096); bit j of
+    // `taken` marks an element already selected. Lane p ends up holding the
+    // p-th selected id.
+    uint64_t taken = 0;
+    int mysel = -1;
+    for (int p = 0; p < k; p++) {
+        float bv = -__builtin_inff();
+        int bi = 0x7fffffff;
+        for (int i = lane, j = 0; i < E; i += 64, j++) {
+            const float v = ((taken >> j) & 1ull) ? -__builtin_inff() : l[i];
+            if (v > bv || (v == bv && i < bi)) {
+                bv = v;
+                bi = i;
+            }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o, 64);
+            const int oi = __shfl_xor(bi, o, 64);
+            if (ov > bv || (ov == bv && oi < bi)) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        if ((bi & 63) == lane) taken |= 1ull << (bi >> 6);
+        if (lane == p) mysel = bi;
+    }
+    // softmax: each lane p < k holds id p; lane 0 accumulates sequentially.
+    const float lv = lane < k ? l[mysel] : -__builtin_inff();
+    float mx = lv;
+    // max over selected in the reference's order is the plain maximum
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    const double e = lane < k ? exp((double)lv - (double)mx) : 0.0;
+    double sum = 0.0;
+    for (int p = 0; p < k; p++) sum += __shfl(e, p, 64);
+    const bool ok = (sum > 0.0) && isfinite(sum);
+    if (!ok) {
+        if (lane == 0) raise_err(err, EF_NONFINITE_MID);
+        return;
+    }
+    const float inv = (float)(1.0 / sum);
+    if (lane < k) {
+        const float wv = (float)e * inv;
+        ids[(int64_t)row * k + lane] = mysel;
+        if (ids64) ids64[(int64_t)row * k + lane] = mysel;
+        w[(int64_t)row * k + lane] = wv;
+        if (!(wv >= 0.0f) || !isfinite(wv)) raise_err(err, EF_NONFINITE_MID);
+    }
+}
+
+extern "C" int jtk_topk(const float *logits, int rows, int E, int k, int32_t *ids,
+                        int64_t *ids64, float *w, uint32_t *err, hipStream_t s) {
+    hipLaunchKernelGGL(k_topk, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, logits,
+                       rows, E, k, ids, ids64, w, err);
+    return (int)hipGetLastError();
+}
+
+// ---------------- stable expert sort ----------------
+// Pairs q = 0..Tk-1 with expert ids[q]. Blocks of 256 consecutive pairs.
+//  hist   : rank[q] = #{q' < q in the block : ids[q'] == ids[q]},
+//           cnt[b][e] = number of pairs of expert e in block b;
+//  scan_e : cnt[b][e] -> exclusive prefix over b (per expert), tot[e];
+//  off    : off[e] = sum_{e' < e} min(tot[e'], cap);
+//  scatter: global rank g = cnt[b][e] + rank[q]; kept iff g < cap;
+//           perm[off[e] + g] = q.
+#define SQ 256
+__global__ __launch_bounds__(256) void k_sort_hist(const int32_t *__restrict__ ids, int Tk,
+                                                   int E, int32_t *__restrict__ rank,
+                                                   int32_t *__restrict__ cnt, uint32_t *err) {
+    __shared__ int sid[SQ];
+    const int b = blockIdx.x, t = threadIdx.x;
+    const int q = b * SQ + t;
+    int e = -1;
+    if (q < Tk) {
+        e = ids[q];
+        if (e < 0 || e >= E) {
+            raise_err(err, EF_BAD_ID);
+            e = -1;
+        }
+    }
+    sid[t] = e;
+    for (int i = t; i < E; i += 256) cnt[(int64_t)b * E + i] = 0;
+    __syncthreads();
+    int r = 0;
+    bool last = true;
+    for (int i = 0; i < SQ; i++) {
+        const int o = sid[i];
+        r += (i < t && o == e);
+        last &= !(i > t && o == e);
+    }
+    if (q < Tk) rank[q] = r;
+    __syncthreads();  // zeroing above must land before the counts
+    if (q < Tk && e >= 0 && last) cnt[(int64_t)b * E + e] = r + 1;
+}
+
+__global__ __launch_bounds__(256) void k_sort_scan_e(int32_t *__restrict__ cnt, int NB, int E,
+                                                     int32_t *__restrict__ tot) {
+    // one block per expert; sequential prefix in chunks of 256 with a block scan
+    __shared__ int buf[256];
+    const int e = blockIdx.x, t = threadIdx.x;
+    int carry = 0;
+    for (int b0 = 0; b0 < NB; b0 += 256) {
+        const int b = b0 + t;
+        const int v = b < NB ? cnt[(int64_t)b * E + e] : 0;
+        buf[t] = v;
+        __syncthreads();
+        for (int o = 1; o < 256; o <<= 1) {
+            const int x = t >= o ? buf[t - o] : 0;
+            __syncthreads();
+            buf[t] += x;
+            __syncthreads();
+        }
+        if (b < NB) cnt[(int64_t)b * E + e] = carry + buf[t] - v;
+        carry += buf[255];
+        __syncthreads();
+    }
+    if (t == 0) tot[e] = carry;
+}
+
+__global__ __launch_bounds__(1024) void k_sort_off(const int32_t *__restrict__ tot, int E,
+                                                   int64_t cap, int32_t *__restrict__ off,
+                                                   int64_t *__restrict__ off64) {
+    __shared__ int buf[1024];
+    const int t = threadIdx.x;
+    int carry = 0;
+    if (t == 0) {
+        off[0] = 0;
+        if (off64) off64[0] = 0;
+    }
+    for (int e0 = 0; e0 < E; e0 += 1024) {
+        const int e = e0 + t;
+        const int v = e < E ? (int)min((int64_t)tot[e], cap) : 0;
+        buf[t] = v;
+        __syncthreads();
+        for (int o = 1; o < 1024; o <<= 1) {
+            const int x = t >= o ? buf[t - o] : 0;
+            __syncthreads();
+            buf[t] += x;
+            __syncthreads();
+        }
+        if (e < E) {
+            off[e + 1] = carry + buf[t];
+            if (off64) off64[e + 1] = carry + buf[t];
+        }
+        carry += buf[1023];
+        __syncthreads();
+    }
+}
+
+__global__ __launch_bounds__(256) void k_sort_scatter(
+    const int32_t *__restrict__ ids, int Tk, int E, const int32_t *__restrict__ rank,
+    const int32_t *__restrict__ cnt, const int32_t *__restrict__ off, int64_t cap,
+    int32_t *__restrict__ perm, int64_t *__restrict__ perm64, uint8_t *__restrict__ drop) {
+    const int q = blockIdx.x * SQ + threadIdx.x;
+    if (q >= Tk) return;
+    const int e = ids[q];
+    if (e < 0 || e >= E) return;
+    const int64_t g = (int64_t)cnt[(int64_t)blockIdx.x * E + e] + rank[q];
+    const bool kept = g < cap;
+    if (drop) drop[q] = kept ? 0 : 1;
+    if (kept) {
+        perm[off[e] + g] = q;
+        if (perm64) perm64[off[e] + g] = q;
+    }
+}
+
+extern "C" int jtk_sort(const int32_t *ids, int Tk, int E, int64_t cap, int32_t *rank,
+                        int32_t *cnt, int32_t *tot, int32_t *off, int64_t *off64,
+                        int32_t *perm, int64_t *perm64, uint8_t *drop, uint32_t *err,
+                        hipStream_t s) {
+    const int NB = (Tk + SQ - 1) / SQ;
+    hipLaunchKernelGGL(k_sort_hist, dim3((unsigned)NB), dim3(256), 0, s, ids, Tk, E, rank,
+                       cnt, err);
+    hipLaunchKernelGGL(k_sort_scan_e, dim3((unsigned)E), dim3(256), 0, s, cnt, NB, E, tot);
+    hipLaunchKernelGGL(k_sort_off, dim3(1), dim3(1024), 0, s, tot, E, cap, off, off64);
+    hipLaunchKernelGGL(k_sort_scatter, dim3((unsigned)NB), dim3(256), 0, s, ids, Tk, E, rank,
+                       cnt, off, cap, perm, perm64, drop);
+    return (int)hipGetLastError();
+}
+
+// ---------------- grouped-GEMM work list ----------------
+// tiles[i] = (e << 16) | j for the j-th 64-row tile of expert e, experts in
+// ascending order; *ntiles = total.
+__global__ __launch_bounds__(1024) void k_make_tiles(const int32_t *__restrict__ off, int E,
+                                                     int32_t *__restrict__ tiles,
+                                                     int32_t *__restrict__ ntiles) {
+    __shared__ int buf[1024];
+    const int t = threadIdx.x;
+    int carry = 0;
+    for (int e0 = 0; e0 < E; e0 += 1024) {
+        const int e = e0 + t;
+        const int nt = e < E ? (off[e + 1] - off[e] + 63) / 64 : 0;
+        buf[t] = nt;
+        __syncthreads();
+        for (int o = 1; o < 1024; o <<= 1) {
+            const int x = t >= o ? buf[t - o] : 0;
+            __syncthreads();
+            buf[t] += x;
+            __syncthreads();
+        }
+        const int start = carry + buf[t] - nt;
+        for (int j = 0; j < nt; j++) tiles[start + j] = (e << 16) | j;
+        carry += buf[1023];
+        __syncthreads();
+    }
+    if (t == 0) *ntiles = carry;
+}
+
+extern "C" int jtk_make_tiles(const int32_t *off, int E, int32_t *tiles, int32_t *ntiles,
+                              hipStream_t s) {
+    hipLaunchKernelGGL(k_make_tiles, dim3(1), dim3(1024), 0, s, off, E, tiles, ntiles);
+    return (int)hipGetLastError();
+}
+
+// ---------------- combine ----------------
+// One thread per 4 consecutive outputs of a token. drop may be NULL
+// (dropless); dropped slots contribute nothing (src/moe_layer.c:1449-1451).
+__global__ __launch_bounds__(256) void k_combine(const float *__restrict__ w,
+                                                 const float *__restrict__ Ye,
+                                                 const uint8_t *__restrict__ drop,
+                                                 const float *__restrict__ Ys, int S, int T,
+                                                 int k, int n, float *__restrict__ Y,
+                                                 uint32_t *err) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int nq = n / 4;
+    if (idx >= (int64_t)T * nq) return;
+    const int t = (int)(idx / nq), j = (int)(idx % nq) * 4;
+    double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
+    for (int p = 0; p < k; p++) {
+        const int64_t q = (int64_t)t * k + p;
+        if (drop && drop[q]) continue;
+        const double wp = (double)w[q];
+        const float4 y = *(const float4 *)(Ye + q * n + j);
+        a0 = fma(wp, (double)y.x, a0);
+        a1 = fma(wp, (double)y.y, a1);
+        a2 = fma(wp, (double)y.z, a2);
+        a3 = fma(wp, (double)y.w, a3);
+    }
+    for (int s = 0; s < S; s++) {
+        const float4 y = *(const float4 *)(Ys + ((int64_t)s * T + t) * n + j);
+        a0 += (double)y.x;
+        a1 += (double)y.y;
+        a2 += (double)y.z;
+        a3 += (double)y.w;
+    }
+    if (!isfinite(a0) || !isfinite(a1) || !isfinite(a2) || !isfinite(a3))
+        raise_err(err, EF_NONFINITE_MID);
+    *(float4 *)(Y + (int64_t)t * n + j) = make_float4((float)a0, (float)a1, (float)a2, (float)a3);
+}
+
+// Scalar variant for n % 4 != 0 (legacy shapes).
+__global__ __launch_bounds__(256) void k_combine1(const float *__restrict__ w,
+                                                  const float *__restrict__ Ye,
+                                                  const uint8_t *__restrict__ drop,
+                                                  const float *__restrict__ Ys, int S, int T,
+                                                  int k, int n, float *__restrict__ Y,
+                                                  uint32_t *err) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (int64_t)T * n) return;
+    const int t = (int)(idx / n), j = (int)(idx % n);
+    double a = 0.0;
+    for (int p = 0; p < k; p++) {
+        const int64_t q = (int64_t)t * k + p;
+        if (drop && drop[q]) continue;
+        a = fma((double)w[q], (double)Ye[q * n + j], a);
+    }
+    for (int s = 0; s < S; s++) a += (double)Ys[((int64_t)s * T + t) * n + j];
+    if (!isfinite(a)) raise_err(err, EF_NONFINITE_MID);
+    Y[idx] = (float)a;
+}
+
+extern "C" int jtk_combine(const float *w, const float *Ye, const uint8_t *drop,
+                           const float *Ys, int S, int T, int k, int n, float *Y,
+                           uint32_t *err, hipStream_t s) {
+    if (n % 4 == 0) {
+        const int64_t th = (int64_t)T * (n / 4);
+        hipLaunchKernelGGL(k_combine, dim3((unsigned)((th + 255) / 256)), dim3(256), 0, s, w,
+                           Ye, drop, Ys, S, T, k, n, Y, err);
+    } else {
+        const int64_t th = (int64_t)T * n;
+        hipLaunchKernelGGL(k_combine1, dim3((unsigned)((th + 255) / 256)), dim3(256), 0, s, w,
+                           Ye, drop, Ys, S, T, k, n, Y, err);
+    }
+    return (int)hipGetLastError();
+}
+
+// ---------------- helpers for the legacy layer ----------------
+// Renormalise kept weights of tokens with drops (src/moe_layer.c:1171-1201).
+__global__ __launch_bounds__(256) void k_renorm(float *__restrict__ w,
+                                                const uint8_t *__restrict__ drop, int T,
+                                                int k, uint32_t *err) {
+    const int t = blockIdx.x * 256 + threadIdx.x;
+    if (t >= T) return;
+    double s = 0.0;
+    int nd = 0;
+    for (int p = 0; p < k; p++) {
+        const int64_t q = (int64_t)t * k + p;
+        if (drop[q]) nd++;
+        else s += (double)w[q];
+    }
+    if (nd > 0 && s > 0.0) {
+        if (!isfinite(s)) {
+            raise_err(err, EF_NONFINITE_MID);
+            return;
+        }
+        for (int p = 0; p < k; p++) {
+            const int64_t q = (int64_t)t * k + p;
+            if (drop[q]) continue;
+            const double rw = (double)w[q] / s;
+            if (!isfinite(rw) || rw < 0.0) raise_err(err, EF_NONFINITE_MID);
+            w[q] = (float)rw;
+        }
+    }
+}
+
+extern "C" int jtk_renorm(float *w, const uint8_t *drop, int T, int k, uint32_t *err,
+                          hipStream_t s) {
+    hipLaunchKernelGGL(k_renorm, dim3((unsigned)((T + 255) / 256)), dim3(256), 0, s, w, drop,
+                       T, k, err);
+    return (int)hipGetLastError();
+}
+
+// dst[r][:] = src[idx(r)][:] with idx(r) = perm[base + r] / div (fp32 rows).
+__global__ __launch_bounds__(256) void k_gather_rows(const float *__restrict__ src, int n,
+                                                     const int32_t *__restrict__ perm,
+                                                     int base, int div, int rows,
+                                                     float *__restrict__ dst) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)rows * n) return;
+    const int r = (int)(i / n), c = (int)(i % n);
+    const int sr = perm[base + r] / div;
+    dst[i] = src[(int64_t)sr * n + c];
+}
+
+// dst[perm[base + r]][:] = src[r][:].
+__global__ __launch_bounds__(256) void k_scatter_rows(const float *__restrict__ src, int n,
+                                                      const int32_t *__restrict__ perm,
+                                                      int base, int rows,
+                                                      float *__restrict__ dst) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)rows * n) return;
+    const int r = (int)(i / n), c = (int)(i % n);
+    dst[(int64_t)perm[base + r] * n + c] = src[i];
+}
+
+extern "C" int jtk_gather_rows(const float *src, int n, const int32_t *perm, int base,
+                               int div, int rows, float *dst, hipStream_t s) {
+    const int64_t th = (int64_t)rows * n;
+    if (th <= 0) return 0;
+    hipLaunchKernelGGL(k_gather_rows, dim3((unsigned)((th + 255) / 256)), dim3(256), 0, s, src,
+                       n, perm, base, div, rows, dst);
+    return (int)hipGetLastError();
+}
+
+extern "C" int jtk_scatter_rows(const float *src, int n, const int32_t *perm, int base,
+                                int rows, float *dst, hipStream_t s) {
+    const int64_t th = (int64_t)rows * n;
+    if (th <= 0) return 0;
+    hipLaunchKernelGGL(k_scatter_rows, dim3((unsigned)((th + 255) / 256)), dim3(256), 0, s,
+                       src, n, perm, base, rows, dst);
+    return (int)hipGetLastError();
+}
+
+// Elementwise SwiGLU of two fp32 tiles (src/moe_layer.c:129-157).
+__global__ __launch_bounds__(256) void k_silu_tile(const float *__restrict__ G,
+                                                   const float *__restrict__ U, int64_t n,
+                                                   float *__restrict__ S, uint32_t *err) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    float s;
+    if (!silu_mul(G[i], U[i], &s)) raise_err(err, EF_NONFINITE_MID);
+    S[i] = s;
+}
+
+extern "C" int jtk_silu_tile(const float *G, const float *U, int64_t n, float *S,
+                             uint32_t *err, hipStream_t s) {
+    if (n <= 0) return 0;
+    hipLaunchKernelGGL(k_silu_tile, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, G, U,
+                       n, S, err);
+    return (int)hipGetLastError();
+}
+
+// Fill with zero (graph-safe replacement for a memset).
+__global__ __launch_bounds__(256) void k_zero_u32(uint32_t *__restrict__ p, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+extern "C" int jtk_zero_u32(uint32_t *p, int64_t n, hipStream_t s) {
+    if (n <= 0) return 0;
+    hipLaunchKernelGGL(k_zero_u32, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p, n);
+    return (int)hipGetLastError();
+}
+
+// dst[i] = *src for i < n (a device scalar broadcast, e.g. one per-tensor
+// scale repeated per row).
+__global__ __launch_bounds__(256) void k_bcast_f32(float *__restrict__ dst, int64_t n,
+                                                   const float *__restrict__ src) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) dst[i] = *src;
+}
+
+extern "C" int jtk_bcast_f32(float *dst, int64_t n, const float *src, hipStream_t s) {
+    if (n <= 0) return 0;
+    hipLaunchKernelGGL(k_bcast_f32, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, dst, n,
+                       src);
+    return (int)hipGetLastError();
+}

@@ -1,0 +1,154 @@
+"""GPU parity of the prepared quantised MoE layer (jt_hip_moe_*) and the
+W8A8 SwiGLU expert (jt_hip_ffn_*) against the oracle.
+
+Integer/index outputs (quantised codes, routing ids, sort permutation,
+expert offsets) must be identical. fp32 outputs must agree within
+rtol 1e-5 (atol 1e-5 * max|Y|): the only source of difference is the device
+fp64 exp() used by the softmax and SwiGLU versus glibc's, which the test
+also counts (expected: zero or a handful of last-bit differences).
+"""
+import numpy as np
+import pytest
+
+from conftest import announce, zipf_ids
+
+pytestmark = pytest.mark.gpu
+
+
+def mk_weights(rng, n, h, E, S, hs, scale=1.0):
+    f = np.float32
+    Wgate = (rng.standard_normal((E, n)) / np.sqrt(n)).astype(f)
+    Wg = (rng.standard_normal((E, h, n)) * scale / np.sqrt(n)).astype(f)
+    Wu = (rng.standard_normal((E, h, n)) * scale / np.sqrt(n)).astype(f)
+    Wd = (rng.standard_normal((E, h, n)) * scale / np.sqrt(h)).astype(f)
+    if S:
+        sh = [(rng.standard_normal((S, hs, n)) / np.sqrt(n)).astype(f),
+              (rng.standard_normal((S, hs, n)) / np.sqrt(n)).astype(f),
+              (rng.standard_normal((S, hs, n)) / np.sqrt(hs)).astype(f)]
+    else:
+        sh = [None, None, None]
+    return Wgate, Wg, Wu, Wd, sh
+
+
+def close(Y, Y2):
+    tol = 1e-5 * max(float(np.abs(Y2).max()), 1e-30)
+    np.testing.assert_allclose(Y, Y2, rtol=1e-5, atol=tol)
+    return int((Y.view(np.uint32) != Y2.view(np.uint32)).sum())
+
+
+def dev(torch, a):
+    return None if a is None else torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def run_layer(jt, torch, n, h, E, k, S, hs, T, W, X, ids=None, w=None):
+    Wgate, Wg, Wu, Wd, sh = W
+    L = jt.MoE(n, h, E, k, S, hs, T, dev(torch, Wgate), dev(torch, Wg), dev(torch, Wu),
+               dev(torch, Wd), dev(torch, sh[0]), dev(torch, sh[1]), dev(torch, sh[2]))
+    dX = dev(torch, X)
+    dY = torch.zeros((T, n), dtype=torch.float32, device="cuda")
+    if ids is None:
+        rc = L.fwd(dX, dY)
+    else:
+        rc = L.fwd_routed(dX, dev(torch, ids), dev(torch, w), dY)
+    assert rc == 0
+    assert jt.sync_errors() == 0
+    return L, dY.cpu().numpy()
+
+
+def read_buf(torch, L, which, dtype, shape):
+    return L.read(which, dtype, shape)
+
+
+CASES = [
+    # n, h, E, k, S, hs, T
+    (128, 64, 8, 2, 2, 64, 37),
+    (256, 128, 16, 4, 1, 192, 200),
+    (128, 64, 32, 8, 0, 64, 16),
+    (256, 64, 64, 8, 2, 128, 1),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"n{c[0]}h{c[1]}E{c[2]}k{c[3]}S{c[4]}T{c[6]}"
+                                              for c in CASES])
+def test_layer_router_parity(jt, orc, torch_cuda, case):
+    torch = torch_cuda
+    n, h, E, k, S, hs, T = case
+    announce(f"moe layer router {case}")
+    rng = np.random.default_rng(sum(case))
+    W = mk_weights(rng, n, h, E, S, hs)
+    X = rng.standard_normal((T, n)).astype(np.float32)
+    L, Y = run_layer(jt, torch, n, h, E, k, S, hs, T, W, X)
+    OL = orc.moe_q(n, h, E, k, S, hs, W[0], W[1], W[2], W[3], *W[4])
+    o = OL.fwd(X)
+    assert o["rc"] == 0
+    ids = read_buf(torch, L, jt.BUF_IDS, np.int32, (T, k))
+    wts = read_buf(torch, L, jt.BUF_WEIGHTS, np.float32, (T, k))
+    perm = read_buf(torch, L, jt.BUF_PERM, np.int32, (T * k,))
+    off = read_buf(torch, L, jt.BUF_OFF, np.int32, (E + 1,))
+    assert np.array_equal(ids, o["ids"])
+    np.testing.assert_allclose(wts, o["w"], rtol=1e-6, atol=0)
+    assert np.array_equal(off, o["off"]) and np.array_equal(perm, o["perm"])
+    for e in (0, E - 1):
+        gu, gus, dc, ds = L.export_routed(e)
+        ogu, ogus, odc, ods = OL.routed_codes(e)
+        assert np.array_equal(gu, ogu) and np.array_equal(gus, ogus)
+        assert np.array_equal(dc, odc) and np.array_equal(ds, ods)
+    diff = close(Y, o["Y"])
+    print(f"  last-bit differences in Y: {diff} of {Y.size}")
+
+
+@pytest.mark.parametrize("T", [1, 4, 16, 130])
+def test_layer_zipf_routed_parity(jt, orc, torch_cuda, T):
+    torch = torch_cuda
+    n, h, E, k, S, hs = 256, 128, 64, 8, 1, 128
+    announce(f"moe layer zipf-routed T={T}")
+    rng = np.random.default_rng(100 + T)
+    W = mk_weights(rng, n, h, E, S, hs)
+    X = rng.standard_normal((T, n)).astype(np.float32)
+    ids, w = zipf_ids(rng, T, k, E)
+    L, Y = run_layer(jt, torch, n, h, E, k, S, hs, T, W, X, ids, w)
+    o = orc.moe_q(n, h, E, k, S, hs, None, W[1], W[2], W[3], *W[4]).fwd(X, ids, w)
+    assert o["rc"] == 0
+    Ye = read_buf(torch, L, jt.BUF_YE, np.float32, (T * k, n))
+    close(Ye, o["Ye"])
+    close(Y, o["Y"])
+
+
+def test_layer_full_size_token_sample(jt, orc, torch_cuda):
+    """Full-layer prefill shape (T=4096, d=1024, E=256, f=256, k=8, two shared
+    f=2816 experts). Tokens are independent in the dropless layer, so the
+    oracle runs on a sample of 32 tokens and must match those rows."""
+    torch = torch_cuda
+    n, h, E, k, S, hs, T = 1024, 256, 256, 8, 2, 2816, 4096
+    announce("moe layer full size, 32-token sample")
+    rng = np.random.default_rng(4096)
+    W = mk_weights(rng, n, h, E, S, hs)
+    X = rng.standard_normal((T, n)).astype(np.float32)
+    L, Y = run_layer(jt, torch, n, h, E, k, S, hs, T, W, X)
+    off = read_buf(torch, L, jt.BUF_OFF, np.int32, (E + 1,))
+    assert off[0] == 0 and off[-1] == T * k and np.all(np.diff(off) >= 0)
+    sample = np.sort(rng.choice(T, 32, replace=False))
+    o = orc.moe_q(n, h, E, k, S, hs, W[0], W[1], W[2], W[3], *W[4]).fwd(X[sample])
+    assert o["rc"] == 0
+    ids = read_buf(torch, L, jt.BUF_IDS, np.int32, (T, k))
+    assert np.array_equal(ids[sample], o["ids"])
+    close(Y[sample], o["Y"])
+
+
+@pytest.mark.parametrize("M", [1, 4, 16, 17, 100])
+def test_ffn_shared_expert_parity(jt, orc, torch_cuda, M):
+    torch = torch_cuda
+    n, h = 1024, 2816
+    announce(f"ffn n={n} h={h} M={M}")
+    rng = np.random.default_rng(M)
+    Wg = (rng.standard_normal((h, n)) / 32).astype(np.float32)
+    Wu = (rng.standard_normal((h, n)) / 32).astype(np.float32)
+    Wd = (rng.standard_normal((h, n)) / 53).astype(np.float32)
+    X = rng.standard_normal((M, n)).astype(np.float32)
+    F = jt.FFN(dev(torch, Wg), dev(torch, Wu), dev(torch, Wd))
+    dY = torch.zeros((M, n), dtype=torch.float32, device="cuda")
+    F.fwd(dev(torch, X), dY)
+    assert jt.sync_errors() == 0
+    rc, Y2 = orc.ffn_fwd(Wg, Wu, Wd, X)
+    assert rc == 0
+    close(dY.cpu().numpy(), Y2)
