@@ -1,17 +1,19 @@
 // int8 GEMM kernels for gfx950: W8A8 (per-channel weights, per-row
 // activations) and the grouped low-bit routed-expert GEMM.
 //
-// Arithmetic (identical in every kernel of this file):
+// Arithmetic:
 //   acc   = sum_k A[m][k] * W[n][k] in int32 (order-free, exact);
 //   W8A8  : C = (float)((double)acc * ((double)sA[m] * (double)sB[n]))
 //           -- the reference's epilogue, src/w8a8.c:664-676;
 //   low-bit: per 64-K group g the int32 partial acc_g is taken out of the
-//           MFMA and T += (double)acc_g * (double)f16 scale[n][g] in g order
-//           (the product is exact in fp64, so fma and mul+add agree);
-//           C = (float)(T * (double)sA[m]).
-// The matrix instruction is v_mfma_i32_16x16x64_i8; weights arrive in the
-// 16-channel x 64-K panel layout of jt_dev.h so each operand fragment is one
-// coalesced 16-byte (int8), 8-byte (INT4) or 4-byte (INT2) load per lane.
+//           MFMA and T = fmaf((float)acc_g, scale[n][g], T) in g order
+//           (|acc_g| < 2^24, so the float conversion is exact);
+//           C = T * sA[m].
+// The matrix instruction is v_mfma_i32_16x16x64_i8 (4.3 POPS sustained per
+// MI355X). Weights arrive in the 16-channel x 64-K panel layout of jt_dev.h,
+// whose byte order equals the MFMA operand layout, so operand panels are
+// copied global -> LDS with global_load_lds_dwordx4 (lane i's 16 bytes land
+// at LDS base + 16*i) and read back with one ds_read_b128 per lane.
 #include "jt_dev.h"
 #include "jt_launch.h"
 
@@ -20,53 +22,104 @@
 
 enum { EPI_PLAIN = 0, EPI_SWIGLU = 1, EPI_SCATTER = 2 };
 
+typedef __attribute__((address_space(3))) void lds_void;
+
+// One LDS-DMA copy: each lane moves BYTES bytes from its own global address
+// to lds_base + BYTES * lane (lds_base is wave-uniform).
+template <int BYTES>
+__device__ __forceinline__ void dma(const void *g, void *lds_base);
+template <>
+__device__ __forceinline__ void dma<16>(const void *g, void *lds_base) {
+    __builtin_amdgcn_global_load_lds(g, (lds_void *)lds_base, 16, 0, 0);
+}
+template <>
+__device__ __forceinline__ void dma<4>(const void *g, void *lds_base) {
+    __builtin_amdgcn_global_load_lds(g, (lds_void *)lds_base, 4, 0, 0);
+}
+
+// Wait until at most N vector-memory operations of this wave are in flight.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Workgroup barrier without the memory fence of __syncthreads(): the fence
+// would drain every in-flight LDS-DMA stage (s_waitcnt vmcnt(0)). Callers
+// first wait for their own stage with wait_vm, after which the DMA data is in
+// LDS, which all waves of the workgroup see after the barrier.
+__device__ __forceinline__ void barrier_lds() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Stage s of a K loop of length KB was issued before the loads of the
+// min(NST - 2, KB - 1 - s) later stages; wait for s only.
+template <int NST, int PER>
+__device__ __forceinline__ void wait_stage(int later) {
+    if (NST >= 4 && later >= 2) {
+        wait_vm<(NST >= 4 ? 2 : 0) * PER>();
+    } else if (later >= 1) {
+        wait_vm<PER>();
+    } else {
+        wait_vm<0>();
+    }
+}
+
 // ===================== dense W8A8 MFMA GEMM =====================
-// Block tile 128 x 128, K step 64, 4 waves in a 2 x 2 grid of 64 x 64 wave
-// tiles (4 x 4 MFMA tiles each). A [M][lda] row-major int8 (lda >= Kp,
-// Kp % 64 == 0, bytes beyond K are zero), W panels padded to Np (multiple of
-// 128) channels.
+// Block tile 128 x 128, 4 waves as 2 x 2 wave tiles of 64 x 64 (4 x 4 MFMA
+// tiles), K step 64, a ring of NST LDS stages (16 KiB each: 8 A panels and
+// 8 W panels) filled by LDS-DMA NST-1 steps ahead. Each wave copies 4 of
+// the 16 panels of a stage. A [M][lda] row-major int8 (lda >= Kp,
+// Kp % 64 == 0, zero padding past K); W panels padded to Np (multiple of
+// 128) channels. Tiles are ordered channel-block-major and, when the tile
+// count is a multiple of 8, dealt to the 8 XCDs in contiguous chunks so the
+// blocks sharing a weight column block share an L2.
 #define GB_M 128
 #define GB_N 128
+#define GB_NST 4
 
 template <int EPI>
 __global__ __launch_bounds__(256, 2) void k_w8a8_mfma(
     const int8_t *__restrict__ A, int lda, const float *__restrict__ sA,
     const int8_t *__restrict__ Wp, const float *__restrict__ sB, int M, int N, int Kp,
-    float *__restrict__ C, int ldc, uint32_t *err) {
-    __shared__ __attribute__((aligned(16))) int8_t As[2][GB_M * 64];
-    __shared__ __attribute__((aligned(16))) int8_t Bs[2][GB_N * 64];
+    float *__restrict__ C, int ldc, uint32_t *err, int mtiles, int ntiles) {
+    __shared__ __attribute__((aligned(1024))) int8_t smem[GB_NST * 16 * 1024];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int m0 = blockIdx.x * GB_M, n0 = blockIdx.y * GB_N;
+    const int total = mtiles * ntiles;
+    int tile = blockIdx.x;
+    if ((total & 7) == 0) tile = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
+    const int mt = tile % mtiles, nt = tile / mtiles;
+    const int m0 = mt * GB_M, n0 = nt * GB_N;
     const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
     const int KB = Kp / 64;
 
-    // A tile loader: thread t covers rows t/4 and t/4+64, 16-byte chunk t%4.
-    const int a_r = tid >> 2, a_kc = tid & 3;
-    int ra0 = m0 + a_r, ra1 = m0 + a_r + 64;
-    ra0 = ra0 < M ? ra0 : M - 1;
-    ra1 = ra1 < M ? ra1 : M - 1;
-    const int8_t *a_src0 = A + (int64_t)ra0 * lda + a_kc * 16;
-    const int8_t *a_src1 = A + (int64_t)ra1 * lda + a_kc * 16;
-    // LDS position (panel layout): panel = row/16, lane = kc*16 + row%16
-    const int a_dst0 = (a_r >> 4) * 1024 + (a_kc * 16 + (a_r & 15)) * 16;
-    const int a_dst1 = a_dst0 + 4 * 1024;
-    // B tile loader: 8 panels x 1 KiB; thread t copies bytes [16t, 16t+16) and
-    // [16t + 4096, ...), i.e. panels t/64 and t/64 + 4.
-    const int64_t panel_stride = (int64_t)KB * 1024;
-    const int b_p = tid >> 6;
-    const int8_t *b_src0 = Wp + (int64_t)(n0 / 16 + b_p) * panel_stride + lane * 16;
-    const int8_t *b_src1 = b_src0 + 4 * panel_stride;
-
-    v4i ra, rb, rc, rd;
-    ra = *(const v4i *)(a_src0);
-    rb = *(const v4i *)(a_src1);
-    rc = *(const v4i *)(b_src0);
-    rd = *(const v4i *)(b_src1);
-    *(v4i *)(&As[0][a_dst0]) = ra;
-    *(v4i *)(&As[0][a_dst1]) = rb;
-    *(v4i *)(&Bs[0][tid * 16]) = rc;
-    *(v4i *)(&Bs[0][tid * 16 + 4096]) = rd;
-    __syncthreads();
+    // this wave copies panels 4*wave .. 4*wave+3 of every stage
+    // (panels 0-7 = A rows m0+16p.., 8-15 = W channels n0+16(p-8)..)
+    const int8_t *src[4];
+    int64_t step[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int p = wave * 4 + i;
+        if (p < 8) {
+            int r = m0 + p * 16 + (lane & 15);
+            r = r < M ? r : M - 1;
+            src[i] = A + (int64_t)r * lda + (lane >> 4) * 16;
+            step[i] = 64;
+        } else {
+            src[i] = Wp + ((int64_t)(n0 / 16 + p - 8) * KB) * 1024 + lane * 16;
+            step[i] = 1024;
+        }
+    }
+    auto issue = [&](int kb) {
+        int8_t *st = smem + (kb % GB_NST) * 16384;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            dma<16>(src[i] + (int64_t)kb * step[i], st + (wave * 4 + i) * 1024);
+    };
+#pragma unroll
+    for (int s = 0; s < GB_NST - 1; s++)
+        if (s < KB) issue(s);
 
     v4i acc[4][4];
 #pragma unroll
@@ -75,33 +128,20 @@ __global__ __launch_bounds__(256, 2) void k_w8a8_mfma(
         for (int j = 0; j < 4; j++) acc[i][j] = (v4i){0, 0, 0, 0};
 
     for (int kb = 0; kb < KB; kb++) {
-        const int cur = kb & 1;
-        const bool more = kb + 1 < KB;
-        if (more) {
-            const int64_t koff = (int64_t)(kb + 1) * 64;
-            ra = *(const v4i *)(a_src0 + koff);
-            rb = *(const v4i *)(a_src1 + koff);
-            rc = *(const v4i *)(b_src0 + (kb + 1) * 1024);
-            rd = *(const v4i *)(b_src1 + (kb + 1) * 1024);
-        }
+        wait_stage<GB_NST, 4>(min(GB_NST - 2, KB - 1 - kb));
+        barrier_lds();
+        if (kb + GB_NST - 1 < KB) issue(kb + GB_NST - 1);
+        const int8_t *st = smem + (kb % GB_NST) * 16384;
         v4i af[4], bf[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-            af[i] = *(const v4i *)(&As[cur][((wm >> 4) + i) * 1024 + lane * 16]);
+        for (int i = 0; i < 4; i++) af[i] = *(const v4i *)(st + ((wm >> 4) + i) * 1024 + lane * 16);
 #pragma unroll
         for (int j = 0; j < 4; j++)
-            bf[j] = *(const v4i *)(&Bs[cur][((wn >> 4) + j) * 1024 + lane * 16]);
+            bf[j] = *(const v4i *)(st + (8 + (wn >> 4) + j) * 1024 + lane * 16);
 #pragma unroll
         for (int i = 0; i < 4; i++)
 #pragma unroll
             for (int j = 0; j < 4; j++) acc[i][j] = mfma16x16x64(af[i], bf[j], acc[i][j]);
-        if (more) {
-            *(v4i *)(&As[cur ^ 1][a_dst0]) = ra;
-            *(v4i *)(&As[cur ^ 1][a_dst1]) = rb;
-            *(v4i *)(&Bs[cur ^ 1][tid * 16]) = rc;
-            *(v4i *)(&Bs[cur ^ 1][tid * 16 + 4096]) = rd;
-        }
-        __syncthreads();
     }
 
     // epilogue
@@ -263,13 +303,14 @@ extern "C" int jtk_w8a8_gemm(const int8_t *A, int lda, const float *sA, const in
         }
 #undef GEMV
     } else {
-        dim3 grid((unsigned)((M + GB_M - 1) / GB_M), (unsigned)(Np / GB_N));
+        const int mt = (M + GB_M - 1) / GB_M, nt = Np / GB_N;
+        dim3 grid((unsigned)(mt * nt));
         if (swiglu)
             hipLaunchKernelGGL((k_w8a8_mfma<EPI_SWIGLU>), grid, dim3(256), 0, s, A, lda, sA, Wp,
-                               sB, M, N, Kp, C, ldc, err);
+                               sB, M, N, Kp, C, ldc, err, mt, nt);
         else
             hipLaunchKernelGGL((k_w8a8_mfma<EPI_PLAIN>), grid, dim3(256), 0, s, A, lda, sA, Wp,
-                               sB, M, N, Kp, C, ldc, err);
+                               sB, M, N, Kp, C, ldc, err, mt, nt);
     }
     return (int)hipGetLastError();
 }
@@ -281,8 +322,17 @@ extern "C" int jtk_w8a8_gemm(const int8_t *A, int lda, const float *sA, const in
 //       output S[pos][hidden] (ldo = h);
 //   down    (BITS 4, EPI_SCATTER): A row = Sq[pos], sA = ss[pos],
 //       output Ye[perm[pos]][col] (ldo = n).
-// Waves split the 128 channels (32 each = 2 panels); all four share the
-// 64-row A tile through LDS (double-buffered per 64-K group).
+// Each 64-K group is one pipeline stage in LDS: the 4 gathered A panels
+// (one per wave, LDS-DMA with per-lane row addresses) and the 8 weight
+// panel-groups of the 128 channels (raw bytes, 256 B per DMA). Waves split
+// the 128 channels (32 each = 2 panels); B fragments are unpacked from LDS
+// to signed int8 in registers.
+#define LB_NST 4
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
 template <int BITS, int EPI>
 __global__ __launch_bounds__(256, 2) void k_lowbit_grouped(
     const int8_t *__restrict__ A, int lda, const float *__restrict__ sA,
@@ -290,7 +340,12 @@ __global__ __launch_bounds__(256, 2) void k_lowbit_grouped(
     const int32_t *__restrict__ tiles, const int32_t *__restrict__ ntiles,
     const uint8_t *__restrict__ Wp, const uint16_t *__restrict__ Ws, int64_t wp_stride,
     int64_t ws_stride, int N, int K, float *__restrict__ out, int ldo, uint32_t *err) {
-    __shared__ __attribute__((aligned(16))) int8_t As[2][64 * 64];
+    constexpr int PB = BITS == 2 ? 256 : 512;       // bytes per panel-group
+    constexpr int BDMA = PB / 256;                  // 256-byte DMAs per panel-group
+    constexpr int SOFF = 4096 + 8 * PB;             // scales after A and weight bytes
+    constexpr int STAGE = SOFF + 4 * 256;           // + one 256-byte scale slot per wave
+    constexpr int PER = 2 + 2 * BDMA;               // DMAs per wave per stage
+    __shared__ __attribute__((aligned(1024))) int8_t smem[LB_NST * STAGE];
     __shared__ int rowsrc[64];
     __shared__ float rowscale[64];
     __shared__ int rowdst[64];
@@ -318,51 +373,66 @@ __global__ __launch_bounds__(256, 2) void k_lowbit_grouped(
     __syncthreads();
     const int G = K / 64;
     const int n0 = blockIdx.y * 128;
-    // A loader: thread t -> row t/4, chunk t%4 (one 16-byte load per group)
-    const int a_r = tid >> 2, a_kc = tid & 3;
-    const int8_t *a_src = A + (int64_t)rowsrc[a_r] * lda + a_kc * 16;
-    const int a_dst = (a_r >> 4) * 1024 + (a_kc * 16 + (a_r & 15)) * 16;
-    // this wave's two panels
-    const int pan0 = (n0 >> 4) + wave * 2;
-    constexpr int PB = BITS == 2 ? 256 : 512;  // bytes per panel-group
+    // A: wave w copies panel w (rows 16w..16w+15) of every stage;
+    // lane l = kc*16 + r -> row 16w + r, bytes [16kc, 16kc+16) of the group
+    const int8_t *a_src = A + (int64_t)rowsrc[wave * 16 + (lane & 15)] * lda + (lane >> 4) * 16;
+    // B: wave w copies the panel-groups of panels pb0 + 2w and pb0 + 2w + 1
+    const int pb0 = n0 >> 4;
     const uint8_t *wbase = Wp + (int64_t)e * wp_stride;
-    const uint16_t *sbase = Ws + (int64_t)e * ws_stride;
-    const uint8_t *wq0 = wbase + (int64_t)pan0 * G * PB + lane * (PB / 64);
-    const uint8_t *wq1 = wq0 + (int64_t)G * PB;
-    const uint16_t *sc0 = sbase + (int64_t)pan0 * G * 16 + (lane & 15);
-    const uint16_t *sc1 = sc0 + (int64_t)G * 16;
+    const uint8_t *b_src0 = wbase + (int64_t)(pb0 + 2 * wave) * G * PB + lane * 4;
+    const uint8_t *b_src1 = b_src0 + (int64_t)G * PB;
+    // this wave's two panels (absolute panel index within the expert)
+    const int pan0 = pb0 + wave * 2;
+    // fp16 group scales of the two panels: lanes 0-7 copy panel pan0's 16
+    // values (2 per lane), lanes 8-15 panel pan0+1's; lanes 16-63 repeat them
+    // (the 4-byte DMA always writes 64 lanes)
+    const int sl = lane & 15;
+    const uint8_t *s_src = (const uint8_t *)(Ws + (int64_t)e * ws_stride +
+                                             (int64_t)(pan0 + (sl >> 3)) * G * 16) +
+                           (sl & 7) * 4;
+    auto issue = [&](int g) {
+        int8_t *st = smem + (g % LB_NST) * STAGE;
+        dma<16>(a_src + (int64_t)g * 64, st + wave * 1024);
+#pragma unroll
+        for (int d = 0; d < BDMA; d++) {
+            dma<4>(b_src0 + (int64_t)g * PB + d * 256, st + 4096 + (2 * wave) * PB + d * 256);
+            dma<4>(b_src1 + (int64_t)g * PB + d * 256, st + 4096 + (2 * wave + 1) * PB + d * 256);
+        }
+        dma<4>(s_src + (int64_t)g * 32, st + SOFF + wave * 256);
+    };
+#pragma unroll
+    for (int s = 0; s < LB_NST - 1; s++)
+        if (s < G) issue(s);
 
-    *(v4i *)(&As[0][a_dst]) = *(const v4i *)(a_src);
-    double T[4][2][4];
+    float T[4][2][4];
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int j = 0; j < 2; j++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) T[i][j][r] = 0.0;
-    __syncthreads();
+            for (int r = 0; r < 4; r++) T[i][j][r] = 0.0f;
 
     for (int g = 0; g < G; g++) {
-        const int cur = g & 1;
-        v4i an;
-        if (g + 1 < G) an = *(const v4i *)(a_src + (int64_t)(g + 1) * 64);
+        wait_stage<LB_NST, PER>(min(LB_NST - 2, G - 1 - g));
+        barrier_lds();
+        if (g + LB_NST - 1 < G) issue(g + LB_NST - 1);
+        const int8_t *st = smem + (g % LB_NST) * STAGE;
+        const uint16_t *ss = (const uint16_t *)(st + SOFF + wave * 256);
+        const float s0 = f16_to_f32(ss[lane & 15]);
+        const float s1 = f16_to_f32(ss[16 + (lane & 15)]);
         v4i b[2];
         if (BITS == 2) {
-            const uint32_t w0 = *(const uint32_t *)(wq0 + (int64_t)g * PB);
-            const uint32_t w1 = *(const uint32_t *)(wq1 + (int64_t)g * PB);
-            b[0] = unpack_int2(w0);
-            b[1] = unpack_int2(w1);
+            b[0] = unpack_int2(*(const uint32_t *)(st + 4096 + (2 * wave) * PB + lane * 4));
+            b[1] = unpack_int2(*(const uint32_t *)(st + 4096 + (2 * wave + 1) * PB + lane * 4));
         } else {
-            const uint2 w0 = *(const uint2 *)(wq0 + (int64_t)g * PB);
-            const uint2 w1 = *(const uint2 *)(wq1 + (int64_t)g * PB);
+            const uint2 w0 = *(const uint2 *)(st + 4096 + (2 * wave) * PB + lane * 8);
+            const uint2 w1 = *(const uint2 *)(st + 4096 + (2 * wave + 1) * PB + lane * 8);
             b[0] = unpack_int4(w0.x, w0.y);
             b[1] = unpack_int4(w1.x, w1.y);
         }
-        const double s0 = f16_to_f64(sc0[g * 16]);
-        const double s1 = f16_to_f64(sc1[g * 16]);
         v4i af[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) af[i] = *(const v4i *)(&As[cur][i * 1024 + lane * 16]);
+        for (int i = 0; i < 4; i++) af[i] = *(const v4i *)(st + i * 1024 + lane * 16);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const v4i z = {0, 0, 0, 0};
@@ -370,12 +440,10 @@ __global__ __launch_bounds__(256, 2) void k_lowbit_grouped(
             const v4i c1 = mfma16x16x64(af[i], b[1], z);
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                T[i][0][r] = fma((double)c0[r], s0, T[i][0][r]);
-                T[i][1][r] = fma((double)c1[r], s1, T[i][1][r]);
+                T[i][0][r] = __builtin_fmaf((float)c0[r], s0, T[i][0][r]);
+                T[i][1][r] = __builtin_fmaf((float)c1[r], s1, T[i][1][r]);
             }
         }
-        if (g + 1 < G) *(v4i *)(&As[cur ^ 1][a_dst]) = an;
-        __syncthreads();
     }
 
     const int lr = (lane >> 4) * 4, lc = lane & 15;
@@ -389,9 +457,9 @@ __global__ __launch_bounds__(256, 2) void k_lowbit_grouped(
             for (int r = 0; r < 4; r++) {
                 const int rr = i * 16 + lr + r;
                 if (rr >= nrows) continue;
-                const double sa = (double)rowscale[rr];
-                const float gv = (float)(T[i][0][r] * sa);
-                const float uv = (float)(T[i][1][r] * sa);
+                const float sa = rowscale[rr];
+                const float gv = T[i][0][r] * sa;
+                const float uv = T[i][1][r] * sa;
                 bad |= (!isfinite(gv)) || (!isfinite(uv));
                 float sv;
                 badmid |= !silu_mul(gv, uv, &sv);
@@ -408,7 +476,7 @@ __global__ __launch_bounds__(256, 2) void k_lowbit_grouped(
                 for (int r = 0; r < 4; r++) {
                     const int rr = i * 16 + lr + r;
                     if (rr >= nrows) continue;
-                    const float f = (float)(T[i][j][r] * (double)rowscale[rr]);
+                    const float f = T[i][j][r] * rowscale[rr];
                     bad |= !isfinite(f);
                     out[(int64_t)rowdst[rr] * ldo + col] = f;
                 }

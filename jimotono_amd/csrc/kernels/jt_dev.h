@@ -71,6 +71,20 @@ __device__ __forceinline__ int quant_code(float x, double scale_d) {
     qd = qd > 127.0 ? 127.0 : (qd < -127.0 ? -127.0 : qd);
     return (int)qd;
 }
+// Same code as quant_code without a per-element divide: y = x * RN(1/scale_d)
+// differs from the exact quotient x/scale_d by at most 2^-52 relative, i.e.
+// < 3e-14 for |x/scale_d| <= 128. round() of the two can differ only if a
+// half-integer lies between them, so whenever frac|y| is within 1e-9 of 0.5
+// the exact quotient is recomputed; otherwise round(y) is the exact answer.
+__device__ __forceinline__ int quant_code_fast(float x, double scale_d, double inv_d) {
+    if (scale_d == 0.0) return 0;
+    double y = (double)x * inv_d;
+    const double a = fabs(y);
+    if (fabs((a - floor(a)) - 0.5) < 1e-9) y = (double)x / scale_d;
+    double qd = round(y);
+    qd = qd > 127.0 ? 127.0 : (qd < -127.0 ? -127.0 : qd);
+    return (int)qd;
+}
 
 // ---- IEEE binary16 <-> binary64, round to nearest even ----
 __device__ __forceinline__ double f16_to_f64(uint16_t h) {

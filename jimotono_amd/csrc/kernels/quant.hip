@@ -17,12 +17,25 @@ __global__ __launch_bounds__(256) void k_quant_rows(
     int64_t nrows = row_count ? (int64_t)*row_count : rows;
     if (r >= nrows) return;
     const float *x = X + r * cols;
+    int8_t *q = Q + r * ldq;
+    // float4 loads / 4-byte code stores when the row allows it
+    const bool vec = (cols & 3) == 0 && (((uintptr_t)x | (uintptr_t)q) & 3) == 0 &&
+                     ((uintptr_t)x & 15) == 0;
     float m = 0.0f;
     int bad = 0;
-    for (int c = lane; c < cols; c += 64) {
-        float v = x[c];
-        bad |= !isfinite(v);
-        m = fmaxf(m, fabsf(v));
+    if (vec) {
+        const float4 *x4 = (const float4 *)x;
+        for (int c = lane; c < (cols >> 2); c += 64) {
+            const float4 v = x4[c];
+            bad |= (!isfinite(v.x)) || (!isfinite(v.y)) || (!isfinite(v.z)) || (!isfinite(v.w));
+            m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        }
+    } else {
+        for (int c = lane; c < cols; c += 64) {
+            float v = x[c];
+            bad |= !isfinite(v);
+            m = fmaxf(m, fabsf(v));
+        }
     }
     m = wave_max_f(m);
     bad = wave_or_i(bad);
@@ -32,8 +45,22 @@ __global__ __launch_bounds__(256) void k_quant_rows(
         return;
     }
     if (lane == 0) scale[r] = p.scale_f;
-    int8_t *q = Q + r * ldq;
-    for (int c = lane; c < cols; c += 64) q[c] = (int8_t)quant_code(x[c], p.scale_d);
+    const double inv = p.scale_d != 0.0 ? 1.0 / p.scale_d : 0.0;
+    if (vec) {
+        const float4 *x4 = (const float4 *)x;
+        uint32_t *q4 = (uint32_t *)q;
+        for (int c = lane; c < (cols >> 2); c += 64) {
+            const float4 v = x4[c];
+            const uint32_t b0 = (uint8_t)quant_code_fast(v.x, p.scale_d, inv);
+            const uint32_t b1 = (uint8_t)quant_code_fast(v.y, p.scale_d, inv);
+            const uint32_t b2 = (uint8_t)quant_code_fast(v.z, p.scale_d, inv);
+            const uint32_t b3 = (uint8_t)quant_code_fast(v.w, p.scale_d, inv);
+            q4[c] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+        }
+    } else {
+        for (int c = lane; c < cols; c += 64)
+            q[c] = (int8_t)quant_code_fast(x[c], p.scale_d, inv);
+    }
 }
 
 extern "C" int jtk_quant_rows(const float *X, int64_t rows, int cols, int8_t *Q,

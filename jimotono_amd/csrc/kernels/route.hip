@@ -17,9 +17,13 @@
 #include "jt_launch.h"
 
 // ---------------- router logits ----------------
-// Block: 64 tokens x 64 experts, 256 threads, each a 4 x 4 (token, expert)
-// micro-tile with 4 lane partials per output. K streamed in chunks of 32
-// through LDS (stored transposed, k-major, so each thread reads float4s).
+// Block: 64 tokens x 64 experts, 256 threads in 4 groups of 64; group p
+// accumulates the reference's lane partial l_p = sum over j = p (mod 4) of
+// x_j*w_j (j ascending) for all 64 x 64 outputs, each thread an 8 x 8
+// (token, expert) register tile of fp64 accumulators. K is staged through
+// LDS as fp32, k-major, in chunks of 32 (double-buffered). At the end the
+// partials meet in LDS and are combined as (l0+l1)+(l2+l3), then the tail
+// j >= n & ~3 is added in order, as in the reference.
 #define RT_T 64
 #define RT_E 64
 #define RT_KC 32
@@ -28,55 +32,101 @@ __global__ __launch_bounds__(256) void k_router_logits(const float *__restrict__
                                                        int E, int n,
                                                        float *__restrict__ logits,
                                                        uint32_t *err) {
-    __shared__ float xs[RT_KC][RT_T + 4];
-    __shared__ float ws[RT_KC][RT_E + 4];
+    // [stage][x|w][k][row]: 32 KiB, reused as the 64 x 64 fp64 partial buffer
+    __shared__ __attribute__((aligned(16))) float lds[2][2][RT_KC][64];
+    auto xs = [&](int b, int k) -> float * { return &lds[b][0][k][0]; };
+    auto ws = [&](int b, int k) -> float * { return &lds[b][1][k][0]; };
     const int tid = threadIdx.x;
     const int t0 = blockIdx.x * RT_T, e0 = blockIdx.y * RT_E;
-    const int ty = tid >> 4, tx = tid & 15;  // tokens ty*4.., experts tx*4..
-    double part[4][4][4];
+    const int p = tid >> 6;                  // lane partial of this thread
+    const int ty = (tid >> 3) & 7, tx = tid & 7;  // tokens ty*8.., experts tx*8..
+    double acc[8][8];
 #pragma unroll
-    for (int a = 0; a < 4; a++)
+    for (int a = 0; a < 8; a++)
 #pragma unroll
-        for (int b = 0; b < 4; b++)
-#pragma unroll
-            for (int p = 0; p < 4; p++) part[a][b][p] = 0.0;
+        for (int b = 0; b < 8; b++) acc[a][b] = 0.0;
     const int n4 = n & ~3;
+    // stage loader: thread -> (row r = tid/4, 8 consecutive k at 8*(tid%4))
+    const int lr = tid >> 2, lk = (tid & 3) * 8;
+    const float *xrow = X + (int64_t)min(t0 + lr, T - 1) * n;
+    const float *wrow = Wg + (int64_t)min(e0 + lr, E - 1) * n;
+    float xv[8], wv[8];
+    auto gload = [&](int k0) {
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const int k = k0 + lk + c;
+            xv[c] = k < n4 ? xrow[k] : 0.0f;
+            wv[c] = k < n4 ? wrow[k] : 0.0f;
+        }
+    };
+    auto sstore = [&](int buf) {
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            xs(buf, lk + c)[lr] = xv[c];
+            ws(buf, lk + c)[lr] = wv[c];
+        }
+    };
+    gload(0);
+    sstore(0);
+    __syncthreads();
+    int buf = 0;
     for (int k0 = 0; k0 < n4; k0 += RT_KC) {
-        // load 64 x 32 floats of X and of Wgate: 2048 floats each, 8/thread
-        for (int i = tid; i < RT_T * RT_KC; i += 256) {
-            const int r = i / RT_KC, c = i % RT_KC;
-            const int t = min(t0 + r, T - 1), e = min(e0 + r, E - 1);
-            const int k = k0 + c;
-            xs[c][r] = k < n4 ? X[(int64_t)t * n + k] : 0.0f;
-            ws[c][r] = k < n4 ? Wg[(int64_t)e * n + k] : 0.0f;
-        }
-        __syncthreads();
+        const bool more = k0 + RT_KC < n4;
+        if (more) gload(k0 + RT_KC);
         const int kend = min(RT_KC, n4 - k0);
-        for (int c = 0; c < kend; c += 4) {
+        for (int i = p; i < kend; i += 4) {
+            const float4 x0 = *(const float4 *)(xs(buf, i) + ty * 8);
+            const float4 x1 = *(const float4 *)(xs(buf, i) + ty * 8 + 4);
+            const float4 w0 = *(const float4 *)(ws(buf, i) + tx * 8);
+            const float4 w1 = *(const float4 *)(ws(buf, i) + tx * 8 + 4);
+            const double xa[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            const double wa[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
-            for (int p = 0; p < 4; p++) {
-                const float4 xv = *(const float4 *)(&xs[c + p][ty * 4]);
-                const float4 wv = *(const float4 *)(&ws[c + p][tx * 4]);
-                const double xa[4] = {xv.x, xv.y, xv.z, xv.w};
-                const double wa[4] = {wv.x, wv.y, wv.z, wv.w};
+            for (int a = 0; a < 8; a++)
 #pragma unroll
-                for (int a = 0; a < 4; a++)
-#pragma unroll
-                    for (int b = 0; b < 4; b++) part[a][b][p] = fma(xa[a], wa[b], part[a][b][p]);
-            }
+                for (int b = 0; b < 8; b++) acc[a][b] = fma(xa[a], wa[b], acc[a][b]);
         }
+        if (more) sstore(buf ^ 1);
         __syncthreads();
+        buf ^= 1;
     }
+    // combine partials through LDS (reusing the staging arrays, 32 KiB of
+    // fp64 per partial): l1 -> l0+l1, l3 -> l2+l3, then (l0+l1)+(l2+l3)
+    double *red = (double *)&lds[0][0][0][0];
+    auto put = [&]() {
+#pragma unroll
+        for (int a = 0; a < 8; a++)
+#pragma unroll
+            for (int b = 0; b < 8; b++) red[(ty * 8 + a) * 64 + tx * 8 + b] = acc[a][b];
+    };
+    auto add = [&]() {
+#pragma unroll
+        for (int a = 0; a < 8; a++)
+#pragma unroll
+            for (int b = 0; b < 8; b++) acc[a][b] = acc[a][b] + red[(ty * 8 + a) * 64 + tx * 8 + b];
+    };
+    if (p == 1) put();
+    __syncthreads();
+    if (p == 0) add();
+    __syncthreads();
+    if (p == 3) put();
+    __syncthreads();
+    if (p == 2) add();
+    __syncthreads();
+    if (p == 2) put();
+    __syncthreads();
+    if (p != 0) return;
+    add();
     uint32_t bad = 0;
 #pragma unroll
-    for (int a = 0; a < 4; a++) {
-        const int t = t0 + ty * 4 + a;
+    for (int a = 0; a < 8; a++) {
+        const int t = t0 + ty * 8 + a;
         if (t >= T) continue;
 #pragma unroll
-        for (int b = 0; b < 4; b++) {
-            const int e = e0 + tx * 4 + b;
+        for (int b = 0; b < 8; b++) {
+            const int e = e0 + tx * 8 + b;
             if (e >= E) continue;
-            double s = (part[a][b][0] + part[a][b][1]) + (part[a][b][2] + part[a][b][3]);
+            double s = acc[a][b];
             for (int j = n4; j < n; j++)
                 s = s + (double)X[(int64_t)t * n + j] * (double)Wg[(int64_t)e * n + j];
             const float f = (float)s;

@@ -278,7 +278,7 @@ int or_gemm_lowbit_group(const int8_t *Aq, const float *sA,
     int nn = (1 << bits) - 1;
     for (int m = 0; m < M; m++)
         for (int n = 0; n < N; n++) {
-            double T = 0.0;
+            float T = 0.0f;
             for (int g = 0; g < G; g++) {
                 int32_t acc = 0;
                 for (int i = 0; i < group; i++) {
@@ -287,9 +287,10 @@ int or_gemm_lowbit_group(const int8_t *Aq, const float *sA,
                            (2 * (int32_t)codes[(size_t)n * K + k] - nn);
                 }
                 if (acc_out) acc_out[((size_t)m * N + n) * G + g] = acc;
-                T = T + (double)acc * or_f16_to_f64(scales[(size_t)n * G + g]);
+                /* |acc| < 2^24, so (float)acc is exact; one rounding per group */
+                T = fmaf((float)acc, (float)or_f16_to_f64(scales[(size_t)n * G + g]), T);
             }
-            float f = (float)(T * (double)sA[m]);
+            float f = T * sA[m];
             if (!isfinite((double)f)) rc = RC_INVAL;
             C[(size_t)m * N + n] = f;
         }

@@ -82,8 +82,9 @@ int or_lowbit_pack_rows(const float *W, int N, int K, int bits, int group,
 
 /* Grouped low-bit GEMM on prepared codes, C[M][N]:
  *   acc_g = sum_{k in g} Aq[m][k] * (2*codes[n][k] - (2^bits-1))   (int32)
- *   T     = sum_g (double)acc_g * (double)f16(scales[n][g])  (g ascending)
- *   C     = (float)(T * (double)sA[m])
+ *   T     = fmaf((float)acc_g, f16(scales[n][g]), T), fp32, g ascending
+ *           from T = 0 (one rounding per group; (float)acc_g is exact)
+ *   C     = T * sA[m] (fp32)
  * acc_out [M][N][K/group] may be NULL. rc 2 on a non-finite C. */
 int or_gemm_lowbit_group(const int8_t *Aq, const float *sA,
                          const uint8_t *codes, const uint16_t *scales,
