@@ -201,6 +201,7 @@ static const char *const k_stage_names[ST_N] = {
     "shared_gateup", "shared_quant",  "shared_down",  "combine"};
 
 #define PROF_RING 16
+#define MOE_SIDE 4 /* side streams for the shared experts */
 
 struct jt_hip_moe {
     jt_hip_moe_desc d;
@@ -217,6 +218,11 @@ struct jt_hip_moe {
     int32_t *ids, *rank, *cnt, *tot, *off, *perm, *tiles, *ntiles;
     int8_t *Sqr;
     int last_T;
+    /* shared experts run on side streams forked after the input quantiser
+     * and joined before the combine; expert e uses side[e % nside] */
+    int nside;
+    hipStream_t side[MOE_SIDE];
+    hipEvent_t ev_fork, ev_join[MOE_SIDE];
     /* profiling: ring of per-forward event sets */
     int prof;
     hipEvent_t ev[PROF_RING][ST_N + 1 + 3 * JT_MOE_MAX_SHARED];
@@ -235,6 +241,11 @@ void jt_hip_moe_free(jt_hip_moe *L) {
     (void)hipDeviceSynchronize();
     for (size_t i = 0; i < sizeof(p) / sizeof(p[0]); i++) (void)hipFree(p[i]);
     for (int s = 0; s < JT_MOE_MAX_SHARED; s++) jt_hip_ffn_free(L->sh[s]);
+    for (int i = 0; i < L->nside; i++) {
+        (void)hipEventDestroy(L->ev_join[i]);
+        (void)hipStreamDestroy(L->side[i]);
+    }
+    if (L->nside) (void)hipEventDestroy(L->ev_fork);
     if (L->ev_ready)
         for (int r = 0; r < PROF_RING; r++)
             for (int i = 0; i < ST_N + 1 + 3 * JT_MOE_MAX_SHARED; i++)
@@ -317,6 +328,22 @@ int jt_hip_moe_prepare(const jt_hip_moe_desc *desc, const float *dWgate, const f
         rc = ffn_prepare_on(rt, dWg_s + so, dWu_s + so, dWd_s + so, n, hs, &L->sh[s]);
         if (rc == JT_OK) rc = ffn_reserve(L->sh[s], T, 0);
     }
+    if (rc == JT_OK && d.n_shared > 0) {
+        const int ns = d.n_shared < MOE_SIDE ? d.n_shared : MOE_SIDE;
+        e = hipEventCreateWithFlags(&L->ev_fork, hipEventDisableTiming);
+        for (int i = 0; i < ns && e == hipSuccess; i++) {
+            e = hipStreamCreateWithFlags(&L->side[i], hipStreamNonBlocking);
+            if (e != hipSuccess) break;
+            e = hipEventCreateWithFlags(&L->ev_join[i], hipEventDisableTiming);
+            if (e != hipSuccess) {
+                (void)hipStreamDestroy(L->side[i]);
+                break;
+            }
+            L->nside = i + 1;
+        }
+        if (e != hipSuccess && L->nside == 0) (void)hipEventDestroy(L->ev_fork);
+        rc = jt_rt_err(e);
+    }
     if (rc != JT_OK) {
         jt_hip_moe_free(L);
         return rc;
@@ -390,6 +417,18 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
 
     prof_mark(L, slot, ST_QUANT_X, s);
     le |= jtk_quant_rows(dX, T, n, L->Xq, n, L->sx, NULL, err, s);
+    /* Without profiling the shared experts overlap the routed path on side
+     * streams; with profiling every stage runs in order on s so that each
+     * stage's events bracket its kernels alone. */
+    const int fork = S > 0 && !L->prof;
+    if (fork) {
+        le |= (int)hipEventRecord(L->ev_fork, s);
+        for (int i = 0; i < L->nside; i++) le |= (int)hipStreamWaitEvent(L->side[i], L->ev_fork, 0);
+        for (int e = 0; e < S; e++) /* launch errors are collected; the join still happens */
+            le |= ffn_run_q(rt, L->sh[e], L->Xq, L->sx, T, L->Ys + (size_t)e * T * n,
+                            L->side[e % L->nside], NULL);
+        for (int i = 0; i < L->nside; i++) le |= (int)hipEventRecord(L->ev_join[i], L->side[i]);
+    }
     prof_mark(L, slot, ST_ROUTER, s);
     if (d_ids) {
         le |= (int)hipMemcpyAsync(L->ids, d_ids, (size_t)Tk * 4, hipMemcpyDeviceToDevice, s);
@@ -415,10 +454,14 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
     le |= jtk_lowbit_grouped(4, L->Sqr, h, L->ssr, L->perm, L->off, k, L->tiles, L->ntiles,
                              max_tiles, L->dn_P, L->dn_S, L->dn_pstride, L->dn_sstride, n, h,
                              L->Ye, n, err, s);
-    for (int e = 0; e < S; e++) {
-        hipEvent_t *ev = L->prof ? &L->ev[slot][ST_N + 1 + 3 * e] : NULL;
-        rc = ffn_run_q(rt, L->sh[e], L->Xq, L->sx, T, L->Ys + (size_t)e * T * n, s, ev);
-        if (rc != JT_OK) return rc;
+    if (fork) {
+        for (int i = 0; i < L->nside; i++) le |= (int)hipStreamWaitEvent(s, L->ev_join[i], 0);
+    } else {
+        for (int e = 0; e < S; e++) {
+            hipEvent_t *ev = L->prof ? &L->ev[slot][ST_N + 1 + 3 * e] : NULL;
+            rc = ffn_run_q(rt, L->sh[e], L->Xq, L->sx, T, L->Ys + (size_t)e * T * n, s, ev);
+            if (rc != JT_OK) return rc;
+        }
     }
     prof_mark(L, slot, ST_COMBINE, s);
     le |= jtk_combine(L->w, L->Ye, NULL, L->Ys, S, T, k, n, dY, err, s);

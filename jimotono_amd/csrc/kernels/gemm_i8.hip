@@ -14,187 +14,11 @@
 // whose byte order equals the MFMA operand layout, so operand panels are
 // copied global -> LDS with global_load_lds_dwordx4 (lane i's 16 bytes land
 // at LDS base + 16*i) and read back with one ds_read_b128 per lane.
-#include "jt_dev.h"
+#include "gemm_w8a8.h"
 #include "jt_launch.h"
 
 // Output fragment layout of v_mfma_i32_16x16x64_i8 (4 int32 per lane):
 // element r of lane l is row 4*(l/16)+r, column l%16 of the 16x16 tile.
-
-enum { EPI_PLAIN = 0, EPI_SWIGLU = 1, EPI_SCATTER = 2 };
-
-typedef __attribute__((address_space(3))) void lds_void;
-
-// One LDS-DMA copy: each lane moves BYTES bytes from its own global address
-// to lds_base + BYTES * lane (lds_base is wave-uniform).
-template <int BYTES>
-__device__ __forceinline__ void dma(const void *g, void *lds_base);
-template <>
-__device__ __forceinline__ void dma<16>(const void *g, void *lds_base) {
-    __builtin_amdgcn_global_load_lds(g, (lds_void *)lds_base, 16, 0, 0);
-}
-template <>
-__device__ __forceinline__ void dma<4>(const void *g, void *lds_base) {
-    __builtin_amdgcn_global_load_lds(g, (lds_void *)lds_base, 4, 0, 0);
-}
-
-// Wait until at most N vector-memory operations of this wave are in flight.
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-// Workgroup barrier without the memory fence of __syncthreads(): the fence
-// would drain every in-flight LDS-DMA stage (s_waitcnt vmcnt(0)). Callers
-// first wait for their own stage with wait_vm, after which the DMA data is in
-// LDS, which all waves of the workgroup see after the barrier.
-__device__ __forceinline__ void barrier_lds() {
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
-
-// Stage s of a K loop of length KB was issued before the loads of the
-// min(NST - 2, KB - 1 - s) later stages; wait for s only.
-template <int NST, int PER>
-__device__ __forceinline__ void wait_stage(int later) {
-    if (NST >= 4 && later >= 2) {
-        wait_vm<(NST >= 4 ? 2 : 0) * PER>();
-    } else if (later >= 1) {
-        wait_vm<PER>();
-    } else {
-        wait_vm<0>();
-    }
-}
-
-// ===================== dense W8A8 MFMA GEMM =====================
-// Block tile 128 x 128, 4 waves as 2 x 2 wave tiles of 64 x 64 (4 x 4 MFMA
-// tiles), K step 64, a ring of NST LDS stages (16 KiB each: 8 A panels and
-// 8 W panels) filled by LDS-DMA NST-1 steps ahead. Each wave copies 4 of
-// the 16 panels of a stage. A [M][lda] row-major int8 (lda >= Kp,
-// Kp % 64 == 0, zero padding past K); W panels padded to Np (multiple of
-// 128) channels. Tiles are ordered channel-block-major and, when the tile
-// count is a multiple of 8, dealt to the 8 XCDs in contiguous chunks so the
-// blocks sharing a weight column block share an L2.
-#define GB_M 128
-#define GB_N 128
-#define GB_NST 4
-
-template <int EPI>
-__global__ __launch_bounds__(256, 2) void k_w8a8_mfma(
-    const int8_t *__restrict__ A, int lda, const float *__restrict__ sA,
-    const int8_t *__restrict__ Wp, const float *__restrict__ sB, int M, int N, int Kp,
-    float *__restrict__ C, int ldc, uint32_t *err, int mtiles, int ntiles) {
-    __shared__ __attribute__((aligned(1024))) int8_t smem[GB_NST * 16 * 1024];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int total = mtiles * ntiles;
-    int tile = blockIdx.x;
-    if ((total & 7) == 0) tile = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
-    const int mt = tile % mtiles, nt = tile / mtiles;
-    const int m0 = mt * GB_M, n0 = nt * GB_N;
-    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
-    const int KB = Kp / 64;
-
-    // this wave copies panels 4*wave .. 4*wave+3 of every stage
-    // (panels 0-7 = A rows m0+16p.., 8-15 = W channels n0+16(p-8)..)
-    const int8_t *src[4];
-    int64_t step[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int p = wave * 4 + i;
-        if (p < 8) {
-            int r = m0 + p * 16 + (lane & 15);
-            r = r < M ? r : M - 1;
-            src[i] = A + (int64_t)r * lda + (lane >> 4) * 16;
-            step[i] = 64;
-        } else {
-            src[i] = Wp + ((int64_t)(n0 / 16 + p - 8) * KB) * 1024 + lane * 16;
-            step[i] = 1024;
-        }
-    }
-    auto issue = [&](int kb) {
-        int8_t *st = smem + (kb % GB_NST) * 16384;
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-            dma<16>(src[i] + (int64_t)kb * step[i], st + (wave * 4 + i) * 1024);
-    };
-#pragma unroll
-    for (int s = 0; s < GB_NST - 1; s++)
-        if (s < KB) issue(s);
-
-    v4i acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = (v4i){0, 0, 0, 0};
-
-    for (int kb = 0; kb < KB; kb++) {
-        wait_stage<GB_NST, 4>(min(GB_NST - 2, KB - 1 - kb));
-        barrier_lds();
-        if (kb + GB_NST - 1 < KB) issue(kb + GB_NST - 1);
-        const int8_t *st = smem + (kb % GB_NST) * 16384;
-        v4i af[4], bf[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) af[i] = *(const v4i *)(st + ((wm >> 4) + i) * 1024 + lane * 16);
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-            bf[j] = *(const v4i *)(st + (8 + (wn >> 4) + j) * 1024 + lane * 16);
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) acc[i][j] = mfma16x16x64(af[i], bf[j], acc[i][j]);
-    }
-
-    // epilogue
-    const int lr = (lane >> 4) * 4, lc = lane & 15;
-    uint32_t bad = 0;
-    if (EPI == EPI_PLAIN) {
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int col = n0 + wn + j * 16 + lc;
-            if (col >= N) continue;
-            const double sb = (double)sB[col];
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int row = m0 + wm + i * 16 + lr + r;
-                    if (row >= M) continue;
-                    const float f = (float)((double)acc[i][j][r] * ((double)sA[row] * sb));
-                    bad |= !isfinite(f);
-                    C[(int64_t)row * ldc + col] = f;
-                }
-        }
-        if (bad) raise_err(err, EF_RANGE);
-    } else {
-        // packed channels: [gate 16][up 16] per 32; tiles j = 0,2 are gate,
-        // j = 1,3 the matching up; output column = hidden unit.
-        uint32_t badmid = 0;
-#pragma unroll
-        for (int jj = 0; jj < 2; jj++) {
-            const int cg = n0 + wn + (2 * jj) * 16 + lc;  // packed gate channel
-            const int cu = cg + 16;
-            const int hid = (n0 + wn) / 2 + jj * 16 + lc;
-            if (cu >= N) continue;
-            const double sbg = (double)sB[cg], sbu = (double)sB[cu];
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int row = m0 + wm + i * 16 + lr + r;
-                    if (row >= M) continue;
-                    const double sa = (double)sA[row];
-                    const float g = (float)((double)acc[i][2 * jj][r] * (sa * sbg));
-                    const float u = (float)((double)acc[i][2 * jj + 1][r] * (sa * sbu));
-                    bad |= (!isfinite(g)) || (!isfinite(u));
-                    float s;
-                    badmid |= !silu_mul(g, u, &s);
-                    C[(int64_t)row * ldc + hid] = s;
-                }
-        }
-        if (bad) raise_err(err, EF_RANGE);
-        if (badmid) raise_err(err, EF_NONFINITE_MID);
-    }
-}
 
 // ===================== decode GEMV (M <= 16) =====================
 // One block per pair of panels (32 packed channels); the 4 waves split the K
@@ -252,16 +76,31 @@ __global__ __launch_bounds__(256) void k_w8a8_gemv(
             if (lane < 16) red[wave][m][q * 16 + lane] = v;
         }
     __syncthreads();
-    // 32 channels x MR rows, one (row, channel) per thread
+    // 32 channels x MR rows, one (row, channel) per thread. Scales are read
+    // before any store (loads and stores share one vmcnt on gfx9).
+    constexpr int PT = (MR * 32 + 255) / 256;
+    double sa_t[PT], sg_t[PT], su_t[PT];
+#pragma unroll
+    for (int q = 0; q < PT; q++) {
+        const int idx = tid + q * 256;
+        const int m = min(idx >> 5, M - 1), c = idx & 31;
+        sa_t[q] = (double)sA[m];
+        const int cg = min(p0 * 16 + c, N - 1), cu = min(p0 * 16 + c + 16, N - 1);
+        sg_t[q] = (double)sB[cg];
+        su_t[q] = (double)sB[cu];
+    }
     uint32_t bad = 0, badmid = 0;
-    for (int idx = tid; idx < MR * 32; idx += 256) {
+#pragma unroll
+    for (int q = 0; q < PT; q++) {
+        const int idx = tid + q * 256;
+        if (idx >= MR * 32) continue;
         const int m = idx >> 5, c = idx & 31;
         if (m >= M) continue;
         const int s = red[0][m][c] + red[1][m][c] + red[2][m][c] + red[3][m][c];
         if (EPI == EPI_PLAIN) {
             const int col = p0 * 16 + c;
             if (col >= N) continue;
-            const float f = (float)((double)s * ((double)sA[m] * (double)sB[col]));
+            const float f = (float)((double)s * (sa_t[q] * sg_t[q]));
             bad |= !isfinite(f);
             C[(int64_t)m * ldc + col] = f;
         } else {
@@ -270,9 +109,8 @@ __global__ __launch_bounds__(256) void k_w8a8_gemv(
             if (cu >= N) continue;
             const int su = red[0][m][c + 16] + red[1][m][c + 16] + red[2][m][c + 16] +
                            red[3][m][c + 16];
-            const double sa = (double)sA[m];
-            const float g = (float)((double)s * (sa * (double)sB[cg]));
-            const float u = (float)((double)su * (sa * (double)sB[cu]));
+            const float g = (float)((double)s * (sa_t[q] * sg_t[q]));
+            const float u = (float)((double)su * (sa_t[q] * su_t[q]));
             bad |= (!isfinite(g)) || (!isfinite(u));
             float sv;
             badmid |= !silu_mul(g, u, &sv);
@@ -303,14 +141,25 @@ extern "C" int jtk_w8a8_gemm(const int8_t *A, int lda, const float *sA, const in
         }
 #undef GEMV
     } else {
-        const int mt = (M + GB_M - 1) / GB_M, nt = Np / GB_N;
-        dim3 grid((unsigned)(mt * nt));
-        if (swiglu)
-            hipLaunchKernelGGL((k_w8a8_mfma<EPI_SWIGLU>), grid, dim3(256), 0, s, A, lda, sA, Wp,
-                               sB, M, N, Kp, C, ldc, err, mt, nt);
-        else
-            hipLaunchKernelGGL((k_w8a8_mfma<EPI_PLAIN>), grid, dim3(256), 0, s, A, lda, sA, Wp,
-                               sB, M, N, Kp, C, ldc, err, mt, nt);
+        // Tile choice (measured on MI355X): few 128x128 tiles -> 8 waves per
+        // block with an intra-block k-split; otherwise 128 x 256 tiles of
+        // 8 waves; SwiGLU pairs need an even number of 16-channel tiles.
+        const int mt128 = (M + 127) / 128;
+        const bool n256 = (Np % 256) == 0;
+        hipError_t e;
+        if (swiglu) {
+            e = n256 ? launch_w8a8_tile<EPI_SWIGLU, 128, 256, 2, 4, 1, 3, 4>(
+                           A, lda, sA, Wp, sB, M, N, Np, Kp, C, ldc, err, s)
+                     : launch_w8a8_tile<EPI_SWIGLU, 128, 128, 2, 2, 2, 2, 4>(
+                           A, lda, sA, Wp, sB, M, N, Np, Kp, C, ldc, err, s);
+        } else if (!n256 || mt128 * (Np / 128) <= 512) {
+            e = launch_w8a8_tile<EPI_PLAIN, 128, 128, 2, 2, 2, 3, 4>(A, lda, sA, Wp, sB, M, N, Np,
+                                                                     Kp, C, ldc, err, s);
+        } else {
+            e = launch_w8a8_tile<EPI_PLAIN, 128, 256, 2, 4, 1, 3, 4>(A, lda, sA, Wp, sB, M, N, Np,
+                                                                     Kp, C, ldc, err, s);
+        }
+        return (int)e;
     }
     return (int)hipGetLastError();
 }
@@ -327,13 +176,15 @@ extern "C" int jtk_w8a8_gemm(const int8_t *A, int lda, const float *sA, const in
 // panel-groups of the 128 channels (raw bytes, 256 B per DMA). Waves split
 // the 128 channels (32 each = 2 panels); B fragments are unpacked from LDS
 // to signed int8 in registers.
-#define LB_NST 4
-
 __device__ __forceinline__ float f16_to_f32(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);
 }
 
-template <int BITS, int EPI>
+#ifndef LB_STAGES
+#define LB_STAGES 4
+#endif
+
+template <int BITS, int EPI, int NST>
 __global__ __launch_bounds__(256, 2) void k_lowbit_grouped(
     const int8_t *__restrict__ A, int lda, const float *__restrict__ sA,
     const int32_t *__restrict__ perm, const int32_t *__restrict__ off, int topk,
@@ -345,7 +196,7 @@ __global__ __launch_bounds__(256, 2) void k_lowbit_grouped(
     constexpr int SOFF = 4096 + 8 * PB;             // scales after A and weight bytes
     constexpr int STAGE = SOFF + 4 * 256;           // + one 256-byte scale slot per wave
     constexpr int PER = 2 + 2 * BDMA;               // DMAs per wave per stage
-    __shared__ __attribute__((aligned(1024))) int8_t smem[LB_NST * STAGE];
+    extern __shared__ __attribute__((aligned(1024))) int8_t smem[];  // NST * STAGE bytes
     __shared__ int rowsrc[64];
     __shared__ float rowscale[64];
     __shared__ int rowdst[64];
@@ -391,7 +242,7 @@ __global__ __launch_bounds__(256, 2) void k_lowbit_grouped(
                                              (int64_t)(pan0 + (sl >> 3)) * G * 16) +
                            (sl & 7) * 4;
     auto issue = [&](int g) {
-        int8_t *st = smem + (g % LB_NST) * STAGE;
+        int8_t *st = smem + (g % NST) * STAGE;
         dma<16>(a_src + (int64_t)g * 64, st + wave * 1024);
 #pragma unroll
         for (int d = 0; d < BDMA; d++) {
@@ -401,7 +252,7 @@ __global__ __launch_bounds__(256, 2) void k_lowbit_grouped(
         dma<4>(s_src + (int64_t)g * 32, st + SOFF + wave * 256);
     };
 #pragma unroll
-    for (int s = 0; s < LB_NST - 1; s++)
+    for (int s = 0; s < NST - 1; s++)
         if (s < G) issue(s);
 
     float T[4][2][4];
@@ -413,10 +264,10 @@ __global__ __launch_bounds__(256, 2) void k_lowbit_grouped(
             for (int r = 0; r < 4; r++) T[i][j][r] = 0.0f;
 
     for (int g = 0; g < G; g++) {
-        wait_stage<LB_NST, PER>(min(LB_NST - 2, G - 1 - g));
+        wait_stage<PER>(min(NST - 2, G - 1 - g));
         barrier_lds();
-        if (g + LB_NST - 1 < G) issue(g + LB_NST - 1);
-        const int8_t *st = smem + (g % LB_NST) * STAGE;
+        if (g + NST - 1 < G) issue(g + NST - 1);
+        const int8_t *st = smem + (g % NST) * STAGE;
         const uint16_t *ss = (const uint16_t *)(st + SOFF + wave * 256);
         const float s0 = f16_to_f32(ss[lane & 15]);
         const float s1 = f16_to_f32(ss[16 + (lane & 15)]);
@@ -486,6 +337,32 @@ __global__ __launch_bounds__(256, 2) void k_lowbit_grouped(
     if (badmid) raise_err(err, EF_NONFINITE_MID);
 }
 
+template <int BITS, int EPI, int NST>
+static hipError_t launch_lowbit(dim3 grid, hipStream_t s, const int8_t *A, int lda,
+                                const float *sA, const int32_t *perm, const int32_t *off,
+                                int topk, const int32_t *tiles, const int32_t *ntiles,
+                                const uint8_t *Wp, const uint16_t *Ws, int64_t wp_stride,
+                                int64_t ws_stride, int N, int K, float *out, int ldo,
+                                uint32_t *err) {
+    constexpr int PB = BITS == 2 ? 256 : 512;
+    constexpr int lds = NST * (4096 + 8 * PB + 4 * 256);
+    auto kern = k_lowbit_grouped<BITS, EPI, NST>;
+    static bool attr_set[64];
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    if (!attr_set[dev]) {
+        e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                lds);
+        if (e != hipSuccess) return e;
+        attr_set[dev] = true;
+    }
+    hipLaunchKernelGGL(kern, grid, dim3(256), lds, s, A, lda, sA, perm, off, topk, tiles, ntiles,
+                       Wp, Ws, wp_stride, ws_stride, N, K, out, ldo, err);
+    return hipGetLastError();
+}
+
 extern "C" int jtk_lowbit_grouped(int bits, const int8_t *A, int lda, const float *sA,
                                   const int32_t *perm, const int32_t *off, int topk,
                                   const int32_t *tiles, const int32_t *ntiles, int max_tiles,
@@ -494,13 +371,14 @@ extern "C" int jtk_lowbit_grouped(int bits, const int8_t *A, int lda, const floa
                                   uint32_t *err, hipStream_t s) {
     if (max_tiles <= 0) return 0;
     dim3 grid((unsigned)max_tiles, (unsigned)(N / 128));
+    hipError_t e;
     if (bits == 2)
-        hipLaunchKernelGGL((k_lowbit_grouped<2, EPI_SWIGLU>), grid, dim3(256), 0, s, A, lda,
-                           sA, perm, off, topk, tiles, ntiles, Wp, Ws, wp_stride, ws_stride,
-                           N, K, out, ldo, err);
+        e = launch_lowbit<2, EPI_SWIGLU, LB_STAGES>(grid, s, A, lda, sA, perm, off, topk, tiles,
+                                                    ntiles, Wp, Ws, wp_stride, ws_stride, N, K,
+                                                    out, ldo, err);
     else
-        hipLaunchKernelGGL((k_lowbit_grouped<4, EPI_SCATTER>), grid, dim3(256), 0, s, A, lda,
-                           sA, perm, off, topk, tiles, ntiles, Wp, Ws, wp_stride, ws_stride,
-                           N, K, out, ldo, err);
-    return (int)hipGetLastError();
+        e = launch_lowbit<4, EPI_SCATTER, LB_STAGES>(grid, s, A, lda, sA, perm, off, topk,
+                                                     tiles, ntiles, Wp, Ws, wp_stride, ws_stride,
+                                                     N, K, out, ldo, err);
+    return (int)e;
 }

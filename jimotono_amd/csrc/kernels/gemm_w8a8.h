@@ -1,0 +1,294 @@
+// Dense W8A8 MFMA GEMM for gfx950, templated on the tile geometry.
+//
+// C[m][n] = epilogue(acc[m][n]), acc = sum_k A[m][k] * W[n][k] in int32 with
+// v_mfma_i32_16x16x64_i8. A is row-major int8 [M][lda] (lda >= Kp,
+// Kp % 64 == 0, zero bytes past K); W is in the 16-channel x 64-K panel
+// layout of jt_dev.h, padded to Np channels (multiple of BN).
+//
+// Block tile BM x BN. WGM x WGN waves tile the block with (BM/WGM) x (BN/WGN)
+// wave tiles; KS such wave groups split each stage's KS k-blocks of 64
+// between them (intra-block split-K; int32 partial sums are exchanged
+// through LDS at the end, which is exact). Operand panels (1 KiB each) go
+// global -> LDS with global_load_lds_dwordx4 into a ring of NST stages filled
+// NST-1 stages ahead; a wave waits only for its own copies of the stage it
+// is about to use and the workgroup then meets at a fence-less barrier.
+// Tile order: when the tile count is a multiple of 8 the blocks are dealt to
+// the 8 XCDs in contiguous chunks, and inside a chunk tiles walk GM
+// row-tiles at a time (all column tiles of a GM-row group before the next
+// group) so the concurrently resident blocks of an XCD share A rows and W
+// columns in its L2.
+#pragma once
+#include "jt_dev.h"
+
+enum { EPI_PLAIN = 0, EPI_SWIGLU = 1, EPI_SCATTER = 2 };
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// One LDS-DMA copy: each lane moves BYTES bytes from its own global address
+// to lds_base + BYTES * lane (lds_base is wave-uniform).
+template <int BYTES>
+__device__ __forceinline__ void dma(const void *g, void *lds_base);
+template <>
+__device__ __forceinline__ void dma<16>(const void *g, void *lds_base) {
+    __builtin_amdgcn_global_load_lds(g, (lds_void *)lds_base, 16, 0, 0);
+}
+template <>
+__device__ __forceinline__ void dma<4>(const void *g, void *lds_base) {
+    __builtin_amdgcn_global_load_lds(g, (lds_void *)lds_base, 4, 0, 0);
+}
+
+// Wait until at most N vector-memory operations of this wave are in flight.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Workgroup barrier without the memory fence of __syncthreads(): the fence
+// would drain every in-flight LDS-DMA stage (s_waitcnt vmcnt(0)). Callers
+// first wait for their own stage with wait_vm, after which the DMA data is in
+// LDS, which all waves of the workgroup see after the barrier.
+__device__ __forceinline__ void barrier_lds() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Wait for the oldest in-flight stage when `later` stages of PER copies each
+// were issued after it (the counter field holds at most 63; a smaller bound
+// only waits longer).
+template <int PER>
+__device__ __forceinline__ void wait_stage(int later) {
+#define JT_WAIT_CASE(k)                              \
+    case k:                                          \
+        wait_vm<(k * PER < 63 ? k * PER : 63)>(); \
+        break;
+    switch (later) {
+        JT_WAIT_CASE(0)
+        JT_WAIT_CASE(1)
+        JT_WAIT_CASE(2)
+        JT_WAIT_CASE(3)
+        JT_WAIT_CASE(4)
+        JT_WAIT_CASE(5)
+        JT_WAIT_CASE(6)
+        default:
+            wait_vm<(7 * PER < 63 ? 7 * PER : 63)>();
+    }
+#undef JT_WAIT_CASE
+}
+
+// Linear tile index -> (row tile, column tile), walking GM row tiles at a
+// time: all column tiles of a group of GM row tiles before the next group.
+template <int GM>
+__device__ __forceinline__ void tile_coords(int lin, int mtiles, int ntiles, int &mt, int &nt) {
+    const int per_group = GM * ntiles;
+    const int first_m = (lin / per_group) * GM;
+    const int gsz = min(mtiles - first_m, GM);
+    mt = first_m + (lin % per_group) % gsz;
+    nt = (lin % per_group) / gsz;
+}
+
+// Epilogue of one wave tile at (r0, c0): acc[i][j] element r of lane l is
+// row r0 + 16i + 4(l/16) + r, column c0 + 16j + l%16. With HALF > 0 only the
+// rows i / HALF == part are written (the other part belongs to a partner wave).
+//   EPI_PLAIN : C[row][col] = (float)((double)acc * ((double)sA[row] * sB[col]))
+//   EPI_SWIGLU: channels packed [gate 16][up 16] per 32 (tile 2jj gate, 2jj+1
+//               up); C[row][hidden] = silu(g) * u in fp64, rounded to float.
+template <int EPI, int TM, int TN, int HALF>
+__device__ __forceinline__ void w8a8_epilogue(const v4i (&acc)[TM][TN], int part, int r0, int c0,
+                                              int lane, const float *__restrict__ sA,
+                                              const float *__restrict__ sB, int M, int N,
+                                              float *__restrict__ C, int ldc, uint32_t *err) {
+    const int lr = (lane >> 4) * 4, lc = lane & 15;
+    // All scale loads are issued before the first store: gfx9 counts stores
+    // and loads on one vmcnt, so a load after a store would wait for it.
+    double sa[TM][4];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int row = r0 + i * 16 + lr + r;
+            sa[i][r] = (double)sA[row < M ? row : M - 1];
+        }
+    double sb[TN];
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+        const int col = c0 + j * 16 + lc;
+        sb[j] = (double)sB[col < N ? col : N - 1];
+    }
+    // Wave-uniform bounds: interior tiles store without per-element checks.
+    const bool full = r0 + 16 * TM <= M && c0 + 16 * TN <= N;
+    uint32_t bad = 0, badmid = 0;
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+        if (HALF > 0 && i / (HALF > 0 ? HALF : 1) != part) continue;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int row = r0 + i * 16 + lr + r;
+            float *crow = C + (int64_t)row * ldc;
+            if (EPI == EPI_PLAIN) {
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    const int col = c0 + j * 16 + lc;
+                    const float f = (float)((double)acc[i][j][r] * (sa[i][r] * sb[j]));
+                    if (full || (row < M && col < N)) {
+                        bad |= !isfinite(f);
+                        crow[col] = f;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int jj = 0; jj < TN / 2; jj++) {
+                    const int cu = c0 + (2 * jj + 1) * 16 + lc;
+                    const int hid = c0 / 2 + jj * 16 + lc;
+                    const float g =
+                        (float)((double)acc[i][2 * jj][r] * (sa[i][r] * sb[2 * jj]));
+                    const float u =
+                        (float)((double)acc[i][2 * jj + 1][r] * (sa[i][r] * sb[2 * jj + 1]));
+                    if (full || (row < M && cu < N)) {
+                        bad |= (!isfinite(g)) || (!isfinite(u));
+                        float sv;
+                        badmid |= !silu_mul(g, u, &sv);
+                        crow[hid] = sv;
+                    }
+                }
+            }
+        }
+    }
+    if (bad) raise_err(err, EF_RANGE);
+    if (badmid) raise_err(err, EF_NONFINITE_MID);
+}
+
+template <int EPI, int BM, int BN, int WGM, int WGN, int KS, int NST, int GM>
+__global__ __launch_bounds__(64 * WGM * WGN * KS) void k_w8a8_tile(
+    const int8_t *__restrict__ A, int lda, const float *__restrict__ sA,
+    const int8_t *__restrict__ Wp, const float *__restrict__ sB, int M, int N, int Kp,
+    float *__restrict__ C, int ldc, uint32_t *err, int mtiles, int ntiles) {
+    constexpr int NWG = WGM * WGN;  // waves per k-group
+    constexpr int WTM = BM / WGM, WTN = BN / WGN;
+    constexpr int TM = WTM / 16, TN = WTN / 16;
+    constexpr int AP = BM / 16, BP = BN / 16, NP = AP + BP;
+    constexpr int PPW = NP / NWG;  // panels copied per wave per stage
+    constexpr int STAGE = NP * KS * 1024;
+    static_assert(NP % NWG == 0, "panels must split evenly over waves");
+    static_assert(NST >= 2 && NST <= 8, "2..8 stages");
+    static_assert(KS == 1 || KS == 2, "k-split of 1 or 2");
+    static_assert(KS == 1 || TM % 2 == 0, "k-split halves the wave tile rows");
+    static_assert(KS == 1 || NST * STAGE >= 2 * NWG * (TM / 2) * TN * 1024,
+                  "exchange buffer fits the stage ring");
+    static_assert(EPI != EPI_SWIGLU || TN % 2 == 0, "gate/up pairs need even TN");
+    extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wg = wave % NWG, kg = wave / NWG;
+    const int total = mtiles * ntiles;
+    int pid = blockIdx.x;
+    if ((total & 7) == 0) pid = (pid & 7) * (total >> 3) + (pid >> 3);
+    int mt, nt;
+    tile_coords<GM>(pid, mtiles, ntiles, mt, nt);
+    const int m0 = mt * BM, n0 = nt * BN;
+    const int wm = (wg / WGN) * WTM, wn = (wg % WGN) * WTN;
+    const int KB = Kp / 64;
+    const int NSG = (KB + KS - 1) / KS;  // stages
+
+    // Copy i of a wave moves panel p = wg*PPW + i of k-block sub = kg.
+    const int8_t *src[PPW];
+    int step[PPW];
+#pragma unroll
+    for (int i = 0; i < PPW; i++) {
+        const int p = wg * PPW + i;
+        if (p < AP) {
+            int r = m0 + p * 16 + (lane & 15);
+            r = r < M ? r : M - 1;
+            src[i] = A + (int64_t)r * lda + (lane >> 4) * 16;
+            step[i] = 64;
+        } else {
+            src[i] = Wp + ((int64_t)(n0 / 16 + p - AP) * KB) * 1024 + lane * 16;
+            step[i] = 1024;
+        }
+    }
+    auto issue = [&](int sg) {
+        int8_t *st = smem + (sg % NST) * STAGE + kg * NP * 1024;
+        int kb = sg * KS + kg;
+        kb = kb < KB ? kb : KB - 1;  // a past-the-end block reloads the last one
+#pragma unroll
+        for (int i = 0; i < PPW; i++)
+            dma<16>(src[i] + (int64_t)kb * step[i], st + (wg * PPW + i) * 1024);
+    };
+#pragma unroll
+    for (int s = 0; s < NST - 1; s++)
+        if (s < NSG) issue(s);
+
+    v4i acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = (v4i){0, 0, 0, 0};
+
+    for (int sg = 0; sg < NSG; sg++) {
+        wait_stage<PPW>(min(NST - 2, NSG - 1 - sg));
+        barrier_lds();
+        if (sg + NST - 1 < NSG) issue(sg + NST - 1);
+        if (sg * KS + kg < KB) {
+            const int8_t *st = smem + (sg % NST) * STAGE + kg * NP * 1024;
+            v4i bf[TN];
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+                bf[j] = *(const v4i *)(st + (AP + (wn >> 4) + j) * 1024 + lane * 16);
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                const v4i af = *(const v4i *)(st + ((wm >> 4) + i) * 1024 + lane * 16);
+#pragma unroll
+                for (int j = 0; j < TN; j++) acc[i][j] = mfma16x16x64(af, bf[j], acc[i][j]);
+            }
+        }
+    }
+
+    // With a k-split each wave finishes the rows i / TE == kg of its wave
+    // tile after adding the partner group's partial sums (register arrays
+    // are indexed with constants only).
+    constexpr int TE = KS == 1 ? TM : TM / 2;
+    if (KS == 2) {
+        barrier_lds();  // every wave is done reading the stage ring
+        v4i *xbuf = (v4i *)smem;  // slot (writer group, wg, i % TE, j) x 64 lanes
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+                if (i / TE != kg)
+                    xbuf[(((kg * NWG + wg) * TE + i % TE) * TN + j) * 64 + lane] = acc[i][j];
+        __syncthreads();  // LDS writes complete and visible
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+                if (i / TE == kg)
+                    acc[i][j] += xbuf[((((1 - kg) * NWG + wg) * TE + i % TE) * TN + j) * 64 + lane];
+    }
+    w8a8_epilogue<EPI, TM, TN, KS == 2 ? TE : 0>(acc, kg, m0 + wm, n0 + wn, lane, sA, sB, M, N,
+                                                  C, ldc, err);
+}
+
+// Host-side launch of one configuration (dynamic LDS = NST stages).
+template <int EPI, int BM, int BN, int WGM, int WGN, int KS, int NST, int GM>
+inline hipError_t launch_w8a8_tile(const int8_t *A, int lda, const float *sA, const int8_t *Wp,
+                                   const float *sB, int M, int N, int Np, int Kp, float *C,
+                                   int ldc, uint32_t *err, hipStream_t s) {
+    auto kern = k_w8a8_tile<EPI, BM, BN, WGM, WGN, KS, NST, GM>;
+    constexpr int lds = NST * (BM + BN) / 16 * KS * 1024;
+    // dynamic LDS above 64 KiB must be enabled per device, once
+    static bool attr_set[64];
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    if (!attr_set[dev]) {
+        e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                lds);
+        if (e != hipSuccess) return e;
+        attr_set[dev] = true;
+    }
+    const int mt = (M + BM - 1) / BM, nt = Np / BN;
+    hipLaunchKernelGGL(kern, dim3((unsigned)(mt * nt)), dim3(64 * WGM * WGN * KS), lds, s, A,
+                       lda, sA, Wp, sB, M, N, Kp, C, ldc, err, mt, nt);
+    return hipGetLastError();
+}

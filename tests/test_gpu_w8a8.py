@@ -72,7 +72,9 @@ def test_dequant_fakequant_per_channel(jt, orc):
 
 
 SHAPES = [(1, 8, 16), (4, 40, 72), (16, 130, 64), (17, 128, 128), (64, 1024, 1024),
-          (200, 40, 72), (5, 2816, 1024), (33, 1024, 2816)]
+          (200, 40, 72), (5, 2816, 1024), (33, 1024, 2816),
+          # many tiles: the 128 x 256 tile configuration, ragged M, K padded
+          (2100, 4096, 200)]
 
 
 @pytest.mark.parametrize("M,N,K", SHAPES)
