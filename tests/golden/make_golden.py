@@ -1,0 +1,160 @@
+#!/usr/bin/env python3
+"""Write the golden vectors of tests/golden/ref_vectors.npz.
+
+Expected outputs come from the reference's own hot-path functions,
+compiled from the reference sources into oracle/_ref/libjtref.so by
+``make -C oracle ref`` (src/w8a8.c, lowbit.c, tmac.c, routing.c,
+moe_gemm.c, moe_layer.c, train_bwd.c with the reference's flags). Inputs
+are seeded and synthetic. The fixture is data only: inputs and the
+reference's outputs, no reference code.
+
+    make -C oracle ref && python3 tests/golden/make_golden.py
+
+Cases (key prefixes in the .npz):
+  quant_rows_*   jt_w8a8_quant_per_channel, rows with exact ties, a zero row
+  quant_tensor_* jt_w8a8_quant_per_tensor
+  fakequant_rows / dequant_rows  jt_w8a8_fakequant_per_channel / dequant
+  gemm_pc_* / gemm_pt_*  jt_w8a8_gemm_per_channel / _per_tensor
+  gemm_f32_*     jt_gemm_mat_f32
+  fq2_* / fq4_*  jt_lowbit_fakequant
+  c2i2_* / c2i4_*  jt_lowbit_col_to_idx
+  lut2_* / lut4_*  jt_lowbit_gemm_lut
+  tmac_*         jt_tmac_lut_ctor + jt_tmac_lookup_accum
+  topk_*         jt_routing_topk (random logits, exact ties, -inf masks)
+  sort_*         jt_moe_batch_sort at cap 1.0 and 1.5 (drops)
+  layer{f}_*     jt_moe_fwd_batch, f = 0 fp32, 1 W8A8 flag, 2 low-bit mode 1
+"""
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+
+from oracle.pyoracle import RefLib  # noqa: E402
+
+OUT = os.path.join(HERE, "ref_vectors.npz")
+
+
+def main():
+    R = RefLib()
+    rng = np.random.default_rng(20261201)
+    g = {}
+
+    # ---- W8A8 quantisers ----
+    X = rng.standard_normal((9, 77)).astype(np.float32)
+    X[3] = 0.0
+    # row 5: values that land exactly on .5 after division (max 127 -> scale 1)
+    X[5] = np.float32(0.0)
+    X[5, :6] = np.array([127.0, 0.5, -0.5, 2.5, -3.5, 126.5], np.float32)
+    rc, Q, s = R.quant_rows(X)
+    assert rc == 0
+    g.update(quant_rows_X=X, quant_rows_Q=Q, quant_rows_s=s)
+    F = np.zeros_like(X)
+    assert R.lib.jt_w8a8_fakequant_per_channel(X, X.shape[0], X.shape[1], F) == 0
+    D = np.zeros_like(X)
+    assert R.lib.jt_w8a8_dequant_per_channel(Q, s, X.shape[0], X.shape[1], D) == 0
+    g.update(fakequant_rows=F, dequant_rows=D)
+    x = (rng.standard_normal(1001) * 3).astype(np.float32)
+    rc, q, s1 = R.quant_tensor(x)
+    assert rc == 0
+    g.update(quant_tensor_x=x, quant_tensor_q=q, quant_tensor_s=np.float32(s1))
+
+    # ---- W8A8 GEMMs ----
+    M, N, K = 13, 40, 96
+    Aq = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    Bq = rng.integers(-127, 128, (K, N), dtype=np.int8)
+    sB = rng.uniform(1e-3, 1e-2, N).astype(np.float32)
+    rc, C = R.gemm_per_channel(Aq, Bq, 0.0173, sB)
+    assert rc == 0
+    g.update(gemm_pc_A=Aq, gemm_pc_B=Bq, gemm_pc_sA=np.float32(0.0173), gemm_pc_sB=sB,
+             gemm_pc_C=C)
+    rc, C = R.gemm_per_tensor(Aq, Bq, 0.031, 0.0047)
+    assert rc == 0
+    g.update(gemm_pt_sA=np.float32(0.031), gemm_pt_sB=np.float32(0.0047), gemm_pt_C=C)
+    A = rng.standard_normal((7, 33)).astype(np.float32)
+    B = rng.standard_normal((33, 19)).astype(np.float32)
+    rc, C = R.gemm_f32(A, B)
+    assert rc == 0
+    g.update(gemm_f32_A=A, gemm_f32_B=B, gemm_f32_C=C)
+
+    # ---- low-bit levels ----
+    w = rng.standard_normal(257).astype(np.float32)
+    for bits in (2, 4):
+        rc, fq = R.lowbit_fakequant(w, bits)
+        assert rc == 0
+        g[f"fq{bits}_w"], g[f"fq{bits}_out"] = w, fq
+        col = rng.standard_normal(64).astype(np.float32)
+        rc, idx, ws = R.col_to_idx(col, bits)
+        assert rc == 0
+        g[f"c2i{bits}_col"], g[f"c2i{bits}_idx"], g[f"c2i{bits}_ws"] = col, idx, np.float32(ws)
+        Xl = rng.standard_normal((5, 64)).astype(np.float32)
+        Wl = rng.standard_normal((64, 24)).astype(np.float32)
+        rc, Y = R.lowbit_gemm_lut(Xl, Wl, bits)
+        assert rc == 0
+        g[f"lut{bits}_X"], g[f"lut{bits}_W"], g[f"lut{bits}_Y"] = Xl, Wl, Y
+
+    # ---- T-MAC LUT ----
+    act = rng.standard_normal((3, 64)).astype(np.float32)
+    rc, ql, sc, bi = R.tmac_lut_ctor(act)
+    assert rc == 0
+    col = rng.standard_normal(64).astype(np.float32)
+    outs = []
+    for bits in (2, 4):
+        rc, idx, ws = R.col_to_idx(col, bits)
+        for r in range(3):
+            rc, o = R.tmac_lookup_accum(ql[r].ravel(), idx, sc[r], bi[r], bits, ws)
+            assert rc == 0
+            outs.append(o)
+    g.update(tmac_act=act, tmac_qlut=ql, tmac_scales=sc, tmac_biases=bi, tmac_col=col,
+             tmac_out=np.array(outs, np.float32))
+
+    # ---- routing top-k ----
+    L = rng.standard_normal((8, 256)).astype(np.float32)
+    L[1, 10:20] = 2.5  # exact ties
+    L[2, :] = 1.0      # all equal
+    L[3, 100:] = -np.inf  # masked
+    ids = np.zeros((8, 8), np.int64)
+    wts = np.zeros((8, 8), np.float32)
+    for t in range(8):
+        rc, ids[t], wts[t] = R.topk(L[t], 8)
+        assert rc == 0
+    g.update(topk_logits=L, topk_ids=ids, topk_w=wts)
+
+    # ---- batch sort ----
+    T, k, E = 64, 8, 32
+    p = 1.0 / np.arange(1, E + 1) ** 1.1
+    p /= p.sum()
+    sid = np.stack([rng.choice(E, size=k, replace=False, p=p) for _ in range(T)])
+    g["sort_ids"] = sid.astype(np.int64)
+    for tag, cap in (("c10", 1.0), ("c15", 1.5)):
+        rc, perm, off, drop = R.batch_sort(sid, T, k, E, cap)
+        assert rc == 0
+        g[f"sort_{tag}_perm"], g[f"sort_{tag}_off"], g[f"sort_{tag}_drop"] = perm, off, drop
+
+    # ---- legacy layer (small) ----
+    T, n, h, E, k, S = 6, 64, 32, 8, 2, 1
+    Xl = rng.standard_normal((T, n)).astype(np.float32)
+    Wgate = (rng.standard_normal((E, n)) / 8).astype(np.float32)
+    Wg = (rng.standard_normal((E, h, n)) / 8).astype(np.float32)
+    Wu = (rng.standard_normal((E, h, n)) / 8).astype(np.float32)
+    Wd = (rng.standard_normal((E, h, n)) / 6).astype(np.float32)
+    Wgs = (rng.standard_normal((S, h, n)) / 8).astype(np.float32)
+    Wus = (rng.standard_normal((S, h, n)) / 8).astype(np.float32)
+    Wds = (rng.standard_normal((S, h, n)) / 6).astype(np.float32)
+    g.update(layer_X=Xl, layer_Wgate=Wgate, layer_Wg=Wg, layer_Wu=Wu, layer_Wd=Wd,
+             layer_Wgs=Wgs, layer_Wus=Wus, layer_Wds=Wds)
+    for f, (w8, lb) in enumerate(((0, 0), (1, 0), (0, 1))):
+        r = R.moe_fwd_batch(Xl, Wgate, Wg, Wu, Wd, Wgs, Wus, Wds, k, 1.5, w8, lb)
+        assert r["rc"] == 0
+        for key in ("Y", "ids", "w", "perm", "off", "drop"):
+            g[f"layer{f}_{key}"] = r[key]
+
+    np.savez_compressed(OUT, **g)
+    print(f"wrote {OUT}: {len(g)} arrays, {os.path.getsize(OUT)} bytes")
+
+
+if __name__ == "__main__":
+    main()

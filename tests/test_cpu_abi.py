@@ -1,0 +1,146 @@
+"""CPU checks of the boundary: the C-ABI library and its host-side logic.
+
+No GPU is touched: the library is loaded, its exports are compared with the
+prototypes of include/jimotono/*.h, argument validation that precedes any
+device work is exercised, and the product's refusal to run without its HIP
+library or without a GPU is checked.
+"""
+import ctypes as C
+import errno as E
+import os
+import re
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+INC = os.path.join(ROOT, "include", "jimotono")
+LIB = os.path.join(ROOT, "jimotono_amd", "libjimotono_hip.so")
+
+_DECL = re.compile(r"^\s*(?:[A-Za-z_][\w\s\*]*?)\b(jt_\w+)\s*\(", re.M)
+
+
+def declared():
+    names = set()
+    for f in sorted(os.listdir(INC)):
+        if not f.endswith(".h"):
+            continue
+        text = open(os.path.join(INC, f)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        text = re.sub(r"//[^\n]*", "", text)
+        text = re.sub(r"#define[^\n]*", "", text)
+        for m in _DECL.finditer(text):
+            names.add(m.group(1))
+    return names
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(LIB):
+        pytest.fail(f"{LIB} not built: run `make -C jimotono_amd/csrc`")
+    return C.CDLL(LIB, use_errno=True)
+
+
+def test_headers_declare_the_path():
+    names = declared()
+    for must in ("jt_w8a8_gemm_per_channel", "jt_w8a8_quant_per_channel", "jt_routing_topk",
+                 "jt_moe_batch_sort", "jt_moe_fwd_batch", "jt_lowbit_gemm_lut",
+                 "jt_tmac_lut_ctor", "jt_gemm_mat_f32", "jt_hip_moe_fwd", "jt_hip_w8a8_gemm"):
+        assert must in names
+    assert len(names) >= 40
+
+
+def test_every_declared_symbol_is_exported(lib):
+    missing = [n for n in sorted(declared()) if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+
+
+def test_no_gpu_fails_loudly(lib):
+    """Without a visible GPU the entry points report JT_ERR_IO with errno
+    ENODEV (include/jimotono/common.h); there is no CPU fallback."""
+    try:
+        import torch
+        if torch.cuda.is_available():
+            pytest.skip("a GPU is visible")
+    except ImportError:
+        pass
+    lib.jt_hip_init.argtypes = [C.c_int]
+    C.set_errno(0)
+    assert lib.jt_hip_init(0) == 3 and C.get_errno() == E.ENODEV
+    f32 = np.ones(4, np.float32)
+    q = np.zeros(4, np.int8)
+    s = np.zeros(1, np.float32)
+    fn = lib.jt_w8a8_quant_per_tensor
+    fn.argtypes = [C.c_void_p, C.c_size_t, C.c_void_p, C.c_void_p]
+    assert fn(f32.ctypes.data, 4, q.ctypes.data, s.ctypes.data) == 3
+    assert not q.any() and s[0] == 0  # outputs untouched
+
+
+def test_validation_before_device_work(lib):
+    """Fail-closed argument checks of the reference (src/w8a8.c:910-953,
+    bench/kernel/test_w8a8.c:86-112) run before any device call."""
+    g = lib.jt_w8a8_gemm_per_channel
+    g.argtypes = [C.c_void_p, C.c_void_p, C.c_float, C.c_void_p, C.c_void_p, C.c_int,
+                  C.c_int, C.c_int]
+    A = np.ones((2, 4), np.int8)
+    B = np.ones((4, 3), np.int8)
+    sB = np.ones(3, np.float32)
+    out = np.full((2, 3), 7.0, np.float32)
+    p = lambda a: a.ctypes.data  # noqa: E731
+    cases = [
+        (None, p(B), 1.0, p(sB), p(out), 2, 3, 4),
+        (p(A), p(B), 0.0, p(sB), p(out), 2, 3, 4),
+        (p(A), p(B), float("nan"), p(sB), p(out), 2, 3, 4),
+        (p(A), p(B), 1.0, p(sB), p(out), 2, 4097, 4),
+        (p(A), p(B), 1.0, p(sB), p(out), -1, 3, 4),
+        (p(A), p(B), 1.0, p(sB), p(out), 2, 3, 0),
+        (p(A), p(B), 1.0, None, p(out), 2, 3, 4),
+    ]
+    for c in cases:
+        C.set_errno(0)
+        assert g(*c) == 2 and C.get_errno() == E.EINVAL, c
+    assert np.all(out == 7.0)
+    # M == 0 is a successful no-op (src/w8a8.c:959-971)
+    assert g(p(A), p(B), 1.0, p(sB), p(out), 0, 3, 4) == 0
+    t = lib.jt_routing_topk
+    t.argtypes = [C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p, C.c_void_p]
+    lg = np.zeros(2, np.float32)
+    ids = np.zeros(2, np.uint64)
+    w = np.zeros(2, np.float32)
+    for args in [(None, 2, 1), (p(lg), 0, 1), (p(lg), 2, 0), (p(lg), 2, 3)]:
+        assert t(args[0], args[1], args[2], p(ids), p(w)) == 2
+    m = lib.jt_lowbit_set_mode
+    m.argtypes = [C.c_int]
+    assert m(3) == 2 and m(-1) == 2
+    bf = lib.jt_lowbit_bits_for
+    bf.argtypes = [C.c_int, C.POINTER(C.c_int)]
+    b = C.c_int(0)
+    assert bf(0, C.byref(b)) == 0 and b.value == 2
+    assert bf(1, C.byref(b)) == 0 and b.value == 4
+
+
+def test_api_refuses_without_library(monkeypatch, tmp_path):
+    import jimotono_amd.api as api
+    monkeypatch.setattr(api, "LIB_PATH", str(tmp_path / "missing.so"))
+    monkeypatch.setattr(api, "_LIB", None)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        api.lib()
+
+
+def test_bench_refuses_multi_gpu():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2 and "one MI355X" in r.stderr
+
+
+def test_product_never_imports_the_oracle():
+    """Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline may
+    use oracle/; the package and the C sources never do."""
+    pkg = os.path.join(ROOT, "jimotono_amd")
+    for dp, _, fs in os.walk(pkg):
+        for f in fs:
+            if f.endswith((".py", ".c", ".h", ".hip", "Makefile")):
+                text = open(os.path.join(dp, f), errors="ignore").read()
+                assert "oracle" not in text.replace("oracle/", "").lower() or f == "README", f
