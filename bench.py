@@ -40,6 +40,13 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-sub", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=15.0)
+    p.add_argument("--serial", action="store_true",
+                   help="run the timed region with every stage in order on one stream "
+                        "(as the profiled pass does), so that a kernel trace of the "
+                        "whole run sees each kernel alone on the GPU")
+    p.add_argument("--copy-probe", action="store_true",
+                   help="also run a plain 256 MiB device copy (the reference kernel "
+                        "for scaling HBM byte counters)")
     return p.parse_args()
 
 
@@ -108,8 +115,17 @@ def main():
         step()
     torch.cuda.synchronize()
     assert api.sync_errors(stream) == 0
+    if args.copy_probe:
+        src = torch.empty(64 << 20, device="cuda", dtype=torch.float32).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(2):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     # timed region: the production path (shared experts overlap the routed
-    # path on side streams)
+    # path on side streams), or with --serial every stage in stream order
+    if args.serial:
+        L.set_profiling(True)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -120,6 +136,7 @@ def main():
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
     ev_ms = e0.elapsed_time(e1) / args.steps
+    L.set_profiling(False)
     assert api.sync_errors(stream) == 0
     ms_per_step = wall_ms
     tokens_per_s = T / (ms_per_step / 1e3)
@@ -149,10 +166,14 @@ def main():
     dom_ms = per_launch[dom]
     achieved = ops[dom] / (dom_ms / 1e3)
     total_ops = 2.0 * T * (S * (2 * hs * n + n * hs) + k * (2 * h * n + n * h))
+    traffic = measured_traffic(dom)
     roofline = {"bound": "mfma", "kernel": dom, "achieved": achieved / 1e12,
                 "peak": INT8_PEAK / 1e12, "unit": "TFLOP/s",
-                "frac": achieved / INT8_PEAK, "traffic": None,
+                "frac": achieved / INT8_PEAK,
+                "traffic": None if traffic is None else traffic["bytes"],
                 "ops_per_launch": ops[dom], "avg_launch_ms": dom_ms}
+    if traffic is not None:
+        roofline["traffic_source"] = traffic["source"]
 
     out = {
         "metric": "MoE-layer tokens/s; int8 TOPS (prefill) and HBM GB/s (decode) vs roofline",
@@ -160,6 +181,7 @@ def main():
         "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "int8",
         "data": "synthetic (seeded N(0,1) activations, random-init weights)",
+        "serial": bool(args.serial),
         "config": {"workload": "moe_layer_prefill", "tokens": T, "d_model": n,
                    "routed_experts": E, "expert_ffn": h, "topk": k, "shared_experts": S,
                    "shared_ffn": hs, "routed_quant": "INT2 gate/up, INT4 down, fp16 g64",
@@ -186,6 +208,20 @@ def main():
     if not args.no_sub:
         out["sub"] = sub_benchmarks(np, torch, api, stream)
     print(json.dumps(out), flush=True)
+
+
+def measured_traffic(stage):
+    """HBM bytes per launch of a stage's kernel from the committed rocprofv3
+    PMC summary (FETCH_SIZE and WRITE_SIZE, each scaled by the same counter's
+    reading for a plain copy of known size), or None when none is recorded."""
+    path = os.path.join(ROOT, "profiles", f"{stage}_pmc_traffic.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return {"bytes": float(line.split(":", 1)[1]),
+                    "source": os.path.relpath(path, ROOT)}
+    return None
 
 
 def cpu_baseline(np, torch, W, X, n, h, E, k, S, hs, seconds):
