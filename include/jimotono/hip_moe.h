@@ -16,8 +16,9 @@
  * on that stream. Arguments are validated on the host before anything is
  * enqueued (JT_ERR_INVAL, nothing written). Data-dependent failures found by
  * the kernels (a non-finite activation, an overflowing epilogue) raise bits in
- * a per-stream device error word instead of a partial result being trusted;
- * jt_hip_sync_errors() waits for the stream and returns them.
+ * the library's device error word (one per process, shared by every stream)
+ * instead of a partial result being trusted; jt_hip_sync_errors() waits for
+ * a stream and returns (and clears) the bits raised so far by any stream.
  *
  * Formats of a prepared layer (built on the GPU from fp32 weights):
  *  - shared experts: int8 codes, one fp32 scale per output channel (the
@@ -45,7 +46,7 @@ extern "C" {
 /* Bind the calling thread's HIP device (idempotent; called implicitly by
  * every other entry point with device 0). */
 int jt_hip_init(int device);
-/* Wait for `stream`, then read and clear its device error word.
+/* Wait for `stream`, then read and clear the library's device error word.
  * *out_flags gets the raised JT_HIP_EF_* bits (0 = clean). Returns JT_OK, or
  * JT_ERR_IO on a HIP failure. */
 int jt_hip_sync_errors(void *stream, uint32_t *out_flags);

@@ -366,6 +366,8 @@ class RefLib:
         L.jt_moe_fwd_batch.argtypes = [_f32p] * 9 + [C.c_int] * 6 + [
             _u64p, _f32p] + [C.c_void_p] * 5 + [C.c_float, _u64p, _u64p, _u8p,
                                                 C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
+        L.jt_moe_fwd.argtypes = [_f32p] * 9 + [C.c_int] * 5 + [_u64p, _f32p, _f32p] + [
+            C.c_void_p] * 5
 
     def quant_rows(self, X):
         X = _c(X, np.float32)
@@ -494,6 +496,25 @@ class RefLib:
         return dict(rc=rc, Y=Y, ids=ids.astype(np.int64), w=w,
                     perm=perm[: kept.value].astype(np.int64), off=off.astype(np.int64),
                     drop=drop, Ysel=Ysel)
+
+
+    def moe_fwd_single(self, x, Wgate, Wg, Wu, Wd, Wg_s, Wu_s, Wd_s, k):
+        """jt_moe_fwd for one token; returns rc, Y, ids, weights, logits."""
+        x = _c(x, np.float32).ravel()
+        n = x.size
+        E, h = Wg.shape[0], Wg.shape[1]
+        S = 0 if Wg_s is None else Wg_s.shape[0]
+        z = np.zeros(1, np.float32)
+        Y = np.zeros(n, np.float32)
+        ids = np.zeros(k, np.uint64)
+        w = np.zeros(k, np.float32)
+        lg = np.zeros(E, np.float32)
+        rc = self.lib.jt_moe_fwd(
+            x, _c(Wgate, np.float32), _c(Wg, np.float32), _c(Wu, np.float32),
+            _c(Wd, np.float32), z if S == 0 else _c(Wg_s, np.float32),
+            z if S == 0 else _c(Wu_s, np.float32), z if S == 0 else _c(Wd_s, np.float32),
+            Y, n, h, E, k, S, ids, w, lg, None, None, None, None, None)
+        return rc, Y, ids.astype(np.int64), w, lg
 
 
 def ref_available() -> bool:

@@ -23,6 +23,8 @@ Cases (key prefixes in the .npz):
   topk_*         jt_routing_topk (random logits, exact ties, -inf masks)
   sort_*         jt_moe_batch_sort at cap 1.0 and 1.5 (drops)
   layer{f}_*     jt_moe_fwd_batch, f = 0 fp32, 1 W8A8 flag, 2 low-bit mode 1
+  logits_*       jt_moe_fwd out_logits (gate logits, src/moe_layer.c:67-86), with
+                 rows whose fp64 sum depends on the 4-lane summation order
 """
 import os
 import sys
@@ -151,6 +153,27 @@ def main():
         assert r["rc"] == 0
         for key in ("Y", "ids", "w", "perm", "off", "drop"):
             g[f"layer{f}_{key}"] = r[key]
+
+    # ---- gate logits (jt_moe_fwd's out_logits): random rows with an odd
+    # tail, and rows whose fp64 sum depends on the 4-lane order ----
+    n, E = 1027, 6
+    Wg1 = (rng.standard_normal((E, 4, n)) / 30).astype(np.float32)
+    WgateL = (rng.standard_normal((E, n)) / 30).astype(np.float32)
+    lgs = []
+    XL = rng.standard_normal((12, n)).astype(np.float32)
+    for t in range(12):
+        rc, _, _, _, lg = R.moe_fwd_single(XL[t], WgateL, Wg1, Wg1, Wg1, None, None, None, 2)
+        assert rc == 0
+        lgs.append(lg)
+    g.update(logits_X=XL, logits_Wgate=WgateL, logits_out=np.array(lgs, np.float32))
+    big = np.float32(2.0 ** 60)
+    pat = np.array([big, 1, 1, 1, -big, 1, 1, 1, 1, -1, 1], np.float32)
+    Wadv = np.stack([pat, pat[::-1].copy(), np.roll(pat, 1), np.roll(pat, 2)])
+    Wa1 = np.zeros((4, 1, 11), np.float32)
+    rc, _, _, _, lga = R.moe_fwd_single(np.ones(11, np.float32), Wadv, Wa1, Wa1, Wa1, None,
+                                        None, None, 1)
+    assert rc == 0
+    g.update(logits_adv_W=Wadv, logits_adv_out=lga)
 
     np.savez_compressed(OUT, **g)
     print(f"wrote {OUT}: {len(g)} arrays, {os.path.getsize(OUT)} bytes")

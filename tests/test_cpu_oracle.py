@@ -117,6 +117,20 @@ def test_golden_layer(orc, gold, f, w8, lb):
     assert np.array_equal(bits(r["Y"]), bits(gold[f"layer{f}_Y"]))
 
 
+def test_golden_logits(orc, gold):
+    X, W = gold["logits_X"], gold["logits_Wgate"]
+    got = np.array([[orc.logit_lane4(X[t], W[e]) for e in range(W.shape[0])]
+                    for t in range(X.shape[0])], np.float32)
+    assert np.array_equal(bits(got), bits(gold["logits_out"]))
+    Wa = gold["logits_adv_W"]
+    ones = np.ones(Wa.shape[1], np.float32)
+    adv = np.array([orc.logit_lane4(ones, Wa[e]) for e in range(Wa.shape[0])], np.float32)
+    assert np.array_equal(bits(adv), bits(gold["logits_adv_out"]))
+    # the sequential sum gives other values for these rows: the lane order is pinned
+    seq = np.array([np.float32(sum(float(v) for v in Wa[e])) for e in range(Wa.shape[0])])
+    assert not np.array_equal(seq, gold["logits_adv_out"])
+
+
 # ------------------------------------------- the reference tests' answers
 
 def test_known_topk(orc):

@@ -1,0 +1,160 @@
+"""GPU parity of the remaining host-pointer ABI (the reference's own entry
+points, run on the MI355X) against the oracle.
+
+Reference behaviour followed: src/moe_gemm.c:17-170 (fp32 GEMM, transpose),
+src/lowbit.c:31-267 (levels, col_to_idx, T-MAC GEMM), src/tmac.c:168-506
+(LUT), src/routing.c:16-76 (top-k), src/moe_layer.c:895-978 (batch sort) and
+:1616-1663 (batched layer in its fp32, W8A8 and low-bit modes).
+
+Bit-exact except where the value passes through exp (softmax weights,
+SwiGLU): there the reference's own tolerance applies (test_routing.c:35-37,
+test_moe_layer.c:146-189).
+"""
+import numpy as np
+import pytest
+
+from conftest import announce
+
+pytestmark = pytest.mark.gpu
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+@pytest.mark.parametrize("M,N,K", [(7, 19, 33), (64, 96, 128), (130, 70, 257)])
+def test_gemm_mat_f32(jt, orc, M, N, K):
+    announce(f"gemm_mat_f32 {M}x{N}x{K}")
+    rng = np.random.default_rng(M + N + K)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    rc, C = jt.gemm_mat_f32(A, B)
+    assert rc == 0 and np.array_equal(bits(C), bits(orc.gemm_f32(A, B)))
+
+
+def test_transpose_f32(jt):
+    announce("transpose_f32")
+    rng = np.random.default_rng(1)
+    for r, c in [(1, 1), (3, 70), (129, 65)]:
+        A = rng.standard_normal((r, c)).astype(np.float32)
+        rc, T = jt.transpose_f32(A)
+        assert rc == 0 and np.array_equal(T, A.T)
+
+
+@pytest.mark.parametrize("b", [2, 4])
+def test_lowbit_levels(jt, orc, b):
+    announce(f"lowbit fakequant / col_to_idx bits={b}")
+    rng = np.random.default_rng(b)
+    w = rng.standard_normal(1000).astype(np.float32)
+    rc, fq = jt.lowbit_fakequant(w, b)
+    rc2, fq2 = orc.lowbit_fakequant(w, b)
+    assert rc == rc2 == 0 and np.array_equal(bits(fq), bits(fq2))
+    for k in (32, 64, 256):
+        col = rng.standard_normal(k).astype(np.float32)
+        rc, idx, ws = jt.lowbit_col_to_idx(col, b)
+        rc2, idx2, ws2 = orc.col_to_idx(col, b)
+        assert rc == rc2 == 0 and np.array_equal(idx, idx2) and ws == ws2
+
+
+@pytest.mark.parametrize("b", [2, 4])
+@pytest.mark.parametrize("me,h,k", [(1, 24, 64), (5, 40, 256), (3, 17, 100)])
+def test_lowbit_gemm_lut(jt, orc, b, me, h, k):
+    announce(f"lowbit_gemm_lut bits={b} {me}x{h}x{k}")
+    rng = np.random.default_rng(b * 100 + me + h + k)
+    X = rng.standard_normal((me, k)).astype(np.float32)
+    W = rng.standard_normal((k, h)).astype(np.float32)
+    rc, Y = jt.lowbit_gemm_lut(X, W, b)
+    rc2, Y2 = orc.lowbit_gemm_lut(X, W, b)
+    assert rc == rc2 == 0 and np.array_equal(bits(Y), bits(Y2))
+
+
+def test_tmac(jt, orc):
+    announce("tmac lut ctor + lookup")
+    rng = np.random.default_rng(3)
+    act = rng.standard_normal((4, 128)).astype(np.float32)
+    rc, q, s, b = jt.tmac_lut_ctor(act)
+    rc2, q2, s2, b2 = orc.tmac_lut_ctor(act)
+    assert rc == rc2 == 0
+    assert np.array_equal(q, q2) and np.array_equal(bits(s), bits(s2))
+    assert np.array_equal(bits(b), bits(b2))
+    col = rng.standard_normal(128).astype(np.float32)
+    for bb in (2, 4):
+        _, idx, ws = orc.col_to_idx(col, bb)
+        for r in range(4):
+            rc, o = jt.tmac_lookup_accum(q[r], idx, s[r], b[r], bb, ws)
+            rc2, o2 = orc.tmac_lookup_accum(q2[r].ravel(), idx, s2[r], b2[r], bb, ws)
+            assert rc == rc2 == 0 and bits(np.float32(o)) == bits(np.float32(o2))
+
+
+def test_routing_topk(jt, orc):
+    announce("routing_topk")
+    rng = np.random.default_rng(4)
+    cases = [rng.standard_normal(256).astype(np.float32),
+             np.full(64, 1.0, np.float32),
+             np.round(rng.standard_normal(300) * 2).astype(np.float32) / 2,
+             np.array([2.0, 1.0, -np.inf, -np.inf], np.float32)]
+    for lg in cases:
+        for k in (1, 2, min(8, lg.size)):
+            rc, ids, w = jt.routing_topk(lg, k)
+            rc2, ids2, w2 = orc.topk(lg, k)
+            assert rc == rc2 == 0 and np.array_equal(ids, ids2)
+            np.testing.assert_allclose(w, w2, rtol=1e-6, atol=0)
+    assert jt.routing_topk(np.array([1.0, np.nan], np.float32), 1)[0] == 2
+
+
+@pytest.mark.parametrize("cap", [1.0, 1.5])
+def test_batch_sort(jt, orc, cap):
+    announce(f"moe_batch_sort cap={cap}")
+    rng = np.random.default_rng(5)
+    T, k, E = 200, 4, 16
+    p = 1.0 / np.arange(1, E + 1) ** 1.1
+    p /= p.sum()
+    ids = np.stack([rng.choice(E, size=k, replace=False, p=p) for _ in range(T)])
+    rc, perm, off, drop, dropped = jt.moe_batch_sort(ids, T, k, E, cap)
+    rc2, perm2, off2, drop2 = orc.batch_sort(ids, T, k, E, cap)
+    assert rc == rc2 == 0
+    assert np.array_equal(perm, perm2) and np.array_equal(off, off2)
+    assert np.array_equal(drop, drop2) and dropped == int(drop2.sum())
+
+
+@pytest.mark.parametrize("w8,lb", [(0, 0), (1, 0), (0, 1), (0, 2), (1, 1)])
+def test_moe_fwd_batch_modes(jt, orc, w8, lb):
+    announce(f"moe_fwd_batch w8a8={w8} lowbit={lb}")
+    rng = np.random.default_rng(10 + 3 * w8 + lb)
+    T, n, h, E, k, S = 12, 128, 64, 8, 2, 1
+    X = rng.standard_normal((T, n)).astype(np.float32)
+    W = [(rng.standard_normal(s) / 8).astype(np.float32)
+         for s in [(E, n), (E, h, n), (E, h, n), (E, h, n), (S, h, n), (S, h, n), (S, h, n)]]
+    lib = jt.lib()
+    assert lib.jt_w8a8_set_enabled(w8) == 0 and lib.jt_lowbit_set_mode(lb) == 0
+    try:
+        r = jt.moe_fwd_batch(X, *W, k, 1.25)
+        ru = jt.moe_fwd_batch(X, *W, k, 1.25, unchecked=True)
+    finally:
+        lib.jt_w8a8_set_enabled(0)
+        lib.jt_lowbit_set_mode(0)
+    o = orc.moe_fwd_batch(X, *W, k, 1.25, w8, lb)
+    assert r["rc"] == o["rc"] == 0 and ru["rc"] == 0
+    for key in ("ids", "perm", "off", "drop"):
+        assert np.array_equal(r[key], o[key]), key
+        assert np.array_equal(ru[key], o[key]), key
+    np.testing.assert_allclose(r["w"], o["w"], rtol=1e-6, atol=0)
+    tol = 1e-5 * float(np.abs(o["Y"]).max())
+    np.testing.assert_allclose(r["Y"], o["Y"], rtol=1e-5, atol=tol)
+    assert np.array_equal(bits(r["Y"]), bits(ru["Y"]))
+
+
+def test_moe_fwd_batch_known_answer(jt):
+    """bench/kernel/test_moe_layer.c:146-189 through the batched entry."""
+    announce("moe_fwd_batch known answer")
+    X = np.array([[1.0, 0.5]], np.float32)
+    Wgate = np.array([1, 0, 0, 1, -1, 0], np.float32).reshape(3, 2)
+    Wg = np.array([0.5, -0.5, 0.5, 1.0, 0, 0], np.float32).reshape(3, 1, 2)
+    Wu = np.array([1.0, 0, 0.5, -0.5, 0, 0], np.float32).reshape(3, 1, 2)
+    Wd = np.array([1.0, 2.0, -1.0, 0.5, 0, 0], np.float32).reshape(3, 1, 2)
+    Ws = [np.array(v, np.float32).reshape(1, 1, 2) for v in ([0.5, 0.5], [1.0, -1.0],
+                                                              [0.5, -0.5])]
+    r = jt.moe_fwd_batch(X, Wgate, Wg, Wu, Wd, *Ws, 2, 1.5)
+    assert r["rc"] == 0 and list(r["ids"][0]) == [0, 1]
+    assert abs(r["Y"][0, 0] - 0.14582792210843093) < 1e-5
+    assert abs(r["Y"][0, 1] - 0.08212054137232436) < 1e-5
