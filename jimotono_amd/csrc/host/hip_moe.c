@@ -7,7 +7,9 @@
  *   2 router         fp64 gate logits, lane order          (src/moe_layer.c:67-86)
  *   3 topk           top-k + softmax                       (src/routing.c:16-76)
  *   4 sort           dropless stable expert sort           (src/moe_layer.c:895-978)
- *   5 tiles          64-row work list of the sorted pairs
+ *   5 tiles          work list of the sorted pairs: 64-row tiles, or 16-row
+ *                    tiles when experts get few rows (decode); up to 1024
+ *                    pairs the sort and the list are one launch
  *   6 routed_gateup  INT2 grouped GEMM + SwiGLU            (src/moe_layer.c:1301-1365)
  *   7 routed_quant   per-row int8 requantisation of SwiGLU output
  *   8 routed_down    INT4 grouped GEMM, rows scattered to their (token, slot)
@@ -216,6 +218,8 @@ struct jt_hip_moe {
     int8_t *Xq;
     float *sx, *logits, *w, *Sr, *ssr, *Ye, *Ys;
     int32_t *ids, *rank, *cnt, *tot, *off, *perm, *tiles, *ntiles;
+    const int32_t *cur_ids; /* ids / weights of the last forward (caller's */
+    const float *cur_w;     /* arrays after jt_hip_moe_fwd_routed) */
     int8_t *Sqr;
     int last_T;
     /* shared experts run on side streams forked after the input quantiser
@@ -297,7 +301,7 @@ int jt_hip_moe_prepare(const jt_hip_moe_desc *desc, const float *dWgate, const f
     ALLOC(L->tot, (size_t)E * 4);
     ALLOC(L->off, (size_t)(E + 1) * 4);
     ALLOC(L->perm, (size_t)Tk * 4);
-    ALLOC(L->tiles, (size_t)(Tk / 64 + E + 1) * 4);
+    ALLOC(L->tiles, (size_t)(Tk / 16 + E + 1) * 16); /* int4 descriptors */
     ALLOC(L->ntiles, 4);
     ALLOC(L->Sr, (size_t)Tk * h * 4);
     ALLOC(L->Sqr, (size_t)Tk * h);
@@ -408,7 +412,6 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
     hipStream_t s = stream ? (hipStream_t)stream : rt->stream;
     const int n = d->n, h = d->h, E = d->n_experts, k = d->topk, S = d->n_shared;
     const int Tk = T * k;
-    const int max_tiles = Tk / 64 + E;
     uint32_t *err = rt->d_err;
     int slot = 0, rc = prof_begin(L, &slot);
     if (rc != JT_OK) return rc;
@@ -430,29 +433,43 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
         for (int i = 0; i < L->nside; i++) le |= (int)hipEventRecord(L->ev_join[i], L->side[i]);
     }
     prof_mark(L, slot, ST_ROUTER, s);
+    const int32_t *ids = L->ids;
+    const float *w = L->w;
     if (d_ids) {
-        le |= (int)hipMemcpyAsync(L->ids, d_ids, (size_t)Tk * 4, hipMemcpyDeviceToDevice, s);
-        le |= (int)hipMemcpyAsync(L->w, d_w, (size_t)Tk * 4, hipMemcpyDeviceToDevice, s);
+        ids = d_ids; /* caller-routed: read in place */
+        w = d_w;
         prof_mark(L, slot, ST_TOPK, s);
     } else {
         le |= jtk_router_logits(dX, L->Wgate, T, E, n, L->logits, err, s);
         prof_mark(L, slot, ST_TOPK, s);
         le |= jtk_topk(L->logits, T, E, k, L->ids, NULL, L->w, err, s);
     }
+    L->cur_ids = ids;
+    L->cur_w = w;
+    /* 16-row tiles when experts average at most 16 rows; the single-launch
+     * sort up to 1024 pairs */
+    const int R = Tk <= 16 * E ? 16 : 64;
+    const int max_tiles = Tk / R + E;
     prof_mark(L, slot, ST_SORT, s);
-    le |= jtk_sort(L->ids, Tk, E, (int64_t)Tk, L->rank, L->cnt, L->tot, L->off, NULL, L->perm,
-                   NULL, NULL, err, s);
-    prof_mark(L, slot, ST_TILES, s);
-    le |= jtk_make_tiles(L->off, E, L->tiles, L->ntiles, s);
+    if (Tk <= 1024 && E <= 4096) {
+        le |= jtk_sort_small(ids, Tk, E, (int64_t)Tk, R, L->off, NULL, L->perm, NULL, NULL,
+                             L->tiles, L->ntiles, err, s);
+        prof_mark(L, slot, ST_TILES, s);
+    } else {
+        le |= jtk_sort(ids, Tk, E, (int64_t)Tk, L->rank, L->cnt, L->tot, L->off, NULL, L->perm,
+                       NULL, NULL, err, s);
+        prof_mark(L, slot, ST_TILES, s);
+        le |= jtk_make_tiles(L->off, E, R, L->tiles, L->ntiles, s);
+    }
     prof_mark(L, slot, ST_R_GATEUP, s);
     le |= jtk_lowbit_grouped(2, L->Xq, n, L->sx, L->perm, L->off, k, L->tiles, L->ntiles,
-                             max_tiles, L->gu_P, L->gu_S, L->gu_pstride, L->gu_sstride, 2 * h,
+                             max_tiles, R, L->gu_P, L->gu_S, L->gu_pstride, L->gu_sstride, 2 * h,
                              n, L->Sr, h, err, s);
     prof_mark(L, slot, ST_R_QUANT, s);
     le |= jtk_quant_rows(L->Sr, Tk, h, L->Sqr, h, L->ssr, NULL, err, s);
     prof_mark(L, slot, ST_R_DOWN, s);
     le |= jtk_lowbit_grouped(4, L->Sqr, h, L->ssr, L->perm, L->off, k, L->tiles, L->ntiles,
-                             max_tiles, L->dn_P, L->dn_S, L->dn_pstride, L->dn_sstride, n, h,
+                             max_tiles, R, L->dn_P, L->dn_S, L->dn_pstride, L->dn_sstride, n, h,
                              L->Ye, n, err, s);
     if (fork) {
         for (int i = 0; i < L->nside; i++) le |= (int)hipStreamWaitEvent(s, L->ev_join[i], 0);
@@ -464,7 +481,7 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
         }
     }
     prof_mark(L, slot, ST_COMBINE, s);
-    le |= jtk_combine(L->w, L->Ye, NULL, L->Ys, S, T, k, n, dY, err, s);
+    le |= jtk_combine(w, L->Ye, NULL, L->Ys, S, T, k, n, dY, err, s);
     prof_mark(L, slot, ST_N, s);
     return le ? jt_rt_err(hipErrorLaunchFailure) : JT_OK;
 }
@@ -485,8 +502,8 @@ int jt_hip_moe_buffer(const jt_hip_moe *L, int which, void **dptr, size_t *bytes
     const size_t T = (size_t)L->last_T, k = (size_t)L->d.topk, n = (size_t)L->d.n;
     const size_t E = (size_t)L->d.n_experts, S = (size_t)L->d.n_shared;
     switch (which) {
-    case JT_HIP_BUF_IDS: *dptr = L->ids; *bytes = T * k * 4; break;
-    case JT_HIP_BUF_WEIGHTS: *dptr = L->w; *bytes = T * k * 4; break;
+    case JT_HIP_BUF_IDS: *dptr = (void *)(L->cur_ids ? L->cur_ids : L->ids); *bytes = T * k * 4; break;
+    case JT_HIP_BUF_WEIGHTS: *dptr = (void *)(L->cur_w ? L->cur_w : L->w); *bytes = T * k * 4; break;
     case JT_HIP_BUF_PERM: *dptr = L->perm; *bytes = T * k * 4; break;
     case JT_HIP_BUF_OFF: *dptr = L->off; *bytes = (E + 1) * 4; break;
     case JT_HIP_BUF_XQ: *dptr = L->Xq; *bytes = T * n; break;

@@ -20,101 +20,95 @@
 // Output fragment layout of v_mfma_i32_16x16x64_i8 (4 int32 per lane):
 // element r of lane l is row 4*(l/16)+r, column l%16 of the 16x16 tile.
 
-// ===================== decode GEMV (M <= 16) =====================
-// One block per pair of panels (32 packed channels); the 4 waves split the K
-// blocks round-robin. Lane l owns channel l%16 and k-chunk l/16 of every
-// 64-K block, multiplies its 16 weight bytes with the same 16 activation
-// bytes of each row (v_dot4_i32_i8), then the partial sums are reduced over
-// the 4 k-chunks (lane shuffles) and the 4 waves (LDS) -- integer sums, so
-// the result equals the MFMA kernel's bit for bit.
-template <int EPI, int MR>
-__global__ __launch_bounds__(256) void k_w8a8_gemv(
+// ===================== skinny GEMM (decode, M <= 16) =====================
+// One block of 16 waves per unit of NP panels (NP = 2 for SwiGLU: a gate
+// block and its up block; NP = 1 otherwise). Wave w takes the 64-K blocks
+// w, w+16, w+32, ... and issues all their loads before any math, so the
+// whole weight matrix is in flight across the grid at once (decode shapes
+// are bound by HBM latency and bandwidth). The M <= 16 activation rows are
+// the A operand of one v_mfma_i32_16x16x64_i8 per panel (rows >= M read as
+// zero); the 16 waves' int32 partial tiles are summed through LDS (exact).
+#define SK_WAVES 16
+#define SK_UNROLL 4
+
+template <int EPI, int NP>
+__global__ __launch_bounds__(64 * SK_WAVES) void k_w8a8_skinny(
     const int8_t *__restrict__ A, int lda, const float *__restrict__ sA,
     const int8_t *__restrict__ Wp, const float *__restrict__ sB, int M, int N, int Kp,
     float *__restrict__ C, int ldc, uint32_t *err) {
-    __shared__ int red[4][MR][32];
+    __shared__ v4i red[SK_WAVES][NP][64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int KB = Kp / 64;
-    const int p0 = blockIdx.x * 2;  // first of the two panels
-    const int kc = lane >> 4;
-    int acc[2][MR];
+    const int p0 = blockIdx.x * NP;
+    const int row = lane & 15, kc = lane >> 4;
+    const int8_t *arow = A + (int64_t)min(row, M - 1) * lda + kc * 16;
+    v4i acc[NP];
 #pragma unroll
-    for (int q = 0; q < 2; q++)
+    for (int q = 0; q < NP; q++) acc[q] = (v4i){0, 0, 0, 0};
+    for (int kb0 = wave; kb0 < KB; kb0 += SK_WAVES * SK_UNROLL) {
+        v4i a[SK_UNROLL], b[SK_UNROLL][NP];
 #pragma unroll
-        for (int m = 0; m < MR; m++) acc[q][m] = 0;
-    const int8_t *w0 = Wp + (int64_t)p0 * KB * 1024 + lane * 16;
-    const int8_t *w1 = w0 + (int64_t)KB * 1024;
-    for (int kb = wave; kb < KB; kb += 4) {
-        const v4i b0 = *(const v4i *)(w0 + (int64_t)kb * 1024);
-        const v4i b1 = *(const v4i *)(w1 + (int64_t)kb * 1024);
-        const int koff = kb * 64 + kc * 16;
+        for (int u = 0; u < SK_UNROLL; u++) {
+            const int kb = kb0 + u * SK_WAVES;
+            if (kb < KB) {
 #pragma unroll
-        for (int m = 0; m < MR; m++) {
-            if (m < M) {
-                const v4i a = *(const v4i *)(A + (int64_t)m * lda + koff);
-                int t0 = acc[0][m], t1 = acc[1][m];
-                t0 = __builtin_amdgcn_sdot4(a.x, b0.x, t0, false);
-                t0 = __builtin_amdgcn_sdot4(a.y, b0.y, t0, false);
-                t0 = __builtin_amdgcn_sdot4(a.z, b0.z, t0, false);
-                t0 = __builtin_amdgcn_sdot4(a.w, b0.w, t0, false);
-                t1 = __builtin_amdgcn_sdot4(a.x, b1.x, t1, false);
-                t1 = __builtin_amdgcn_sdot4(a.y, b1.y, t1, false);
-                t1 = __builtin_amdgcn_sdot4(a.z, b1.z, t1, false);
-                t1 = __builtin_amdgcn_sdot4(a.w, b1.w, t1, false);
-                acc[0][m] = t0;
-                acc[1][m] = t1;
+                for (int q = 0; q < NP; q++)
+                    b[u][q] = *(const v4i *)(Wp + ((int64_t)(p0 + q) * KB + kb) * 1024 +
+                                             lane * 16);
+                a[u] = *(const v4i *)(arow + kb * 64);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < SK_UNROLL; u++) {
+            const int kb = kb0 + u * SK_WAVES;
+            if (kb < KB) {
+                const v4i av = row < M ? a[u] : (v4i){0, 0, 0, 0};
+#pragma unroll
+                for (int q = 0; q < NP; q++) acc[q] = mfma16x16x64(av, b[u][q], acc[q]);
             }
         }
     }
 #pragma unroll
-    for (int q = 0; q < 2; q++)
-#pragma unroll
-        for (int m = 0; m < MR; m++) {
-            int v = acc[q][m];
-            v += __shfl_xor(v, 16, 64);
-            v += __shfl_xor(v, 32, 64);
-            if (lane < 16) red[wave][m][q * 16 + lane] = v;
-        }
+    for (int q = 0; q < NP; q++) red[wave][q][lane] = acc[q];
     __syncthreads();
-    // 32 channels x MR rows, one (row, channel) per thread. Scales are read
-    // before any store (loads and stores share one vmcnt on gfx9).
-    constexpr int PT = (MR * 32 + 255) / 256;
-    double sa_t[PT], sg_t[PT], su_t[PT];
+    if (wave != 0) return;
 #pragma unroll
-    for (int q = 0; q < PT; q++) {
-        const int idx = tid + q * 256;
-        const int m = min(idx >> 5, M - 1), c = idx & 31;
-        sa_t[q] = (double)sA[m];
-        const int cg = min(p0 * 16 + c, N - 1), cu = min(p0 * 16 + c + 16, N - 1);
-        sg_t[q] = (double)sB[cg];
-        su_t[q] = (double)sB[cu];
+    for (int q = 0; q < NP; q++) {
+        v4i t = red[0][q][lane];
+#pragma unroll
+        for (int w = 1; w < SK_WAVES; w++) t += red[w][q][lane];
+        acc[q] = t;
     }
+    // element r of lane l: row 4*(l/16) + r, channel l%16 of each panel.
+    // Scales first: loads and stores share one vmcnt on gfx9.
+    const int lr = (lane >> 4) * 4, lc = lane & 15;
+    double sa[4], sb[NP];
+#pragma unroll
+    for (int r = 0; r < 4; r++) sa[r] = (double)sA[min(lr + r, M - 1)];
+#pragma unroll
+    for (int q = 0; q < NP; q++) sb[q] = (double)sB[min((p0 + q) * 16 + lc, N - 1)];
     uint32_t bad = 0, badmid = 0;
 #pragma unroll
-    for (int q = 0; q < PT; q++) {
-        const int idx = tid + q * 256;
-        if (idx >= MR * 32) continue;
-        const int m = idx >> 5, c = idx & 31;
+    for (int r = 0; r < 4; r++) {
+        const int m = lr + r;
         if (m >= M) continue;
-        const int s = red[0][m][c] + red[1][m][c] + red[2][m][c] + red[3][m][c];
         if (EPI == EPI_PLAIN) {
-            const int col = p0 * 16 + c;
-            if (col >= N) continue;
-            const float f = (float)((double)s * (sa_t[q] * sg_t[q]));
-            bad |= !isfinite(f);
-            C[(int64_t)m * ldc + col] = f;
-        } else {
-            if (c >= 16) continue;  // gate lanes combine with their up twin
-            const int cg = p0 * 16 + c, cu = cg + 16;
-            if (cu >= N) continue;
-            const int su = red[0][m][c + 16] + red[1][m][c + 16] + red[2][m][c + 16] +
-                           red[3][m][c + 16];
-            const float g = (float)((double)s * (sa_t[q] * sg_t[q]));
-            const float u = (float)((double)su * (sa_t[q] * su_t[q]));
+#pragma unroll
+            for (int q = 0; q < NP; q++) {
+                const int col = (p0 + q) * 16 + lc;
+                const float f = (float)((double)acc[q][r] * (sa[r] * sb[q]));
+                if (col < N) {
+                    bad |= !isfinite(f);
+                    C[(int64_t)m * ldc + col] = f;
+                }
+            }
+        } else if ((p0 + 1) * 16 + lc < N) {  // panel p0 = gate block, p0+1 its up block
+            const float g = (float)((double)acc[0][r] * (sa[r] * sb[0]));
+            const float u = (float)((double)acc[NP - 1][r] * (sa[r] * sb[NP - 1]));
             bad |= (!isfinite(g)) || (!isfinite(u));
             float sv;
             badmid |= !silu_mul(g, u, &sv);
-            C[(int64_t)m * ldc + (p0 / 2) * 16 + c] = sv;
+            C[(int64_t)m * ldc + blockIdx.x * 16 + lc] = sv;
         }
     }
     if (bad) raise_err(err, EF_RANGE);
@@ -126,20 +120,14 @@ extern "C" int jtk_w8a8_gemm(const int8_t *A, int lda, const float *sA, const in
                              int ldc, int swiglu, uint32_t *err, hipStream_t s) {
     if (M <= 0) return 0;
     if (M <= 16) {
-        dim3 grid((unsigned)(Np / 32));
-#define GEMV(E, R)                                                                     \
-    hipLaunchKernelGGL((k_w8a8_gemv<E, R>), grid, dim3(256), 0, s, A, lda, sA, Wp, sB, M, N, \
-                       Kp, C, ldc, err)
-        if (swiglu) {
-            if (M <= 1) GEMV(EPI_SWIGLU, 1);
-            else if (M <= 4) GEMV(EPI_SWIGLU, 4);
-            else GEMV(EPI_SWIGLU, 16);
-        } else {
-            if (M <= 1) GEMV(EPI_PLAIN, 1);
-            else if (M <= 4) GEMV(EPI_PLAIN, 4);
-            else GEMV(EPI_PLAIN, 16);
-        }
-#undef GEMV
+        if (swiglu)
+            hipLaunchKernelGGL((k_w8a8_skinny<EPI_SWIGLU, 2>), dim3((unsigned)(Np / 32)),
+                               dim3(64 * SK_WAVES), 0, s, A, lda, sA, Wp, sB, M, N, Kp, C, ldc,
+                               err);
+        else
+            hipLaunchKernelGGL((k_w8a8_skinny<EPI_PLAIN, 1>), dim3((unsigned)(Np / 16)),
+                               dim3(64 * SK_WAVES), 0, s, A, lda, sA, Wp, sB, M, N, Kp, C, ldc,
+                               err);
     } else {
         // Tile choice (measured on MI355X): few 128x128 tiles -> 8 waves per
         // block with an intra-block k-split; otherwise 128 x 256 tiles of
@@ -166,7 +154,8 @@ extern "C" int jtk_w8a8_gemm(const int8_t *A, int lda, const float *sA, const in
 
 // ===================== grouped low-bit GEMM =====================
 // Work item = (expert e, 64-row tile of that expert's rows) x 128 packed
-// channels. Rows of expert e are the sorted pairs pos = off[e] .. off[e+1]-1.
+// channels. A tile descriptor is {e, first sorted row, rows} (int4); rows of
+// expert e are the sorted pairs pos = off[e] .. off[e+1]-1.
 //   gate/up (BITS 2, EPI_SWIGLU): A row = Xq[perm[pos] / topk], sA = sx[token],
 //       output S[pos][hidden] (ldo = h);
 //   down    (BITS 4, EPI_SCATTER): A row = Sq[pos], sA = ss[pos],
@@ -203,13 +192,11 @@ __global__ __launch_bounds__(256, 2) void k_lowbit_grouped(
     const int tile = blockIdx.x;
     if (tile >= *ntiles) return;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int packed = tiles[tile];
-    const int e = packed >> 16, row0 = (packed & 0xFFFF) * 64;
-    const int base = off[e], Me = off[e + 1] - base;
-    const int nrows = min(64, Me - row0);
+    const int4 td = ((const int4 *)tiles)[tile];  // {expert, first sorted row, rows}
+    const int e = td.x, pos0 = td.y, nrows = td.z;
     if (tid < 64) {
         const int r = min(tid, nrows - 1);
-        const int pos = base + row0 + r;
+        const int pos = pos0 + r;
         int src;
         if (EPI == EPI_SWIGLU) {
             src = perm[pos] / topk;
@@ -337,6 +324,147 @@ __global__ __launch_bounds__(256, 2) void k_lowbit_grouped(
     if (badmid) raise_err(err, EF_NONFINITE_MID);
 }
 
+// ===================== grouped low-bit GEMM, few rows per expert =====================
+// Decode-sized batches (a handful of rows per expert): work item = (expert
+// e, 16 sorted rows) x 32 packed channels (2 panels), one block of
+// min(G, 16) waves where G = K/64 groups. Wave w takes the groups w, w+16,
+// ...: for each it issues the gathered A rows, the two panels' raw INT2/INT4
+// bytes and their fp16 scales at once, runs one MFMA per panel and parks
+// (float)acc_g and the group scale in LDS. Wave 0 then folds the groups in
+// ascending order, T = fmaf((float)acc_g, scale_g, T) -- the same fp32
+// sequence as the 64-row kernel and the oracle -- and writes the epilogue.
+// Many waves with one group each keep the most loads in flight, which is
+// what decode-sized work is bound by.
+#define LS_WAVES 16
+#define LS_GMAX 64
+
+template <int BITS, int EPI>
+__global__ __launch_bounds__(64 * LS_WAVES) void k_lowbit_skinny(
+    const int8_t *__restrict__ A, int lda, const float *__restrict__ sA,
+    const int32_t *__restrict__ perm, const int4 *__restrict__ tiles,
+    const int32_t *__restrict__ ntiles, int topk, const uint8_t *__restrict__ Wp,
+    const uint16_t *__restrict__ Ws, int64_t wp_stride, int64_t ws_stride, int N, int K,
+    float *__restrict__ out, int ldo, uint32_t *err) {
+    constexpr int PB = BITS == 2 ? 256 : 512;  // bytes per panel-group
+    extern __shared__ __attribute__((aligned(16))) float ls_smem[];
+    const int tile = blockIdx.x;
+    if (tile >= *ntiles) return;
+    const int G = K / 64;
+    float4 *accf = (float4 *)ls_smem;               // [G][2][64]
+    float *scl = ls_smem + (size_t)G * 2 * 64 * 4;  // [G][2][16]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nw = blockDim.x >> 6;
+    const int4 td = tiles[tile];  // {expert, first sorted row, rows}
+    const int e = td.x, pos0 = td.y, nrows = td.z;
+    const int r = lane & 15, kc = lane >> 4;
+    const int pos = pos0 + min(r, nrows - 1);
+    const int src = EPI == EPI_SWIGLU ? perm[pos] / topk : pos;
+    const int8_t *arow = A + (int64_t)src * lda + kc * 16;
+    const int pan0 = blockIdx.y * 2;
+    const uint8_t *wb = Wp + (int64_t)e * wp_stride;
+    const uint16_t *sb = Ws + (int64_t)e * ws_stride;
+    for (int g = wave; g < G; g += nw) {
+        v4i a = *(const v4i *)(arow + (int64_t)g * 64);
+        if (r >= nrows) a = (v4i){0, 0, 0, 0};
+        v4i b[2];
+        uint16_t sc[2];
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const uint8_t *pg = wb + ((int64_t)(pan0 + q) * G + g) * PB;
+            if (BITS == 2) {
+                b[q] = unpack_int2(*(const uint32_t *)(pg + lane * 4));
+            } else {
+                const uint2 w = *(const uint2 *)(pg + lane * 8);
+                b[q] = unpack_int4(w.x, w.y);
+            }
+            sc[q] = sb[((int64_t)(pan0 + q) * G + g) * 16 + (lane & 15)];
+        }
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const v4i c = mfma16x16x64(a, b[q], (v4i){0, 0, 0, 0});
+            accf[(g * 2 + q) * 64 + lane] =
+                make_float4((float)c[0], (float)c[1], (float)c[2], (float)c[3]);
+            if (lane < 16) scl[(g * 2 + q) * 16 + lane] = f16_to_f32(sc[q]);
+        }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    // element q of lane l: row 4*(l/16) + q, channel l%16 of each panel.
+    // Row metadata first (loads and stores share one vmcnt on gfx9).
+    const int lc = lane & 15, lr = (lane >> 4) * 4;
+    float sa[4];
+    int dst[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int p = pos0 + min(lr + i, nrows - 1);
+        const int s2 = EPI == EPI_SWIGLU ? perm[p] / topk : p;
+        sa[i] = sA[s2];
+        dst[i] = EPI == EPI_SWIGLU ? p : perm[p];
+    }
+    float T[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    for (int g = 0; g < G; g++) {
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const float4 v = accf[(g * 2 + q) * 64 + lane];
+            const float s = scl[(g * 2 + q) * 16 + lc];
+            T[q][0] = __builtin_fmaf(v.x, s, T[q][0]);
+            T[q][1] = __builtin_fmaf(v.y, s, T[q][1]);
+            T[q][2] = __builtin_fmaf(v.z, s, T[q][2]);
+            T[q][3] = __builtin_fmaf(v.w, s, T[q][3]);
+        }
+    }
+    uint32_t bad = 0, badmid = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        if (lr + i >= nrows) continue;
+        if (EPI == EPI_SWIGLU) {
+            const float gv = T[0][i] * sa[i];
+            const float uv = T[1][i] * sa[i];
+            bad |= (!isfinite(gv)) || (!isfinite(uv));
+            float sv;
+            badmid |= !silu_mul(gv, uv, &sv);
+            out[(int64_t)dst[i] * ldo + blockIdx.y * 16 + lc] = sv;
+        } else {
+#pragma unroll
+            for (int q = 0; q < 2; q++) {
+                const int col = (pan0 + q) * 16 + lc;
+                if (col >= N) continue;
+                const float f = T[q][i] * sa[i];
+                bad |= !isfinite(f);
+                out[(int64_t)dst[i] * ldo + col] = f;
+            }
+        }
+    }
+    if (bad) raise_err(err, EF_RANGE);
+    if (badmid) raise_err(err, EF_NONFINITE_MID);
+}
+
+template <int BITS, int EPI>
+static hipError_t launch_lowbit_skinny(dim3 grid, int G, hipStream_t s, const int8_t *A,
+                                       int lda, const float *sA, const int32_t *perm,
+                                       const int4 *tiles, const int32_t *ntiles, int topk,
+                                       const uint8_t *Wp, const uint16_t *Ws, int64_t wp_stride,
+                                       int64_t ws_stride, int N, int K, float *out, int ldo,
+                                       uint32_t *err) {
+    const size_t lds = (size_t)G * 2 * 64 * 16 + (size_t)G * 2 * 16 * 4;
+    auto kern = k_lowbit_skinny<BITS, EPI>;
+    static bool attr_set[64];
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    if (!attr_set[dev]) {
+        e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                LS_GMAX * 2 * 64 * 16 + LS_GMAX * 2 * 16 * 4);
+        if (e != hipSuccess) return e;
+        attr_set[dev] = true;
+    }
+    const int nw = G < LS_WAVES ? G : LS_WAVES;
+    hipLaunchKernelGGL(kern, grid, dim3(64 * nw), lds, s, A, lda, sA, perm, tiles, ntiles, topk,
+                       Wp, Ws, wp_stride, ws_stride, N, K, out, ldo, err);
+    return hipGetLastError();
+}
+
 template <int BITS, int EPI, int NST>
 static hipError_t launch_lowbit(dim3 grid, hipStream_t s, const int8_t *A, int lda,
                                 const float *sA, const int32_t *perm, const int32_t *off,
@@ -366,12 +494,28 @@ static hipError_t launch_lowbit(dim3 grid, hipStream_t s, const int8_t *A, int l
 extern "C" int jtk_lowbit_grouped(int bits, const int8_t *A, int lda, const float *sA,
                                   const int32_t *perm, const int32_t *off, int topk,
                                   const int32_t *tiles, const int32_t *ntiles, int max_tiles,
-                                  const uint8_t *Wp, const uint16_t *Ws, int64_t wp_stride,
-                                  int64_t ws_stride, int N, int K, float *out, int ldo,
-                                  uint32_t *err, hipStream_t s) {
+                                  int rows_per_tile, const uint8_t *Wp, const uint16_t *Ws,
+                                  int64_t wp_stride, int64_t ws_stride, int N, int K, float *out,
+                                  int ldo, uint32_t *err, hipStream_t s) {
     if (max_tiles <= 0) return 0;
-    dim3 grid((unsigned)max_tiles, (unsigned)(N / 128));
     hipError_t e;
+    if (rows_per_tile == 16) {
+        const int G = K / 64;
+        if (G > LS_GMAX || N % 32) return (int)hipErrorInvalidValue;
+        dim3 grid((unsigned)max_tiles, (unsigned)(N / 32));
+        const int4 *t4 = (const int4 *)tiles;
+        if (bits == 2)
+            e = launch_lowbit_skinny<2, EPI_SWIGLU>(grid, G, s, A, lda, sA, perm, t4, ntiles, topk,
+                                                    Wp, Ws, wp_stride, ws_stride, N, K, out, ldo,
+                                                    err);
+        else
+            e = launch_lowbit_skinny<4, EPI_SCATTER>(grid, G, s, A, lda, sA, perm, t4, ntiles,
+                                                     topk, Wp, Ws, wp_stride, ws_stride, N, K,
+                                                     out, ldo, err);
+        return (int)e;
+    }
+    if (rows_per_tile != 64) return (int)hipErrorInvalidValue;
+    dim3 grid((unsigned)max_tiles, (unsigned)(N / 128));
     if (bits == 2)
         e = launch_lowbit<2, EPI_SWIGLU, LB_STAGES>(grid, s, A, lda, sA, perm, off, topk, tiles,
                                                     ntiles, Wp, Ws, wp_stride, ws_stride, N, K,

@@ -39,11 +39,12 @@ int jtk_quant_weight_rows(const float *W, int64_t ld_n, int64_t ld_k, int N, int
 int jtk_w8a8_gemm(const int8_t *A, int lda, const float *sA, const int8_t *Wp,
                   const float *sB, int M, int N, int Np, int Kp, float *C, int ldc,
                   int swiglu, uint32_t *err, hipStream_t s);
+/* rows_per_tile 64 (batches) or 16 (few rows per expert) */
 int jtk_lowbit_grouped(int bits, const int8_t *A, int lda, const float *sA,
                        const int32_t *perm, const int32_t *off, int topk,
                        const int32_t *tiles, const int32_t *ntiles, int max_tiles,
-                       const uint8_t *Wp, const uint16_t *Ws, int64_t wp_stride,
-                       int64_t ws_stride, int N, int K, float *out, int ldo,
+                       int rows_per_tile, const uint8_t *Wp, const uint16_t *Ws,
+                       int64_t wp_stride, int64_t ws_stride, int N, int K, float *out, int ldo,
                        uint32_t *err, hipStream_t s);
 
 /* route.hip */
@@ -54,8 +55,13 @@ int jtk_topk(const float *logits, int rows, int E, int k, int32_t *ids, int64_t 
 int jtk_sort(const int32_t *ids, int Tk, int E, int64_t cap, int32_t *rank, int32_t *cnt,
              int32_t *tot, int32_t *off, int64_t *off64, int32_t *perm, int64_t *perm64,
              uint8_t *drop, uint32_t *err, hipStream_t s);
-int jtk_make_tiles(const int32_t *off, int E, int32_t *tiles, int32_t *ntiles,
+/* tiles: int4 {expert, first sorted row, rows, 0} per R-row tile */
+int jtk_make_tiles(const int32_t *off, int E, int R, int32_t *tiles, int32_t *ntiles,
                    hipStream_t s);
+/* one-launch sort + R-row tile list for Tk <= 1024 pairs and E <= 4096 */
+int jtk_sort_small(const int32_t *ids, int Tk, int E, int64_t cap, int R, int32_t *off,
+                   int64_t *off64, int32_t *perm, int64_t *perm64, uint8_t *drop,
+                   int32_t *tiles, int32_t *ntiles, uint32_t *err, hipStream_t s);
 int jtk_combine(const float *w, const float *Ye, const uint8_t *drop, const float *Ys,
                 int S, int T, int k, int n, float *Y, uint32_t *err, hipStream_t s);
 int jtk_renorm(float *w, const uint8_t *drop, int T, int k, uint32_t *err, hipStream_t s);

@@ -7,7 +7,12 @@
 #include "jt_dev.h"
 #include "jt_launch.h"
 
-// One wavefront per row; blockDim = 256 (4 rows per block).
+// One wavefront per row; blockDim = 256 (4 rows per block). Rows of up to
+// 64*4*QR_REG floats (4096) are read once into registers with all loads in
+// flight, reduced, and quantised from the registers; longer or unaligned
+// rows take the two-pass loop.
+#define QR_REG 16
+
 __global__ __launch_bounds__(256) void k_quant_rows(
     const float *__restrict__ X, int64_t rows, int cols, int8_t *__restrict__ Q,
     int64_t ldq, float *__restrict__ scale, const int32_t *__restrict__ row_count,
@@ -18,11 +23,49 @@ __global__ __launch_bounds__(256) void k_quant_rows(
     if (r >= nrows) return;
     const float *x = X + r * cols;
     int8_t *q = Q + r * ldq;
-    // float4 loads / 4-byte code stores when the row allows it
     const bool vec = (cols & 3) == 0 && (((uintptr_t)x | (uintptr_t)q) & 3) == 0 &&
                      ((uintptr_t)x & 15) == 0;
     float m = 0.0f;
     int bad = 0;
+    if (vec && cols <= 64 * 4 * QR_REG) {
+        const float4 *x4 = (const float4 *)x;
+        const int n4 = cols >> 2;
+        float4 v[QR_REG];
+#pragma unroll
+        for (int i = 0; i < QR_REG; i++) {
+            const int c = lane + 64 * i;
+            v[i] = c < n4 ? x4[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int i = 0; i < QR_REG; i++) {
+            bad |= (!isfinite(v[i].x)) || (!isfinite(v[i].y)) || (!isfinite(v[i].z)) ||
+                   (!isfinite(v[i].w));
+            m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)),
+                               fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+        }
+        m = wave_max_f(m);
+        bad = wave_or_i(bad);
+        QuantParams p = quant_params(m);
+        if (bad || !p.ok) {
+            if (lane == 0) raise_err(err, bad ? EF_NONFINITE_INPUT : EF_RANGE);
+            return;
+        }
+        if (lane == 0) scale[r] = p.scale_f;
+        const double inv = p.scale_d != 0.0 ? 1.0 / p.scale_d : 0.0;
+        uint32_t *q4 = (uint32_t *)q;
+#pragma unroll
+        for (int i = 0; i < QR_REG; i++) {
+            const int c = lane + 64 * i;
+            if (c < n4) {
+                const uint32_t b0 = (uint8_t)quant_code_fast(v[i].x, p.scale_d, inv);
+                const uint32_t b1 = (uint8_t)quant_code_fast(v[i].y, p.scale_d, inv);
+                const uint32_t b2 = (uint8_t)quant_code_fast(v[i].z, p.scale_d, inv);
+                const uint32_t b3 = (uint8_t)quant_code_fast(v[i].w, p.scale_d, inv);
+                q4[c] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+            }
+        }
+        return;
+    }
     if (vec) {
         const float4 *x4 = (const float4 *)x;
         for (int c = lane; c < (cols >> 2); c += 64) {

@@ -347,17 +347,23 @@ extern "C" int jtk_sort(const int32_t *ids, int Tk, int E, int64_t cap, int32_t 
 }
 
 // ---------------- grouped-GEMM work list ----------------
-// tiles[i] = (e << 16) | j for the j-th 64-row tile of expert e, experts in
-// ascending order; *ntiles = total.
+// tiles[i] = {e, off[e] + j*R, rows, 0} (int4) for the j-th R-row tile of
+// expert e, experts in ascending order; *ntiles = total.
+__device__ __forceinline__ void put_tiles(int4 *tiles, int start, int e, int base, int cnt,
+                                          int R) {
+    for (int j = 0; j * R < cnt; j++)
+        tiles[start + j] = make_int4(e, base + j * R, min(R, cnt - j * R), 0);
+}
+
 __global__ __launch_bounds__(1024) void k_make_tiles(const int32_t *__restrict__ off, int E,
-                                                     int32_t *__restrict__ tiles,
+                                                     int R, int4 *__restrict__ tiles,
                                                      int32_t *__restrict__ ntiles) {
     __shared__ int buf[1024];
     const int t = threadIdx.x;
     int carry = 0;
     for (int e0 = 0; e0 < E; e0 += 1024) {
         const int e = e0 + t;
-        const int nt = e < E ? (off[e + 1] - off[e] + 63) / 64 : 0;
+        const int nt = e < E ? (off[e + 1] - off[e] + R - 1) / R : 0;
         buf[t] = nt;
         __syncthreads();
         for (int o = 1; o < 1024; o <<= 1) {
@@ -367,16 +373,133 @@ __global__ __launch_bounds__(1024) void k_make_tiles(const int32_t *__restrict__
             __syncthreads();
         }
         const int start = carry + buf[t] - nt;
-        for (int j = 0; j < nt; j++) tiles[start + j] = (e << 16) | j;
+        if (e < E) put_tiles(tiles, start, e, off[e], off[e + 1] - off[e], R);
         carry += buf[1023];
         __syncthreads();
     }
     if (t == 0) *ntiles = carry;
 }
 
-extern "C" int jtk_make_tiles(const int32_t *off, int E, int32_t *tiles, int32_t *ntiles,
+extern "C" int jtk_make_tiles(const int32_t *off, int E, int R, int32_t *tiles,
+                              int32_t *ntiles, hipStream_t s) {
+    hipLaunchKernelGGL(k_make_tiles, dim3(1), dim3(1024), 0, s, off, E, R, (int4 *)tiles,
+                       ntiles);
+    return (int)hipGetLastError();
+}
+
+// ---------------- small-batch sort + work list in one block ----------------
+// The same stable counting sort (rank of pair q = number of earlier pairs
+// with its expert; kept iff rank < cap) and the same R-row tile list, for
+// Tk <= SORT_SMALL pairs: one workgroup, everything in LDS, one launch
+// instead of five. Each of the 1024 threads owns one pair and 4 experts.
+#define SORT_SMALL 1024
+#define SORT_EMAX 4096
+
+// Exclusive scan of one int per thread over a 1024-thread block: wave scans
+// with lane shuffles, then one pass over the 16 wave totals (2 barriers).
+__device__ __forceinline__ int block_excl_scan_1024(int v, int *wsum, int *total) {
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    int x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
+    }
+    if (lane == 63) wsum[wave] = x;
+    __syncthreads();
+    int before = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < 16; w++) {
+        const int c = wsum[w];
+        before += w < wave ? c : 0;
+        all += c;
+    }
+    *total = all;
+    __syncthreads();  // wsum is reused by the next scan
+    return before + x - v;
+}
+
+__global__ __launch_bounds__(1024) void k_sort_small(
+    const int32_t *__restrict__ ids, int Tk, int E, int64_t cap, int R,
+    int32_t *__restrict__ off, int64_t *__restrict__ off64, int32_t *__restrict__ perm,
+    int64_t *__restrict__ perm64, uint8_t *__restrict__ drop, int32_t *__restrict__ tiles,
+    int32_t *__restrict__ ntiles, uint32_t *err) {
+    __shared__ __attribute__((aligned(16))) int sid[SORT_SMALL];
+    __shared__ int cnt[SORT_EMAX];
+    __shared__ int eoff[SORT_EMAX + 1];
+    __shared__ int buf[16];
+    const int t = threadIdx.x;
+    int e = -1;
+    if (t < Tk) {
+        e = ids[t];
+        if (e < 0 || e >= E) {
+            raise_err(err, EF_BAD_ID);
+            e = -1;
+        }
+    }
+    sid[t] = e;
+    for (int i = t; i < E; i += 1024) cnt[i] = 0;
+    __syncthreads();
+    if (e >= 0) atomicAdd(&cnt[e], 1);
+    int r = 0;  // stable rank: earlier pairs with the same expert
+    if (e >= 0) {
+        const int4 *s4 = (const int4 *)sid;
+        int i = 0;
+        for (; i + 4 <= t; i += 4) {
+            const int4 v = s4[i >> 2];
+            r += (v.x == e) + (v.y == e) + (v.z == e) + (v.w == e);
+        }
+        for (; i < t; i++) r += (sid[i] == e);
+    }
+    __syncthreads();
+    // per-thread experts 4t..4t+3: kept counts and tile counts
+    int kc[4], nt[4], ks = 0, ts = 0;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int x = 4 * t + u;
+        kc[u] = x < E ? (int)min((int64_t)cnt[x], cap) : 0;
+        nt[u] = (kc[u] + R - 1) / R;
+        ks += kc[u];
+        ts += nt[u];
+    }
+    int ktot, ttot;
+    int kbase = block_excl_scan_1024(ks, buf, &ktot);
+    int tbase = block_excl_scan_1024(ts, buf, &ttot);
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int x = 4 * t + u;
+        if (x < E) {
+            eoff[x] = kbase;
+            off[x] = kbase;
+            if (off64) off64[x] = kbase;
+            put_tiles((int4 *)tiles, tbase, x, kbase, kc[u], R);
+        }
+        kbase += kc[u];
+        tbase += nt[u];
+    }
+    if (t == 0) {
+        off[E] = ktot;
+        if (off64) off64[E] = ktot;
+        *ntiles = ttot;
+    }
+    __syncthreads();
+    if (e >= 0) {
+        const bool kept = r < cap;
+        if (drop) drop[t] = kept ? 0 : 1;
+        if (kept) {
+            perm[eoff[e] + r] = t;
+            if (perm64) perm64[eoff[e] + r] = t;
+        }
+    }
+}
+
+extern "C" int jtk_sort_small(const int32_t *ids, int Tk, int E, int64_t cap, int R,
+                              int32_t *off, int64_t *off64, int32_t *perm, int64_t *perm64,
+                              uint8_t *drop, int32_t *tiles, int32_t *ntiles, uint32_t *err,
                               hipStream_t s) {
-    hipLaunchKernelGGL(k_make_tiles, dim3(1), dim3(1024), 0, s, off, E, tiles, ntiles);
+    if (Tk > SORT_SMALL || E > SORT_EMAX) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_sort_small, dim3(1), dim3(1024), 0, s, ids, Tk, E, cap, R, off, off64,
+                       perm, perm64, drop, tiles, ntiles, err);
     return (int)hipGetLastError();
 }
 
