@@ -71,19 +71,27 @@ __device__ __forceinline__ int quant_code(float x, double scale_d) {
     qd = qd > 127.0 ? 127.0 : (qd < -127.0 ? -127.0 : qd);
     return (int)qd;
 }
-// Same code as quant_code without a per-element divide: y = x * RN(1/scale_d)
-// differs from the exact quotient x/scale_d by at most 2^-52 relative, i.e.
-// < 3e-14 for |x/scale_d| <= 128. round() of the two can differ only if a
-// half-integer lies between them, so whenever frac|y| is within 1e-9 of 0.5
-// the exact quotient is recomputed; otherwise round(y) is the exact answer.
-__device__ __forceinline__ int quant_code_fast(float x, double scale_d, double inv_d) {
+// Same code as quant_code without fp64 per element: y = x * inv_f with
+// inv_f = (float)(1/scale_d) differs from the exact quotient x/scale_d by
+// less than 2^-22 relative (two fp32 roundings and the fp64 reciprocal),
+// i.e. < 3.1e-5 absolute for |x/scale_d| <= 128. round-half-away of the two
+// can differ only if a half-integer lies between them, so whenever frac|y|
+// is within 1e-4 of 0.5 the exact fp64 quotient is recomputed; otherwise
+// floor(|y| + 0.5) is the exact answer (|y| + 0.5 is not within an ulp of an
+// integer there, so its fp32 rounding cannot cross one).
+__device__ __forceinline__ int quant_code_fast(float x, double scale_d, float inv_f) {
     if (scale_d == 0.0) return 0;
-    double y = (double)x * inv_d;
-    const double a = fabs(y);
-    if (fabs((a - floor(a)) - 0.5) < 1e-9) y = (double)x / scale_d;
-    double qd = round(y);
-    qd = qd > 127.0 ? 127.0 : (qd < -127.0 ? -127.0 : qd);
-    return (int)qd;
+    if (!(inv_f < __builtin_inff())) return quant_code(x, scale_d);  // 1/scale_d > FLT_MAX
+    const float y = x * inv_f;
+    const float a = fabsf(y);
+    if (fabsf((a - floorf(a)) - 0.5f) < 1e-4f) return quant_code(x, scale_d);
+    int q = (int)floorf(a + 0.5f);
+    q = q > 127 ? 127 : q;
+    return y < 0.0f ? -q : q;
+}
+// inv_f for quant_code_fast: (float)(1/scale_d), 0 for an all-zero row
+__device__ __forceinline__ float quant_inv_f(double scale_d) {
+    return scale_d != 0.0 ? (float)(1.0 / scale_d) : 0.0f;
 }
 
 // ---- IEEE binary16 <-> binary64, round to nearest even ----

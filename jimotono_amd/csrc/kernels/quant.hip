@@ -38,10 +38,12 @@ __global__ __launch_bounds__(256) void k_quant_rows(
         }
 #pragma unroll
         for (int i = 0; i < QR_REG; i++) {
-            bad |= (!isfinite(v[i].x)) || (!isfinite(v[i].y)) || (!isfinite(v[i].z)) ||
-                   (!isfinite(v[i].w));
-            m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)),
-                               fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+            if (64 * i < n4) {  // wave-uniform; constant indices keep v[] in registers
+                bad |= (!isfinite(v[i].x)) || (!isfinite(v[i].y)) || (!isfinite(v[i].z)) ||
+                       (!isfinite(v[i].w));
+                m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)),
+                                   fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+            }
         }
         m = wave_max_f(m);
         bad = wave_or_i(bad);
@@ -51,12 +53,12 @@ __global__ __launch_bounds__(256) void k_quant_rows(
             return;
         }
         if (lane == 0) scale[r] = p.scale_f;
-        const double inv = p.scale_d != 0.0 ? 1.0 / p.scale_d : 0.0;
+        const float inv = quant_inv_f(p.scale_d);
         uint32_t *q4 = (uint32_t *)q;
 #pragma unroll
         for (int i = 0; i < QR_REG; i++) {
             const int c = lane + 64 * i;
-            if (c < n4) {
+            if (64 * i < n4 && c < n4) {
                 const uint32_t b0 = (uint8_t)quant_code_fast(v[i].x, p.scale_d, inv);
                 const uint32_t b1 = (uint8_t)quant_code_fast(v[i].y, p.scale_d, inv);
                 const uint32_t b2 = (uint8_t)quant_code_fast(v[i].z, p.scale_d, inv);
@@ -88,7 +90,7 @@ __global__ __launch_bounds__(256) void k_quant_rows(
         return;
     }
     if (lane == 0) scale[r] = p.scale_f;
-    const double inv = p.scale_d != 0.0 ? 1.0 / p.scale_d : 0.0;
+    const float inv = quant_inv_f(p.scale_d);
     if (vec) {
         const float4 *x4 = (const float4 *)x;
         uint32_t *q4 = (uint32_t *)q;

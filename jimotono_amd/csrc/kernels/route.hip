@@ -32,13 +32,12 @@ __global__ __launch_bounds__(256) void k_router_logits(const float *__restrict__
                                                        int E, int n,
                                                        float *__restrict__ logits,
                                                        uint32_t *err) {
-    // [stage][x|w][k][row]: 32 KiB, reused as the 64 x 64 fp64 partial buffer
-    __shared__ __attribute__((aligned(16))) float lds[2][2][RT_KC][64];
-    auto xs = [&](int b, int k) -> float * { return &lds[b][0][k][0]; };
-    auto ws = [&](int b, int k) -> float * { return &lds[b][1][k][0]; };
+    // [stage][x|w][k][row] fp64 (widened once when staged): 64 KiB, reused
+    // as the 64 x 64 fp64 partial buffer
+    __shared__ __attribute__((aligned(16))) double lds[2][2][RT_KC][64];
     const int tid = threadIdx.x;
     const int t0 = blockIdx.x * RT_T, e0 = blockIdx.y * RT_E;
-    const int p = tid >> 6;                  // lane partial of this thread
+    const int p = tid >> 6;                       // lane partial of this thread
     const int ty = (tid >> 3) & 7, tx = tid & 7;  // tokens ty*8.., experts tx*8..
     double acc[8][8];
 #pragma unroll
@@ -46,24 +45,36 @@ __global__ __launch_bounds__(256) void k_router_logits(const float *__restrict__
 #pragma unroll
         for (int b = 0; b < 8; b++) acc[a][b] = 0.0;
     const int n4 = n & ~3;
-    // stage loader: thread -> (row r = tid/4, 8 consecutive k at 8*(tid%4))
-    const int lr = tid >> 2, lk = (tid & 3) * 8;
+    // stage loader: thread -> row tid%64, k = 8*(tid/64) .. +7 of the chunk;
+    // LDS stores of consecutive threads are consecutive (no bank conflicts)
+    const int lr = tid & 63, lk = (tid >> 6) * 8;
     const float *xrow = X + (int64_t)min(t0 + lr, T - 1) * n;
     const float *wrow = Wg + (int64_t)min(e0 + lr, E - 1) * n;
+    const bool vec = (n & 3) == 0;
     float xv[8], wv[8];
     auto gload = [&](int k0) {
+        const int kb = k0 + lk;
+        if (vec && kb + 8 <= n4) {
+            const float4 a0 = *(const float4 *)(xrow + kb), a1 = *(const float4 *)(xrow + kb + 4);
+            const float4 b0 = *(const float4 *)(wrow + kb), b1 = *(const float4 *)(wrow + kb + 4);
+            xv[0] = a0.x; xv[1] = a0.y; xv[2] = a0.z; xv[3] = a0.w;
+            xv[4] = a1.x; xv[5] = a1.y; xv[6] = a1.z; xv[7] = a1.w;
+            wv[0] = b0.x; wv[1] = b0.y; wv[2] = b0.z; wv[3] = b0.w;
+            wv[4] = b1.x; wv[5] = b1.y; wv[6] = b1.z; wv[7] = b1.w;
+        } else {
 #pragma unroll
-        for (int c = 0; c < 8; c++) {
-            const int k = k0 + lk + c;
-            xv[c] = k < n4 ? xrow[k] : 0.0f;
-            wv[c] = k < n4 ? wrow[k] : 0.0f;
+            for (int c = 0; c < 8; c++) {
+                const int k = kb + c;
+                xv[c] = k < n4 ? xrow[k] : 0.0f;
+                wv[c] = k < n4 ? wrow[k] : 0.0f;
+            }
         }
     };
     auto sstore = [&](int buf) {
 #pragma unroll
         for (int c = 0; c < 8; c++) {
-            xs(buf, lk + c)[lr] = xv[c];
-            ws(buf, lk + c)[lr] = wv[c];
+            lds[buf][0][lk + c][lr] = (double)xv[c];
+            lds[buf][1][lk + c][lr] = (double)wv[c];
         }
     };
     gload(0);
@@ -75,12 +86,16 @@ __global__ __launch_bounds__(256) void k_router_logits(const float *__restrict__
         if (more) gload(k0 + RT_KC);
         const int kend = min(RT_KC, n4 - k0);
         for (int i = p; i < kend; i += 4) {
-            const float4 x0 = *(const float4 *)(xs(buf, i) + ty * 8);
-            const float4 x1 = *(const float4 *)(xs(buf, i) + ty * 8 + 4);
-            const float4 w0 = *(const float4 *)(ws(buf, i) + tx * 8);
-            const float4 w1 = *(const float4 *)(ws(buf, i) + tx * 8 + 4);
-            const double xa[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-            const double wa[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+            double xa[8], wa[8];
+#pragma unroll
+            for (int c = 0; c < 8; c += 2) {
+                const double2 xx = *(const double2 *)&lds[buf][0][i][ty * 8 + c];
+                const double2 ww = *(const double2 *)&lds[buf][1][i][tx * 8 + c];
+                xa[c] = xx.x;
+                xa[c + 1] = xx.y;
+                wa[c] = ww.x;
+                wa[c + 1] = ww.y;
+            }
 #pragma unroll
             for (int a = 0; a < 8; a++)
 #pragma unroll
@@ -90,9 +105,9 @@ __global__ __launch_bounds__(256) void k_router_logits(const float *__restrict__
         __syncthreads();
         buf ^= 1;
     }
-    // combine partials through LDS (reusing the staging arrays, 32 KiB of
-    // fp64 per partial): l1 -> l0+l1, l3 -> l2+l3, then (l0+l1)+(l2+l3)
-    double *red = (double *)&lds[0][0][0][0];
+    // combine partials through LDS (reusing the staging arrays):
+    // l1 -> l0+l1, l3 -> l2+l3, then (l0+l1)+(l2+l3)
+    double *red = &lds[0][0][0][0];
     auto put = [&]() {
 #pragma unroll
         for (int a = 0; a < 8; a++)
