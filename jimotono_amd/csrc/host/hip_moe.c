@@ -220,6 +220,14 @@ struct jt_hip_moe {
     int32_t *ids, *rank, *cnt, *tot, *off, *perm, *tiles, *ntiles;
     const int32_t *cur_ids; /* ids / weights of the last forward (caller's */
     const float *cur_w;     /* arrays after jt_hip_moe_fwd_routed) */
+    /* router on the int8 matrix cores with exact verification (E <= 256,
+     * d % 64 == 0):
+     * residual codes of X and of Wgate, row {scale, l1}, approximate logits */
+    int fast_router;
+    int8_t *Xl, *rWh, *rWl;
+    double *xinfo, *winfo, *approx;
+    int16_t *rcand; /* [T][E] candidate experts of each token */
+    int32_t *rnc;   /* [T] candidate counts */
     int8_t *Sqr;
     int last_T;
     /* shared experts run on side streams forked after the input quantiser
@@ -241,7 +249,7 @@ void jt_hip_moe_free(jt_hip_moe *L) {
     void *p[] = {L->Wgate, L->gu_P, L->gu_S, L->dn_P,  L->dn_S, L->Xq,   L->sx,
                  L->logits, L->w,  L->Sr,   L->ssr,  L->Ye,   L->Ys,   L->ids,
                  L->rank,  L->cnt, L->tot,  L->off,  L->perm, L->tiles, L->ntiles,
-                 L->Sqr};
+                 L->Sqr,   L->Xl,  L->rWh,  L->rWl,  L->xinfo, L->winfo, L->approx, L->rcand, L->rnc};
     (void)hipDeviceSynchronize();
     for (size_t i = 0; i < sizeof(p) / sizeof(p[0]); i++) (void)hipFree(p[i]);
     for (int s = 0; s < JT_MOE_MAX_SHARED; s++) jt_hip_ffn_free(L->sh[s]);
@@ -308,6 +316,21 @@ int jt_hip_moe_prepare(const jt_hip_moe_desc *desc, const float *dWgate, const f
     ALLOC(L->ssr, (size_t)Tk * 4);
     ALLOC(L->Ye, (size_t)Tk * n * 4);
     ALLOC(L->Ys, (size_t)(d.n_shared > 0 ? d.n_shared : 1) * T * n * 4);
+    const int Ep = (E + 63) / 64 * 64;
+    int8_t *wh_rm = NULL, *wl_rm = NULL;
+    L->fast_router = dWgate != NULL && E <= 256 && n % 64 == 0;
+    if (L->fast_router) {
+        ALLOC(L->Xl, (size_t)T * n);
+        ALLOC(L->xinfo, (size_t)T * 16);
+        ALLOC(L->approx, (size_t)T * E * 8);
+        ALLOC(L->rcand, (size_t)T * E * 2);
+        ALLOC(L->rnc, (size_t)T * 4);
+        ALLOC(L->rWh, (size_t)Ep * n);
+        ALLOC(L->rWl, (size_t)Ep * n);
+        ALLOC(L->winfo, (size_t)E * 16);
+        ALLOC(wh_rm, (size_t)E * n);
+        ALLOC(wl_rm, (size_t)E * n);
+    }
 #undef ALLOC
     if (e == hipSuccess && dWgate)
         e = hipMemcpyAsync(L->Wgate, dWgate, (size_t)E * n * sizeof(float),
@@ -316,6 +339,12 @@ int jt_hip_moe_prepare(const jt_hip_moe_desc *desc, const float *dWgate, const f
     if (rc == JT_OK) {
         jtk_check_finite(dWgate ? L->Wgate : NULL, dWgate ? (int64_t)E * n : 0, rt->d_err,
                          rt->stream);
+        if (L->fast_router) {
+            jtk_router_codes(L->Wgate, E, n, wh_rm, wl_rm, NULL, L->winfo, rt->d_err,
+                             rt->stream);
+            jtk_pack_i8(wh_rm, E, n, 0, Ep, n, L->rWh, rt->stream);
+            jtk_pack_i8(wl_rm, E, n, 0, Ep, n, L->rWl, rt->stream);
+        }
         /* routed gate/up: rows of Wg/Wu [E][h][n] are channels, K = n */
         jtk_pack_lowbit(dWg, dWu, (int64_t)h * n, n, 1, E, 2 * h, n, 2, L->gu_P, L->gu_S,
                         NULL, NULL, rt->d_err, rt->stream);
@@ -326,6 +355,8 @@ int jt_hip_moe_prepare(const jt_hip_moe_desc *desc, const float *dWgate, const f
         rc = jt_rt_flags(rt, rt->stream, &f);
         if (rc == JT_OK) rc = jt_rt_flags_to_rc(f);
     }
+    (void)hipFree(wh_rm); /* jt_rt_flags synchronised the stream */
+    (void)hipFree(wl_rm);
     const int hs = d.h_shared;
     for (int s = 0; s < d.n_shared && rc == JT_OK; s++) {
         const int64_t so = (int64_t)s * hs * n;
@@ -418,8 +449,12 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
     int le = 0;
     L->last_T = T;
 
+    const int fast = !d_ids && L->fast_router;
     prof_mark(L, slot, ST_QUANT_X, s);
-    le |= jtk_quant_rows(dX, T, n, L->Xq, n, L->sx, NULL, err, s);
+    if (fast) /* the expert codes Xq plus the router's residual codes */
+        le |= jtk_router_codes(dX, T, n, L->Xq, L->Xl, L->sx, L->xinfo, err, s);
+    else
+        le |= jtk_quant_rows(dX, T, n, L->Xq, n, L->sx, NULL, err, s);
     /* Without profiling the shared experts overlap the routed path on side
      * streams; with profiling every stage runs in order on s so that each
      * stage's events bracket its kernels alone. */
@@ -439,6 +474,12 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
         ids = d_ids; /* caller-routed: read in place */
         w = d_w;
         prof_mark(L, slot, ST_TOPK, s);
+    } else if (fast) {
+        le |= jtk_router_approx(L->Xq, L->Xl, n, L->xinfo, L->rWh, L->rWl, L->winfo, T, E,
+                                L->approx, s);
+        prof_mark(L, slot, ST_TOPK, s);
+        le |= jtk_topk_verify(L->approx, L->xinfo, L->winfo, dX, L->Wgate, T, E, n, k, L->rcand,
+                              L->rnc, L->ids, L->w, L->logits, err, s);
     } else {
         le |= jtk_router_logits(dX, L->Wgate, T, E, n, L->logits, err, s);
         prof_mark(L, slot, ST_TOPK, s);

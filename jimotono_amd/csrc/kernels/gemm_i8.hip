@@ -332,7 +332,7 @@ __global__ __launch_bounds__(256, 2) void k_lowbit_grouped(
 // bytes and their fp16 scales at once, runs one MFMA per panel and parks
 // (float)acc_g and the group scale in LDS. Wave 0 then folds the groups in
 // ascending order, T = fmaf((float)acc_g, scale_g, T) -- the same fp32
-// sequence as the 64-row kernel and the oracle -- and writes the epilogue.
+// sequence as the 64-row kernel -- and writes the epilogue.
 // Many waves with one group each keep the most loads in flight, which is
 // what decode-sized work is bound by.
 #define LS_WAVES 16

@@ -47,6 +47,17 @@ int jtk_lowbit_grouped(int bits, const int8_t *A, int lda, const float *sA,
                        int64_t wp_stride, int64_t ws_stride, int N, int K, float *out, int ldo,
                        uint32_t *err, hipStream_t s);
 
+/* router.hip: int8 MFMA candidates + exact fp64 verification of the gate */
+int jtk_router_codes(const float *X, int rows, int n, int8_t *qh, int8_t *ql, float *sf,
+                     double *info, uint32_t *err, hipStream_t s);
+int jtk_router_approx(const int8_t *Xh, const int8_t *Xl, int n, const double *xinfo,
+                      const int8_t *Wh, const int8_t *Wl, const double *winfo, int T, int E,
+                      double *approx, hipStream_t s);
+int jtk_topk_verify(const double *approx, const double *xinfo, const double *winfo,
+                    const float *X, const float *Wg, int T, int E, int n, int k, int16_t *cand,
+                    int32_t *ncand, int32_t *ids, float *w, float *logits, uint32_t *err,
+                    hipStream_t s);
+
 /* route.hip */
 int jtk_router_logits(const float *X, const float *Wg, int T, int E, int n, float *logits,
                       uint32_t *err, hipStream_t s);

@@ -1,0 +1,450 @@
+// Fast router for gfx950: int8 MFMA candidates, exact fp64 verification.
+//
+// The reference's gate logit is l = (float)dot(x, w) summed in fp64 in its
+// AVX2 lane order (src/moe_layer.c:67-86) and top-k selects by (value desc,
+// index asc) (src/routing.c:39-74). Computing all T x E logits that way is
+// fp64 vector work. This path computes an approximation with a proven
+// error bound on the int8 matrix cores and evaluates the reference's exact
+// sum only for the experts the bound cannot rule out:
+//
+//  1. k_router_codes: each row r (tokens, and the expert rows of Wgate at
+//     prepare) is written as x = s*(qh + ql/254) + eps with the row
+//     quantiser's scale s = max|x|/127, qh = round(x/s) (the very codes the
+//     experts consume), ql = round((x - s*qh)*254/s), |eps| <= s/508; also
+//     l1 = sum|x|.
+//  2. k_router_approx: a = s_x s_w (HH + (HL + LH)/254 + LL/254^2) from four
+//     exact int32 MFMA sums. |dot - a| <= m with
+//     m = (s_w/508) l1_x + (s_x/508) l1_w + 3n (s_x/508)(s_w/508)
+//     (plus slack for the fp64 evaluation of a and of the reference sum).
+//  3. k_router_select (one wave per token): L = a - m, U = a + m; thr <=
+//     the k-th largest L; candidates are the experts with U >= thr - delta,
+//     delta = 2^-22 |thr| (so a non-candidate's float logit is strictly
+//     below k candidates' float logits).
+//  4. k_router_exact (one lane per token and candidate): the reference's
+//     exact lane-order fp64 sum for each candidate; top-k and softmax then
+//     run on those exact float logits exactly as the reference does. Every
+//     expert outside the candidate set is provably outside the reference's
+//     top-k.
+// logits[t][e] holds the exact float logit for candidates and the float of
+// the approximation for the others.
+#include "gemm_w8a8.h"
+#include "jt_launch.h"
+
+// ---- 1. codes of a row ----
+// One wavefront per row; blockDim = 256 (4 rows). qh/sf follow the row
+// quantiser (k_quant_rows) bit for bit; info = {s (fp64), l1}.
+__global__ __launch_bounds__(256) void k_router_codes(const float *__restrict__ X, int rows,
+                                                      int n, int8_t *__restrict__ qh,
+                                                      int8_t *__restrict__ ql,
+                                                      float *__restrict__ sf,
+                                                      double2 *__restrict__ info,
+                                                      uint32_t *err) {
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const float *x = X + (int64_t)r * n;
+    float m = 0.0f;
+    double l1 = 0.0;
+    int bad = 0;
+    for (int c = lane; c < n; c += 64) {
+        const float v = x[c];
+        bad |= !isfinite(v);
+        m = fmaxf(m, fabsf(v));
+        l1 += fabs((double)v);
+    }
+    m = wave_max_f(m);
+    bad = wave_or_i(bad);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) l1 += __shfl_xor(l1, o, 64);
+    const QuantParams p = quant_params(m);
+    if (bad || !p.ok) {
+        if (lane == 0) raise_err(err, bad ? EF_NONFINITE_INPUT : EF_RANGE);
+        return;
+    }
+    if (lane == 0) {
+        if (sf) sf[r] = p.scale_f;
+        info[r] = make_double2(p.scale_d, l1);
+    }
+    const float inv = quant_inv_f(p.scale_d);
+    const double lo = p.scale_d / 254.0;
+    for (int c = lane; c < n; c += 64) {
+        const float v = x[c];
+        const int q = quant_code_fast(v, p.scale_d, inv);
+        qh[(int64_t)r * n + c] = (int8_t)q;
+        int q2 = 0;
+        if (p.scale_d != 0.0) {
+            const double res = (double)v - p.scale_d * (double)q;
+            double t = round(res / lo);
+            t = t > 127.0 ? 127.0 : (t < -127.0 ? -127.0 : t);
+            q2 = (int)t;
+        }
+        ql[(int64_t)r * n + c] = (int8_t)q2;
+    }
+}
+
+extern "C" int jtk_router_codes(const float *X, int rows, int n, int8_t *qh, int8_t *ql,
+                                float *sf, double *info, uint32_t *err, hipStream_t s) {
+    if (rows <= 0) return 0;
+    hipLaunchKernelGGL(k_router_codes, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, X,
+                       rows, n, qh, ql, sf, (double2 *)info, err);
+    return (int)hipGetLastError();
+}
+
+// ---- 2. approximate logits ----
+// Block = 64 tokens x 64 experts, 4 waves of 16 tokens; per 64-K block a
+// wave issues its 2 A fragments and 8 panels (hi/lo of 4 expert panels),
+// then 16 MFMAs into the four int32 sums of each 16x16 tile.
+__global__ __launch_bounds__(256) void k_router_approx(
+    const int8_t *__restrict__ Xh, const int8_t *__restrict__ Xl, int n,
+    const double2 *__restrict__ xinfo, const int8_t *__restrict__ Wh,
+    const int8_t *__restrict__ Wl, const double2 *__restrict__ winfo, int T, int E,
+    double *__restrict__ approx) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int t0 = blockIdx.x * 64 + wave * 16, e0 = blockIdx.y * 64;
+    const int KB = n / 64;
+    const int r = lane & 15, kc = lane >> 4;
+    const int64_t arow = (int64_t)min(t0 + r, T - 1) * n + kc * 16;
+    const int pb = e0 / 16;
+    v4i hh[4], hl[4], lh[4], ll[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) hh[j] = hl[j] = lh[j] = ll[j] = (v4i){0, 0, 0, 0};
+    for (int kb = 0; kb < KB; kb++) {
+        const v4i ah = *(const v4i *)(Xh + arow + kb * 64);
+        const v4i al = *(const v4i *)(Xl + arow + kb * 64);
+        v4i bh[4], bl[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int64_t po = ((int64_t)(pb + j) * KB + kb) * 1024 + lane * 16;
+            bh[j] = *(const v4i *)(Wh + po);
+            bl[j] = *(const v4i *)(Wl + po);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            hh[j] = mfma16x16x64(ah, bh[j], hh[j]);
+            hl[j] = mfma16x16x64(ah, bl[j], hl[j]);
+            lh[j] = mfma16x16x64(al, bh[j], lh[j]);
+            ll[j] = mfma16x16x64(al, bl[j], ll[j]);
+        }
+    }
+    const int lr = (lane >> 4) * 4, lc = lane & 15;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int e = e0 + j * 16 + lc;
+        if (e >= E) continue;
+        const double sw = winfo[e].x;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int t = t0 + lr + q;
+            if (t >= T) continue;
+            const double v = (double)hh[j][q] + ((double)hl[j][q] + (double)lh[j][q]) / 254.0 +
+                             (double)ll[j][q] / 64516.0;
+            approx[(int64_t)t * E + e] = xinfo[t].x * sw * v;
+        }
+    }
+}
+
+extern "C" int jtk_router_approx(const int8_t *Xh, const int8_t *Xl, int n, const double *xinfo,
+                                 const int8_t *Wh, const int8_t *Wl, const double *winfo, int T,
+                                 int E, double *approx, hipStream_t s) {
+    if (T <= 0) return 0;
+    dim3 grid((unsigned)((T + 63) / 64), (unsigned)((E + 63) / 64));
+    hipLaunchKernelGGL(k_router_approx, grid, dim3(256), 0, s, Xh, Xl, n,
+                       (const double2 *)xinfo, Wh, Wl, (const double2 *)winfo, T, E, approx);
+    return (int)hipGetLastError();
+}
+
+// ---- 3. candidates ----
+#define RV_EMAX 512    // experts per token: RV_EMAX / 64 per lane
+#define RV_WPB 4       // waves (tokens) per block
+#define RV_KEYBITS 24  // leading key bits resolved by the threshold select
+
+// order-preserving map of a float to an unsigned 32-bit key
+__device__ __forceinline__ uint32_t okey(float f) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, f);
+    return (b >> 31) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float unkey(uint32_t k) {
+    return __builtin_bit_cast(float, (k >> 31) ? (k & 0x7fffffffu) : ~k);
+}
+// largest float <= d
+__device__ __forceinline__ float float_rd(double d) {
+    float f = (float)d;
+    if ((double)f > d) f = nextafterf(f, -__builtin_inff());
+    return f;
+}
+
+// One wavefront per token: bounds L = a - m, U = a + m, thr <= the k-th
+// largest L, candidates = {U >= thr - delta} in ascending expert order into
+// cand[t][0..nc), nc into ncand[t]; the others' logits get the float of a.
+//
+// thr: each lane keeps the largest of its RV_EMAX / 64 lower bounds (as
+// floats rounded down); the k-th largest of those 64 lane maxima is a
+// subset's k-th largest, hence <= the k-th largest L. It is found as the
+// largest RV_KEYBITS-bit key prefix with at least k lane maxima at or above
+// it, one wave ballot per bit (k <= min(E, 64) lanes hold a bound).
+__global__ __launch_bounds__(64 * RV_WPB) void k_router_select(
+    const double *__restrict__ approx, const double2 *__restrict__ xinfo,
+    const double2 *__restrict__ winfo, int T, int E, int n, int k,
+    int16_t *__restrict__ cand, int32_t *__restrict__ ncand, float *__restrict__ logits) {
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * RV_WPB + (threadIdx.x >> 6);
+    if (t >= T) return;
+    constexpr int EPL = RV_EMAX / 64;
+    const double sx = xinfo[t].x, l1x = xinfo[t].y;
+    const double ux = sx * (1.0 / 508.0);
+    double ap[EPL], hi[EPL];
+    uint32_t kmax = 0;  // below every real key
+#pragma unroll
+    for (int j = 0; j < EPL; j++) {
+        const int e = lane + 64 * j;
+        ap[j] = 0.0;
+        hi[j] = -__builtin_inf();
+        if (e < E) {
+            const double a = approx[(int64_t)t * E + e];
+            const double sw = winfo[e].x, l1w = winfo[e].y;
+            const double uw = sw * (1.0 / 508.0);
+            double m = uw * l1x + ux * l1w + 3.0 * n * ux * uw;
+            m = m * (1.0 + 1e-9) + 1e-9 * sx * sw * n * 16641.0 + 1e-12 * l1x * 128.0 * sw;
+            ap[j] = a;
+            hi[j] = a + m;
+            kmax = max(kmax, okey(float_rd(a - m)));
+        }
+    }
+    uint32_t kappa = 0;
+    for (int bit = 31; bit >= 32 - RV_KEYBITS; bit--) {
+        const uint32_t trial = kappa | (1u << bit);
+        if (__popcll(__ballot(kmax >= trial)) >= k) kappa = trial;
+    }
+    const double thr = (double)unkey(kappa);
+    // a prefix of the key of -inf decodes to a NaN: every expert is then a
+    // candidate
+    const double cut = thr == thr ? thr - (fabs(thr) * 0x1p-22 + 1e-300) : -__builtin_inf();
+    int nc = 0;
+#pragma unroll
+    for (int j = 0; j < EPL; j++) {
+        const int e = lane + 64 * j;
+        const bool c = e < E && hi[j] >= cut;
+        const uint64_t mask = __ballot(c);
+        if (c) cand[(int64_t)t * E + nc + __popcll(mask & ((1ull << lane) - 1ull))] = (int16_t)e;
+        else if (e < E) logits[(int64_t)t * E + e] = (float)ap[j];
+        nc += __popcll(mask);
+    }
+    if (lane == 0) ncand[t] = nc;
+}
+
+// ---- 4. exact logits of the candidates, top-k, softmax ----
+#define RX_G 16       // lanes per token (4 tokens per wavefront)
+#define RX_WPB 4      // wavefronts per block
+#define RX_EMAX 256   // experts (the candidate values of a token sit in LDS)
+#define RX_CH 32      // row elements per stage (8 float4 steps)
+#define RX_SL 9       // 16-byte LDS slots per staged gate row: 8 + 1 pad
+#define RX_NBUF 3     // stages per wavefront (two in flight while one is summed)
+#define RX_WDMA RX_SL // gate-row DMA instructions per stage: 64 rows x 9 slots / 64
+#define RX_STAGE_B (64 * RX_SL * 16 + 1024)  // 64 gate rows + the 4 token rows
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+// One stage of a wavefront: for each lane's gate row (64 rows, padded to 9
+// slots so that lanes reading their own rows hit distinct banks) and the
+// wave's 4 token rows, elements [h0, h0 + RX_CH). Every lane issues every
+// DMA, so each stage is exactly RX_WDMA + 1 vector-memory instructions.
+__device__ __forceinline__ void rx_issue(const float *Wg, const int *woff, const float *xsrc,
+                                         int h0, char *stage) {
+#pragma unroll
+    for (int m = 0; m < RX_WDMA; m++) dma<16>(Wg + woff[m] + h0, stage + m * 1024);
+    dma<16>(xsrc + h0, stage + 64 * RX_SL * 16);
+}
+
+// A lane owns a (token, candidate) pair and runs the reference's four lane
+// partials (element j into partial j % 4, src/moe_layer.c:67-86) as four
+// independent fp64 chains over float4 steps; the final sum is
+// (p0 + p1) + (p2 + p3). The gate rows of the wave's 64 lanes and its 4
+// token rows stream through a 3-stage LDS ring filled by LDS-DMA (coalesced
+// 1 KiB requests; rows read straight from global memory by 64 lanes at once
+// would touch 64 cache lines per load). Then top-k by (value desc, index
+// asc) over the candidates and softmax exactly as k_topk
+// (src/routing.c:39-74).
+__global__ __launch_bounds__(64 * RX_WPB) void k_router_exact(
+    const int16_t *__restrict__ cand, const int32_t *__restrict__ ncand,
+    const float *__restrict__ X, const float *__restrict__ Wg, int T, int E, int n, int k,
+    int32_t *__restrict__ ids, float *__restrict__ w, float *__restrict__ logits,
+    uint32_t *err) {
+    constexpr int TPB = RX_WPB * 64 / RX_G;  // tokens per block
+    constexpr int TPW = 64 / RX_G;           // tokens per wavefront
+    extern __shared__ __attribute__((aligned(16))) char rx_smem[];
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int tl = threadIdx.x / RX_G, slot = threadIdx.x % RX_G;
+    char *ring = rx_smem + (size_t)wid * RX_NBUF * RX_STAGE_B;
+    float *cval = (float *)(rx_smem + (size_t)RX_WPB * RX_NBUF * RX_STAGE_B);  // [TPB][RX_EMAX]
+    double *exl = (double *)(cval + TPB * RX_EMAX);                              // [TPB][64]
+    short *sel = (short *)(exl + TPB * 64);                                      // [TPB][64]
+    const int t = blockIdx.x * TPB + tl;
+    const bool valid = t < T;
+    const int nc = valid ? ncand[t] : 0;
+    int ncw = nc;  // the largest count among the wave's tokens
+    ncw = max(ncw, __shfl_xor(ncw, 16, 64));
+    ncw = max(ncw, __shfl_xor(ncw, 32, 64));
+    const int16_t *ct = cand + (int64_t)t * E;
+    // token rows: lane l < 32 fetches 16 B of token l / 8 (slot l % 8); the
+    // upper half repeats it into the unused half of the token area
+    const int xt = min(blockIdx.x * TPB + wid * TPW + ((lane & 31) >> 3), T - 1);
+    const float *xsrc = X + (int64_t)xt * n + (lane & 7) * 4;
+    float *cv = cval + tl * RX_EMAX;
+    const int nch = n / RX_CH;
+    int bad = 0;
+    for (int c0 = 0; c0 < ncw; c0 += RX_G) {
+        const int c = c0 + slot;
+        const bool act = c < nc;
+        const int e = act ? ct[c] : 0;
+        // DMA m, lane l fills slot q = 64 m + l: row q / 9 (the gate row of
+        // lane q / 9), step q % 9 (step 8 is the pad: a repeat of step 7)
+        int woff[RX_WDMA];
+#pragma unroll
+        for (int m = 0; m < RX_WDMA; m++) {
+            const int q = 64 * m + lane, r = q / RX_SL, j = q % RX_SL;
+            woff[m] = __shfl(e, r, 64) * n + 4 * min(j, RX_SL - 2);
+        }
+        double p0 = 0.0, p1 = 0.0, p2 = 0.0, p3 = 0.0;
+        // the stage waits count this pass's DMAs only: retire the previous
+        // pass's logit stores first
+        wait_vm<0>();
+        rx_issue(Wg, woff, xsrc, 0, ring);
+        if (nch > 1) rx_issue(Wg, woff, xsrc, RX_CH, ring + RX_STAGE_B);
+        for (int ch = 0; ch < nch; ch++) {
+            if (ch + 2 < nch) {
+                rx_issue(Wg, woff, xsrc, (ch + 2) * RX_CH, ring + ((ch + 2) % RX_NBUF) * RX_STAGE_B);
+                wait_vm<2 * (RX_WDMA + 1)>();
+            } else if (ch + 1 < nch) {
+                wait_vm<RX_WDMA + 1>();
+            } else {
+                wait_vm<0>();
+            }
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            const char *st = ring + (ch % RX_NBUF) * RX_STAGE_B;
+            if (act) {
+                // LDS reads in asm: the compiler cannot tell these addresses
+                // from the stages still in flight and would otherwise drain
+                // every DMA (vmcnt(0)) before them
+                const uint32_t wa = lds_addr(st) + lane * RX_SL * 16;
+                const uint32_t xa = lds_addr(st) + 64 * RX_SL * 16 + (tl % TPW) * 128;
+                f4 wv[RX_CH / 4], xv[RX_CH / 4];
+                static_assert(RX_CH / 4 == 8, "eight steps per stage");
+                // one statement, so that no use of a value is scheduled
+                // before the wait
+                asm volatile(
+                    "ds_read_b128 %0, %16 offset:0\n\tds_read_b128 %1, %17 offset:0\n\t"
+                    "ds_read_b128 %2, %16 offset:16\n\tds_read_b128 %3, %17 offset:16\n\t"
+                    "ds_read_b128 %4, %16 offset:32\n\tds_read_b128 %5, %17 offset:32\n\t"
+                    "ds_read_b128 %6, %16 offset:48\n\tds_read_b128 %7, %17 offset:48\n\t"
+                    "ds_read_b128 %8, %16 offset:64\n\tds_read_b128 %9, %17 offset:64\n\t"
+                    "ds_read_b128 %10, %16 offset:80\n\tds_read_b128 %11, %17 offset:80\n\t"
+                    "ds_read_b128 %12, %16 offset:96\n\tds_read_b128 %13, %17 offset:96\n\t"
+                    "ds_read_b128 %14, %16 offset:112\n\tds_read_b128 %15, %17 offset:112\n\t"
+                    "s_waitcnt lgkmcnt(0)"
+                    : "=&v"(wv[0]), "=&v"(xv[0]), "=&v"(wv[1]), "=&v"(xv[1]), "=&v"(wv[2]),
+                      "=&v"(xv[2]), "=&v"(wv[3]), "=&v"(xv[3]), "=&v"(wv[4]), "=&v"(xv[4]),
+                      "=&v"(wv[5]), "=&v"(xv[5]), "=&v"(wv[6]), "=&v"(xv[6]), "=&v"(wv[7]),
+                      "=&v"(xv[7])
+                    : "v"(wa), "v"(xa)
+                    : "memory");
+#pragma unroll
+                for (int u = 0; u < RX_CH / 4; u++) {
+                    p0 = fma((double)xv[u].x, (double)wv[u].x, p0);
+                    p1 = fma((double)xv[u].y, (double)wv[u].y, p1);
+                    p2 = fma((double)xv[u].z, (double)wv[u].z, p2);
+                    p3 = fma((double)xv[u].w, (double)wv[u].w, p3);
+                }
+            }
+            // the stage is refilled two iterations on
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+        }
+        if (act) {
+            const double tot = (p0 + p1) + (p2 + p3);
+            const float f = (float)tot;
+            bad |= (!isfinite(tot)) || (!isfinite(f));
+            cv[c] = f;
+            logits[(int64_t)t * E + e] = f;
+        }
+    }
+    // a non-finite logit is the reference's error (src/routing.c:39-54)
+    if (__ballot(bad != 0)) {
+        if (lane == 0) raise_err(err, EF_NONFINITE_MID);
+        return;
+    }
+    // cval written by some lanes is read by others below
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    // rank of each candidate = candidates before it in (value desc, index
+    // asc) order; the list is in ascending expert order
+    short *sl = sel + tl * 64;
+    double *xl2 = exl + tl * 64;
+    for (int c = slot; c < nc; c += RX_G) {
+        const float f = cv[c];
+        int rank = 0;
+        for (int j = 0; j < nc; j++) {
+            const float g = cv[j];
+            rank += (g > f) || (g == f && j < c);
+        }
+        if (rank < k) sl[rank] = (short)c;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    // the rank-0 value is the maximum
+    const bool ok = valid && nc >= k;
+    const float mx = ok ? cv[sl[0]] : 0.0f;
+    for (int r = slot; r < k; r += RX_G)
+        if (ok) xl2[r] = exp((double)cv[sl[r]] - (double)mx);
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    if (!valid) return;
+    double sum = 0.0;
+    for (int r = 0; r < k; r++) sum += xl2[r];
+    if (!ok || !((sum > 0.0) && isfinite(sum))) {
+        if (slot == 0) raise_err(err, EF_NONFINITE_MID);
+        return;
+    }
+    const float inv = (float)(1.0 / sum);
+    for (int r = slot; r < k; r += RX_G) {
+        const float wv = (float)xl2[r] * inv;
+        ids[(int64_t)t * k + r] = ct[sl[r]];
+        w[(int64_t)t * k + r] = wv;
+        if (!(wv >= 0.0f) || !isfinite(wv)) raise_err(err, EF_NONFINITE_MID);
+    }
+}
+
+extern "C" int jtk_topk_verify(const double *approx, const double *xinfo, const double *winfo,
+                               const float *X, const float *Wg, int T, int E, int n, int k,
+                               int16_t *cand, int32_t *ncand, int32_t *ids, float *w,
+                               float *logits, uint32_t *err, hipStream_t s) {
+    if (T <= 0) return 0;
+    if (E > RX_EMAX || k < 1 || k > 64 || k > E || n % RX_CH != 0 ||
+        (int64_t)E * n > 0x7fffffff)
+        return (int)hipErrorInvalidValue;
+    constexpr int TPB = RX_WPB * 64 / RX_G;
+    constexpr size_t lds =
+        (size_t)RX_WPB * RX_NBUF * RX_STAGE_B + (size_t)TPB * (RX_EMAX * 4 + 64 * 8 + 64 * 2);
+    static_assert(lds <= 160 * 1024, "LDS budget");
+    static bool attr_set[64];
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= 64) return (int)hipErrorInvalidDevice;
+    if (!attr_set[dev]) {
+        e = hipFuncSetAttribute((const void *)k_router_exact,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return (int)e;
+        attr_set[dev] = true;
+    }
+    hipLaunchKernelGGL(k_router_select, dim3((unsigned)((T + RV_WPB - 1) / RV_WPB)),
+                       dim3(64 * RV_WPB), 0, s, approx, (const double2 *)xinfo,
+                       (const double2 *)winfo, T, E, n, k, cand, ncand, logits);
+    hipLaunchKernelGGL(k_router_exact, dim3((unsigned)((T + TPB - 1) / TPB)),
+                       dim3(64 * RX_WPB), lds, s, (const int16_t *)cand, (const int32_t *)ncand,
+                       X, Wg, T, E, n, k, ids, w, logits, err);
+    return (int)hipGetLastError();
+}
