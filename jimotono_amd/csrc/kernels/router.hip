@@ -32,7 +32,19 @@
 
 // ---- 1. codes of a row ----
 // One wavefront per row; blockDim = 256 (4 rows). qh/sf follow the row
-// quantiser (k_quant_rows) bit for bit; info = {s (fp64), l1}.
+// quantiser (k_quant_rows) bit for bit; info = {s (fp64), l1}. The residual
+// code rounds (x - s qh) * (254 / s) to nearest: |x - s (qh + ql/254)| <=
+// s/508 up to the fp64 rounding of the product, which the bound's slack
+// covers. Rows of up to 64 * 4 * RC_REG elements (n % 4 == 0) are read once
+// into registers with all loads in flight.
+#define RC_REG 16
+
+__device__ __forceinline__ uint32_t router_lo_code(float v, int q, double sd, double inv_lo) {
+    double t = rint(((double)v - sd * (double)q) * inv_lo);
+    t = t > 127.0 ? 127.0 : (t < -127.0 ? -127.0 : t);
+    return (uint32_t)(uint8_t)(int8_t)(int)t;
+}
+
 __global__ __launch_bounds__(256) void k_router_codes(const float *__restrict__ X, int rows,
                                                       int n, int8_t *__restrict__ qh,
                                                       int8_t *__restrict__ ql,
@@ -46,6 +58,63 @@ __global__ __launch_bounds__(256) void k_router_codes(const float *__restrict__ 
     float m = 0.0f;
     double l1 = 0.0;
     int bad = 0;
+    const bool vec = (n & 3) == 0 && ((uintptr_t)x & 15) == 0 &&
+                     (((uintptr_t)qh | (uintptr_t)ql) & 3) == 0;
+    if (vec && n <= 64 * 4 * RC_REG) {
+        const float4 *x4 = (const float4 *)x;
+        const int n4 = n >> 2;
+        float4 v[RC_REG];
+#pragma unroll
+        for (int i = 0; i < RC_REG; i++) {
+            const int c = lane + 64 * i;
+            v[i] = c < n4 ? x4[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int i = 0; i < RC_REG; i++) {
+            if (64 * i < n4) {  // wave-uniform; constant indices keep v[] in registers
+                bad |= (!isfinite(v[i].x)) || (!isfinite(v[i].y)) || (!isfinite(v[i].z)) ||
+                       (!isfinite(v[i].w));
+                m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)),
+                                   fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+                l1 += (fabs((double)v[i].x) + fabs((double)v[i].y)) +
+                      (fabs((double)v[i].z) + fabs((double)v[i].w));
+            }
+        }
+        m = wave_max_f(m);
+        bad = wave_or_i(bad);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) l1 += __shfl_xor(l1, o, 64);
+        const QuantParams p = quant_params(m);
+        if (bad || !p.ok) {
+            if (lane == 0) raise_err(err, bad ? EF_NONFINITE_INPUT : EF_RANGE);
+            return;
+        }
+        if (lane == 0) {
+            if (sf) sf[r] = p.scale_f;
+            info[r] = make_double2(p.scale_d, l1);
+        }
+        const float inv = quant_inv_f(p.scale_d);
+        const double inv_lo = p.scale_d != 0.0 ? 254.0 / p.scale_d : 0.0;
+        uint32_t *qh4 = (uint32_t *)(qh + (int64_t)r * n);
+        uint32_t *ql4 = (uint32_t *)(ql + (int64_t)r * n);
+#pragma unroll
+        for (int i = 0; i < RC_REG; i++) {
+            const int c = lane + 64 * i;
+            if (64 * i < n4 && c < n4) {
+                const int q0 = quant_code_fast(v[i].x, p.scale_d, inv);
+                const int q1 = quant_code_fast(v[i].y, p.scale_d, inv);
+                const int q2 = quant_code_fast(v[i].z, p.scale_d, inv);
+                const int q3 = quant_code_fast(v[i].w, p.scale_d, inv);
+                qh4[c] = (uint32_t)(uint8_t)q0 | ((uint32_t)(uint8_t)q1 << 8) |
+                         ((uint32_t)(uint8_t)q2 << 16) | ((uint32_t)(uint8_t)q3 << 24);
+                ql4[c] = router_lo_code(v[i].x, q0, p.scale_d, inv_lo) |
+                         (router_lo_code(v[i].y, q1, p.scale_d, inv_lo) << 8) |
+                         (router_lo_code(v[i].z, q2, p.scale_d, inv_lo) << 16) |
+                         (router_lo_code(v[i].w, q3, p.scale_d, inv_lo) << 24);
+            }
+        }
+        return;
+    }
     for (int c = lane; c < n; c += 64) {
         const float v = x[c];
         bad |= !isfinite(v);
@@ -66,19 +135,12 @@ __global__ __launch_bounds__(256) void k_router_codes(const float *__restrict__ 
         info[r] = make_double2(p.scale_d, l1);
     }
     const float inv = quant_inv_f(p.scale_d);
-    const double lo = p.scale_d / 254.0;
+    const double inv_lo = p.scale_d != 0.0 ? 254.0 / p.scale_d : 0.0;
     for (int c = lane; c < n; c += 64) {
         const float v = x[c];
         const int q = quant_code_fast(v, p.scale_d, inv);
         qh[(int64_t)r * n + c] = (int8_t)q;
-        int q2 = 0;
-        if (p.scale_d != 0.0) {
-            const double res = (double)v - p.scale_d * (double)q;
-            double t = round(res / lo);
-            t = t > 127.0 ? 127.0 : (t < -127.0 ? -127.0 : t);
-            q2 = (int)t;
-        }
-        ql[(int64_t)r * n + c] = (int8_t)q2;
+        ql[(int64_t)r * n + c] = (int8_t)router_lo_code(v, q, p.scale_d, inv_lo);
     }
 }
 

@@ -500,6 +500,27 @@ int or_topk(const float *logits, size_t n, size_t k, int64_t *ids,
     return RC_OK;
 }
 
+/* Router over T tokens: logits[t][e] = (float)or_logit_lane4(x_t, w_e)
+ * (src/moe_layer.c:67-86), then or_topk of each token's row
+ * (src/routing.c:16-76); a non-finite logit is an error, as in the
+ * reference's layer (src/moe_layer.c:391-399). */
+int or_router(const float *X, const float *Wgate, int T, int E, int n, int k,
+              int64_t *ids, float *w, float *logits) {
+    if (!X || !Wgate || !ids || !w || !logits || T <= 0 || E <= 0 || n <= 0 ||
+        k <= 0 || k > E)
+        return RC_INVAL;
+    for (int t = 0; t < T; t++) {
+        float *lg = logits + (size_t)t * E;
+        for (int e = 0; e < E; e++) {
+            lg[e] = (float)or_logit_lane4(X + (size_t)t * n, Wgate + (size_t)e * n, n);
+            if (!isfinite(lg[e])) return RC_INVAL;
+        }
+        int rc = or_topk(lg, (size_t)E, (size_t)k, ids + (size_t)t * k, w + (size_t)t * k);
+        if (rc != RC_OK) return rc;
+    }
+    return RC_OK;
+}
+
 int or_batch_sort(const int64_t *ids, int T, int k, int E, float cap_factor,
                   int64_t *perm, int64_t *off, unsigned char *drop,
                   int64_t *out_kept) {

@@ -112,6 +112,8 @@ double or_logit_lane4(const float *x, const float *w, int n);
 /* src/routing.c:16-76. ids as int64 (size_t in the reference). */
 int or_topk(const float *logits, size_t n, size_t k, int64_t *ids,
             float *weights);
+int or_router(const float *X, const float *Wgate, int T, int E, int n, int k,
+              int64_t *ids, float *w, float *logits);
 /* src/moe_layer.c:895-978 with cap_factor in [1,1.5]; cap_factor <= 0
  * selects the dropless variant (cap = T*k). */
 int or_batch_sort(const int64_t *ids, int T, int k, int E, float cap_factor,

@@ -84,6 +84,8 @@ class Oracle:
         L.or_logit_lane4.argtypes = [_f32p, _f32p, C.c_int]
         L.or_logit_lane4.restype = C.c_double
         L.or_topk.argtypes = [_f32p, C.c_size_t, C.c_size_t, _i64p, _f32p]
+        L.or_router.argtypes = [_f32p, _f32p, C.c_int, C.c_int, C.c_int, C.c_int, _i64p,
+                                _f32p, _f32p]
         L.or_batch_sort.argtypes = [_i64p, C.c_int, C.c_int, C.c_int, C.c_float, _i64p,
                                     _i64p, _u8p, C.c_void_p]
         L.or_silu_mul.argtypes = [C.c_float, C.c_float, C.POINTER(C.c_float)]
@@ -220,6 +222,17 @@ class Oracle:
         w = np.zeros(k, np.float32)
         rc = self.lib.or_topk(logits, logits.size, k, ids, w)
         return rc, ids, w
+
+    def router(self, X, Wgate, k):
+        X = _c(X, np.float32)
+        Wgate = _c(Wgate, np.float32)
+        T, n = X.shape
+        E = Wgate.shape[0]
+        ids = np.zeros((T, k), np.int64)
+        w = np.zeros((T, k), np.float32)
+        logits = np.zeros((T, E), np.float32)
+        rc = self.lib.or_router(X, Wgate, T, E, n, k, ids, w, logits)
+        return rc, ids, w, logits
 
     def batch_sort(self, ids, T, k, E, cap_factor):
         ids = _c(ids, np.int64).ravel()

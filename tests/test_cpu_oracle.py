@@ -330,6 +330,34 @@ def test_topk_brute_force(orc):
         assert np.allclose(w, (e / e.sum()), rtol=2e-7, atol=1e-7)
 
 
+def test_router_composition(orc, gold):
+    """or_router = or_logit_lane4 per (token, expert) then or_topk per token,
+    on the golden logit vectors (whose logits are pinned above) and on a
+    tie-heavy case; a non-finite logit is an error."""
+    X, W = gold["logits_X"], gold["logits_Wgate"]
+    k = min(4, W.shape[0])
+    rc, ids, w, lg = orc.router(X, W, k)
+    assert rc == 0 and np.array_equal(bits(lg), bits(gold["logits_out"]))
+    for t in range(X.shape[0]):
+        rc2, ids2, w2 = orc.topk(gold["logits_out"][t], k)
+        assert rc2 == 0 and np.array_equal(ids[t], ids2) and np.array_equal(bits(w[t]), bits(w2))
+    rng = np.random.default_rng(14)
+    Wt = np.round(rng.standard_normal((24, 8)) * 2).astype(np.float32)
+    Wt[7] = Wt[3]
+    Xt = np.round(rng.standard_normal((30, 8)) * 2).astype(np.float32)
+    Xt[0] = 0.0
+    rc, ids, w, lg = orc.router(Xt, Wt, 5)
+    assert rc == 0
+    for t in range(30):
+        ref = (Xt[t].astype(np.float64) * Wt.astype(np.float64)).sum(axis=1)  # exact: small integers
+        order = sorted(range(24), key=lambda e: (-ref[e], e))[:5]
+        assert list(ids[t]) == order
+    assert list(ids[0]) == [0, 1, 2, 3, 4]
+    Xbad = Xt.copy()
+    Xbad[3, 2] = np.inf
+    assert orc.router(Xbad, Wt, 5)[0] != 0
+
+
 def test_sort_invariants(orc):
     rng = np.random.default_rng(13)
     T, k, E = 300, 6, 40
