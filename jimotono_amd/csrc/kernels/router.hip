@@ -313,11 +313,13 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p) {
 // slots so that lanes reading their own rows hit distinct banks) and the
 // wave's 4 token rows, elements [h0, h0 + RX_CH). Every lane issues every
 // DMA, so each stage is exactly RX_WDMA + 1 vector-memory instructions.
-__device__ __forceinline__ void rx_issue(const float *Wg, const int *woff, const float *xsrc,
-                                         int h0, char *stage) {
+// The bases are wave-uniform and the per-lane byte offsets 32-bit, so the
+// DMAs take the scalar-base addressing form with no per-stage vector math.
+__device__ __forceinline__ void rx_issue(const char *wbase, const uint32_t *woff,
+                                         const char *xbase, uint32_t xoff, char *stage) {
 #pragma unroll
-    for (int m = 0; m < RX_WDMA; m++) dma<16>(Wg + woff[m] + h0, stage + m * 1024);
-    dma<16>(xsrc + h0, stage + 64 * RX_SL * 16);
+    for (int m = 0; m < RX_WDMA; m++) dma<16>(wbase + woff[m], stage + m * 1024);
+    dma<16>(xbase + xoff, stage + 64 * RX_SL * 16);
 }
 
 // A lane owns a (token, candidate) pair and runs the reference's four lane
@@ -337,7 +339,8 @@ __global__ __launch_bounds__(64 * RX_WPB) void k_router_exact(
     constexpr int TPB = RX_WPB * 64 / RX_G;  // tokens per block
     constexpr int TPW = 64 / RX_G;           // tokens per wavefront
     extern __shared__ __attribute__((aligned(16))) char rx_smem[];
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int tl = threadIdx.x / RX_G, slot = threadIdx.x % RX_G;
     char *ring = rx_smem + (size_t)wid * RX_NBUF * RX_STAGE_B;
     float *cval = (float *)(rx_smem + (size_t)RX_WPB * RX_NBUF * RX_STAGE_B);  // [TPB][RX_EMAX]
@@ -352,8 +355,9 @@ __global__ __launch_bounds__(64 * RX_WPB) void k_router_exact(
     const int16_t *ct = cand + (int64_t)t * E;
     // token rows: lane l < 32 fetches 16 B of token l / 8 (slot l % 8); the
     // upper half repeats it into the unused half of the token area
-    const int xt = min(blockIdx.x * TPB + wid * TPW + ((lane & 31) >> 3), T - 1);
-    const float *xsrc = X + (int64_t)xt * n + (lane & 7) * 4;
+    const int t0 = blockIdx.x * TPB + wid * TPW;  // the wave's first token
+    const int xt = min(t0 + ((lane & 31) >> 3), T - 1);
+    const uint32_t xoff = (uint32_t)(((xt - t0) * n + (lane & 7) * 4) * 4);
     float *cv = cval + tl * RX_EMAX;
     const int nch = n / RX_CH;
     int bad = 0;
@@ -363,68 +367,107 @@ __global__ __launch_bounds__(64 * RX_WPB) void k_router_exact(
         const int e = act ? ct[c] : 0;
         // DMA m, lane l fills slot q = 64 m + l: row q / 9 (the gate row of
         // lane q / 9), step q % 9 (step 8 is the pad: a repeat of step 7)
-        int woff[RX_WDMA];
+        uint32_t woff[RX_WDMA];  // bytes from the stage's column of Wg
 #pragma unroll
         for (int m = 0; m < RX_WDMA; m++) {
             const int q = 64 * m + lane, r = q / RX_SL, j = q % RX_SL;
-            woff[m] = __shfl(e, r, 64) * n + 4 * min(j, RX_SL - 2);
+            woff[m] = (uint32_t)((__shfl(e, r, 64) * n + 4 * min(j, RX_SL - 2)) * 4);
         }
+        // stage s covers columns [s RX_CH, (s + 1) RX_CH)
+        auto issue = [&](int sidx, char *st) {
+            rx_issue((const char *)(Wg + sidx * RX_CH), woff,
+                     (const char *)(X + (int64_t)t0 * n + sidx * RX_CH), xoff, st);
+        };
         double p0 = 0.0, p1 = 0.0, p2 = 0.0, p3 = 0.0;
-        // the stage waits count this pass's DMAs only: retire the previous
-        // pass's logit stores first
-        wait_vm<0>();
-        rx_issue(Wg, woff, xsrc, 0, ring);
-        if (nch > 1) rx_issue(Wg, woff, xsrc, RX_CH, ring + RX_STAGE_B);
-        for (int ch = 0; ch < nch; ch++) {
-            if (ch + 2 < nch) {
-                rx_issue(Wg, woff, xsrc, (ch + 2) * RX_CH, ring + ((ch + 2) % RX_NBUF) * RX_STAGE_B);
-                wait_vm<2 * (RX_WDMA + 1)>();
-            } else if (ch + 1 < nch) {
-                wait_vm<RX_WDMA + 1>();
-            } else {
-                wait_vm<0>();
-            }
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            const char *st = ring + (ch % RX_NBUF) * RX_STAGE_B;
-            if (act) {
-                // LDS reads in asm: the compiler cannot tell these addresses
-                // from the stages still in flight and would otherwise drain
-                // every DMA (vmcnt(0)) before them
-                const uint32_t wa = lds_addr(st) + lane * RX_SL * 16;
-                const uint32_t xa = lds_addr(st) + 64 * RX_SL * 16 + (tl % TPW) * 128;
-                f4 wv[RX_CH / 4], xv[RX_CH / 4];
-                static_assert(RX_CH / 4 == 8, "eight steps per stage");
-                // one statement, so that no use of a value is scheduled
-                // before the wait
-                asm volatile(
-                    "ds_read_b128 %0, %16 offset:0\n\tds_read_b128 %1, %17 offset:0\n\t"
-                    "ds_read_b128 %2, %16 offset:16\n\tds_read_b128 %3, %17 offset:16\n\t"
-                    "ds_read_b128 %4, %16 offset:32\n\tds_read_b128 %5, %17 offset:32\n\t"
-                    "ds_read_b128 %6, %16 offset:48\n\tds_read_b128 %7, %17 offset:48\n\t"
-                    "ds_read_b128 %8, %16 offset:64\n\tds_read_b128 %9, %17 offset:64\n\t"
-                    "ds_read_b128 %10, %16 offset:80\n\tds_read_b128 %11, %17 offset:80\n\t"
-                    "ds_read_b128 %12, %16 offset:96\n\tds_read_b128 %13, %17 offset:96\n\t"
-                    "ds_read_b128 %14, %16 offset:112\n\tds_read_b128 %15, %17 offset:112\n\t"
-                    "s_waitcnt lgkmcnt(0)"
-                    : "=&v"(wv[0]), "=&v"(xv[0]), "=&v"(wv[1]), "=&v"(xv[1]), "=&v"(wv[2]),
-                      "=&v"(xv[2]), "=&v"(wv[3]), "=&v"(xv[3]), "=&v"(wv[4]), "=&v"(xv[4]),
-                      "=&v"(wv[5]), "=&v"(xv[5]), "=&v"(wv[6]), "=&v"(xv[6]), "=&v"(wv[7]),
-                      "=&v"(xv[7])
-                    : "v"(wa), "v"(xa)
-                    : "memory");
+        constexpr int PER = RX_WDMA + 1;  // vector-memory instructions per stage
+        const uint32_t wrow = lane * RX_SL * 16;
+        const uint32_t xrow = 64 * RX_SL * 16 + (tl % TPW) * 128;
+        auto stage = [&](int sidx) { return ring + (sidx % RX_NBUF) * RX_STAGE_B; };
+        // LDS reads of a stage in asm (the compiler cannot tell them from
+        // the stages still in flight and would drain every DMA before them);
+        // their wait is a separate statement that takes the registers as
+        // in/out operands, so the summing of the previous stage overlaps
+        // the reads
+        auto rd = [&](f4 *wv, f4 *xv, int sidx) {
+            if (!act) return;
+            const uint32_t wa = lds_addr(stage(sidx)) + wrow, xa = lds_addr(stage(sidx)) + xrow;
+            asm volatile(
+                "ds_read_b128 %0, %16 offset:0\n\tds_read_b128 %1, %17 offset:0\n\t"
+                "ds_read_b128 %2, %16 offset:16\n\tds_read_b128 %3, %17 offset:16\n\t"
+                "ds_read_b128 %4, %16 offset:32\n\tds_read_b128 %5, %17 offset:32\n\t"
+                "ds_read_b128 %6, %16 offset:48\n\tds_read_b128 %7, %17 offset:48\n\t"
+                "ds_read_b128 %8, %16 offset:64\n\tds_read_b128 %9, %17 offset:64\n\t"
+                "ds_read_b128 %10, %16 offset:80\n\tds_read_b128 %11, %17 offset:80\n\t"
+                "ds_read_b128 %12, %16 offset:96\n\tds_read_b128 %13, %17 offset:96\n\t"
+                "ds_read_b128 %14, %16 offset:112\n\tds_read_b128 %15, %17 offset:112"
+                : "=&v"(wv[0]), "=&v"(xv[0]), "=&v"(wv[1]), "=&v"(xv[1]), "=&v"(wv[2]),
+                  "=&v"(xv[2]), "=&v"(wv[3]), "=&v"(xv[3]), "=&v"(wv[4]), "=&v"(xv[4]),
+                  "=&v"(wv[5]), "=&v"(xv[5]), "=&v"(wv[6]), "=&v"(xv[6]), "=&v"(wv[7]),
+                  "=&v"(xv[7])
+                : "v"(wa), "v"(xa)
+                : "memory");
+        };
+        auto wt = [&](f4 *wv, f4 *xv) {
+            asm volatile("s_waitcnt lgkmcnt(0)"
+                         : "+v"(wv[0]), "+v"(xv[0]), "+v"(wv[1]), "+v"(xv[1]), "+v"(wv[2]),
+                           "+v"(xv[2]), "+v"(wv[3]), "+v"(xv[3]), "+v"(wv[4]), "+v"(xv[4]),
+                           "+v"(wv[5]), "+v"(xv[5]), "+v"(wv[6]), "+v"(xv[6]), "+v"(wv[7]),
+                           "+v"(xv[7])
+                         :
+                         : "memory");
+        };
+        auto fm = [&](const f4 *wv, const f4 *xv) {
+            if (!act) return;
 #pragma unroll
-                for (int u = 0; u < RX_CH / 4; u++) {
-                    p0 = fma((double)xv[u].x, (double)wv[u].x, p0);
-                    p1 = fma((double)xv[u].y, (double)wv[u].y, p1);
-                    p2 = fma((double)xv[u].z, (double)wv[u].z, p2);
-                    p3 = fma((double)xv[u].w, (double)wv[u].w, p3);
-                }
+            for (int u = 0; u < RX_CH / 4; u++) {
+                p0 = fma((double)xv[u].x, (double)wv[u].x, p0);
+                p1 = fma((double)xv[u].y, (double)wv[u].y, p1);
+                p2 = fma((double)xv[u].z, (double)wv[u].z, p2);
+                p3 = fma((double)xv[u].w, (double)wv[u].w, p3);
             }
-            // the stage is refilled two iterations on
+        };
+        auto sync = [&]() {
             __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
             __builtin_amdgcn_wave_barrier();
+        };
+        static_assert(RX_CH / 4 == 8, "eight steps per stage");
+        f4 wA[8], xA[8], wB[8], xB[8];
+        // stage s lives in ring slot s % 3; nch is even and >= 2. The stage
+        // waits count this pass's DMAs only: retire the previous pass's
+        // logit stores first.
+        wait_vm<0>();
+        issue(0, stage(0));
+        issue(1, stage(1));
+        if (nch > 2) {
+            issue(2, stage(2));
+            wait_vm<2 * PER>();
+        } else {
+            wait_vm<PER>();
         }
+        sync();
+        rd(wA, xA, 0);
+        for (int ch = 0; ch < nch; ch += 2) {
+            // stage ch (A) is summed while stage ch + 1 (B) is read
+            wt(wA, xA);  // slot ch % 3 is free again
+            if (ch + 2 < nch) wait_vm<PER>();
+            else wait_vm<0>();
+            sync();
+            rd(wB, xB, ch + 1);
+            if (ch + 3 < nch) issue(ch + 3, stage(ch + 3));
+            fm(wA, xA);
+            // stage ch + 1 (B) is summed while stage ch + 2 (A) is read
+            wt(wB, xB);  // slot (ch + 1) % 3 is free again
+            if (ch + 2 < nch) {
+                if (ch + 3 < nch) wait_vm<PER>();
+                else wait_vm<0>();
+                sync();
+                rd(wA, xA, ch + 2);
+                if (ch + 4 < nch) issue(ch + 4, stage(ch + 4));
+            }
+            fm(wB, xB);
+        }
+        // every read of the ring is complete (wt) before the next pass
+        // refills it
         if (act) {
             const double tot = (p0 + p1) + (p2 + p3);
             const float f = (float)tot;
@@ -484,8 +527,8 @@ extern "C" int jtk_topk_verify(const double *approx, const double *xinfo, const 
                                int16_t *cand, int32_t *ncand, int32_t *ids, float *w,
                                float *logits, uint32_t *err, hipStream_t s) {
     if (T <= 0) return 0;
-    if (E > RX_EMAX || k < 1 || k > 64 || k > E || n % RX_CH != 0 ||
-        (int64_t)E * n > 0x7fffffff)
+    if (E > RX_EMAX || k < 1 || k > 64 || k > E || n % (2 * RX_CH) != 0 ||
+        (int64_t)E * n > 0x1fffffff || (int64_t)4 * n * 4 > 0x7fffffff)
         return (int)hipErrorInvalidValue;
     constexpr int TPB = RX_WPB * 64 / RX_G;
     constexpr size_t lds =
