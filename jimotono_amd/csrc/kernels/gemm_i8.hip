@@ -170,7 +170,7 @@ __device__ __forceinline__ float f16_to_f32(uint16_t h) {
 }
 
 #ifndef LB_STAGES
-#define LB_STAGES 4
+#define LB_STAGES 2  // measured on MI355X: 2 stages beat 3-7 (more blocks resident)
 #endif
 
 template <int BITS, int EPI, int NST>
@@ -273,6 +273,7 @@ __global__ __launch_bounds__(256, 2) void k_lowbit_grouped(
         for (int i = 0; i < 4; i++) af[i] = *(const v4i *)(st + i * 1024 + lane * 16);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
+            if (16 * i >= nrows) continue;  // wave-uniform: padding rows of a short tile
             const v4i z = {0, 0, 0, 0};
             const v4i c0 = mfma16x16x64(af[i], b[0], z);
             const v4i c1 = mfma16x16x64(af[i], b[1], z);
@@ -318,6 +319,168 @@ __global__ __launch_bounds__(256, 2) void k_lowbit_grouped(
                     bad |= !isfinite(f);
                     out[(int64_t)rowdst[rr] * ldo + col] = f;
                 }
+        }
+    }
+    if (bad) raise_err(err, EF_RANGE);
+    if (badmid) raise_err(err, EF_NONFINITE_MID);
+}
+
+// ===================== grouped low-bit GEMM, A tile resident =====================
+// Same work and arithmetic as k_lowbit_grouped, with the block's 64 gathered
+// A rows (all K) loaded into LDS once and CPB consecutive 128-channel groups
+// per block: the pipeline streams only weight panel-groups and scales
+// (stage s = channel group s / G, k-group s % G), and each channel group's
+// epilogue runs as soon as its G k-groups are summed. This amortises the
+// row gathering and the pipeline fill over CPB times more MFMA work.
+template <int BITS, int EPI, int NST>
+__global__ __launch_bounds__(256, 2) void k_lowbit_grouped_res(
+    const int8_t *__restrict__ A, int lda, const float *__restrict__ sA,
+    const int32_t *__restrict__ perm, int topk, const int32_t *__restrict__ tiles,
+    const int32_t *__restrict__ ntiles, const uint8_t *__restrict__ Wp,
+    const uint16_t *__restrict__ Ws, int64_t wp_stride, int64_t ws_stride, int N, int K,
+    int cpb, float *__restrict__ out, int ldo, uint32_t *err) {
+    constexpr int PB = BITS == 2 ? 256 : 512;  // bytes per panel-group
+    constexpr int BDMA = PB / 256;             // 256-byte DMAs per panel-group
+    constexpr int SOFF = 8 * PB;               // scales after the weight bytes
+    constexpr int STAGE = SOFF + 4 * 256;      // + one 256-byte scale slot per wave
+    constexpr int PER = 2 * BDMA + 1;          // DMAs per wave per stage
+    extern __shared__ __attribute__((aligned(1024))) int8_t smem[];  // A tile + NST stages
+    __shared__ int rowsrc[64];
+    __shared__ float rowscale[64];
+    __shared__ int rowdst[64];
+    const int tile = blockIdx.x;
+    if (tile >= *ntiles) return;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int4 td = ((const int4 *)tiles)[tile];  // {expert, first sorted row, rows}
+    const int e = td.x, pos0 = td.y, nrows = td.z;
+    if (tid < 64) {
+        const int r = min(tid, nrows - 1);
+        const int pos = pos0 + r;
+        int src;
+        if (EPI == EPI_SWIGLU) {
+            src = perm[pos] / topk;
+            rowdst[tid] = pos;
+        } else {
+            src = pos;
+            rowdst[tid] = perm[pos];
+        }
+        rowsrc[tid] = src;
+        rowscale[tid] = sA[src];
+    }
+    __syncthreads();
+    const int G = K / 64;
+    int8_t *atile = smem;                       // [G][4 panels][1 KiB]
+    int8_t *ring = smem + (size_t)G * 4096;
+    // A: wave w copies panel w (rows 16w..16w+15) of every k-group, once
+    const int8_t *a_src = A + (int64_t)rowsrc[wave * 16 + (lane & 15)] * lda + (lane >> 4) * 16;
+    for (int g = 0; g < G; g++) dma<16>(a_src + (int64_t)g * 64, atile + g * 4096 + wave * 1024);
+    const int pbb = (blockIdx.y * cpb * 128) >> 4;  // the block's first panel
+    const uint8_t *wbase = Wp + (int64_t)e * wp_stride;
+    const uint8_t *sbase = (const uint8_t *)(Ws + (int64_t)e * ws_stride);
+    const int sl = lane & 15;
+    auto issue = [&](int s) {
+        int8_t *st = ring + (s % NST) * STAGE;
+        const int cg = s / G, g = s % G;
+        const int pan0 = pbb + cg * 8 + 2 * wave;  // this wave's first panel
+        const uint8_t *b0 = wbase + ((int64_t)pan0 * G + g) * PB + lane * 4;
+        const uint8_t *b1 = b0 + (int64_t)G * PB;
+#pragma unroll
+        for (int d = 0; d < BDMA; d++) {
+            dma<4>(b0 + d * 256, st + (2 * wave) * PB + d * 256);
+            dma<4>(b1 + d * 256, st + (2 * wave + 1) * PB + d * 256);
+        }
+        // fp16 group scales of the two panels: lanes 0-7 panel pan0's 16
+        // values (2 per lane), lanes 8-15 panel pan0+1's; lanes 16-63 repeat
+        dma<4>(sbase + ((int64_t)(pan0 + (sl >> 3)) * G + g) * 32 + (sl & 7) * 4,
+               st + SOFF + wave * 256);
+    };
+    const int NS = cpb * G;
+#pragma unroll
+    for (int s = 0; s < NST - 1; s++)
+        if (s < NS) issue(s);
+
+    float T[4][2][4];
+    const int lr = (lane >> 4) * 4, lc = lane & 15;
+    uint32_t bad = 0, badmid = 0;
+    for (int s = 0; s < NS; s++) {
+        const int cg = s / G, g = s % G;
+        // the A tile was issued before stage 0, so stage waits cover it
+        wait_stage<PER>(min(NST - 2, NS - 1 - s));
+        barrier_lds();
+        if (s + NST - 1 < NS) issue(s + NST - 1);
+        if (g == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) T[i][j][r] = 0.0f;
+        }
+        const int8_t *st = ring + (s % NST) * STAGE;
+        const uint16_t *ss = (const uint16_t *)(st + SOFF + wave * 256);
+        const float s0 = f16_to_f32(ss[lane & 15]);
+        const float s1 = f16_to_f32(ss[16 + (lane & 15)]);
+        v4i b[2];
+        if (BITS == 2) {
+            b[0] = unpack_int2(*(const uint32_t *)(st + (2 * wave) * PB + lane * 4));
+            b[1] = unpack_int2(*(const uint32_t *)(st + (2 * wave + 1) * PB + lane * 4));
+        } else {
+            const uint2 w0 = *(const uint2 *)(st + (2 * wave) * PB + lane * 8);
+            const uint2 w1 = *(const uint2 *)(st + (2 * wave + 1) * PB + lane * 8);
+            b[0] = unpack_int4(w0.x, w0.y);
+            b[1] = unpack_int4(w1.x, w1.y);
+        }
+        v4i af[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) af[i] = *(const v4i *)(atile + g * 4096 + i * 1024 + lane * 16);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            if (16 * i >= nrows) continue;  // wave-uniform: padding rows of a short tile
+            const v4i z = {0, 0, 0, 0};
+            const v4i c0 = mfma16x16x64(af[i], b[0], z);
+            const v4i c1 = mfma16x16x64(af[i], b[1], z);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                T[i][0][r] = __builtin_fmaf((float)c0[r], s0, T[i][0][r]);
+                T[i][1][r] = __builtin_fmaf((float)c1[r], s1, T[i][1][r]);
+            }
+        }
+        if (g != G - 1) continue;
+        // epilogue of channel group cg
+        const int pan0 = pbb + cg * 8 + 2 * wave;
+        if (EPI == EPI_SWIGLU) {
+            // wave's panels: pan0 = gate block, pan0+1 = matching up block
+            const int hid = (pan0 / 2) * 16 + lc;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int rr = i * 16 + lr + r;
+                    if (rr >= nrows) continue;
+                    const float sa = rowscale[rr];
+                    const float gv = T[i][0][r] * sa;
+                    const float uv = T[i][1][r] * sa;
+                    bad |= (!isfinite(gv)) || (!isfinite(uv));
+                    float sv;
+                    badmid |= !silu_mul(gv, uv, &sv);
+                    out[(int64_t)rowdst[rr] * ldo + hid] = sv;
+                }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const int col = (pan0 + j) * 16 + lc;
+                if (col >= N) continue;
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int rr = i * 16 + lr + r;
+                        if (rr >= nrows) continue;
+                        const float f = T[i][j][r] * rowscale[rr];
+                        bad |= !isfinite(f);
+                        out[(int64_t)rowdst[rr] * ldo + col] = f;
+                    }
+            }
         }
     }
     if (bad) raise_err(err, EF_RANGE);
@@ -491,6 +654,35 @@ static hipError_t launch_lowbit(dim3 grid, hipStream_t s, const int8_t *A, int l
     return hipGetLastError();
 }
 
+#define LBR_KMAX 1024  // resident A tile: 64 rows x K bytes of LDS
+
+template <int BITS, int EPI, int NST>
+static hipError_t launch_lowbit_res(dim3 grid, int cpb, hipStream_t s, const int8_t *A, int lda,
+                                    const float *sA, const int32_t *perm, int topk,
+                                    const int32_t *tiles, const int32_t *ntiles,
+                                    const uint8_t *Wp, const uint16_t *Ws, int64_t wp_stride,
+                                    int64_t ws_stride, int N, int K, float *out, int ldo,
+                                    uint32_t *err) {
+    constexpr int PB = BITS == 2 ? 256 : 512;
+    constexpr int lds_max = LBR_KMAX * 64 + NST * (8 * PB + 4 * 256);
+    const int lds = K * 64 + NST * (8 * PB + 4 * 256);
+    auto kern = k_lowbit_grouped_res<BITS, EPI, NST>;
+    static bool attr_set[64];
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    if (!attr_set[dev]) {
+        e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                lds_max);
+        if (e != hipSuccess) return e;
+        attr_set[dev] = true;
+    }
+    hipLaunchKernelGGL(kern, grid, dim3(256), lds, s, A, lda, sA, perm, topk, tiles, ntiles, Wp,
+                       Ws, wp_stride, ws_stride, N, K, cpb, out, ldo, err);
+    return hipGetLastError();
+}
+
 extern "C" int jtk_lowbit_grouped(int bits, const int8_t *A, int lda, const float *sA,
                                   const int32_t *perm, const int32_t *off, int topk,
                                   const int32_t *tiles, const int32_t *ntiles, int max_tiles,
@@ -515,6 +707,24 @@ extern "C" int jtk_lowbit_grouped(int bits, const int8_t *A, int lda, const floa
         return (int)e;
     }
     if (rows_per_tile != 64) return (int)hipErrorInvalidValue;
+    if (bits == 4 && K <= LBR_KMAX && N % 128 == 0) {
+        // channel groups per block: as many as keep about 1536 blocks
+        const int ncg = N / 128;
+        int ny = (1536 + max_tiles - 1) / max_tiles;
+        if (ny > ncg) ny = ncg;
+        while (ncg % ny) ny++;
+        dim3 grid((unsigned)max_tiles, (unsigned)ny);
+        if (bits == 2)
+            e = launch_lowbit_res<2, EPI_SWIGLU, LB_STAGES>(grid, ncg / ny, s, A, lda, sA, perm,
+                                                            topk, tiles, ntiles, Wp, Ws, wp_stride,
+                                                            ws_stride, N, K, out, ldo, err);
+        else
+            e = launch_lowbit_res<4, EPI_SCATTER, LB_STAGES>(grid, ncg / ny, s, A, lda, sA, perm,
+                                                             topk, tiles, ntiles, Wp, Ws,
+                                                             wp_stride, ws_stride, N, K, out, ldo,
+                                                             err);
+        return (int)e;
+    }
     dim3 grid((unsigned)max_tiles, (unsigned)(N / 128));
     if (bits == 2)
         e = launch_lowbit<2, EPI_SWIGLU, LB_STAGES>(grid, s, A, lda, sA, perm, off, topk, tiles,
