@@ -25,20 +25,43 @@ __device__ __forceinline__ void raise_err(uint32_t *err, uint32_t bits) {
 }
 
 // ---- wavefront reductions (64 lanes) ----
+// Wave reductions on DPP lane moves (no LDS traffic): row_shr 1, 2, 4, 8
+// leaves each 16-lane row's result in its lane 15, row_bcast 15 and 31 carry
+// rows into lane 63, which is then read as a scalar. Lanes without a DPP
+// source keep their own value (old = v), so no identity element is needed.
+#define JT_DPP(v, ctrl, rmask) \
+    __builtin_amdgcn_update_dpp((v), (v), (ctrl), (rmask), 0xf, false)
+template <typename Op>
+__device__ __forceinline__ int wave_reduce_i(int v, Op op) {
+    v = op(v, JT_DPP(v, 0x111, 0xf));  // row_shr:1
+    v = op(v, JT_DPP(v, 0x112, 0xf));  // row_shr:2
+    v = op(v, JT_DPP(v, 0x114, 0xf));  // row_shr:4
+    v = op(v, JT_DPP(v, 0x118, 0xf));  // row_shr:8
+    v = op(v, JT_DPP(v, 0x142, 0xa));  // row_bcast:15 into rows 1, 3
+    v = op(v, JT_DPP(v, 0x143, 0xc));  // row_bcast:31 into rows 2, 3
+    return __builtin_amdgcn_readlane(v, 63);
+}
+#undef JT_DPP
 __device__ __forceinline__ float wave_max_f(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, JT_WAVE));
-    return v;
+    return __builtin_bit_cast(float, wave_reduce_i(__builtin_bit_cast(int, v), [](int a, int b) {
+        return __builtin_bit_cast(int, fmaxf(__builtin_bit_cast(float, a),
+                                             __builtin_bit_cast(float, b)));
+    }));
+}
+__device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
+    return (uint32_t)wave_reduce_i((int)v, [](int a, int b) {
+        return (int)max((uint32_t)a, (uint32_t)b);
+    });
+}
+// bits of |x|
+__device__ __forceinline__ uint32_t abs_bits(float x) {
+    return __builtin_bit_cast(uint32_t, x) & 0x7fffffffu;
 }
 __device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, JT_WAVE);
-    return v;
+    return wave_reduce_i(v, [](int a, int b) { return a + b; });
 }
 __device__ __forceinline__ int wave_or_i(int v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v |= __shfl_xor(v, o, JT_WAVE);
-    return v;
+    return wave_reduce_i(v, [](int a, int b) { return a | b; });
 }
 
 // ---- the reference's int8 quantiser (src/w8a8.c:815-850) ----
@@ -75,19 +98,17 @@ __device__ __forceinline__ int quant_code(float x, double scale_d) {
 // inv_f = (float)(1/scale_d) differs from the exact quotient x/scale_d by
 // less than 2^-22 relative (two fp32 roundings and the fp64 reciprocal),
 // i.e. < 3.1e-5 absolute for |x/scale_d| <= 128. round-half-away of the two
-// can differ only if a half-integer lies between them, so whenever frac|y|
-// is within 1e-4 of 0.5 the exact fp64 quotient is recomputed; otherwise
-// floor(|y| + 0.5) is the exact answer (|y| + 0.5 is not within an ulp of an
-// integer there, so its fp32 rounding cannot cross one).
+// can differ only if a half-integer lies between them, so whenever y is
+// within 1e-4 of a half-integer (|y - rint(y)| > 0.4999) the exact fp64
+// quotient is recomputed; otherwise rint(y) is not a tie and equals the
+// exact round-half-away code.
 __device__ __forceinline__ int quant_code_fast(float x, double scale_d, float inv_f) {
     if (scale_d == 0.0) return 0;
     if (!(inv_f < __builtin_inff())) return quant_code(x, scale_d);  // 1/scale_d > FLT_MAX
     const float y = x * inv_f;
-    const float a = fabsf(y);
-    if (fabsf((a - floorf(a)) - 0.5f) < 1e-4f) return quant_code(x, scale_d);
-    int q = (int)floorf(a + 0.5f);
-    q = q > 127 ? 127 : q;
-    return y < 0.0f ? -q : q;
+    const float q = rintf(y);  // y - q is exact; no tie outside the guard band
+    if (fabsf(y - q) > 0.4999f) return quant_code(x, scale_d);
+    return (int)__builtin_amdgcn_fmed3f(q, -127.0f, 127.0f);
 }
 // inv_f for quant_code_fast: (float)(1/scale_d), 0 for an all-zero row
 __device__ __forceinline__ float quant_inv_f(double scale_d) {

@@ -36,17 +36,20 @@ __global__ __launch_bounds__(256) void k_quant_rows(
             const int c = lane + 64 * i;
             v[i] = c < n4 ? x4[c] : make_float4(0.f, 0.f, 0.f, 0.f);
         }
+        // max |x| over the bit patterns with the sign cleared: for
+        // non-negative floats integer order is float order, and any inf or
+        // NaN lands at or above the bits of +inf
+        uint32_t mu = 0;
 #pragma unroll
         for (int i = 0; i < QR_REG; i++) {
             if (64 * i < n4) {  // wave-uniform; constant indices keep v[] in registers
-                bad |= (!isfinite(v[i].x)) || (!isfinite(v[i].y)) || (!isfinite(v[i].z)) ||
-                       (!isfinite(v[i].w));
-                m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)),
-                                   fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+                mu = max(mu, max(abs_bits(v[i].x), abs_bits(v[i].y)));
+                mu = max(mu, max(abs_bits(v[i].z), abs_bits(v[i].w)));
             }
         }
-        m = wave_max_f(m);
-        bad = wave_or_i(bad);
+        mu = wave_max_u(mu);
+        bad = mu >= 0x7f800000u;
+        m = __builtin_bit_cast(float, mu);
         QuantParams p = quant_params(m);
         if (bad || !p.ok) {
             if (lane == 0) raise_err(err, bad ? EF_NONFINITE_INPUT : EF_RANGE);

@@ -65,6 +65,11 @@ CASES = [
     (256, 128, 16, 4, 1, 192, 200),
     (128, 64, 32, 8, 0, 64, 16),
     (256, 64, 64, 8, 2, 128, 1),
+    # 64-row tiles whose down projection quantises its own rows (f = 256,
+    # 512, 1024 take the fused path)
+    (256, 512, 8, 2, 1, 128, 300),
+    (128, 1024, 4, 2, 0, 64, 200),
+    (128, 256, 16, 4, 0, 64, 260),
 ]
 
 
