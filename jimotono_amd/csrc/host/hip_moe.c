@@ -497,10 +497,18 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
                              L->tiles, L->ntiles, err, s);
         prof_mark(L, slot, ST_TILES, s);
     } else {
-        le |= jtk_sort(ids, Tk, E, (int64_t)Tk, L->rank, L->cnt, L->tot, L->off, NULL, L->perm,
-                       NULL, NULL, err, s);
-        prof_mark(L, slot, ST_TILES, s);
-        le |= jtk_make_tiles(L->off, E, R, L->tiles, L->ntiles, s);
+        /* sort and tile list in two launches when E <= 1024 and Tk <= 65536 */
+        const int rs = jtk_sort_mid(ids, Tk, E, (int64_t)Tk, R, L->rank, L->cnt, L->off, NULL,
+                                    L->perm, NULL, NULL, L->tiles, L->ntiles, err, s);
+        if (rs != (int)hipErrorInvalidValue) {
+            le |= rs;
+            prof_mark(L, slot, ST_TILES, s);
+        } else {
+            le |= jtk_sort(ids, Tk, E, (int64_t)Tk, L->rank, L->cnt, L->tot, L->off, NULL,
+                           L->perm, NULL, NULL, err, s);
+            prof_mark(L, slot, ST_TILES, s);
+            le |= jtk_make_tiles(L->off, E, R, L->tiles, L->ntiles, s);
+        }
     }
     prof_mark(L, slot, ST_R_GATEUP, s);
     le |= jtk_lowbit_grouped(2, L->Xq, n, L->sx, L->perm, L->off, k, L->tiles, L->ntiles,

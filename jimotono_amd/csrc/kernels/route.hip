@@ -247,6 +247,7 @@ extern "C" int jtk_topk(const float *logits, int rows, int E, int k, int32_t *id
 //  scatter: global rank g = cnt[b][e] + rank[q]; kept iff g < cap;
 //           perm[off[e] + g] = q.
 #define SQ 256
+#define SORT_MID_NB 256  // medium-batch sort: up to 256 blocks of 256 pairs
 __global__ __launch_bounds__(256) void k_sort_hist(const int32_t *__restrict__ ids, int Tk,
                                                    int E, int32_t *__restrict__ rank,
                                                    int32_t *__restrict__ cnt, uint32_t *err) {
@@ -347,10 +348,18 @@ __global__ __launch_bounds__(256) void k_sort_scatter(
     }
 }
 
+extern "C" int jtk_sort_mid(const int32_t *ids, int Tk, int E, int64_t cap, int R,
+                            int32_t *rank, int32_t *cnt, int32_t *off, int64_t *off64,
+                            int32_t *perm, int64_t *perm64, uint8_t *drop, int32_t *tiles,
+                            int32_t *ntiles, uint32_t *err, hipStream_t s);
+
 extern "C" int jtk_sort(const int32_t *ids, int Tk, int E, int64_t cap, int32_t *rank,
                         int32_t *cnt, int32_t *tot, int32_t *off, int64_t *off64,
                         int32_t *perm, int64_t *perm64, uint8_t *drop, uint32_t *err,
                         hipStream_t s) {
+    if (Tk > 0 && E <= 1024 && (Tk + SQ - 1) / SQ <= SORT_MID_NB)
+        return jtk_sort_mid(ids, Tk, E, cap, 0, rank, cnt, off, off64, perm, perm64, drop, NULL,
+                            NULL, err, s);
     const int NB = (Tk + SQ - 1) / SQ;
     hipLaunchKernelGGL(k_sort_hist, dim3((unsigned)NB), dim3(256), 0, s, ids, Tk, E, rank,
                        cnt, err);
@@ -515,6 +524,141 @@ extern "C" int jtk_sort_small(const int32_t *ids, int Tk, int E, int64_t cap, in
     if (Tk > SORT_SMALL || E > SORT_EMAX) return (int)hipErrorInvalidValue;
     hipLaunchKernelGGL(k_sort_small, dim3(1), dim3(1024), 0, s, ids, Tk, E, cap, R, off, off64,
                        perm, perm64, drop, tiles, ntiles, err);
+    return (int)hipGetLastError();
+}
+
+// ---------------- medium-batch sort: two launches ----------------
+// The same stable counting sort and tile list for E <= 1024 experts and up
+// to SORT_MID_NB blocks of 256 pairs. Launch 1 (one block per 256 pairs):
+// each wave finds the lanes holding its lane's expert with one ballot per
+// expert-id bit, so a pair's rank is its rank in its wave plus the counts
+// of its expert in the block's earlier waves; the block's per-expert
+// counts go to cnt. Launch 2 (same blocks, 1024 threads): the per-expert
+// sums over all blocks and over the earlier blocks (1024 / E threads per
+// expert, each over a segment of the blocks), the scan of the kept counts
+// into the expert offsets, and the placement of the block's own pairs;
+// block 0 also writes off[] and the tile list. Replaces hist, per-expert
+// scan, offsets, scatter and tile launches.
+__global__ __launch_bounds__(256) void k_sort_mid_rank(const int32_t *__restrict__ ids, int Tk,
+                                                       int E, int32_t *__restrict__ rank,
+                                                       int32_t *__restrict__ cnt,
+                                                       uint32_t *err) {
+    __shared__ int wc[4][1024];  // per-wave counts of each expert
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, b = blockIdx.x;
+    const int q = b * SQ + t;
+    int e = -1;
+    if (q < Tk) {
+        e = ids[q];
+        if (e < 0 || e >= E) {
+            raise_err(err, EF_BAD_ID);
+            e = -1;
+        }
+    }
+    for (int i = t; i < 4 * E; i += 256) wc[i / E][i % E] = 0;
+    __syncthreads();
+    // lanes of this wave with expert e: agree on every bit of the id
+    uint64_t m = __ballot(e >= 0);
+    const int nbits = E > 1 ? 32 - __builtin_clz((unsigned)(E - 1)) : 1;
+    for (int bit = 0; bit < nbits; bit++) {
+        const bool one = (e >> bit) & 1;
+        const uint64_t bm = __ballot(one);
+        m &= one ? bm : ~bm;
+    }
+    const int rw = __popcll(m & ((1ull << lane) - 1ull));
+    if (e >= 0 && rw == __popcll(m) - 1) wc[wave][e] = rw + 1;  // the group's last lane
+    __syncthreads();
+    if (e >= 0) {
+        int r = rw;
+        for (int w = 0; w < wave; w++) r += wc[w][e];
+        rank[q] = r;
+    }
+    for (int x = t; x < E; x += 256)
+        cnt[(int64_t)b * E + x] = wc[0][x] + wc[1][x] + wc[2][x] + wc[3][x];
+}
+
+__global__ __launch_bounds__(1024) void k_sort_mid_place(
+    const int32_t *__restrict__ ids, int Tk, int E, int64_t cap, int NB,
+    const int32_t *__restrict__ rank, const int32_t *__restrict__ cnt, int R,
+    int32_t *__restrict__ off, int64_t *__restrict__ off64, int32_t *__restrict__ perm,
+    int64_t *__restrict__ perm64, uint8_t *__restrict__ drop, int32_t *__restrict__ tiles,
+    int32_t *__restrict__ ntiles) {
+    __shared__ int eoff[1024], epre[1024], ps[1024], ts[1024], wsum[16];
+    const int t = threadIdx.x, b = blockIdx.x;
+    // thread (segment s, expert x) sums the blocks [s NB / seg, (s+1) NB / seg)
+    const int seg = 1024 / E;
+    const int x = t % E, sgi = t / E;
+    if (sgi < seg) {
+        int pre = 0, tot = 0;
+        const int b0 = sgi * NB / seg, b1 = (sgi + 1) * NB / seg;
+#pragma unroll 8
+        for (int bb = b0; bb < b1; bb++) {
+            const int c = cnt[(int64_t)bb * E + x];
+            pre += bb < b ? c : 0;
+            tot += c;
+        }
+        ps[t] = pre;
+        ts[t] = tot;
+    }
+    __syncthreads();
+    int pre = 0, tot = 0;  // pairs of expert t in earlier blocks, in all blocks
+    if (t < E)
+        for (int si = 0; si < seg; si++) {
+            pre += ps[si * E + t];
+            tot += ts[si * E + t];
+        }
+    const int kc = t < E ? (int)min((int64_t)tot, cap) : 0;
+    int ktot;
+    const int kbase = block_excl_scan_1024(kc, wsum, &ktot);
+    if (t < E) {
+        eoff[t] = kbase;
+        epre[t] = pre;
+    }
+    if (b == 0) {
+        if (t < E) {
+            off[t] = kbase;
+            if (off64) off64[t] = kbase;
+        }
+        if (t == 0) {
+            off[E] = ktot;
+            if (off64) off64[E] = ktot;
+        }
+        if (tiles) {
+            const int nt = (kc + R - 1) / R;
+            int ttot;
+            const int tbase = block_excl_scan_1024(nt, wsum, &ttot);
+            if (t < E) put_tiles((int4 *)tiles, tbase, t, kbase, kc, R);
+            if (t == 0) *ntiles = ttot;
+        }
+    }
+    __syncthreads();
+    if (t >= SQ) return;
+    const int q = b * SQ + t;
+    if (q >= Tk) return;
+    const int e = ids[q];
+    if (e < 0 || e >= E) return;
+    const int64_t g = (int64_t)epre[e] + rank[q];
+    const bool kept = g < cap;
+    if (drop) drop[q] = kept ? 0 : 1;
+    if (kept) {
+        perm[eoff[e] + g] = q;
+        if (perm64) perm64[eoff[e] + g] = q;
+    }
+}
+
+// Sort (and, with tiles != NULL, the R-row tile list) in two launches;
+// returns hipErrorInvalidValue when E > 1024 or Tk > SORT_MID_NB * 256.
+// cnt holds ceil(Tk / 256) * E ints.
+extern "C" int jtk_sort_mid(const int32_t *ids, int Tk, int E, int64_t cap, int R,
+                            int32_t *rank, int32_t *cnt, int32_t *off, int64_t *off64,
+                            int32_t *perm, int64_t *perm64, uint8_t *drop, int32_t *tiles,
+                            int32_t *ntiles, uint32_t *err, hipStream_t s) {
+    const int NB = (Tk + SQ - 1) / SQ;
+    if (Tk <= 0 || E <= 0 || E > 1024 || NB > SORT_MID_NB || (tiles && R <= 0))
+        return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_sort_mid_rank, dim3((unsigned)NB), dim3(256), 0, s, ids, Tk, E, rank,
+                       cnt, err);
+    hipLaunchKernelGGL(k_sort_mid_place, dim3((unsigned)NB), dim3(1024), 0, s, ids, Tk, E, cap,
+                       NB, rank, cnt, R, off, off64, perm, perm64, drop, tiles, ntiles);
     return (int)hipGetLastError();
 }
 

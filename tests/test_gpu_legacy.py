@@ -102,14 +102,17 @@ def test_routing_topk(jt, orc):
     assert jt.routing_topk(np.array([1.0, np.nan], np.float32), 1)[0] == 2
 
 
+# 800 pairs: one-block sort; 40000 pairs of 256 experts: two-launch sort;
+# more than 1024 experts or more than 65536 pairs: five-launch sort
+@pytest.mark.parametrize("T,k,E", [(200, 4, 16), (5000, 8, 256), (2000, 2, 1500),
+                                   (9000, 8, 300)])
 @pytest.mark.parametrize("cap", [1.0, 1.5])
-def test_batch_sort(jt, orc, cap):
-    announce(f"moe_batch_sort cap={cap}")
-    rng = np.random.default_rng(5)
-    T, k, E = 200, 4, 16
+def test_batch_sort(jt, orc, cap, T, k, E):
+    announce(f"moe_batch_sort T={T} k={k} E={E} cap={cap}")
+    rng = np.random.default_rng(5 + T + E)
     p = 1.0 / np.arange(1, E + 1) ** 1.1
     p /= p.sum()
-    ids = np.stack([rng.choice(E, size=k, replace=False, p=p) for _ in range(T)])
+    ids = np.argsort(rng.random((T, E)) ** (1.0 / p[None, :]), axis=1)[:, ::-1][:, :k]
     rc, perm, off, drop, dropped = jt.moe_batch_sort(ids, T, k, E, cap)
     rc2, perm2, off2, drop2 = orc.batch_sort(ids, T, k, E, cap)
     assert rc == rc2 == 0
