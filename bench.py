@@ -185,7 +185,8 @@ def main():
         "config": {"workload": "moe_layer_prefill", "tokens": T, "d_model": n,
                    "routed_experts": E, "expert_ffn": h, "topk": k, "shared_experts": S,
                    "shared_ffn": hs, "routed_quant": "INT2 gate/up, INT4 down, fp16 g64",
-                   "shared_quant": "W8A8 per-channel", "router": "fp64 top-8",
+                   "shared_quant": "W8A8 per-channel",
+                   "router": "exact fp64 top-8 (int8 MFMA bounds, fp64 candidates)",
                    "parallelism": "single GPU"},
         "roofline": roofline,
         "layer_int8_tops": total_ops / (ms_per_step / 1e3) / 1e12,

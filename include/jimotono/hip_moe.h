@@ -137,7 +137,10 @@ enum jt_hip_moe_buf {
     JT_HIP_BUF_XSCALE = 5,  /* fp32 [T] */
     JT_HIP_BUF_YE = 6,      /* fp32 [T*k][n], routed expert output per pair */
     JT_HIP_BUF_YS = 7,      /* fp32 [S][T][n], shared expert outputs */
-    JT_HIP_BUF_LOGITS = 8,  /* fp32 [T][E] */
+    JT_HIP_BUF_LOGITS = 8,  /* fp32 [T][E]: the reference's logit for every expert that
+                               could reach the top-k (every selected one); with the
+                               int8-bounded router (E <= 256, d % 64 == 0) the others
+                               hold the float of their int8 approximation */
 };
 int jt_hip_moe_buffer(const jt_hip_moe *L, int which, void **dptr,
                       size_t *bytes);
