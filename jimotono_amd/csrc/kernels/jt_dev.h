@@ -158,14 +158,70 @@ __device__ __forceinline__ int lowbit_code(double w, double maxabs, int bits) {
     return (int)l;
 }
 
+// ---- exp for the SwiGLU, fp64 ----
+// Tang's table-driven method (ACM TOMS 15(2), 1989): x = (64m + j) ln2/64 + r
+// with |r| <= ln2/128, exp(x) = 2^m * 2^(j/64) * e^r, e^r from its degree-5
+// Taylor polynomial (truncation below 2^-54 relative), applied as
+// t + t (e^r - 1) with one rounding. ln2/64 is split in two parts
+// (Cody-Waite) so the reduction is accurate to a few ulp of r. Within about
+// an ulp of exp; x is clamped to [-746, 710], where the double result is 0
+// and inf.
+__device__ const double jt_exp2_64th[64] = {
+    1.0, 1.0108892860517005, 1.0218971486541166, 1.0330248790212284,
+    1.0442737824274138, 1.0556451783605572, 1.0671404006768237, 1.0787607977571199,
+    1.0905077326652577, 1.102382583307841, 1.1143867425958924, 1.1265216186082418,
+    1.1387886347566916, 1.1511892299529827, 1.1637248587775775, 1.1763969916502812,
+    1.189207115002721, 1.202156731452703, 1.215247359980469, 1.22848053610687,
+    1.241857812073484, 1.255380757024691, 1.2690509571917332, 1.2828700160787783,
+    1.2968395546510096, 1.3109612115247644, 1.3252366431597413, 1.339667524053303,
+    1.3542555469368927, 1.3690024229745905, 1.383909881963832, 1.3989796725383112,
+    1.4142135623730951, 1.42961333839197, 1.4451808069770467, 1.460917794180647,
+    1.4768261459394993, 1.4929077282912648, 1.5091644275934228, 1.5255981507445384,
+    1.5422108254079407, 1.559004400237837, 1.5759808451078865, 1.593142151342267,
+    1.6104903319492543, 1.6280274218573478, 1.645755478153965, 1.6636765803267364,
+    1.681792830507429, 1.7001063537185235, 1.718619298122478, 1.7373338352737062,
+    1.7562521603732995, 1.7753764925265212, 1.7947090750031072, 1.8142521755003989,
+    1.8340080864093424, 1.8539791250833855, 1.8741676341103, 1.8945759815869656,
+    1.9152065613971474, 1.9360617934922943, 1.9571441241754002, 1.978456026387951};
+__device__ __forceinline__ double exp_tang(double x) {
+    x = fmin(fmax(x, -746.0), 710.0);
+    const double kd = rint(x * 92.33248261689366);  // 64 / ln2
+    const int k = (int)kd;
+    double r = fma(-kd, 0.010830424696249145, x);  // ln2/64, high part
+    r = fma(-kd, 3.623510646634843e-19, r);        // low part
+    double q = fma(r, 1.0 / 120.0, 1.0 / 24.0);  // e^r - 1 = r (1 + r/2 + ...)
+    q = fma(r, q, 1.0 / 6.0);
+    q = fma(r, q, 0.5);
+    q = fma(r, q, 1.0);
+    q *= r;
+    const double t = jt_exp2_64th[k & 63];
+    return ldexp(fma(t, q, t), k >> 6);  // t (1 + q) with one rounding
+}
+// 1/d for 1 <= d < 2^1000: hardware reciprocal and two Newton steps (within
+// an ulp of the correctly rounded quotient)
+__device__ __forceinline__ double recip_ge1(double d) {
+    double r = __builtin_amdgcn_rcp(d);
+    double e = fma(-d, r, 1.0);
+    r = fma(r, e, r);
+    e = fma(-d, r, 1.0);
+    return fma(r, e, r);
+}
+
 // ---- SwiGLU of the reference (src/moe_layer.c:139-156) ----
+// v = (g * (1 / (1 + exp(-g)))) * u in fp64, rounded to float, with the
+// reference's operation order. exp and the reciprocal are each within about
+// an ulp of the reference's glibc results, so v differs from the
+// reference's only where it lies within a few 1e-16 of a float rounding
+// boundary. The reference's finiteness test on sig, silu and v fails
+// exactly when g or u is not finite (for finite g, sig is in [0, 1] and v is
+// a finite double), which is what is returned.
 __device__ __forceinline__ bool silu_mul(float g, float u, float *s) {
-    double gi = (double)g, ui = (double)u;
-    double sig = 1.0 / (1.0 + exp(-gi));
-    double silu = gi * sig;
-    double v = silu * ui;
-    *s = (float)v;
-    return isfinite(v) && isfinite(sig) && isfinite(silu);
+    const double gi = (double)g, ui = (double)u;
+    const double ex = exp_tang(-gi);
+    const double sig = ex > 1e300 ? 0.0 : recip_ge1(1.0 + ex);
+    const double silu = gi * sig;
+    *s = (float)(silu * ui);
+    return isfinite(g) && isfinite(u);
 }
 
 // ---- panel layouts of prepared weights ----
