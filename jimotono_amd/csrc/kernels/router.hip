@@ -154,8 +154,8 @@ extern "C" int jtk_router_codes(const float *X, int rows, int n, int8_t *qh, int
 
 // ---- 2. approximate logits ----
 // Block = 64 tokens x 64 experts, 4 waves of 16 tokens; per 64-K block a
-// wave issues its 2 A fragments and 8 panels (hi/lo of 4 expert panels),
-// then 16 MFMAs into the four int32 sums of each 16x16 tile.
+// wave loads its 2 A fragments and 8 panels (hi/lo of 4 expert panels) one
+// block ahead, then runs 16 MFMAs into three int32 sums per 16x16 tile.
 __global__ __launch_bounds__(256) void k_router_approx(
     const int8_t *__restrict__ Xh, const int8_t *__restrict__ Xl, int n,
     const double2 *__restrict__ xinfo, const int8_t *__restrict__ Wh,
@@ -167,26 +167,42 @@ __global__ __launch_bounds__(256) void k_router_approx(
     const int r = lane & 15, kc = lane >> 4;
     const int64_t arow = (int64_t)min(t0 + r, T - 1) * n + kc * 16;
     const int pb = e0 / 16;
-    v4i hh[4], hl[4], lh[4], ll[4];
+    // HL and LH share their scale, so one int32 sum holds both (|sum| <
+    // 2 n 127^2 < 2^31 for n <= 4096)
+    v4i hh[4], mid[4], ll[4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) hh[j] = hl[j] = lh[j] = ll[j] = (v4i){0, 0, 0, 0};
-    for (int kb = 0; kb < KB; kb++) {
-        const v4i ah = *(const v4i *)(Xh + arow + kb * 64);
-        const v4i al = *(const v4i *)(Xl + arow + kb * 64);
-        v4i bh[4], bl[4];
+    for (int j = 0; j < 4; j++) hh[j] = mid[j] = ll[j] = (v4i){0, 0, 0, 0};
+    struct Frag {
+        v4i ah, al, bh[4], bl[4];
+    };
+    auto load = [&](int kb, Frag &f) {
+        f.ah = *(const v4i *)(Xh + arow + kb * 64);
+        f.al = *(const v4i *)(Xl + arow + kb * 64);
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int64_t po = ((int64_t)(pb + j) * KB + kb) * 1024 + lane * 16;
-            bh[j] = *(const v4i *)(Wh + po);
-            bl[j] = *(const v4i *)(Wl + po);
+            f.bh[j] = *(const v4i *)(Wh + po);
+            f.bl[j] = *(const v4i *)(Wl + po);
         }
+    };
+    auto mma = [&](const Frag &f) {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            hh[j] = mfma16x16x64(ah, bh[j], hh[j]);
-            hl[j] = mfma16x16x64(ah, bl[j], hl[j]);
-            lh[j] = mfma16x16x64(al, bh[j], lh[j]);
-            ll[j] = mfma16x16x64(al, bl[j], ll[j]);
+            hh[j] = mfma16x16x64(f.ah, f.bh[j], hh[j]);
+            mid[j] = mfma16x16x64(f.ah, f.bl[j], mid[j]);
+            mid[j] = mfma16x16x64(f.al, f.bh[j], mid[j]);
+            ll[j] = mfma16x16x64(f.al, f.bl[j], ll[j]);
         }
+    };
+    // the next k-block's fragments load while the current one is summed
+    Frag fa, fb;
+    load(0, fa);
+    for (int kb = 0; kb < KB; kb += 2) {
+        if (kb + 1 < KB) load(kb + 1, fb);
+        mma(fa);
+        if (kb + 1 >= KB) break;
+        if (kb + 2 < KB) load(kb + 2, fa);
+        mma(fb);
     }
     const int lr = (lane >> 4) * 4, lc = lane & 15;
 #pragma unroll
@@ -198,8 +214,8 @@ __global__ __launch_bounds__(256) void k_router_approx(
         for (int q = 0; q < 4; q++) {
             const int t = t0 + lr + q;
             if (t >= T) continue;
-            const double v = (double)hh[j][q] + ((double)hl[j][q] + (double)lh[j][q]) / 254.0 +
-                             (double)ll[j][q] / 64516.0;
+            const double v =
+                (double)hh[j][q] + (double)mid[j][q] / 254.0 + (double)ll[j][q] / 64516.0;
             approx[(int64_t)t * E + e] = xinfo[t].x * sw * v;
         }
     }
