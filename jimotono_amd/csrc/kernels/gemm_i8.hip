@@ -189,7 +189,7 @@ __global__ __launch_bounds__(256, 2) void k_lowbit_grouped(
     __shared__ int rowsrc[64];
     __shared__ float rowscale[64];
     __shared__ int rowdst[64];
-    const int tile = blockIdx.x;
+    const int tile = blockIdx.y;  // x walks the channel groups of a tile first
     if (tile >= *ntiles) return;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int4 td = ((const int4 *)tiles)[tile];  // {expert, first sorted row, rows}
@@ -210,7 +210,7 @@ __global__ __launch_bounds__(256, 2) void k_lowbit_grouped(
     }
     __syncthreads();
     const int G = K / 64;
-    const int n0 = blockIdx.y * 128;
+    const int n0 = blockIdx.x * 128;
     // A: wave w copies panel w (rows 16w..16w+15) of every stage;
     // lane l = kc*16 + r -> row 16w + r, bytes [16kc, 16kc+16) of the group
     const int8_t *a_src = A + (int64_t)rowsrc[wave * 16 + (lane & 15)] * lda + (lane >> 4) * 16;
@@ -348,7 +348,7 @@ __global__ __launch_bounds__(256, 2) void k_lowbit_grouped_res(
     __shared__ int rowsrc[64];
     __shared__ float rowscale[64];
     __shared__ int rowdst[64];
-    const int tile = blockIdx.x;
+    const int tile = blockIdx.y;  // x walks the channel groups of a tile first
     if (tile >= *ntiles) return;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int4 td = ((const int4 *)tiles)[tile];  // {expert, first sorted row, rows}
@@ -374,7 +374,7 @@ __global__ __launch_bounds__(256, 2) void k_lowbit_grouped_res(
     // A: wave w copies panel w (rows 16w..16w+15) of every k-group, once
     const int8_t *a_src = A + (int64_t)rowsrc[wave * 16 + (lane & 15)] * lda + (lane >> 4) * 16;
     for (int g = 0; g < G; g++) dma<16>(a_src + (int64_t)g * 64, atile + g * 4096 + wave * 1024);
-    const int pbb = (blockIdx.y * cpb * 128) >> 4;  // the block's first panel
+    const int pbb = (blockIdx.x * cpb * 128) >> 4;  // the block's first panel
     const uint8_t *wbase = Wp + (int64_t)e * wp_stride;
     const uint8_t *sbase = (const uint8_t *)(Ws + (int64_t)e * ws_stride);
     const int sl = lane & 15;
@@ -510,7 +510,7 @@ __global__ __launch_bounds__(64 * LS_WAVES) void k_lowbit_skinny(
     float *__restrict__ out, int ldo, uint32_t *err) {
     constexpr int PB = BITS == 2 ? 256 : 512;  // bytes per panel-group
     extern __shared__ __attribute__((aligned(16))) float ls_smem[];
-    const int tile = blockIdx.x;
+    const int tile = blockIdx.y;  // x walks the channel groups of a tile first
     if (tile >= *ntiles) return;
     const int G = K / 64;
     float4 *accf = (float4 *)ls_smem;               // [G][2][64]
@@ -523,7 +523,7 @@ __global__ __launch_bounds__(64 * LS_WAVES) void k_lowbit_skinny(
     const int pos = pos0 + min(r, nrows - 1);
     const int src = EPI == EPI_SWIGLU ? perm[pos] / topk : pos;
     const int8_t *arow = A + (int64_t)src * lda + kc * 16;
-    const int pan0 = blockIdx.y * 2;
+    const int pan0 = blockIdx.x * 2;
     const uint8_t *wb = Wp + (int64_t)e * wp_stride;
     const uint16_t *sb = Ws + (int64_t)e * ws_stride;
     for (int g = wave; g < G; g += nw) {
@@ -586,7 +586,7 @@ __global__ __launch_bounds__(64 * LS_WAVES) void k_lowbit_skinny(
             bad |= (!isfinite(gv)) || (!isfinite(uv));
             float sv;
             badmid |= !silu_mul(gv, uv, &sv);
-            out[(int64_t)dst[i] * ldo + blockIdx.y * 16 + lc] = sv;
+            out[(int64_t)dst[i] * ldo + blockIdx.x * 16 + lc] = sv;
         } else {
 #pragma unroll
             for (int q = 0; q < 2; q++) {
@@ -690,11 +690,12 @@ extern "C" int jtk_lowbit_grouped(int bits, const int8_t *A, int lda, const floa
                                   int64_t wp_stride, int64_t ws_stride, int N, int K, float *out,
                                   int ldo, uint32_t *err, hipStream_t s) {
     if (max_tiles <= 0) return 0;
+    if (max_tiles > 65535) return (int)hipErrorInvalidValue;  // tiles run on grid y
     hipError_t e;
     if (rows_per_tile == 16) {
         const int G = K / 64;
         if (G > LS_GMAX || N % 32) return (int)hipErrorInvalidValue;
-        dim3 grid((unsigned)max_tiles, (unsigned)(N / 32));
+        dim3 grid((unsigned)(N / 32), (unsigned)max_tiles);
         const int4 *t4 = (const int4 *)tiles;
         if (bits == 2)
             e = launch_lowbit_skinny<2, EPI_SWIGLU>(grid, G, s, A, lda, sA, perm, t4, ntiles, topk,
@@ -713,7 +714,7 @@ extern "C" int jtk_lowbit_grouped(int bits, const int8_t *A, int lda, const floa
         int ny = (1536 + max_tiles - 1) / max_tiles;
         if (ny > ncg) ny = ncg;
         while (ncg % ny) ny++;
-        dim3 grid((unsigned)max_tiles, (unsigned)ny);
+        dim3 grid((unsigned)ny, (unsigned)max_tiles);
         if (bits == 2)
             e = launch_lowbit_res<2, EPI_SWIGLU, LB_STAGES>(grid, ncg / ny, s, A, lda, sA, perm,
                                                             topk, tiles, ntiles, Wp, Ws, wp_stride,
@@ -725,7 +726,7 @@ extern "C" int jtk_lowbit_grouped(int bits, const int8_t *A, int lda, const floa
                                                              err);
         return (int)e;
     }
-    dim3 grid((unsigned)max_tiles, (unsigned)(N / 128));
+    dim3 grid((unsigned)(N / 128), (unsigned)max_tiles);
     if (bits == 2)
         e = launch_lowbit<2, EPI_SWIGLU, LB_STAGES>(grid, s, A, lda, sA, perm, off, topk, tiles,
                                                     ntiles, Wp, Ws, wp_stride, ws_stride, N, K,
