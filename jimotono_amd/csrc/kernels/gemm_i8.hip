@@ -14,6 +14,8 @@
 // whose byte order equals the MFMA operand layout, so operand panels are
 // copied global -> LDS with global_load_lds_dwordx4 (lane i's 16 bytes land
 // at LDS base + 16*i) and read back with one ds_read_b128 per lane.
+#include <type_traits>
+
 #include "gemm_w8a8.h"
 #include "jt_launch.h"
 
@@ -489,107 +491,140 @@ __global__ __launch_bounds__(256, 2) void k_lowbit_grouped_res(
 
 // ===================== grouped low-bit GEMM, few rows per expert =====================
 // Decode-sized batches (a handful of rows per expert): work item = (expert
-// e, 16 sorted rows) x 32 packed channels (2 panels), one block of
-// min(G, 16) waves where G = K/64 groups. Wave w takes the groups w, w+16,
-// ...: for each it issues the gathered A rows, the two panels' raw INT2/INT4
-// bytes and their fp16 scales at once, runs one MFMA per panel and parks
-// (float)acc_g and the group scale in LDS. Wave 0 then folds the groups in
-// ascending order, T = fmaf((float)acc_g, scale_g, T) -- the same fp32
-// sequence as the 64-row kernel -- and writes the epilogue.
-// Many waves with one group each keep the most loads in flight, which is
-// what decode-sized work is bound by.
-#define LS_WAVES 16
+// e, 16 sorted rows) x 64 packed channels (4 panels). A block has
+// nw = ceil(G / gpw) waves, gpw = min(4, G) consecutive 64-K groups per
+// wave (G = K/64). Each wave issues every load it needs at once -- the raw
+// INT2/INT4 bytes and fp16 scales of its groups (which need only the
+// expert) before the gathered A rows (which need the permutation) -- and
+// runs one MFMA per (group, panel). The group fold
+// T = fmaf((float)acc_g, scale_g, T) in ascending g, the same fp32 sequence
+// as the 64-row kernel, is then handed from wave to wave through LDS (wave
+// w folds its groups onto wave w-1's T); the last wave writes the epilogue.
+#define LS_PANELS 4
 #define LS_GMAX 64
 
+// raw panel-group bytes of one lane -> signed int8 operand
+__device__ __forceinline__ v4i unpack_raw(uint32_t w) { return unpack_int2(w); }
+__device__ __forceinline__ v4i unpack_raw(uint2 w) { return unpack_int4(w.x, w.y); }
+
 template <int BITS, int EPI>
-__global__ __launch_bounds__(64 * LS_WAVES) void k_lowbit_skinny(
+__global__ __launch_bounds__(1024) void k_lowbit_skinny(
     const int8_t *__restrict__ A, int lda, const float *__restrict__ sA,
     const int32_t *__restrict__ perm, const int4 *__restrict__ tiles,
     const int32_t *__restrict__ ntiles, int topk, const uint8_t *__restrict__ Wp,
     const uint16_t *__restrict__ Ws, int64_t wp_stride, int64_t ws_stride, int N, int K,
     float *__restrict__ out, int ldo, uint32_t *err) {
     constexpr int PB = BITS == 2 ? 256 : 512;  // bytes per panel-group
-    extern __shared__ __attribute__((aligned(16))) float ls_smem[];
+    typedef typename std::conditional<BITS == 2, uint32_t, uint2>::type raw_t;
+    __shared__ float4 tbuf[LS_PANELS][64];
     const int tile = blockIdx.y;  // x walks the channel groups of a tile first
     if (tile >= *ntiles) return;
     const int G = K / 64;
-    float4 *accf = (float4 *)ls_smem;               // [G][2][64]
-    float *scl = ls_smem + (size_t)G * 2 * 64 * 4;  // [G][2][16]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nw = blockDim.x >> 6;
+    const int gpw = G < 4 ? G : 4;
+    const int g0 = wave * gpw;
     const int4 td = tiles[tile];  // {expert, first sorted row, rows}
     const int e = td.x, pos0 = td.y, nrows = td.z;
+    const int pan0 = blockIdx.x * LS_PANELS;
+    const uint8_t *wb = Wp + (int64_t)e * wp_stride;
+    const uint16_t *sb = Ws + (int64_t)e * ws_stride;
+    raw_t braw[4][LS_PANELS];
+    uint16_t sc[4][LS_PANELS];
+#pragma unroll
+    for (int gi = 0; gi < 4; gi++) {
+        const int g = g0 + gi;
+        if (gi < gpw && g < G) {
+#pragma unroll
+            for (int q = 0; q < LS_PANELS; q++) {
+                const uint8_t *pg = wb + ((int64_t)(pan0 + q) * G + g) * PB;
+                braw[gi][q] = *(const raw_t *)(pg + lane * sizeof(raw_t));
+                sc[gi][q] = sb[((int64_t)(pan0 + q) * G + g) * 16 + (lane & 15)];
+            }
+        }
+    }
     const int r = lane & 15, kc = lane >> 4;
     const int pos = pos0 + min(r, nrows - 1);
     const int src = EPI == EPI_SWIGLU ? perm[pos] / topk : pos;
     const int8_t *arow = A + (int64_t)src * lda + kc * 16;
-    const int pan0 = blockIdx.x * 2;
-    const uint8_t *wb = Wp + (int64_t)e * wp_stride;
-    const uint16_t *sb = Ws + (int64_t)e * ws_stride;
-    for (int g = wave; g < G; g += nw) {
-        v4i a = *(const v4i *)(arow + (int64_t)g * 64);
-        if (r >= nrows) a = (v4i){0, 0, 0, 0};
-        v4i b[2];
-        uint16_t sc[2];
+    v4i a[4];
 #pragma unroll
-        for (int q = 0; q < 2; q++) {
-            const uint8_t *pg = wb + ((int64_t)(pan0 + q) * G + g) * PB;
-            if (BITS == 2) {
-                b[q] = unpack_int2(*(const uint32_t *)(pg + lane * 4));
-            } else {
-                const uint2 w = *(const uint2 *)(pg + lane * 8);
-                b[q] = unpack_int4(w.x, w.y);
-            }
-            sc[q] = sb[((int64_t)(pan0 + q) * G + g) * 16 + (lane & 15)];
-        }
-#pragma unroll
-        for (int q = 0; q < 2; q++) {
-            const v4i c = mfma16x16x64(a, b[q], (v4i){0, 0, 0, 0});
-            accf[(g * 2 + q) * 64 + lane] =
-                make_float4((float)c[0], (float)c[1], (float)c[2], (float)c[3]);
-            if (lane < 16) scl[(g * 2 + q) * 16 + lane] = f16_to_f32(sc[q]);
-        }
-    }
-    __syncthreads();
-    if (wave != 0) return;
-    // element q of lane l: row 4*(l/16) + q, channel l%16 of each panel.
-    // Row metadata first (loads and stores share one vmcnt on gfx9).
+    for (int gi = 0; gi < 4; gi++)
+        if (gi < gpw && g0 + gi < G) a[gi] = *(const v4i *)(arow + (int64_t)(g0 + gi) * 64);
+    // the last wave also needs the rows' scales and destinations
     const int lc = lane & 15, lr = (lane >> 4) * 4;
     float sa[4];
     int dst[4];
+    if (wave == nw - 1) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int p = pos0 + min(lr + i, nrows - 1);
-        const int s2 = EPI == EPI_SWIGLU ? perm[p] / topk : p;
-        sa[i] = sA[s2];
-        dst[i] = EPI == EPI_SWIGLU ? p : perm[p];
-    }
-    float T[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-    for (int g = 0; g < G; g++) {
-#pragma unroll
-        for (int q = 0; q < 2; q++) {
-            const float4 v = accf[(g * 2 + q) * 64 + lane];
-            const float s = scl[(g * 2 + q) * 16 + lc];
-            T[q][0] = __builtin_fmaf(v.x, s, T[q][0]);
-            T[q][1] = __builtin_fmaf(v.y, s, T[q][1]);
-            T[q][2] = __builtin_fmaf(v.z, s, T[q][2]);
-            T[q][3] = __builtin_fmaf(v.w, s, T[q][3]);
+        for (int i = 0; i < 4; i++) {
+            const int p = pos0 + min(lr + i, nrows - 1);
+            const int s2 = EPI == EPI_SWIGLU ? perm[p] / topk : p;
+            sa[i] = sA[s2];
+            dst[i] = EPI == EPI_SWIGLU ? p : perm[p];
         }
     }
+    v4i acc[4][LS_PANELS];
+#pragma unroll
+    for (int gi = 0; gi < 4; gi++) {
+        if (!(gi < gpw && g0 + gi < G)) continue;
+        const v4i av = r < nrows ? a[gi] : (v4i){0, 0, 0, 0};
+#pragma unroll
+        for (int q = 0; q < LS_PANELS; q++) {
+            acc[gi][q] = mfma16x16x64(av, unpack_raw(braw[gi][q]), (v4i){0, 0, 0, 0});
+        }
+    }
+    // element q of lane l: row 4*(l/16) + q, channel l%16 of each panel
+    float T[LS_PANELS][4];
+    for (int ph = 0; ph < nw; ph++) {
+        if (wave == ph) {
+#pragma unroll
+            for (int q = 0; q < LS_PANELS; q++) {
+                const float4 t = ph == 0 ? make_float4(0.f, 0.f, 0.f, 0.f) : tbuf[q][lane];
+                T[q][0] = t.x;
+                T[q][1] = t.y;
+                T[q][2] = t.z;
+                T[q][3] = t.w;
+            }
+#pragma unroll
+            for (int gi = 0; gi < 4; gi++) {
+                if (!(gi < gpw && g0 + gi < G)) continue;
+#pragma unroll
+                for (int q = 0; q < LS_PANELS; q++) {
+                    const float s = f16_to_f32(sc[gi][q]);
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        T[q][i] = __builtin_fmaf((float)acc[gi][q][i], s, T[q][i]);
+                }
+            }
+            if (ph + 1 < nw)
+#pragma unroll
+                for (int q = 0; q < LS_PANELS; q++)
+                    tbuf[q][lane] = make_float4(T[q][0], T[q][1], T[q][2], T[q][3]);
+        }
+        if (ph + 1 < nw) __syncthreads();
+    }
+    if (wave != nw - 1) return;
     uint32_t bad = 0, badmid = 0;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         if (lr + i >= nrows) continue;
         if (EPI == EPI_SWIGLU) {
-            const float gv = T[0][i] * sa[i];
-            const float uv = T[1][i] * sa[i];
-            bad |= (!isfinite(gv)) || (!isfinite(uv));
-            float sv;
-            badmid |= !silu_mul(gv, uv, &sv);
-            out[(int64_t)dst[i] * ldo + blockIdx.x * 16 + lc] = sv;
+            // panels pan0 + 2j (gate block) and pan0 + 2j + 1 (its up block)
+#pragma unroll
+            for (int j = 0; j < LS_PANELS / 2; j++) {
+                const int hid = (pan0 / 2 + j) * 16 + lc;
+                if ((pan0 + 2 * j + 1) * 16 + lc >= N) continue;
+                const float gv = T[2 * j][i] * sa[i];
+                const float uv = T[2 * j + 1][i] * sa[i];
+                bad |= (!isfinite(gv)) || (!isfinite(uv));
+                float sv;
+                badmid |= !silu_mul(gv, uv, &sv);
+                out[(int64_t)dst[i] * ldo + hid] = sv;
+            }
         } else {
 #pragma unroll
-            for (int q = 0; q < 2; q++) {
+            for (int q = 0; q < LS_PANELS; q++) {
                 const int col = (pan0 + q) * 16 + lc;
                 if (col >= N) continue;
                 const float f = T[q][i] * sa[i];
@@ -609,21 +644,10 @@ static hipError_t launch_lowbit_skinny(dim3 grid, int G, hipStream_t s, const in
                                        const uint8_t *Wp, const uint16_t *Ws, int64_t wp_stride,
                                        int64_t ws_stride, int N, int K, float *out, int ldo,
                                        uint32_t *err) {
-    const size_t lds = (size_t)G * 2 * 64 * 16 + (size_t)G * 2 * 16 * 4;
     auto kern = k_lowbit_skinny<BITS, EPI>;
-    static bool attr_set[64];
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return e;
-    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
-    if (!attr_set[dev]) {
-        e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                LS_GMAX * 2 * 64 * 16 + LS_GMAX * 2 * 16 * 4);
-        if (e != hipSuccess) return e;
-        attr_set[dev] = true;
-    }
-    const int nw = G < LS_WAVES ? G : LS_WAVES;
-    hipLaunchKernelGGL(kern, grid, dim3(64 * nw), lds, s, A, lda, sA, perm, tiles, ntiles, topk,
+    const int gpw = G < 4 ? G : 4;
+    const int nw = (G + gpw - 1) / gpw;  // <= 16 for G <= LS_GMAX
+    hipLaunchKernelGGL(kern, grid, dim3(64 * nw), 0, s, A, lda, sA, perm, tiles, ntiles, topk,
                        Wp, Ws, wp_stride, ws_stride, N, K, out, ldo, err);
     return hipGetLastError();
 }
@@ -694,8 +718,8 @@ extern "C" int jtk_lowbit_grouped(int bits, const int8_t *A, int lda, const floa
     hipError_t e;
     if (rows_per_tile == 16) {
         const int G = K / 64;
-        if (G > LS_GMAX || N % 32) return (int)hipErrorInvalidValue;
-        dim3 grid((unsigned)(N / 32), (unsigned)max_tiles);
+        if (G > LS_GMAX || N % (16 * LS_PANELS)) return (int)hipErrorInvalidValue;
+        dim3 grid((unsigned)(N / (16 * LS_PANELS)), (unsigned)max_tiles);
         const int4 *t4 = (const int4 *)tiles;
         if (bits == 2)
             e = launch_lowbit_skinny<2, EPI_SWIGLU>(grid, G, s, A, lda, sA, perm, t4, ntiles, topk,
