@@ -221,10 +221,82 @@ __global__ __launch_bounds__(256) void k_router_approx(
     }
 }
 
+// Few tokens (decode): block = 16 tokens x 16 experts, RA_W waves splitting
+// the k-blocks (wave w takes kb = w, w + RA_W, ...; all its loads of a batch
+// of 4 issued at once), int32 partial sums added in LDS (exact) by wave 0.
+// Many small blocks instead of a few long ones: the latency of one k-block
+// chain is what bounds a decode-sized call.
+#define RA_W 8
+__global__ __launch_bounds__(64 * RA_W) void k_router_approx_small(
+    const int8_t *__restrict__ Xh, const int8_t *__restrict__ Xl, int n,
+    const double2 *__restrict__ xinfo, const int8_t *__restrict__ Wh,
+    const int8_t *__restrict__ Wl, const double2 *__restrict__ winfo, int T, int E,
+    double *__restrict__ approx) {
+    __shared__ v4i part[RA_W][3][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int t0 = blockIdx.x * 16, pan = blockIdx.y;
+    const int KB = n / 64;
+    const int r = lane & 15, kc = lane >> 4;
+    const int64_t arow = (int64_t)min(t0 + r, T - 1) * n + kc * 16;
+    v4i hh = {0, 0, 0, 0}, mid = {0, 0, 0, 0}, ll = {0, 0, 0, 0};
+    for (int kb0 = wave; kb0 < KB; kb0 += 4 * RA_W) {
+        v4i ah[4], al[4], bh[4], bl[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int kb = kb0 + u * RA_W;
+            if (kb < KB) {
+                ah[u] = *(const v4i *)(Xh + arow + kb * 64);
+                al[u] = *(const v4i *)(Xl + arow + kb * 64);
+                const int64_t po = ((int64_t)pan * KB + kb) * 1024 + lane * 16;
+                bh[u] = *(const v4i *)(Wh + po);
+                bl[u] = *(const v4i *)(Wl + po);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            if (kb0 + u * RA_W < KB) {
+                hh = mfma16x16x64(ah[u], bh[u], hh);
+                mid = mfma16x16x64(ah[u], bl[u], mid);
+                mid = mfma16x16x64(al[u], bh[u], mid);
+                ll = mfma16x16x64(al[u], bl[u], ll);
+            }
+        }
+    }
+    part[wave][0][lane] = hh;
+    part[wave][1][lane] = mid;
+    part[wave][2][lane] = ll;
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int w = 1; w < RA_W; w++) {
+        hh += part[w][0][lane];
+        mid += part[w][1][lane];
+        ll += part[w][2][lane];
+    }
+    const int lr = (lane >> 4) * 4, lc = lane & 15;
+    const int e = pan * 16 + lc;
+    if (e >= E) return;
+    const double sw = winfo[e].x;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int t = t0 + lr + q;
+        if (t >= T) continue;
+        const double v = (double)hh[q] + (double)mid[q] / 254.0 + (double)ll[q] / 64516.0;
+        approx[(int64_t)t * E + e] = xinfo[t].x * sw * v;
+    }
+}
+
 extern "C" int jtk_router_approx(const int8_t *Xh, const int8_t *Xl, int n, const double *xinfo,
                                  const int8_t *Wh, const int8_t *Wl, const double *winfo, int T,
                                  int E, double *approx, hipStream_t s) {
     if (T <= 0) return 0;
+    if (T <= 256) {
+        dim3 g((unsigned)((T + 15) / 16), (unsigned)((E + 15) / 16));
+        hipLaunchKernelGGL(k_router_approx_small, g, dim3(64 * RA_W), 0, s, Xh, Xl, n,
+                           (const double2 *)xinfo, Wh, Wl, (const double2 *)winfo, T, E,
+                           approx);
+        return (int)hipGetLastError();
+    }
     dim3 grid((unsigned)((T + 63) / 64), (unsigned)((E + 63) / 64));
     hipLaunchKernelGGL(k_router_approx, grid, dim3(256), 0, s, Xh, Xl, n,
                        (const double2 *)xinfo, Wh, Wl, (const double2 *)winfo, T, E, approx);
@@ -244,6 +316,12 @@ __device__ __forceinline__ uint32_t okey(float f) {
 __device__ __forceinline__ float unkey(uint32_t k) {
     return __builtin_bit_cast(float, (k >> 31) ? (k & 0x7fffffffu) : ~k);
 }
+__device__ __forceinline__ double readlane_f64(double v, int l) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)b, l);
+    const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), l);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
 // largest float <= d
 __device__ __forceinline__ float float_rd(double d) {
     float f = (float)d;
@@ -260,13 +338,14 @@ __device__ __forceinline__ float float_rd(double d) {
 // subset's k-th largest, hence <= the k-th largest L. It is found as the
 // largest RV_KEYBITS-bit key prefix with at least k lane maxima at or above
 // it, one wave ballot per bit (k <= min(E, 64) lanes hold a bound).
-__global__ __launch_bounds__(64 * RV_WPB) void k_router_select(
-    const double *__restrict__ approx, const double2 *__restrict__ xinfo,
-    const double2 *__restrict__ winfo, int T, int E, int n, int k,
-    int16_t *__restrict__ cand, int32_t *__restrict__ ncand, float *__restrict__ logits) {
-    const int lane = threadIdx.x & 63;
-    const int t = blockIdx.x * RV_WPB + (threadIdx.x >> 6);
-    if (t >= T) return;
+// The candidates of token t into cand[0..nc) (ascending expert order) and
+// the float of the approximation into the logits of the others; returns nc
+// (wave-uniform). Called by one whole wavefront.
+__device__ __forceinline__ int select_token(const double *__restrict__ approx,
+                                            const double2 *__restrict__ xinfo,
+                                            const double2 *__restrict__ winfo, int t, int E,
+                                            int n, int k, int lane, int16_t *cand,
+                                            float *__restrict__ logits) {
     constexpr int EPL = RV_EMAX / 64;
     const double sx = xinfo[t].x, l1x = xinfo[t].y;
     const double ux = sx * (1.0 / 508.0);
@@ -303,10 +382,22 @@ __global__ __launch_bounds__(64 * RV_WPB) void k_router_select(
         const int e = lane + 64 * j;
         const bool c = e < E && hi[j] >= cut;
         const uint64_t mask = __ballot(c);
-        if (c) cand[(int64_t)t * E + nc + __popcll(mask & ((1ull << lane) - 1ull))] = (int16_t)e;
+        if (c) cand[nc + __popcll(mask & ((1ull << lane) - 1ull))] = (int16_t)e;
         else if (e < E) logits[(int64_t)t * E + e] = (float)ap[j];
         nc += __popcll(mask);
     }
+    return nc;
+}
+
+__global__ __launch_bounds__(64 * RV_WPB) void k_router_select(
+    const double *__restrict__ approx, const double2 *__restrict__ xinfo,
+    const double2 *__restrict__ winfo, int T, int E, int n, int k,
+    int16_t *__restrict__ cand, int32_t *__restrict__ ncand, float *__restrict__ logits) {
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * RV_WPB + (threadIdx.x >> 6);
+    if (t >= T) return;
+    const int nc =
+        select_token(approx, xinfo, winfo, t, E, n, k, lane, cand + (int64_t)t * E, logits);
     if (lane == 0) ncand[t] = nc;
 }
 
@@ -538,11 +629,145 @@ __global__ __launch_bounds__(64 * RX_WPB) void k_router_exact(
     }
 }
 
+// ---- 3+4 for few tokens: one wavefront per token ----
+// Decode-sized calls have too few tokens to fill the GPU with the 16-token
+// blocks above, and one wave's four fp64 chains per lane are then the
+// latency. Here a wavefront owns one token: it selects the candidates as
+// k_router_select does, then gives each of up to 16 candidates four lanes,
+// lane p running the reference's partial p (element j into partial j % 4,
+// src/moe_layer.c:67-86) as one fp64 chain over rows staged in LDS by
+// LDS-DMA, 1024 elements at a time (rows padded by 4 floats so the 16
+// candidates' lanes hit different banks). (l0 + l1) + (l2 + l3) is formed
+// with lane shuffles; top-k and softmax as k_router_exact.
+#define RS_CH 1024
+#define RS_STRIDE (RS_CH + 4)
+__global__ __launch_bounds__(64) void k_router_topk_small(
+    const double *__restrict__ approx, const double2 *__restrict__ xinfo,
+    const double2 *__restrict__ winfo, const float *__restrict__ X,
+    const float *__restrict__ Wg, int T, int E, int n, int k, int32_t *__restrict__ ids,
+    float *__restrict__ w, float *__restrict__ logits, uint32_t *err) {
+    extern __shared__ __attribute__((aligned(16))) char rs_smem[];
+    float *xs = (float *)rs_smem;                          // [RS_CH]
+    float *ws = xs + RS_CH;                                // [16][RS_STRIDE]
+    float *cval = ws + 16 * RS_STRIDE;                     // [RV_EMAX]
+    double *exl = (double *)(cval + RV_EMAX);              // [64]
+    int16_t *cand = (int16_t *)(exl + 64);                 // [RV_EMAX]
+    int16_t *sel = cand + RV_EMAX;                         // [64]
+    const int lane = threadIdx.x, t = blockIdx.x;
+    const int nc = select_token(approx, xinfo, winfo, t, E, n, k, lane, cand, logits);
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    const int slot = lane >> 2, p = lane & 3;
+    int bad = 0;
+    for (int c0 = 0; c0 < nc; c0 += 16) {
+        const int c = c0 + slot;
+        const bool act = c < nc;
+        double sp = 0.0;
+        for (int h0 = 0; h0 < n; h0 += RS_CH) {
+            const int ch = min(RS_CH, n - h0);  // a multiple of 256
+            // row of slot r: expert cand[c0 + r] (inactive slots stage
+            // expert cand[0]); 1 KiB of a row per DMA
+            for (int r = 0; r < 16; r++) {
+                const int er = cand[c0 + r < nc ? c0 + r : 0];
+                const float *src = Wg + (int64_t)er * n + h0 + lane * 4;
+                for (int q = 0; q < ch / 256; q++)
+                    dma<16>(src + q * 256, ws + r * RS_STRIDE + q * 256);
+            }
+            for (int q = 0; q < ch / 256; q++)
+                dma<16>(X + (int64_t)t * n + h0 + q * 256 + lane * 4, xs + q * 256);
+            wait_vm<0>();
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            if (act) {
+                const float *wr = ws + slot * RS_STRIDE;
+                for (int i = p; i < ch; i += 64) {
+                    float xv[16], wv[16];
+#pragma unroll
+                    for (int u = 0; u < 16; u++) {
+                        xv[u] = xs[i + 4 * u];
+                        wv[u] = wr[i + 4 * u];
+                    }
+#pragma unroll
+                    for (int u = 0; u < 16; u++) sp = fma((double)xv[u], (double)wv[u], sp);
+                }
+            }
+            // the next chunk overwrites the staged rows
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+        }
+        const double s1 = __shfl_down(sp, 1, 64), s2 = __shfl_down(sp, 2, 64),
+                     s3 = __shfl_down(sp, 3, 64);
+        if (act && p == 0) {
+            const double tot = (sp + s1) + (s2 + s3);
+            const float f = (float)tot;
+            bad |= (!isfinite(tot)) || (!isfinite(f));
+            cval[c] = f;
+            logits[(int64_t)t * E + cand[c]] = f;
+        }
+    }
+    if (__ballot(bad != 0)) {
+        if (lane == 0) raise_err(err, EF_NONFINITE_MID);
+        return;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    for (int c = lane; c < nc; c += 64) {
+        const float f = cval[c];
+        int rank = 0;
+        for (int j = 0; j < nc; j++) {
+            const float g = cval[j];
+            rank += (g > f) || (g == f && j < c);
+        }
+        if (rank < k) sel[rank] = (int16_t)c;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    if (nc < k) {
+        if (lane == 0) raise_err(err, EF_NONFINITE_MID);
+        return;
+    }
+    // the rank-0 value is the maximum
+    const float mx = cval[sel[0]];
+    const double ex = lane < k ? exp((double)cval[sel[lane]] - (double)mx) : 0.0;
+    double sum = 0.0;
+    for (int r = 0; r < k; r++) sum += readlane_f64(ex, r);
+    if (!((sum > 0.0) && isfinite(sum))) {
+        if (lane == 0) raise_err(err, EF_NONFINITE_MID);
+        return;
+    }
+    const float inv = (float)(1.0 / sum);
+    if (lane < k) {
+        const float wv = (float)ex * inv;
+        ids[(int64_t)t * k + lane] = cand[sel[lane]];
+        w[(int64_t)t * k + lane] = wv;
+        if (!(wv >= 0.0f) || !isfinite(wv)) raise_err(err, EF_NONFINITE_MID);
+    }
+}
+
 extern "C" int jtk_topk_verify(const double *approx, const double *xinfo, const double *winfo,
                                const float *X, const float *Wg, int T, int E, int n, int k,
                                int16_t *cand, int32_t *ncand, int32_t *ids, float *w,
                                float *logits, uint32_t *err, hipStream_t s) {
     if (T <= 0) return 0;
+    if (T <= 256 && E <= RV_EMAX && k >= 1 && k <= 64 && k <= E && n % 256 == 0) {
+        constexpr size_t lds_s = (size_t)(RS_CH + 16 * RS_STRIDE + RV_EMAX) * 4 + 64 * 8 +
+                                 (RV_EMAX + 64) * 2;
+        static bool attr_small[64];
+        int dev = 0;
+        hipError_t e = hipGetDevice(&dev);
+        if (e != hipSuccess) return (int)e;
+        if (dev < 0 || dev >= 64) return (int)hipErrorInvalidDevice;
+        if (!attr_small[dev]) {
+            e = hipFuncSetAttribute((const void *)k_router_topk_small,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_s);
+            if (e != hipSuccess) return (int)e;
+            attr_small[dev] = true;
+        }
+        hipLaunchKernelGGL(k_router_topk_small, dim3((unsigned)T), dim3(64), lds_s, s, approx,
+                           (const double2 *)xinfo, (const double2 *)winfo, X, Wg, T, E, n, k,
+                           ids, w, logits, err);
+        return (int)hipGetLastError();
+    }
     if (E > RX_EMAX || k < 1 || k > 64 || k > E || n % (2 * RX_CH) != 0 ||
         (int64_t)E * n > 0x1fffffff || (int64_t)4 * n * 4 > 0x7fffffff)
         return (int)hipErrorInvalidValue;
