@@ -110,6 +110,18 @@ __device__ __forceinline__ int quant_code_fast(float x, double scale_d, float in
     if (fabsf(y - q) > 0.4999f) return quant_code(x, scale_d);
     return (int)__builtin_amdgcn_fmed3f(q, -127.0f, 127.0f);
 }
+// The guard-band test of quant_code_fast without its fallback, for unrolled
+// rows: the exact path inlined at each of 64 codes would make a kernel tens
+// of KiB long (a decode-sized launch then waits on instruction fetch), so
+// the caller recomputes with quant_code the codes whose `fail` came back set.
+// inv_f = 0 (all-zero row) gives code 0; inv_f = inf makes y - q NaN and
+// so fails, like the explicit test in quant_code_fast.
+__device__ __forceinline__ int quant_code_try(float x, float inv_f, bool &fail) {
+    const float y = x * inv_f;
+    const float q = rintf(y);
+    fail |= !(fabsf(y - q) <= 0.4999f);
+    return (int)__builtin_amdgcn_fmed3f(q, -127.0f, 127.0f);
+}
 // inv_f for quant_code_fast: (float)(1/scale_d), 0 for an all-zero row
 __device__ __forceinline__ float quant_inv_f(double scale_d) {
     return scale_d != 0.0 ? (float)(1.0 / scale_d) : 0.0f;

@@ -58,16 +58,34 @@ __global__ __launch_bounds__(256) void k_quant_rows(
         if (lane == 0) scale[r] = p.scale_f;
         const float inv = quant_inv_f(p.scale_d);
         uint32_t *q4 = (uint32_t *)q;
+        uint32_t fmask = 0;  // bit i: a code of v[i] needs the exact quotient
 #pragma unroll
         for (int i = 0; i < QR_REG; i++) {
             const int c = lane + 64 * i;
-            if (64 * i < n4 && c < n4) {
-                const uint32_t b0 = (uint8_t)quant_code_fast(v[i].x, p.scale_d, inv);
-                const uint32_t b1 = (uint8_t)quant_code_fast(v[i].y, p.scale_d, inv);
-                const uint32_t b2 = (uint8_t)quant_code_fast(v[i].z, p.scale_d, inv);
-                const uint32_t b3 = (uint8_t)quant_code_fast(v[i].w, p.scale_d, inv);
-                q4[c] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+            if (64 * i < n4) {  // wave-uniform
+                bool f = false;
+                const uint32_t b0 = (uint8_t)quant_code_try(v[i].x, inv, f);
+                const uint32_t b1 = (uint8_t)quant_code_try(v[i].y, inv, f);
+                const uint32_t b2 = (uint8_t)quant_code_try(v[i].z, inv, f);
+                const uint32_t b3 = (uint8_t)quant_code_try(v[i].w, inv, f);
+                fmask |= (uint32_t)f << i;
+                if (c < n4) q4[c] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
             }
+        }
+        // rare: rewrite those words exactly, picking v[j] out of the
+        // registers with selects (a dynamic index would spill v[] to scratch)
+        while (fmask) {
+            const int j = __builtin_ctz(fmask);
+            fmask &= fmask - 1;
+            float4 u = v[0];
+#pragma unroll
+            for (int i = 1; i < QR_REG; i++)
+                if (i == j) u = v[i];
+            const uint32_t b0 = (uint8_t)quant_code(u.x, p.scale_d);
+            const uint32_t b1 = (uint8_t)quant_code(u.y, p.scale_d);
+            const uint32_t b2 = (uint8_t)quant_code(u.z, p.scale_d);
+            const uint32_t b3 = (uint8_t)quant_code(u.w, p.scale_d);
+            q4[lane + 64 * j] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
         }
         return;
     }

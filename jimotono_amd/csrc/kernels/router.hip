@@ -97,14 +97,17 @@ __global__ __launch_bounds__(256) void k_router_codes(const float *__restrict__ 
         const double inv_lo = p.scale_d != 0.0 ? 254.0 / p.scale_d : 0.0;
         uint32_t *qh4 = (uint32_t *)(qh + (int64_t)r * n);
         uint32_t *ql4 = (uint32_t *)(ql + (int64_t)r * n);
+        uint32_t fmask = 0;  // bit i: a code of v[i] needs the exact quotient
 #pragma unroll
         for (int i = 0; i < RC_REG; i++) {
             const int c = lane + 64 * i;
             if (64 * i < n4 && c < n4) {
-                const int q0 = quant_code_fast(v[i].x, p.scale_d, inv);
-                const int q1 = quant_code_fast(v[i].y, p.scale_d, inv);
-                const int q2 = quant_code_fast(v[i].z, p.scale_d, inv);
-                const int q3 = quant_code_fast(v[i].w, p.scale_d, inv);
+                bool f = false;
+                const int q0 = quant_code_try(v[i].x, inv, f);
+                const int q1 = quant_code_try(v[i].y, inv, f);
+                const int q2 = quant_code_try(v[i].z, inv, f);
+                const int q3 = quant_code_try(v[i].w, inv, f);
+                fmask |= (uint32_t)f << i;
                 qh4[c] = (uint32_t)(uint8_t)q0 | ((uint32_t)(uint8_t)q1 << 8) |
                          ((uint32_t)(uint8_t)q2 << 16) | ((uint32_t)(uint8_t)q3 << 24);
                 ql4[c] = router_lo_code(v[i].x, q0, p.scale_d, inv_lo) |
@@ -112,6 +115,27 @@ __global__ __launch_bounds__(256) void k_router_codes(const float *__restrict__ 
                          (router_lo_code(v[i].z, q2, p.scale_d, inv_lo) << 16) |
                          (router_lo_code(v[i].w, q3, p.scale_d, inv_lo) << 24);
             }
+        }
+        // rare: rewrite those words exactly, picking v[j] out of the
+        // registers with selects (a dynamic index would spill v[] to scratch)
+        while (fmask) {
+            const int j = __builtin_ctz(fmask);
+            fmask &= fmask - 1;
+            float4 u = v[0];
+#pragma unroll
+            for (int i = 1; i < RC_REG; i++)
+                if (i == j) u = v[i];
+            const int q0 = quant_code(u.x, p.scale_d);
+            const int q1 = quant_code(u.y, p.scale_d);
+            const int q2 = quant_code(u.z, p.scale_d);
+            const int q3 = quant_code(u.w, p.scale_d);
+            const int c = lane + 64 * j;
+            qh4[c] = (uint32_t)(uint8_t)q0 | ((uint32_t)(uint8_t)q1 << 8) |
+                     ((uint32_t)(uint8_t)q2 << 16) | ((uint32_t)(uint8_t)q3 << 24);
+            ql4[c] = router_lo_code(u.x, q0, p.scale_d, inv_lo) |
+                     (router_lo_code(u.y, q1, p.scale_d, inv_lo) << 8) |
+                     (router_lo_code(u.z, q2, p.scale_d, inv_lo) << 16) |
+                     (router_lo_code(u.w, q3, p.scale_d, inv_lo) << 24);
         }
         return;
     }

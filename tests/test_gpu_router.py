@@ -82,6 +82,8 @@ def adversarial(rng, T, n, E):
     X[8] = X[8] * f(2.0 ** -60)                   # tiny but normal
     X[9, ::2] = 0.0                               # half sparse
     X[10] = np.float32(1.0)                       # constant row
+    X[11] = rng.integers(-126, 126, n) + f(0.5)   # int8 codes on exact ties
+    X[11, 0] = f(127.0)
     return W, X
 
 

@@ -43,6 +43,28 @@ def test_quant_ties_round_half_away(jt, orc):
     assert np.array_equal(q, orc.quant_tensor(x)[1])
 
 
+@pytest.mark.parametrize("cols", [256, 1024, 2816, 4096, 4100])
+def test_quant_rows_ties(jt, orc, cols):
+    """Per-row codes on exact ties, at every register slot of a row: the
+    kernel's single-precision guess must hand each tie to the exact path."""
+    announce(f"quant rows ties cols={cols}")
+    rng = np.random.default_rng(cols)
+    X = (rng.standard_normal((9, cols)) * 20).astype(np.float32)
+    X[:, 0] = 127.0                                   # scale_d = 1 on every row
+    X[0, 1:] = rng.integers(-126, 126, cols - 1) + 0.5  # all ties
+    X[1, 1:] = np.clip(X[1, 1:], -126, 126)
+    X[1, rng.integers(1, cols, 40)] = -3.5            # a few scattered ties
+    X[2, 1::64] = 7.5                                 # one lane, every slot
+    X[3, 4 * 63 + 1::256] = -0.5                      # the last lane
+    rc, Q, s = jt.w8a8_quant_per_channel(X)
+    rc2, Q2, s2 = orc.quant_rows(X)
+    assert rc == 0 and rc2 == 0
+    assert np.array_equal(Q, Q2)
+    assert np.array_equal(bits(s), bits(s2))
+    assert Q[0, 1:].tolist() == [int(v + 0.5) if v > 0 else int(v - 0.5)
+                                 for v in X[0, 1:].tolist()]
+
+
 @pytest.mark.parametrize("n", [1, 255, 4096, 100003])
 def test_quant_per_tensor_and_dequant(jt, orc, n):
     announce(f"quant_per_tensor n={n}")
