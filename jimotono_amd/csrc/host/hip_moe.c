@@ -511,15 +511,25 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
         }
     }
     prof_mark(L, slot, ST_R_GATEUP, s);
-    le |= jtk_lowbit_grouped(2, L->Xq, n, L->sx, L->perm, L->off, k, L->tiles, L->ntiles,
-                             max_tiles, R, L->gu_P, L->gu_S, L->gu_pstride, L->gu_sstride, 2 * h,
-                             n, L->Sr, h, err, s);
-    prof_mark(L, slot, ST_R_QUANT, s);
-    le |= jtk_quant_rows(L->Sr, Tk, h, L->Sqr, h, L->ssr, NULL, err, s);
-    prof_mark(L, slot, ST_R_DOWN, s);
-    le |= jtk_lowbit_grouped(4, L->Sqr, h, L->ssr, L->perm, L->off, k, L->tiles, L->ntiles,
-                             max_tiles, R, L->dn_P, L->dn_S, L->dn_pstride, L->dn_sstride, n, h,
-                             L->Ye, n, err, s);
+    if (R == 16 && h == 256 && n % 256 == 0 && n <= 1024) {
+        /* 16-row tiles: gate/up, SwiGLU, row codes and down in one launch
+         * (the three stages are timed as one, under routed_gateup) */
+        le |= jtk_routed_ffn16(L->Xq, L->sx, L->perm, L->tiles, L->ntiles, max_tiles, k,
+                               L->gu_P, L->gu_S, L->gu_pstride, L->gu_sstride, L->dn_P, L->dn_S,
+                               L->dn_pstride, L->dn_sstride, n, h, L->Ye, err, s);
+        prof_mark(L, slot, ST_R_QUANT, s);
+        prof_mark(L, slot, ST_R_DOWN, s);
+    } else {
+        le |= jtk_lowbit_grouped(2, L->Xq, n, L->sx, L->perm, L->off, k, L->tiles, L->ntiles,
+                                 max_tiles, R, L->gu_P, L->gu_S, L->gu_pstride, L->gu_sstride,
+                                 2 * h, n, L->Sr, h, err, s);
+        prof_mark(L, slot, ST_R_QUANT, s);
+        le |= jtk_quant_rows(L->Sr, Tk, h, L->Sqr, h, L->ssr, NULL, err, s);
+        prof_mark(L, slot, ST_R_DOWN, s);
+        le |= jtk_lowbit_grouped(4, L->Sqr, h, L->ssr, L->perm, L->off, k, L->tiles, L->ntiles,
+                                 max_tiles, R, L->dn_P, L->dn_S, L->dn_pstride, L->dn_sstride, n,
+                                 h, L->Ye, n, err, s);
+    }
     if (fork) {
         for (int i = 0; i < L->nside; i++) le |= (int)hipStreamWaitEvent(s, L->ev_join[i], 0);
     } else {

@@ -652,6 +652,215 @@ static hipError_t launch_lowbit_skinny(dim3 grid, int G, hipStream_t s, const in
     return hipGetLastError();
 }
 
+// ===================== routed FFN of a 16-row tile, one launch =====================
+// Decode-sized batches: one block of 8 waves runs a whole (expert, <= 16
+// sorted rows) tile through gate/up, SwiGLU, the per-row int8 quantiser and
+// the down projection, so the three steps cost one launch and the
+// intermediate rows never leave LDS. Every weight byte of the expert (INT2
+// gate/up, INT4 down) and its fp16 scales are requested at the start: the
+// raw panels into registers (8 waves, so each has 256 of them), the scales
+// and the gathered A rows by LDS-DMA. Wave w owns h-channel blocks 2w and
+// 2w+1 (gate panel 2j, up panel 2j+1 of block j, every 64-K group in
+// ascending order) and then down panels DPW*w .. DPW*w+DPW-1. The arithmetic
+// is that of k_lowbit_skinny + k_quant_rows + k_lowbit_skinny: the same fp32
+// group folds, the same SwiGLU and the same row codes, so the outputs are
+// identical. h = 256 (16 blocks of 16 channels); n = 64*G1.
+#define RF_H 256
+#define RF_WAVES 8
+#define RF_HSTR (RF_H + 4)   // fp32 gate/up row stride (floats)
+#define RF_QSTR (RF_H + 16)  // int8 h row stride (bytes)
+
+__device__ __forceinline__ void lds_barrier() {
+    // LDS writes done, then the barrier (no wait on in-flight global loads)
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+template <int G1>
+__global__ __launch_bounds__(64 * RF_WAVES) void k_routed_ffn16(
+    const int8_t *__restrict__ Xq, const float *__restrict__ sx,
+    const int32_t *__restrict__ perm, const int4 *__restrict__ tiles,
+    const int32_t *__restrict__ ntiles, int topk, const uint8_t *__restrict__ guP,
+    const uint16_t *__restrict__ guS, int64_t gu_pstride, int64_t gu_sstride,
+    const uint8_t *__restrict__ dnP, const uint16_t *__restrict__ dnS, int64_t dn_pstride,
+    int64_t dn_sstride, float *__restrict__ Ye, uint32_t *err) {
+    constexpr int N = 64 * G1;                    // model width
+    constexpr int HB = (RF_H / 16) / RF_WAVES;    // h blocks per wave (2)
+    constexpr int DPW = (N / 16) / RF_WAVES;      // down panels per wave
+    constexpr int ASTR = N + 16;                  // A row stride (bytes)
+    constexpr int GUS_B = (2 * RF_H / 16) * G1 * 32;  // gate/up scale bytes of one expert
+    constexpr int DNS_B = (N / 16) * (RF_H / 64) * 32;
+    static_assert(N % 256 == 0 && N <= 1024, "n = 256, 512, 768 or 1024");
+    static_assert(GUS_B % 1024 == 0 && DNS_B % 1024 == 0, "1 KiB scale copies");
+    __shared__ __attribute__((aligned(16))) int8_t As[16 * ASTR];
+    __shared__ __attribute__((aligned(16))) uint16_t gus[GUS_B / 2];
+    __shared__ __attribute__((aligned(16))) uint16_t dns[DNS_B / 2];
+    __shared__ __attribute__((aligned(16))) float gb[16 * RF_HSTR];
+    __shared__ __attribute__((aligned(16))) float ub[16 * RF_HSTR];
+    __shared__ __attribute__((aligned(16))) int8_t hq[16 * RF_QSTR];
+    __shared__ float rsa[16], rsq[16];
+    __shared__ int rdst[16];
+    const int tile = blockIdx.x;
+    if (tile >= *ntiles) return;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int4 td = tiles[tile];  // {expert, first sorted row, rows}
+    const int e = td.x, pos0 = td.y, nrows = td.z;
+    if (nrows <= 0) return;
+    const uint8_t *gp = guP + (int64_t)e * gu_pstride;
+    const uint8_t *dp = dnP + (int64_t)e * dn_pstride;
+    const uint8_t *gsb = (const uint8_t *)(guS + (int64_t)e * gu_sstride);
+    const uint8_t *dsb = (const uint8_t *)(dnS + (int64_t)e * dn_sstride);
+    // Requests in the order their inputs are known: the scales and raw
+    // panels need only the expert, the A rows need the permutation (scalar
+    // loads, one more round trip). Loads complete in issue order, so the
+    // weights are in by the time the A rows are.
+    for (int c = wave; c < GUS_B / 1024; c += RF_WAVES)
+        dma<16>(gsb + c * 1024 + lane * 16, (char *)gus + c * 1024);
+    for (int c = wave; c < DNS_B / 1024; c += RF_WAVES)
+        dma<16>(dsb + c * 1024 + lane * 16, (char *)dns + c * 1024);
+    // raw weights into registers (wave-uniform bases and constant offsets:
+    // one address register for all)
+    const uint8_t *gw = gp + (int64_t)(2 * HB * wave) * G1 * 256;
+    const uint8_t *dw = dp + (int64_t)(DPW * wave) * 4 * 512;
+    uint32_t rg[HB][G1], ru[HB][G1];
+#pragma unroll
+    for (int j = 0; j < HB; j++)
+#pragma unroll
+        for (int g = 0; g < G1; g++) {
+            rg[j][g] = *(const uint32_t *)(gw + ((2 * j) * G1 + g) * 256 + lane * 4);
+            ru[j][g] = *(const uint32_t *)(gw + ((2 * j + 1) * G1 + g) * 256 + lane * 4);
+        }
+    uint2 rd[DPW][4];
+#pragma unroll
+    for (int q = 0; q < DPW; q++)
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+            rd[q][g] = *(const uint2 *)(dw + (q * 4 + g) * 512 + lane * 8);
+    // rows wave and wave+8 of A, with their token scale and Ye row
+#pragma unroll
+    for (int j = 0; j < 16 / RF_WAVES; j++) {
+        const int row = wave + RF_WAVES * j;
+        const int pv = perm[pos0 + min(row, nrows - 1)];
+        const int src = pv / topk;
+        if (lane < N / 16) dma<16>(Xq + (int64_t)src * N + lane * 16, As + row * ASTR);
+        if (lane == 0) {
+            rsa[row] = sx[src];
+            rdst[row] = pv;
+        }
+    }
+    wait_vm<0>();   // this wave's copies have landed
+    lds_barrier();  // ... and every other wave's
+    // ---- gate/up: rows 4*(lane/16)+i, h channel 16*(HB*wave+j) + lane%16 ----
+    const int r = lane & 15, kc = lane >> 4, lc = lane & 15, lr = (lane >> 4) * 4;
+    float Tg[HB][4], Tu[HB][4];
+#pragma unroll
+    for (int j = 0; j < HB; j++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) Tg[j][i] = Tu[j][i] = 0.f;
+    // one group at a time, the next A fragment read one group ahead
+    v4i an = *(const v4i *)(As + r * ASTR + kc * 16);
+#pragma unroll
+    for (int g = 0; g < G1; g++) {
+        const v4i a = an;
+        if (g + 1 < G1) an = *(const v4i *)(As + r * ASTR + (g + 1) * 64 + kc * 16);
+#pragma unroll
+        for (int j = 0; j < HB; j++) {
+            const int hb = HB * wave + j;
+            const v4i cg = mfma16x16x64(a, unpack_int2(rg[j][g]), (v4i){0, 0, 0, 0});
+            const v4i cu = mfma16x16x64(a, unpack_int2(ru[j][g]), (v4i){0, 0, 0, 0});
+            const float sg = f16_to_f32(gus[((2 * hb) * G1 + g) * 16 + lc]);
+            const float su = f16_to_f32(gus[((2 * hb + 1) * G1 + g) * 16 + lc]);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                Tg[j][i] = __builtin_fmaf((float)cg[i], sg, Tg[j][i]);
+                Tu[j][i] = __builtin_fmaf((float)cu[i], su, Tu[j][i]);
+                // pin the fold here: left alone the compiler keeps every
+                // group's MFMA result live and folds after the loop
+                asm volatile("" : "+v"(Tg[j][i]), "+v"(Tu[j][i]));
+            }
+        }
+    }
+    uint32_t flags = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int row = lr + i;
+        if (row >= nrows) continue;
+        const float sa = rsa[row];
+#pragma unroll
+        for (int j = 0; j < HB; j++) {
+            const float gv = Tg[j][i] * sa, uv = Tu[j][i] * sa;
+            if (!isfinite(gv) || !isfinite(uv)) flags |= EF_RANGE;
+            gb[row * RF_HSTR + 16 * (HB * wave + j) + lc] = gv;
+            ub[row * RF_HSTR + 16 * (HB * wave + j) + lc] = uv;
+        }
+    }
+    lds_barrier();
+    // ---- SwiGLU and the per-row int8 codes of h, rows wave and wave+8 ----
+#pragma unroll 1
+    for (int row = wave; row < nrows; row += RF_WAVES) {
+        const float4 g4 = *(const float4 *)(gb + row * RF_HSTR + lane * 4);
+        const float4 u4 = *(const float4 *)(ub + row * RF_HSTR + lane * 4);
+        float4 v;
+        bool ok = silu_mul(g4.x, u4.x, &v.x);
+        ok &= silu_mul(g4.y, u4.y, &v.y);
+        ok &= silu_mul(g4.z, u4.z, &v.z);
+        ok &= silu_mul(g4.w, u4.w, &v.w);
+        if (!ok) flags |= EF_NONFINITE_MID;
+        uint32_t mu = max(max(abs_bits(v.x), abs_bits(v.y)), max(abs_bits(v.z), abs_bits(v.w)));
+        mu = wave_max_u(mu);
+        const QuantParams qp = quant_params(__builtin_bit_cast(float, mu));
+        if (mu >= 0x7f800000u) {
+            flags |= EF_NONFINITE_INPUT;
+        } else if (!qp.ok) {
+            flags |= EF_RANGE;
+        } else {
+            const float inv = quant_inv_f(qp.scale_d);
+            const uint32_t b0 = (uint8_t)quant_code_fast(v.x, qp.scale_d, inv);
+            const uint32_t b1 = (uint8_t)quant_code_fast(v.y, qp.scale_d, inv);
+            const uint32_t b2 = (uint8_t)quant_code_fast(v.z, qp.scale_d, inv);
+            const uint32_t b3 = (uint8_t)quant_code_fast(v.w, qp.scale_d, inv);
+            *(uint32_t *)(hq + row * RF_QSTR + lane * 4) = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+            if (lane == 0) rsq[row] = qp.scale_f;
+        }
+    }
+    lds_barrier();
+    // ---- down: rows 4*(lane/16)+i, channel 16*(DPW*wave+q) + lane%16 ----
+    float Td[DPW][4];
+#pragma unroll
+    for (int q = 0; q < DPW; q++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) Td[q][i] = 0.f;
+#pragma unroll
+    for (int g = 0; g < RF_H / 64; g++) {
+        const v4i a = *(const v4i *)(hq + r * RF_QSTR + g * 64 + kc * 16);
+#pragma unroll
+        for (int q = 0; q < DPW; q++) {
+            const v4i c = mfma16x16x64(a, unpack_int4(rd[q][g].x, rd[q][g].y),
+                                       (v4i){0, 0, 0, 0});
+            const float sd = f16_to_f32(dns[((DPW * wave + q) * 4 + g) * 16 + lc]);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                Td[q][i] = __builtin_fmaf((float)c[i], sd, Td[q][i]);
+                asm volatile("" : "+v"(Td[q][i]));
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int row = lr + i;
+        if (row >= nrows) continue;
+        const float sa = rsq[row];
+        float *y = Ye + (int64_t)rdst[row] * N + 16 * DPW * wave + lc;
+#pragma unroll
+        for (int q = 0; q < DPW; q++) {
+            const float f = Td[q][i] * sa;
+            if (!isfinite(f)) flags |= EF_RANGE;
+            y[16 * q] = f;
+        }
+    }
+    if (flags) raise_err(err, flags);
+}
+
 template <int BITS, int EPI, int NST>
 static hipError_t launch_lowbit(dim3 grid, hipStream_t s, const int8_t *A, int lda,
                                 const float *sA, const int32_t *perm, const int32_t *off,
@@ -705,6 +914,30 @@ static hipError_t launch_lowbit_res(dim3 grid, int cpb, hipStream_t s, const int
     hipLaunchKernelGGL(kern, grid, dim3(256), lds, s, A, lda, sA, perm, topk, tiles, ntiles, Wp,
                        Ws, wp_stride, ws_stride, N, K, cpb, out, ldo, err);
     return hipGetLastError();
+}
+
+extern "C" int jtk_routed_ffn16(const int8_t *Xq, const float *sx, const int32_t *perm,
+                                const int32_t *tiles, const int32_t *ntiles, int max_tiles,
+                                int topk, const uint8_t *guP, const uint16_t *guS,
+                                int64_t gu_pstride, int64_t gu_sstride, const uint8_t *dnP,
+                                const uint16_t *dnS, int64_t dn_pstride, int64_t dn_sstride, int n,
+                                int h, float *Ye, uint32_t *err, hipStream_t s) {
+    if (max_tiles <= 0) return 0;
+    if (h != RF_H) return (int)hipErrorInvalidValue;
+    const int4 *t4 = (const int4 *)tiles;
+#define RF_LAUNCH(G)                                                                            \
+    hipLaunchKernelGGL(k_routed_ffn16<G>, dim3((unsigned)max_tiles), dim3(64 * RF_WAVES), 0, s, Xq, sx, \
+                       perm, t4, ntiles, topk, guP, guS, gu_pstride, gu_sstride, dnP, dnS,      \
+                       dn_pstride, dn_sstride, Ye, err)
+    switch (n) {
+    case 256: RF_LAUNCH(4); break;
+    case 512: RF_LAUNCH(8); break;
+    case 768: RF_LAUNCH(12); break;
+    case 1024: RF_LAUNCH(16); break;
+    default: return (int)hipErrorInvalidValue;
+    }
+#undef RF_LAUNCH
+    return (int)hipGetLastError();
 }
 
 extern "C" int jtk_lowbit_grouped(int bits, const int8_t *A, int lda, const float *sA,

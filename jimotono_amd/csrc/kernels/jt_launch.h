@@ -47,6 +47,15 @@ int jtk_lowbit_grouped(int bits, const int8_t *A, int lda, const float *sA,
                        int64_t wp_stride, int64_t ws_stride, int N, int K, float *out, int ldo,
                        uint32_t *err, hipStream_t s);
 
+/* the routed FFN of 16-row tiles in one launch (h = 256, n = 256..1024 in
+ * steps of 256); hipErrorInvalidValue for other shapes */
+int jtk_routed_ffn16(const int8_t *Xq, const float *sx, const int32_t *perm,
+                     const int32_t *tiles, const int32_t *ntiles, int max_tiles, int topk,
+                     const uint8_t *guP, const uint16_t *guS, int64_t gu_pstride,
+                     int64_t gu_sstride, const uint8_t *dnP, const uint16_t *dnS,
+                     int64_t dn_pstride, int64_t dn_sstride, int n, int h, float *Ye,
+                     uint32_t *err, hipStream_t s);
+
 /* router.hip: int8 MFMA candidates + exact fp64 verification of the gate */
 int jtk_router_codes(const float *X, int rows, int n, int8_t *qh, int8_t *ql, float *sf,
                      double *info, uint32_t *err, hipStream_t s);

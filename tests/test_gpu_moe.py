@@ -70,6 +70,12 @@ CASES = [
     (256, 512, 8, 2, 1, 128, 300),
     (128, 1024, 4, 2, 0, 64, 200),
     (128, 256, 16, 4, 0, 64, 260),
+    # 16-row tiles with f = 256: one launch per tile for gate/up, SwiGLU,
+    # row codes and down (n = 256, 512, 768, 1024)
+    (256, 256, 64, 8, 1, 128, 16),
+    (512, 256, 32, 4, 0, 64, 40),
+    (768, 256, 16, 2, 1, 64, 100),
+    (1024, 256, 256, 8, 2, 512, 16),
 ]
 
 
@@ -116,6 +122,26 @@ def test_layer_zipf_routed_parity(jt, orc, torch_cuda, T):
     assert o["rc"] == 0
     Ye = read_buf(torch, L, jt.BUF_YE, np.float32, (T * k, n))
     close(Ye, o["Ye"])
+    close(Y, o["Y"])
+
+
+@pytest.mark.parametrize("T", [1, 16, 33])
+def test_layer_decode_fused_zipf(jt, orc, torch_cuda, T):
+    """Decode widths (d=1024, E=256, f=256, k=8) under Zipf(1.1) routing: the
+    popular experts get several 16-row tiles, including short ones."""
+    torch = torch_cuda
+    n, h, E, k, S, hs = 1024, 256, 256, 8, 0, 0
+    announce(f"moe layer decode fused zipf T={T}")
+    rng = np.random.default_rng(1600 + T)
+    W = mk_weights(rng, n, h, E, S, hs)
+    X = rng.standard_normal((T, n)).astype(np.float32)
+    ids, w = zipf_ids(rng, T, k, E)
+    L, Y = run_layer(jt, torch, n, h, E, k, S, hs, T, W, X, ids, w)
+    o = orc.moe_q(n, h, E, k, S, hs, None, W[1], W[2], W[3], *W[4]).fwd(X, ids, w)
+    assert o["rc"] == 0
+    Ye = read_buf(torch, L, jt.BUF_YE, np.float32, (T * k, n))
+    diff = close(Ye, o["Ye"])
+    print(f"  last-bit differences in Ye: {diff} of {Ye.size}")
     close(Y, o["Y"])
 
 
