@@ -449,9 +449,15 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
     int le = 0;
     L->last_T = T;
 
-    const int fast = !d_ids && L->fast_router;
+    /* up to 16 tokens: every logit exact in one launch (with the codes Xq),
+     * then top-k; larger batches: int8 bounds and exact candidates */
+    const int small = !d_ids && L->Wgate && T <= 16 && n % 256 == 0 &&
+                      (size_t)(T + 4) * (n + 4) * 4 <= 160 * 1024;
+    const int fast = !d_ids && !small && L->fast_router;
     prof_mark(L, slot, ST_QUANT_X, s);
-    if (fast) /* the expert codes Xq plus the router's residual codes */
+    if (small) /* the codes Xq and all T x E logits (timed as quant_x) */
+        le |= jtk_router_logits_small(dX, L->Wgate, T, E, n, L->logits, L->Xq, L->sx, err, s);
+    else if (fast) /* the expert codes Xq plus the router's residual codes */
         le |= jtk_router_codes(dX, T, n, L->Xq, L->Xl, L->sx, L->xinfo, err, s);
     else
         le |= jtk_quant_rows(dX, T, n, L->Xq, n, L->sx, NULL, err, s);
@@ -474,6 +480,9 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
         ids = d_ids; /* caller-routed: read in place */
         w = d_w;
         prof_mark(L, slot, ST_TOPK, s);
+    } else if (small) {
+        prof_mark(L, slot, ST_TOPK, s);
+        le |= jtk_topk(L->logits, T, E, k, L->ids, NULL, L->w, err, s);
     } else if (fast) {
         le |= jtk_router_approx(L->Xq, L->Xl, n, L->xinfo, L->rWh, L->rWl, L->winfo, T, E,
                                 L->approx, s);

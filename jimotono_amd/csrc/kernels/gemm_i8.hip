@@ -653,20 +653,20 @@ static hipError_t launch_lowbit_skinny(dim3 grid, int G, hipStream_t s, const in
 }
 
 // ===================== routed FFN of a 16-row tile, one launch =====================
-// Decode-sized batches: one block of 8 waves runs a whole (expert, <= 16
+// Decode-sized batches: one block of 16 waves runs a whole (expert, <= 16
 // sorted rows) tile through gate/up, SwiGLU, the per-row int8 quantiser and
 // the down projection, so the three steps cost one launch and the
 // intermediate rows never leave LDS. Every weight byte of the expert (INT2
 // gate/up, INT4 down) and its fp16 scales are requested at the start: the
-// raw panels into registers (8 waves, so each has 256 of them), the scales
-// and the gathered A rows by LDS-DMA. Wave w owns h-channel blocks 2w and
-// 2w+1 (gate panel 2j, up panel 2j+1 of block j, every 64-K group in
-// ascending order) and then down panels DPW*w .. DPW*w+DPW-1. The arithmetic
+// raw panels into registers, the scales and the gathered A rows by
+// LDS-DMA. Wave w owns h-channel block w (gate panel 2w, up panel 2w+1,
+// every 64-K group in ascending order) and then down panels
+// DPW*w .. DPW*w+DPW-1. The arithmetic
 // is that of k_lowbit_skinny + k_quant_rows + k_lowbit_skinny: the same fp32
 // group folds, the same SwiGLU and the same row codes, so the outputs are
 // identical. h = 256 (16 blocks of 16 channels); n = 64*G1.
 #define RF_H 256
-#define RF_WAVES 8
+#define RF_WAVES 16
 #define RF_HSTR (RF_H + 4)   // fp32 gate/up row stride (floats)
 #define RF_QSTR (RF_H + 16)  // int8 h row stride (bytes)
 
@@ -736,7 +736,7 @@ __global__ __launch_bounds__(64 * RF_WAVES) void k_routed_ffn16(
 #pragma unroll
         for (int g = 0; g < 4; g++)
             rd[q][g] = *(const uint2 *)(dw + (q * 4 + g) * 512 + lane * 8);
-    // rows wave and wave+8 of A, with their token scale and Ye row
+    // row `wave` of A, with its token scale and Ye row
 #pragma unroll
     for (int j = 0; j < 16 / RF_WAVES; j++) {
         const int row = wave + RF_WAVES * j;
@@ -758,7 +758,14 @@ __global__ __launch_bounds__(64 * RF_WAVES) void k_routed_ffn16(
 #pragma unroll
         for (int i = 0; i < 4; i++) Tg[j][i] = Tu[j][i] = 0.f;
     // one group at a time, the next A fragment read one group ahead
+    // the next group's A fragment and scales are read one group ahead
     v4i an = *(const v4i *)(As + r * ASTR + kc * 16);
+    uint16_t sgn[HB], sun[HB];
+#pragma unroll
+    for (int j = 0; j < HB; j++) {
+        sgn[j] = gus[((2 * (HB * wave + j)) * G1) * 16 + lc];
+        sun[j] = gus[((2 * (HB * wave + j) + 1) * G1) * 16 + lc];
+    }
 #pragma unroll
     for (int g = 0; g < G1; g++) {
         const v4i a = an;
@@ -766,10 +773,13 @@ __global__ __launch_bounds__(64 * RF_WAVES) void k_routed_ffn16(
 #pragma unroll
         for (int j = 0; j < HB; j++) {
             const int hb = HB * wave + j;
+            const float sg = f16_to_f32(sgn[j]), su = f16_to_f32(sun[j]);
+            if (g + 1 < G1) {
+                sgn[j] = gus[((2 * hb) * G1 + g + 1) * 16 + lc];
+                sun[j] = gus[((2 * hb + 1) * G1 + g + 1) * 16 + lc];
+            }
             const v4i cg = mfma16x16x64(a, unpack_int2(rg[j][g]), (v4i){0, 0, 0, 0});
             const v4i cu = mfma16x16x64(a, unpack_int2(ru[j][g]), (v4i){0, 0, 0, 0});
-            const float sg = f16_to_f32(gus[((2 * hb) * G1 + g) * 16 + lc]);
-            const float su = f16_to_f32(gus[((2 * hb + 1) * G1 + g) * 16 + lc]);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 Tg[j][i] = __builtin_fmaf((float)cg[i], sg, Tg[j][i]);
@@ -795,7 +805,7 @@ __global__ __launch_bounds__(64 * RF_WAVES) void k_routed_ffn16(
         }
     }
     lds_barrier();
-    // ---- SwiGLU and the per-row int8 codes of h, rows wave and wave+8 ----
+    // ---- SwiGLU and the per-row int8 codes of h, wave w on row w ----
 #pragma unroll 1
     for (int row = wave; row < nrows; row += RF_WAVES) {
         const float4 g4 = *(const float4 *)(gb + row * RF_HSTR + lane * 4);

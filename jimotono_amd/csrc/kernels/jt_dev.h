@@ -41,6 +41,33 @@ __device__ __forceinline__ int wave_reduce_i(int v, Op op) {
     v = op(v, JT_DPP(v, 0x143, 0xc));  // row_bcast:31 into rows 2, 3
     return __builtin_amdgcn_readlane(v, 63);
 }
+// the same on 64-bit values (both halves move with the same DPP control);
+// the maximum is returned to every lane
+template <int CTRL, int RMASK>
+__device__ __forceinline__ uint64_t dpp_max_u64(uint64_t v) {
+    const int lo = (int)(uint32_t)v, hi = (int)(uint32_t)(v >> 32);
+    const uint32_t olo = (uint32_t)__builtin_amdgcn_update_dpp(lo, lo, CTRL, RMASK, 0xf, false);
+    const uint32_t ohi = (uint32_t)__builtin_amdgcn_update_dpp(hi, hi, CTRL, RMASK, 0xf, false);
+    const uint64_t o = ((uint64_t)ohi << 32) | olo;
+    return o > v ? o : v;
+}
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+    v = dpp_max_u64<0x111, 0xf>(v);  // row_shr:1
+    v = dpp_max_u64<0x112, 0xf>(v);  // row_shr:2
+    v = dpp_max_u64<0x114, 0xf>(v);  // row_shr:4
+    v = dpp_max_u64<0x118, 0xf>(v);  // row_shr:8
+    v = dpp_max_u64<0x142, 0xa>(v);  // row_bcast:15
+    v = dpp_max_u64<0x143, 0xc>(v);  // row_bcast:31
+    const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)v, 63);
+    const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
+    return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ double readlane_f64(double v, int l) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)b, l);
+    const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), l);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
 #undef JT_DPP
 __device__ __forceinline__ float wave_max_f(float v) {
     return __builtin_bit_cast(float, wave_reduce_i(__builtin_bit_cast(int, v), [](int a, int b) {

@@ -62,6 +62,10 @@ int jtk_router_codes(const float *X, int rows, int n, int8_t *qh, int8_t *ql, fl
 int jtk_router_approx(const int8_t *Xh, const int8_t *Xl, int n, const double *xinfo,
                       const int8_t *Wh, const int8_t *Wl, const double *winfo, int T, int E,
                       double *approx, hipStream_t s);
+/* T <= 16: every logit exact in fp64 (all T x E), plus the tokens' int8
+ * codes and scales; n % 256 == 0 */
+int jtk_router_logits_small(const float *X, const float *Wg, int T, int E, int n,
+                            float *logits, int8_t *Xq, float *sx, uint32_t *err, hipStream_t s);
 int jtk_topk_verify(const double *approx, const double *xinfo, const double *winfo,
                     const float *X, const float *Wg, int T, int E, int n, int k, int16_t *cand,
                     int32_t *ncand, int32_t *ids, float *w, float *logits, uint32_t *err,

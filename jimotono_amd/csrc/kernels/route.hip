@@ -164,58 +164,63 @@ extern "C" int jtk_router_logits(const float *X, const float *Wg, int T, int E, 
 // (value desc, index asc) with already-selected entries treated as -INF,
 // which is exactly the reference's strict-greater linear scan. NaN logits
 // are rejected (EF_NONFINITE_MID). ids are written as int32 and, when ids64
-// is non-NULL, also as 64-bit values (the reference's size_t).
+// is non-NULL, also as 64-bit values (the reference's size_t). The row is
+// read from memory once into LDS (4 * E floats per block), so the k rounds
+// pay LDS rather than memory latency.
 __global__ __launch_bounds__(256) void k_topk(const float *__restrict__ logits, int rows,
                                               int E, int k, int32_t *__restrict__ ids,
                                               int64_t *__restrict__ ids64,
                                               float *__restrict__ w, uint32_t *err) {
+    extern __shared__ float tk_smem[];
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;
-    const float *l = logits + (int64_t)row * E;
+    const float *lg = logits + (int64_t)row * E;
+    float *l = tk_smem + (threadIdx.x >> 6) * E;
     int nan = 0;
-    for (int i = lane; i < E; i += 64) nan |= isnan(l[i]);
+    for (int i = lane; i < E; i += 64) {
+        const float v = lg[i];
+        nan |= isnan(v);
+        l[i] = v;
+    }
+    // the row is written and read by this wavefront only
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
     nan = wave_or_i(nan);
     if (nan) {
         if (lane == 0) raise_err(err, EF_NONFINITE_MID);
         return;
     }
     // Lane l owns elements i = l + 64*j (j < 64, E <= 4096); bit j of
-    // `taken` marks an element already selected. Lane p ends up holding the
-    // p-th selected id.
+    // `taken` marks an element already selected. Each round takes the wave
+    // maximum of 64-bit keys (order-preserving bits of the value, -0 folded
+    // into +0 since the reference's comparisons treat them as equal, then
+    // ~i so that ties go to the lower index) with DPP moves. A taken
+    // element keys as -inf, as in the reference's scan, so when only -inf
+    // is left the lowest index wins even if already taken.
     uint64_t taken = 0;
     int mysel = -1;
     for (int p = 0; p < k; p++) {
-        float bv = -__builtin_inff();
-        int bi = 0x7fffffff;
+        uint64_t best = 0;
         for (int i = lane, j = 0; i < E; i += 64, j++) {
-            const float v = ((taken >> j) & 1ull) ? -__builtin_inff() : l[i];
-            if (v > bv || (v == bv && i < bi)) {
-                bv = v;
-                bi = i;
-            }
+            const float v = ((taken >> j) & 1ull) ? -__builtin_inff() : l[i] + 0.0f;
+            uint32_t u = __builtin_bit_cast(uint32_t, v);
+            u ^= (u >> 31) ? 0xffffffffu : 0x80000000u;
+            const uint64_t key = ((uint64_t)u << 32) | (uint32_t)~i;
+            best = key > best ? key : best;
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o, 64);
-            const int oi = __shfl_xor(bi, o, 64);
-            if (ov > bv || (ov == bv && oi < bi)) {
-                bv = ov;
-                bi = oi;
-            }
-        }
+        const int bi = (int)~(uint32_t)wave_max_u64(best);
         if ((bi & 63) == lane) taken |= 1ull << (bi >> 6);
         if (lane == p) mysel = bi;
     }
-    // softmax: each lane p < k holds id p; lane 0 accumulates sequentially.
+    // softmax over the selected, in selection order; the first selected is
+    // the maximum
     const float lv = lane < k ? l[mysel] : -__builtin_inff();
-    float mx = lv;
-    // max over selected in the reference's order is the plain maximum
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    const float mx = __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                   __builtin_bit_cast(int, lv), 0));
     const double e = lane < k ? exp((double)lv - (double)mx) : 0.0;
     double sum = 0.0;
-    for (int p = 0; p < k; p++) sum += __shfl(e, p, 64);
+    for (int p = 0; p < k; p++) sum += readlane_f64(e, p);
     const bool ok = (sum > 0.0) && isfinite(sum);
     if (!ok) {
         if (lane == 0) raise_err(err, EF_NONFINITE_MID);
@@ -233,8 +238,21 @@ __global__ __launch_bounds__(256) void k_topk(const float *__restrict__ logits, 
 
 extern "C" int jtk_topk(const float *logits, int rows, int E, int k, int32_t *ids,
                         int64_t *ids64, float *w, uint32_t *err, hipStream_t s) {
-    hipLaunchKernelGGL(k_topk, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, logits,
-                       rows, E, k, ids, ids64, w, err);
+    if (rows <= 0) return 0;
+    if (E > 4096) return (int)hipErrorInvalidValue;
+    static bool attr_set[64];
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= 64) return (int)hipErrorInvalidDevice;
+    if (!attr_set[dev]) {
+        e = hipFuncSetAttribute((const void *)k_topk, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                4 * 4096 * 4);
+        if (e != hipSuccess) return (int)e;
+        attr_set[dev] = true;
+    }
+    hipLaunchKernelGGL(k_topk, dim3((unsigned)((rows + 3) / 4)), dim3(256), (size_t)4 * E * 4, s,
+                       logits, rows, E, k, ids, ids64, w, err);
     return (int)hipGetLastError();
 }
 

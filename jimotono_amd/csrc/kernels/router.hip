@@ -340,12 +340,6 @@ __device__ __forceinline__ uint32_t okey(float f) {
 __device__ __forceinline__ float unkey(uint32_t k) {
     return __builtin_bit_cast(float, (k >> 31) ? (k & 0x7fffffffu) : ~k);
 }
-__device__ __forceinline__ double readlane_f64(double v, int l) {
-    const uint64_t b = __builtin_bit_cast(uint64_t, v);
-    const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)b, l);
-    const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), l);
-    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
-}
 // largest float <= d
 __device__ __forceinline__ float float_rd(double d) {
     float f = (float)d;
@@ -816,5 +810,112 @@ extern "C" int jtk_topk_verify(const double *approx, const double *xinfo, const 
     hipLaunchKernelGGL(k_router_exact, dim3((unsigned)((T + TPB - 1) / TPB)),
                        dim3(64 * RX_WPB), lds, s, (const int16_t *)cand, (const int32_t *)ncand,
                        X, Wg, T, E, n, k, ids, w, logits, err);
+    return (int)hipGetLastError();
+}
+
+// ---- decode-sized router: every logit exact, plus the token codes ----
+// For T <= 16 tokens the bound/candidate stages cost more launches than the
+// fp64 work they save, so every (token, expert) logit is computed exactly:
+// a block stages the T token rows (fp32, rows padded by 4 floats so the 16
+// token rows hit different banks) and 4 gate rows by LDS-DMA; wave w owns
+// expert 4*blockIdx.x + w and lane 4t + p runs the reference's partial p of
+// token t (element j into partial j % 4, src/moe_layer.c:67-86) as one fp64
+// chain, then (l0 + l1) + (l2 + l3) by lane shuffles. Block b < T also
+// writes token b's int8 codes and scale (the row quantiser,
+// src/w8a8.c:787-855) from the staged row. n % 256 == 0, T * (n + 4) * 4 +
+// 4 * (n + 4) * 4 bytes of LDS.
+#define RL_TMAX 16
+__global__ __launch_bounds__(256) void k_router_logits_small(
+    const float *__restrict__ X, const float *__restrict__ Wg, int T, int E, int n,
+    float *__restrict__ logits, int8_t *__restrict__ Xq, float *__restrict__ sx,
+    uint32_t *err) {
+    extern __shared__ __attribute__((aligned(16))) float rl_smem[];
+    const int stride = n + 4;
+    float *xs = rl_smem;                  // [T][n + 4]
+    float *ws = rl_smem + T * stride;     // [4][n + 4]
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int e = blockIdx.x * 4 + wave;
+    const int nc = n / 256;  // 1 KiB copies per row
+    for (int c = wave; c < T * nc; c += 4) {
+        const int t = c / nc, q = c % nc;
+        dma<16>(X + (int64_t)t * n + q * 256 + lane * 4, xs + t * stride + q * 256);
+    }
+    const int er = min(e, E - 1);
+    for (int q = 0; q < nc; q++)
+        dma<16>(Wg + (int64_t)er * n + q * 256 + lane * 4, ws + wave * stride + q * 256);
+    wait_vm<0>();
+    __syncthreads();
+    const int t = lane >> 2, p = lane & 3;
+    const bool act = t < T && e < E;
+    double acc = 0.0;
+    if (act) {
+        const float *xr = xs + t * stride + p;
+        const float *wr = ws + wave * stride + p;
+        for (int j = 0; j < n; j += 64) {
+            float xv[16], wv[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) {
+                xv[u] = xr[j + 4 * u];
+                wv[u] = wr[j + 4 * u];
+            }
+#pragma unroll
+            for (int u = 0; u < 16; u++) acc = fma((double)xv[u], (double)wv[u], acc);
+        }
+    }
+    const double a1 = __shfl_down(acc, 1, 64), a2 = __shfl_down(acc, 2, 64),
+                 a3 = __shfl_down(acc, 3, 64);
+    uint32_t bad = 0;
+    if (act && p == 0) {
+        const double tot = (acc + a1) + (a2 + a3);
+        const float f = (float)tot;
+        bad = (!isfinite(tot)) || (!isfinite(f));
+        logits[(int64_t)t * E + e] = f;
+    }
+    if (__ballot(bad != 0) && lane == 0) raise_err(err, EF_NONFINITE_MID);
+    // token blockIdx.x's codes (wave 0)
+    if (wave != 0 || (int)blockIdx.x >= T) return;
+    const int r = blockIdx.x;
+    const float *xr = xs + r * stride;
+    uint32_t mu = 0;
+    for (int c = lane; c < n; c += 64) mu = max(mu, abs_bits(xr[c]));
+    mu = wave_max_u(mu);
+    const QuantParams qp = quant_params(__builtin_bit_cast(float, mu));
+    if (mu >= 0x7f800000u || !qp.ok) {
+        if (lane == 0) raise_err(err, mu >= 0x7f800000u ? EF_NONFINITE_INPUT : EF_RANGE);
+        return;
+    }
+    if (lane == 0) sx[r] = qp.scale_f;
+    const float inv = quant_inv_f(qp.scale_d);
+    for (int c = lane * 4; c < n; c += 256) {
+        const uint32_t b0 = (uint8_t)quant_code_fast(xr[c], qp.scale_d, inv);
+        const uint32_t b1 = (uint8_t)quant_code_fast(xr[c + 1], qp.scale_d, inv);
+        const uint32_t b2 = (uint8_t)quant_code_fast(xr[c + 2], qp.scale_d, inv);
+        const uint32_t b3 = (uint8_t)quant_code_fast(xr[c + 3], qp.scale_d, inv);
+        *(uint32_t *)(Xq + (int64_t)r * n + c) = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+    }
+}
+
+extern "C" int jtk_router_logits_small(const float *X, const float *Wg, int T, int E, int n,
+                                       float *logits, int8_t *Xq, float *sx, uint32_t *err,
+                                       hipStream_t s) {
+    if (T <= 0) return 0;
+    if (T > RL_TMAX || n % 256 != 0 || E <= 0) return (int)hipErrorInvalidValue;
+    const size_t lds = (size_t)(T + 4) * (n + 4) * 4;
+    if (lds > 160 * 1024) return (int)hipErrorInvalidValue;
+    static bool attr_set[64];
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= 64) return (int)hipErrorInvalidDevice;
+    if (!attr_set[dev]) {
+        e = hipFuncSetAttribute((const void *)k_router_logits_small,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        if (e != hipSuccess) return (int)e;
+        attr_set[dev] = true;
+    }
+    const int nb = (E + 3) / 4 > T ? (E + 3) / 4 : T;
+    hipLaunchKernelGGL(k_router_logits_small, dim3((unsigned)nb), dim3(256), lds, s, X, Wg, T, E,
+                       n, logits, Xq, sx, err);
     return (int)hipGetLastError();
 }

@@ -92,13 +92,19 @@ def test_routing_topk(jt, orc):
     cases = [rng.standard_normal(256).astype(np.float32),
              np.full(64, 1.0, np.float32),
              np.round(rng.standard_normal(300) * 2).astype(np.float32) / 2,
-             np.array([2.0, 1.0, -np.inf, -np.inf], np.float32)]
+             np.array([2.0, 1.0, -np.inf, -np.inf], np.float32),
+             # signed zeros compare equal: ties go to the lower index
+             np.array([-0.0, 0.0, -0.0, 0.0, -1.0, 0.0, -0.0, 1e-45], np.float32),
+             rng.standard_normal(4096).astype(np.float32)]
     for lg in cases:
         for k in (1, 2, min(8, lg.size)):
             rc, ids, w = jt.routing_topk(lg, k)
             rc2, ids2, w2 = orc.topk(lg, k)
             assert rc == rc2 == 0 and np.array_equal(ids, ids2)
             np.testing.assert_allclose(w, w2, rtol=1e-6, atol=0)
+    # every selected logit -inf: the softmax has no finite maximum
+    lg = np.full(6, -np.inf, np.float32)
+    assert jt.routing_topk(lg, 2)[0] == orc.topk(lg, 2)[0]
     assert jt.routing_topk(np.array([1.0, np.nan], np.float32), 1)[0] == 2
 
 

@@ -2,10 +2,11 @@
 (gate logits in the reference's lane order, src/moe_layer.c:67-86, then
 top-k and softmax, src/routing.c:16-76).
 
-For E <= 256 and d % 64 == 0 the layer bounds every logit with int8 matrix
-products and evaluates the reference's fp64 sum only for the experts the
-bounds cannot rule out; other shapes take the fp64 router for every
-expert. Both must give the reference's ids exactly (including ties, which
+Up to 16 tokens (d % 256 == 0) the layer evaluates the reference's fp64
+sum for every expert in one launch. Otherwise, for E <= 256 and d % 64 == 0
+it bounds every logit with int8 matrix products and evaluates the fp64 sum
+only for the experts the bounds cannot rule out; other shapes take the fp64
+router for every expert. Both must give the reference's ids exactly (including ties, which
 go to the lower expert index), the selected logits bit for bit, and the
 softmax weights within rtol 1e-6 (device exp versus glibc's).
 """
@@ -108,3 +109,19 @@ def test_router_widths(jt, orc, torch_cuda, n):
     X = rng.standard_normal((T, n)).astype(np.float32)
     ids, w, lg = route(jt, torch_cuda, X, Wgate, k)
     check(orc, X, Wgate, k, ids, w, lg)
+
+
+@pytest.mark.parametrize("T,n,E,k", [(16, 256, 64, 8), (11, 1024, 256, 8), (1, 512, 320, 6),
+                                     (16, 1024, 40, 40)],
+                         ids=["T16d256", "T11d1024", "T1E320", "T16k40"])
+def test_router_decode_all_exact(jt, orc, torch_cuda, T, n, E, k):
+    """Decode batches: every logit is exact, so all of BUF_LOGITS must equal
+    the oracle's bit for bit, and the adversarial rows keep their ids."""
+    announce(f"router decode T={T} d={n} E={E} k={k}")
+    rng = np.random.default_rng(T * 1000 + E)
+    Wgate, X = adversarial(rng, max(T, 16), n, E)
+    X = X[:T]
+    ids, w, lg = route(jt, torch_cuda, X, Wgate, k)
+    check(orc, X, Wgate, k, ids, w, lg)
+    rc, _, _, olg = orc.router(X, Wgate, k)
+    assert np.array_equal(bits(lg), bits(olg))
