@@ -473,6 +473,10 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
                             L->side[e % L->nside], NULL);
         for (int i = 0; i < L->nside; i++) le |= (int)hipEventRecord(L->ev_join[i], L->side[i]);
     }
+    /* 16-row tiles when experts average at most 16 rows; the single-launch
+     * sort up to 1024 pairs */
+    const int R = Tk <= 16 * E ? 16 : 64;
+    const int max_tiles = Tk / R + E;
     prof_mark(L, slot, ST_ROUTER, s);
     const int32_t *ids = L->ids;
     const float *w = L->w;
@@ -496,10 +500,6 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
     }
     L->cur_ids = ids;
     L->cur_w = w;
-    /* 16-row tiles when experts average at most 16 rows; the single-launch
-     * sort up to 1024 pairs */
-    const int R = Tk <= 16 * E ? 16 : 64;
-    const int max_tiles = Tk / R + E;
     prof_mark(L, slot, ST_SORT, s);
     if (Tk <= 1024 && E <= 4096) {
         le |= jtk_sort_small(ids, Tk, E, (int64_t)Tk, R, L->off, NULL, L->perm, NULL, NULL,

@@ -160,23 +160,14 @@ extern "C" int jtk_router_logits(const float *X, const float *Wg, int T, int E, 
 }
 
 // ---------------- top-k + softmax ----------------
-// One wavefront per row of logits [rows][E]. Selection is an argmax by
-// (value desc, index asc) with already-selected entries treated as -INF,
-// which is exactly the reference's strict-greater linear scan. NaN logits
-// are rejected (EF_NONFINITE_MID). ids are written as int32 and, when ids64
-// is non-NULL, also as 64-bit values (the reference's size_t). The row is
-// read from memory once into LDS (4 * E floats per block), so the k rounds
-// pay LDS rather than memory latency.
-__global__ __launch_bounds__(256) void k_topk(const float *__restrict__ logits, int rows,
-                                              int E, int k, int32_t *__restrict__ ids,
-                                              int64_t *__restrict__ ids64,
-                                              float *__restrict__ w, uint32_t *err) {
-    extern __shared__ float tk_smem[];
-    const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= rows) return;
-    const float *lg = logits + (int64_t)row * E;
-    float *l = tk_smem + (threadIdx.x >> 6) * E;
+// Top-k and softmax of one row, one wavefront: the row is copied to the
+// wave's LDS row l (E floats), then selected; lanes p < k write id p and
+// weight p. Returns false (and raises the error) on a NaN logit or a
+// non-finite softmax; *id gets lane p's id (-1 on other lanes / failure).
+__device__ bool topk_wave(const float *__restrict__ lg, float *l, int E, int k, int lane,
+                          int64_t row, int32_t *__restrict__ ids, int64_t *__restrict__ ids64,
+                          float *__restrict__ w, uint32_t *err, int *id) {
+    *id = -1;
     int nan = 0;
     for (int i = lane; i < E; i += 64) {
         const float v = lg[i];
@@ -189,7 +180,7 @@ __global__ __launch_bounds__(256) void k_topk(const float *__restrict__ logits, 
     nan = wave_or_i(nan);
     if (nan) {
         if (lane == 0) raise_err(err, EF_NONFINITE_MID);
-        return;
+        return false;
     }
     // Lane l owns elements i = l + 64*j (j < 64, E <= 4096); bit j of
     // `taken` marks an element already selected. Each round takes the wave
@@ -224,16 +215,38 @@ __global__ __launch_bounds__(256) void k_topk(const float *__restrict__ logits, 
     const bool ok = (sum > 0.0) && isfinite(sum);
     if (!ok) {
         if (lane == 0) raise_err(err, EF_NONFINITE_MID);
-        return;
+        return false;
     }
     const float inv = (float)(1.0 / sum);
     if (lane < k) {
         const float wv = (float)e * inv;
-        ids[(int64_t)row * k + lane] = mysel;
-        if (ids64) ids64[(int64_t)row * k + lane] = mysel;
-        w[(int64_t)row * k + lane] = wv;
+        ids[row * k + lane] = mysel;
+        if (ids64) ids64[row * k + lane] = mysel;
+        w[row * k + lane] = wv;
         if (!(wv >= 0.0f) || !isfinite(wv)) raise_err(err, EF_NONFINITE_MID);
+        *id = mysel;
     }
+    return true;
+}
+
+// One wavefront per row of logits [rows][E]. Selection is an argmax by
+// (value desc, index asc) with already-selected entries treated as -INF,
+// which is exactly the reference's strict-greater linear scan. NaN logits
+// are rejected (EF_NONFINITE_MID). ids are written as int32 and, when ids64
+// is non-NULL, also as 64-bit values (the reference's size_t). The row is
+// read from memory once into LDS (4 * E floats per block), so the k rounds
+// pay LDS rather than memory latency.
+__global__ __launch_bounds__(256) void k_topk(const float *__restrict__ logits, int rows,
+                                              int E, int k, int32_t *__restrict__ ids,
+                                              int64_t *__restrict__ ids64,
+                                              float *__restrict__ w, uint32_t *err) {
+    extern __shared__ float tk_smem[];
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    int id;
+    (void)topk_wave(logits + (int64_t)row * E, tk_smem + (threadIdx.x >> 6) * E, E, k, lane, row,
+                    ids, ids64, w, err, &id);
 }
 
 extern "C" int jtk_topk(const float *logits, int rows, int E, int k, int32_t *ids,
@@ -461,24 +474,21 @@ __device__ __forceinline__ int block_excl_scan_1024(int v, int *wsum, int *total
     return before + x - v;
 }
 
-__global__ __launch_bounds__(1024) void k_sort_small(
-    const int32_t *__restrict__ ids, int Tk, int E, int64_t cap, int R,
-    int32_t *__restrict__ off, int64_t *__restrict__ off64, int32_t *__restrict__ perm,
-    int64_t *__restrict__ perm64, uint8_t *__restrict__ drop, int32_t *__restrict__ tiles,
-    int32_t *__restrict__ ntiles, uint32_t *err) {
-    __shared__ __attribute__((aligned(16))) int sid[SORT_SMALL];
-    __shared__ int cnt[SORT_EMAX];
-    __shared__ int eoff[SORT_EMAX + 1];
-    __shared__ int buf[16];
+// The body of the one-block sort: thread t holds pair t's expert e (-1:
+// none). The LDS arrays are the caller's.
+struct SortSmallLds {
+    int sid[SORT_SMALL];
+    int cnt[SORT_EMAX];
+    int eoff[SORT_EMAX + 1];
+    int buf[16];
+};
+__device__ void sort_small_core(int e, int Tk, int E, int64_t cap, int R,
+                                int32_t *__restrict__ off, int64_t *__restrict__ off64,
+                                int32_t *__restrict__ perm, int64_t *__restrict__ perm64,
+                                uint8_t *__restrict__ drop, int32_t *__restrict__ tiles,
+                                int32_t *__restrict__ ntiles, SortSmallLds &sm) {
+    int *sid = sm.sid, *cnt = sm.cnt, *eoff = sm.eoff, *buf = sm.buf;
     const int t = threadIdx.x;
-    int e = -1;
-    if (t < Tk) {
-        e = ids[t];
-        if (e < 0 || e >= E) {
-            raise_err(err, EF_BAD_ID);
-            e = -1;
-        }
-    }
     sid[t] = e;
     for (int i = t; i < E; i += 1024) cnt[i] = 0;
     __syncthreads();
@@ -533,6 +543,24 @@ __global__ __launch_bounds__(1024) void k_sort_small(
             if (perm64) perm64[eoff[e] + r] = t;
         }
     }
+}
+
+__global__ __launch_bounds__(1024) void k_sort_small(
+    const int32_t *__restrict__ ids, int Tk, int E, int64_t cap, int R,
+    int32_t *__restrict__ off, int64_t *__restrict__ off64, int32_t *__restrict__ perm,
+    int64_t *__restrict__ perm64, uint8_t *__restrict__ drop, int32_t *__restrict__ tiles,
+    int32_t *__restrict__ ntiles, uint32_t *err) {
+    __shared__ __attribute__((aligned(16))) SortSmallLds sm;
+    const int t = threadIdx.x;
+    int e = -1;
+    if (t < Tk) {
+        e = ids[t];
+        if (e < 0 || e >= E) {
+            raise_err(err, EF_BAD_ID);
+            e = -1;
+        }
+    }
+    sort_small_core(e, Tk, E, cap, R, off, off64, perm, perm64, drop, tiles, ntiles, sm);
 }
 
 extern "C" int jtk_sort_small(const int32_t *ids, int Tk, int E, int64_t cap, int R,
