@@ -108,7 +108,7 @@ def test_layer_router_parity(jt, orc, torch_cuda, case):
     print(f"  last-bit differences in Y: {diff} of {Y.size}")
 
 
-@pytest.mark.parametrize("T", [1, 4, 16, 130])
+@pytest.mark.parametrize("T", [1, 4, 16, 130, 600])
 def test_layer_zipf_routed_parity(jt, orc, torch_cuda, T):
     torch = torch_cuda
     n, h, E, k, S, hs = 256, 128, 64, 8, 1, 128
