@@ -193,7 +193,8 @@ __global__ __launch_bounds__(256, 2) void k_lowbit_grouped(
     __shared__ int rowdst[64];
     const int tile = blockIdx.y;  // x walks the channel groups of a tile first
     if (tile >= *ntiles) return;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar addressing
     const int4 td = ((const int4 *)tiles)[tile];  // {expert, first sorted row, rows}
     const int e = td.x, pos0 = td.y, nrows = td.z;
     if (tid < 64) {
@@ -219,7 +220,9 @@ __global__ __launch_bounds__(256, 2) void k_lowbit_grouped(
     // B: wave w copies the panel-groups of panels pb0 + 2w and pb0 + 2w + 1
     const int pb0 = n0 >> 4;
     const uint8_t *wbase = Wp + (int64_t)e * wp_stride;
-    const uint8_t *b_src0 = wbase + (int64_t)(pb0 + 2 * wave) * G * PB + lane * 4;
+    // (wave-uniform bases; the lane offset is added at each copy so the
+    // compiler keeps one offset register and advances the bases in SGPRs)
+    const uint8_t *b_src0 = wbase + (int64_t)(pb0 + 2 * wave) * G * PB;
     const uint8_t *b_src1 = b_src0 + (int64_t)G * PB;
     // this wave's two panels (absolute panel index within the expert)
     const int pan0 = pb0 + wave * 2;
@@ -227,18 +230,19 @@ __global__ __launch_bounds__(256, 2) void k_lowbit_grouped(
     // values (2 per lane), lanes 8-15 panel pan0+1's; lanes 16-63 repeat them
     // (the 4-byte DMA always writes 64 lanes)
     const int sl = lane & 15;
-    const uint8_t *s_src = (const uint8_t *)(Ws + (int64_t)e * ws_stride +
-                                             (int64_t)(pan0 + (sl >> 3)) * G * 16) +
-                           (sl & 7) * 4;
+    const uint8_t *s_src = (const uint8_t *)(Ws + (int64_t)e * ws_stride + (int64_t)pan0 * G * 16);
+    const int s_off = (sl >> 3) * G * 32 + (sl & 7) * 4;
     auto issue = [&](int g) {
         int8_t *st = smem + (g % NST) * STAGE;
         dma<16>(a_src + (int64_t)g * 64, st + wave * 1024);
 #pragma unroll
         for (int d = 0; d < BDMA; d++) {
-            dma<4>(b_src0 + (int64_t)g * PB + d * 256, st + 4096 + (2 * wave) * PB + d * 256);
-            dma<4>(b_src1 + (int64_t)g * PB + d * 256, st + 4096 + (2 * wave + 1) * PB + d * 256);
+            dma<4>(b_src0 + (int64_t)g * PB + d * 256 + lane * 4,
+                   st + 4096 + (2 * wave) * PB + d * 256);
+            dma<4>(b_src1 + (int64_t)g * PB + d * 256 + lane * 4,
+                   st + 4096 + (2 * wave + 1) * PB + d * 256);
         }
-        dma<4>(s_src + (int64_t)g * 32, st + SOFF + wave * 256);
+        dma<4>(s_src + (int64_t)g * 32 + s_off, st + SOFF + wave * 256);
     };
 #pragma unroll
     for (int s = 0; s < NST - 1; s++)
@@ -352,7 +356,8 @@ __global__ __launch_bounds__(256, 2) void k_lowbit_grouped_res(
     __shared__ int rowdst[64];
     const int tile = blockIdx.y;  // x walks the channel groups of a tile first
     if (tile >= *ntiles) return;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar addressing
     const int4 td = ((const int4 *)tiles)[tile];  // {expert, first sorted row, rows}
     const int e = td.x, pos0 = td.y, nrows = td.z;
     if (tid < 64) {
@@ -384,16 +389,17 @@ __global__ __launch_bounds__(256, 2) void k_lowbit_grouped_res(
         int8_t *st = ring + (s % NST) * STAGE;
         const int cg = s / G, g = s % G;
         const int pan0 = pbb + cg * 8 + 2 * wave;  // this wave's first panel
-        const uint8_t *b0 = wbase + ((int64_t)pan0 * G + g) * PB + lane * 4;
+        // wave-uniform bases, the lane offset added at each copy
+        const uint8_t *b0 = wbase + ((int64_t)pan0 * G + g) * PB;
         const uint8_t *b1 = b0 + (int64_t)G * PB;
 #pragma unroll
         for (int d = 0; d < BDMA; d++) {
-            dma<4>(b0 + d * 256, st + (2 * wave) * PB + d * 256);
-            dma<4>(b1 + d * 256, st + (2 * wave + 1) * PB + d * 256);
+            dma<4>(b0 + d * 256 + lane * 4, st + (2 * wave) * PB + d * 256);
+            dma<4>(b1 + d * 256 + lane * 4, st + (2 * wave + 1) * PB + d * 256);
         }
         // fp16 group scales of the two panels: lanes 0-7 panel pan0's 16
         // values (2 per lane), lanes 8-15 panel pan0+1's; lanes 16-63 repeat
-        dma<4>(sbase + ((int64_t)(pan0 + (sl >> 3)) * G + g) * 32 + (sl & 7) * 4,
+        dma<4>(sbase + ((int64_t)pan0 * G + g) * 32 + ((sl >> 3) * G * 32 + (sl & 7) * 4),
                st + SOFF + wave * 256);
     };
     const int NS = cpb * G;
