@@ -17,7 +17,8 @@ The JSON line carries, beside the contract fields:
                   host, or the oracle restatement when _ref is absent;
   sub          -- the other BASELINE shapes: W8A8 GEMM 64x1024x1024,
                   shared-expert decode M in {1,4,16}, routed decode T=16,
-                  and the E=512 stress grouped GEMM.
+                  the full decode layer at T=16 and the E=512 stress
+                  grouped GEMM.
 """
 import argparse
 import json
@@ -44,6 +45,10 @@ def parse():
                    help="run the timed region with every stage in order on one stream "
                         "(as the profiled pass does), so that a kernel trace of the "
                         "whole run sees each kernel alone on the GPU")
+    p.add_argument("--decode-only", action="store_true",
+                   help="run only the full decode-layer sub-benchmark (T=16, router, "
+                        "two shared and 256 routed experts) and print its JSON line; "
+                        "the workload of the decode kernel-trace profile")
     p.add_argument("--copy-probe", action="store_true",
                    help="also run a plain 256 MiB device copy (the reference kernel "
                         "for scaling HBM byte counters)")
@@ -98,6 +103,10 @@ def main():
     # so torch's default stream (handle 0) cannot carry the timing events
     stream = torch.cuda.Stream()
     torch.cuda.set_stream(stream)
+    if args.decode_only:
+        print(json.dumps({"decode_layer_T16": decode_layer(torch, api, stream, args.steps,
+                                                           args.warmup)}), flush=True)
+        return
 
     # ---------------- main workload: full layer prefill ----------------
     n, h, E, k, S, hs, T = 1024, 256, 256, 8, 2, 2816, 4096
@@ -317,6 +326,38 @@ def cpu_baseline_port(np, Xh, Wgate, Wg, Wu, Wd, Wgs, Wus, Wds, n, h, E, k, S, h
                       f"restatement, {el:.1f} s single-threaded", "seconds": el}
 
 
+def decode_layer(torch, api, stream, steps, warmup):
+    """Full decode layer: T=16 tokens through the router (top-8 of 256), two
+    shared experts (ffn 2816) and the routed experts (ffn 256), d=1024. Four
+    layer copies (90 MB of weights each) rotate so the weights stream from
+    HBM, as they would through a model's layers."""
+    n, h, E, k, S, hs, T = 1024, 256, 256, 8, 2, 2816, 16
+    layers = [make_layer(torch, api, n, h, E, k, S, hs, T, seed=900 + c)[0] for c in range(4)]
+    X = torch.randn(T, n, device="cuda")
+    Y = torch.empty(T, n, device="cuda")
+    it = [0]
+
+    def step():
+        rc = layers[it[0] % len(layers)].fwd(X, Y, stream)
+        assert rc == 0
+        it[0] += 1
+    _, ev = time_fn(torch, step, max(steps, 8) * 4, max(warmup, 2) * 4, stream)
+    assert api.sync_errors(stream) == 0
+    # weight bytes one forward reads: the shared experts, the fp32 gate and
+    # the routed experts its tokens touch (counted on layer 0's routing)
+    import numpy as np
+    assert layers[0].fwd(X, Y, stream) == 0
+    torch.cuda.synchronize()
+    touched = len(np.unique(layers[0].read(api.BUF_IDS, np.int32, (T, k))))
+    per_expert = 2 * h * n // 4 + n * h // 2 + 2 * (2 * h * n // 64 + n * h // 64)
+    wbytes = S * (3 * hs * n + 4 * (2 * hs + n)) + 4 * E * n + touched * per_expert
+    del layers
+    torch.cuda.empty_cache()
+    return {"us_per_layer": ev * 1e3, "tokens": T, "touched_experts": touched,
+            "weight_bytes": wbytes, "gbps": wbytes / (ev / 1e3) / 1e9,
+            "hbm_frac": wbytes / (ev / 1e3) / HBM_PEAK}
+
+
 def sub_benchmarks(np, torch, api, stream):
     res = {}
     # --- W8A8 GEMM 64x1024x1024 (per-row activation scales) ---
@@ -390,6 +431,8 @@ def sub_benchmarks(np, torch, api, stream):
                                 "hbm_frac": rbytes / (ev / 1e3) / HBM_PEAK}
     del layers
     torch.cuda.empty_cache()
+    # --- full decode layer: router, two shared and the routed experts ---
+    res["decode_layer_T16"] = decode_layer(torch, api, stream, 10, 2)
     # --- stress prefill: T=16384, d=2048, E=512, f=512, k=8, Zipf(1.1) ---
     n, h, E, k, T = 2048, 512, 512, 8, 16384
     ids = np.stack([rng.choice(E, k, replace=False, p=(1.0 / np.arange(1, E + 1) ** 1.1)
