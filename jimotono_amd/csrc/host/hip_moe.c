@@ -160,10 +160,20 @@ static int ffn_run_q(jt_rt *rt, jt_hip_ffn *F, const int8_t *Xq, const float *sx
     int e = jtk_w8a8_gemm(Xq, F->Kpn, sx, F->gu_P, F->gu_s, T, 2 * F->h, F->Np_gu, F->Kpn,
                           F->S, F->h, 1, rt->d_err, s);
     if (ev) (void)hipEventRecord(ev[1], s);
-    e |= jtk_quant_rows(F->S, T, F->h, F->Sq, F->Kph, F->ss, NULL, rt->d_err, s);
-    if (ev) (void)hipEventRecord(ev[2], s);
-    e |= jtk_w8a8_gemm(F->Sq, F->Kph, F->ss, F->d_P, F->d_s, T, F->n, F->Np_d, F->Kph, dY,
-                       F->n, 0, rt->d_err, s);
+    /* up to 16 rows the down projection quantises the hidden rows itself
+     * (timed with the down stage) */
+    const int f = T <= 16 ? jtk_w8a8_gemm_xq(F->S, F->h, F->h, F->d_P, F->d_s, T, F->n, F->Np_d,
+                                             F->Kph, dY, F->n, 0, rt->d_err, s)
+                          : (int)hipErrorInvalidValue;
+    if (f == (int)hipErrorInvalidValue) {
+        e |= jtk_quant_rows(F->S, T, F->h, F->Sq, F->Kph, F->ss, NULL, rt->d_err, s);
+        if (ev) (void)hipEventRecord(ev[2], s);
+        e |= jtk_w8a8_gemm(F->Sq, F->Kph, F->ss, F->d_P, F->d_s, T, F->n, F->Np_d, F->Kph, dY,
+                           F->n, 0, rt->d_err, s);
+    } else {
+        if (ev) (void)hipEventRecord(ev[2], s);
+        e |= f;
+    }
     return e ? jt_rt_err(hipErrorLaunchFailure) : JT_OK;
 }
 
@@ -175,6 +185,22 @@ int jt_hip_ffn_fwd(jt_hip_ffn *F, const float *dX, float *dY, int T, void *strea
     int rc = ffn_reserve(F, T, 1);
     if (rc != JT_OK) return rc;
     hipStream_t s = stream ? (hipStream_t)stream : rt->stream;
+    if (T <= 16) {
+        /* decode: both GEMMs quantise their rows themselves (two launches) */
+        int e = jtk_w8a8_gemm_xq(dX, F->n, F->n, F->gu_P, F->gu_s, T, 2 * F->h, F->Np_gu,
+                                 F->Kpn, F->S, F->h, 1, rt->d_err, s);
+        if (e != (int)hipErrorInvalidValue) {
+            if (e) return jt_rt_err(hipErrorLaunchFailure);
+            e = jtk_w8a8_gemm_xq(F->S, F->h, F->h, F->d_P, F->d_s, T, F->n, F->Np_d, F->Kph,
+                                 dY, F->n, 0, rt->d_err, s);
+            if (e == (int)hipErrorInvalidValue) {
+                e = jtk_quant_rows(F->S, T, F->h, F->Sq, F->Kph, F->ss, NULL, rt->d_err, s);
+                e |= jtk_w8a8_gemm(F->Sq, F->Kph, F->ss, F->d_P, F->d_s, T, F->n, F->Np_d,
+                                   F->Kph, dY, F->n, 0, rt->d_err, s);
+            }
+            return e ? jt_rt_err(hipErrorLaunchFailure) : JT_OK;
+        }
+    }
     if (jtk_quant_rows(dX, T, F->n, F->Xq, F->Kpn, F->sx, NULL, rt->d_err, s))
         return jt_rt_err(hipErrorLaunchFailure);
     return ffn_run_q(rt, F, F->Xq, F->sx, T, dY, s, NULL);

@@ -33,30 +33,124 @@
 #define SK_WAVES 16
 #define SK_UNROLL 4
 
-template <int EPI, int NP>
+//
+// QA (quantised activations made here): A is fp32 X [M][lda] with K valid
+// columns. Every block first issues its weight loads, then quantises the M
+// rows into LDS with the row quantiser's arithmetic (wave m on row m: the
+// same scale and codes as k_quant_rows) and reads its A fragments from
+// there, so a decode-sized expert needs no separate quantiser launch. The
+// rows are re-quantised by every block; at M <= 16 that is at most 16 * K
+// floats read from L2 per block.
+template <int EPI, int NP, int QV>  // QV > 0: QA with K <= 256 * QV
 __global__ __launch_bounds__(64 * SK_WAVES) void k_w8a8_skinny(
-    const int8_t *__restrict__ A, int lda, const float *__restrict__ sA,
-    const int8_t *__restrict__ Wp, const float *__restrict__ sB, int M, int N, int Kp,
+    const void *__restrict__ Ain, int lda, const float *__restrict__ sAin,
+    const int8_t *__restrict__ Wp, const float *__restrict__ sB, int M, int N, int Kp, int K,
     float *__restrict__ C, int ldc, uint32_t *err) {
     __shared__ v4i red[SK_WAVES][NP][64];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    extern __shared__ __attribute__((aligned(16))) int8_t sk_aq[];  // QA: [16][Kp + 16]
+    __shared__ float sk_sa[16];
+    constexpr bool QA = QV > 0;
+    constexpr int NV = QA ? QV : 1;
+    const int tid = threadIdx.x, lane = tid & 63;
+    // wave-uniform in a scalar register: guards on it then branch, which
+    // matters because v_mfma ignores EXEC (an exec-masked MFMA still runs)
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int KB = Kp / 64;
     const int p0 = blockIdx.x * NP;
     const int row = lane & 15, kc = lane >> 4;
-    const int8_t *arow = A + (int64_t)min(row, M - 1) * lda + kc * 16;
+    const int astr = Kp + 16;
+    const int8_t *arow = QA ? sk_aq + row * astr + kc * 16
+                            : (const int8_t *)Ain + (int64_t)min(row, M - 1) * lda + kc * 16;
+    const float *sA = QA ? sk_sa : sAin;
     v4i acc[NP];
 #pragma unroll
     for (int q = 0; q < NP; q++) acc[q] = (v4i){0, 0, 0, 0};
-    for (int kb0 = wave; kb0 < KB; kb0 += SK_WAVES * SK_UNROLL) {
-        v4i a[SK_UNROLL], b[SK_UNROLL][NP];
+    v4i b0[SK_UNROLL][NP];  // QA: the first round's weights, loaded before the rows
+    if (QA) {
+        const int kb0 = wave;
 #pragma unroll
         for (int u = 0; u < SK_UNROLL; u++) {
             const int kb = kb0 + u * SK_WAVES;
             if (kb < KB) {
 #pragma unroll
                 for (int q = 0; q < NP; q++)
-                    b[u][q] = *(const v4i *)(Wp + ((int64_t)(p0 + q) * KB + kb) * 1024 +
-                                             lane * 16);
+                    b0[u][q] = *(const v4i *)(Wp + ((int64_t)(p0 + q) * KB + kb) * 1024 +
+                                              lane * 16);
+            }
+        }
+        uint32_t flags = 0;
+        if (wave < M) {  // row `wave`: k_quant_rows's scale and codes
+            // (K % 4 == 0, K <= 256 * QV, 16-byte aligned rows: checked at launch)
+            const float4 *x4 = (const float4 *)((const float *)Ain + (int64_t)wave * lda);
+            const int n4 = K >> 2;
+            float4 v[NV];
+#pragma unroll
+            for (int j = 0; j < NV; j++) {
+                const int c = lane + 64 * j;
+                v[j] = c < n4 ? x4[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+            uint32_t mu = 0;
+#pragma unroll
+            for (int j = 0; j < NV; j++)
+                if (64 * j < n4) {
+                    mu = max(mu, max(abs_bits(v[j].x), abs_bits(v[j].y)));
+                    mu = max(mu, max(abs_bits(v[j].z), abs_bits(v[j].w)));
+                }
+            mu = wave_max_u(mu);
+            const QuantParams qp = quant_params(__builtin_bit_cast(float, mu));
+            uint32_t *qr = (uint32_t *)(sk_aq + wave * astr);
+            for (int c = n4 + lane; c < Kp / 4; c += 64) qr[c] = 0;  // K padding
+            if (mu >= 0x7f800000u || !qp.ok) {
+                flags = mu >= 0x7f800000u ? EF_NONFINITE_INPUT : EF_RANGE;
+            } else {
+                const float inv = quant_inv_f(qp.scale_d);
+                uint32_t fmask = 0;  // bit j: a code of v[j] needs the exact quotient
+#pragma unroll
+                for (int j = 0; j < NV; j++) {
+                    const int c = lane + 64 * j;
+                    if (64 * j < n4) {
+                        bool f = false;
+                        const uint32_t q0 = (uint8_t)quant_code_try(v[j].x, inv, f);
+                        const uint32_t q1 = (uint8_t)quant_code_try(v[j].y, inv, f);
+                        const uint32_t q2 = (uint8_t)quant_code_try(v[j].z, inv, f);
+                        const uint32_t q3 = (uint8_t)quant_code_try(v[j].w, inv, f);
+                        fmask |= (uint32_t)f << j;
+                        if (c < n4) qr[c] = q0 | (q1 << 8) | (q2 << 16) | (q3 << 24);
+                    }
+                }
+                while (fmask) {  // rare: redo those words exactly
+                    const int j = __builtin_ctz(fmask);
+                    fmask &= fmask - 1;
+                    float4 u = v[0];
+#pragma unroll
+                    for (int i = 1; i < NV; i++)
+                        if (i == j) u = v[i];
+                    qr[lane + 64 * j] = (uint32_t)(uint8_t)quant_code(u.x, qp.scale_d) |
+                                        ((uint32_t)(uint8_t)quant_code(u.y, qp.scale_d) << 8) |
+                                        ((uint32_t)(uint8_t)quant_code(u.z, qp.scale_d) << 16) |
+                                        ((uint32_t)(uint8_t)quant_code(u.w, qp.scale_d) << 24);
+                }
+            }
+            if (lane == 0) sk_sa[wave] = qp.scale_f;
+        }
+        if (flags && lane == 0 && blockIdx.x == 0) raise_err(err, flags);
+        __syncthreads();
+    }
+    for (int kb0 = wave; kb0 < KB; kb0 += SK_WAVES * SK_UNROLL) {
+        v4i a[SK_UNROLL], b[SK_UNROLL][NP];
+#pragma unroll
+        for (int u = 0; u < SK_UNROLL; u++) {
+            const int kb = kb0 + u * SK_WAVES;
+            if (kb < KB) {
+                if (QA && kb0 == wave) {
+#pragma unroll
+                    for (int q = 0; q < NP; q++) b[u][q] = b0[u][q];
+                } else {
+#pragma unroll
+                    for (int q = 0; q < NP; q++)
+                        b[u][q] = *(const v4i *)(Wp + ((int64_t)(p0 + q) * KB + kb) * 1024 +
+                                                 lane * 16);
+                }
                 a[u] = *(const v4i *)(arow + kb * 64);
             }
         }
@@ -117,19 +211,74 @@ __global__ __launch_bounds__(64 * SK_WAVES) void k_w8a8_skinny(
     if (badmid) raise_err(err, EF_NONFINITE_MID);
 }
 
+template <int QV>
+static hipError_t launch_skinny_xq(const float *X, int ldx, int K, const int8_t *Wp,
+                                   const float *sB, int M, int N, int Np, int Kp, float *C,
+                                   int ldc, int swiglu, uint32_t *err, hipStream_t s) {
+    const size_t lds = (size_t)16 * (Kp + 16);
+    static bool attr_set[64];
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    if (!attr_set[dev]) {
+        if constexpr (QV <= 12)
+            e = hipFuncSetAttribute((const void *)k_w8a8_skinny<EPI_SWIGLU, 2, QV>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute((const void *)k_w8a8_skinny<EPI_PLAIN, 1, QV>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
+        if (e != hipSuccess) return e;
+        attr_set[dev] = true;
+    }
+    if (swiglu) {
+        // (the SwiGLU epilogue and 16 float4 per lane do not fit 128 VGPRs)
+        if constexpr (QV <= 12)
+            hipLaunchKernelGGL((k_w8a8_skinny<EPI_SWIGLU, 2, QV>), dim3((unsigned)(Np / 32)),
+                               dim3(64 * SK_WAVES), lds, s, (const void *)X, ldx,
+                               (const float *)NULL, Wp, sB, M, N, Kp, K, C, ldc, err);
+        else
+            return hipErrorInvalidValue;
+    } else
+        hipLaunchKernelGGL((k_w8a8_skinny<EPI_PLAIN, 1, QV>), dim3((unsigned)(Np / 16)),
+                           dim3(64 * SK_WAVES), lds, s, (const void *)X, ldx, (const float *)NULL,
+                           Wp, sB, M, N, Kp, K, C, ldc, err);
+    return hipGetLastError();
+}
+
+extern "C" int jtk_w8a8_gemm_xq(const float *X, int ldx, int K, const int8_t *Wp,
+                                const float *sB, int M, int N, int Np, int Kp, float *C, int ldc,
+                                int swiglu, uint32_t *err, hipStream_t s) {
+    if (M <= 0) return 0;
+    if (M > 16 || K <= 0 || K > Kp || Kp % 64 || K % 4 || K > 4096 || ldx % 4 ||
+        ((uintptr_t)X & 15) || (size_t)16 * (Kp + 16) > 96 * 1024)
+        return (int)hipErrorInvalidValue;
+    const int nv = (K + 255) / 256;  // float4 per lane of a row
+    hipError_t e;
+    if (nv <= 4)
+        e = launch_skinny_xq<4>(X, ldx, K, Wp, sB, M, N, Np, Kp, C, ldc, swiglu, err, s);
+    else if (nv <= 8)
+        e = launch_skinny_xq<8>(X, ldx, K, Wp, sB, M, N, Np, Kp, C, ldc, swiglu, err, s);
+    else if (nv <= 12)
+        e = launch_skinny_xq<12>(X, ldx, K, Wp, sB, M, N, Np, Kp, C, ldc, swiglu, err, s);
+    else
+        e = launch_skinny_xq<16>(X, ldx, K, Wp, sB, M, N, Np, Kp, C, ldc, swiglu, err, s);
+    return (int)e;
+}
+
 extern "C" int jtk_w8a8_gemm(const int8_t *A, int lda, const float *sA, const int8_t *Wp,
                              const float *sB, int M, int N, int Np, int Kp, float *C,
                              int ldc, int swiglu, uint32_t *err, hipStream_t s) {
     if (M <= 0) return 0;
     if (M <= 16) {
         if (swiglu)
-            hipLaunchKernelGGL((k_w8a8_skinny<EPI_SWIGLU, 2>), dim3((unsigned)(Np / 32)),
-                               dim3(64 * SK_WAVES), 0, s, A, lda, sA, Wp, sB, M, N, Kp, C, ldc,
-                               err);
+            hipLaunchKernelGGL((k_w8a8_skinny<EPI_SWIGLU, 2, 0>), dim3((unsigned)(Np / 32)),
+                               dim3(64 * SK_WAVES), 0, s, (const void *)A, lda, sA, Wp, sB, M, N,
+                               Kp, Kp, C, ldc, err);
         else
-            hipLaunchKernelGGL((k_w8a8_skinny<EPI_PLAIN, 1>), dim3((unsigned)(Np / 16)),
-                               dim3(64 * SK_WAVES), 0, s, A, lda, sA, Wp, sB, M, N, Kp, C, ldc,
-                               err);
+            hipLaunchKernelGGL((k_w8a8_skinny<EPI_PLAIN, 1, 0>), dim3((unsigned)(Np / 16)),
+                               dim3(64 * SK_WAVES), 0, s, (const void *)A, lda, sA, Wp, sB, M, N,
+                               Kp, Kp, C, ldc, err);
     } else {
         // Tile choice (measured on MI355X): few 128x128 tiles -> 8 waves per
         // block with an intra-block k-split; otherwise 128 x 256 tiles of
@@ -526,7 +675,10 @@ __global__ __launch_bounds__(1024) void k_lowbit_skinny(
     const int tile = blockIdx.y;  // x walks the channel groups of a tile first
     if (tile >= *ntiles) return;
     const int G = K / 64;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    // wave-uniform in a scalar register: guards on it then branch, which
+    // matters because v_mfma ignores EXEC (an exec-masked MFMA still runs)
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nw = blockDim.x >> 6;
     const int gpw = G < 4 ? G : 4;
     const int g0 = wave * gpw;

@@ -178,7 +178,10 @@ __global__ __launch_bounds__(64 * WGM * WGN * KS) void k_w8a8_tile(
     static_assert(EPI != EPI_SWIGLU || TN % 2 == 0, "gate/up pairs need even TN");
     extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    // wave-uniform in a scalar register: guards on it then branch, which
+    // matters because v_mfma ignores EXEC (an exec-masked MFMA still runs)
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wg = wave % NWG, kg = wave / NWG;
     const int total = mtiles * ntiles;
     int pid = blockIdx.x;

@@ -39,6 +39,13 @@ int jtk_quant_weight_rows(const float *W, int64_t ld_n, int64_t ld_k, int N, int
 int jtk_w8a8_gemm(const int8_t *A, int lda, const float *sA, const int8_t *Wp,
                   const float *sB, int M, int N, int Np, int Kp, float *C, int ldc,
                   int swiglu, uint32_t *err, hipStream_t s);
+/* M <= 16 on fp32 activations X [M][ldx] (K valid columns): each block
+ * quantises the rows itself with the row quantiser's arithmetic.
+ * hipErrorInvalidValue (nothing launched) unless K % 4 == 0, K <= 4096
+ * (3072 with SwiGLU), ldx % 4 == 0 and X is 16-byte aligned */
+int jtk_w8a8_gemm_xq(const float *X, int ldx, int K, const int8_t *Wp, const float *sB, int M,
+                     int N, int Np, int Kp, float *C, int ldc, int swiglu, uint32_t *err,
+                     hipStream_t s);
 /* rows_per_tile 64 (batches) or 16 (few rows per expert) */
 int jtk_lowbit_grouped(int bits, const int8_t *A, int lda, const float *sA,
                        const int32_t *perm, const int32_t *off, int topk,

@@ -185,7 +185,8 @@ __global__ __launch_bounds__(256) void k_router_approx(
     const double2 *__restrict__ xinfo, const int8_t *__restrict__ Wh,
     const int8_t *__restrict__ Wl, const double2 *__restrict__ winfo, int T, int E,
     double *__restrict__ approx) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: MFMA guards branch
     const int t0 = blockIdx.x * 64 + wave * 16, e0 = blockIdx.y * 64;
     const int KB = n / 64;
     const int r = lane & 15, kc = lane >> 4;
@@ -257,7 +258,8 @@ __global__ __launch_bounds__(64 * RA_W) void k_router_approx_small(
     const int8_t *__restrict__ Wl, const double2 *__restrict__ winfo, int T, int E,
     double *__restrict__ approx) {
     __shared__ v4i part[RA_W][3][64];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: MFMA guards branch
     const int t0 = blockIdx.x * 16, pan = blockIdx.y;
     const int KB = n / 64;
     const int r = lane & 15, kc = lane >> 4;

@@ -183,3 +183,43 @@ def test_ffn_shared_expert_parity(jt, orc, torch_cuda, M):
     rc, Y2 = orc.ffn_fwd(Wg, Wu, Wd, X)
     assert rc == 0
     close(dY.cpu().numpy(), Y2)
+
+
+@pytest.mark.parametrize("n,h,M", [(256, 128, 3), (768, 3072, 16), (4096, 64, 2)],
+                         ids=["n256", "h3072", "n4096_fallback"])
+def test_ffn_decode_widths(jt, orc, torch_cuda, n, h, M):
+    """Decode-sized experts quantise their activation rows inside the GEMMs
+    (K <= 3072 with SwiGLU, <= 4096 plain); wider rows fall back to the
+    separate quantiser. Same codes either way, so the same outputs."""
+    torch = torch_cuda
+    announce(f"ffn decode n={n} h={h} M={M}")
+    rng = np.random.default_rng(n + h + M)
+    Wg = (rng.standard_normal((h, n)) / np.sqrt(n)).astype(np.float32)
+    Wu = (rng.standard_normal((h, n)) / np.sqrt(n)).astype(np.float32)
+    Wd = (rng.standard_normal((h, n)) / np.sqrt(h)).astype(np.float32)
+    X = rng.standard_normal((M, n)).astype(np.float32)
+    if M > 1:
+        X[1] = 0.0                     # zero row: scale 1, codes 0
+    F = jt.FFN(dev(torch, Wg), dev(torch, Wu), dev(torch, Wd))
+    dY = torch.zeros((M, n), dtype=torch.float32, device="cuda")
+    F.fwd(dev(torch, X), dY)
+    assert jt.sync_errors() == 0
+    rc, Y2 = orc.ffn_fwd(Wg, Wu, Wd, X)
+    assert rc == 0
+    close(dY.cpu().numpy(), Y2)
+
+
+def test_ffn_decode_nonfinite_row(jt, torch_cuda):
+    """A NaN in a decode activation row is reported (the reference's
+    quantiser rejects non-finite input)."""
+    torch = torch_cuda
+    announce("ffn decode non-finite row")
+    n, h = 256, 128
+    rng = np.random.default_rng(7)
+    W = [(rng.standard_normal((h, n)) / 16).astype(np.float32) for _ in range(3)]
+    F = jt.FFN(*(dev(torch, w) for w in W))
+    X = rng.standard_normal((4, n)).astype(np.float32)
+    X[2, 5] = np.nan
+    dY = torch.zeros((4, n), dtype=torch.float32, device="cuda")
+    F.fwd(dev(torch, X), dY)
+    assert jt.sync_errors() & 0x1  # JT_HIP_EF_NONFINITE_INPUT
