@@ -177,16 +177,21 @@ extern "C" int jtk_router_codes(const float *X, int rows, int n, int8_t *qh, int
 }
 
 // ---- 2. approximate logits ----
-// Block = 64 tokens x 64 experts, 4 waves of 16 tokens; per 64-K block a
+// Block = 64 tokens x 64 experts, 8 waves: 4 waves of 16 tokens times 2
+// k-halves (wave group g takes the k-blocks of parity g); per 64-K block a
 // wave loads its 2 A fragments and 8 panels (hi/lo of 4 expert panels) one
-// block ahead, then runs 16 MFMAs into three int32 sums per 16x16 tile.
-__global__ __launch_bounds__(256) void k_router_approx(
+// block ahead, then runs 16 MFMAs into three int32 sums per 16x16 tile. The
+// second group's int32 sums are added to the first's through LDS (exact).
+// Two waves per SIMD instead of one hide the load latency of the k chain.
+__global__ __launch_bounds__(512) void k_router_approx(
     const int8_t *__restrict__ Xh, const int8_t *__restrict__ Xl, int n,
     const double2 *__restrict__ xinfo, const int8_t *__restrict__ Wh,
     const int8_t *__restrict__ Wl, const double2 *__restrict__ winfo, int T, int E,
     double *__restrict__ approx) {
+    __shared__ v4i part[4][3][4][64];  // group 1's sums: [token wave][hh|mid|ll][j]
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: MFMA guards branch
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: MFMA guards branch
+    const int wave = wv & 3, kg = wv >> 2;
     const int t0 = blockIdx.x * 64 + wave * 16, e0 = blockIdx.y * 64;
     const int KB = n / 64;
     const int r = lane & 15, kc = lane >> 4;
@@ -219,15 +224,32 @@ __global__ __launch_bounds__(256) void k_router_approx(
             ll[j] = mfma16x16x64(f.al, f.bl[j], ll[j]);
         }
     };
-    // the next k-block's fragments load while the current one is summed
+    // the next k-block's fragments load while the current one is summed;
+    // this group's k-blocks are kg, kg + 2, kg + 4, ...
     Frag fa, fb;
-    load(0, fa);
-    for (int kb = 0; kb < KB; kb += 2) {
-        if (kb + 1 < KB) load(kb + 1, fb);
+    if (kg < KB) load(kg, fa);
+    for (int kb = kg; kb < KB; kb += 4) {
+        if (kb + 2 < KB) load(kb + 2, fb);
         mma(fa);
-        if (kb + 1 >= KB) break;
-        if (kb + 2 < KB) load(kb + 2, fa);
+        if (kb + 2 >= KB) break;
+        if (kb + 4 < KB) load(kb + 4, fa);
         mma(fb);
+    }
+    if (kg == 1) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            part[wave][0][j][lane] = hh[j];
+            part[wave][1][j][lane] = mid[j];
+            part[wave][2][j][lane] = ll[j];
+        }
+    }
+    __syncthreads();
+    if (kg == 1) return;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        hh[j] += part[wave][0][j][lane];
+        mid[j] += part[wave][1][j][lane];
+        ll[j] += part[wave][2][j][lane];
     }
     const int lr = (lane >> 4) * 4, lc = lane & 15;
 #pragma unroll
@@ -324,7 +346,7 @@ extern "C" int jtk_router_approx(const int8_t *Xh, const int8_t *Xl, int n, cons
         return (int)hipGetLastError();
     }
     dim3 grid((unsigned)((T + 63) / 64), (unsigned)((E + 63) / 64));
-    hipLaunchKernelGGL(k_router_approx, grid, dim3(256), 0, s, Xh, Xl, n,
+    hipLaunchKernelGGL(k_router_approx, grid, dim3(512), 0, s, Xh, Xl, n,
                        (const double2 *)xinfo, Wh, Wl, (const double2 *)winfo, T, E, approx);
     return (int)hipGetLastError();
 }
