@@ -15,7 +15,7 @@ The JSON line carries, beside the contract fields:
   cpu_baseline -- the reference CPU kernels (oracle/_ref, built from the
                   reference sources) timed on a bounded token sample on this
                   host, or the oracle restatement when _ref is absent;
-  sub          -- the other BASELINE shapes: W8A8 GEMM 64x1024x1024,
+  sub          -- the other benchmark shapes: W8A8 GEMM 64x1024x1024,
                   shared-expert decode M in {1,4,16}, routed decode T=16,
                   the full decode layer at T=16 and the E=512 stress
                   grouped GEMM.
@@ -88,8 +88,9 @@ def time_fn(torch, fn, steps, warmup, stream):
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one MI355X: this build has no multi-GPU path "
-              "(see the sharding notes in DESIGN.md); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one MI355X: there is no multi-GPU path "
+              "(tokens and experts would shard across GPUs, not built here); "
+              "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     import numpy as np
     import torch
