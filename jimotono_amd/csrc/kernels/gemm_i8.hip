@@ -65,8 +65,22 @@ __global__ __launch_bounds__(64 * SK_WAVES) void k_w8a8_skinny(
     v4i acc[NP];
 #pragma unroll
     for (int q = 0; q < NP; q++) acc[q] = (v4i){0, 0, 0, 0};
-    v4i b0[SK_UNROLL][NP];  // QA: the first round's weights, loaded before the rows
+    v4i b0[SK_UNROLL][NP];  // QA: the first round's weights
     if (QA) {
+        // the row loads go first: they are L2 hits and the quantiser needs
+        // them, while the weights stream in behind them (loads return in
+        // issue order, so the wait for the rows does not wait for weights)
+        const int n4 = K >> 2;
+        float4 v[NV];
+        if (wave < M) {
+            // (K % 4 == 0, K <= 256 * QV, 16-byte aligned rows: checked at launch)
+            const float4 *x4 = (const float4 *)((const float *)Ain + (int64_t)wave * lda);
+#pragma unroll
+            for (int j = 0; j < NV; j++) {
+                const int c = lane + 64 * j;
+                v[j] = c < n4 ? x4[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
         const int kb0 = wave;
 #pragma unroll
         for (int u = 0; u < SK_UNROLL; u++) {
@@ -80,15 +94,6 @@ __global__ __launch_bounds__(64 * SK_WAVES) void k_w8a8_skinny(
         }
         uint32_t flags = 0;
         if (wave < M) {  // row `wave`: k_quant_rows's scale and codes
-            // (K % 4 == 0, K <= 256 * QV, 16-byte aligned rows: checked at launch)
-            const float4 *x4 = (const float4 *)((const float *)Ain + (int64_t)wave * lda);
-            const int n4 = K >> 2;
-            float4 v[NV];
-#pragma unroll
-            for (int j = 0; j < NV; j++) {
-                const int c = lane + 64 * j;
-                v[j] = c < n4 ? x4[c] : make_float4(0.f, 0.f, 0.f, 0.f);
-            }
             uint32_t mu = 0;
 #pragma unroll
             for (int j = 0; j < NV; j++)
