@@ -145,6 +145,24 @@ def test_layer_decode_fused_zipf(jt, orc, torch_cuda, T):
     close(Y, o["Y"])
 
 
+@pytest.mark.parametrize("T", [16, 700])
+def test_layer_stress_widths_zipf(jt, orc, torch_cuda, T):
+    """The stress shape's widths (d=2048, f=512, k=8; 128 of its 512 experts
+    to keep the oracle's weight preparation short) under Zipf(1.1) routing
+    at a decode and a small prefill batch (16-row and 64-row tiles)."""
+    torch = torch_cuda
+    n, h, E, k, S, hs = 2048, 512, 128, 8, 0, 0
+    announce(f"moe layer stress widths zipf T={T}")
+    rng = np.random.default_rng(2048 + T)
+    W = mk_weights(rng, n, h, E, S, hs)
+    X = rng.standard_normal((T, n)).astype(np.float32)
+    ids, w = zipf_ids(rng, T, k, E)
+    L, Y = run_layer(jt, torch, n, h, E, k, S, hs, T, W, X, ids, w)
+    o = orc.moe_q(n, h, E, k, S, hs, None, W[1], W[2], W[3], *W[4]).fwd(X, ids, w)
+    assert o["rc"] == 0
+    close(Y, o["Y"])
+
+
 def test_layer_full_size_token_sample(jt, orc, torch_cuda):
     """Full-layer prefill shape (T=4096, d=1024, E=256, f=256, k=8, two shared
     f=2816 experts). Tokens are independent in the dropless layer, so the
