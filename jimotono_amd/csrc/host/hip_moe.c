@@ -558,11 +558,23 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
         prof_mark(L, slot, ST_R_QUANT, s);
         prof_mark(L, slot, ST_R_DOWN, s);
     } else {
-        le |= jtk_lowbit_grouped(2, L->Xq, n, L->sx, L->perm, L->off, k, L->tiles, L->ntiles,
-                                 max_tiles, R, L->gu_P, L->gu_S, L->gu_pstride, L->gu_sstride,
-                                 2 * h, n, L->Sr, h, err, s);
-        prof_mark(L, slot, ST_R_QUANT, s);
-        le |= jtk_quant_rows(L->Sr, Tk, h, L->Sqr, h, L->ssr, NULL, err, s);
+        /* 64-row tiles with f = 256 or 512: the gate/up launch also writes
+         * the hidden rows' int8 codes (timed as routed_gateup) */
+        const int gq = R == 64 ? jtk_lowbit_gateup_q(L->Xq, n, L->sx, L->perm, k, L->tiles,
+                                                     L->ntiles, max_tiles, L->gu_P, L->gu_S,
+                                                     L->gu_pstride, L->gu_sstride, n, L->Sqr,
+                                                     L->ssr, h, err, s)
+                               : (int)hipErrorInvalidValue;
+        if (gq == (int)hipErrorInvalidValue) {
+            le |= jtk_lowbit_grouped(2, L->Xq, n, L->sx, L->perm, L->off, k, L->tiles,
+                                     L->ntiles, max_tiles, R, L->gu_P, L->gu_S, L->gu_pstride,
+                                     L->gu_sstride, 2 * h, n, L->Sr, h, err, s);
+            prof_mark(L, slot, ST_R_QUANT, s);
+            le |= jtk_quant_rows(L->Sr, Tk, h, L->Sqr, h, L->ssr, NULL, err, s);
+        } else {
+            le |= gq;
+            prof_mark(L, slot, ST_R_QUANT, s);
+        }
         prof_mark(L, slot, ST_R_DOWN, s);
         le |= jtk_lowbit_grouped(4, L->Sqr, h, L->ssr, L->perm, L->off, k, L->tiles, L->ntiles,
                                  max_tiles, R, L->dn_P, L->dn_S, L->dn_pstride, L->dn_sstride, n,

@@ -328,6 +328,9 @@ __device__ __forceinline__ float f16_to_f32(uint16_t h) {
 #ifndef LB_STAGES
 #define LB_STAGES 2  // measured on MI355X: 2 stages beat 3-7 (more blocks resident)
 #endif
+#ifndef LB_GQ_PPW
+#define LB_GQ_PPW 4  // fused gate/up at f = 256: 8 waves of 4 panels (measured: beats 16 of 2)
+#endif
 
 template <int BITS, int EPI, int NST>
 __global__ __launch_bounds__(256, 2) void k_lowbit_grouped(
@@ -483,6 +486,185 @@ __global__ __launch_bounds__(256, 2) void k_lowbit_grouped(
     }
     if (bad) raise_err(err, EF_RANGE);
     if (badmid) raise_err(err, EF_NONFINITE_MID);
+}
+
+// ============ routed gate/up + SwiGLU + row codes, 64-row tiles ============
+// A block covers all 2f gate/up channels of one (expert, 64-row) tile, so
+// the SwiGLU rows are complete inside the block and leave it as int8 codes:
+// no fp32 hidden rows in memory and no separate quantiser launch. NW waves
+// of PPW panels each (NW * PPW = 2f/16); wave w owns panels PPW*w ..
+// PPW*w+PPW-1, i.e. PPW/2 gate/up pairs (2j, 2j+1). One two-stage ring slot
+// per 64-K group holds the 4 gathered A panels (waves 0-3 copy one each),
+// every wave's INT2 panel-groups and its fp16 scales. The folds are k_lowbit_grouped's. Epilogue: SwiGLU, the
+// row max |h| (DPP over a panel's 16 channels, then LDS over the waves), the
+// row quantiser's parameters once per row, and the codes of
+// k_quant_rows written straight to Sq with the scale to ss.
+template <int NW, int PPW>
+__global__ __launch_bounds__(64 * NW) void k_lowbit_gu_q(
+    const int8_t *__restrict__ A, int lda, const float *__restrict__ sA,
+    const int32_t *__restrict__ perm, int topk, const int32_t *__restrict__ tiles,
+    const int32_t *__restrict__ ntiles, const uint8_t *__restrict__ Wp,
+    const uint16_t *__restrict__ Ws, int64_t wp_stride, int64_t ws_stride, int K,
+    int8_t *__restrict__ Sq, float *__restrict__ ss, int h, uint32_t *err) {
+    constexpr int PB = 256;                     // INT2 bytes per panel-group
+    constexpr int SOFF = 4096 + NW * PPW * PB;  // scales after A and weights
+    constexpr int NJ = PPW / 2;                 // gate/up pairs per wave
+    constexpr int STAGE = SOFF + NW * 256;      // one 256-byte scale slot per wave
+    extern __shared__ __attribute__((aligned(1024))) int8_t smem[];  // 2 * STAGE
+    __shared__ int rowsrc[64];
+    __shared__ float rowscale[64];
+    __shared__ uint32_t pmax[NW][64];
+    __shared__ double rsd[64];
+    __shared__ float rinv[64];
+    __shared__ uint32_t rbad[64];
+    const int tile = blockIdx.x;
+    if (tile >= *ntiles) return;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int4 td = ((const int4 *)tiles)[tile];  // {expert, first sorted row, rows}
+    const int e = td.x, pos0 = td.y, nrows = td.z;
+    if (tid < 64) {
+        const int src = perm[pos0 + min(tid, nrows - 1)] / topk;
+        rowsrc[tid] = src;
+        rowscale[tid] = sA[src];
+    }
+    __syncthreads();
+    const int G = K / 64;
+    const int8_t *a_src =
+        A + (int64_t)rowsrc[(wave & 3) * 16 + (lane & 15)] * lda + (lane >> 4) * 16;
+    const int pan0 = PPW * wave;  // this wave's first panel within the expert
+    const uint8_t *wb = Wp + (int64_t)e * wp_stride + (int64_t)pan0 * G * PB;
+    const uint8_t *sbase =
+        (const uint8_t *)(Ws + (int64_t)e * ws_stride + (int64_t)pan0 * G * 16);
+    // scales: lanes 0..8*PPW-1 copy panel l >> 3's 16 values, 2 per lane;
+    // the other lanes repeat them (the 4-byte DMA always writes 64 lanes)
+    const int sl = lane & (8 * PPW - 1);
+    const int s_off = (sl >> 3) * G * 32 + (sl & 7) * 4;
+    auto issue = [&](int g) {
+        int8_t *st = smem + (g & 1) * STAGE;
+        if (wave < 4) dma<16>(a_src + (int64_t)g * 64, st + wave * 1024);
+#pragma unroll
+        for (int q = 0; q < PPW; q++)
+            dma<4>(wb + ((int64_t)q * G + g) * PB + lane * 4,
+                   st + 4096 + (PPW * wave + q) * PB);
+        dma<4>(sbase + (int64_t)g * 32 + s_off, st + SOFF + wave * 256);
+    };
+    issue(0);
+    float T[4][PPW][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int q = 0; q < PPW; q++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) T[i][q][r] = 0.0f;
+    for (int g = 0; g < G; g++) {
+        wait_vm<0>();   // this wave's copies of stage g (the only ones in flight)
+        barrier_lds();  // ... and every other wave's; stage g-1 is free
+        if (g + 1 < G) issue(g + 1);
+        const int8_t *st = smem + (g & 1) * STAGE;
+        const uint16_t *s16 = (const uint16_t *)(st + SOFF + wave * 256);
+        float sc[PPW];
+        v4i b[PPW];
+#pragma unroll
+        for (int q = 0; q < PPW; q++) {
+            sc[q] = f16_to_f32(s16[q * 16 + (lane & 15)]);
+            b[q] = unpack_int2(
+                *(const uint32_t *)(st + 4096 + (PPW * wave + q) * PB + lane * 4));
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            if (16 * i >= nrows) continue;  // wave-uniform: padding rows of a short tile
+            const v4i af = *(const v4i *)(st + i * 1024 + lane * 16);
+#pragma unroll
+            for (int q = 0; q < PPW; q++) {
+                const v4i c = mfma16x16x64(af, b[q], (v4i){0, 0, 0, 0});
+#pragma unroll
+                for (int r = 0; r < 4; r++) T[i][q][r] = __builtin_fmaf((float)c[r], sc[q], T[i][q][r]);
+            }
+        }
+    }
+    // ---- SwiGLU of rows 16i + 4(l/16) + r, hidden channels (NJ w + jj)*16 + l%16 ----
+    const int lr = (lane >> 4) * 4, lc = lane & 15;
+    uint32_t flags = 0;
+    float sv[4][NJ][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int rr = 16 * i + lr + r;
+            const float sa = rowscale[rr < nrows ? rr : 0];
+#pragma unroll
+            for (int jj = 0; jj < NJ; jj++) {
+                sv[i][jj][r] = 0.0f;
+                if (rr < nrows) {
+                    const float gv = T[i][2 * jj][r] * sa, uv = T[i][2 * jj + 1][r] * sa;
+                    if (!isfinite(gv) || !isfinite(uv)) flags |= EF_RANGE;
+                    if (!silu_mul(gv, uv, &sv[i][jj][r])) flags |= EF_NONFINITE_MID;
+                }
+            }
+            uint32_t m = 0;
+#pragma unroll
+            for (int jj = 0; jj < NJ; jj++) m = max(m, abs_bits(sv[i][jj][r]));
+            m = row16_allmax_u(m);  // over this wave's 16 * NJ channels of the row
+            if (lc == 0) pmax[wave][rr] = m;
+        }
+    __syncthreads();
+    // ---- the row quantiser's parameters, once per row ----
+    if (tid < 64) {
+        uint32_t mu = pmax[0][tid];
+#pragma unroll
+        for (int w = 1; w < NW; w++) mu = max(mu, pmax[w][tid]);
+        const QuantParams qp = quant_params(__builtin_bit_cast(float, mu));
+        const uint32_t bad = mu >= 0x7f800000u ? EF_NONFINITE_INPUT : (qp.ok ? 0u : EF_RANGE);
+        rsd[tid] = qp.scale_d;
+        rinv[tid] = quant_inv_f(qp.scale_d);
+        rbad[tid] = bad;
+        if (tid < nrows) {
+            ss[pos0 + tid] = qp.scale_f;
+            flags |= bad;
+        }
+    }
+    __syncthreads();
+    // ---- codes, straight to Sq [sorted row][h] ----
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int rr = 16 * i + lr + r;
+            if (rr >= nrows || rbad[rr]) continue;
+            const float inv = rinv[rr];
+            int8_t *qrow = Sq + (int64_t)(pos0 + rr) * h + NJ * wave * 16 + lc;
+#pragma unroll
+            for (int jj = 0; jj < NJ; jj++) {
+                bool f = false;
+                int q = quant_code_try(sv[i][jj][r], inv, f);
+                if (f) q = quant_code_call(sv[i][jj][r], rsd[rr]);
+                qrow[16 * jj] = (int8_t)q;
+            }
+        }
+    if (flags) raise_err(err, flags);
+}
+
+extern "C" int jtk_lowbit_gateup_q(const int8_t *A, int lda, const float *sA,
+                                   const int32_t *perm, int topk, const int32_t *tiles,
+                                   const int32_t *ntiles, int max_tiles, const uint8_t *Wp,
+                                   const uint16_t *Ws, int64_t wp_stride, int64_t ws_stride,
+                                   int K, int8_t *Sq, float *ss, int h, uint32_t *err,
+                                   hipStream_t s) {
+    if (max_tiles <= 0) return 0;
+    if (K % 64 || (h != 256 && h != 512)) return (int)hipErrorInvalidValue;
+    if (h == 256) {
+        constexpr int PPW = LB_GQ_PPW, NW = 32 / PPW, STAGE = 4096 + NW * PPW * 256 + NW * 256;
+        hipLaunchKernelGGL((k_lowbit_gu_q<NW, PPW>), dim3((unsigned)max_tiles), dim3(64 * NW),
+                           2 * STAGE, s, A, lda, sA, perm, topk, tiles, ntiles, Wp, Ws,
+                           wp_stride, ws_stride, K, Sq, ss, h, err);
+    } else {
+        constexpr int PPW = 4, NW = 16, STAGE = 4096 + NW * PPW * 256 + NW * 256;
+        hipLaunchKernelGGL((k_lowbit_gu_q<NW, PPW>), dim3((unsigned)max_tiles), dim3(64 * NW),
+                           2 * STAGE, s, A, lda, sA, perm, topk, tiles, ntiles, Wp, Ws,
+                           wp_stride, ws_stride, K, Sq, ss, h, err);
+    }
+    return (int)hipGetLastError();
 }
 
 // ===================== grouped low-bit GEMM, A tile resident =====================

@@ -62,6 +62,15 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
     const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
     return ((uint64_t)hi << 32) | lo;
 }
+// max over the 16 lanes of each DPP row, in every lane of the row (row
+// rotations 1, 2, 4, 8)
+__device__ __forceinline__ uint32_t row16_allmax_u(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x121, 0xf, 0xf, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x122, 0xf, 0xf, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x124, 0xf, 0xf, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x128, 0xf, 0xf, false));
+    return v;
+}
 __device__ __forceinline__ double readlane_f64(double v, int l) {
     const uint64_t b = __builtin_bit_cast(uint64_t, v);
     const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)b, l);
@@ -148,6 +157,10 @@ __device__ __forceinline__ int quant_code_try(float x, float inv_f, bool &fail) 
     const float q = rintf(y);
     fail |= !(fabsf(y - q) <= 0.4999f);
     return (int)__builtin_amdgcn_fmed3f(q, -127.0f, 127.0f);
+}
+// quant_code as a real call, for rare fallbacks inside unrolled code
+__device__ __attribute__((noinline)) int quant_code_call(float x, double scale_d) {
+    return quant_code(x, scale_d);
 }
 // inv_f for quant_code_fast: (float)(1/scale_d), 0 for an all-zero row
 __device__ __forceinline__ float quant_inv_f(double scale_d) {

@@ -46,6 +46,14 @@ int jtk_w8a8_gemm(const int8_t *A, int lda, const float *sA, const int8_t *Wp,
 int jtk_w8a8_gemm_xq(const float *X, int ldx, int K, const int8_t *Wp, const float *sB, int M,
                      int N, int Np, int Kp, float *C, int ldc, int swiglu, uint32_t *err,
                      hipStream_t s);
+/* 64-row tiles, f = h in {256, 512}: gate/up, SwiGLU and the row codes of
+ * the hidden rows in one launch (Sq [Tk][h] int8, ss [Tk]); hipErrorInvalidValue
+ * for other shapes */
+int jtk_lowbit_gateup_q(const int8_t *A, int lda, const float *sA, const int32_t *perm,
+                        int topk, const int32_t *tiles, const int32_t *ntiles, int max_tiles,
+                        const uint8_t *Wp, const uint16_t *Ws, int64_t wp_stride,
+                        int64_t ws_stride, int K, int8_t *Sq, float *ss, int h, uint32_t *err,
+                        hipStream_t s);
 /* rows_per_tile 64 (batches) or 16 (few rows per expert) */
 int jtk_lowbit_grouped(int bits, const int8_t *A, int lda, const float *sA,
                        const int32_t *perm, const int32_t *off, int topk,

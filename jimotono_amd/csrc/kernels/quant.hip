@@ -137,15 +137,6 @@ __global__ __launch_bounds__(256) void k_quant_rows(
 // loads in flight. The row maximum is an all-reduce over the 16 lanes with
 // DPP row rotations; the codes are k_quant_rows's.
 #define QS_MAXV 8  // float4 per lane: cols <= 512
-__device__ __forceinline__ uint32_t row16_allmax_u(uint32_t v) {
-#define QS_DPP(x, ctrl) (uint32_t) __builtin_amdgcn_update_dpp((int)(x), (int)(x), (ctrl), 0xf, 0xf, false)
-    v = max(v, QS_DPP(v, 0x121));  // row_ror:1
-    v = max(v, QS_DPP(v, 0x122));  // row_ror:2
-    v = max(v, QS_DPP(v, 0x124));  // row_ror:4
-    v = max(v, QS_DPP(v, 0x128));  // row_ror:8
-#undef QS_DPP
-    return v;
-}
 __global__ __launch_bounds__(256) void k_quant_rows16(const float *__restrict__ X, int64_t rows,
                                                       int cols, int8_t *__restrict__ Q,
                                                       int64_t ldq, float *__restrict__ scale,
