@@ -831,6 +831,117 @@ __global__ __launch_bounds__(256, 2) void k_lowbit_grouped_res(
     if (badmid) raise_err(err, EF_NONFINITE_MID);
 }
 
+// ============ routed down projection, weights in registers ============
+// 64-row tiles of the INT4 down projection (K = h = 64 * G). The A rows
+// are the tile's sorted hidden codes (contiguous rows pos0 .. pos0+nrows-1)
+// and output row r goes to out[perm[pos0 + r]]. Block = 4 waves; wave w
+// owns the CPW 16-channel panels starting at (4 * blockIdx.x + w) * CPW and
+// requests every raw INT4 panel group of them into registers at the start,
+// its fp16 group scales and one 16-row panel of the A tile by LDS-DMA, then
+// waits once: no per-group ring, so each block pays one memory latency.
+// The fold T = fmaf((float)acc_g, scale_g, T) runs in ascending g, the
+// arithmetic of k_lowbit_grouped_res, so the outputs are identical.
+template <int G, int CPW>
+__global__ __launch_bounds__(256) void k_lowbit_down_rr(
+    const int8_t *__restrict__ A, int lda, const float *__restrict__ sA,
+    const int32_t *__restrict__ perm, const int4 *__restrict__ tiles,
+    const int32_t *__restrict__ ntiles, const uint8_t *__restrict__ Wp,
+    const uint16_t *__restrict__ Ws, int64_t wp_stride, int64_t ws_stride,
+    float *__restrict__ out, int ldo, uint32_t *err) {
+    static_assert((CPW * G * 32) % 256 == 0, "scale copies of 256 bytes");
+    __shared__ __attribute__((aligned(1024))) int8_t atile[G * 4 * 1024];  // [g][panel][64 x 16 B]
+    __shared__ __attribute__((aligned(16))) uint16_t scl[4][CPW * G * 16];   // per wave [q][g][16]
+    __shared__ float rsc[64];
+    __shared__ int rdst[64];
+    const int tile = blockIdx.y;
+    if (tile >= *ntiles) return;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int4 td = tiles[tile];  // {expert, first sorted row, rows}
+    const int e = td.x, pos0 = td.y, nrows = td.z;
+    if (nrows <= 0) return;
+    // row scale and destination of row `lane` (wave 0), written to LDS later
+    float my_sa = 0.0f;
+    int my_dst = 0;
+    if (wave == 0) {
+        const int r = pos0 + min(lane, nrows - 1);
+        my_sa = sA[r];
+        my_dst = perm[r];
+    }
+    const int pan0 = (blockIdx.x * 4 + wave) * CPW;
+    const uint8_t *wb = Wp + (int64_t)e * wp_stride + (int64_t)pan0 * G * 512;
+    uint2 rw[CPW][G];
+#pragma unroll
+    for (int q = 0; q < CPW; q++)
+#pragma unroll
+        for (int g = 0; g < G; g++) rw[q][g] = *(const uint2 *)(wb + (q * G + g) * 512 + lane * 8);
+    const uint8_t *sb = (const uint8_t *)(Ws + (int64_t)e * ws_stride) + (int64_t)pan0 * G * 32;
+#pragma unroll
+    for (int c = 0; c < CPW * G * 32 / 256; c++)
+        dma<4>(sb + c * 256 + lane * 4, (char *)scl[wave] + c * 256);
+    if (16 * wave < nrows) {
+        const int row = min(16 * wave + (lane & 15), nrows - 1);
+        const int8_t *as = A + (int64_t)(pos0 + row) * lda + (lane >> 4) * 16;
+#pragma unroll
+        for (int g = 0; g < G; g++) dma<16>(as + g * 64, atile + (g * 4 + wave) * 1024);
+    }
+    wait_vm<0>();
+    if (wave == 0) {
+        rsc[lane] = my_sa;
+        rdst[lane] = my_dst;
+    }
+    lds_barrier();
+    const int lr = (lane >> 4) * 4, lc = lane & 15;
+    float T[4][CPW][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int q = 0; q < CPW; q++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) T[i][q][r] = 0.0f;
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        v4i b[CPW];
+        float sc[CPW];
+#pragma unroll
+        for (int q = 0; q < CPW; q++) {
+            b[q] = unpack_int4(rw[q][g].x, rw[q][g].y);
+            sc[q] = f16_to_f32(scl[wave][(q * G + g) * 16 + lc]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            if (16 * i >= nrows) continue;  // wave-uniform: padding rows of a short tile
+            const v4i af = *(const v4i *)(atile + (g * 4 + i) * 1024 + lane * 16);
+#pragma unroll
+            for (int q = 0; q < CPW; q++) {
+                const v4i c = mfma16x16x64(af, b[q], (v4i){0, 0, 0, 0});
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    T[i][q][r] = __builtin_fmaf((float)c[r], sc[q], T[i][q][r]);
+                    asm volatile("" : "+v"(T[i][q][r]));  // fold now, not after the loop
+                }
+            }
+        }
+    }
+    uint32_t bad = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int rr = 16 * i + lr + r;
+            if (rr >= nrows) continue;
+            const float sa = rsc[rr];
+            float *y = out + (int64_t)rdst[rr] * ldo + pan0 * 16 + lc;
+#pragma unroll
+            for (int q = 0; q < CPW; q++) {
+                const float f = T[i][q][r] * sa;
+                bad |= !isfinite(f);
+                y[16 * q] = f;
+            }
+        }
+    if (bad) raise_err(err, EF_RANGE);
+}
+
 // ===================== grouped low-bit GEMM, few rows per expert =====================
 // Decode-sized batches (a handful of rows per expert): work item = (expert
 // e, 16 sorted rows) x 64 packed channels (4 panels). A block has
@@ -1014,11 +1125,6 @@ static hipError_t launch_lowbit_skinny(dim3 grid, int G, hipStream_t s, const in
 #define RF_WAVES 16
 #define RF_HSTR (RF_H + 4)   // fp32 gate/up row stride (floats)
 #define RF_QSTR (RF_H + 16)  // int8 h row stride (bytes)
-
-__device__ __forceinline__ void lds_barrier() {
-    // LDS writes done, then the barrier (no wait on in-flight global loads)
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
 
 template <int G1>
 __global__ __launch_bounds__(64 * RF_WAVES) void k_routed_ffn16(
@@ -1320,6 +1426,19 @@ extern "C" int jtk_lowbit_grouped(int bits, const int8_t *A, int lda, const floa
         return (int)e;
     }
     if (rows_per_tile != 64) return (int)hipErrorInvalidValue;
+    if (bits == 4 && (K == 256 || K == 512) && N % 256 == 0) {
+        // weights in registers: 2 panels per wave at K = 256, 4 at K = 512
+        const int4 *t4 = (const int4 *)tiles;
+        if (K == 256)
+            hipLaunchKernelGGL((k_lowbit_down_rr<4, 2>), dim3((unsigned)(N / 128), (unsigned)max_tiles),
+                               dim3(256), 0, s, A, lda, sA, perm, t4, ntiles, Wp, Ws, wp_stride,
+                               ws_stride, out, ldo, err);
+        else
+            hipLaunchKernelGGL((k_lowbit_down_rr<8, 4>), dim3((unsigned)(N / 256), (unsigned)max_tiles),
+                               dim3(256), 0, s, A, lda, sA, perm, t4, ntiles, Wp, Ws, wp_stride,
+                               ws_stride, out, ldo, err);
+        return (int)hipGetLastError();
+    }
     if (bits == 4 && K <= LBR_KMAX && N % 128 == 0) {
         // channel groups per block: as many as keep about 1536 blocks
         const int ncg = N / 128;

@@ -53,6 +53,12 @@ __device__ __forceinline__ void barrier_lds() {
     asm volatile("" ::: "memory");
 }
 
+// This wave's LDS writes done, then the workgroup barrier (no wait on
+// in-flight global loads).
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // Wait for the oldest in-flight stage when `later` stages of PER copies each
 // were issued after it (the counter field holds at most 63; a smaller bound
 // only waits longer).

@@ -70,6 +70,9 @@ CASES = [
     (256, 512, 8, 2, 1, 128, 300),
     (128, 1024, 4, 2, 0, 64, 200),
     (128, 256, 16, 4, 0, 64, 260),
+    # down projection with its weights in registers (K = 256 and 512)
+    (512, 256, 16, 4, 1, 128, 400),
+    (256, 512, 16, 2, 0, 64, 333),
     # 16-row tiles with f = 256: one launch per tile for gate/up, SwiGLU,
     # row codes and down (n = 256, 512, 768, 1024)
     (256, 256, 64, 8, 1, 128, 16),
