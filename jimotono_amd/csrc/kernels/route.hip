@@ -744,6 +744,62 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ w,
     *(float4 *)(Y + (int64_t)t * n + j) = make_float4((float)a0, (float)a1, (float)a2, (float)a3);
 }
 
+// The same sum with the top-k K a compile-time constant: every load of a
+// thread (its K expert rows, the K weights and drop flags, up to 8 shared
+// rows) is issued before the first FMA, so a thread waits for memory once
+// instead of once per slot (the runtime-k loop above issues one row, waits,
+// adds, and only then loads the next). The sums run in the same order.
+#define CMB_SMAX 8
+template <int K, bool DROP>
+__global__ __launch_bounds__(256) void k_combine_k(const float *__restrict__ w,
+                                                   const float *__restrict__ Ye,
+                                                   const uint8_t *__restrict__ drop,
+                                                   const float *__restrict__ Ys, int S, int T,
+                                                   int n, float *__restrict__ Y, uint32_t *err) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int nq = n / 4;
+    if (idx >= (int64_t)T * nq) return;
+    const int t = (int)(idx / nq), j = (int)(idx % nq) * 4;
+    const int64_t q0 = (int64_t)t * K;
+    // all loads first, with no branch between them
+    float wv[K];
+    float4 yv[K];
+    uint8_t dr[K];
+#pragma unroll
+    for (int p = 0; p < K; p++) {
+        wv[p] = w[q0 + p];
+        yv[p] = *(const float4 *)(Ye + (q0 + p) * n + j);
+        if (DROP) dr[p] = drop[q0 + p];
+    }
+    float4 ys[CMB_SMAX];
+    if (S > 0) {  // kernel-uniform; rows past S - 1 repeat the last one (not summed)
+#pragma unroll
+        for (int s = 0; s < CMB_SMAX; s++)
+            ys[s] = *(const float4 *)(Ys + ((int64_t)min(s, S - 1) * T + t) * n + j);
+    }
+    double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
+#pragma unroll
+    for (int p = 0; p < K; p++) {
+        if (DROP && dr[p]) continue;
+        const double wp = (double)wv[p];
+        a0 = fma(wp, (double)yv[p].x, a0);
+        a1 = fma(wp, (double)yv[p].y, a1);
+        a2 = fma(wp, (double)yv[p].z, a2);
+        a3 = fma(wp, (double)yv[p].w, a3);
+    }
+#pragma unroll
+    for (int s = 0; s < CMB_SMAX; s++) {
+        if (s >= S) break;
+        a0 += (double)ys[s].x;
+        a1 += (double)ys[s].y;
+        a2 += (double)ys[s].z;
+        a3 += (double)ys[s].w;
+    }
+    if (!isfinite(a0) || !isfinite(a1) || !isfinite(a2) || !isfinite(a3))
+        raise_err(err, EF_NONFINITE_MID);
+    *(float4 *)(Y + (int64_t)t * n + j) = make_float4((float)a0, (float)a1, (float)a2, (float)a3);
+}
+
 // Scalar variant for n % 4 != 0 (legacy shapes).
 __global__ __launch_bounds__(256) void k_combine1(const float *__restrict__ w,
                                                   const float *__restrict__ Ye,
@@ -770,8 +826,25 @@ extern "C" int jtk_combine(const float *w, const float *Ye, const uint8_t *drop,
                            uint32_t *err, hipStream_t s) {
     if (n % 4 == 0) {
         const int64_t th = (int64_t)T * (n / 4);
-        hipLaunchKernelGGL(k_combine, dim3((unsigned)((th + 255) / 256)), dim3(256), 0, s, w,
-                           Ye, drop, Ys, S, T, k, n, Y, err);
+        const dim3 grid((unsigned)((th + 255) / 256));
+#define CMB_K(KK)                                                                        \
+    case KK:                                                                             \
+        if (drop)                                                                        \
+            hipLaunchKernelGGL((k_combine_k<KK, true>), grid, dim3(256), 0, s, w, Ye, drop, \
+                               Ys, S, T, n, Y, err);                                     \
+        else                                                                             \
+            hipLaunchKernelGGL((k_combine_k<KK, false>), grid, dim3(256), 0, s, w, Ye,    \
+                               drop, Ys, S, T, n, Y, err);                               \
+        break;
+        if (S <= CMB_SMAX && k >= 1 && k <= 8) {
+            switch (k) {
+                CMB_K(1) CMB_K(2) CMB_K(3) CMB_K(4) CMB_K(5) CMB_K(6) CMB_K(7) CMB_K(8)
+            }
+        } else {
+            hipLaunchKernelGGL(k_combine, grid, dim3(256), 0, s, w, Ye, drop, Ys, S, T, k, n, Y,
+                               err);
+        }
+#undef CMB_K
     } else {
         const int64_t th = (int64_t)T * n;
         hipLaunchKernelGGL(k_combine1, dim3((unsigned)((th + 255) / 256)), dim3(256), 0, s, w,
