@@ -55,13 +55,16 @@ __global__ __launch_bounds__(256) void k_quant_rows(
             if (lane == 0) raise_err(err, bad ? EF_NONFINITE_INPUT : EF_RANGE);
             return;
         }
-        if (lane == 0) scale[r] = p.scale_f;
         const float inv = quant_inv_f(p.scale_d);
         uint32_t *q4 = (uint32_t *)q;
         uint32_t fmask = 0;  // bit i: a code of v[i] needs the exact quotient
+        // every word first, then every store: stores between the steps make
+        // the compiler wait for each store before it reuses that store's
+        // address registers, one memory round trip per word
+        uint32_t wd[QR_REG];
 #pragma unroll
         for (int i = 0; i < QR_REG; i++) {
-            const int c = lane + 64 * i;
+            wd[i] = 0;
             if (64 * i < n4) {  // wave-uniform
                 bool f = false;
                 const uint32_t b0 = (uint8_t)quant_code_try(v[i].x, inv, f);
@@ -69,9 +72,15 @@ __global__ __launch_bounds__(256) void k_quant_rows(
                 const uint32_t b2 = (uint8_t)quant_code_try(v[i].z, inv, f);
                 const uint32_t b3 = (uint8_t)quant_code_try(v[i].w, inv, f);
                 fmask |= (uint32_t)f << i;
-                if (c < n4) q4[c] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+                wd[i] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
             }
         }
+#pragma unroll
+        for (int i = 0; i < QR_REG; i++) {
+            const int c = lane + 64 * i;
+            if (64 * i < n4 && c < n4) q4[c] = wd[i];
+        }
+        if (lane == 0) scale[r] = p.scale_f;
         // rare: rewrite those words exactly, picking v[j] out of the
         // registers with selects (a dynamic index would spill v[] to scratch)
         while (fmask) {
@@ -165,12 +174,13 @@ __global__ __launch_bounds__(256) void k_quant_rows16(const float *__restrict__ 
         if (sub == 0) raise_err(err, mu >= 0x7f800000u ? EF_NONFINITE_INPUT : EF_RANGE);
         return;
     }
-    if (sub == 0) scale[r] = p.scale_f;
     const float inv = quant_inv_f(p.scale_d);
     uint32_t *q4 = (uint32_t *)(Q + r * ldq);
     uint32_t fmask = 0;  // bit j: a code of v[j] needs the exact quotient
+    uint32_t wd[QS_MAXV];  // every word first, then the stores (as in k_quant_rows)
 #pragma unroll
-    for (int j = 0; j < QS_MAXV; j++)
+    for (int j = 0; j < QS_MAXV; j++) {
+        wd[j] = 0;
         if (j < nv) {
             bool f = false;
             const uint32_t b0 = (uint8_t)quant_code_try(v[j].x, inv, f);
@@ -178,8 +188,13 @@ __global__ __launch_bounds__(256) void k_quant_rows16(const float *__restrict__ 
             const uint32_t b2 = (uint8_t)quant_code_try(v[j].z, inv, f);
             const uint32_t b3 = (uint8_t)quant_code_try(v[j].w, inv, f);
             fmask |= (uint32_t)f << j;
-            q4[sub + 16 * j] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+            wd[j] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
         }
+    }
+#pragma unroll
+    for (int j = 0; j < QS_MAXV; j++)
+        if (j < nv) q4[sub + 16 * j] = wd[j];
+    if (sub == 0) scale[r] = p.scale_f;
     while (fmask) {  // rare: rewrite those words exactly
         const int j = __builtin_ctz(fmask);
         fmask &= fmask - 1;
