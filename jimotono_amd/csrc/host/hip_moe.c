@@ -229,7 +229,11 @@ static const char *const k_stage_names[ST_N] = {
     "shared_gateup", "shared_quant",  "shared_down",  "combine"};
 
 #define PROF_RING 16
-#define MOE_SIDE 4 /* side streams for the shared experts */
+/* side streams for the shared experts: one, so the experts run one after
+ * the other beside the routed path (measured at 4096 tokens: 0.360 ms per
+ * layer against 0.370 with one side stream per expert, which leaves fewer
+ * CUs to the routed chain) */
+#define MOE_SIDE 1
 
 struct jt_hip_moe {
     jt_hip_moe_desc d;
@@ -256,7 +260,7 @@ struct jt_hip_moe {
     int32_t *rnc;   /* [T] candidate counts */
     int8_t *Sqr;
     int last_T;
-    /* shared experts run on side streams forked after the input quantiser
+    /* shared experts run on a side stream forked after the input quantiser
      * and joined before the combine; expert e uses side[e % nside] */
     int nside;
     hipStream_t side[MOE_SIDE];
