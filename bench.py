@@ -206,6 +206,24 @@ def main():
         "stages_ms_per_step": {s: v / count for s, v in stages.items()},
     }
 
+    # ---------------- PCIe-inclusive rate (never the value) ----------------
+    # the same forward when the caller hands over host buffers: pinned X in,
+    # the layer, pinned Y out, in stream order on the one stream
+    Xh = torch.empty(T, n, dtype=torch.float32, pin_memory=True)
+    Xh.copy_(X.cpu())
+    Yh = torch.empty(T, n, dtype=torch.float32, pin_memory=True)
+
+    def host_step():
+        X.copy_(Xh, non_blocking=True)
+        step()
+        Yh.copy_(Y, non_blocking=True)
+
+    _, pcie_ms = time_fn(torch, host_step, max(2, args.steps // 2), 2, stream)
+    assert api.sync_errors(stream) == 0
+    out["pcie_inclusive"] = {"tokens_per_s": T / (pcie_ms / 1e3), "ms_per_step": pcie_ms,
+                             "bytes_over_pcie_per_step": 2 * T * n * 4}
+    del Xh, Yh
+
     # ---------------- CPU baseline ----------------
     if not args.no_cpu_baseline:
         try:
