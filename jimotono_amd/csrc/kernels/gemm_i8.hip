@@ -1462,10 +1462,12 @@ extern "C" int jtk_lowbit_grouped(int bits, const int8_t *A, int lda, const floa
     }
     if (rows_per_tile != 64) return (int)hipErrorInvalidValue;
     if (bits == 4 && (K == 256 || K == 512) && N % 256 == 0) {
-        // weights in registers: 2 panels per wave at K = 256, 4 at K = 512
+        // weights in registers: 4 panels per wave (measured in the overlapped
+        // layer at K = 256: 4 panels 0.3525 ms against 2 panels 0.3577; the
+        // fewer, longer blocks leave more room to the shared experts)
         const int4 *t4 = (const int4 *)tiles;
         if (K == 256)
-            hipLaunchKernelGGL((k_lowbit_down_rr<4, 2>), dim3((unsigned)(N / 128), (unsigned)max_tiles),
+            hipLaunchKernelGGL((k_lowbit_down_rr<4, 4>), dim3((unsigned)(N / 256), (unsigned)max_tiles),
                                dim3(256), 0, s, A, lda, sA, perm, t4, ntiles, Wp, Ws, wp_stride,
                                ws_stride, out, ldo, err);
         else
