@@ -750,7 +750,9 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ w,
 // instead of once per slot (the runtime-k loop above issues one row, waits,
 // adds, and only then loads the next). The sums run in the same order.
 #define CMB_SMAX 8
-template <int K, bool DROP>
+// SN: shared rows loaded per thread, S itself when S <= 2, else CMB_SMAX
+// (rows past S - 1 then repeat the last one and are not summed)
+template <int K, int SN, bool DROP>
 __global__ __launch_bounds__(256) void k_combine_k(const float *__restrict__ w,
                                                    const float *__restrict__ Ye,
                                                    const uint8_t *__restrict__ drop,
@@ -771,10 +773,10 @@ __global__ __launch_bounds__(256) void k_combine_k(const float *__restrict__ w,
         yv[p] = *(const float4 *)(Ye + (q0 + p) * n + j);
         if (DROP) dr[p] = drop[q0 + p];
     }
-    float4 ys[CMB_SMAX];
-    if (S > 0) {  // kernel-uniform; rows past S - 1 repeat the last one (not summed)
+    float4 ys[SN > 0 ? SN : 1];
+    if (S > 0) {  // kernel-uniform
 #pragma unroll
-        for (int s = 0; s < CMB_SMAX; s++)
+        for (int s = 0; s < SN; s++)
             ys[s] = *(const float4 *)(Ys + ((int64_t)min(s, S - 1) * T + t) * n + j);
     }
     double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
@@ -788,7 +790,7 @@ __global__ __launch_bounds__(256) void k_combine_k(const float *__restrict__ w,
         a3 = fma(wp, (double)yv[p].w, a3);
     }
 #pragma unroll
-    for (int s = 0; s < CMB_SMAX; s++) {
+    for (int s = 0; s < SN; s++) {
         if (s >= S) break;
         a0 += (double)ys[s].x;
         a1 += (double)ys[s].y;
@@ -827,14 +829,24 @@ extern "C" int jtk_combine(const float *w, const float *Ye, const uint8_t *drop,
     if (n % 4 == 0) {
         const int64_t th = (int64_t)T * (n / 4);
         const dim3 grid((unsigned)((th + 255) / 256));
-#define CMB_K(KK)                                                                        \
-    case KK:                                                                             \
-        if (drop)                                                                        \
-            hipLaunchKernelGGL((k_combine_k<KK, true>), grid, dim3(256), 0, s, w, Ye, drop, \
-                               Ys, S, T, n, Y, err);                                     \
-        else                                                                             \
-            hipLaunchKernelGGL((k_combine_k<KK, false>), grid, dim3(256), 0, s, w, Ye,    \
-                               drop, Ys, S, T, n, Y, err);                               \
+#define CMB_KS(KK, SN)                                                                     \
+    if (drop)                                                                              \
+        hipLaunchKernelGGL((k_combine_k<KK, SN, true>), grid, dim3(256), 0, s, w, Ye, drop, \
+                           Ys, S, T, n, Y, err);                                           \
+    else                                                                                   \
+        hipLaunchKernelGGL((k_combine_k<KK, SN, false>), grid, dim3(256), 0, s, w, Ye,      \
+                           drop, Ys, S, T, n, Y, err);
+#define CMB_K(KK)                                                                          \
+    case KK:                                                                               \
+        if (S == 0) {                                                                      \
+            CMB_KS(KK, 0)                                                                  \
+        } else if (S == 1) {                                                               \
+            CMB_KS(KK, 1)                                                                  \
+        } else if (S == 2) {                                                               \
+            CMB_KS(KK, 2)                                                                  \
+        } else {                                                                           \
+            CMB_KS(KK, CMB_SMAX)                                                           \
+        }                                                                                  \
         break;
         if (S <= CMB_SMAX && k >= 1 && k <= 8) {
             switch (k) {
@@ -845,6 +857,7 @@ extern "C" int jtk_combine(const float *w, const float *Ye, const uint8_t *drop,
                                err);
         }
 #undef CMB_K
+#undef CMB_KS
     } else {
         const int64_t th = (int64_t)T * n;
         hipLaunchKernelGGL(k_combine1, dim3((unsigned)((th + 255) / 256)), dim3(256), 0, s, w,
