@@ -12,7 +12,8 @@
  * drop-in; this API is what a caller that keeps activations on the GPU uses.
  *
  * All pointers named d* are device (HBM) pointers; `stream` is a hipStream_t
- * passed as void* (NULL = the library's own stream). Calls are asynchronous
+ * passed as void* (NULL = the HIP null stream, which is also torch's default
+ * stream, so work the caller queued there is ordered). Calls are asynchronous
  * on that stream. Arguments are validated on the host before anything is
  * enqueued (JT_ERR_INVAL, nothing written). Data-dependent failures found by
  * the kernels (a non-finite activation, an overflowing epilogue) raise bits in
@@ -46,7 +47,8 @@ extern "C" {
 /* Bind the calling thread's HIP device (idempotent; called implicitly by
  * every other entry point with device 0). */
 int jt_hip_init(int device);
-/* Wait for `stream`, then read and clear the library's device error word.
+/* Wait for `stream` (NULL: for the whole device), then read and clear the
+ * library's device error word.
  * *out_flags gets the raised JT_HIP_EF_* bits (0 = clean). Returns JT_OK, or
  * JT_ERR_IO on a HIP failure. */
 int jt_hip_sync_errors(void *stream, uint32_t *out_flags);

@@ -284,8 +284,13 @@ def _ptr(t):
 
 
 def _stream(stream):
+    """HIP stream handle for a call: torch's current stream when None (its
+    default stream is the HIP null stream, handle 0, which the library takes
+    as the null stream too), so the call is ordered with the caller's torch
+    work on that stream."""
     if stream is None:
-        return None
+        import torch
+        stream = torch.cuda.current_stream()
     return C.c_void_p(stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream))
 
 

@@ -184,7 +184,7 @@ int jt_hip_ffn_fwd(jt_hip_ffn *F, const float *dX, float *dY, int T, void *strea
     if (T == 0) return JT_OK;
     int rc = ffn_reserve(F, T, 1);
     if (rc != JT_OK) return rc;
-    hipStream_t s = stream ? (hipStream_t)stream : rt->stream;
+    hipStream_t s = (hipStream_t)stream; /* NULL: the HIP null stream */
     if (T <= 16) {
         /* decode: both GEMMs quantise their rows themselves (two launches) */
         int e = jtk_w8a8_gemm_xq(dX, F->n, F->n, F->gu_P, F->gu_s, T, 2 * F->h, F->Np_gu,
@@ -470,7 +470,7 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
     jt_rt *rt = jt_rt_get();
     if (!rt) return JT_ERR_IO;
     if (T == 0) return JT_OK;
-    hipStream_t s = stream ? (hipStream_t)stream : rt->stream;
+    hipStream_t s = (hipStream_t)stream; /* NULL: the HIP null stream */
     const int n = d->n, h = d->h, E = d->n_experts, k = d->topk, S = d->n_shared;
     const int Tk = T * k;
     uint32_t *err = rt->d_err;

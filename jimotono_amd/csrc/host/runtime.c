@@ -39,7 +39,10 @@ jt_rt *jt_rt_get(void) {
     }
     memset(&g_rt, 0, sizeof(g_rt));
     g_rt.device = g_req_device;
-    if (hipStreamCreateWithFlags(&g_rt.stream, hipStreamNonBlocking) != hipSuccess ||
+    /* a blocking stream: the synchronous host-pointer calls and the weight
+     * preparation are ordered after work the caller queued on the null
+     * stream (torch's default stream, for one) */
+    if (hipStreamCreateWithFlags(&g_rt.stream, hipStreamDefault) != hipSuccess ||
         hipMalloc((void **)&g_rt.d_err, 256) != hipSuccess ||
         hipMalloc((void **)&g_rt.d_scratch, 4096) != hipSuccess ||
         hipMemset(g_rt.d_err, 0, 256) != hipSuccess) {
@@ -131,5 +134,9 @@ int jt_hip_sync_errors(void *stream, uint32_t *out_flags) {
         errno = EINVAL;
         return JT_ERR_INVAL;
     }
-    return jt_rt_flags(rt, stream ? (hipStream_t)stream : rt->stream, out_flags);
+    if (!stream) { /* NULL: wait for the whole device, then read the word */
+        hipError_t e = hipDeviceSynchronize();
+        if (e != hipSuccess) return jt_rt_err(e);
+    }
+    return jt_rt_flags(rt, (hipStream_t)stream, out_flags);
 }

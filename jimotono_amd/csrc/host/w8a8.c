@@ -259,7 +259,7 @@ int jt_hip_quant_rows(const float *dX, int rows, int cols, int8_t *dXq, float *d
     jt_rt *rt = jt_rt_get();
     if (!rt) return JT_ERR_IO;
     if (rows == 0) return JT_OK;
-    hipStream_t s = stream ? (hipStream_t)stream : rt->stream;
+    hipStream_t s = (hipStream_t)stream; /* NULL: the HIP null stream */
     if (jtk_quant_rows(dX, rows, cols, dXq, cols, dscale, NULL, rt->d_err, s))
         return jt_rt_err(hipErrorLaunchFailure);
     return JT_OK;
@@ -354,7 +354,7 @@ int jt_hip_w8a8_gemm(const jt_hip_w8a8 *W, const int8_t *dAq, const float *dsA, 
     jt_rt *rt = jt_rt_get();
     if (!rt) return JT_ERR_IO;
     if (M == 0) return JT_OK;
-    hipStream_t s = stream ? (hipStream_t)stream : rt->stream;
+    hipStream_t s = (hipStream_t)stream; /* NULL: the HIP null stream */
     if (jtk_w8a8_gemm(dAq, W->K, dsA, W->P, W->sB, M, W->N, W->Np, W->Kp, dC, W->N, 0,
                       rt->d_err, s))
         return jt_rt_err(hipErrorLaunchFailure);

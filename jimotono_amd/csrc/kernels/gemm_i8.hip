@@ -119,7 +119,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) void k_w8a8_skinny(
                         const uint32_t q1 = (uint8_t)quant_code_try(v[j].y, inv, f);
                         const uint32_t q2 = (uint8_t)quant_code_try(v[j].z, inv, f);
                         const uint32_t q3 = (uint8_t)quant_code_try(v[j].w, inv, f);
-                        fmask |= (uint32_t)f << j;
+                        fmask |= (uint32_t)(f && c < n4) << j;  // never rewrite past the row
                         if (c < n4) qr[c] = q0 | (q1 << 8) | (q2 << 16) | (q3 << 24);
                     }
                 }

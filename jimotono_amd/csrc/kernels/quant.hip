@@ -71,7 +71,10 @@ __global__ __launch_bounds__(256) void k_quant_rows(
                 const uint32_t b1 = (uint8_t)quant_code_try(v[i].y, inv, f);
                 const uint32_t b2 = (uint8_t)quant_code_try(v[i].z, inv, f);
                 const uint32_t b3 = (uint8_t)quant_code_try(v[i].w, inv, f);
-                fmask |= (uint32_t)f << i;
+                // lanes past the row hold zeros; with inv = inf (max|x| below
+                // ~3.7e-37) their codes would fail too, and the exact rewrite
+                // below must not store past the row
+                fmask |= (uint32_t)(f && lane + 64 * i < n4) << i;
                 wd[i] = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
             }
         }

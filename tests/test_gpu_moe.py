@@ -230,6 +230,60 @@ def test_ffn_decode_widths(jt, orc, torch_cuda, n, h, M):
     close(dY.cpu().numpy(), Y2)
 
 
+def test_ffn_decode_tiny_row(jt, orc, torch_cuda):
+    """A decode activation row with max|x| ~ 1e-38 (its codes all take the
+    exact path) between normal rows, at n = 128 where half the lanes of the
+    in-GEMM quantiser are past the row."""
+    torch = torch_cuda
+    announce("ffn decode tiny row n=128 h=128")
+    n, h, M = 128, 128, 3
+    rng = np.random.default_rng(128)
+    Wg = (rng.standard_normal((h, n)) / np.sqrt(n)).astype(np.float32)
+    Wu = (rng.standard_normal((h, n)) / np.sqrt(n)).astype(np.float32)
+    Wd = (rng.standard_normal((h, n)) / np.sqrt(h)).astype(np.float32)
+    X = rng.standard_normal((M, n)).astype(np.float32)
+    X[1] *= np.float32(1e-38)
+    F = jt.FFN(dev(torch, Wg), dev(torch, Wu), dev(torch, Wd))
+    dY = torch.zeros((M, n), dtype=torch.float32, device="cuda")
+    F.fwd(dev(torch, X), dY)
+    assert jt.sync_errors() == 0
+    rc, Y2 = orc.ffn_fwd(Wg, Wu, Wd, X)
+    assert rc == 0
+    close(dY.cpu().numpy(), Y2)
+
+
+def test_layer_ordered_with_torch_default_stream(jt, orc, torch_cuda):
+    """A torch kernel writes X on torch's default stream, the layer runs with
+    no stream given, and a torch op reads Y, with no synchronisation in
+    between: the forward must be ordered after the producer and before the
+    consumer."""
+    torch = torch_cuda
+    n, h, E, k, S, hs, T = 256, 128, 16, 4, 1, 128, 600
+    announce("layer ordered with torch's default stream")
+    rng = np.random.default_rng(77)
+    W = mk_weights(rng, n, h, E, S, hs)
+    Wgate, Wg, Wu, Wd, sh = W
+    L = jt.MoE(n, h, E, k, S, hs, T, dev(torch, Wgate), dev(torch, Wg), dev(torch, Wu),
+               dev(torch, Wd), dev(torch, sh[0]), dev(torch, sh[1]), dev(torch, sh[2]))
+    X0 = rng.standard_normal((T, n)).astype(np.float32)
+    src = dev(torch, X0 * 0.5)
+    torch.cuda.synchronize()
+    dX = torch.empty((T, n), dtype=torch.float32, device="cuda")
+    dY = torch.full((T, n), float("nan"), dtype=torch.float32, device="cuda")
+    big = torch.randn(4096, 4096, device="cuda")
+    for _ in range(3):                      # keep the default stream busy
+        big = big @ big / 64.0
+    torch.mul(src, 2.0, out=dX)             # X = X0, written last on the default stream
+    assert L.fwd(dX, dY) == 0
+    Ysum = dY.double().sum(dim=1)           # consumer on the default stream
+    got = Ysum.cpu().numpy()
+    assert jt.sync_errors() == 0
+    o = orc.moe_q(n, h, E, k, S, hs, Wgate, Wg, Wu, Wd, *sh).fwd(X0)
+    assert o["rc"] == 0
+    ref = o["Y"].astype(np.float64).sum(axis=1)
+    np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-4 * np.abs(ref).max())
+
+
 def test_ffn_decode_nonfinite_row(jt, torch_cuda):
     """A NaN in a decode activation row is reported (the reference's
     quantiser rejects non-finite input)."""

@@ -65,6 +65,25 @@ def test_quant_rows_ties(jt, orc, cols):
                                  for v in X[0, 1:].tolist()]
 
 
+@pytest.mark.parametrize("cols", [100, 640, 2816])
+def test_quant_tiny_rows_stay_in_row(jt, orc, cols):
+    """Rows with max|x| below ~3.7e-37 make the fp32 reciprocal of the scale
+    infinite, so every code of the row goes to the exact fp64 path. That
+    path must rewrite only the row's own words: the tiny rows sit between
+    normal rows, and the output has no slack after the last row."""
+    announce(f"quant tiny rows cols={cols}")
+    rng = np.random.default_rng(cols + 1)
+    X = rng.standard_normal((6, cols)).astype(np.float32)
+    X[1] *= np.float32(1e-38)
+    X[3] = (rng.standard_normal(cols) * 1e-39).astype(np.float32)  # subnormal
+    X[5] *= np.float32(3e-38)                                       # last row
+    rc, Q, s = jt.w8a8_quant_per_channel(X)
+    rc2, Q2, s2 = orc.quant_rows(X)
+    assert rc == 0 and rc2 == 0
+    assert np.array_equal(Q, Q2)
+    assert np.array_equal(bits(s), bits(s2))
+
+
 @pytest.mark.parametrize("n", [1, 255, 4096, 100003])
 def test_quant_per_tensor_and_dequant(jt, orc, n):
     announce(f"quant_per_tensor n={n}")
