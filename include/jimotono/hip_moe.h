@@ -143,6 +143,9 @@ enum jt_hip_moe_buf {
                                could reach the top-k (every selected one); with the
                                int8-bounded router (E <= 256, d % 64 == 0) the others
                                hold the float of their int8 approximation */
+    JT_HIP_BUF_HQ = 9,      /* int8 [T*k][h]: routed hidden rows (SwiGLU output) as
+                               int8 codes, in sorted row order (row r is pair perm[r]) */
+    JT_HIP_BUF_HSCALE = 10, /* fp32 [T*k]: their per-row scales, same order */
 };
 int jt_hip_moe_buffer(const jt_hip_moe *L, int which, void **dptr,
                       size_t *bytes);

@@ -376,7 +376,8 @@ class FFN:
             self.h = None
 
 
-BUF_IDS, BUF_WEIGHTS, BUF_PERM, BUF_OFF, BUF_XQ, BUF_XSCALE, BUF_YE, BUF_YS, BUF_LOGITS = range(9)
+(BUF_IDS, BUF_WEIGHTS, BUF_PERM, BUF_OFF, BUF_XQ, BUF_XSCALE, BUF_YE, BUF_YS, BUF_LOGITS,
+ BUF_HQ, BUF_HSCALE) = range(11)
 
 
 class MoE:

@@ -558,7 +558,8 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
          * (the three stages are timed as one, under routed_gateup) */
         le |= jtk_routed_ffn16(L->Xq, L->sx, L->perm, L->tiles, L->ntiles, max_tiles, k,
                                L->gu_P, L->gu_S, L->gu_pstride, L->gu_sstride, L->dn_P, L->dn_S,
-                               L->dn_pstride, L->dn_sstride, n, h, L->Ye, err, s);
+                               L->dn_pstride, L->dn_sstride, n, h, L->Ye, L->Sqr, L->ssr, err,
+                               s);
         prof_mark(L, slot, ST_R_QUANT, s);
         prof_mark(L, slot, ST_R_DOWN, s);
     } else {
@@ -624,6 +625,8 @@ int jt_hip_moe_buffer(const jt_hip_moe *L, int which, void **dptr, size_t *bytes
     case JT_HIP_BUF_YE: *dptr = L->Ye; *bytes = T * k * n * 4; break;
     case JT_HIP_BUF_YS: *dptr = L->Ys; *bytes = S * T * n * 4; break;
     case JT_HIP_BUF_LOGITS: *dptr = L->logits; *bytes = T * E * 4; break;
+    case JT_HIP_BUF_HQ: *dptr = L->Sqr; *bytes = T * k * (size_t)L->d.h; break;
+    case JT_HIP_BUF_HSCALE: *dptr = L->ssr; *bytes = T * k * 4; break;
     default: FAIL(JT_ERR_INVAL, EINVAL);
     }
     return JT_OK;

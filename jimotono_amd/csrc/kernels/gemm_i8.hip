@@ -1168,7 +1168,8 @@ __global__ __launch_bounds__(64 * RF_WAVES) void k_routed_ffn16(
     const int32_t *__restrict__ ntiles, int topk, const uint8_t *__restrict__ guP,
     const uint16_t *__restrict__ guS, int64_t gu_pstride, int64_t gu_sstride,
     const uint8_t *__restrict__ dnP, const uint16_t *__restrict__ dnS, int64_t dn_pstride,
-    int64_t dn_sstride, float *__restrict__ Ye, uint32_t *err) {
+    int64_t dn_sstride, float *__restrict__ Ye, int8_t *__restrict__ Hq,
+    float *__restrict__ Hs, uint32_t *err) {
     constexpr int N = 64 * G1;                    // model width
     constexpr int HB = (RF_H / 16) / RF_WAVES;    // h blocks per wave (2)
     constexpr int DPW = (N / 16) / RF_WAVES;      // down panels per wave
@@ -1315,8 +1316,15 @@ __global__ __launch_bounds__(64 * RF_WAVES) void k_routed_ffn16(
             const uint32_t b1 = (uint8_t)quant_code_fast(v.y, qp.scale_d, inv);
             const uint32_t b2 = (uint8_t)quant_code_fast(v.z, qp.scale_d, inv);
             const uint32_t b3 = (uint8_t)quant_code_fast(v.w, qp.scale_d, inv);
-            *(uint32_t *)(hq + row * RF_QSTR + lane * 4) = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
-            if (lane == 0) rsq[row] = qp.scale_f;
+            const uint32_t wd = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+            *(uint32_t *)(hq + row * RF_QSTR + lane * 4) = wd;
+            // the hidden row's codes and scale also go to memory, in sorted
+            // row order like the 64-row path's
+            *(uint32_t *)(Hq + (int64_t)(pos0 + row) * RF_H + lane * 4) = wd;
+            if (lane == 0) {
+                rsq[row] = qp.scale_f;
+                Hs[pos0 + row] = qp.scale_f;
+            }
         }
     }
     lds_barrier();
@@ -1417,14 +1425,15 @@ extern "C" int jtk_routed_ffn16(const int8_t *Xq, const float *sx, const int32_t
                                 int topk, const uint8_t *guP, const uint16_t *guS,
                                 int64_t gu_pstride, int64_t gu_sstride, const uint8_t *dnP,
                                 const uint16_t *dnS, int64_t dn_pstride, int64_t dn_sstride, int n,
-                                int h, float *Ye, uint32_t *err, hipStream_t s) {
+                                int h, float *Ye, int8_t *Hq, float *Hs, uint32_t *err,
+                                hipStream_t s) {
     if (max_tiles <= 0) return 0;
     if (h != RF_H) return (int)hipErrorInvalidValue;
     const int4 *t4 = (const int4 *)tiles;
 #define RF_LAUNCH(G)                                                                            \
     hipLaunchKernelGGL(k_routed_ffn16<G>, dim3((unsigned)max_tiles), dim3(64 * RF_WAVES), 0, s, Xq, sx, \
                        perm, t4, ntiles, topk, guP, guS, gu_pstride, gu_sstride, dnP, dnS,      \
-                       dn_pstride, dn_sstride, Ye, err)
+                       dn_pstride, dn_sstride, Ye, Hq, Hs, err)
     switch (n) {
     case 256: RF_LAUNCH(4); break;
     case 512: RF_LAUNCH(8); break;

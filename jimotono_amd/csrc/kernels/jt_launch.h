@@ -69,7 +69,7 @@ int jtk_routed_ffn16(const int8_t *Xq, const float *sx, const int32_t *perm,
                      const uint8_t *guP, const uint16_t *guS, int64_t gu_pstride,
                      int64_t gu_sstride, const uint8_t *dnP, const uint16_t *dnS,
                      int64_t dn_pstride, int64_t dn_sstride, int n, int h, float *Ye,
-                     uint32_t *err, hipStream_t s);
+                     int8_t *Hq, float *Hs, uint32_t *err, hipStream_t s);
 
 /* router.hip: int8 MFMA candidates + exact fp64 verification of the gate */
 int jtk_router_codes(const float *X, int rows, int n, int8_t *qh, int8_t *ql, float *sf,

@@ -959,7 +959,7 @@ static int shared_token(const or_moe_q *L, int s, const int8_t *xq, float sx,
 int or_moe_q_fwd(const or_moe_q *L, const float *X, int T,
                  const int32_t *ids_in, const float *w_in, float *Y,
                  int32_t *ids_o, float *w_o, int32_t *perm_o, int32_t *off_o,
-                 float *Ye_o, float *Ys_o) {
+                 float *Ye_o, float *Ys_o, int8_t *Hq_o, float *Hs_o) {
     int n = L->n, h = L->h, E = L->E, k = L->k, S = L->S, hs = L->hs;
     int G = L->group;
     size_t Tk = (size_t)T * k, nh = (size_t)n * h;
@@ -1028,6 +1028,8 @@ int or_moe_q_fwd(const or_moe_q *L, const float *X, int T,
                 if (or_silu_mul(g[i], u[i], &sb[i]) != RC_OK) goto out;
             float ss;
             if (quant_span(sb, (size_t)h, sq, &ss) != RC_OK) goto out;
+            if (Hq_o) memcpy(Hq_o + (size_t)r * h, sq, (size_t)h);
+            if (Hs_o) Hs_o[r] = ss;
             if (or_gemm_lowbit_group(sq, &ss, dc, dsc, 4, G, Ye + (size_t)q * n,
                                      NULL, 1, n, h) != RC_OK)
                 goto out;

@@ -171,7 +171,7 @@ void or_moe_q_free(or_moe_q *L);
 int or_moe_q_fwd(const or_moe_q *L, const float *X, int T,
                  const int32_t *ids_in, const float *w_in, float *Y,
                  int32_t *ids, float *w, int32_t *perm, int32_t *off,
-                 float *Ye, float *Ys);
+                 float *Ye, float *Ys, int8_t *Hq, float *Hs);
 
 /* One W8A8 SwiGLU expert as used for the shared experts of or_moe_q_fwd:
  * Wg, Wu, Wd [h][n] fp32, prepared on the fly; Y [T][n]. */

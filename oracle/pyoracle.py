@@ -96,7 +96,7 @@ class Oracle:
         L.or_moe_q_free.argtypes = [C.POINTER(_OrMoeQ)]
         L.or_moe_q_free.restype = None
         L.or_moe_q_fwd.argtypes = [C.POINTER(_OrMoeQ), _f32p, C.c_int, C.c_void_p,
-                                   C.c_void_p, _f32p] + [C.c_void_p] * 6
+                                   C.c_void_p, _f32p] + [C.c_void_p] * 8
         L.or_ffn_fwd.argtypes = [_f32p, _f32p, _f32p, C.c_int, C.c_int, _f32p, C.c_int,
                                  _f32p]
 
@@ -334,14 +334,18 @@ class OracleMoeQ:
         off = np.zeros(E + 1, np.int32)
         Ye = np.zeros((T * k, n), np.float32)
         Ys = np.zeros((max(S, 1), T, n), np.float32)
+        Hq = np.zeros((T * k, self.h), np.int8)
+        Hs = np.zeros(T * k, np.float32)
         ids_in = None if ids is None else _c(ids, np.int32)
         w_in = None if w is None else _c(w, np.float32)
         rc = self.o.lib.or_moe_q_fwd(
             C.byref(self.st), X, T, None if ids_in is None else ids_in.ctypes.data,
             None if w_in is None else w_in.ctypes.data, Y, ids_o.ctypes.data,
             w_o.ctypes.data, perm.ctypes.data, off.ctypes.data, Ye.ctypes.data,
-            Ys.ctypes.data)
-        return dict(rc=rc, Y=Y, ids=ids_o, w=w_o, perm=perm, off=off, Ye=Ye, Ys=Ys[:S])
+            Ys.ctypes.data, Hq.ctypes.data, Hs.ctypes.data)
+        # Hq/Hs: the routed hidden rows' int8 codes and scales in sorted order
+        return dict(rc=rc, Y=Y, ids=ids_o, w=w_o, perm=perm, off=off, Ye=Ye, Ys=Ys[:S],
+                    Hq=Hq, Hs=Hs)
 
 
 class RefLib:

@@ -25,6 +25,13 @@ Cases (key prefixes in the .npz):
   layer{f}_*     jt_moe_fwd_batch, f = 0 fp32, 1 W8A8 flag, 2 low-bit mode 1
   logits_*       jt_moe_fwd out_logits (gate logits, src/moe_layer.c:67-86), with
                  rows whose fp64 sum depends on the 4-lane summation order
+  shared_*       jt_moe_fwd_batch with the W8A8 flag, one token per call, routed
+                 down weights zero: Y is the shared experts' W8A8 SwiGLU output
+                 (inputs from gen.shared_case)
+  acc{0,2}_*     jt_moe_fwd_batch in fp32 (0) and true-LUT low-bit (2) modes on
+                 gen.accuracy_case(acc_salt), a salt whose routing drops nothing
+  lpat_lut{2,4}  jt_lowbit_gemm_lut on the reference test's own inputs
+                 (bench/kernel/test_lowbit.c:112-157, gen.lpat_lut_inputs)
 """
 import os
 import sys
@@ -36,6 +43,8 @@ ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, ROOT)
 
 from oracle.pyoracle import RefLib  # noqa: E402
+sys.path.insert(0, HERE)
+from gen import accuracy_case, lpat_lut_inputs, shared_case  # noqa: E402
 
 OUT = os.path.join(HERE, "ref_vectors.npz")
 
@@ -174,6 +183,41 @@ def main():
                                         None, None, 1)
     assert rc == 0
     g.update(logits_adv_W=Wadv, logits_adv_out=lga)
+
+    # ---- shared experts through the reference's W8A8 layer, T = 1 per call
+    # (per-tensor activations of one row = per-token), so the reference
+    # computes the prepared layer's shared-expert formula ----
+    X, Wgate, Wg, Wu, Wd, Wgs, Wus, Wds = shared_case()
+    ys = []
+    for t in range(X.shape[0]):
+        r = R.moe_fwd_batch(X[t:t + 1], Wgate, Wg, Wu, Wd, Wgs, Wus, Wds, 2, 1.0, 1, 0)
+        assert r["rc"] == 0 and not r["drop"].any()
+        assert not r["Ysel"].any()  # routed outputs are exactly zero
+        ys.append(r["Y"][0])
+    g["shared_Y"] = np.array(ys, np.float32)
+
+    # ---- fp32 and true-LUT layers on a routing that drops nothing ----
+    for salt in range(1000, 1100, 10):
+        args = accuracy_case(salt)
+        r0 = R.moe_fwd_batch(*args, 2, 1.5, 0, 0)
+        assert r0["rc"] == 0
+        if not r0["drop"].any():
+            break
+    else:
+        raise RuntimeError("no salt without drops")
+    r2 = R.moe_fwd_batch(*args, 2, 1.5, 0, 2)
+    assert r2["rc"] == 0 and not r2["drop"].any()
+    g["acc_salt"] = np.int64(salt)
+    for key in ("Y", "Ysel", "ids", "w"):
+        g[f"acc0_{key}"] = r0[key]
+    g["acc2_Y"], g["acc2_Ysel"] = r2["Y"], r2["Ysel"]
+
+    # ---- the reference low-bit test's own inputs ----
+    Xp, Wp = lpat_lut_inputs()
+    for bits in (2, 4):
+        rc, Y = R.lowbit_gemm_lut(Xp, Wp, bits)
+        assert rc == 0
+        g[f"lpat_lut{bits}"] = Y
 
     np.savez_compressed(OUT, **g)
     print(f"wrote {OUT}: {len(g)} arrays, {os.path.getsize(OUT)} bytes")

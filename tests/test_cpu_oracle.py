@@ -460,3 +460,184 @@ def test_live_vs_reference(orc, ref):
         for key in ("ids", "perm", "off", "drop"):
             assert np.array_equal(r1[key], r2[key]), key
         assert np.array_equal(bits(r1["Y"]), bits(r2["Y"]))
+
+
+# ------------------------------ the shared expert, rebuilt from pinned parts
+
+def _np_quant_rows(X):
+    """Closed form of the row quantiser (pinned by test_quant_closed_form and
+    the golden quant_rows vectors): fp64 max|x|/127, round half away from
+    zero, clamp +-127; a zero row gets scale 1 and codes 0."""
+    X64 = np.asarray(X, np.float32).astype(np.float64)
+    mx = np.abs(X64).max(axis=1)
+    sd = np.where(mx == 0, 1.0, mx / 127.0)
+    q = np.clip(_round_half_away(X64 / sd[:, None]), -127, 127)
+    q[mx == 0] = 0
+    return q.astype(np.int64), np.where(mx == 0, 1.0, mx / 127.0).astype(np.float32)
+
+
+def _np_epilogue(acc, sa, sw):
+    """W8A8 epilogue (float)((double)acc * ((double)sA * (double)sB))."""
+    return (acc.astype(np.float64) * (np.float64(sa) * sw.astype(np.float64))).astype(np.float32)
+
+
+def _np_silu_mul(g, u):
+    """SwiGLU of the reference, fp64 with glibc exp (math.exp), one value at
+    a time: (float)((g * (1 / (1 + exp(-g)))) * u)."""
+    out = np.empty(g.shape, np.float32)
+    for i, (gi, ui) in enumerate(zip(g.tolist(), u.tolist())):
+        out[i] = np.float32((gi * (1.0 / (1.0 + math.exp(-gi)))) * ui)
+    return out
+
+
+def _np_ffn(Wg, Wu, Wd, X, swap_gu=False, wd_untransposed=False, wd_per_tensor=False):
+    """One W8A8 SwiGLU expert from the pinned pieces: per-token codes of X,
+    int8 gate/up rows of Wg/Wu [h][n] (one scale per hidden channel),
+    integer dots, the W8A8 epilogue, SwiGLU, requantised hidden row, and the
+    down projection with Wd [h][n] read as B[K = h][N = n] (output channel j
+    is column j, quantised over its h values). The keyword switches plant
+    the slips a restatement could make."""
+    gq, gs = _np_quant_rows(Wg)
+    uq, us = _np_quant_rows(Wu)
+    if swap_gu:
+        gq, gs, uq, us = uq, us, gq, gs
+    Wdn = Wd if wd_untransposed else np.ascontiguousarray(Wd.T)   # [n][h]
+    if wd_per_tensor:
+        dq, ds1 = _np_quant_rows(Wdn.reshape(1, -1))
+        dq, ds = dq.reshape(Wdn.shape), np.full(Wdn.shape[0], ds1[0], np.float32)
+    else:
+        dq, ds = _np_quant_rows(Wdn)
+    xq, xs = _np_quant_rows(X)
+    Y = np.zeros((X.shape[0], Wdn.shape[0]), np.float32)
+    for t in range(X.shape[0]):
+        g = _np_epilogue(gq @ xq[t], xs[t], gs)
+        u = _np_epilogue(uq @ xq[t], xs[t], us)
+        s = _np_silu_mul(g, u)
+        sq, ss = _np_quant_rows(s[None, :])
+        Y[t] = _np_epilogue(dq @ sq[0], ss[0], ds)
+    return Y
+
+
+def test_shared_expert_rebuilt_from_pinned_parts(orc):
+    """or_ffn_fwd (the shared experts of the prepared layer) equals the
+    composition of pinned pieces to the bit, and each planted slip (gate and
+    up swapped, Wd not transposed, a per-tensor down scale) is caught."""
+    n, h, T = 64, 64, 6   # square Wd, so an untransposed read still has the right shape
+    rng = np.random.default_rng(31)
+    Wg = (rng.standard_normal((h, n)) / 8).astype(np.float32)
+    Wu = (rng.standard_normal((h, n)) / 8).astype(np.float32)
+    Wd = (rng.standard_normal((h, n)) / 8).astype(np.float32)
+    X = rng.standard_normal((T, n)).astype(np.float32)
+    X[2] = 0.0
+    rc, Y = orc.ffn_fwd(Wg, Wu, Wd, X)
+    assert rc == 0
+    assert np.array_equal(bits(Y), bits(_np_ffn(Wg, Wu, Wd, X)))
+    for slip in ("swap_gu", "wd_untransposed", "wd_per_tensor"):
+        assert not np.array_equal(bits(Y), bits(_np_ffn(Wg, Wu, Wd, X, **{slip: True}))), slip
+    # a rectangular expert (h != n)
+    n, h = 128, 96
+    Wg = (rng.standard_normal((h, n)) / 11).astype(np.float32)
+    Wu = (rng.standard_normal((h, n)) / 11).astype(np.float32)
+    Wd = (rng.standard_normal((h, n)) / 10).astype(np.float32)
+    X = rng.standard_normal((3, n)).astype(np.float32)
+    rc, Y = orc.ffn_fwd(Wg, Wu, Wd, X)
+    assert rc == 0 and np.array_equal(bits(Y), bits(_np_ffn(Wg, Wu, Wd, X)))
+
+
+def test_shared_expert_vs_reference_w8a8_layer(orc, gold):
+    """The reference's own layer in W8A8 mode, one token per call and with
+    zero routed down weights, computes exactly the shared experts of the
+    prepared layer (per-token activations; every down column has the same
+    max|w|, so its per-tensor weight scale is the per-channel one). Its Y
+    must equal the oracle's shared experts summed in fp64, bit for bit, and
+    the numpy rebuild as well."""
+    from golden.gen import shared_case
+    X, Wgate, Wg, Wu, Wd, Wgs, Wus, Wds = shared_case()
+    acc = np.zeros(X.shape, np.float64)
+    acc_np = np.zeros(X.shape, np.float64)
+    for s in range(Wgs.shape[0]):
+        rc, ys = orc.ffn_fwd(Wgs[s], Wus[s], Wds[s], X)
+        assert rc == 0
+        acc += ys.astype(np.float64)
+        acc_np += _np_ffn(Wgs[s], Wus[s], Wds[s], X).astype(np.float64)
+    assert np.array_equal(bits(acc.astype(np.float32)), bits(gold["shared_Y"]))
+    assert np.array_equal(bits(acc_np.astype(np.float32)), bits(gold["shared_Y"]))
+    # the prepared oracle layer with the same weights (routed output 0)
+    L = orc.moe_q(X.shape[1], Wg.shape[1], Wg.shape[0], 2, Wgs.shape[0], Wgs.shape[1],
+                  Wgate, Wg, Wu, Wd, Wgs, Wus, Wds)
+    r = L.fwd(X)
+    assert r["rc"] == 0 and not r["Ye"].any()
+    assert np.array_equal(bits(r["Y"]), bits(gold["shared_Y"]))
+
+
+# ------------------------- accuracy of the prepared low-bit format (tolerance)
+
+def _rel(a, b):
+    """Mean |a - b| over mean |b| (bench/kernel/test_lowbit.c:130-157)."""
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return np.abs(a - b).mean() / (np.abs(b).mean() + 1e-6)
+
+
+def _group_gemm(orc, X, Wnk, b):
+    _, Xq, sx = orc.quant_rows(X)
+    _, codes, sc = orc.lowbit_pack_rows(Wnk, b)
+    rc, Y, _ = orc.gemm_lowbit_group(Xq, sx, codes, sc, b)
+    assert rc == 0
+    return Y
+
+
+def test_group64_accuracy_on_reference_inputs(orc, gold):
+    """The reference's accuracy contract for its low-bit GEMM
+    (bench/kernel/test_lowbit.c:112-157: INT4 rel < 0.10, INT2 rel < 0.45
+    against the fp64 product) holds for the group-64 format that replaces it,
+    on the reference test's own inputs."""
+    from golden.gen import lpat_lut_inputs
+    X, W = lpat_lut_inputs()                          # W [K][H]
+    Yr = X.astype(np.float64) @ W.astype(np.float64)
+    for b, thr in ((4, 0.10), (2, 0.45)):
+        Y = _group_gemm(orc, X, np.ascontiguousarray(W.T), b)
+        assert _rel(Y, Yr) < thr, (b, _rel(Y, Yr))
+        # the reference's own T-MAC result on the same inputs meets it too
+        assert _rel(gold[f"lpat_lut{b}"], Yr) < thr
+        assert np.array_equal(bits(orc.lowbit_gemm_lut(X, W, b)[1]), bits(gold[f"lpat_lut{b}"]))
+
+
+@pytest.mark.parametrize("dist", ["normal", "uniform", "laplace"])
+def test_group64_no_worse_than_tmac(orc, dist):
+    """At the layer's shapes the group-64 GEMM is at least as accurate as
+    the reference's T-MAC GEMM it replaces (src/lowbit.c:158-267, per-column
+    scale and an int8 LUT per 32 activations), both against fp64."""
+    rng = np.random.default_rng(32)
+    for (M, K, N) in ((64, 1024, 256), (64, 256, 1024)):
+        X = rng.standard_normal((M, K)).astype(np.float32)
+        W = {"normal": rng.standard_normal, "uniform": lambda s: rng.uniform(-1, 1, s),
+             "laplace": lambda s: rng.laplace(size=s)}[dist]((N, K)).astype(np.float32)
+        Yr = X.astype(np.float64) @ W.astype(np.float64).T
+        for b in (2, 4):
+            ours = _rel(_group_gemm(orc, X, W, b), Yr)
+            tmac = _rel(orc.lowbit_gemm_lut(X, np.ascontiguousarray(W.T), b)[1], Yr)
+            assert ours <= tmac * 1.01, (dist, M, K, N, b, ours, tmac)
+
+
+def test_prepared_layer_vs_reference_fp32_layer(orc, gold):
+    """The prepared quantised layer against the reference's fp32 layer
+    (jt_moe_fwd_batch, flags off) on a routing without drops: the routing is
+    identical, and the error of the routed expert outputs and of Y is below
+    that of the reference's own true-LUT low-bit layer (flag mode 2, the
+    scheme the group-64 path replaces) on the same inputs."""
+    from golden.gen import accuracy_case
+    args = accuracy_case(int(gold["acc_salt"]))
+    X, Wgate, Wg, Wu, Wd, Wgs, Wus, Wds = args
+    T, n = X.shape
+    E, h = Wg.shape[:2]
+    k, S = gold["acc0_ids"].shape[1], Wgs.shape[0]
+    r = orc.moe_q(n, h, E, k, S, h, *args[1:]).fwd(X)
+    assert r["rc"] == 0
+    assert np.array_equal(r["ids"], gold["acc0_ids"])
+    assert np.array_equal(bits(r["w"]), bits(gold["acc0_w"]))
+    ye_ours, ye_lut = _rel(r["Ye"], gold["acc0_Ysel"]), _rel(gold["acc2_Ysel"], gold["acc0_Ysel"])
+    y_ours, y_lut = _rel(r["Y"], gold["acc0_Y"]), _rel(gold["acc2_Y"], gold["acc0_Y"])
+    print(f"rel error vs fp32 layer: Ye {ye_ours:.3f} (LUT {ye_lut:.3f}), "
+          f"Y {y_ours:.3f} (LUT {y_lut:.3f})")
+    assert ye_ours < ye_lut and y_ours < y_lut

@@ -59,6 +59,25 @@ def read_buf(torch, L, which, dtype, shape):
     return L.read(which, dtype, shape)
 
 
+def check_hidden(jt, L, o, T, k, n, h, max_frac=0.01):
+    """The routed hidden rows' int8 codes and scales against the oracle's
+    (sorted order). Where a row's codes and scale are the oracle's, its
+    expert output Ye must be the oracle's to the bit (the down projection is
+    integer MFMA plus the oracle's group fold); rows whose codes differ (an
+    exp() result on the other side of a rounding boundary) are counted and
+    bounded."""
+    Hq = L.read(jt.BUF_HQ, np.int8, (T * k, h))
+    Hs = L.read(jt.BUF_HSCALE, np.float32, (T * k,))
+    Ye = L.read(jt.BUF_YE, np.float32, (T * k, n))
+    same = np.all(Hq == o["Hq"], axis=1) & (Hs.view(np.uint32) == o["Hs"].view(np.uint32))
+    pairs = o["perm"][same]
+    assert np.array_equal(Ye[pairs].view(np.uint32), o["Ye"][pairs].view(np.uint32))
+    ndiff = int((~same).sum())
+    print(f"  hidden rows with other codes than the oracle's: {ndiff} of {T * k}")
+    assert ndiff <= max(1, int(max_frac * T * k))
+    return ndiff
+
+
 CASES = [
     # n, h, E, k, S, hs, T
     (128, 64, 8, 2, 2, 64, 37),
@@ -107,6 +126,7 @@ def test_layer_router_parity(jt, orc, torch_cuda, case):
         ogu, ogus, odc, ods = OL.routed_codes(e)
         assert np.array_equal(gu, ogu) and np.array_equal(gus, ogus)
         assert np.array_equal(dc, odc) and np.array_equal(ds, ods)
+    check_hidden(jt, L, o, T, k, n, h)
     diff = close(Y, o["Y"])
     print(f"  last-bit differences in Y: {diff} of {Y.size}")
 
@@ -125,6 +145,7 @@ def test_layer_zipf_routed_parity(jt, orc, torch_cuda, T):
     assert o["rc"] == 0
     Ye = read_buf(torch, L, jt.BUF_YE, np.float32, (T * k, n))
     close(Ye, o["Ye"])
+    check_hidden(jt, L, o, T, k, n, h)
     close(Y, o["Y"])
 
 
@@ -145,6 +166,7 @@ def test_layer_decode_fused_zipf(jt, orc, torch_cuda, T):
     Ye = read_buf(torch, L, jt.BUF_YE, np.float32, (T * k, n))
     diff = close(Ye, o["Ye"])
     print(f"  last-bit differences in Ye: {diff} of {Ye.size}")
+    check_hidden(jt, L, o, T, k, n, h)
     close(Y, o["Y"])
 
 
@@ -163,7 +185,44 @@ def test_layer_stress_widths_zipf(jt, orc, torch_cuda, T):
     L, Y = run_layer(jt, torch, n, h, E, k, S, hs, T, W, X, ids, w)
     o = orc.moe_q(n, h, E, k, S, hs, None, W[1], W[2], W[3], *W[4]).fwd(X, ids, w)
     assert o["rc"] == 0
+    check_hidden(jt, L, o, T, k, n, h)
     close(Y, o["Y"])
+
+
+def _rel(a, b):
+    """Mean |a - b| over mean |b| (bench/kernel/test_lowbit.c:130-157)."""
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return np.abs(a - b).mean() / (np.abs(b).mean() + 1e-6)
+
+
+def test_layer_vs_reference_fp32_layer(jt, torch_cuda):
+    """The GPU layer against the reference's fp32 layer (golden vectors of
+    jt_moe_fwd_batch with the flags off, on a routing without drops): the
+    routing is the reference's, and the error of the routed expert outputs
+    and of Y is below that of the reference's own true-LUT low-bit layer
+    (flag mode 2, the scheme the group-64 weights replace)."""
+    import os
+    from golden.gen import accuracy_case
+    torch = torch_cuda
+    gold = np.load(os.path.join(os.path.dirname(__file__), "golden", "ref_vectors.npz"))
+    args = accuracy_case(int(gold["acc_salt"]))
+    X, Wgate, Wg, Wu, Wd, Wgs, Wus, Wds = args
+    T, n = X.shape
+    E, h = Wg.shape[:2]
+    k, S = gold["acc0_ids"].shape[1], Wgs.shape[0]
+    announce(f"layer vs reference fp32 layer T={T} n={n} h={h} E={E} k={k} S={S}")
+    L, Y = run_layer(jt, torch, n, h, E, k, S, h, T, (Wgate, Wg, Wu, Wd, [Wgs, Wus, Wds]), X)
+    ids = L.read(jt.BUF_IDS, np.int32, (T, k))
+    wts = L.read(jt.BUF_WEIGHTS, np.float32, (T, k))
+    assert np.array_equal(ids, gold["acc0_ids"])
+    np.testing.assert_allclose(wts, gold["acc0_w"], rtol=1e-6, atol=0)
+    Ye = L.read(jt.BUF_YE, np.float32, (T * k, n))
+    ye_ours, ye_lut = _rel(Ye, gold["acc0_Ysel"]), _rel(gold["acc2_Ysel"], gold["acc0_Ysel"])
+    y_ours, y_lut = _rel(Y, gold["acc0_Y"]), _rel(gold["acc2_Y"], gold["acc0_Y"])
+    print(f"  rel error vs fp32 layer: Ye {ye_ours:.3f} (LUT {ye_lut:.3f}), "
+          f"Y {y_ours:.3f} (LUT {y_lut:.3f})")
+    assert ye_ours < ye_lut and y_ours < y_lut
 
 
 def test_layer_full_size_token_sample(jt, orc, torch_cuda):
