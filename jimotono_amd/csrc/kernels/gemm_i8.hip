@@ -221,7 +221,7 @@ static hipError_t launch_skinny_xq(const float *X, int ldx, int K, const int8_t 
                                    const float *sB, int M, int N, int Np, int Kp, float *C,
                                    int ldc, int swiglu, uint32_t *err, hipStream_t s) {
     const size_t lds = (size_t)16 * (Kp + 16);
-    static bool attr_set[64];
+    static std::atomic<bool> attr_set[64];  // set once per device; a repeat is harmless
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
@@ -663,7 +663,7 @@ static hipError_t launch_gu_q(int lds, int max_tiles, hipStream_t s, const int8_
                               int8_t *Sq, float *ss, int h, uint32_t *err) {
     auto kern = k_lowbit_gu_q<NW, PPW, NST>;
     // dynamic LDS above 64 KiB must be enabled per device, once
-    static bool attr_set[64];
+    static std::atomic<bool> attr_set[64];  // set once per device; a repeat is harmless
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
@@ -1375,7 +1375,7 @@ static hipError_t launch_lowbit(dim3 grid, hipStream_t s, const int8_t *A, int l
     constexpr int PB = BITS == 2 ? 256 : 512;
     constexpr int lds = NST * (4096 + 8 * PB + 4 * 256);
     auto kern = k_lowbit_grouped<BITS, EPI, NST>;
-    static bool attr_set[64];
+    static std::atomic<bool> attr_set[64];  // set once per device; a repeat is harmless
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
@@ -1404,7 +1404,7 @@ static hipError_t launch_lowbit_res(dim3 grid, int cpb, hipStream_t s, const int
     constexpr int lds_max = LBR_KMAX * 64 + NST * (8 * PB + 4 * 256);
     const int lds = K * 64 + NST * (8 * PB + 4 * 256);
     auto kern = k_lowbit_grouped_res<BITS, EPI, NST>;
-    static bool attr_set[64];
+    static std::atomic<bool> attr_set[64];  // set once per device; a repeat is harmless
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;

@@ -285,7 +285,7 @@ inline hipError_t launch_w8a8_tile(const int8_t *A, int lda, const float *sA, co
     auto kern = k_w8a8_tile<EPI, BM, BN, WGM, WGN, KS, NST, GM>;
     constexpr int lds = NST * (BM + BN) / 16 * KS * 1024;
     // dynamic LDS above 64 KiB must be enabled per device, once
-    static bool attr_set[64];
+    static std::atomic<bool> attr_set[64];  // set once per device; a repeat is harmless
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;

@@ -7,6 +7,7 @@
 // fp64 and the fused form rounds identically to the separate one.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <atomic>
 #include <stdint.h>
 
 #define JT_WAVE 64

@@ -253,7 +253,7 @@ extern "C" int jtk_topk(const float *logits, int rows, int E, int k, int32_t *id
                         int64_t *ids64, float *w, uint32_t *err, hipStream_t s) {
     if (rows <= 0) return 0;
     if (E > 4096) return (int)hipErrorInvalidValue;
-    static bool attr_set[64];
+    static std::atomic<bool> attr_set[64];  // set once per device; a repeat is harmless
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return (int)e;

@@ -794,7 +794,7 @@ extern "C" int jtk_topk_verify(const double *approx, const double *xinfo, const 
     if (T <= 256 && E <= RV_EMAX && k >= 1 && k <= 64 && k <= E && n % 256 == 0) {
         constexpr size_t lds_s = (size_t)(RS_CH + 16 * RS_STRIDE + RV_EMAX) * 4 + 64 * 8 +
                                  (RV_EMAX + 64) * 2;
-        static bool attr_small[64];
+        static std::atomic<bool> attr_small[64];
         int dev = 0;
         hipError_t e = hipGetDevice(&dev);
         if (e != hipSuccess) return (int)e;
@@ -817,7 +817,7 @@ extern "C" int jtk_topk_verify(const double *approx, const double *xinfo, const 
     constexpr size_t lds =
         (size_t)RX_WPB * RX_NBUF * RX_STAGE_B + (size_t)TPB * (RX_EMAX * 4 + 64 * 8 + 64 * 2);
     static_assert(lds <= 160 * 1024, "LDS budget");
-    static bool attr_set[64];
+    static std::atomic<bool> attr_set[64];  // set once per device; a repeat is harmless
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return (int)e;
@@ -927,7 +927,7 @@ extern "C" int jtk_router_logits_small(const float *X, const float *Wg, int T, i
     if (T > RL_TMAX || n % 256 != 0 || E <= 0) return (int)hipErrorInvalidValue;
     const size_t lds = (size_t)(T + 4) * (n + 4) * 4;
     if (lds > 160 * 1024) return (int)hipErrorInvalidValue;
-    static bool attr_set[64];
+    static std::atomic<bool> attr_set[64];  // set once per device; a repeat is harmless
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return (int)e;
