@@ -92,6 +92,19 @@ int jt_hip_ffn_prepare(const float *dWg, const float *dWu, const float *dWd,
 /* dY [T][n] = the expert output for dX [T][n] (fp32). */
 int jt_hip_ffn_fwd(jt_hip_ffn *F, const float *dX, float *dY, int T,
                    void *stream);
+/* jt_hip_ffn_fwd that allocates nothing. No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Its workspace is a fixed 16 MiB device array per GPU, held until the
+ * process ends, instead of the expert's own grow-on-demand buffers.
+ * The workspace of T rows is, each part rounded up to 256 bytes:
+ *   T*round_up(n,64) + 4T + 4T*h + T*round_up(h,64) + 4T bytes;
+ * a larger T returns JT_ERR_NOSUP with errno E2BIG, nothing enqueued
+ * (n = 1024, h = 2816: T <= 1110). Every call on one GPU shares the array,
+ * so calls that overlap on a GPU (two streams, two threads) race; calls in
+ * one stream's order do not. Same outputs as jt_hip_ffn_fwd, bit for bit. */
+int jt_hip_ffn_fwd_noalloc(jt_hip_ffn *F, const float *dX, float *dY, int T,
+                           void *stream);
 void jt_hip_ffn_free(jt_hip_ffn *F);
 
 /* ---- quantised MoE layer ---- */

@@ -77,6 +77,7 @@ _PROTOS = {
     "jt_hip_w8a8_free": ([_vp], None),
     "jt_hip_ffn_prepare": [_vp, _vp, _vp, _i, _i, C.POINTER(_vp)],
     "jt_hip_ffn_fwd": [_vp, _vp, _vp, _i, _vp],
+    "jt_hip_ffn_fwd_noalloc": [_vp, _vp, _vp, _i, _vp],
     "jt_hip_ffn_free": ([_vp], None),
     "jt_hip_moe_prepare": [C.POINTER(_Desc)] + [_vp] * 7 + [C.POINTER(_vp)],
     "jt_hip_moe_fwd": [_vp, _vp, _vp, _i, _vp],
@@ -369,6 +370,13 @@ class FFN:
     def fwd(self, X, Y, stream=None):
         _check(lib().jt_hip_ffn_fwd(self.h, _ptr(X), _ptr(Y), X.shape[0], _stream(stream)),
                "jt_hip_ffn_fwd")
+
+    def fwd_noalloc(self, X, Y, stream=None):
+        """jt_hip_ffn_fwd_noalloc: the same forward on the library's fixed
+        device scratch; returns the return code (JT_ERR_NOSUP when T is too
+        large for the scratch)."""
+        return lib().jt_hip_ffn_fwd_noalloc(self.h, _ptr(X), _ptr(Y), X.shape[0],
+                                            _stream(stream))
 
     def __del__(self):
         if getattr(self, "h", None) and _LIB is not None:

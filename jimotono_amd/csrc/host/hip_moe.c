@@ -153,28 +153,66 @@ static int ffn_reserve(jt_hip_ffn *F, int T, int with_x) {
     return JT_OK;
 }
 
+/* Workspace of one expert forward: Xq [T][Kpn] (zero K padding), sx [T],
+ * S [T][h], Sq [T][Kph] (zero K padding), ss [T]. */
+typedef struct ffn_ws {
+    int8_t *Xq;
+    float *sx, *S;
+    int8_t *Sq;
+    float *ss;
+} ffn_ws;
+
+static ffn_ws ffn_own_ws(const jt_hip_ffn *F) {
+    ffn_ws w = {F->Xq, F->sx, F->S, F->Sq, F->ss};
+    return w;
+}
+
 /* Expert on already-quantised activations Xq [T][Kpn] (zero K padding). */
-static int ffn_run_q(jt_rt *rt, jt_hip_ffn *F, const int8_t *Xq, const float *sx, int T,
-                     float *dY, hipStream_t s, hipEvent_t *ev) {
+static int ffn_run_q(jt_rt *rt, const jt_hip_ffn *F, const ffn_ws *ws, const int8_t *Xq,
+                     const float *sx, int T, float *dY, hipStream_t s, hipEvent_t *ev) {
     if (ev) (void)hipEventRecord(ev[0], s);
     int e = jtk_w8a8_gemm(Xq, F->Kpn, sx, F->gu_P, F->gu_s, T, 2 * F->h, F->Np_gu, F->Kpn,
-                          F->S, F->h, 1, rt->d_err, s);
+                          ws->S, F->h, 1, rt->d_err, s);
     if (ev) (void)hipEventRecord(ev[1], s);
     /* up to 16 rows the down projection quantises the hidden rows itself
      * (timed with the down stage) */
-    const int f = T <= 16 ? jtk_w8a8_gemm_xq(F->S, F->h, F->h, F->d_P, F->d_s, T, F->n, F->Np_d,
-                                             F->Kph, dY, F->n, 0, rt->d_err, s)
+    const int f = T <= 16 ? jtk_w8a8_gemm_xq(ws->S, F->h, F->h, F->d_P, F->d_s, T, F->n,
+                                             F->Np_d, F->Kph, dY, F->n, 0, rt->d_err, s)
                           : (int)hipErrorInvalidValue;
     if (f == (int)hipErrorInvalidValue) {
-        e |= jtk_quant_rows(F->S, T, F->h, F->Sq, F->Kph, F->ss, NULL, rt->d_err, s);
+        e |= jtk_quant_rows(ws->S, T, F->h, ws->Sq, F->Kph, ws->ss, NULL, rt->d_err, s);
         if (ev) (void)hipEventRecord(ev[2], s);
-        e |= jtk_w8a8_gemm(F->Sq, F->Kph, F->ss, F->d_P, F->d_s, T, F->n, F->Np_d, F->Kph, dY,
+        e |= jtk_w8a8_gemm(ws->Sq, F->Kph, ws->ss, F->d_P, F->d_s, T, F->n, F->Np_d, F->Kph, dY,
                            F->n, 0, rt->d_err, s);
     } else {
         if (ev) (void)hipEventRecord(ev[2], s);
         e |= f;
     }
     return e ? jt_rt_err(hipErrorLaunchFailure) : JT_OK;
+}
+
+/* The expert on fp32 rows dX with the workspace ws (T > 0). */
+static int ffn_fwd_on(jt_rt *rt, const jt_hip_ffn *F, const ffn_ws *ws, const float *dX,
+                      float *dY, int T, hipStream_t s) {
+    if (T <= 16) {
+        /* decode: both GEMMs quantise their rows themselves (two launches) */
+        int e = jtk_w8a8_gemm_xq(dX, F->n, F->n, F->gu_P, F->gu_s, T, 2 * F->h, F->Np_gu,
+                                 F->Kpn, ws->S, F->h, 1, rt->d_err, s);
+        if (e != (int)hipErrorInvalidValue) {
+            if (e) return jt_rt_err(hipErrorLaunchFailure);
+            e = jtk_w8a8_gemm_xq(ws->S, F->h, F->h, F->d_P, F->d_s, T, F->n, F->Np_d, F->Kph,
+                                 dY, F->n, 0, rt->d_err, s);
+            if (e == (int)hipErrorInvalidValue) {
+                e = jtk_quant_rows(ws->S, T, F->h, ws->Sq, F->Kph, ws->ss, NULL, rt->d_err, s);
+                e |= jtk_w8a8_gemm(ws->Sq, F->Kph, ws->ss, F->d_P, F->d_s, T, F->n, F->Np_d,
+                                   F->Kph, dY, F->n, 0, rt->d_err, s);
+            }
+            return e ? jt_rt_err(hipErrorLaunchFailure) : JT_OK;
+        }
+    }
+    if (jtk_quant_rows(dX, T, F->n, ws->Xq, F->Kpn, ws->sx, NULL, rt->d_err, s))
+        return jt_rt_err(hipErrorLaunchFailure);
+    return ffn_run_q(rt, F, ws, ws->Xq, ws->sx, T, dY, s, NULL);
 }
 
 int jt_hip_ffn_fwd(jt_hip_ffn *F, const float *dX, float *dY, int T, void *stream) {
@@ -184,26 +222,45 @@ int jt_hip_ffn_fwd(jt_hip_ffn *F, const float *dX, float *dY, int T, void *strea
     if (T == 0) return JT_OK;
     int rc = ffn_reserve(F, T, 1);
     if (rc != JT_OK) return rc;
-    hipStream_t s = (hipStream_t)stream; /* NULL: the HIP null stream */
-    if (T <= 16) {
-        /* decode: both GEMMs quantise their rows themselves (two launches) */
-        int e = jtk_w8a8_gemm_xq(dX, F->n, F->n, F->gu_P, F->gu_s, T, 2 * F->h, F->Np_gu,
-                                 F->Kpn, F->S, F->h, 1, rt->d_err, s);
-        if (e != (int)hipErrorInvalidValue) {
-            if (e) return jt_rt_err(hipErrorLaunchFailure);
-            e = jtk_w8a8_gemm_xq(F->S, F->h, F->h, F->d_P, F->d_s, T, F->n, F->Np_d, F->Kph,
-                                 dY, F->n, 0, rt->d_err, s);
-            if (e == (int)hipErrorInvalidValue) {
-                e = jtk_quant_rows(F->S, T, F->h, F->Sq, F->Kph, F->ss, NULL, rt->d_err, s);
-                e |= jtk_w8a8_gemm(F->Sq, F->Kph, F->ss, F->d_P, F->d_s, T, F->n, F->Np_d,
-                                   F->Kph, dY, F->n, 0, rt->d_err, s);
-            }
-            return e ? jt_rt_err(hipErrorLaunchFailure) : JT_OK;
-        }
+    const ffn_ws ws = ffn_own_ws(F);
+    return ffn_fwd_on(rt, F, &ws, dX, dY, T, (hipStream_t)stream); /* NULL: the null stream */
+}
+
+/* Byte offsets of the workspace of a T-row forward inside one buffer, each
+ * part 256-byte aligned; returns the total. */
+static size_t ffn_ws_layout(const jt_hip_ffn *F, int T, size_t off[5]) {
+    const size_t t = (size_t)T;
+    const size_t sz[5] = {t * (size_t)F->Kpn, t * 4, t * (size_t)F->h * 4, t * (size_t)F->Kph,
+                          t * 4};
+    size_t at = 0;
+    for (int i = 0; i < 5; i++) {
+        off[i] = at;
+        at += jt_round_up(sz[i], 256);
     }
-    if (jtk_quant_rows(dX, T, F->n, F->Xq, F->Kpn, F->sx, NULL, rt->d_err, s))
-        return jt_rt_err(hipErrorLaunchFailure);
-    return ffn_run_q(rt, F, F->Xq, F->sx, T, dY, s, NULL);
+    return at;
+}
+
+int jt_hip_ffn_fwd_noalloc(jt_hip_ffn *F, const float *dX, float *dY, int T, void *stream) {
+    if (!F || !dX || !dY || T < 0) FAIL(JT_ERR_INVAL, EINVAL);
+    size_t off[5];
+    if (T > 0 && ffn_ws_layout(F, T, off) > JT_SCRATCH_BYTES) FAIL(JT_ERR_NOSUP, E2BIG);
+    jt_rt *rt = jt_rt_get(); /* set up already: F was prepared through it */
+    if (!rt) return JT_ERR_IO;
+    if (T == 0) return JT_OK;
+    uint8_t *base = jtk_scratch();
+    if (!base) FAIL(JT_ERR_IO, EIO);
+    const ffn_ws ws = {(int8_t *)(base + off[0]), (float *)(base + off[1]),
+                       (float *)(base + off[2]), (int8_t *)(base + off[3]),
+                       (float *)(base + off[4])};
+    hipStream_t s = (hipStream_t)stream; /* NULL: the HIP null stream */
+    /* the scratch keeps the previous call's bytes: the GEMMs read the K
+     * padding of the code rows, which must be zero (a fill kernel, not a
+     * memset node, so the call can be captured) */
+    int e = 0;
+    if (F->Kpn > F->n) e |= jtk_scratch_zero((uint32_t *)ws.Xq, (int64_t)T * F->Kpn / 4, s);
+    if (F->Kph > F->h) e |= jtk_scratch_zero((uint32_t *)ws.Sq, (int64_t)T * F->Kph / 4, s);
+    if (e) return jt_rt_err(hipErrorLaunchFailure);
+    return ffn_fwd_on(rt, F, &ws, dX, dY, T, s);
 }
 
 /* ======================= MoE layer ======================= */
@@ -501,9 +558,11 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
     if (fork) {
         le |= (int)hipEventRecord(L->ev_fork, s);
         for (int i = 0; i < L->nside; i++) le |= (int)hipStreamWaitEvent(L->side[i], L->ev_fork, 0);
-        for (int e = 0; e < S; e++) /* launch errors are collected; the join still happens */
-            le |= ffn_run_q(rt, L->sh[e], L->Xq, L->sx, T, L->Ys + (size_t)e * T * n,
+        for (int e = 0; e < S; e++) { /* launch errors are collected; the join still happens */
+            const ffn_ws ws = ffn_own_ws(L->sh[e]);
+            le |= ffn_run_q(rt, L->sh[e], &ws, L->Xq, L->sx, T, L->Ys + (size_t)e * T * n,
                             L->side[e % L->nside], NULL);
+        }
         for (int i = 0; i < L->nside; i++) le |= (int)hipEventRecord(L->ev_join[i], L->side[i]);
     }
     /* 16-row tiles when experts average at most 16 rows; the single-launch
@@ -590,7 +649,8 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
     } else {
         for (int e = 0; e < S; e++) {
             hipEvent_t *ev = L->prof ? &L->ev[slot][ST_N + 1 + 3 * e] : NULL;
-            rc = ffn_run_q(rt, L->sh[e], L->Xq, L->sx, T, L->Ys + (size_t)e * T * n, s, ev);
+            const ffn_ws ws = ffn_own_ws(L->sh[e]);
+            rc = ffn_run_q(rt, L->sh[e], &ws, L->Xq, L->sx, T, L->Ys + (size_t)e * T * n, s, ev);
             if (rc != JT_OK) return rc;
         }
     }

@@ -49,6 +49,15 @@ jt_rt *jt_rt_get(void) {
         errno = EIO;
         return NULL;
     }
+    /* every code object now, not at the first launch of one of its kernels
+     * (a no-allocation entry point must not make the runtime allocate) */
+    if (jtk_preload() != 0) {
+        errno = EIO;
+        return NULL;
+    }
+    /* the no-allocation entry points' scratch address on this device; if the
+     * lookup fails they report JT_ERR_IO and everything else still works */
+    (void)jtk_scratch_init();
     g_rt.ready = 1;
     return &g_rt;
 }

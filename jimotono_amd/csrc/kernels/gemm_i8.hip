@@ -1514,3 +1514,10 @@ extern "C" int jtk_lowbit_grouped(int bits, const int8_t *A, int lda, const floa
                                                      N, K, out, ldo, err);
     return (int)e;
 }
+
+// Load this file's code object now: the runtime otherwise loads it, and
+// allocates device memory for it, at the first launch of one of its kernels.
+extern "C" int jtk_preload_gemm_i8(void) {
+    hipFuncAttributes a;
+    return (int)hipFuncGetAttributes(&a, (const void *)(k_w8a8_skinny<EPI_PLAIN, 1, 0>));
+}

@@ -13,6 +13,19 @@
 extern "C" {
 #endif
 
+/* noalloc.hip: a fixed device scratch array of JT_SCRATCH_BYTES per device,
+ * for entry points that must not allocate. jtk_scratch_init looks up the
+ * current device's address of the array once (at the library's set-up);
+ * jtk_scratch returns it (NULL before the set-up on that device). */
+#define JT_SCRATCH_BYTES ((size_t)16 << 20)
+int jtk_scratch_init(void);
+void *jtk_scratch(void);
+/* p[0..n) = 0 (a fill kernel whose code object is loaded at set-up) */
+int jtk_scratch_zero(uint32_t *p, int64_t n, hipStream_t s);
+/* Load every code object of the library on the current device, so that no
+ * later launch makes the runtime load one (and allocate device memory). */
+int jtk_preload(void);
+
 /* quant.hip */
 int jtk_quant_rows(const float *X, int64_t rows, int cols, int8_t *Q, int64_t ldq,
                    float *scale, const int32_t *row_count, uint32_t *err, hipStream_t s);

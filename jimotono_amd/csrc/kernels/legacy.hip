@@ -345,3 +345,10 @@ extern "C" int jtk_lowbit_fq_cols(float *W, int k, int h, int bits, float *ws, u
                        k, h, bits, ws);
     return (int)hipGetLastError();
 }
+
+// Load this file's code object now: the runtime otherwise loads it, and
+// allocates device memory for it, at the first launch of one of its kernels.
+extern "C" int jtk_preload_legacy(void) {
+    hipFuncAttributes a;
+    return (int)hipFuncGetAttributes(&a, (const void *)(k_gemm_f32));
+}

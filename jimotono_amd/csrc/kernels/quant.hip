@@ -608,3 +608,10 @@ extern "C" int jtk_quant_weight_rows(const float *W, int64_t ld_n, int64_t ld_k,
                        W, ld_n, ld_k, N, K, Q, scale, err);
     return (int)hipGetLastError();
 }
+
+// Load this file's code object now: the runtime otherwise loads it, and
+// allocates device memory for it, at the first launch of one of its kernels.
+extern "C" int jtk_preload_quant(void) {
+    hipFuncAttributes a;
+    return (int)hipFuncGetAttributes(&a, (const void *)(k_quant_rows));
+}

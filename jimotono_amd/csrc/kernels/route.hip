@@ -988,3 +988,10 @@ extern "C" int jtk_bcast_f32(float *dst, int64_t n, const float *src, hipStream_
                        src);
     return (int)hipGetLastError();
 }
+
+// Load this file's code object now: the runtime otherwise loads it, and
+// allocates device memory for it, at the first launch of one of its kernels.
+extern "C" int jtk_preload_route(void) {
+    hipFuncAttributes a;
+    return (int)hipFuncGetAttributes(&a, (const void *)(k_topk));
+}

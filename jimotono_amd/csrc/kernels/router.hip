@@ -943,3 +943,10 @@ extern "C" int jtk_router_logits_small(const float *X, const float *Wg, int T, i
                        n, logits, Xq, sx, err);
     return (int)hipGetLastError();
 }
+
+// Load this file's code object now: the runtime otherwise loads it, and
+// allocates device memory for it, at the first launch of one of its kernels.
+extern "C" int jtk_preload_router(void) {
+    hipFuncAttributes a;
+    return (int)hipFuncGetAttributes(&a, (const void *)(k_router_codes));
+}
