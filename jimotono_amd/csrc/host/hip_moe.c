@@ -365,7 +365,9 @@ int jt_hip_moe_prepare(const jt_hip_moe_desc *desc, const float *dWgate, const f
     if (d.n_shared > 0 && (!dWg_s || !dWu_s || !dWd_s || d.h_shared <= 0 ||
                            d.h_shared % 16 != 0 || d.h_shared > JT_BWD_MAX_WIDE))
         FAIL(JT_ERR_INVAL, EINVAL);
-    if ((int64_t)d.max_tokens * d.topk > (int64_t)64 * 65535) FAIL(JT_ERR_INVAL, EINVAL);
+    /* the tile list of the largest forward must fit one launch grid
+     * (65535 blocks): 64-row tiles plus one short tile per expert */
+    if ((int64_t)d.max_tokens * d.topk / 64 + d.n_experts > 65535) FAIL(JT_ERR_INVAL, EINVAL);
     jt_rt *rt = jt_rt_get();
     if (!rt) return JT_ERR_IO;
     jt_hip_moe *L = calloc(1, sizeof(*L));

@@ -293,9 +293,8 @@ int jt_routing_topk(const float *logits, size_t n, size_t k, size_t *out_ids,
                     float *out_weights) {
     if (!logits || !out_ids || !out_weights) FAIL(JT_ERR_INVAL, EINVAL);
     if (n == 0 || k == 0 || k > n) FAIL(JT_ERR_INVAL, EINVAL);
-    /* one wavefront holds the selection: the kernel supports n <= 4096 and
-     * k <= 64, the reference's layer limits (moe_layer.h:52-53) */
-    if (n > JT_MOE_MAX_EXPERTS || k > JT_MOE_MAX_TOPK) FAIL(JT_ERR_NOSUP, EINVAL);
+    /* indices are 31-bit on the device (an 8 GiB row of logits) */
+    if (n > 0x7fffffffu) FAIL(JT_ERR_NOSUP, EINVAL);
     jt_rt *rt = jt_rt_get();
     if (!rt) return JT_ERR_IO;
     int rc = JT_OK;
@@ -305,7 +304,13 @@ int jt_routing_topk(const float *logits, size_t n, size_t k, size_t *out_ids,
     float *dw = jt_rt_buf(rt, JT_SLOT_D, k * 4, &rc);
     if (!dl || !di || !di64 || !dw) return rc;
     if ((rc = jt_rt_h2d(rt, dl, logits, n * 4)) != JT_OK) return rc;
-    LAUNCHED(jtk_topk(dl, 1, (int)n, (int)k, di, di64, dw, rt->d_err, rt->stream));
+    /* one wavefront holds rows up to the layer's limits (moe_layer.h:52-53);
+     * longer rows or larger k take the block kernel */
+    if (n <= JT_MOE_MAX_EXPERTS && k <= JT_MOE_MAX_TOPK) {
+        LAUNCHED(jtk_topk(dl, 1, (int)n, (int)k, di, di64, dw, rt->d_err, rt->stream));
+    } else {
+        LAUNCHED(jtk_topk_block(dl, (int64_t)n, (int64_t)k, di64, dw, rt->d_err, rt->stream));
+    }
     if ((rc = finish(rt)) != JT_OK) return rc;
     int64_t *tmp = malloc(k * 8);
     if (!tmp) FAIL(JT_ERR_NOMEM, ENOMEM);

@@ -68,6 +68,11 @@ typedef struct {
  * (src/moe_layer.c:228-274). */
 static int w8a8_pc(jt_rt *rt, w8_ws *w, const float *A, const float *Brow, float *C, int M,
                    int N, int K) {
+    /* the reference's W8A8 GEMM limit, src/w8a8.c:926-929 (EINVAL) */
+    if (M > JT_BWD_MAX_WIDE || N > JT_BWD_MAX_WIDE || K > JT_BWD_MAX_WIDE) {
+        errno = EINVAL;
+        return JT_ERR_INVAL;
+    }
     const int Kp = (int)jt_round_up((size_t)K, 64), Np = (int)jt_round_up((size_t)N, 128);
     hipStream_t s = rt->stream;
     int le = jtk_quant_tensor(A, (int64_t)M * K, w->Bq, w->sA1, rt->d_scratch, rt->d_err, s);
@@ -85,6 +90,11 @@ static int w8a8_pc(jt_rt *rt, w8_ws *w, const float *A, const float *Brow, float
 /* C[M][N] = A[M][K] x Bkn[K][N], both per tensor (src/moe_layer.c:185-223). */
 static int w8a8_pt(jt_rt *rt, w8_ws *w, const float *A, const float *Bkn, float *C, int M,
                    int N, int K) {
+    /* the reference's W8A8 GEMM limit, src/w8a8.c:926-929 (EINVAL) */
+    if (M > JT_BWD_MAX_WIDE || N > JT_BWD_MAX_WIDE || K > JT_BWD_MAX_WIDE) {
+        errno = EINVAL;
+        return JT_ERR_INVAL;
+    }
     const int Kp = (int)jt_round_up((size_t)K, 64), Np = (int)jt_round_up((size_t)N, 128);
     hipStream_t s = rt->stream;
     int le = jtk_quant_tensor(A, (int64_t)M * K, w->Bq, w->sA1, rt->d_scratch, rt->d_err, s);

@@ -102,6 +102,10 @@ int jtk_topk_verify(const double *approx, const double *xinfo, const double *win
 /* route.hip */
 int jtk_router_logits(const float *X, const float *Wg, int T, int E, int n, float *logits,
                       uint32_t *err, hipStream_t s);
+/* one row of any length n < 2^31 and any k <= n (one block; the legacy
+ * jt_routing_topk beyond the wavefront kernel's n <= 4096, k <= 64) */
+int jtk_topk_block(const float *logits, int64_t n, int64_t k, int64_t *ids64, float *w,
+                   uint32_t *err, hipStream_t s);
 int jtk_topk(const float *logits, int rows, int E, int k, int32_t *ids, int64_t *ids64,
              float *w, uint32_t *err, hipStream_t s);
 int jtk_sort(const int32_t *ids, int Tk, int E, int64_t cap, int32_t *rank, int32_t *cnt,

@@ -269,6 +269,96 @@ extern "C" int jtk_topk(const float *logits, int rows, int E, int k, int32_t *id
     return (int)hipGetLastError();
 }
 
+// Top-k of one row of any length n (< 2^31) and any k <= n, in one block
+// of 1024 threads: the reference's selection order is the descending order
+// of the keys (order-preserving value bits with -0 folded into +0, then ~i
+// so ties go to the lower index), so round p takes the largest key below
+// round p-1's key with a streaming block max and needs no taken-set.
+// Elements at -inf never beat the masked ones: once only -inf remains
+// (p >= c, c = number of values above -inf) the reference's scan keeps its
+// first index, 0. The softmax then runs over the k selected logits in
+// selection order as in topk_wave (one thread: the fp64 sum is sequential).
+#define TKB_THREADS 1024
+__global__ __launch_bounds__(TKB_THREADS) void k_topk_block(const float *__restrict__ lg,
+                                                            int64_t n, int64_t k,
+                                                            int64_t *__restrict__ ids64,
+                                                            float *__restrict__ w,
+                                                            uint32_t *err) {
+    __shared__ uint64_t red[TKB_THREADS / 64];
+    __shared__ int64_t sh_c;
+    __shared__ int sh_nan;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    // NaN check and c
+    int nan = 0;
+    int64_t c = 0;
+    for (int64_t i = tid; i < n; i += TKB_THREADS) {
+        const float v = lg[i];
+        nan |= isnan(v);
+        c += v > -__builtin_inff();
+    }
+    if (tid == 0) {
+        sh_c = 0;
+        sh_nan = 0;
+    }
+    __syncthreads();
+    nan = wave_or_i(nan);
+    for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o);
+    if (lane == 0) {
+        atomicAdd((unsigned long long *)&sh_c, (unsigned long long)c);
+        if (nan) atomicOr(&sh_nan, 1);
+    }
+    __syncthreads();
+    if (sh_nan) {
+        if (tid == 0) raise_err(err, EF_NONFINITE_MID);
+        return;
+    }
+    const int64_t cnt = sh_c, kk = k < cnt ? k : cnt;
+    uint64_t prev = ~0ull;
+    for (int64_t p = 0; p < kk; p++) {
+        uint64_t best = 0;
+        for (int64_t i = tid; i < n; i += TKB_THREADS) {
+            uint32_t u = __builtin_bit_cast(uint32_t, lg[i] + 0.0f);
+            u ^= (u >> 31) ? 0xffffffffu : 0x80000000u;
+            const uint64_t key = ((uint64_t)u << 32) | (uint32_t)~(uint32_t)i;
+            best = (key < prev && key > best) ? key : best;
+        }
+        best = wave_max_u64(best);
+        if (lane == 0) red[wv] = best;
+        __syncthreads();
+        best = red[0];
+        for (int j = 1; j < TKB_THREADS / 64; j++) best = red[j] > best ? red[j] : best;
+        __syncthreads();  // red[] is rewritten next round
+        prev = best;
+        if (tid == 0) ids64[p] = (int64_t)(uint32_t)~(uint32_t)best;
+    }
+    for (int64_t p = kk + tid; p < k; p += TKB_THREADS) ids64[p] = 0;
+    __syncthreads();
+    if (tid != 0) return;
+    // softmax over the selected, in selection order (src/routing.c:56-75);
+    // ids from kk on are 0 (written by other threads: not read back)
+    const float mx = lg[kk > 0 ? ids64[0] : 0];
+    double sum = 0.0;
+    for (int64_t p = 0; p < k; p++) {
+        const double e = exp((double)lg[p < kk ? ids64[p] : 0] - (double)mx);
+        sum += e;
+        w[p] = (float)e;
+    }
+    if (!(sum > 0.0) || !isfinite(sum)) {
+        raise_err(err, EF_NONFINITE_MID);
+        return;
+    }
+    const float inv = (float)(1.0 / sum);
+    for (int64_t p = 0; p < k; p++) w[p] = w[p] * inv;
+}
+
+extern "C" int jtk_topk_block(const float *logits, int64_t n, int64_t k, int64_t *ids64,
+                              float *w, uint32_t *err, hipStream_t s) {
+    if (n <= 0 || k <= 0 || k > n || n > 0x7fffffffLL) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_topk_block, dim3(1), dim3(TKB_THREADS), 0, s, logits, n, k, ids64, w,
+                       err);
+    return (int)hipGetLastError();
+}
+
 // ---------------- stable expert sort ----------------
 // Pairs q = 0..Tk-1 with expert ids[q]. Blocks of 256 consecutive pairs.
 //  hist   : rank[q] = #{q' < q in the block : ids[q'] == ids[q]},

@@ -607,6 +607,8 @@ static int fq_cols(float *W, int k, int h, int bits) {
 /* A per-tensor, B per-channel, B given as [N][K] (src/moe_layer.c:228-274). */
 static int w8a8_pc(const float *A, const float *Brow, float *C, int M, int N,
                    int K) {
+    /* M, N, K <= JT_BWD_MAX_WIDE (src/w8a8.c:926-929) */
+    if (M > 4096 || N > 4096 || K > 4096) return RC_INVAL;
     int rc = RC_NOMEM;
     int8_t *Aq = malloc((size_t)M * K), *BqT = malloc((size_t)N * K),
            *Bq = malloc((size_t)N * K);
@@ -626,6 +628,7 @@ out:
 /* Both sides per tensor, B given as [K][N] (src/moe_layer.c:185-223). */
 static int w8a8_pt(const float *A, const float *Bkn, float *C, int M, int N,
                    int K) {
+    if (M > 4096 || N > 4096 || K > 4096) return RC_INVAL; /* src/w8a8.c:926-929 */
     int rc = RC_NOMEM;
     int8_t *Aq = malloc((size_t)M * K), *Bq = malloc((size_t)K * N);
     float sA = 1.0f, sB = 1.0f;

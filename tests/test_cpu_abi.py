@@ -144,3 +144,42 @@ def test_product_never_imports_the_oracle():
             if f.endswith((".py", ".c", ".h", ".hip", "Makefile")):
                 text = open(os.path.join(dp, f), errors="ignore").read()
                 assert "oracle" not in text.replace("oracle/", "").lower() or f == "README", f
+
+
+def test_tmac_size_functions(lib):
+    """jt_tmac_qlut_bytes / jt_tmac_param_bytes (src/tmac.c:168-228): host
+    arithmetic only, so they run without a GPU. Checked against the closed
+    forms n*(k/4)*8 and n*(k/32)*4, the fail-closed cases (NULL, zero, k not
+    a multiple of the group, size_t overflow -> ENOMEM) and, when it has been
+    built, the reference's own functions on the same arguments."""
+    fq, fp = lib.jt_tmac_qlut_bytes, lib.jt_tmac_param_bytes
+    for f in (fq, fp):
+        f.argtypes = [C.c_size_t, C.c_size_t, C.POINTER(C.c_size_t)]
+    ref = None
+    from oracle.pyoracle import REF_SO, ref_available
+    if ref_available():
+        ref = C.CDLL(REF_SO, use_errno=True)
+        for name in ("jt_tmac_qlut_bytes", "jt_tmac_param_bytes"):
+            getattr(ref, name).argtypes = [C.c_size_t, C.c_size_t, C.POINTER(C.c_size_t)]
+    big = (1 << 64) - 1
+    cases = [(1, 32), (3, 64), (7, 1024), (256, 4096), (0, 32), (4, 0), (4, 33), (4, 36),
+             (big, 32), (big // 8 + 1, 32), (big // 64, 32)]
+    for n, k in cases:
+        for f, name, g, per in ((fq, "jt_tmac_qlut_bytes", 4, 8),
+                                (fp, "jt_tmac_param_bytes", 32, 4)):
+            out = C.c_size_t(12345)
+            C.set_errno(0)
+            rc = f(n, k, C.byref(out))
+            er = C.get_errno()
+            if n == 0 or k == 0 or k % g:
+                assert rc == 2 and er == E.EINVAL and out.value == 0, (name, n, k)
+            elif n * (k // g) * per > big:
+                assert rc == 1 and er == E.ENOMEM and out.value == 0, (name, n, k)
+            else:
+                assert rc == 0 and out.value == n * (k // g) * per, (name, n, k)
+            if ref is not None:
+                o2 = C.c_size_t(12345)
+                C.set_errno(0)
+                rc2 = getattr(ref, name)(n, k, C.byref(o2))
+                assert (rc2, C.get_errno(), o2.value) == (rc, er, out.value), (name, n, k)
+    assert fq(4, 32, None) == 2 and fp(4, 32, None) == 2

@@ -641,3 +641,23 @@ def test_prepared_layer_vs_reference_fp32_layer(orc, gold):
     print(f"rel error vs fp32 layer: Ye {ye_ours:.3f} (LUT {ye_lut:.3f}), "
           f"Y {y_ours:.3f} (LUT {y_lut:.3f})")
     assert ye_ours < ye_lut and y_ours < y_lut
+
+
+def test_w8a8_layer_row_limit_vs_reference(orc, ref):
+    """With the W8A8 flag on, the reference's layer runs its shared experts
+    as one W8A8 GEMM of M = T rows and fails closed with EINVAL above
+    JT_BWD_MAX_WIDE = 4096 rows (src/w8a8.c:926-929); so does the oracle."""
+    rng = np.random.default_rng(33)
+    T, n, h, E, k, S = 4097, 64, 64, 8, 2, 1
+    args = [rng.standard_normal((T, n)).astype(np.float32)] + [
+        (rng.standard_normal(s) / 8).astype(np.float32)
+        for s in [(E, n), (E, h, n), (E, h, n), (E, h, n), (S, h, n), (S, h, n), (S, h, n)]]
+    r1 = orc.moe_fwd_batch(*args, k, 1.5, 1, 0)
+    r2 = ref.moe_fwd_batch(*args, k, 1.5, 1, 0)
+    assert r1["rc"] == r2["rc"] == 2
+    assert not r1["Y"].any() and not r2["Y"].any()
+    # one row fewer passes in both
+    r1 = orc.moe_fwd_batch(*(a[:4096] if i == 0 else a for i, a in enumerate(args)), k, 1.5, 1, 0)
+    r2 = ref.moe_fwd_batch(*(a[:4096] if i == 0 else a for i, a in enumerate(args)), k, 1.5, 1, 0)
+    assert r1["rc"] == r2["rc"] == 0
+    assert np.array_equal(bits(r1["Y"]), bits(r2["Y"]))

@@ -10,6 +10,8 @@ Bit-exact except where the value passes through exp (softmax weights,
 SwiGLU): there the reference's own tolerance applies (test_routing.c:35-37,
 test_moe_layer.c:146-189).
 """
+import errno
+
 import numpy as np
 import pytest
 
@@ -167,3 +169,62 @@ def test_moe_fwd_batch_known_answer(jt):
     assert r["rc"] == 0 and list(r["ids"][0]) == [0, 1]
     assert abs(r["Y"][0, 0] - 0.14582792210843093) < 1e-5
     assert abs(r["Y"][0, 1] - 0.08212054137232436) < 1e-5
+
+
+def test_moe_fwd_batch_w8a8_row_limit(jt, orc):
+    """With the W8A8 flag the shared experts are one W8A8 GEMM of M = T rows;
+    above 4096 rows the reference fails closed with EINVAL (src/w8a8.c:926-929)
+    and writes nothing, as the oracle does."""
+    announce("moe_fwd_batch w8a8 T=4097")
+    rng = np.random.default_rng(4097)
+    T, n, h, E, k, S = 4097, 64, 64, 8, 2, 1
+    X = rng.standard_normal((T, n)).astype(np.float32)
+    W = [(rng.standard_normal(s) / 8).astype(np.float32)
+         for s in [(E, n), (E, h, n), (E, h, n), (E, h, n), (S, h, n), (S, h, n), (S, h, n)]]
+    lib = jt.lib()
+    assert lib.jt_w8a8_set_enabled(1) == 0
+    try:
+        r = jt.moe_fwd_batch(X, *W, k, 1.5)
+        err = jt.errno()
+    finally:
+        lib.jt_w8a8_set_enabled(0)
+    o = orc.moe_fwd_batch(X, *W, k, 1.5, 1, 0)
+    assert r["rc"] == o["rc"] == 2 and err == errno.EINVAL
+    assert not r["Y"].any() and not r["ids"].any()
+
+
+@pytest.mark.parametrize("n,k,mode", [(8192, 100, "normal"), (4097, 8, "normal"),
+                                      (100, 65, "normal"), (10000, 50, "ties"),
+                                      (5000, 300, "masked"), (70000, 200, "normal"),
+                                      (4096, 64, "normal")])
+def test_routing_topk_any_n_k(jt, orc, n, k, mode):
+    """jt_routing_topk for any n and any k <= n (src/routing.c:16-76): the
+    same ids as the reference's strict-> scan, including ties (lower index
+    first), rows with fewer than k values above -inf (the remaining rounds
+    keep index 0), and the softmax weights to the reference's tolerance."""
+    announce(f"routing_topk n={n} k={k} {mode}")
+    rng = np.random.default_rng(n + k)
+    lg = rng.standard_normal(n).astype(np.float32)
+    if mode == "ties":
+        lg = np.round(lg * 2).astype(np.float32) / 2      # few distinct values
+        lg[rng.integers(0, n, 30)] = -0.0
+    if mode == "masked":
+        lg[rng.permutation(n)[:n - 200]] = -np.inf        # 200 finite values < k
+    rc, ids, w = jt.routing_topk(lg, k)
+    rc2, ids2, w2 = orc.topk(lg, k)
+    assert rc == rc2 == 0
+    assert np.array_equal(ids, ids2)
+    np.testing.assert_allclose(w, w2, rtol=1e-6, atol=1e-12)
+    if mode == "masked":
+        assert (ids[200:] == 0).all()
+
+
+def test_routing_topk_large_rejects(jt, orc):
+    """A +inf among the selected makes the softmax non-finite and a NaN
+    anywhere is rejected: rc 2 (EINVAL) in both, beyond the wavefront kernel."""
+    announce("routing_topk large rejects")
+    lg = np.random.default_rng(1).standard_normal(6000).astype(np.float32)
+    lg[4321] = np.inf
+    assert jt.routing_topk(lg, 70)[0] == orc.topk(lg, 70)[0] == 2
+    lg[4321] = np.nan
+    assert jt.routing_topk(lg, 70)[0] == orc.topk(lg, 70)[0] == 2

@@ -98,6 +98,10 @@ CASES = [
     (512, 256, 32, 4, 0, 64, 40),
     (768, 256, 16, 2, 1, 64, 100),
     (1024, 256, 256, 8, 2, 512, 16),
+    # three to eight shared experts in the combine, with k <= 8 and k > 8
+    (256, 128, 16, 4, 3, 64, 100),
+    (128, 64, 32, 12, 8, 64, 50),
+    (128, 64, 64, 16, 5, 128, 9),
 ]
 
 
