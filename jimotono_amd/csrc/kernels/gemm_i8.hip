@@ -521,12 +521,14 @@ __global__ __launch_bounds__(64 * NW) void k_lowbit_gu_q(
     __shared__ double rsd[64];
     __shared__ float rinv[64];
     __shared__ uint32_t rbad[64];
+    __shared__ double exp_tab[64];
     const int tile = blockIdx.x;
     if (tile >= *ntiles) return;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int4 td = ((const int4 *)tiles)[tile];  // {expert, first sorted row, rows}
     const int e = td.x, pos0 = td.y, nrows = td.z;
+    const double tabv = exp_tab_load(lane);  // staged in LDS for the SwiGLU
     if (tid < 64) {
         const int src = perm[pos0 + min(tid, nrows - 1)] / topk;
         rowsrc[tid] = src;
@@ -597,6 +599,8 @@ __global__ __launch_bounds__(64 * NW) void k_lowbit_gu_q(
     const int lr = (lane >> 4) * 4, lc = lane & 15;
     uint32_t flags = 0;
     float sv[4][NJ][4];
+    exp_tab_stage(exp_tab, lane, tabv);
+    uint32_t gmx = 0;  // max |g|, |u| bits: non-finite iff >= those of +inf
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -608,8 +612,8 @@ __global__ __launch_bounds__(64 * NW) void k_lowbit_gu_q(
                 sv[i][jj][r] = 0.0f;
                 if (rr < nrows) {
                     const float gv = T[i][2 * jj][r] * sa, uv = T[i][2 * jj + 1][r] * sa;
-                    if (!isfinite(gv) || !isfinite(uv)) flags |= EF_RANGE;
-                    if (!silu_mul(gv, uv, &sv[i][jj][r])) flags |= EF_NONFINITE_MID;
+                    gmx = max(gmx, max(abs_bits(gv), abs_bits(uv)));
+                    (void)silu_mul(gv, uv, &sv[i][jj][r], exp_tab);
                 }
             }
             uint32_t m = 0;
@@ -618,6 +622,7 @@ __global__ __launch_bounds__(64 * NW) void k_lowbit_gu_q(
             m = row16_allmax_u(m);  // over this wave's 16 * NJ channels of the row
             if (lc == 0) pmax[wave][rr] = m;
         }
+    if (gmx >= 0x7f800000u) flags |= EF_RANGE | EF_NONFINITE_MID;
     __syncthreads();
     // ---- the row quantiser's parameters, once per row ----
     if (tid < 64) {
@@ -1186,9 +1191,13 @@ __global__ __launch_bounds__(64 * RF_WAVES) void k_routed_ffn16(
     __shared__ __attribute__((aligned(16))) int8_t hq[16 * RF_QSTR];
     __shared__ float rsa[16], rsq[16];
     __shared__ int rdst[16];
+    __shared__ double exp_tab[64];
     const int tile = blockIdx.x;
     if (tile >= *ntiles) return;
     const int lane = threadIdx.x & 63;
+    // the SwiGLU's exp table entry, requested before the weights so that its
+    // wait does not wait for them
+    const double tabv = exp_tab_load(lane);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int4 td = tiles[tile];  // {expert, first sorted row, rows}
     const int e = td.x, pos0 = td.y, nrows = td.z;
@@ -1291,6 +1300,7 @@ __global__ __launch_bounds__(64 * RF_WAVES) void k_routed_ffn16(
             ub[row * RF_HSTR + 16 * (HB * wave + j) + lc] = uv;
         }
     }
+    exp_tab_stage(exp_tab, lane, tabv);
     lds_barrier();
     // ---- SwiGLU and the per-row int8 codes of h, wave w on row w ----
 #pragma unroll 1
@@ -1298,10 +1308,10 @@ __global__ __launch_bounds__(64 * RF_WAVES) void k_routed_ffn16(
         const float4 g4 = *(const float4 *)(gb + row * RF_HSTR + lane * 4);
         const float4 u4 = *(const float4 *)(ub + row * RF_HSTR + lane * 4);
         float4 v;
-        bool ok = silu_mul(g4.x, u4.x, &v.x);
-        ok &= silu_mul(g4.y, u4.y, &v.y);
-        ok &= silu_mul(g4.z, u4.z, &v.z);
-        ok &= silu_mul(g4.w, u4.w, &v.w);
+        bool ok = silu_mul(g4.x, u4.x, &v.x, exp_tab);
+        ok &= silu_mul(g4.y, u4.y, &v.y, exp_tab);
+        ok &= silu_mul(g4.z, u4.z, &v.z, exp_tab);
+        ok &= silu_mul(g4.w, u4.w, &v.w, exp_tab);
         if (!ok) flags |= EF_NONFINITE_MID;
         uint32_t mu = max(max(abs_bits(v.x), abs_bits(v.y)), max(abs_bits(v.z), abs_bits(v.w)));
         mu = wave_max_u(mu);

@@ -101,29 +101,65 @@ __device__ __forceinline__ void tile_coords(int lin, int mtiles, int ntiles, int
 //               up); C[row][hidden] = silu(g) * u in fp64, rounded to float.
 template <int EPI, int TM, int TN, int HALF>
 __device__ __forceinline__ void w8a8_epilogue(const v4i (&acc)[TM][TN], int part, int r0, int c0,
-                                              int lane, const float *__restrict__ sA,
-                                              const float *__restrict__ sB, int M, int N,
-                                              float *__restrict__ C, int ldc, uint32_t *err) {
+                                              int lane, const float *rs, const float *cs,
+                                              int M, int N, float *__restrict__ C, int ldc,
+                                              uint32_t *err, const double *exp_tab) {
     const int lr = (lane >> 4) * 4, lc = lane & 15;
-    // All scale loads are issued before the first store: gfx9 counts stores
-    // and loads on one vmcnt, so a load after a store would wait for it.
-    double sa[TM][4];
+    // The scales (rs: this wave tile's rows, cs: its columns) and the exp
+    // table were copied to LDS with the first stage, so the epilogue issues
+    // no global load: gfx9 counts stores and loads on one vmcnt, and a load
+    // after a store would wait for the store.
+    float4 saf[TM];
 #pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int row = r0 + i * 16 + lr + r;
-            sa[i][r] = (double)sA[row < M ? row : M - 1];
-        }
+    for (int i = 0; i < TM; i++) saf[i] = *(const float4 *)(rs + i * 16 + lr);
     double sb[TN];
 #pragma unroll
-    for (int j = 0; j < TN; j++) {
-        const int col = c0 + j * 16 + lc;
-        sb[j] = (double)sB[col < N ? col : N - 1];
-    }
+    for (int j = 0; j < TN; j++) sb[j] = (double)cs[j * 16 + lc];
+#define sa(i, r) ((double)((r) == 0 ? saf[i].x : (r) == 1 ? saf[i].y : (r) == 2 ? saf[i].z : saf[i].w))
     // Wave-uniform bounds: interior tiles store without per-element checks.
     const bool full = r0 + 16 * TM <= M && c0 + 16 * TN <= N;
     uint32_t bad = 0, badmid = 0;
+    if (EPI == EPI_SWIGLU) {
+        // A non-finite g or u (the only way silu_mul fails) shows as a
+        // maximum of the sign-cleared bit patterns at or above that of +inf.
+        uint32_t mx = 0;
+        auto one = [&](int i, int r, int jj, float *dst) {
+            const float g = (float)((double)acc[i][2 * jj][r] * (sa(i, r) * sb[2 * jj]));
+            const float u =
+                (float)((double)acc[i][2 * jj + 1][r] * (sa(i, r) * sb[2 * jj + 1]));
+            mx = max(mx, max(abs_bits(g), abs_bits(u)));
+            float sv;
+            (void)silu_mul(g, u, &sv, exp_tab);
+            *dst = sv;
+        };
+        if (full) {  // an interior tile: straight-line code
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                if (HALF > 0 && i / (HALF > 0 ? HALF : 1) != part) continue;
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    float *crow = C + (int64_t)(r0 + i * 16 + lr + r) * ldc + c0 / 2 + lc;
+#pragma unroll
+                    for (int jj = 0; jj < TN / 2; jj++) one(i, r, jj, crow + jj * 16);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                if (HALF > 0 && i / (HALF > 0 ? HALF : 1) != part) continue;
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int row = r0 + i * 16 + lr + r;
+                    float *crow = C + (int64_t)row * ldc + c0 / 2 + lc;
+#pragma unroll
+                    for (int jj = 0; jj < TN / 2; jj++)
+                        if (row < M && c0 + (2 * jj + 1) * 16 + lc < N) one(i, r, jj, crow + jj * 16);
+                }
+            }
+        }
+        if (mx >= 0x7f800000u) raise_err(err, EF_RANGE | EF_NONFINITE_MID);
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < TM; i++) {
         if (HALF > 0 && i / (HALF > 0 ? HALF : 1) != part) continue;
@@ -135,7 +171,7 @@ __device__ __forceinline__ void w8a8_epilogue(const v4i (&acc)[TM][TN], int part
 #pragma unroll
                 for (int j = 0; j < TN; j++) {
                     const int col = c0 + j * 16 + lc;
-                    const float f = (float)((double)acc[i][j][r] * (sa[i][r] * sb[j]));
+                    const float f = (float)((double)acc[i][j][r] * (sa(i, r) * sb[j]));
                     if (full || (row < M && col < N)) {
                         bad |= !isfinite(f);
                         crow[col] = f;
@@ -147,9 +183,9 @@ __device__ __forceinline__ void w8a8_epilogue(const v4i (&acc)[TM][TN], int part
                     const int cu = c0 + (2 * jj + 1) * 16 + lc;
                     const int hid = c0 / 2 + jj * 16 + lc;
                     const float g =
-                        (float)((double)acc[i][2 * jj][r] * (sa[i][r] * sb[2 * jj]));
+                        (float)((double)acc[i][2 * jj][r] * (sa(i, r) * sb[2 * jj]));
                     const float u =
-                        (float)((double)acc[i][2 * jj + 1][r] * (sa[i][r] * sb[2 * jj + 1]));
+                        (float)((double)acc[i][2 * jj + 1][r] * (sa(i, r) * sb[2 * jj + 1]));
                     if (full || (row < M && cu < N)) {
                         bad |= (!isfinite(g)) || (!isfinite(u));
                         float sv;
@@ -163,6 +199,7 @@ __device__ __forceinline__ void w8a8_epilogue(const v4i (&acc)[TM][TN], int part
     if (bad) raise_err(err, EF_RANGE);
     if (badmid) raise_err(err, EF_NONFINITE_MID);
 }
+#undef sa
 
 template <int EPI, int BM, int BN, int WGM, int WGN, int KS, int NST, int GM>
 __global__ __launch_bounds__(64 * WGM * WGN * KS) void k_w8a8_tile(
@@ -214,6 +251,24 @@ __global__ __launch_bounds__(64 * WGM * WGN * KS) void k_w8a8_tile(
             src[i] = Wp + ((int64_t)(n0 / 16 + p - AP) * KB) * 1024 + lane * 16;
             step[i] = 1024;
         }
+    }
+    // the epilogue's row and column scales (and the SwiGLU's exp table) go
+    // to LDS ahead of the first stage; they are older than every stage copy,
+    // so the first stage's wait covers them
+    __shared__ __attribute__((aligned(16))) float s_rs[BM];
+    __shared__ __attribute__((aligned(16))) float s_cs[BN];
+    // The exp table goes to LDS through registers (loaded here, stored by
+    // every wave at the epilogue, exp_tab_stage): reads of an LDS-DMA
+    // target make the compiler wait for every outstanding vector memory
+    // operation, stores included.
+    __shared__ __attribute__((aligned(16))) double s_tab[EPI == EPI_SWIGLU ? 64 : 2];
+    const double tabv = EPI == EPI_SWIGLU ? exp_tab_load(lane) : 0.0;
+    static_assert((BM + BN) / 64 <= NWG * KS, "a wave per 64 scales");
+    if (wave < BM / 64) {
+        dma<4>(sA + min(m0 + 64 * wave + lane, M - 1), s_rs + 64 * wave);
+    } else if (wave < (BM + BN) / 64) {
+        const int w = wave - BM / 64;
+        dma<4>(sB + min(n0 + 64 * w + lane, N - 1), s_cs + 64 * w);
     }
     auto issue = [&](int sg) {
         int8_t *st = smem + (sg % NST) * STAGE + kg * NP * 1024;
@@ -273,8 +328,9 @@ __global__ __launch_bounds__(64 * WGM * WGN * KS) void k_w8a8_tile(
                 if (i / TE == kg)
                     acc[i][j] += xbuf[((((1 - kg) * NWG + wg) * TE + i % TE) * TN + j) * 64 + lane];
     }
-    w8a8_epilogue<EPI, TM, TN, KS == 2 ? TE : 0>(acc, kg, m0 + wm, n0 + wn, lane, sA, sB, M, N,
-                                                  C, ldc, err);
+    if (EPI == EPI_SWIGLU) exp_tab_stage(s_tab, lane, tabv);
+    w8a8_epilogue<EPI, TM, TN, KS == 2 ? TE : 0>(acc, kg, m0 + wm, n0 + wn, lane, s_rs + wm,
+                                                  s_cs + wn, M, N, C, ldc, err, s_tab);
 }
 
 // Host-side launch of one configuration (dynamic LDS = NST stages).

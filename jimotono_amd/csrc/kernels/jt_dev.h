@@ -236,7 +236,8 @@ __device__ const double jt_exp2_64th[64] = {
     1.7562521603732995, 1.7753764925265212, 1.7947090750031072, 1.8142521755003989,
     1.8340080864093424, 1.8539791250833855, 1.8741676341103, 1.8945759815869656,
     1.9152065613971474, 1.9360617934922943, 1.9571441241754002, 1.978456026387951};
-__device__ __forceinline__ double exp_tang(double x) {
+template <typename TAB>
+__device__ __forceinline__ double exp_tang(double x, const TAB &tab) {
     x = fmin(fmax(x, -746.0), 710.0);
     const double kd = rint(x * 92.33248261689366);  // 64 / ln2
     const int k = (int)kd;
@@ -247,8 +248,23 @@ __device__ __forceinline__ double exp_tang(double x) {
     q = fma(r, q, 0.5);
     q = fma(r, q, 1.0);
     q *= r;
-    const double t = jt_exp2_64th[k & 63];
+    const double t = tab[k & 63];
     return ldexp(fma(t, q, t), k >> 6);  // t (1 + q) with one rounding
+}
+__device__ __forceinline__ double exp_tang(double x) { return exp_tang(x, jt_exp2_64th); }
+
+// The table in LDS: a kernel declares `__shared__ double tab[64]` and, where
+// the whole wavefront is active, each wave stores lane l's entry l
+// (exp_tab_stage, the entry loaded with the other epilogue loads by
+// exp_tab_load). Every wave writes the same values, so the overlapping
+// stores are benign, and a wave's LDS operations are processed in order,
+// so the wave's own reads after its stores see the table without a
+// barrier. The per-element lookup is then an LDS read: a global load per
+// element made each element wait on vmcnt, which also counts the stores
+// of the elements before it.
+__device__ __forceinline__ double exp_tab_load(int lane) { return jt_exp2_64th[lane & 63]; }
+__device__ __forceinline__ void exp_tab_stage(double *tab, int lane, double v) {
+    tab[lane & 63] = v;
 }
 // 1/d for 1 <= d < 2^1000: hardware reciprocal and two Newton steps (within
 // an ulp of the correctly rounded quotient)
@@ -268,13 +284,17 @@ __device__ __forceinline__ double recip_ge1(double d) {
 // boundary. The reference's finiteness test on sig, silu and v fails
 // exactly when g or u is not finite (for finite g, sig is in [0, 1] and v is
 // a finite double), which is what is returned.
-__device__ __forceinline__ bool silu_mul(float g, float u, float *s) {
+template <typename TAB>
+__device__ __forceinline__ bool silu_mul(float g, float u, float *s, const TAB &tab) {
     const double gi = (double)g, ui = (double)u;
-    const double ex = exp_tang(-gi);
+    const double ex = exp_tang(-gi, tab);
     const double sig = ex > 1e300 ? 0.0 : recip_ge1(1.0 + ex);
     const double silu = gi * sig;
     *s = (float)(silu * ui);
     return isfinite(g) && isfinite(u);
+}
+__device__ __forceinline__ bool silu_mul(float g, float u, float *s) {
+    return silu_mul(g, u, s, jt_exp2_64th);
 }
 
 // ---- panel layouts of prepared weights ----
