@@ -142,6 +142,17 @@ int jt_hip_moe_fwd_routed(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
                           const float *d_weights, float *dY, int T,
                           void *stream);
 
+/* The forward plus the residual add of the reference's training loop
+ * (bench/kernel/train_tinystories.c:1147-1160, after jt_moe_fwd_batch),
+ * fused into the combine: dY = (float)((double)dX + (double)m) with
+ * m = the layer output as jt_hip_moe_fwd writes it (two roundings, as
+ * there; a non-finite sum raises JT_HIP_EF_NONFINITE_MID). d_ids and
+ * d_weights as in jt_hip_moe_fwd_routed, or both NULL to run the router.
+ * dY may be dX (in place). */
+int jt_hip_moe_fwd_residual(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
+                            const float *d_weights, float *dY, int T,
+                            void *stream);
+
 /* Device buffers of the last forward, for inspection. */
 enum jt_hip_moe_buf {
     JT_HIP_BUF_IDS = 0,     /* int32 [T][k] */
@@ -169,6 +180,27 @@ int jt_hip_moe_buffer(const jt_hip_moe *L, int which, void **dptr,
 int jt_hip_moe_export_routed(const jt_hip_moe *L, int e, uint8_t *gu_codes,
                              uint16_t *gu_scales, uint8_t *d_codes,
                              uint16_t *d_scales);
+
+/* A prepared layer as bytes, in the order the kernels read its weights,
+ * so that a model is stored once as its execution plan (the reference's
+ * "model format = execution plan", DESIGN.MD:94-104, with quantised
+ * artifacts kept out of the repository, ROADMAP.MD:149-157). The buffer
+ * holds a 4 KiB header (magic "JTMOEQ1", version 1, the layer's sizes, a
+ * section table, a 64-bit checksum of the payload) and the device arrays
+ * byte for byte, each section 4 KiB aligned: the router gate (with its
+ * int8 code panels when the layer has them), the routed INT2 gate/up and
+ * INT4 down panels with their fp16 group scales, and each shared expert's
+ * int8 panels with their fp32 channel scales. buf == NULL only sets
+ * *bytes (the size needed); a cap below it returns JT_ERR_INVAL. */
+int jt_hip_moe_save(const jt_hip_moe *L, void *buf, size_t cap, size_t *bytes);
+/* A layer from jt_hip_moe_save's bytes (host memory): the arrays are
+ * copied to the GPU as they are, with no quantisation or packing, and the
+ * workspace is sized for max_tokens as in jt_hip_moe_desc. A wrong magic,
+ * version, size, section table or checksum returns JT_ERR_INVAL (EINVAL)
+ * with nothing allocated. The layer's forwards are bit-identical to the
+ * saved layer's. */
+int jt_hip_moe_load(const void *buf, size_t bytes, int max_tokens,
+                    jt_hip_moe **out);
 
 /* Per-stage device time of the most recent forwards, recorded with HIP
  * events on the forward's stream while profiling is on. */

@@ -82,8 +82,11 @@ _PROTOS = {
     "jt_hip_moe_prepare": [C.POINTER(_Desc)] + [_vp] * 7 + [C.POINTER(_vp)],
     "jt_hip_moe_fwd": [_vp, _vp, _vp, _i, _vp],
     "jt_hip_moe_fwd_routed": [_vp, _vp, _vp, _vp, _vp, _i, _vp],
+    "jt_hip_moe_fwd_residual": [_vp, _vp, _vp, _vp, _vp, _i, _vp],
     "jt_hip_moe_buffer": [_vp, _i, C.POINTER(_vp), C.POINTER(_sz)],
     "jt_hip_moe_export_routed": [_vp, _i, _u8p, _u16p, _u8p, _u16p],
+    "jt_hip_moe_save": [_vp, _vp, _sz, C.POINTER(_sz)],
+    "jt_hip_moe_load": [_vp, _sz, _i, C.POINTER(_vp)],
     "jt_hip_moe_set_profiling": [_vp, _i],
     "jt_hip_moe_stage_times": [_vp, C.POINTER(C.c_char_p), C.POINTER(C.c_double), _i,
                                C.POINTER(_i), C.POINTER(_i)],
@@ -392,14 +395,37 @@ class MoE:
     """Prepared quantised MoE layer (jt_hip_moe)."""
 
     def __init__(self, n, h, E, k, S, hs, max_tokens, Wgate, Wg, Wu, Wd, Wg_s=None,
-                 Wu_s=None, Wd_s=None, group=64):
+                 Wu_s=None, Wd_s=None, group=64, _handle=None):
         self.desc = _Desc(n, h, E, k, S, hs, group, max_tokens)
         self.n, self.h, self.E, self.k, self.S, self.hs = n, h, E, k, S, hs
+        if _handle is not None:
+            self.h_ = _handle
+            return
         hd = C.c_void_p()
         _check(lib().jt_hip_moe_prepare(C.byref(self.desc), _ptr(Wgate), _ptr(Wg), _ptr(Wu),
                                         _ptr(Wd), _ptr(Wg_s), _ptr(Wu_s), _ptr(Wd_s),
                                         C.byref(hd)), "jt_hip_moe_prepare")
         self.h_ = hd
+
+    def save(self) -> bytes:
+        """The layer serialised by jt_hip_moe_save."""
+        nb = C.c_size_t()
+        _check(lib().jt_hip_moe_save(self.h_, None, 0, C.byref(nb)), "jt_hip_moe_save")
+        buf = C.create_string_buffer(nb.value)
+        _check(lib().jt_hip_moe_save(self.h_, buf, nb.value, C.byref(nb)), "jt_hip_moe_save")
+        return buf.raw
+
+    @classmethod
+    def load(cls, data: bytes, max_tokens: int):
+        """A layer rebuilt from save()'s bytes by jt_hip_moe_load (raises on a
+        bad buffer; rc and errno as the C function)."""
+        hd = C.c_void_p()
+        rc = lib().jt_hip_moe_load(data, len(data), max_tokens, C.byref(hd))
+        if rc != JT_OK:
+            raise ValueError(f"jt_hip_moe_load rc={rc} errno={errno()}")
+        f = np.frombuffer(data[16:44], np.int32)
+        return cls(int(f[0]), int(f[1]), int(f[2]), int(f[3]), int(f[4]), int(f[5]),
+                   max_tokens, None, None, None, None, group=int(f[6]), _handle=hd)
 
     def fwd(self, X, Y, stream=None):
         return lib().jt_hip_moe_fwd(self.h_, _ptr(X), _ptr(Y), X.shape[0], _stream(stream))
@@ -407,6 +433,11 @@ class MoE:
     def fwd_routed(self, X, ids, w, Y, stream=None):
         return lib().jt_hip_moe_fwd_routed(self.h_, _ptr(X), _ptr(ids), _ptr(w), _ptr(Y),
                                            X.shape[0], _stream(stream))
+
+    def fwd_residual(self, X, Y, ids=None, w=None, stream=None):
+        """Y = X + layer(X) with the reference's two roundings (Y may be X)."""
+        return lib().jt_hip_moe_fwd_residual(self.h_, _ptr(X), _ptr(ids), _ptr(w), _ptr(Y),
+                                             X.shape[0], _stream(stream))
 
     def buffer(self, which):
         p, nb = C.c_void_p(), C.c_size_t()

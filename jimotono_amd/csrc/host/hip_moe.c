@@ -58,8 +58,9 @@ void jt_hip_ffn_free(jt_hip_ffn *F) {
     free(F);
 }
 
-static int ffn_prepare_on(jt_rt *rt, const float *dWg, const float *dWu, const float *dWd,
-                          int n, int h, jt_hip_ffn **out) {
+/* An expert with its weight arrays allocated (scales zeroed, panels not
+ * written yet). */
+static int ffn_alloc(jt_rt *rt, int n, int h, jt_hip_ffn **out) {
     jt_hip_ffn *F = calloc(1, sizeof(*F));
     if (!F) FAIL(JT_ERR_NOMEM, ENOMEM);
     F->n = n;
@@ -68,8 +69,6 @@ static int ffn_prepare_on(jt_rt *rt, const float *dWg, const float *dWu, const f
     F->Kph = (int)jt_round_up((size_t)h, 64);
     F->Np_gu = (int)jt_round_up((size_t)2 * h, 128);
     F->Np_d = (int)jt_round_up((size_t)n, 128);
-    int8_t *qg = NULL, *qu = NULL, *qgu = NULL, *qd = NULL;
-    float *sg = NULL, *su = NULL;
     hipError_t e = hipSuccess;
 #define ALLOC(p, bytes) \
     if (e == hipSuccess) e = hipMalloc((void **)&(p), (size_t)(bytes))
@@ -77,6 +76,27 @@ static int ffn_prepare_on(jt_rt *rt, const float *dWg, const float *dWu, const f
     ALLOC(F->gu_s, (size_t)F->Np_gu * sizeof(float));
     ALLOC(F->d_P, (size_t)F->Np_d * F->Kph);
     ALLOC(F->d_s, (size_t)F->Np_d * sizeof(float));
+#undef ALLOC
+    if (e == hipSuccess) e = hipMemsetAsync(F->gu_s, 0, (size_t)F->Np_gu * sizeof(float), rt->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(F->d_s, 0, (size_t)F->Np_d * sizeof(float), rt->stream);
+    if (e != hipSuccess) {
+        jt_hip_ffn_free(F);
+        return jt_rt_err(e);
+    }
+    *out = F;
+    return JT_OK;
+}
+
+static int ffn_prepare_on(jt_rt *rt, const float *dWg, const float *dWu, const float *dWd,
+                          int n, int h, jt_hip_ffn **out) {
+    jt_hip_ffn *F = NULL;
+    int rc = ffn_alloc(rt, n, h, &F);
+    if (rc != JT_OK) return rc;
+    int8_t *qg = NULL, *qu = NULL, *qgu = NULL, *qd = NULL;
+    float *sg = NULL, *su = NULL;
+    hipError_t e = hipSuccess;
+#define ALLOC(p, bytes) \
+    if (e == hipSuccess) e = hipMalloc((void **)&(p), (size_t)(bytes))
     ALLOC(qg, (size_t)h * n);
     ALLOC(qu, (size_t)h * n);
     ALLOC(qgu, (size_t)2 * h * n);
@@ -84,9 +104,7 @@ static int ffn_prepare_on(jt_rt *rt, const float *dWg, const float *dWu, const f
     ALLOC(sg, (size_t)h * sizeof(float));
     ALLOC(su, (size_t)h * sizeof(float));
 #undef ALLOC
-    if (e == hipSuccess) e = hipMemsetAsync(F->gu_s, 0, (size_t)F->Np_gu * sizeof(float), rt->stream);
-    if (e == hipSuccess) e = hipMemsetAsync(F->d_s, 0, (size_t)F->Np_d * sizeof(float), rt->stream);
-    int rc = jt_rt_err(e);
+    rc = jt_rt_err(e);
     if (rc == JT_OK) {
         /* gate/up rows are output channels, K = n contiguous */
         jtk_quant_weight_rows(dWg, n, 1, h, n, qg, sg, rt->d_err, rt->stream);
@@ -352,26 +370,29 @@ void jt_hip_moe_free(jt_hip_moe *L) {
     free(L);
 }
 
-int jt_hip_moe_prepare(const jt_hip_moe_desc *desc, const float *dWgate, const float *dWg,
-                       const float *dWu, const float *dWd, const float *dWg_s,
-                       const float *dWu_s, const float *dWd_s, jt_hip_moe **out) {
-    if (!desc || !dWg || !dWu || !dWd || !out) FAIL(JT_ERR_INVAL, EINVAL);
-    const jt_hip_moe_desc d = *desc;
+/* The prepare-time checks of a layer's sizes (jimotono/hip_moe.h). */
+static int moe_check_desc(const jt_hip_moe_desc *dp) {
+    const jt_hip_moe_desc d = *dp;
     if (d.n <= 0 || d.n % 128 != 0 || d.n > JT_BWD_MAX_WIDE || d.h <= 0 || d.h % 64 != 0 ||
         d.h > JT_BWD_MAX_WIDE || d.n_experts <= 0 || d.n_experts > JT_MOE_MAX_EXPERTS ||
         d.topk <= 0 || d.topk > d.n_experts || d.topk > JT_MOE_MAX_TOPK || d.n_shared < 0 ||
         d.n_shared > JT_MOE_MAX_SHARED || d.group != 64 || d.max_tokens <= 0)
         FAIL(JT_ERR_INVAL, EINVAL);
-    if (d.n_shared > 0 && (!dWg_s || !dWu_s || !dWd_s || d.h_shared <= 0 ||
-                           d.h_shared % 16 != 0 || d.h_shared > JT_BWD_MAX_WIDE))
+    if (d.n_shared > 0 &&
+        (d.h_shared <= 0 || d.h_shared % 16 != 0 || d.h_shared > JT_BWD_MAX_WIDE))
         FAIL(JT_ERR_INVAL, EINVAL);
     /* the tile list of the largest forward must fit one launch grid
      * (65535 blocks): 64-row tiles plus one short tile per expert */
     if ((int64_t)d.max_tokens * d.topk / 64 + d.n_experts > 65535) FAIL(JT_ERR_INVAL, EINVAL);
-    jt_rt *rt = jt_rt_get();
-    if (!rt) return JT_ERR_IO;
+    return JT_OK;
+}
+
+/* A layer with every device array allocated (weights unwritten) and its
+ * workspace sized for d.max_tokens; the shared experts are not created. */
+static int moe_alloc(const jt_hip_moe_desc *dp, int has_gate, jt_hip_moe **out) {
     jt_hip_moe *L = calloc(1, sizeof(*L));
     if (!L) FAIL(JT_ERR_NOMEM, ENOMEM);
+    const jt_hip_moe_desc d = *dp;
     L->d = d;
     const int n = d.n, h = d.h, E = d.n_experts, T = d.max_tokens;
     const int64_t Tk = (int64_t)T * d.topk;
@@ -383,7 +404,7 @@ int jt_hip_moe_prepare(const jt_hip_moe_desc *desc, const float *dWgate, const f
     hipError_t e = hipSuccess;
 #define ALLOC(p, bytes) \
     if (e == hipSuccess) e = hipMalloc((void **)&(p), (size_t)(bytes))
-    if (dWgate) ALLOC(L->Wgate, (size_t)E * n * sizeof(float));
+    if (has_gate) ALLOC(L->Wgate, (size_t)E * n * sizeof(float));
     ALLOC(L->gu_P, L->gu_pstride * E);
     ALLOC(L->gu_S, L->gu_sstride * E * 2);
     ALLOC(L->dn_P, L->dn_pstride * E);
@@ -405,10 +426,9 @@ int jt_hip_moe_prepare(const jt_hip_moe_desc *desc, const float *dWgate, const f
     ALLOC(L->ssr, (size_t)Tk * 4);
     ALLOC(L->Ye, (size_t)Tk * n * 4);
     ALLOC(L->Ys, (size_t)(d.n_shared > 0 ? d.n_shared : 1) * T * n * 4);
-    const int Ep = (E + 63) / 64 * 64;
-    int8_t *wh_rm = NULL, *wl_rm = NULL;
-    L->fast_router = dWgate != NULL && E <= 256 && n % 64 == 0;
+    L->fast_router = has_gate && E <= 256 && n % 64 == 0;
     if (L->fast_router) {
+        const int Ep = (E + 63) / 64 * 64;
         ALLOC(L->Xl, (size_t)T * n);
         ALLOC(L->xinfo, (size_t)T * 16);
         ALLOC(L->approx, (size_t)T * E * 8);
@@ -417,14 +437,65 @@ int jt_hip_moe_prepare(const jt_hip_moe_desc *desc, const float *dWgate, const f
         ALLOC(L->rWh, (size_t)Ep * n);
         ALLOC(L->rWl, (size_t)Ep * n);
         ALLOC(L->winfo, (size_t)E * 16);
-        ALLOC(wh_rm, (size_t)E * n);
-        ALLOC(wl_rm, (size_t)E * n);
     }
 #undef ALLOC
+    if (e != hipSuccess) {
+        jt_hip_moe_free(L);
+        return jt_rt_err(e);
+    }
+    *out = L;
+    return JT_OK;
+}
+
+/* The shared experts' workspace and the side stream of a layer whose
+ * weights are in place. */
+static int moe_finish(jt_hip_moe *L) {
+    int rc = JT_OK;
+    for (int s = 0; s < L->d.n_shared && rc == JT_OK; s++)
+        rc = ffn_reserve(L->sh[s], L->d.max_tokens, 0);
+    if (rc == JT_OK && L->d.n_shared > 0) {
+        const int ns = L->d.n_shared < MOE_SIDE ? L->d.n_shared : MOE_SIDE;
+        hipError_t e = hipEventCreateWithFlags(&L->ev_fork, hipEventDisableTiming);
+        for (int i = 0; i < ns && e == hipSuccess; i++) {
+            e = hipStreamCreateWithFlags(&L->side[i], hipStreamNonBlocking);
+            if (e != hipSuccess) break;
+            e = hipEventCreateWithFlags(&L->ev_join[i], hipEventDisableTiming);
+            if (e != hipSuccess) {
+                (void)hipStreamDestroy(L->side[i]);
+                break;
+            }
+            L->nside = i + 1;
+        }
+        if (e != hipSuccess && L->nside == 0) (void)hipEventDestroy(L->ev_fork);
+        rc = jt_rt_err(e);
+    }
+    return rc;
+}
+
+int jt_hip_moe_prepare(const jt_hip_moe_desc *desc, const float *dWgate, const float *dWg,
+                       const float *dWu, const float *dWd, const float *dWg_s,
+                       const float *dWu_s, const float *dWd_s, jt_hip_moe **out) {
+    if (!desc || !dWg || !dWu || !dWd || !out) FAIL(JT_ERR_INVAL, EINVAL);
+    int rc = moe_check_desc(desc);
+    if (rc != JT_OK) return rc;
+    const jt_hip_moe_desc d = *desc;
+    if (d.n_shared > 0 && (!dWg_s || !dWu_s || !dWd_s)) FAIL(JT_ERR_INVAL, EINVAL);
+    jt_rt *rt = jt_rt_get();
+    if (!rt) return JT_ERR_IO;
+    jt_hip_moe *L = NULL;
+    if ((rc = moe_alloc(desc, dWgate != NULL, &L)) != JT_OK) return rc;
+    const int n = d.n, h = d.h, E = d.n_experts;
+    const int Ep = (E + 63) / 64 * 64;
+    int8_t *wh_rm = NULL, *wl_rm = NULL;
+    hipError_t e = hipSuccess;
+    if (L->fast_router) {
+        e = hipMalloc((void **)&wh_rm, (size_t)E * n);
+        if (e == hipSuccess) e = hipMalloc((void **)&wl_rm, (size_t)E * n);
+    }
     if (e == hipSuccess && dWgate)
         e = hipMemcpyAsync(L->Wgate, dWgate, (size_t)E * n * sizeof(float),
                            hipMemcpyDeviceToDevice, rt->stream);
-    int rc = jt_rt_err(e);
+    rc = jt_rt_err(e);
     if (rc == JT_OK) {
         jtk_check_finite(dWgate ? L->Wgate : NULL, dWgate ? (int64_t)E * n : 0, rt->d_err,
                          rt->stream);
@@ -450,24 +521,8 @@ int jt_hip_moe_prepare(const jt_hip_moe_desc *desc, const float *dWgate, const f
     for (int s = 0; s < d.n_shared && rc == JT_OK; s++) {
         const int64_t so = (int64_t)s * hs * n;
         rc = ffn_prepare_on(rt, dWg_s + so, dWu_s + so, dWd_s + so, n, hs, &L->sh[s]);
-        if (rc == JT_OK) rc = ffn_reserve(L->sh[s], T, 0);
     }
-    if (rc == JT_OK && d.n_shared > 0) {
-        const int ns = d.n_shared < MOE_SIDE ? d.n_shared : MOE_SIDE;
-        e = hipEventCreateWithFlags(&L->ev_fork, hipEventDisableTiming);
-        for (int i = 0; i < ns && e == hipSuccess; i++) {
-            e = hipStreamCreateWithFlags(&L->side[i], hipStreamNonBlocking);
-            if (e != hipSuccess) break;
-            e = hipEventCreateWithFlags(&L->ev_join[i], hipEventDisableTiming);
-            if (e != hipSuccess) {
-                (void)hipStreamDestroy(L->side[i]);
-                break;
-            }
-            L->nside = i + 1;
-        }
-        if (e != hipSuccess && L->nside == 0) (void)hipEventDestroy(L->ev_fork);
-        rc = jt_rt_err(e);
-    }
+    if (rc == JT_OK) rc = moe_finish(L);
     if (rc != JT_OK) {
         jt_hip_moe_free(L);
         return rc;
@@ -522,7 +577,7 @@ static int prof_begin(jt_hip_moe *L, int *slot) {
 }
 
 static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
-                       const float *d_w, float *dY, int T, void *stream) {
+                       const float *d_w, const float *dR, float *dY, int T, void *stream) {
     const jt_hip_moe_desc *d = &L->d;
     if (!dX || !dY || T < 0 || T > d->max_tokens) FAIL(JT_ERR_INVAL, EINVAL);
     if (!d_ids && !L->Wgate) FAIL(JT_ERR_INVAL, EINVAL);
@@ -657,20 +712,28 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
         }
     }
     prof_mark(L, slot, ST_COMBINE, s);
-    le |= jtk_combine(w, L->Ye, NULL, L->Ys, S, T, k, n, dY, err, s);
+    le |= jtk_combine(w, L->Ye, NULL, L->Ys, S, T, k, n, dR, dY, err, s);
     prof_mark(L, slot, ST_N, s);
     return le ? jt_rt_err(hipErrorLaunchFailure) : JT_OK;
 }
 
 int jt_hip_moe_fwd(jt_hip_moe *L, const float *dX, float *dY, int T, void *stream) {
     if (!L) FAIL(JT_ERR_INVAL, EINVAL);
-    return moe_forward(L, dX, NULL, NULL, dY, T, stream);
+    return moe_forward(L, dX, NULL, NULL, NULL, dY, T, stream);
 }
 
 int jt_hip_moe_fwd_routed(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
                           const float *d_weights, float *dY, int T, void *stream) {
     if (!L || !d_ids || !d_weights) FAIL(JT_ERR_INVAL, EINVAL);
-    return moe_forward(L, dX, d_ids, d_weights, dY, T, stream);
+    return moe_forward(L, dX, d_ids, d_weights, NULL, dY, T, stream);
+}
+
+int jt_hip_moe_fwd_residual(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
+                            const float *d_weights, float *dY, int T, void *stream) {
+    if (!L || (!d_ids) != (!d_weights)) FAIL(JT_ERR_INVAL, EINVAL);
+    /* the residual is the layer input; dY may be dX (every kernel that reads
+     * dX runs before the combine, which reads each element before writing it) */
+    return moe_forward(L, dX, d_ids, d_weights, dX, dY, T, stream);
 }
 
 int jt_hip_moe_buffer(const jt_hip_moe *L, int which, void **dptr, size_t *bytes) {
@@ -754,6 +817,170 @@ int jt_hip_moe_export_routed(const jt_hip_moe *L, int e, uint8_t *gu_codes,
     free(hp);
     free(hs);
     return rc;
+}
+
+/* ======================= serialised layer ======================= */
+/*
+ * Format "JTMOEQ" version 1: a 4 KiB header, then the layer's device arrays
+ * byte for byte, each section starting on a 4 KiB boundary, in this order:
+ *   gate fp32 [E][n] and, for the int8-bounded router, its hi/lo code
+ *   panels and row info (only with a router gate);
+ *   routed gate/up INT2 panels [E][2h/16][n/64][256 B], their fp16 scales,
+ *   down INT4 panels [E][n/16][h/64][512 B], their fp16 scales;
+ *   per shared expert: gate/up int8 panels (gate and up interleaved in
+ *   blocks of 16 channels), their fp32 scales, down panels, their scales.
+ * Every array is in the order the kernels read it, so a load is a copy.
+ * Header (little-endian): magic "JTMOEQ1\0", u32 version, u32 header bytes,
+ * i32 n, h, E, k, S, h_shared, group, u32 flags (bit 0: router gate),
+ * u32 section count, u64 payload bytes, u64 payload checksum, then one
+ * {u64 offset, u64 bytes} per section (offsets from the file start).
+ */
+#define MQ_HDR 4096u
+#define MQ_ALIGN 4096u
+#define MQ_MAXSEC (4 + 4 + 4 * JT_MOE_MAX_SHARED)
+static const char k_mq_magic[8] = {'J', 'T', 'M', 'O', 'E', 'Q', '1', '\0'};
+
+typedef struct mq_sec {
+    void *dev;
+    size_t bytes;
+} mq_sec;
+
+/* The sections of a layer (device pointers and sizes), in file order. */
+static int mq_sections(const jt_hip_moe *L, mq_sec *sec) {
+    const jt_hip_moe_desc *d = &L->d;
+    const size_t E = (size_t)d->n_experts, n = (size_t)d->n;
+    int ns = 0;
+    if (L->Wgate) {
+        sec[ns++] = (mq_sec){L->Wgate, E * n * 4};
+        if (L->fast_router) {
+            const size_t Ep = (E + 63) / 64 * 64;
+            sec[ns++] = (mq_sec){L->rWh, Ep * n};
+            sec[ns++] = (mq_sec){L->rWl, Ep * n};
+            sec[ns++] = (mq_sec){L->winfo, E * 16};
+        }
+    }
+    sec[ns++] = (mq_sec){L->gu_P, (size_t)L->gu_pstride * E};
+    sec[ns++] = (mq_sec){L->gu_S, (size_t)L->gu_sstride * E * 2};
+    sec[ns++] = (mq_sec){L->dn_P, (size_t)L->dn_pstride * E};
+    sec[ns++] = (mq_sec){L->dn_S, (size_t)L->dn_sstride * E * 2};
+    for (int s = 0; s < d->n_shared; s++) {
+        const jt_hip_ffn *F = L->sh[s];
+        sec[ns++] = (mq_sec){F->gu_P, (size_t)F->Np_gu * F->Kpn};
+        sec[ns++] = (mq_sec){F->gu_s, (size_t)F->Np_gu * 4};
+        sec[ns++] = (mq_sec){F->d_P, (size_t)F->Np_d * F->Kph};
+        sec[ns++] = (mq_sec){F->d_s, (size_t)F->Np_d * 4};
+    }
+    return ns;
+}
+
+/* 64-bit FNV-1a over 8-byte words (the payload is a multiple of 4 KiB). */
+static uint64_t mq_checksum(const uint8_t *p, size_t bytes) {
+    uint64_t hsh = 0xcbf29ce484222325ull;
+    for (size_t i = 0; i + 8 <= bytes; i += 8) {
+        uint64_t w;
+        memcpy(&w, p + i, 8);
+        hsh = (hsh ^ w) * 0x100000001b3ull;
+    }
+    return hsh;
+}
+
+static void put32(uint8_t *p, uint32_t v) { memcpy(p, &v, 4); }
+static void put64(uint8_t *p, uint64_t v) { memcpy(p, &v, 8); }
+static uint32_t get32(const uint8_t *p) {
+    uint32_t v;
+    memcpy(&v, p, 4);
+    return v;
+}
+static uint64_t get64(const uint8_t *p) {
+    uint64_t v;
+    memcpy(&v, p, 8);
+    return v;
+}
+
+static size_t mq_layout(const mq_sec *sec, int ns, size_t *off) {
+    size_t at = MQ_HDR;
+    for (int i = 0; i < ns; i++) {
+        off[i] = at;
+        at += jt_round_up(sec[i].bytes, MQ_ALIGN);
+    }
+    return at;
+}
+
+int jt_hip_moe_save(const jt_hip_moe *L, void *buf, size_t cap, size_t *bytes) {
+    if (!L || !bytes) FAIL(JT_ERR_INVAL, EINVAL);
+    mq_sec sec[MQ_MAXSEC];
+    size_t off[MQ_MAXSEC];
+    const int ns = mq_sections(L, sec);
+    const size_t total = mq_layout(sec, ns, off);
+    *bytes = total;
+    if (!buf) return JT_OK;
+    if (cap < total) FAIL(JT_ERR_INVAL, EINVAL);
+    jt_rt *rt = jt_rt_get();
+    if (!rt) return JT_ERR_IO;
+    uint8_t *b = buf;
+    memset(b, 0, total);
+    for (int i = 0; i < ns; i++) {
+        const int rc = jt_rt_d2h(rt, b + off[i], sec[i].dev, sec[i].bytes);
+        if (rc != JT_OK) return rc;
+    }
+    const jt_hip_moe_desc *d = &L->d;
+    memcpy(b, k_mq_magic, 8);
+    put32(b + 8, 1);
+    put32(b + 12, MQ_HDR);
+    const int32_t f[7] = {d->n, d->h, d->n_experts, d->topk, d->n_shared, d->h_shared, d->group};
+    memcpy(b + 16, f, sizeof(f));
+    put32(b + 44, L->Wgate ? 1u : 0u);
+    put32(b + 48, (uint32_t)ns);
+    put64(b + 52, (uint64_t)(total - MQ_HDR));
+    put64(b + 60, mq_checksum(b + MQ_HDR, total - MQ_HDR));
+    for (int i = 0; i < ns; i++) {
+        put64(b + 68 + 16 * i, (uint64_t)off[i]);
+        put64(b + 76 + 16 * i, (uint64_t)sec[i].bytes);
+    }
+    return JT_OK;
+}
+
+int jt_hip_moe_load(const void *buf, size_t bytes, int max_tokens, jt_hip_moe **out) {
+    if (!buf || !out || bytes < MQ_HDR) FAIL(JT_ERR_INVAL, EINVAL);
+    const uint8_t *b = buf;
+    if (memcmp(b, k_mq_magic, 8) != 0 || get32(b + 8) != 1 || get32(b + 12) != MQ_HDR)
+        FAIL(JT_ERR_INVAL, EINVAL);
+    int32_t f[7];
+    memcpy(f, b + 16, sizeof(f));
+    const uint32_t flags = get32(b + 44);
+    if (flags > 1u) FAIL(JT_ERR_INVAL, EINVAL);
+    const jt_hip_moe_desc d = {f[0], f[1], f[2], f[3], f[4], f[5], f[6], max_tokens};
+    int rc = moe_check_desc(&d);
+    if (rc != JT_OK) return rc;
+    const uint64_t payload = get64(b + 52);
+    if (payload != bytes - MQ_HDR || mq_checksum(b + MQ_HDR, bytes - MQ_HDR) != get64(b + 60))
+        FAIL(JT_ERR_INVAL, EINVAL);
+    jt_rt *rt = jt_rt_get();
+    if (!rt) return JT_ERR_IO;
+    jt_hip_moe *L = NULL;
+    if ((rc = moe_alloc(&d, (int)(flags & 1u), &L)) != JT_OK) return rc;
+    for (int s = 0; s < d.n_shared && rc == JT_OK; s++) rc = ffn_alloc(rt, d.n, d.h_shared, &L->sh[s]);
+    mq_sec sec[MQ_MAXSEC];
+    size_t off[MQ_MAXSEC];
+    int ns = 0;
+    if (rc == JT_OK) {
+        ns = mq_sections(L, sec);
+        /* the section table must be exactly this layer's layout */
+        if (get32(b + 48) != (uint32_t)ns || mq_layout(sec, ns, off) != bytes) rc = JT_ERR_INVAL;
+        for (int i = 0; i < ns && rc == JT_OK; i++)
+            if (get64(b + 68 + 16 * i) != off[i] || get64(b + 76 + 16 * i) != sec[i].bytes)
+                rc = JT_ERR_INVAL;
+        if (rc != JT_OK) errno = EINVAL;
+    }
+    for (int i = 0; i < ns && rc == JT_OK; i++)
+        rc = jt_rt_h2d(rt, sec[i].dev, b + off[i], sec[i].bytes);
+    if (rc == JT_OK) rc = moe_finish(L);
+    if (rc != JT_OK) {
+        jt_hip_moe_free(L);
+        return rc;
+    }
+    *out = L;
+    return JT_OK;
 }
 
 int jt_hip_moe_set_profiling(jt_hip_moe *L, int on) {

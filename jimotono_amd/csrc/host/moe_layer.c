@@ -301,7 +301,7 @@ static int fwd_batch(const float *X, const float *Wgate, const float *Wg, const 
         }
     }
     /* combine (src/moe_layer.c:1443-1463, 1549-1574) */
-    le |= jtk_combine(w, Ysel, drop, Ys, S, T, k, n, dY, err, s);
+    le |= jtk_combine(w, Ysel, drop, Ys, S, T, k, n, NULL, dY, err, s);
     if (rc == JT_OK && le) rc = jt_rt_err(hipErrorLaunchFailure);
     if (rc != JT_OK) goto out;
     if ((rc = jt_rt_flags(rt, s, &f)) != JT_OK) goto out;

@@ -121,8 +121,10 @@ int jtk_sort_small(const int32_t *ids, int Tk, int E, int64_t cap, int R, int32_
 int jtk_sort_mid(const int32_t *ids, int Tk, int E, int64_t cap, int R, int32_t *rank,
                  int32_t *cnt, int32_t *off, int64_t *off64, int32_t *perm, int64_t *perm64,
                  uint8_t *drop, int32_t *tiles, int32_t *ntiles, uint32_t *err, hipStream_t s);
+/* R: optional residual [T][n] (may alias Y): Y = (float)((double)R + (double)(float)sum) */
 int jtk_combine(const float *w, const float *Ye, const uint8_t *drop, const float *Ys,
-                int S, int T, int k, int n, float *Y, uint32_t *err, hipStream_t s);
+                int S, int T, int k, int n, const float *R, float *Y, uint32_t *err,
+                hipStream_t s);
 int jtk_renorm(float *w, const uint8_t *drop, int T, int k, uint32_t *err, hipStream_t s);
 int jtk_gather_rows(const float *src, int n, const int32_t *perm, int base, int div,
                     int rows, float *dst, hipStream_t s);

@@ -801,11 +801,33 @@ extern "C" int jtk_sort_mid(const int32_t *ids, int Tk, int E, int64_t cap, int 
 // ---------------- combine ----------------
 // One thread per 4 consecutive outputs of a token. drop may be NULL
 // (dropless); dropped slots contribute nothing (src/moe_layer.c:1449-1451).
+// With a residual R [T][n] (may alias Y: each thread reads its 4 values
+// before it writes them) the output is the training loop's
+// (float)((double)R + (double)(float)moe), rounded twice as there
+// (bench/kernel/train_tinystories.c:1147-1160); a non-finite sum is an
+// error there too.
+__device__ __forceinline__ float res_add(const float *R, int64_t at, float y, bool &bad) {
+    const double v = (double)R[at] + (double)y;
+    bad |= !isfinite(v);
+    return (float)v;
+}
+__device__ __forceinline__ void combine_store(float *Y, const float *R, int64_t at, double a0,
+                                              double a1, double a2, double a3, uint32_t *err) {
+    bool bad = !isfinite(a0) || !isfinite(a1) || !isfinite(a2) || !isfinite(a3);
+    float4 o = make_float4((float)a0, (float)a1, (float)a2, (float)a3);
+    if (R) {  // kernel-uniform
+        const float4 r = *(const float4 *)(R + at);
+        o = make_float4(res_add(&r.x, 0, o.x, bad), res_add(&r.y, 0, o.y, bad),
+                        res_add(&r.z, 0, o.z, bad), res_add(&r.w, 0, o.w, bad));
+    }
+    if (bad) raise_err(err, EF_NONFINITE_MID);
+    *(float4 *)(Y + at) = o;
+}
 __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ w,
                                                  const float *__restrict__ Ye,
                                                  const uint8_t *__restrict__ drop,
                                                  const float *__restrict__ Ys, int S, int T,
-                                                 int k, int n, float *__restrict__ Y,
+                                                 int k, int n, const float *R, float *Y,
                                                  uint32_t *err) {
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int nq = n / 4;
@@ -829,9 +851,7 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ w,
         a2 += (double)y.z;
         a3 += (double)y.w;
     }
-    if (!isfinite(a0) || !isfinite(a1) || !isfinite(a2) || !isfinite(a3))
-        raise_err(err, EF_NONFINITE_MID);
-    *(float4 *)(Y + (int64_t)t * n + j) = make_float4((float)a0, (float)a1, (float)a2, (float)a3);
+    combine_store(Y, R, (int64_t)t * n + j, a0, a1, a2, a3, err);
 }
 
 // The same sum with the top-k K a compile-time constant: every load of a
@@ -847,7 +867,8 @@ __global__ __launch_bounds__(256) void k_combine_k(const float *__restrict__ w,
                                                    const float *__restrict__ Ye,
                                                    const uint8_t *__restrict__ drop,
                                                    const float *__restrict__ Ys, int S, int T,
-                                                   int n, float *__restrict__ Y, uint32_t *err) {
+                                                   int n, const float *R, float *Y,
+                                                   uint32_t *err) {
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int nq = n / 4;
     if (idx >= (int64_t)T * nq) return;
@@ -887,9 +908,7 @@ __global__ __launch_bounds__(256) void k_combine_k(const float *__restrict__ w,
         a2 += (double)ys[s].z;
         a3 += (double)ys[s].w;
     }
-    if (!isfinite(a0) || !isfinite(a1) || !isfinite(a2) || !isfinite(a3))
-        raise_err(err, EF_NONFINITE_MID);
-    *(float4 *)(Y + (int64_t)t * n + j) = make_float4((float)a0, (float)a1, (float)a2, (float)a3);
+    combine_store(Y, R, (int64_t)t * n + j, a0, a1, a2, a3, err);
 }
 
 // Scalar variant for n % 4 != 0 (legacy shapes).
@@ -897,7 +916,7 @@ __global__ __launch_bounds__(256) void k_combine1(const float *__restrict__ w,
                                                   const float *__restrict__ Ye,
                                                   const uint8_t *__restrict__ drop,
                                                   const float *__restrict__ Ys, int S, int T,
-                                                  int k, int n, float *__restrict__ Y,
+                                                  int k, int n, const float *R, float *Y,
                                                   uint32_t *err) {
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (idx >= (int64_t)T * n) return;
@@ -909,12 +928,15 @@ __global__ __launch_bounds__(256) void k_combine1(const float *__restrict__ w,
         a = fma((double)w[q], (double)Ye[q * n + j], a);
     }
     for (int s = 0; s < S; s++) a += (double)Ys[((int64_t)s * T + t) * n + j];
-    if (!isfinite(a)) raise_err(err, EF_NONFINITE_MID);
-    Y[idx] = (float)a;
+    bool bad = !isfinite(a);
+    float o = (float)a;
+    if (R) o = res_add(R, idx, o, bad);
+    if (bad) raise_err(err, EF_NONFINITE_MID);
+    Y[idx] = o;
 }
 
 extern "C" int jtk_combine(const float *w, const float *Ye, const uint8_t *drop,
-                           const float *Ys, int S, int T, int k, int n, float *Y,
+                           const float *Ys, int S, int T, int k, int n, const float *R, float *Y,
                            uint32_t *err, hipStream_t s) {
     if (n % 4 == 0) {
         const int64_t th = (int64_t)T * (n / 4);
@@ -922,10 +944,10 @@ extern "C" int jtk_combine(const float *w, const float *Ye, const uint8_t *drop,
 #define CMB_KS(KK, SN)                                                                     \
     if (drop)                                                                              \
         hipLaunchKernelGGL((k_combine_k<KK, SN, true>), grid, dim3(256), 0, s, w, Ye, drop, \
-                           Ys, S, T, n, Y, err);                                           \
+                           Ys, S, T, n, R, Y, err);                                        \
     else                                                                                   \
         hipLaunchKernelGGL((k_combine_k<KK, SN, false>), grid, dim3(256), 0, s, w, Ye,      \
-                           drop, Ys, S, T, n, Y, err);
+                           drop, Ys, S, T, n, R, Y, err);
 #define CMB_K(KK)                                                                          \
     case KK:                                                                               \
         if (S == 0) {                                                                      \
@@ -943,15 +965,15 @@ extern "C" int jtk_combine(const float *w, const float *Ye, const uint8_t *drop,
                 CMB_K(1) CMB_K(2) CMB_K(3) CMB_K(4) CMB_K(5) CMB_K(6) CMB_K(7) CMB_K(8)
             }
         } else {
-            hipLaunchKernelGGL(k_combine, grid, dim3(256), 0, s, w, Ye, drop, Ys, S, T, k, n, Y,
-                               err);
+            hipLaunchKernelGGL(k_combine, grid, dim3(256), 0, s, w, Ye, drop, Ys, S, T, k, n, R,
+                               Y, err);
         }
 #undef CMB_K
 #undef CMB_KS
     } else {
         const int64_t th = (int64_t)T * n;
         hipLaunchKernelGGL(k_combine1, dim3((unsigned)((th + 255) / 256)), dim3(256), 0, s, w,
-                           Ye, drop, Ys, S, T, k, n, Y, err);
+                           Ye, drop, Ys, S, T, k, n, R, Y, err);
     }
     return (int)hipGetLastError();
 }

@@ -1102,3 +1102,16 @@ out:
     free(L.sgu_q); free(L.sgu_s); free(L.sd_q); free(L.sd_s);
     return rc;
 }
+
+/* Residual add of the reference's training loop after its MoE layer
+ * (bench/kernel/train_tinystories.c:1147-1160): y = (float)((double)x +
+ * (double)m) per element; rc 2 (y untouched from that element on) when a
+ * sum is not finite. */
+int or_residual_add(const float *X, const float *Mo, float *Y, size_t n) {
+    for (size_t i = 0; i < n; i++) {
+        double v = (double)X[i] + (double)Mo[i];
+        if (!isfinite(v)) return RC_INVAL;
+        Y[i] = (float)v;
+    }
+    return RC_OK;
+}

@@ -173,6 +173,10 @@ int or_moe_q_fwd(const or_moe_q *L, const float *X, int T,
                  int32_t *ids, float *w, int32_t *perm, int32_t *off,
                  float *Ye, float *Ys, int8_t *Hq, float *Hs);
 
+/* Residual add after the layer, bench/kernel/train_tinystories.c:1147-1160:
+ * Y = (float)((double)X + (double)Mo); rc 2 on a non-finite sum. */
+int or_residual_add(const float *X, const float *Mo, float *Y, size_t n);
+
 /* One W8A8 SwiGLU expert as used for the shared experts of or_moe_q_fwd:
  * Wg, Wu, Wd [h][n] fp32, prepared on the fly; Y [T][n]. */
 int or_ffn_fwd(const float *Wg, const float *Wu, const float *Wd, int n,

@@ -99,6 +99,7 @@ class Oracle:
                                    C.c_void_p, _f32p] + [C.c_void_p] * 8
         L.or_ffn_fwd.argtypes = [_f32p, _f32p, _f32p, C.c_int, C.c_int, _f32p, C.c_int,
                                  _f32p]
+        L.or_residual_add.argtypes = [_f32p, _f32p, _f32p, C.c_size_t]
 
     # ---- W8A8 ----
     def quant_rows(self, X):
@@ -281,6 +282,13 @@ class Oracle:
         Y = np.zeros((T, n), np.float32)
         rc = self.lib.or_ffn_fwd(_c(Wg, np.float32), _c(Wu, np.float32), _c(Wd, np.float32),
                                  n, h, X, T, Y)
+        return rc, Y
+
+    def residual_add(self, X, Mo):
+        X = _c(X, np.float32)
+        Y = np.zeros_like(X)
+        rc = self.lib.or_residual_add(X.ravel(), _c(Mo, np.float32).ravel(), Y.reshape(-1),
+                                      X.size)
         return rc, Y
 
     def moe_q(self, n, h, E, k, S, hs, Wgate, Wg, Wu, Wd, Wg_s=None, Wu_s=None,

@@ -661,3 +661,27 @@ def test_w8a8_layer_row_limit_vs_reference(orc, ref):
     r2 = ref.moe_fwd_batch(*(a[:4096] if i == 0 else a for i, a in enumerate(args)), k, 1.5, 1, 0)
     assert r1["rc"] == r2["rc"] == 0
     assert np.array_equal(bits(r1["Y"]), bits(r2["Y"]))
+
+
+def test_residual_add_closed_form(orc):
+    """or_residual_add: (float)((double)x + (double)m), as the reference's
+    training loop adds the residual after its layer
+    (bench/kernel/train_tinystories.c:1147-1160). Rounding the fp64 sum once
+    differs from the float sum x + m on inputs like these, and a non-finite
+    sum is rejected."""
+    rng = np.random.default_rng(34)
+    X = (rng.standard_normal((7, 129)) * 1e3).astype(np.float32)
+    Mo = (rng.standard_normal((7, 129)) * 1e-3).astype(np.float32)
+    X[0, :4] = [1.0, 2.0 ** 24, -3.0, 3e38]
+    Mo[0, :4] = [2.0 ** -24, 1.0, 3.0, 3e38]   # a tie to even, an exact 0, an overflow to inf
+    rc, Y = orc.residual_add(X[1:], Mo[1:])
+    assert rc == 0
+    want = (X[1:].astype(np.float64) + Mo[1:].astype(np.float64)).astype(np.float32)
+    assert np.array_equal(bits(Y), bits(want))
+    rc, Y = orc.residual_add(X[0, :3], Mo[0, :3])
+    assert rc == 0 and Y.tolist() == [1.0, 2.0 ** 24, 0.0]
+    # 3e38 + 3e38 is finite in fp64 and overflows only when rounded to float
+    rc, Y = orc.residual_add(X[0, 3:4], Mo[0, 3:4])
+    assert rc == 0 and np.isinf(Y[0])
+    inf = np.array([np.inf], np.float32)
+    assert orc.residual_add(inf, np.zeros(1, np.float32))[0] == 2

@@ -361,3 +361,103 @@ def test_ffn_decode_nonfinite_row(jt, torch_cuda):
     dY = torch.zeros((4, n), dtype=torch.float32, device="cuda")
     F.fwd(dev(torch, X), dY)
     assert jt.sync_errors() & 0x1  # JT_HIP_EF_NONFINITE_INPUT
+
+
+@pytest.mark.parametrize("routed,T", [(False, 300), (True, 16), (False, 1)])
+def test_layer_residual_fused(jt, orc, torch_cuda, routed, T):
+    """jt_hip_moe_fwd_residual: Y = X + layer(X) with the training loop's two
+    roundings (bench/kernel/train_tinystories.c:1147-1160) fused into the
+    combine. Bit-exact against the layer's own output plus the oracle's
+    residual add, also in place (Y = X), and to tolerance against the oracle
+    layer."""
+    torch = torch_cuda
+    n, h, E, k, S, hs = 256, 128, 16, 4, 2, 128
+    announce(f"layer residual routed={routed} T={T}")
+    rng = np.random.default_rng(900 + T)
+    W = mk_weights(rng, n, h, E, S, hs)
+    Wgate, Wg, Wu, Wd, sh = W
+    X = rng.standard_normal((T, n)).astype(np.float32)
+    ids, w = zipf_ids(rng, T, k, E) if routed else (None, None)
+    L = jt.MoE(n, h, E, k, S, hs, T, dev(torch, Wgate), dev(torch, Wg), dev(torch, Wu),
+               dev(torch, Wd), dev(torch, sh[0]), dev(torch, sh[1]), dev(torch, sh[2]))
+    dX = dev(torch, X)
+    di, dw = dev(torch, ids), dev(torch, w)
+    Y0 = torch.zeros((T, n), dtype=torch.float32, device="cuda")
+    rc = L.fwd_routed(dX, di, dw, Y0) if routed else L.fwd(dX, Y0)
+    assert rc == 0
+    Y1 = torch.zeros((T, n), dtype=torch.float32, device="cuda")
+    assert L.fwd_residual(dX, Y1, di, dw) == 0
+    Xin = dev(torch, X)
+    assert L.fwd_residual(Xin, Xin, di, dw) == 0        # in place
+    assert jt.sync_errors() == 0
+    m = Y0.cpu().numpy()
+    rc, want = orc.residual_add(X, m)
+    assert rc == 0
+    assert np.array_equal(Y1.cpu().numpy().view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(Xin.cpu().numpy().view(np.uint32), want.view(np.uint32))
+    o = orc.moe_q(n, h, E, k, S, hs, None if routed else Wgate, Wg, Wu, Wd, *sh).fwd(X, ids, w)
+    assert o["rc"] == 0
+    close(Y1.cpu().numpy(), orc.residual_add(X, o["Y"])[1])
+
+
+def test_layer_residual_nonfinite(jt, torch_cuda):
+    """A sum that is not finite in fp64 is reported, as the training loop's
+    EINVAL (an infinite input is already rejected by the quantiser)."""
+    torch = torch_cuda
+    n, h, E, k, S, hs, T = 128, 64, 8, 2, 0, 0, 4
+    announce("layer residual non-finite")
+    rng = np.random.default_rng(5)
+    W = mk_weights(rng, n, h, E, S, hs)
+    L = jt.MoE(n, h, E, k, S, hs, T, dev(torch, W[0]), dev(torch, W[1]), dev(torch, W[2]),
+               dev(torch, W[3]))
+    X = rng.standard_normal((T, n)).astype(np.float32)
+    X[2, 7] = np.inf
+    Y = torch.zeros((T, n), dtype=torch.float32, device="cuda")
+    L.fwd_residual(dev(torch, X), Y)
+    assert jt.sync_errors() != 0
+
+
+@pytest.mark.parametrize("router", [True, False])
+def test_layer_save_load_roundtrip(jt, orc, torch_cuda, router):
+    """jt_hip_moe_save / jt_hip_moe_load: the reloaded layer (no quantisation,
+    no packing on load) gives the saved layer's outputs bit for bit, saves to
+    the same bytes, and a corrupted, truncated or foreign buffer is refused."""
+    torch = torch_cuda
+    n, h, E, k, S, hs, T = 256, 128, 16, 4, 2, 192, 130
+    announce(f"layer save/load router={router}")
+    rng = np.random.default_rng(77 + router)
+    W = mk_weights(rng, n, h, E, S, hs)
+    Wgate, Wg, Wu, Wd, sh = W
+    X = rng.standard_normal((T, n)).astype(np.float32)
+    L = jt.MoE(n, h, E, k, S, hs, T, dev(torch, Wgate) if router else None, dev(torch, Wg),
+               dev(torch, Wu), dev(torch, Wd), dev(torch, sh[0]), dev(torch, sh[1]),
+               dev(torch, sh[2]))
+    ids, w = (None, None) if router else zipf_ids(rng, T, k, E)
+    dX = dev(torch, X)
+
+    def fwd(layer):
+        Y = torch.zeros((T, n), dtype=torch.float32, device="cuda")
+        rc = layer.fwd(dX, Y) if router else layer.fwd_routed(dX, dev(torch, ids),
+                                                              dev(torch, w), Y)
+        assert rc == 0
+        assert jt.sync_errors() == 0
+        return Y.cpu().numpy()
+
+    Y1 = fwd(L)
+    blob = L.save()
+    assert blob[:7] == b"JTMOEQ1" and len(blob) % 4096 == 0
+    L2 = jt.MoE.load(blob, T + 50)
+    Y2 = fwd(L2)
+    assert np.array_equal(Y1.view(np.uint32), Y2.view(np.uint32))
+    assert L2.save() == blob
+    for e in (0, E - 1):
+        assert all(np.array_equal(a, b) for a, b in zip(L.export_routed(e), L2.export_routed(e)))
+    # the oracle layer agrees with the reloaded one as with the original
+    o = orc.moe_q(n, h, E, k, S, hs, Wgate if router else None, Wg, Wu, Wd, *sh).fwd(X, ids, w)
+    close(Y2, o["Y"])
+    bad = bytearray(blob)
+    bad[len(bad) // 2] ^= 0x40                  # one payload bit
+    for b_, mt in ((bytes(bad), T), (blob[:-4096], T), (b"JTMOEQ2" + blob[7:], T),
+                   (blob, 0)):
+        with pytest.raises(ValueError, match="rc=2"):
+            jt.MoE.load(b_, mt)
