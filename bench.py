@@ -41,6 +41,8 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-sub", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=15.0)
+    p.add_argument("--cpu-sub-seconds", type=float, default=1.0,
+                   help="time budget per case of the other shapes' CPU baselines")
     p.add_argument("--serial", action="store_true",
                    help="run the timed region with every stage in order on one stream "
                         "(as the profiled pass does), so that a kernel trace of the "
@@ -100,8 +102,7 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)
     assert api.lib().jt_hip_init(0) == 0
-    # a dedicated stream: the library treats a NULL stream as its own stream,
-    # so torch's default stream (handle 0) cannot carry the timing events
+    # a dedicated stream for the layer and its timing events
     stream = torch.cuda.Stream()
     torch.cuda.set_stream(stream)
     if args.decode_only:
@@ -218,7 +219,10 @@ def main():
         step()
         Yh.copy_(Y, non_blocking=True)
 
+    if args.serial:  # keep every kernel alone on the GPU for a kernel trace
+        L.set_profiling(True)
     _, pcie_ms = time_fn(torch, host_step, max(2, args.steps // 2), 2, stream)
+    L.set_profiling(False)
     assert api.sync_errors(stream) == 0
     out["pcie_inclusive"] = {"tokens_per_s": T / (pcie_ms / 1e3), "ms_per_step": pcie_ms,
                              "bytes_over_pcie_per_step": 2 * T * n * 4}
@@ -236,6 +240,22 @@ def main():
 
     if not args.no_sub:
         out["sub"] = sub_benchmarks(np, torch, api, stream)
+        if not args.no_cpu_baseline:
+            # the reference CPU path of the other shapes, one pinned core
+            try:
+                from oracle.cpu_bench import decode_and_stress
+                cb = decode_and_stress(args.cpu_sub_seconds)
+                host = {k: cb.get(k) for k in ("host_cpu", "cores", "core", "kind", "vnni")
+                        if k in cb}
+                for build, res in cb.items():
+                    if not isinstance(res, dict):
+                        continue
+                    for shape, r in res.items():
+                        tgt = "stress_prefill_E512" if shape.startswith("stress") else shape
+                        if tgt in out["sub"]:
+                            out["sub"][tgt].setdefault("cpu_baseline", dict(host))[build] = r
+            except Exception as ex:  # reported, never fatal
+                out["sub_cpu_baseline_error"] = repr(ex)
     print(json.dumps(out), flush=True)
 
 
@@ -312,19 +332,23 @@ def cpu_baseline(np, torch, W, X, n, h, E, k, S, hs, seconds):
             for t in range(tok):
                 R.gemm_per_channel(Sq[t:t + 1], Bd, ss[t], sdn)
 
+    from oracle.cpu_bench import host_info, pinned
     tok, el = 2, 0.0
-    while True:
-        t0 = time.perf_counter()
-        run(tok)
-        el = time.perf_counter() - t0
-        if el >= seconds or tok >= 256:
-            break
-        tok = min(256, max(tok * 2, int(tok * seconds / max(el, 1e-3) * 0.9)))
+    with pinned() as pn:
+        while True:
+            t0 = time.perf_counter()
+            run(tok)
+            el = time.perf_counter() - t0
+            if el >= seconds or tok >= 256:
+                break
+            tok = min(256, max(tok * 2, int(tok * seconds / max(el, 1e-3) * 0.9)))
     return {"value": tok / el, "unit": "tokens/s", "cores": 1, "kind": "reference",
+            "host_cpu": host_info()[0], "core": pn.core,
             "sample": f"{tok} tokens of the same layer (routed: reference "
                       "jt_lowbit_gemm_lut T-MAC per touched expert; shared: reference "
                       "W8A8 quant + gemm_per_channel per token row; top-k: reference "
-                      f"jt_routing_topk), {el:.1f} s single-threaded",
+                      f"jt_routing_topk), {el:.1f} s on one pinned core, default "
+                      "reference build (-mavx2)",
             "seconds": el}
 
 

@@ -155,7 +155,7 @@ def test_gemm_matches_reference_library(jt, ref):
         assert rc == rc2 == 0 and np.array_equal(bits(C), bits(C2))
 
 
-def test_device_gemm_per_row_scales_cfg1(jt, orc, torch_cuda):
+def test_device_gemm_per_row_scales_64x1024x1024(jt, orc, torch_cuda):
     """64x1024x1024 with per-row activation scales (device-resident API)."""
     torch = torch_cuda
     announce("device w8a8 gemm 64x1024x1024 per-row sA")
