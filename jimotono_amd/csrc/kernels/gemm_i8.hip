@@ -216,6 +216,114 @@ __global__ __launch_bounds__(64 * SK_WAVES) void k_w8a8_skinny(
     if (badmid) raise_err(err, EF_NONFINITE_MID);
 }
 
+// ===================== few-row GEMM (16 < M <= 64) =====================
+// The skinny layout for up to four 16-row MFMA tiles: one block of 8 waves
+// per NP panels (16 or 32 channels), the waves splitting K as in the
+// skinny kernel, each weight fragment feeding the four row tiles. A GEMM
+// of 64 rows then runs on N/16 blocks instead of the N/128 of 128-row
+// tiles (64 x 1024 x 1024: 64 blocks instead of 8). The 8 waves' int32
+// partial tiles are summed through LDS one row tile at a time (exact).
+#define R64_WAVES 8
+template <int EPI, int NP>
+__global__ __launch_bounds__(64 * R64_WAVES) void k_w8a8_rows64(
+    const int8_t *__restrict__ A, int lda, const float *__restrict__ sA,
+    const int8_t *__restrict__ Wp, const float *__restrict__ sB, int M, int N, int Kp,
+    float *__restrict__ C, int ldc, uint32_t *err) {
+    __shared__ v4i red[R64_WAVES][NP][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int KB = Kp / 64;
+    const int p0 = blockIdx.x * NP;
+    const int row = lane & 15, kc = lane >> 4;
+    const int8_t *arow[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) arow[t] = A + (int64_t)min(16 * t + row, M - 1) * lda + kc * 16;
+    v4i acc[4][NP];
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int q = 0; q < NP; q++) acc[t][q] = (v4i){0, 0, 0, 0};
+    for (int kb0 = wave; kb0 < KB; kb0 += 2 * R64_WAVES) {
+        v4i a[2][4], b[2][NP];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int kb = kb0 + u * R64_WAVES;
+            if (kb < KB) {  // wave-uniform: a scalar branch
+#pragma unroll
+                for (int q = 0; q < NP; q++)
+                    b[u][q] = *(const v4i *)(Wp + ((int64_t)(p0 + q) * KB + kb) * 1024 + lane * 16);
+#pragma unroll
+                for (int t = 0; t < 4; t++) a[u][t] = *(const v4i *)(arow[t] + kb * 64);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int kb = kb0 + u * R64_WAVES;
+            if (kb < KB) {
+#pragma unroll
+                for (int t = 0; t < 4; t++)
+#pragma unroll
+                    for (int q = 0; q < NP; q++) acc[t][q] = mfma16x16x64(a[u][t], b[u][q], acc[t][q]);
+            }
+        }
+    }
+    // rows past M hold products of the clamped row M-1 and are not stored
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+#pragma unroll
+        for (int q = 0; q < NP; q++) red[wave][q][lane] = acc[t][q];
+        __syncthreads();
+        if (wave == 0) {
+#pragma unroll
+            for (int q = 0; q < NP; q++) {
+                v4i sum = red[0][q][lane];
+#pragma unroll
+                for (int w = 1; w < R64_WAVES; w++) sum += red[w][q][lane];
+                acc[t][q] = sum;
+            }
+        }
+        __syncthreads();
+    }
+    if (wave != 0) return;
+    const int lr = (lane >> 4) * 4, lc = lane & 15;
+    // all scale loads before the first store (one vmcnt for both)
+    double sa[4][4], sb[NP];
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) sa[t][r] = (double)sA[min(16 * t + lr + r, M - 1)];
+#pragma unroll
+    for (int q = 0; q < NP; q++) sb[q] = (double)sB[min((p0 + q) * 16 + lc, N - 1)];
+    uint32_t bad = 0, badmid = 0;
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int m = 16 * t + lr + r;
+            if (m >= M) continue;
+            if (EPI == EPI_PLAIN) {
+#pragma unroll
+                for (int q = 0; q < NP; q++) {
+                    const int col = (p0 + q) * 16 + lc;
+                    const float f = (float)((double)acc[t][q][r] * (sa[t][r] * sb[q]));
+                    if (col < N) {
+                        bad |= !isfinite(f);
+                        C[(int64_t)m * ldc + col] = f;
+                    }
+                }
+            } else if ((p0 + 1) * 16 + lc < N) {  // panel p0 = gate block, p0+1 its up block
+                const float g = (float)((double)acc[t][0][r] * (sa[t][r] * sb[0]));
+                const float u = (float)((double)acc[t][NP - 1][r] * (sa[t][r] * sb[NP - 1]));
+                bad |= (!isfinite(g)) || (!isfinite(u));
+                float sv;
+                badmid |= !silu_mul(g, u, &sv);
+                C[(int64_t)m * ldc + blockIdx.x * 16 + lc] = sv;
+            }
+        }
+    if (bad) raise_err(err, EF_RANGE);
+    if (badmid) raise_err(err, EF_NONFINITE_MID);
+}
+
 template <int QV>
 static hipError_t launch_skinny_xq(const float *X, int ldx, int K, const int8_t *Wp,
                                    const float *sB, int M, int N, int Np, int Kp, float *C,
@@ -284,6 +392,15 @@ extern "C" int jtk_w8a8_gemm(const int8_t *A, int lda, const float *sA, const in
             hipLaunchKernelGGL((k_w8a8_skinny<EPI_PLAIN, 1, 0>), dim3((unsigned)(Np / 16)),
                                dim3(64 * SK_WAVES), 0, s, (const void *)A, lda, sA, Wp, sB, M, N,
                                Kp, Kp, C, ldc, err);
+    } else if (M <= 64) {  // measured: 1.7-2.5x faster than the 128-row tiles
+        if (swiglu)
+            hipLaunchKernelGGL((k_w8a8_rows64<EPI_SWIGLU, 2>), dim3((unsigned)(Np / 32)),
+                               dim3(64 * R64_WAVES), 0, s, A, lda, sA, Wp, sB, M, N, Kp, C, ldc,
+                               err);
+        else
+            hipLaunchKernelGGL((k_w8a8_rows64<EPI_PLAIN, 1>), dim3((unsigned)(Np / 16)),
+                               dim3(64 * R64_WAVES), 0, s, A, lda, sA, Wp, sB, M, N, Kp, C, ldc,
+                               err);
     } else {
         // Tile choice (measured on MI355X): few 128x128 tiles -> 8 waves per
         // block with an intra-block k-split; otherwise 128 x 256 tiles of
