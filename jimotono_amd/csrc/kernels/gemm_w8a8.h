@@ -263,12 +263,11 @@ __global__ __launch_bounds__(64 * WGM * WGN * KS) void k_w8a8_tile(
     // operation, stores included.
     __shared__ __attribute__((aligned(16))) double s_tab[EPI == EPI_SWIGLU ? 64 : 2];
     const double tabv = EPI == EPI_SWIGLU ? exp_tab_load(lane) : 0.0;
-    static_assert((BM + BN) / 64 <= NWG * KS, "a wave per 64 scales");
-    if (wave < BM / 64) {
-        dma<4>(sA + min(m0 + 64 * wave + lane, M - 1), s_rs + 64 * wave);
-    } else if (wave < (BM + BN) / 64) {
-        const int w = wave - BM / 64;
-        dma<4>(sB + min(n0 + 64 * w + lane, N - 1), s_cs + 64 * w);
+    for (int c = wave; c < (BM + BN) / 64; c += NWG * KS) {  // 64 scales per copy
+        if (c < BM / 64)
+            dma<4>(sA + min(m0 + 64 * c + lane, M - 1), s_rs + 64 * c);
+        else
+            dma<4>(sB + min(n0 + 64 * (c - BM / 64) + lane, N - 1), s_cs + 64 * (c - BM / 64));
     }
     auto issue = [&](int sg) {
         int8_t *st = smem + (sg % NST) * STAGE + kg * NP * 1024;
