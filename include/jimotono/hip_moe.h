@@ -212,6 +212,30 @@ int jt_hip_moe_stage_times(jt_hip_moe *L, const char **names, double *ms,
                            int cap, int *n, int *count);
 void jt_hip_moe_free(jt_hip_moe *L);
 
+/* ---- batched backward on device pointers ----
+ * The device form of jt_moe_bwd_batch (moe_layer.h; reference
+ * src/moe_layer.c:1684-2502): the same arguments as device pointers
+ * (ids, perm, off as size_t), validate = 1 for the checked form, 0 for the
+ * unchecked one, and a caller workspace d_ws of at least
+ * jt_hip_moe_bwd_batch_ws_bytes() bytes, 256-byte aligned. perm needs
+ * off[E] entries. Asynchronous on `stream`; inconsistent ids / off / perm
+ * raise JT_HIP_EF_BAD_ID, non-finite inputs (validate) JT_HIP_EF_NONFINITE_INPUT
+ * and non-finite intermediates JT_HIP_EF_NONFINITE_MID, and the outputs are
+ * then not meaningful (read them with jt_hip_sync_errors). The workspace is
+ * not kept between calls. */
+size_t jt_hip_moe_bwd_batch_ws_bytes(int T, int n, int h, int n_experts,
+                                     int topk, int n_shared);
+int jt_hip_moe_bwd_batch(
+    const float *dY, const float *X, const float *Wgate, const float *Wg,
+    const float *Wu, const float *Wd, const float *Wg_s, const float *Wu_s,
+    const float *Wd_s, const size_t *ids, const float *weights,
+    const float *Gsel, const float *Usel, const float *Ysel, const float *Gs,
+    const float *Us, const size_t *perm, const size_t *off,
+    const unsigned char *drop, float *dX, float *dWgate, float *dWg,
+    float *dWu, float *dWd, float *dWg_s, float *dWu_s, float *dWd_s,
+    float *dLogits, int T, int n, int h, int n_experts, int topk,
+    int n_shared, int validate, void *d_ws, size_t ws_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -13,9 +13,11 @@
  * These are host-pointer entry points: inputs are staged into HBM, every
  * stage (gate logits, top-k, sort, renormalisation, gather, expert GEMMs,
  * SwiGLU, combine, shared experts) runs as HIP kernels, and Y is copied back
- * only after the whole forward succeeded. The single-token training helpers
- * of the reference (jt_moe_fwd, jt_moe_bwd, jt_moe_bwd_batch,
- * jt_moe_sticky_seq_loss) are not part of this library.
+ * only after the whole forward succeeded. The batched backward
+ * (jt_moe_bwd_batch, jt_moe_bwd_batch_unchecked) runs the same way on the
+ * forward's permutation. The single-token training helpers of the reference
+ * (jt_moe_fwd, jt_moe_bwd, jt_moe_sticky_seq_loss) are not part of this
+ * library.
  */
 #include <stddef.h>
 
@@ -79,6 +81,50 @@ int jt_moe_fwd_batch_unchecked(
     size_t *JT_RESTRICT out_perm, size_t *JT_RESTRICT out_off,
     unsigned char *JT_RESTRICT out_drop, size_t *JT_RESTRICT out_kept,
     size_t *JT_RESTRICT out_dropped);
+
+/* Batched backward of T tokens on the forward's permutation (no re-sort).
+ * dY, X [T][n]; weights as the forward; ids, weights [T][k]; caches Gsel,
+ * Usel [T*k][h], Ysel [T*k][n], Gs, Us [T][S][h]; perm [kept], off [E+1],
+ * drop [T*k] as the forward wrote them. Outputs (overwritten): dX [T][n],
+ * dWgate [E][n], dWg/dWu/dWd [E][h][n], dWg_s/dWu_s/dWd_s [S][h][n],
+ * dLogits [T][E] (NULL allowed). JT_OK, or JT_ERR_INVAL with errno EINVAL
+ * and no output written. Reference: moe_layer.h:277-329,
+ * src/moe_layer.c:1684-2467. */
+int jt_moe_bwd_batch(const float *JT_RESTRICT dY, const float *JT_RESTRICT X,
+                     const float *JT_RESTRICT Wgate, const float *JT_RESTRICT Wg,
+                     const float *JT_RESTRICT Wu, const float *JT_RESTRICT Wd,
+                     const float *JT_RESTRICT Wg_s, const float *JT_RESTRICT Wu_s,
+                     const float *JT_RESTRICT Wd_s, const size_t *JT_RESTRICT ids,
+                     const float *JT_RESTRICT weights, const float *JT_RESTRICT Gsel,
+                     const float *JT_RESTRICT Usel, const float *JT_RESTRICT Ysel,
+                     const float *JT_RESTRICT Gs, const float *JT_RESTRICT Us,
+                     const size_t *JT_RESTRICT perm, const size_t *JT_RESTRICT off,
+                     const unsigned char *JT_RESTRICT drop, float *JT_RESTRICT dX,
+                     float *JT_RESTRICT dWgate, float *JT_RESTRICT dWg,
+                     float *JT_RESTRICT dWu, float *JT_RESTRICT dWd,
+                     float *JT_RESTRICT dWg_s, float *JT_RESTRICT dWu_s,
+                     float *JT_RESTRICT dWd_s, float *JT_RESTRICT dLogits, int T, int n,
+                     int h, int n_experts, int topk, int n_shared);
+
+/* Same computation without the finiteness scans of the weights and caches
+ * and without the weight-range test. The index checks the device kernels
+ * depend on (ids < E for kept pairs, off monotone from 0 with
+ * off[E] == kept, perm an exact enumeration of the kept pairs) still run;
+ * a permutation written by the forward always passes them.
+ * Reference: moe_layer.h:330-362, src/moe_layer.c:2469-2502. */
+int jt_moe_bwd_batch_unchecked(
+    const float *JT_RESTRICT dY, const float *JT_RESTRICT X, const float *JT_RESTRICT Wgate,
+    const float *JT_RESTRICT Wg, const float *JT_RESTRICT Wu, const float *JT_RESTRICT Wd,
+    const float *JT_RESTRICT Wg_s, const float *JT_RESTRICT Wu_s,
+    const float *JT_RESTRICT Wd_s, const size_t *JT_RESTRICT ids,
+    const float *JT_RESTRICT weights, const float *JT_RESTRICT Gsel,
+    const float *JT_RESTRICT Usel, const float *JT_RESTRICT Ysel, const float *JT_RESTRICT Gs,
+    const float *JT_RESTRICT Us, const size_t *JT_RESTRICT perm,
+    const size_t *JT_RESTRICT off, const unsigned char *JT_RESTRICT drop,
+    float *JT_RESTRICT dX, float *JT_RESTRICT dWgate, float *JT_RESTRICT dWg,
+    float *JT_RESTRICT dWu, float *JT_RESTRICT dWd, float *JT_RESTRICT dWg_s,
+    float *JT_RESTRICT dWu_s, float *JT_RESTRICT dWd_s, float *JT_RESTRICT dLogits, int T,
+    int n, int h, int n_experts, int topk, int n_shared);
 
 #ifdef __cplusplus
 }

@@ -91,6 +91,10 @@ _PROTOS = {
     "jt_hip_moe_stage_times": [_vp, C.POINTER(C.c_char_p), C.POINTER(C.c_double), _i,
                                C.POINTER(_i), C.POINTER(_i)],
     "jt_hip_moe_free": ([_vp], None),
+    "jt_moe_bwd_batch": [_vp] * 28 + [_i] * 6,
+    "jt_moe_bwd_batch_unchecked": [_vp] * 28 + [_i] * 6,
+    "jt_hip_moe_bwd_batch_ws_bytes": ([_i] * 6, _sz),
+    "jt_hip_moe_bwd_batch": [_vp] * 28 + [_i] * 7 + [_vp, _sz, _vp],
 }
 
 
@@ -254,8 +258,80 @@ def moe_batch_sort(ids, T, k, E, cap_factor):
     return rc, perm[: kept.value].astype(np.int64), off.astype(np.int64), drop, dropped.value
 
 
-def moe_fwd_batch(X, Wgate, Wg, Wu, Wd, Wg_s, Wu_s, Wd_s, k, cap_factor, unchecked=False):
-    """jt_moe_fwd_batch with the process flags as currently set."""
+_BWD_OUT = ("dX", "dWgate", "dWg", "dWu", "dWd", "dWg_s", "dWu_s", "dWd_s", "dLogits")
+
+
+def moe_bwd_batch(dY, X, Wgate, Wg, Wu, Wd, Wg_s, Wu_s, Wd_s, ids, w, Gsel, Usel, Ysel, Gs,
+                  Us, perm, off, drop, k, unchecked=False, logits=True):
+    """jt_moe_bwd_batch (or _unchecked) on numpy arrays: dY, X [T][n];
+    W* [E][h][n] and [S][h][n] (Wg_s None for S = 0); ids, w [T][k];
+    Gsel, Usel [T*k][h]; Ysel [T*k][n]; Gs, Us [T][S][h]; perm, off, drop
+    as the forward returned them. Returns a dict of rc and the outputs
+    (NaN-filled where the call wrote nothing)."""
+    f = lambda a: _c(a, np.float32)
+    dY, X, Wgate, Wg, Wu, Wd = map(f, (dY, X, Wgate, Wg, Wu, Wd))
+    T, n = X.shape
+    E, h = Wg.shape[0], Wg.shape[1]
+    S = 0 if Wg_s is None else Wg_s.shape[0]
+    ins = [dY, X, Wgate, Wg, Wu, Wd]
+    ins += [None] * 3 if S == 0 else [f(Wg_s), f(Wu_s), f(Wd_s)]
+    ins += [_c(ids, np.uint64), f(w), f(Gsel), f(Usel), f(Ysel)]
+    ins += [None] * 2 if S == 0 else [f(Gs), f(Us)]
+    pm = _c(perm, np.uint64)
+    ins += [pm if pm.size else np.zeros(1, np.uint64), _c(off, np.uint64), _c(drop, np.uint8)]
+    shapes = dict(dX=(T, n), dWgate=(E, n), dWg=(E, h, n), dWu=(E, h, n), dWd=(E, h, n))
+    if S:
+        shapes.update(dWg_s=(S, h, n), dWu_s=(S, h, n), dWd_s=(S, h, n))
+    if logits:
+        shapes["dLogits"] = (T, E)
+    out = {nm: np.full(sh, np.nan, np.float32) for nm, sh in shapes.items()}
+    ptr = lambda a: None if a is None else a.ctypes.data
+    fn = lib().jt_moe_bwd_batch_unchecked if unchecked else lib().jt_moe_bwd_batch
+    out["rc"] = fn(*[ptr(a) for a in ins], *[ptr(out.get(nm)) for nm in _BWD_OUT],
+                   T, n, h, E, k, S)
+    return out
+
+
+def moe_bwd_batch_device(dY, X, Wgate, Wg, Wu, Wd, Wg_s, Wu_s, Wd_s, ids, w, Gsel, Usel,
+                         Ysel, Gs, Us, perm, off, drop, k, validate=1, out=None, ws=None,
+                         logits=True, stream=None):
+    """jt_hip_moe_bwd_batch on torch tensors already on the GPU (ids, perm,
+    off int64; drop uint8), asynchronous on `stream` (default: torch's
+    current stream). `out` (dict of output tensors) and `ws` (uint8 tensor
+    of jt_hip_moe_bwd_batch_ws_bytes) are allocated when not given.
+    Returns (rc, out, ws); read the error bits with sync_errors()."""
+    import torch
+    T, n = X.shape
+    E, h = Wg.shape[0], Wg.shape[1]
+    S = 0 if Wg_s is None else Wg_s.shape[0]
+    dev = X.device
+    if out is None:
+        out = dict(dX=torch.empty((T, n), device=dev), dWgate=torch.empty((E, n), device=dev),
+                   dWg=torch.empty((E, h, n), device=dev), dWu=torch.empty((E, h, n), device=dev),
+                   dWd=torch.empty((E, h, n), device=dev))
+        if S:
+            for nm in ("dWg_s", "dWu_s", "dWd_s"):
+                out[nm] = torch.empty((S, h, n), device=dev)
+        if logits:
+            out["dLogits"] = torch.empty((T, E), device=dev)
+    nb = lib().jt_hip_moe_bwd_batch_ws_bytes(T, n, h, E, k, S)
+    if ws is None:
+        ws = torch.empty(nb, dtype=torch.uint8, device=dev)
+    ptr = lambda a: None if a is None else a.data_ptr()
+    ins = [dY, X, Wgate, Wg, Wu, Wd, Wg_s, Wu_s, Wd_s, ids, w, Gsel, Usel, Ysel, Gs, Us, perm,
+           off, drop]
+    st = _stream(stream)
+    rc = lib().jt_hip_moe_bwd_batch(*[ptr(a) for a in ins],
+                                    *[ptr(out.get(nm)) for nm in _BWD_OUT], T, n, h, E, k, S,
+                                    int(validate), ptr(ws), ws.numel(), st)
+    return rc, out, ws
+
+
+def moe_fwd_batch(X, Wgate, Wg, Wu, Wd, Wg_s, Wu_s, Wd_s, k, cap_factor, unchecked=False,
+                  caches=False):
+    """jt_moe_fwd_batch with the process flags as currently set; caches=True
+    also returns the backward's caches Gsel, Usel [T*k][h] and Gs, Us
+    [T][S][h]."""
     X = _c(X, np.float32)
     T, n = X.shape
     E, h = Wg.shape[0], Wg.shape[1]
@@ -271,14 +347,21 @@ def moe_fwd_batch(X, Wgate, Wg, Wu, Wd, Wg_s, Wu_s, Wd_s, k, cap_factor, uncheck
     drop = np.zeros(T * k, np.uint8)
     Ysel = np.zeros((T * k, n), np.float32)
     kept, dropped = C.c_size_t(0), C.c_size_t(0)
+    cache = {}
+    if caches:
+        cache = dict(Gsel=np.zeros((T * k, h), np.float32), Usel=np.zeros((T * k, h), np.float32))
+        if S:
+            cache.update(Gs=np.zeros((T, S, h), np.float32), Us=np.zeros((T, S, h), np.float32))
+    cp = lambda nm: cache[nm].ctypes.data if nm in cache else None
     fn = lib().jt_moe_fwd_batch_unchecked if unchecked else lib().jt_moe_fwd_batch
     p = [a.ctypes.data for a in keep] + [None if a is None else a.ctypes.data for a in sh]
     rc = fn(*p[:5], *p[5:], Y.ctypes.data, T, n, h, E, k, S, ids.ctypes.data, w.ctypes.data,
-            None, None, Ysel.ctypes.data, None, None, cap_factor, perm.ctypes.data,
-            off.ctypes.data, drop.ctypes.data, C.addressof(kept), C.addressof(dropped))
+            cp("Gsel"), cp("Usel"), Ysel.ctypes.data, cp("Gs"), cp("Us"), cap_factor,
+            perm.ctypes.data, off.ctypes.data, drop.ctypes.data, C.addressof(kept),
+            C.addressof(dropped))
     return dict(rc=rc, Y=Y, ids=ids.astype(np.int64), w=w,
                 perm=perm[: kept.value].astype(np.int64), off=off.astype(np.int64),
-                drop=drop, Ysel=Ysel)
+                drop=drop, Ysel=Ysel, **cache)
 
 
 # ---------------- device-resident API ----------------

@@ -155,6 +155,30 @@ int jtk_gemm_f64acc(const float *A, const float *B, float *C, int M, int N, int 
 int jtk_lowbit_fq_cols(float *W, int k, int h, int bits, float *ws, uint32_t *err,
                        hipStream_t s);
 
+/* moe_bwd.hip: batched MoE backward on the forward's permutation.
+ * Device pointers in the reference's argument order (ids, perm, off as
+ * size_t); dLogits and the shared arrays may be NULL (S == 0). */
+typedef struct jtk_bwd_io {
+    const float *dY, *X, *Wgate, *Wg, *Wu, *Wd, *Wg_s, *Wu_s, *Wd_s;
+    const uint64_t *ids;
+    const float *weights, *Gsel, *Usel, *Ysel, *Gs, *Us;
+    const uint64_t *perm, *off;
+    const uint8_t *drop;
+    float *dX, *dWgate, *dWg, *dWu, *dWd, *dWg_s, *dWu_s, *dWd_s, *dLogits;
+} jtk_bwd_io;
+typedef struct jtk_bwd_ws {
+    uint32_t *ctrl, *seen;
+    int32_t *key, *inv, *rowq, *rank, *cnt, *tot, *off2, *perm2, *off32, *tiles, *ntiles;
+    double *dw, *dlog, *gate_dl;
+    int32_t *gate_e, *gate_n, *tokpos, *tokcnt;
+    float *Xp, *dYp, *Dg, *Du, *Ss, *Dxe, *SDg, *SDu, *SSs, *SDxe;
+} jtk_bwd_ws;
+/* Bytes of the workspace; with base != NULL also fills *w with its pieces. */
+size_t jtk_bwd_ws_layout(int T, int n, int h, int E, int k, int S, jtk_bwd_ws *w, char *base);
+/* Enqueues the whole backward; returns nonzero when a launch failed. */
+int jtk_bwd_batch(const jtk_bwd_io *io, int T, int n, int h, int E, int k, int S, int validate,
+                  const jtk_bwd_ws *w, uint32_t *err, hipStream_t s);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1115,3 +1115,307 @@ int or_residual_add(const float *X, const float *Mo, float *Y, size_t n) {
     }
     return RC_OK;
 }
+
+/* ===================== batched backward ===================== */
+
+/* C[r][c] = fp32 sum over kk ascending of A(r, kk) * B(kk, c), one rounded
+ * multiply and one rounded add per step (src/moe_gemm.c:47-61), with
+ * A(r, kk) = A[r*ar + kk*ak] and B(kk, c) = B[kk*bk + c*bc]: the strides
+ * stand for the reference's exact transposes (src/moe_gemm.c:17-41). */
+static void gemm_f32_strided(const float *A, size_t ar, size_t ak,
+                             const float *B, size_t bk, size_t bc, float *C,
+                             int M, int N, int K) {
+    for (int r = 0; r < M; r++)
+        for (int c = 0; c < N; c++) {
+            float acc = 0.0f;
+            for (int kk = 0; kk < K; kk++) {
+                float p = A[(size_t)r * ar + (size_t)kk * ak] *
+                          B[(size_t)kk * bk + (size_t)c * bc];
+                acc = acc + p;
+            }
+            C[(size_t)r * N + c] = acc;
+        }
+}
+
+/* SwiGLU backward of one element in fp64 (src/moe_layer.c:1680-1682,
+ * 2204-2233): sig = 1/(1+exp(-g)), silu = g*sig,
+ * dsilu = sig*(1 + g*(1-sig)); dg = acc*u*dsilu, du = acc*silu,
+ * s = silu*u. Returns 0 when acc or a result is not finite. */
+static int swiglu_bwd_elem(float g, float u, float dot, float *dg, float *du,
+                           float *s) {
+    double gi = (double)g, ui = (double)u, acc = (double)dot;
+    double sig = 1.0 / (1.0 + exp(-gi));
+    double silu = gi * sig;
+    double dsilu = sig * (1.0 + gi * (1.0 - sig));
+    if (!isfinite(acc)) return 0;
+    double gd = acc * ui * dsilu, ud = acc * silu, sv = silu * ui;
+    if (!isfinite(gd) || !isfinite(ud) || !isfinite(sv)) return 0;
+    *dg = (float)gd;
+    *du = (float)ud;
+    *s = (float)sv;
+    return 1;
+}
+
+/* One expert's backward over M rows (src/moe_layer.c:2196-2283 for a routed
+ * expert, :2310-2396 for a shared one): Xr, Dy [M][n]; G, U rows of h with
+ * row stride ldgu; W* [h][n]. dxe [M][n] = (float)((double)(Dg Wg) +
+ * (double)(Du Wu)); oWg = Dg^T Xr, oWu = Du^T Xr, oWd = S^T Dy. */
+static int expert_bwd(const float *Xr, const float *Dy, const float *G,
+                      const float *U, size_t ldgu, const float *Wg,
+                      const float *Wu, const float *Wd, int M, int n, int h,
+                      float *dxe, float *oWg, float *oWu, float *oWd) {
+    size_t Mh = (size_t)M * h, Mn = (size_t)M * n;
+    float *buf = malloc((4 * Mh + 2 * Mn) * sizeof(float));
+    if (!buf) return RC_NOMEM;
+    float *dot = buf, *dg = dot + Mh, *du = dg + Mh, *ss = du + Mh;
+    float *d1 = ss + Mh, *d2 = d1 + Mn;
+    int rc = RC_INVAL;
+    /* dot[m][i] = sum_j Dy[m][j] * Wd[i][j] */
+    gemm_f32_strided(Dy, (size_t)n, 1, Wd, 1, (size_t)n, dot, M, h, n);
+    for (int m = 0; m < M; m++)
+        for (int i = 0; i < h; i++) {
+            size_t a = (size_t)m * ldgu + i, o = (size_t)m * h + i;
+            if (!swiglu_bwd_elem(G[a], U[a], dot[o], &dg[o], &du[o], &ss[o]))
+                goto out;
+        }
+    gemm_f32_strided(dg, (size_t)h, 1, Wg, (size_t)n, 1, d1, M, n, h);
+    gemm_f32_strided(du, (size_t)h, 1, Wu, (size_t)n, 1, d2, M, n, h);
+    for (size_t i = 0; i < Mn; i++) dxe[i] = (float)((double)d1[i] + (double)d2[i]);
+    /* dW[i][j] = sum over m ascending of D[m][i] * rows[m][j] */
+    gemm_f32_strided(dg, 1, (size_t)h, Xr, (size_t)n, 1, oWg, h, n, M);
+    gemm_f32_strided(du, 1, (size_t)h, Xr, (size_t)n, 1, oWu, h, n, M);
+    gemm_f32_strided(ss, 1, (size_t)h, Dy, (size_t)n, 1, oWd, h, n, M);
+    rc = RC_OK;
+out:
+    free(buf);
+    return rc;
+}
+
+static int all_finite_f(const float *x, size_t n) {
+    for (size_t i = 0; i < n; i++)
+        if (!isfinite((double)x[i])) return 0;
+    return 1;
+}
+
+/* src/moe_layer.c:1684-2439. Steps, in the reference's order:
+ *  0. argument checks (validate: finiteness of every input, ids < E,
+ *     weights in [0,1], drop in {0,1}, off monotone from 0, perm an exact
+ *     enumeration of the kept pairs; otherwise only off[E] <= T*k);
+ *  1. dw[q] = lane-4 fp64 dot(Ysel[q], dY[t]) for kept q, 0 for dropped;
+ *  2. per token s = sum_kept (double)w*dw in slot order,
+ *     dlog[q] = (double)w*(dw - s), dLogits[t][ids[q]] = (float)dlog;
+ *  3. gate-path dX: the first two kept slots of the token, ordered by
+ *     expert id, acc = sum dlog*(double)Wgate[e][j], dx[t][j] += acc;
+ *  4. dWgate[e][j] += (float)(dlog*(double)X[t][j]) in token/slot order;
+ *  5. routed experts in id order on their perm rows, rows weighted
+ *     dYe = (float)((double)w*(double)dY); dx[t] += (double)dxe in perm order;
+ *  6. shared experts in index order on all tokens, dY unweighted;
+ *  7. dX = (float)dx after a finiteness check. */
+int or_moe_bwd_batch(const float *dY, const float *X, const float *Wgate,
+                     const float *Wg, const float *Wu, const float *Wd,
+                     const float *Wg_s, const float *Wu_s, const float *Wd_s,
+                     const int64_t *ids, const float *weights,
+                     const float *Gsel, const float *Usel, const float *Ysel,
+                     const float *Gs, const float *Us, const int64_t *perm,
+                     const int64_t *off, const unsigned char *drop, float *dX,
+                     float *dWgate, float *dWg, float *dWu, float *dWd,
+                     float *dWg_s, float *dWu_s, float *dWd_s, float *dLogits,
+                     int T, int n, int h, int E, int k, int S, int validate) {
+    if (!dY || !X || !Wgate || !Wg || !Wu || !Wd || !ids || !weights ||
+        !Gsel || !Usel || !Ysel || !perm || !off || !drop || !dX ||
+        !dWgate || !dWg || !dWu || !dWd)
+        return RC_INVAL;
+    if (T <= 0 || n <= 0 || h <= 0 || n > 4096 || h > 4096 || E <= 0 ||
+        E > 4096 || k <= 0 || k > E || k > 64 || S < 0 || S > 8)
+        return RC_INVAL;
+    if (S > 0 && (!Wg_s || !Wu_s || !Wd_s || !Gs || !Us || !dWg_s || !dWu_s ||
+                  !dWd_s))
+        return RC_INVAL;
+    const size_t Tk = (size_t)T * k, Tn = (size_t)T * n, nh = (size_t)n * h;
+    size_t kept;
+    if (validate) {
+        if (!all_finite_f(dY, Tn) || !all_finite_f(X, Tn) ||
+            !all_finite_f(Wgate, (size_t)E * n) || !all_finite_f(Wg, E * nh) ||
+            !all_finite_f(Wu, E * nh) || !all_finite_f(Wd, E * nh) ||
+            !all_finite_f(weights, Tk) || !all_finite_f(Gsel, Tk * h) ||
+            !all_finite_f(Usel, Tk * h) || !all_finite_f(Ysel, Tk * n))
+            return RC_INVAL;
+        if (S > 0 && (!all_finite_f(Wg_s, S * nh) || !all_finite_f(Wu_s, S * nh) ||
+                      !all_finite_f(Wd_s, S * nh) ||
+                      !all_finite_f(Gs, Tk / k * S * h) ||
+                      !all_finite_f(Us, Tk / k * S * h)))
+            return RC_INVAL;
+        for (size_t q = 0; q < Tk; q++) {
+            if (ids[q] < 0 || ids[q] >= E) return RC_INVAL;
+            if (!(weights[q] >= 0.0f) || !(weights[q] <= 1.0f)) return RC_INVAL;
+            if (drop[q] > 1) return RC_INVAL;
+        }
+        if (off[0] != 0) return RC_INVAL;
+        for (int e = 0; e < E; e++)
+            if (off[e + 1] < off[e] || (size_t)off[e + 1] > Tk) return RC_INVAL;
+        kept = (size_t)off[E];
+        unsigned char *seen = calloc(Tk, 1);
+        if (!seen) return RC_NOMEM;
+        size_t nkept = 0;
+        int bad = 0;
+        for (size_t i = 0; i < kept && !bad; i++) {
+            int64_t q = perm[i];
+            if (q < 0 || (size_t)q >= Tk || drop[q] || seen[q]) bad = 1;
+            else seen[q] = 1;
+        }
+        for (size_t q = 0; q < Tk && !bad; q++)
+            if (!drop[q]) {
+                nkept++;
+                if (!seen[q]) bad = 1;
+            }
+        free(seen);
+        if (bad || nkept != kept) return RC_INVAL;
+    } else {
+        if (off[E] < 0 || (size_t)off[E] > Tk) return RC_INVAL;
+        kept = (size_t)off[E];
+    }
+    (void)kept;
+    double *dx = calloc(Tn, sizeof(double));
+    double *dw = malloc(Tk * sizeof(double)), *dlog = malloc(Tk * sizeof(double));
+    int rc = RC_NOMEM;
+    float *Xe = NULL, *Dye = NULL, *Ge = NULL, *Ue = NULL, *dxe = NULL;
+    if (!dx || !dw || !dlog) goto out;
+    memset(dWgate, 0, (size_t)E * n * sizeof(float));
+    memset(dWg, 0, E * nh * sizeof(float));
+    memset(dWu, 0, E * nh * sizeof(float));
+    memset(dWd, 0, E * nh * sizeof(float));
+    if (S > 0) {
+        memset(dWg_s, 0, S * nh * sizeof(float));
+        memset(dWu_s, 0, S * nh * sizeof(float));
+        memset(dWd_s, 0, S * nh * sizeof(float));
+    }
+    if (dLogits) memset(dLogits, 0, (size_t)T * E * sizeof(float));
+    rc = RC_INVAL;
+    /* 1 */
+    for (size_t q = 0; q < Tk; q++) {
+        dlog[q] = 0.0;
+        dw[q] = drop[q] ? 0.0 : or_logit_lane4(Ysel + q * n, dY + q / k * n, n);
+        if (!isfinite(dw[q])) goto out;
+    }
+    /* 2 */
+    for (int t = 0; t < T; t++) {
+        double s = 0.0;
+        for (int p = 0; p < k; p++) {
+            size_t q = (size_t)t * k + p;
+            if (!drop[q]) s = s + (double)weights[q] * dw[q];
+        }
+        if (!isfinite(s)) goto out;
+        for (int p = 0; p < k; p++) {
+            size_t q = (size_t)t * k + p;
+            if (drop[q]) continue;
+            if (ids[q] < 0 || ids[q] >= E) goto out;
+            double v = (double)weights[q] * (dw[q] - s);
+            if (!isfinite(v)) goto out;
+            dlog[q] = v;
+            if (dLogits) dLogits[(size_t)t * E + ids[q]] = (float)v;
+        }
+    }
+    /* 3 */
+    for (int t = 0; t < T; t++) {
+        int64_t es[2] = {0, 0};
+        double dl[2] = {0.0, 0.0};
+        int nk = 0;
+        for (int p = 0; p < k && nk < 2; p++) {
+            size_t q = (size_t)t * k + p;
+            if (drop[q]) continue;
+            es[nk] = ids[q];
+            dl[nk] = dlog[q];
+            nk++;
+        }
+        if (nk == 2 && es[0] > es[1]) {
+            int64_t te = es[0];
+            double td = dl[0];
+            es[0] = es[1], dl[0] = dl[1];
+            es[1] = te, dl[1] = td;
+        }
+        for (int j = 0; j < n; j++) {
+            double acc = 0.0;
+            for (int a = 0; a < nk; a++)
+                acc = acc + dl[a] * (double)Wgate[(size_t)es[a] * n + j];
+            dx[(size_t)t * n + j] = dx[(size_t)t * n + j] + acc;
+        }
+    }
+    /* 4 */
+    for (size_t q = 0; q < Tk; q++) {
+        if (drop[q]) continue;
+        const float *xt = X + q / k * n;
+        float *rg = dWgate + (size_t)ids[q] * n;
+        for (int j = 0; j < n; j++) rg[j] = rg[j] + (float)(dlog[q] * (double)xt[j]);
+    }
+    /* 5 */
+    size_t maxMe = 0;
+    for (int e = 0; e < E; e++) {
+        int64_t me = off[e + 1] - off[e];
+        if (me < 0 || me > INT32_MAX) goto out;
+        if ((size_t)me > maxMe) maxMe = (size_t)me;
+    }
+    size_t rows = maxMe > (size_t)T ? maxMe : (size_t)T;
+    rc = RC_NOMEM;
+    Xe = malloc(rows * n * sizeof(float));
+    Dye = malloc(rows * n * sizeof(float));
+    Ge = malloc(rows * h * sizeof(float));
+    Ue = malloc(rows * h * sizeof(float));
+    dxe = malloc(rows * n * sizeof(float));
+    if (!Xe || !Dye || !Ge || !Ue || !dxe) goto out;
+    rc = RC_INVAL;
+    for (int e = 0; e < E; e++) {
+        const size_t b0 = (size_t)off[e];
+        const int Me = (int)(off[e + 1] - off[e]);
+        if (Me == 0) continue;
+        for (int m = 0; m < Me; m++) {
+            int64_t q = perm[b0 + m];
+            if (q < 0 || (size_t)q >= Tk || drop[q]) goto out;
+            const size_t t = (size_t)q / k;
+            const double w = (double)weights[q];
+            memcpy(Xe + (size_t)m * n, X + t * n, n * sizeof(float));
+            memcpy(Ge + (size_t)m * h, Gsel + (size_t)q * h, h * sizeof(float));
+            memcpy(Ue + (size_t)m * h, Usel + (size_t)q * h, h * sizeof(float));
+            for (int j = 0; j < n; j++)
+                Dye[(size_t)m * n + j] = (float)(w * (double)dY[t * n + j]);
+        }
+        int r = expert_bwd(Xe, Dye, Ge, Ue, (size_t)h, Wg + e * nh, Wu + e * nh,
+                           Wd + e * nh, Me, n, h, dxe, dWg + e * nh, dWu + e * nh,
+                           dWd + e * nh);
+        if (r != RC_OK) {
+            rc = r;
+            goto out;
+        }
+        for (int m = 0; m < Me; m++) {
+            double *xa = dx + (size_t)perm[b0 + m] / k * n;
+            for (int j = 0; j < n; j++)
+                xa[j] = xa[j] + (double)dxe[(size_t)m * n + j];
+        }
+    }
+    /* 6 */
+    for (int s = 0; s < S; s++) {
+        int r = expert_bwd(X, dY, Gs + (size_t)s * h, Us + (size_t)s * h,
+                           (size_t)S * h, Wg_s + s * nh, Wu_s + s * nh,
+                           Wd_s + s * nh, T, n, h, dxe, dWg_s + s * nh,
+                           dWu_s + s * nh, dWd_s + s * nh);
+        if (r != RC_OK) {
+            rc = r;
+            goto out;
+        }
+        for (size_t i = 0; i < Tn; i++) dx[i] = dx[i] + (double)dxe[i];
+    }
+    /* 7 */
+    for (size_t i = 0; i < Tn; i++)
+        if (!isfinite(dx[i])) goto out;
+    for (size_t i = 0; i < Tn; i++) dX[i] = (float)dx[i];
+    rc = RC_OK;
+out:
+    free(dx);
+    free(dw);
+    free(dlog);
+    free(Xe);
+    free(Dye);
+    free(Ge);
+    free(Ue);
+    free(dxe);
+    return rc;
+}

@@ -136,6 +136,23 @@ int or_moe_fwd_batch(const float *X, const float *Wgate, const float *Wg,
                      int64_t *out_kept, int w8a8_on, int lowbit_mode,
                      float *cache_Ysel);
 
+/* ---------- batched backward (src/moe_layer.c:1684-2502) ----------
+ * jt_moe_bwd_batch (validate = 1) / jt_moe_bwd_batch_unchecked
+ * (validate = 0) on the forward's permutation. Shapes as in the reference
+ * (moe_layer.h:276-330); ids/perm/off as int64. dLogits may be NULL; the
+ * shared arrays may be NULL when S == 0. Returns 0 or 2 (EINVAL cases). On
+ * 2 the outputs hold whatever the steps before the failure wrote. */
+int or_moe_bwd_batch(const float *dY, const float *X, const float *Wgate,
+                     const float *Wg, const float *Wu, const float *Wd,
+                     const float *Wg_s, const float *Wu_s, const float *Wd_s,
+                     const int64_t *ids, const float *weights,
+                     const float *Gsel, const float *Usel, const float *Ysel,
+                     const float *Gs, const float *Us, const int64_t *perm,
+                     const int64_t *off, const unsigned char *drop, float *dX,
+                     float *dWgate, float *dWg, float *dWu, float *dWd,
+                     float *dWg_s, float *dWu_s, float *dWd_s, float *dLogits,
+                     int T, int n, int h, int E, int k, int S, int validate);
+
 /* ---------- prepared quantised layer (MI355X fast path) ---------- */
 typedef struct or_moe_q {
     int n, h, E, k, S, hs, group;

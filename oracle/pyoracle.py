@@ -50,6 +50,44 @@ class _OrMoeQ(C.Structure):
     ]
 
 
+def bwd_batch_call(fn, idx_dtype, dY, X, Wgate, Wg, Wu, Wd, Wg_s, Wu_s, Wd_s, ids, w,
+                   Gsel, Usel, Ysel, Gs, Us, perm, off, drop, k, extra=(), logits=True):
+    """Call a jt_moe_bwd_batch-shaped function (the reference's, the
+    oracle's or the device library's host-pointer entry). Shapes: dY, X
+    [T][n]; W* [E][h][n] / [S][h][n]; ids, w [T][k]; Gsel, Usel [T*k][h];
+    Ysel [T*k][n]; Gs, Us [T][S][h]; perm [kept]; off [E+1]; drop [T*k].
+    Returns a dict of rc and the outputs."""
+    f32 = lambda a: _c(a, np.float32)
+    dY, X, Wgate, Wg, Wu, Wd = map(f32, (dY, X, Wgate, Wg, Wu, Wd))
+    T, n = X.shape
+    E, h = Wg.shape[0], Wg.shape[1]
+    S = 0 if Wg_s is None else Wg_s.shape[0]
+    ins = [dY, X, Wgate, Wg, Wu, Wd]
+    ins += [None, None, None] if S == 0 else [f32(Wg_s), f32(Wu_s), f32(Wd_s)]
+    ins += [_c(ids, idx_dtype), f32(w), f32(Gsel), f32(Usel), f32(Ysel)]
+    ins += [None, None] if S == 0 else [f32(Gs), f32(Us)]
+    permc = _c(perm, idx_dtype)
+    if permc.size == 0:
+        permc = np.zeros(1, idx_dtype)
+    ins += [permc, _c(off, idx_dtype), _c(drop, np.uint8)]
+    out = dict(dX=np.full((T, n), np.nan, np.float32),
+               dWgate=np.full((E, n), np.nan, np.float32),
+               dWg=np.full((E, h, n), np.nan, np.float32),
+               dWu=np.full((E, h, n), np.nan, np.float32),
+               dWd=np.full((E, h, n), np.nan, np.float32))
+    if S:
+        for nm in ("dWg_s", "dWu_s", "dWd_s"):
+            out[nm] = np.full((S, h, n), np.nan, np.float32)
+    if logits:
+        out["dLogits"] = np.full((T, E), np.nan, np.float32)
+    outs = [out["dX"], out["dWgate"], out["dWg"], out["dWu"], out["dWd"],
+            out.get("dWg_s"), out.get("dWu_s"), out.get("dWd_s"), out.get("dLogits")]
+    ptr = lambda a: None if a is None else a.ctypes.data
+    rc = fn(*[ptr(a) for a in ins + outs], T, n, h, E, k, S, *extra)
+    out["rc"] = rc
+    return out
+
+
 class Oracle:
     """The C restatement. Every method returns numpy arrays (or raises)."""
 
@@ -100,6 +138,7 @@ class Oracle:
         L.or_ffn_fwd.argtypes = [_f32p, _f32p, _f32p, C.c_int, C.c_int, _f32p, C.c_int,
                                  _f32p]
         L.or_residual_add.argtypes = [_f32p, _f32p, _f32p, C.c_size_t]
+        L.or_moe_bwd_batch.argtypes = [C.c_void_p] * 28 + [C.c_int] * 7
 
     # ---- W8A8 ----
     def quant_rows(self, X):
@@ -291,6 +330,11 @@ class Oracle:
                                       X.size)
         return rc, Y
 
+    def moe_bwd_batch(self, *args, validate=1, **kw):
+        """or_moe_bwd_batch; arguments as bwd_batch_call."""
+        return bwd_batch_call(self.lib.or_moe_bwd_batch, np.int64, *args,
+                              extra=(validate,), **kw)
+
     def moe_q(self, n, h, E, k, S, hs, Wgate, Wg, Wu, Wd, Wg_s=None, Wu_s=None,
               Wd_s=None, group=64):
         return OracleMoeQ(self, n, h, E, k, S, hs, group, Wgate, Wg, Wu, Wd, Wg_s, Wu_s,
@@ -393,6 +437,8 @@ class RefLib:
                                                 C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
         L.jt_moe_fwd.argtypes = [_f32p] * 9 + [C.c_int] * 5 + [_u64p, _f32p, _f32p] + [
             C.c_void_p] * 5
+        for fn in (L.jt_moe_bwd_batch, L.jt_moe_bwd_batch_unchecked):
+            fn.argtypes = [C.c_void_p] * 28 + [C.c_int] * 6
 
     def quant_rows(self, X):
         X = _c(X, np.float32)
@@ -490,13 +536,20 @@ class RefLib:
         return rc, perm[: kept.value].astype(np.int64), off.astype(np.int64), drop
 
     def moe_fwd_batch(self, X, Wgate, Wg, Wu, Wd, Wg_s, Wu_s, Wd_s, k, cap_factor,
-                      w8a8_on=0, lowbit_mode=0):
+                      w8a8_on=0, lowbit_mode=0, caches=False):
         X = _c(X, np.float32)
         T, n = X.shape
         E, h = Wg.shape[0], Wg.shape[1]
         S = 0 if Wg_s is None else Wg_s.shape[0]
         z = np.zeros(1, np.float32)
         Y = np.zeros((T, n), np.float32)
+        cache = {}
+        if caches:
+            cache = dict(Gsel=np.zeros((T * k, h), np.float32),
+                         Usel=np.zeros((T * k, h), np.float32))
+            if S:
+                cache.update(Gs=np.zeros((T, S, h), np.float32), Us=np.zeros((T, S, h), np.float32))
+        cp = lambda nm: cache[nm].ctypes.data if nm in cache else None
         ids = np.zeros((T, k), np.uint64)
         w = np.zeros((T, k), np.float32)
         perm = np.zeros(T * k, np.uint64)
@@ -513,15 +566,20 @@ class RefLib:
                 _c(Wd, np.float32), z if S == 0 else _c(Wg_s, np.float32),
                 z if S == 0 else _c(Wu_s, np.float32),
                 z if S == 0 else _c(Wd_s, np.float32), Y, T, n, h, E, k, S, ids, w,
-                None, None, Ysel.ctypes.data, None, None, cap_factor, perm, off, drop,
-                C.byref(kept), C.byref(dropped))
+                cp("Gsel"), cp("Usel"), Ysel.ctypes.data, cp("Gs"), cp("Us"), cap_factor,
+                perm, off, drop, C.byref(kept), C.byref(dropped))
         finally:
             self.lib.jt_w8a8_set_enabled(0)
             self.lib.jt_lowbit_set_mode(0)
         return dict(rc=rc, Y=Y, ids=ids.astype(np.int64), w=w,
                     perm=perm[: kept.value].astype(np.int64), off=off.astype(np.int64),
-                    drop=drop, Ysel=Ysel)
+                    drop=drop, Ysel=Ysel, **cache)
 
+
+    def moe_bwd_batch(self, *args, validate=1, **kw):
+        """jt_moe_bwd_batch / _unchecked; arguments as bwd_batch_call."""
+        fn = self.lib.jt_moe_bwd_batch if validate else self.lib.jt_moe_bwd_batch_unchecked
+        return bwd_batch_call(fn, np.uint64, *args, **kw)
 
     def moe_fwd_single(self, x, Wgate, Wg, Wu, Wd, Wg_s, Wu_s, Wd_s, k):
         """jt_moe_fwd for one token; returns rc, Y, ids, weights, logits."""

@@ -85,3 +85,93 @@ def accuracy_case(salt, T=32, n=128, h=64, E=8, S=1):
     Wus = hpat((S, h, n), salt + 6, 1 / np.sqrt(n))
     Wds = hpat((S, h, n), salt + 7, 1 / np.sqrt(h))
     return X, Wgate, Wg, Wu, Wd, Wgs, Wus, Wds
+
+
+def capacity_sort(ids, E, cap_factor):
+    """The reference's capacity sort (src/moe_layer.c:895-978) of ids [T][k]:
+    stable by expert, the first cap = ceil(cap_factor*T*k/E) pairs of each
+    expert (in flattened index order) kept. cap_factor None: dropless.
+    Returns perm [kept], off [E+1], drop [T*k] (uint8)."""
+    flat = np.asarray(ids, np.int64).ravel()
+    Tk = flat.size
+    cap = Tk if cap_factor is None else int(np.ceil(np.float64(np.float32(cap_factor)) * Tk / E))
+    drop = np.ones(Tk, np.uint8)
+    perm, off = [], [0]
+    for e in range(E):
+        qs = np.nonzero(flat == e)[0][:cap]
+        drop[qs] = 0
+        perm.append(qs)
+        off.append(off[-1] + qs.size)
+    return (np.concatenate(perm).astype(np.int64), np.array(off, np.int64), drop)
+
+
+def bwd_case(T, n, h, E, k, S, salt, cap_factor=None):
+    """Inputs of a batched-backward case: distinct expert ids per token (a
+    hashed shuffle), weights in (0, 1], caches and weights ~ N(0, .), the
+    permutation of the capacity sort. The caches need not come from a
+    forward: the backward reads them as given."""
+    dY = hpat((T, n), salt)
+    X = hpat((T, n), salt + 1)
+    Wgate = hpat((E, n), salt + 2, 1 / np.sqrt(n))
+    Wg = hpat((E, h, n), salt + 3, 1 / np.sqrt(n))
+    Wu = hpat((E, h, n), salt + 4, 1 / np.sqrt(n))
+    Wd = hpat((E, h, n), salt + 5, 1 / np.sqrt(h))
+    keys = hpat((T, E), salt + 6)
+    ids = np.argsort(keys, axis=1, kind="stable")[:, :k].astype(np.int64)
+    w = (np.abs(hpat((T, k), salt + 7)) / 3.5 + 0.01).clip(0, 1).astype(np.float32)
+    Gsel = hpat((T * k, h), salt + 8, 2.0)
+    Usel = hpat((T * k, h), salt + 9)
+    Ysel = hpat((T * k, n), salt + 10)
+    perm, off, drop = capacity_sort(ids, E, cap_factor)
+    Ysel[drop.astype(bool)] = 0.0
+    if S:
+        Wgs = hpat((S, h, n), salt + 11, 1 / np.sqrt(n))
+        Wus = hpat((S, h, n), salt + 12, 1 / np.sqrt(n))
+        Wds = hpat((S, h, n), salt + 13, 1 / np.sqrt(h))
+        Gs = hpat((T, S, h), salt + 14, 2.0)
+        Us = hpat((T, S, h), salt + 15)
+    else:
+        Wgs = Wus = Wds = Gs = Us = None
+    return dict(dY=dY, X=X, Wgate=Wgate, Wg=Wg, Wu=Wu, Wd=Wd, Wg_s=Wgs, Wu_s=Wus,
+                Wd_s=Wds, ids=ids, w=w, Gsel=Gsel, Usel=Usel, Ysel=Ysel, Gs=Gs, Us=Us,
+                perm=perm, off=off, drop=drop, k=k)
+
+
+BWD_ARGS = ("dY", "X", "Wgate", "Wg", "Wu", "Wd", "Wg_s", "Wu_s", "Wd_s", "ids", "w",
+            "Gsel", "Usel", "Ysel", "Gs", "Us", "perm", "off", "drop", "k")
+
+
+def bwd_args(c):
+    """The case's arguments in jt_moe_bwd_batch order."""
+    return [c[a] for a in BWD_ARGS]
+
+
+def ref_bwd_inputs(case):
+    """The inputs of the reference's batched-backward tests
+    (bench/kernel/test_moe_layer.c:1166-1206 for case 0, the shape of
+    test_bwd_batch_gate_bitmatch / test_bwd_batch_equiv; :1440-1488 for
+    case 1, test_bwd_batch_drop), built with the tests' own float32
+    arithmetic. Returns (X, dY, Wgate, Wg, Wu, Wd, Wg_s, Wu_s, Wd_s, k,
+    cap_factor); the forward (jt_moe_fwd_batch) then gives the caches."""
+    f = np.float32
+    if case == 0:
+        T, n, h, E, k, S = 6, 4, 2, 4, 2, 1
+        X = np.array([f(0.4) * lpat(i, 0, 51) + f(0.2) for i in range(T * n)], f).reshape(T, n)
+        dY = np.array([f(0.5) * lpat(i, 1, 71) + f(0.15) for i in range(T * n)], f).reshape(T, n)
+        Wgate = np.array([f(0.3) * lpat(e, j, 52) for e in range(E) for j in range(n)],
+                         f).reshape(E, n)
+        W = [np.array([f(0.3) * lpat(i, r, salt) for i in range(E * h * n)], f).reshape(E, h, n)
+             for r, salt in ((0, 53), (1, 54), (2, 55))]
+        Ws = [np.array([f(0.3) * lpat(i, r, salt) for i in range(S * h * n)], f).reshape(S, h, n)
+              for r, salt in ((0, 56), (1, 57), (2, 58))]
+        return (X, dY, Wgate, *W, *Ws, k, 1.25)
+    T, n, h, E, k = 8, 2, 1, 4, 2
+    X = np.zeros((T, n), f)
+    dY = np.zeros((T, n), f)
+    for t in range(T):
+        X[t] = (1.0, f(0.125) * f(t))
+        dY[t] = (0.5, -0.25)
+    Wgate = np.array([2.0, 0.0, 1.2, -1.5, 0.0, 1.5, -5.0, 0.0], f).reshape(E, n)
+    W = [np.array([f(0.3) * lpat(i, r, salt) for i in range(E * h * n)], f).reshape(E, h, n)
+         for r, salt in ((0, 59), (1, 60), (2, 61))]
+    return (X, dY, Wgate, *W, None, None, None, k, 1.25)

@@ -32,6 +32,11 @@ Cases (key prefixes in the .npz):
                  gen.accuracy_case(acc_salt), a salt whose routing drops nothing
   lpat_lut{2,4}  jt_lowbit_gemm_lut on the reference test's own inputs
                  (bench/kernel/test_lowbit.c:112-157, gen.lpat_lut_inputs)
+  bwdref{0,1}_*  jt_moe_fwd_batch (with its caches) then jt_moe_bwd_batch on the
+                 reference backward tests' own inputs (gen.ref_bwd_inputs):
+                 inputs, forward outputs and every backward output
+  bwdrnd_*       jt_moe_bwd_batch outputs of gen.bwd_case(*BWD_RND) (drops, two
+                 shared experts, n not a multiple of 4)
 """
 import os
 import sys
@@ -44,9 +49,12 @@ sys.path.insert(0, ROOT)
 
 from oracle.pyoracle import RefLib  # noqa: E402
 sys.path.insert(0, HERE)
-from gen import accuracy_case, lpat_lut_inputs, shared_case  # noqa: E402
+from gen import (accuracy_case, bwd_args, bwd_case, lpat_lut_inputs, ref_bwd_inputs,  # noqa: E402
+                 shared_case)
 
 OUT = os.path.join(HERE, "ref_vectors.npz")
+# (T, n, h, E, k, S, salt, cap_factor) of the bwdrnd_* case
+BWD_RND = (24, 42, 24, 6, 3, 2, 300, 1.0)
 
 
 def main():
@@ -218,6 +226,35 @@ def main():
         rc, Y = R.lowbit_gemm_lut(Xp, Wp, bits)
         assert rc == 0
         g[f"lpat_lut{bits}"] = Y
+
+    # ---- batched backward ----
+    for c in (0, 1):
+        X, dY, Wgate, Wg, Wu, Wd, Wgs, Wus, Wds, k, cf = ref_bwd_inputs(c)
+        f = R.moe_fwd_batch(X, Wgate, Wg, Wu, Wd, Wgs, Wus, Wds, k, cf, caches=True)
+        assert f["rc"] == 0
+        if c == 1:  # the reference test's own expectation (test_moe_layer.c:1480-1486)
+            assert f["off"][-1] == 13 and int(f["drop"].sum()) == 3
+        b = R.moe_bwd_batch(dY, X, Wgate, Wg, Wu, Wd, Wgs, Wus, Wds, f["ids"], f["w"],
+                            f["Gsel"], f["Usel"], f["Ysel"], f.get("Gs"), f.get("Us"),
+                            f["perm"], f["off"], f["drop"], k)
+        assert b["rc"] == 0
+        pre = f"bwdref{c}_"
+        g.update({pre + "X": X, pre + "dY": dY, pre + "Wgate": Wgate, pre + "Wg": Wg,
+                  pre + "Wu": Wu, pre + "Wd": Wd, pre + "k": np.int64(k)})
+        if Wgs is not None:
+            g.update({pre + "Wg_s": Wgs, pre + "Wu_s": Wus, pre + "Wd_s": Wds})
+        for key in ("ids", "w", "Gsel", "Usel", "Ysel", "Gs", "Us", "perm", "off", "drop"):
+            if key in f:
+                g[pre + key] = f[key]
+        for key, v in b.items():
+            if key != "rc":
+                g[pre + "out_" + key] = v
+    c = bwd_case(*BWD_RND)
+    b = R.moe_bwd_batch(*bwd_args(c))
+    assert b["rc"] == 0
+    for key, v in b.items():
+        if key != "rc":
+            g["bwdrnd_" + key] = v
 
     np.savez_compressed(OUT, **g)
     print(f"wrote {OUT}: {len(g)} arrays, {os.path.getsize(OUT)} bytes")
