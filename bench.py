@@ -499,7 +499,80 @@ def sub_benchmarks(np, torch, api, stream):
                                   "grouped_gemm_tops": gops / (gemm_ms / 1e3) / 1e12,
                                   "mfma_frac": gops / (gemm_ms / 1e3) / INT8_PEAK,
                                   "stages_ms": {s: v / cnt for s, v in st.items()}}
+    del Ls
+    torch.cuda.empty_cache()
+    # --- batched backward (fp32, bit-exact to the reference's) ---
+    for name, shape in BWD_SHAPES.items():
+        res[name] = bwd_bench(np, torch, api, stream, *shape)
     return res
+
+
+# the training shape of the reference (bench/kernel/train_tinystories.c:78-81,
+# d=64, seq 128 x batch 4) and a layer-sized one
+BWD_SHAPES = {"moe_bwd_T512_train": (512, 64, 32, 8, 2, 1),
+              "moe_bwd_T4096_layer": (4096, 1024, 256, 64, 8, 1)}
+F32_PEAK = 157.3e12   # MI355X fp32 vector (packed FMA)
+F32_MULADD = F32_PEAK / 4  # separate, unpacked multiply and add: 1 flop/lane/instruction
+
+
+def bwd_inputs(np, T, n, h, E, k, S, seed):
+    """Synthetic backward inputs (numpy): distinct ids per token, weights in
+    (0, 1], caches ~ N(0, 1), the capacity sort at cap 1.25."""
+    rng = np.random.default_rng(seed)
+    f = lambda *s: rng.standard_normal(s, dtype=np.float32)  # noqa
+    ids = np.argsort(rng.random((T, E)), axis=1)[:, :k].astype(np.int64)
+    cap = int(np.ceil(1.25 * T * k / E))
+    flat = ids.ravel()
+    drop = np.ones(T * k, np.uint8)
+    perm, off = [], [0]
+    for e in range(E):
+        q = np.nonzero(flat == e)[0][:cap]
+        drop[q] = 0
+        perm.append(q)
+        off.append(off[-1] + q.size)
+    c = dict(dY=f(T, n), X=f(T, n), Wgate=f(E, n) / n ** 0.5, Wg=f(E, h, n) / n ** 0.5,
+             Wu=f(E, h, n) / n ** 0.5, Wd=f(E, h, n) / h ** 0.5,
+             Wg_s=f(S, h, n) / n ** 0.5, Wu_s=f(S, h, n) / n ** 0.5, Wd_s=f(S, h, n) / h ** 0.5,
+             ids=ids, w=rng.uniform(0.01, 1.0, (T, k)).astype(np.float32),
+             Gsel=f(T * k, h), Usel=f(T * k, h), Ysel=f(T * k, n), Gs=f(T, S, h), Us=f(T, S, h),
+             perm=np.concatenate(perm).astype(np.int64), off=np.array(off, np.int64), drop=drop)
+    c["Ysel"][drop.astype(bool)] = 0.0
+    return c
+
+
+BWD_ORDER = ("dY", "X", "Wgate", "Wg", "Wu", "Wd", "Wg_s", "Wu_s", "Wd_s", "ids", "w", "Gsel",
+             "Usel", "Ysel", "Gs", "Us", "perm", "off", "drop")
+
+
+def bwd_bench(np, torch, api, stream, T, n, h, E, k, S):
+    """jt_hip_moe_bwd_batch with every input resident in HBM (checked form):
+    time per call from HIP events on the stream; the fp32 GEMM work is
+    6 GEMMs of kept x h x n plus 6 of T x h x n for the shared experts."""
+    c = bwd_inputs(np, T, n, h, E, k, S, seed=T + n)
+    d = {}
+    for key in BWD_ORDER:
+        v = c[key]
+        dt = torch.int64 if v.dtype == np.int64 else (torch.uint8 if v.dtype == np.uint8
+                                                       else torch.float32)
+        d[key] = torch.from_numpy(np.ascontiguousarray(v)).to("cuda", dt)
+    args = [d[key] for key in BWD_ORDER] + [k]
+    rc, out, ws = api.moe_bwd_batch_device(*args, stream=stream)
+    assert rc == 0 and api.sync_errors(stream) == 0
+
+    def step():
+        r, _, _ = api.moe_bwd_batch_device(*args, out=out, ws=ws, stream=stream)
+        assert r == 0
+    _, ev = time_fn(torch, step, 10 if T > 1024 else 50, 3, stream)
+    assert api.sync_errors(stream) == 0
+    kept = int(c["off"][-1])
+    flops = 2.0 * 6 * (kept + S * T) * h * n
+    del out, ws, d
+    torch.cuda.empty_cache()
+    return {"ms_per_call": ev, "tokens_per_s": T / (ev / 1e3),
+            "shape": dict(T=T, n=n, h=h, E=E, k=k, S=S, cap_factor=1.25, kept=kept),
+            "gemm_flop": flops, "gemm_tflops": flops / (ev / 1e3) / 1e12,
+            "frac_f32_peak": flops / (ev / 1e3) / F32_PEAK,
+            "frac_mul_add_ceiling": flops / (ev / 1e3) / F32_MULADD}
 
 
 if __name__ == "__main__":

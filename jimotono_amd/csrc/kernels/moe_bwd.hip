@@ -28,30 +28,39 @@
 
 namespace {
 
-constexpr int BM = 64, BN = 64, BK = 16, TM = 4, TN = 4, PAD = 4;
 constexpr int EPI_STORE = 0, EPI_DUAL = 1, EPI_DSWIGLU = 2;
+constexpr int MODE_ROWS = 0, MODE_WGRAD = 1;
+constexpr int PAD = 4;
 
-// One GEMM family: C_g(r, c) = sum_k A_g(r, k) B_g(k, c) for groups g.
-//  A_g = A + g*sAg + kbase*sAk (kbase = koff[g] when koff, else 0);
-//  AT: A_g(r, k) = A_g[k*lda + r], else A_g[r*lda + k]; B alike with BT:
-//  B_g(k, c) = B_g[c*ldb + k], else B_g[k*ldb + c].
-//  Rows: a tile list {g, row0, rows} (ragged M, rows are global) or
-//  blockIdx.x*BM within M with g = blockIdx.z.
-struct GemmP {
-    const float *A, *B, *A2, *B2;
-    int lda, ldb;
-    int64_t sAg, sBg, sAk, sBk;
-    float *C, *C2, *C3;
-    int ldc;
-    int64_t sCg;
-    const float *G, *U;     // EPI_DSWIGLU inputs: row q of G_g = G + g*sGg + q*ldg
+// Operands of one side of a launch (side 0: shared experts, side 1: routed).
+// A GEMM computes C(r, c) = sum over k ascending of A(r, k) B(k, c) with
+//  A_g = A[m] + g*sAg + kb*sAk, B_g = B[m] + g*sBg + kb*sBk,
+//  AT: A_g(r, k) = A_g[k*lda + r], else A_g[r*lda + k];
+//  BT: B_g(k, c) = B_g[c*ldb + k], else B_g[k*ldb + c];
+// m selects one of three matrices (weight gradients), or A[1]/B[1] are the
+// second product of EPI_DUAL; g is the expert (group), kb the first row of
+// its K range (koff, ragged K) or 0.
+struct Side {
+    const float *A[3], *B[3];
+    float *C[3];  // EPI_DSWIGLU: Dg, Du, S
+    int lda, ldb, ldc;
+    int64_t sAg, sBg, sCg, sAk, sBk;
+    const float *G, *U;     // EPI_DSWIGLU: row q of G_g = G + g*sGg + q*ldg
     const int32_t *rowq;    // q of each output row (NULL: q = row)
     int ldg;
     int64_t sGg;
-    int M, N, K;
-    const int32_t *koff;    // per-group K ranges (ragged K)
-    const int4 *tiles;      // ragged M
+    int M, K;               // dense rows and fixed K
+    const int32_t *koff;    // ragged K: rows koff[g] .. koff[g+1]
+    const int4 *tiles;      // ragged M: {g, first row, rows}
     const int32_t *ntiles;
+};
+// MODE_ROWS: blockIdx.x < nsh are side 0's dense row tiles (mt_sh per
+// group), the rest side 1's tile list; blockIdx.y the column tile.
+// MODE_WGRAD: blockIdx.z < nsh is side 0, then side 1, z = 3*g + m;
+// blockIdx.x / blockIdx.y the row / column tiles.
+struct GemmP {
+    Side sd[2];
+    int nsh, mt_sh, N;
     uint32_t *err;
 };
 
@@ -71,106 +80,140 @@ __device__ __forceinline__ bool dswiglu(float g, float u, float dot, float *dg, 
     return isfinite(acc) && isfinite(gd) && isfinite(ud) && isfinite(s);
 }
 
-template <bool T_>
-__device__ __forceinline__ void load_a(float (*As)[BM + PAD], const float *Ag, int lda, int rb,
-                                       int rc, int k0, int K, int tid) {
+// A (R x BK) chunk of an operand: NL elements per thread, loaded into
+// registers (next chunk, while the current one is computed) and stored to
+// LDS as [k][r]. KMAJ: memory is contiguous along r (k-major), else along k.
+template <int R, int BK, bool KMAJ>
+struct Chunk {
+    static constexpr int NL = R * BK / 256;
+    float v[NL];
+    __device__ __forceinline__ void load(const float *P, int ld, int b, int cnt, int k0, int K,
+                                         int tid) {
 #pragma unroll
-    for (int it = 0; it < BM * BK / 256; it++) {
-        const int idx = tid + 256 * it;
-        int r, kk;
-        if (T_) {
-            kk = idx / BM, r = idx % BM;
-        } else {
-            r = idx / BK, kk = idx % BK;
+        for (int it = 0; it < NL; it++) {
+            const int idx = tid + 256 * it;
+            const int r = KMAJ ? idx % R : idx / BK, kk = KMAJ ? idx / R : idx % BK;
+            v[it] = (r < cnt && k0 + kk < K)
+                        ? (KMAJ ? P[(int64_t)(k0 + kk) * ld + b + r] : P[(int64_t)(b + r) * ld + k0 + kk])
+                        : 0.0f;
         }
-        float v = 0.0f;
-        if (r < rc && k0 + kk < K)
-            v = T_ ? Ag[(int64_t)(k0 + kk) * lda + rb + r] : Ag[(int64_t)(rb + r) * lda + k0 + kk];
-        As[kk][r] = v;
     }
-}
-
-template <bool T_>
-__device__ __forceinline__ void load_b(float (*Bs)[BN + PAD], const float *Bg, int ldb, int cb,
-                                       int cc, int k0, int K, int tid) {
+    __device__ __forceinline__ void store(float (*S)[R + PAD], int tid) const {
 #pragma unroll
-    for (int it = 0; it < BN * BK / 256; it++) {
-        const int idx = tid + 256 * it;
-        int c, kk;
-        if (T_) {
-            c = idx / BK, kk = idx % BK;
-        } else {
-            kk = idx / BN, c = idx % BN;
+        for (int it = 0; it < NL; it++) {
+            const int idx = tid + 256 * it;
+            const int r = KMAJ ? idx % R : idx / BK, kk = KMAJ ? idx / R : idx % BK;
+            S[kk][r] = v[it];
         }
-        float v = 0.0f;
-        if (c < cc && k0 + kk < K)
-            v = T_ ? Bg[(int64_t)(cb + c) * ldb + k0 + kk] : Bg[(int64_t)(k0 + kk) * ldb + cb + c];
-        Bs[kk][c] = v;
     }
-}
+};
 
-__device__ __forceinline__ void fma_step(float (&acc)[TM][TN], const float *as, const float *bs) {
-    const float4 a = *(const float4 *)as, b = *(const float4 *)bs;
-    const float av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+// acc[i][j] += a[i] * b[j]: one rounded multiply, one rounded add
+template <int TM, int TN>
+__device__ __forceinline__ void mul_add(float (&acc)[TM][TN], const float *as, const float *bs) {
+    float av[TM], bv[TN];
+#pragma unroll
+    for (int i = 0; i < TM; i += 4) *(float4 *)&av[i] = *(const float4 *)(as + i);
+#pragma unroll
+    for (int j = 0; j < TN; j += 4) *(float4 *)&bv[j] = *(const float4 *)(bs + j);
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < TN; j++) acc[i][j] = __fadd_rn(acc[i][j], __fmul_rn(av[i], bv[j]));
 }
 
-template <bool AT, bool BT, int EPI>
+template <bool AT, bool BT, int EPI, int MODE, int TM, int TN>
 __global__ __launch_bounds__(256) void k_bwd_gemm(GemmP p) {
+    constexpr int BM = 16 * TM, BN = 16 * TN, BK = 2048 / (BM > BN ? BM : BN);
     constexpr int NP = EPI == EPI_DUAL ? 2 : 1;
     __shared__ __attribute__((aligned(16))) float As[NP][BK][BM + PAD];
     __shared__ __attribute__((aligned(16))) float Bs[NP][BK][BN + PAD];
     const int tid = threadIdx.x;
-    int g, rb, rc;
-    if (p.tiles) {
-        if ((int)blockIdx.x >= *p.ntiles) return;
-        const int4 tl = p.tiles[blockIdx.x];
-        g = tl.x, rb = tl.y, rc = tl.z;
+    int side, g, m = 0, rb, rc;
+    if (MODE == MODE_ROWS) {
+        const int bx = blockIdx.x;
+        if (bx < p.nsh) {
+            side = 0, g = bx / p.mt_sh, rb = (bx % p.mt_sh) * BM;
+            rc = min(BM, p.sd[0].M - rb);
+        } else {
+            side = 1;
+            if (bx - p.nsh >= *p.sd[1].ntiles) return;
+            const int4 tl = p.sd[1].tiles[bx - p.nsh];
+            g = tl.x, rb = tl.y, rc = tl.z;
+        }
     } else {
-        g = blockIdx.z, rb = blockIdx.x * BM;
-        rc = min(BM, p.M - rb);
+        int z = blockIdx.z;
+        side = z < p.nsh ? 0 : 1;
+        z -= side ? p.nsh : 0;
+        g = z / 3, m = z % 3;
+        rb = blockIdx.x * BM;
+        rc = min(BM, p.sd[side].M - rb);
     }
+    const Side &S = p.sd[side];
     const int cb = blockIdx.y * BN, cc = min(BN, p.N - cb);
-    int K = p.K;
+    int K = S.K;
     int64_t kb = 0;
-    if (p.koff) {
-        kb = p.koff[g];
-        K = p.koff[g + 1] - p.koff[g];
+    if (MODE == MODE_WGRAD && S.koff) {
+        kb = S.koff[g];
+        K = S.koff[g + 1] - S.koff[g];
     }
-    const float *Ag = p.A + g * p.sAg + kb * p.sAk, *Bg = p.B + g * p.sBg + kb * p.sBk;
-    const float *Ag2 = nullptr, *Bg2 = nullptr;
+    const float *Ag = S.A[m] + g * S.sAg + kb * S.sAk, *Bg = S.B[m] + g * S.sBg + kb * S.sBk;
+    const float *Ag2 = Ag, *Bg2 = Bg;
     if (EPI == EPI_DUAL) {
-        Ag2 = p.A2 + g * p.sAg + kb * p.sAk;
-        Bg2 = p.B2 + g * p.sBg + kb * p.sBk;
+        Ag2 = S.A[1] + g * S.sAg + kb * S.sAk;
+        Bg2 = S.B[1] + g * S.sBg + kb * S.sBk;
     }
-    const int ty = tid / (BN / TN), tx = tid % (BN / TN);
-    float acc[TM][TN], acc2[TM][TN];
+    const int ty = tid / 16, tx = tid % 16;
+    float acc[TM][TN], acc2[EPI == EPI_DUAL ? TM : 1][EPI == EPI_DUAL ? TN : 1];
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int j = 0; j < TN; j++) acc[i][j] = acc2[i][j] = 0.0f;
-    for (int k0 = 0; k0 < K; k0 += BK) {
-        load_a<AT>(As[0], Ag, p.lda, rb, rc, k0, K, tid);
-        load_b<BT>(Bs[0], Bg, p.ldb, cb, cc, k0, K, tid);
+        for (int j = 0; j < TN; j++) acc[i][j] = 0.0f;
+    if constexpr (EPI == EPI_DUAL) {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) acc2[i][j] = 0.0f;
+    }
+    Chunk<BM, BK, AT> ca, ca2;
+    Chunk<BN, BK, !BT> cbk, cb2;
+    if (K > 0) {
+        ca.load(Ag, S.lda, rb, rc, 0, K, tid);
+        cbk.load(Bg, S.ldb, cb, cc, 0, K, tid);
         if (EPI == EPI_DUAL) {
-            load_a<AT>(As[NP - 1], Ag2, p.lda, rb, rc, k0, K, tid);
-            load_b<BT>(Bs[NP - 1], Bg2, p.ldb, cb, cc, k0, K, tid);
+            ca2.load(Ag2, S.lda, rb, rc, 0, K, tid);
+            cb2.load(Bg2, S.ldb, cb, cc, 0, K, tid);
+        }
+    }
+    for (int k0 = 0; k0 < K; k0 += BK) {
+        ca.store(As[0], tid);
+        cbk.store(Bs[0], tid);
+        if (EPI == EPI_DUAL) {
+            ca2.store(As[NP - 1], tid);
+            cb2.store(Bs[NP - 1], tid);
         }
         __syncthreads();
+        if (k0 + BK < K) {  // the next chunk's loads overlap this chunk's products
+            ca.load(Ag, S.lda, rb, rc, k0 + BK, K, tid);
+            cbk.load(Bg, S.ldb, cb, cc, k0 + BK, K, tid);
+            if (EPI == EPI_DUAL) {
+                ca2.load(Ag2, S.lda, rb, rc, k0 + BK, K, tid);
+                cb2.load(Bg2, S.ldb, cb, cc, k0 + BK, K, tid);
+            }
+        }
         const int kend = min(BK, K - k0);
         if (kend == BK) {
-#pragma unroll
+#pragma unroll 8
             for (int kk = 0; kk < BK; kk++) {
-                fma_step(acc, &As[0][kk][ty * TM], &Bs[0][kk][tx * TN]);
-                if (EPI == EPI_DUAL) fma_step(acc2, &As[NP - 1][kk][ty * TM], &Bs[NP - 1][kk][tx * TN]);
+                mul_add<TM, TN>(acc, &As[0][kk][ty * TM], &Bs[0][kk][tx * TN]);
+                if constexpr (EPI == EPI_DUAL)
+                    mul_add<TM, TN>(acc2, &As[NP - 1][kk][ty * TM], &Bs[NP - 1][kk][tx * TN]);
             }
         } else {
             for (int kk = 0; kk < kend; kk++) {
-                fma_step(acc, &As[0][kk][ty * TM], &Bs[0][kk][tx * TN]);
-                if (EPI == EPI_DUAL) fma_step(acc2, &As[NP - 1][kk][ty * TM], &Bs[NP - 1][kk][tx * TN]);
+                mul_add<TM, TN>(acc, &As[0][kk][ty * TM], &Bs[0][kk][tx * TN]);
+                if constexpr (EPI == EPI_DUAL)
+                    mul_add<TM, TN>(acc2, &As[NP - 1][kk][ty * TM], &Bs[NP - 1][kk][tx * TN]);
             }
         }
         __syncthreads();
@@ -181,35 +224,61 @@ __global__ __launch_bounds__(256) void k_bwd_gemm(GemmP p) {
         const int r = ty * TM + i;
         if (r >= rc) continue;
         const int64_t row = rb + r;
-        float *crow = p.C + g * p.sCg + row * p.ldc;
+        const int64_t o = g * S.sCg + row * S.ldc;
+        const int64_t q = (EPI == EPI_DSWIGLU && S.rowq) ? S.rowq[row] : row;
 #pragma unroll
         for (int j = 0; j < TN; j++) {
             const int c = tx * TN + j;
             if (c >= cc) continue;
             const int col = cb + c;
-            if (EPI == EPI_STORE) {
-                crow[col] = acc[i][j];
-            } else if (EPI == EPI_DUAL) {
-                crow[col] = (float)((double)acc[i][j] + (double)acc2[i][j]);
+            if constexpr (EPI == EPI_STORE) {
+                S.C[m][o + col] = acc[i][j];
+            } else if constexpr (EPI == EPI_DUAL) {
+                S.C[0][o + col] = (float)((double)acc[i][j] + (double)acc2[i][j]);
             } else {
-                const int64_t q = p.rowq ? p.rowq[row] : row;
-                const int64_t at = g * p.sGg + q * p.ldg + col;
+                const int64_t at = g * S.sGg + q * S.ldg + col;
                 float dg, du, sv;
-                bad |= !dswiglu(p.G[at], p.U[at], acc[i][j], &dg, &du, &sv);
-                const int64_t o = g * p.sCg + row * p.ldc + col;
-                p.C[o] = dg;
-                p.C2[o] = du;
-                p.C3[o] = sv;
+                bad |= !dswiglu(S.G[at], S.U[at], acc[i][j], &dg, &du, &sv);
+                S.C[0][o + col] = dg;
+                S.C[1][o + col] = du;
+                S.C[2][o + col] = sv;
             }
         }
     }
     if (bad) raise_err(p.err, EF_NONFINITE_MID);
 }
 
-template <bool AT, bool BT, int EPI>
+template <bool AT, bool BT, int EPI, int MODE, int TM, int TN>
 int launch_gemm(const GemmP &p, dim3 grid, hipStream_t s) {
-    hipLaunchKernelGGL((k_bwd_gemm<AT, BT, EPI>), grid, dim3(256), 0, s, p);
+    if (grid.x == 0 || grid.y == 0 || grid.z == 0) return 0;
+    hipLaunchKernelGGL((k_bwd_gemm<AT, BT, EPI, MODE, TM, TN>), grid, dim3(256), 0, s, p);
     return (int)hipGetLastError();
+}
+
+// Finiteness of up to 16 arrays in one launch (blockIdx.y = array).
+struct FinList {
+    const float *p[16];
+    int64_t n[16];
+};
+__global__ __launch_bounds__(256) void k_bwd_finite(FinList L, uint32_t *err) {
+    const float *x = L.p[blockIdx.y];
+    const int64_t n = L.n[blockIdx.y];
+    int bad = 0;
+    int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t step = (int64_t)gridDim.x * 256;
+    if (((uintptr_t)x & 15) == 0) {  // float4 body
+        const float4 *x4 = (const float4 *)x;
+        for (; i < n / 4; i += step) {
+            const float4 v = x4[i];
+            bad |= !isfinite(v.x) || !isfinite(v.y) || !isfinite(v.z) || !isfinite(v.w);
+        }
+        for (i = n / 4 * 4 + blockIdx.x * 256 + threadIdx.x; i < n; i += step)
+            bad |= !isfinite(x[i]);
+    } else {
+        for (; i < n; i += step) bad |= !isfinite(x[i]);
+    }
+    bad = wave_or_i(bad);
+    if (bad && (threadIdx.x & 63) == 0) raise_err(err, EF_NONFINITE_INPUT);
 }
 
 __device__ __forceinline__ int block_sum_256(int v, int *red) {
@@ -413,6 +482,7 @@ __global__ __launch_bounds__(256) void k_bwd_token(
 
 // dWgate[e][j] = float sum over the kept pairs of expert e in flattened
 // index order of (float)(dlog*(double)X[t][j]); 0 for experts without one.
+// The pairs are read 16 at a time ahead of the (ordered) sums.
 __global__ __launch_bounds__(256) void k_bwd_dwgate(const int32_t *__restrict__ off2,
                                                     const int32_t *__restrict__ perm2,
                                                     const double *__restrict__ dlog,
@@ -421,8 +491,21 @@ __global__ __launch_bounds__(256) void k_bwd_dwgate(const int32_t *__restrict__ 
     const int e = blockIdx.x, j = blockIdx.y * 256 + threadIdx.x;
     if (j >= n) return;
     float rg = 0.0f;
-    const int i1 = off2[e + 1];
-    for (int i = off2[e]; i < i1; i++) {
+    const int i0 = off2[e], i1 = off2[e + 1];
+    int i = i0;
+    for (; i + 16 <= i1; i += 16) {
+        float x[16];
+        double dl[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            const int q = perm2[i + u];
+            dl[u] = dlog[q];
+            x[u] = X[(int64_t)(q / k) * n + j];
+        }
+#pragma unroll
+        for (int u = 0; u < 16; u++) rg = rg + (float)(dl[u] * (double)x[u]);
+    }
+    for (; i < i1; i++) {
         const int q = perm2[i];
         rg = rg + (float)(dlog[q] * (double)X[(int64_t)(q / k) * n + j]);
     }
@@ -454,6 +537,11 @@ __global__ __launch_bounds__(256) void k_bwd_dx(
 
 inline unsigned cdiv(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }
 
+// Tile shapes (threads hold TM x TN outputs; blocks 16 TM x 16 TN). The row
+// GEMMs share one routed tile list, so they share TM.
+constexpr int TM_ROWS = 4, TN_DOT = 4, TN_DX = 4, TM_WG = 4, TN_WG = 4;
+constexpr int BM_ROWS = 16 * TM_ROWS;
+
 }  // namespace
 
 // Workspace carve-up (256-byte aligned pieces); returns the total bytes.
@@ -479,7 +567,7 @@ extern "C" size_t jtk_bwd_ws_layout(int T, int n, int h, int E, int k, int S, jt
     v.off2 = (int32_t *)take(((size_t)E + 2) * 4);
     v.perm2 = (int32_t *)take(Tk * 4);
     v.off32 = (int32_t *)take(((size_t)E + 1) * 4);
-    v.tiles = (int32_t *)take((Tk / BM + E + 1) * 16);
+    v.tiles = (int32_t *)take((Tk / BM_ROWS + E + 1) * 16);
     v.ntiles = (int32_t *)take(4);
     v.dw = (double *)take(Tk * 8);
     v.dlog = (double *)take(Tk * 8);
@@ -518,24 +606,31 @@ extern "C" int jtk_bwd_batch(const jtk_bwd_io *io, int T, int n, int h, int E, i
                        io->drop, Tk, w->ctrl, w->seen, w->inv, err);
     le |= (int)hipGetLastError();
     if (validate) {  // src/moe_layer.c:1766-1800
-        const int64_t Tn = (int64_t)T * n;
-        le |= jtk_check_finite(io->dY, Tn, err, s);
-        le |= jtk_check_finite(io->X, Tn, err, s);
-        le |= jtk_check_finite(io->Wgate, (int64_t)E * n, err, s);
-        le |= jtk_check_finite(io->Wg, E * nh, err, s);
-        le |= jtk_check_finite(io->Wu, E * nh, err, s);
-        le |= jtk_check_finite(io->Wd, E * nh, err, s);
-        le |= jtk_check_finite(io->weights, Tk, err, s);
-        le |= jtk_check_finite(io->Gsel, (int64_t)Tk * h, err, s);
-        le |= jtk_check_finite(io->Usel, (int64_t)Tk * h, err, s);
-        le |= jtk_check_finite(io->Ysel, (int64_t)Tk * n, err, s);
+        FinList L{};
+        int c = 0;
+        auto add = [&](const float *x, int64_t cnt) {
+            L.p[c] = x;
+            L.n[c++] = cnt;
+        };
+        add(io->dY, (int64_t)T * n);
+        add(io->X, (int64_t)T * n);
+        add(io->Wgate, (int64_t)E * n);
+        add(io->Wg, E * nh);
+        add(io->Wu, E * nh);
+        add(io->Wd, E * nh);
+        add(io->weights, Tk);
+        add(io->Gsel, (int64_t)Tk * h);
+        add(io->Usel, (int64_t)Tk * h);
+        add(io->Ysel, (int64_t)Tk * n);
         if (S) {
-            le |= jtk_check_finite(io->Wg_s, S * nh, err, s);
-            le |= jtk_check_finite(io->Wu_s, S * nh, err, s);
-            le |= jtk_check_finite(io->Wd_s, S * nh, err, s);
-            le |= jtk_check_finite(io->Gs, (int64_t)T * S * h, err, s);
-            le |= jtk_check_finite(io->Us, (int64_t)T * S * h, err, s);
+            add(io->Wg_s, S * nh);
+            add(io->Wu_s, S * nh);
+            add(io->Wd_s, S * nh);
+            add(io->Gs, (int64_t)T * S * h);
+            add(io->Us, (int64_t)T * S * h);
         }
+        hipLaunchKernelGGL(k_bwd_finite, dim3(1024, (unsigned)c), dim3(256), 0, s, L, err);
+        le |= (int)hipGetLastError();
     }
     // gate path
     if (io->dLogits) le |= jtk_zero_u32((uint32_t *)io->dLogits, (int64_t)T * E, s);
@@ -549,75 +644,68 @@ extern "C" int jtk_bwd_batch(const jtk_bwd_io *io, int T, int n, int h, int E, i
                    w->perm2, nullptr, nullptr, err, s);
     hipLaunchKernelGGL(k_bwd_dwgate, dim3((unsigned)E, cdiv(n, 256)), dim3(256), 0, s, w->off2,
                        w->perm2, w->dlog, io->X, k, n, io->dWgate);
-    // routed experts on the perm rows
+    // expert rows in perm order
     hipLaunchKernelGGL(k_bwd_gather, dim3((unsigned)Tk), dim3(256), 0, s, io->perm, io->X,
                        io->dY, io->weights, Tk, k, n, w->ctrl, w->Xp, w->dYp, w->rowq);
     le |= (int)hipGetLastError();
-    le |= jtk_make_tiles(w->off32, E, BM, w->tiles, w->ntiles, s);
-    const unsigned mt = (unsigned)(Tk / BM + E);
+    le |= jtk_make_tiles(w->off32, E, BM_ROWS, w->tiles, w->ntiles, s);
+    const unsigned mt = (unsigned)(Tk / BM_ROWS + E);  // bound on the routed tile count
+    const int mt_sh = (int)cdiv(T, BM_ROWS);
+    // Dg, Du, S = SwiGLU backward of (rows Wd^T): shared experts on all
+    // tokens with dY unweighted, routed experts on their perm rows
     GemmP p{};
-    p.err = err;
-    p.tiles = (const int4 *)w->tiles;
-    p.ntiles = w->ntiles;
-    // Dg, Du, S = SwiGLU backward of (dYp Wd_e^T)
-    p.A = w->dYp, p.lda = n;
-    p.B = io->Wd, p.ldb = n, p.sBg = nh;
-    p.C = w->Dg, p.C2 = w->Du, p.C3 = w->Ss, p.ldc = h;
-    p.G = io->Gsel, p.U = io->Usel, p.rowq = w->rowq, p.ldg = h;
-    p.N = h, p.K = n;
-    le |= launch_gemm<false, true, EPI_DSWIGLU>(p, dim3(mt, cdiv(h, BN)), s);
-    // Dxe = (float)((double)(Dg Wg_e) + (double)(Du Wu_e))
+    p.err = err, p.N = h, p.nsh = S * mt_sh, p.mt_sh = mt_sh;
+    {
+        Side &a = p.sd[0];
+        a.A[0] = io->dY, a.lda = n;
+        a.B[0] = io->Wd_s, a.ldb = n, a.sBg = nh;
+        a.C[0] = w->SDg, a.C[1] = w->SDu, a.C[2] = w->SSs, a.ldc = h, a.sCg = (int64_t)T * h;
+        a.G = io->Gs, a.U = io->Us, a.ldg = S * h, a.sGg = h;
+        a.M = T, a.K = n;
+        Side &b = p.sd[1];
+        b.A[0] = w->dYp, b.lda = n;
+        b.B[0] = io->Wd, b.ldb = n, b.sBg = nh;
+        b.C[0] = w->Dg, b.C[1] = w->Du, b.C[2] = w->Ss, b.ldc = h;
+        b.G = io->Gsel, b.U = io->Usel, b.rowq = w->rowq, b.ldg = h;
+        b.K = n, b.tiles = (const int4 *)w->tiles, b.ntiles = w->ntiles;
+    }
+    le |= launch_gemm<false, true, EPI_DSWIGLU, MODE_ROWS, TM_ROWS, TN_DOT>(
+        p, dim3(p.nsh + mt, cdiv(h, 16 * TN_DOT)), s);
+    // dx rows = (float)((double)(Dg Wg) + (double)(Du Wu))
     p = GemmP{};
-    p.err = err;
-    p.tiles = (const int4 *)w->tiles;
-    p.ntiles = w->ntiles;
-    p.A = w->Dg, p.A2 = w->Du, p.lda = h;
-    p.B = io->Wg, p.B2 = io->Wu, p.ldb = n, p.sBg = nh;
-    p.C = w->Dxe, p.ldc = n;
-    p.N = n, p.K = h;
-    le |= launch_gemm<false, false, EPI_DUAL>(p, dim3(mt, cdiv(n, BN)), s);
-    // dWg_e = Dg^T Xp, dWu_e = Du^T Xp, dWd_e = S^T dYp over the expert's rows
-    const float *dA[3] = {w->Dg, w->Du, w->Ss}, *dB[3] = {w->Xp, w->Xp, w->dYp};
-    float *dC[3] = {io->dWg, io->dWu, io->dWd};
-    for (int m = 0; m < 3; m++) {
-        p = GemmP{};
-        p.err = err;
-        p.koff = w->off32;
-        p.A = dA[m], p.lda = h, p.sAk = h;
-        p.B = dB[m], p.ldb = n, p.sBk = n;
-        p.C = dC[m], p.ldc = n, p.sCg = nh;
-        p.M = h, p.N = n;
-        le |= launch_gemm<true, false, EPI_STORE>(p, dim3(cdiv(h, BM), cdiv(n, BN), E), s);
+    p.err = err, p.N = n, p.nsh = S * mt_sh, p.mt_sh = mt_sh;
+    {
+        Side &a = p.sd[0];
+        a.A[0] = w->SDg, a.A[1] = w->SDu, a.lda = h, a.sAg = (int64_t)T * h;
+        a.B[0] = io->Wg_s, a.B[1] = io->Wu_s, a.ldb = n, a.sBg = nh;
+        a.C[0] = w->SDxe, a.ldc = n, a.sCg = (int64_t)T * n;
+        a.M = T, a.K = h;
+        Side &b = p.sd[1];
+        b.A[0] = w->Dg, b.A[1] = w->Du, b.lda = h;
+        b.B[0] = io->Wg, b.B[1] = io->Wu, b.ldb = n, b.sBg = nh;
+        b.C[0] = w->Dxe, b.ldc = n;
+        b.K = h, b.tiles = (const int4 *)w->tiles, b.ntiles = w->ntiles;
     }
-    // shared experts on all tokens, dY unweighted
-    if (S) {
-        p = GemmP{};
-        p.err = err;
-        p.A = io->dY, p.lda = n;
-        p.B = io->Wd_s, p.ldb = n, p.sBg = nh;
-        p.C = w->SDg, p.C2 = w->SDu, p.C3 = w->SSs, p.ldc = h, p.sCg = (int64_t)T * h;
-        p.G = io->Gs, p.U = io->Us, p.ldg = S * h, p.sGg = h;
-        p.M = T, p.N = h, p.K = n;
-        le |= launch_gemm<false, true, EPI_DSWIGLU>(p, dim3(cdiv(T, BM), cdiv(h, BN), S), s);
-        p = GemmP{};
-        p.err = err;
-        p.A = w->SDg, p.A2 = w->SDu, p.lda = h, p.sAg = (int64_t)T * h;
-        p.B = io->Wg_s, p.B2 = io->Wu_s, p.ldb = n, p.sBg = nh;
-        p.C = w->SDxe, p.ldc = n, p.sCg = (int64_t)T * n;
-        p.M = T, p.N = n, p.K = h;
-        le |= launch_gemm<false, false, EPI_DUAL>(p, dim3(cdiv(T, BM), cdiv(n, BN), S), s);
-        const float *sA[3] = {w->SDg, w->SDu, w->SSs}, *sB[3] = {io->X, io->X, io->dY};
-        float *sC[3] = {io->dWg_s, io->dWu_s, io->dWd_s};
-        for (int m = 0; m < 3; m++) {
-            p = GemmP{};
-            p.err = err;
-            p.A = sA[m], p.lda = h, p.sAg = (int64_t)T * h;
-            p.B = sB[m], p.ldb = n;
-            p.C = sC[m], p.ldc = n, p.sCg = nh;
-            p.M = h, p.N = n, p.K = T;
-            le |= launch_gemm<true, false, EPI_STORE>(p, dim3(cdiv(h, BM), cdiv(n, BN), S), s);
-        }
+    le |= launch_gemm<false, false, EPI_DUAL, MODE_ROWS, TM_ROWS, TN_DX>(
+        p, dim3(p.nsh + mt, cdiv(n, 16 * TN_DX)), s);
+    // weight gradients D^T rows: dWg = Dg^T X, dWu = Du^T X, dWd = S^T dY
+    // (routed: weighted dY rows, over the expert's rows in perm order)
+    p = GemmP{};
+    p.err = err, p.N = n, p.nsh = 3 * S;
+    {
+        Side &a = p.sd[0];
+        a.A[0] = w->SDg, a.A[1] = w->SDu, a.A[2] = w->SSs, a.lda = h, a.sAg = (int64_t)T * h;
+        a.B[0] = io->X, a.B[1] = io->X, a.B[2] = io->dY, a.ldb = n;
+        a.C[0] = io->dWg_s, a.C[1] = io->dWu_s, a.C[2] = io->dWd_s, a.ldc = n, a.sCg = nh;
+        a.M = h, a.K = T;
+        Side &b = p.sd[1];
+        b.A[0] = w->Dg, b.A[1] = w->Du, b.A[2] = w->Ss, b.lda = h, b.sAk = h;
+        b.B[0] = w->Xp, b.B[1] = w->Xp, b.B[2] = w->dYp, b.ldb = n, b.sBk = n;
+        b.C[0] = io->dWg, b.C[1] = io->dWu, b.C[2] = io->dWd, b.ldc = n, b.sCg = nh;
+        b.M = h, b.koff = w->off32;
     }
+    le |= launch_gemm<true, false, EPI_STORE, MODE_WGRAD, TM_WG, TN_WG>(
+        p, dim3(cdiv(h, 16 * TM_WG), cdiv(n, 16 * TN_WG), (unsigned)(3 * (S + E))), s);
     hipLaunchKernelGGL(k_bwd_dx, dim3((unsigned)T, cdiv(n, 256)), dim3(256), 0, s, io->Wgate,
                        w->gate_e, w->gate_dl, w->gate_n, w->tokpos, w->tokcnt, w->Dxe, w->SDxe,
                        S, T, k, n, io->dX, err);

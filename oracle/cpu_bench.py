@@ -173,11 +173,40 @@ def routed_layer(R, seconds, T, n, h, E, k, seed, max_tokens=None):
             "mad_ms": mad * 1e3, "trials": nt, "tokens_per_s": tok / med}
 
 
+def bwd_inputs(R, T, n, h, E, k, S, seed):
+    """Synthetic inputs of the batched backward: distinct ids per token,
+    weights in (0, 1], caches ~ N(0, 1) and the reference's capacity sort at
+    cap 1.25 (jt_moe_batch_sort)."""
+    rng = np.random.default_rng(seed)
+    f = lambda *s: rng.standard_normal(s, dtype=np.float32)  # noqa: E731
+    ids = np.argsort(rng.random((T, E)), axis=1)[:, :k].astype(np.int64)
+    rc, perm, off, drop = R.batch_sort(ids, T, k, E, 1.25)
+    assert rc == 0
+    Ysel = f(T * k, n)
+    Ysel[drop.astype(bool)] = 0.0
+    return [f(T, n), f(T, n), f(E, n) / n ** 0.5, f(E, h, n) / n ** 0.5, f(E, h, n) / n ** 0.5,
+            f(E, h, n) / h ** 0.5, f(S, h, n) / n ** 0.5, f(S, h, n) / n ** 0.5,
+            f(S, h, n) / h ** 0.5, ids, rng.uniform(0.01, 1.0, (T, k)).astype(np.float32),
+            f(T * k, h), f(T * k, h), Ysel, f(T, S, h), f(T, S, h), perm, off, drop, k]
+
+
+def bwd_batch(R, seconds, T, n, h, E, k, S, max_tokens=None, seed=3):
+    """jt_moe_bwd_batch of the reference on T tokens (a sample of max_tokens
+    when smaller); its work is linear in the tokens (every GEMM has the
+    kept rows or T as one dimension), so tokens/s carries over."""
+    tok = T if max_tokens is None else min(T, max_tokens)
+    args = bwd_inputs(R, tok, n, h, E, k, S, seed)
+    med, mad, nt = trials(lambda: R.moe_bwd_batch(*args), seconds, min_trials=1)
+    return {"tokens": tok, "ms_per_sample": med * 1e3, "mad_ms": mad * 1e3, "trials": nt,
+            "tokens_per_s": tok / med}
+
+
 def decode_and_stress(seconds):
     """The W8A8 GEMM 64x1024x1024, the shared-expert decode at 1, 4 and 16
-    rows, the routed decode at 16 tokens and a token sample of the E=512
-    stress shape, on one pinned core, for the default reference build and
-    (for the W8A8 shapes) its VNNI form when the host can run one."""
+    rows, the routed decode at 16 tokens, a token sample of the E=512
+    stress shape and the batched backward (training shape; a token sample of
+    the layer shape), on one pinned core, for the default reference build
+    and (for the W8A8 shapes) its VNNI form when the host can run one."""
     if not ref_available():
         return {"error": "oracle/_ref not built"}
     model, _ = host_info()
@@ -199,5 +228,8 @@ def decode_and_stress(seconds):
                 res["routed_decode_T16"] = routed_layer(R, seconds, 16, 1024, 256, 256, 8, 16)
                 res["stress_prefill_E512_sample"] = routed_layer(R, 2 * seconds, 16384, 2048,
                                                                  512, 512, 8, 17, max_tokens=4)
+                res["moe_bwd_T512_train"] = bwd_batch(R, seconds, 512, 64, 32, 8, 2, 1)
+                res["moe_bwd_T4096_layer"] = bwd_batch(R, seconds, 4096, 1024, 256, 64, 8, 1,
+                                                       max_tokens=512)
             out[name] = res
     return out
