@@ -1,0 +1,48 @@
+#pragma once
+#ifndef JIMOTONO_HIP_GDN2_H
+#define JIMOTONO_HIP_GDN2_H
+/*
+ * Device-resident, batched Gated DeltaNet-2 for the MI355X. No single
+ * counterpart in the reference: it is jt_gdn2_decode_step and
+ * jt_gdn2_prefill_chunk16/32 (reference include/jimotono/gdn2.h:71-113,
+ * src/gdn2.c:252-862) for H independent heads (or sequences) whose states
+ * stay in HBM, each head's result bit-identical to the reference call on
+ * that head. Pointers are device pointers; calls are asynchronous on
+ * `stream` (a hipStream_t as void*, NULL = the null stream). A head whose
+ * inputs hold a non-finite value or an alpha outside [0,1] keeps its state
+ * and outputs and raises JT_HIP_EF_NONFINITE_INPUT (jimotono/hip_moe.h;
+ * read with jt_hip_sync_errors).
+ */
+#include <stddef.h>
+
+#include "jimotono/common.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* One decode step per head: S [H][dk][dv] updated in place, o [H][dv];
+ * q, k, b, alpha [H][dk]; v, w [H][dv]; dk, dv in 1..1024. */
+int jt_hip_gdn2_decode(float *dS, float *dO, const float *dq, const float *dk_,
+                       const float *dv_, const float *db, const float *dw,
+                       const float *dalpha, int H, int dk, int dv, void *stream);
+
+/* Workspace bytes of jt_hip_gdn2_prefill (0 for invalid arguments). */
+size_t jt_hip_gdn2_prefill_ws_bytes(int H, int C, int dk);
+/* Prefill of T tokens per head in T/C chunks of C = 16 or 32 (T % C == 0),
+ * each chunk equal to the reference's jt_gdn2_prefill_chunk{C} on the state
+ * the previous chunk left: Q, K, B, Alpha [H][T][dk]; V, W, Out [H][T][dv];
+ * S [H][dk][dv] in place. A head with a bad value among its T tokens keeps
+ * its S and Out. d_ws: jt_hip_gdn2_prefill_ws_bytes(H, C, dk) bytes,
+ * 16-byte aligned, not kept between calls. */
+int jt_hip_gdn2_prefill(float *dS, float *dOut, const float *dQ,
+                        const float *dK, const float *dV, const float *dB,
+                        const float *dW, const float *dA, int H, int T, int C,
+                        int dk, int dv, void *d_ws, size_t ws_bytes,
+                        void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* JIMOTONO_HIP_GDN2_H */

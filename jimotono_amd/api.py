@@ -95,6 +95,18 @@ _PROTOS = {
     "jt_moe_bwd_batch_unchecked": [_vp] * 28 + [_i] * 6,
     "jt_hip_moe_bwd_batch_ws_bytes": ([_i] * 6, _sz),
     "jt_hip_moe_bwd_batch": [_vp] * 28 + [_i] * 7 + [_vp, _sz, _vp],
+    "jt_gdn2_state_bytes": [_i, _i, C.POINTER(_sz)],
+    "jt_gdn2_state_alloc": [C.POINTER(_vp), _i, _i],
+    "jt_gdn2_state_free": ([_vp], None),
+    "jt_gdn2_state_reset": [_vp, _i, _i],
+    "jt_gdn2_scratch_floats": [_i, _i, C.POINTER(_sz)],
+    "jt_gdn2_l2norm": [_vp, _vp, _i, _fl],
+    "jt_gdn2_decode_step": [_vp] * 8 + [_i, _i, _vp, _sz],
+    "jt_gdn2_prefill_chunk16": [_vp] * 8 + [_i, _i, _vp, _sz],
+    "jt_gdn2_prefill_chunk32": [_vp] * 8 + [_i, _i, _vp, _sz],
+    "jt_hip_gdn2_decode": [_vp] * 8 + [_i] * 3 + [_vp],
+    "jt_hip_gdn2_prefill_ws_bytes": ([_i] * 3, _sz),
+    "jt_hip_gdn2_prefill": [_vp] * 8 + [_i] * 5 + [_vp, _sz, _vp],
 }
 
 
@@ -325,6 +337,88 @@ def moe_bwd_batch_device(dY, X, Wgate, Wg, Wu, Wd, Wg_s, Wu_s, Wd_s, ids, w, Gse
                                     *[ptr(out.get(nm)) for nm in _BWD_OUT], T, n, h, E, k, S,
                                     int(validate), ptr(ws), ws.numel(), st)
     return rc, out, ws
+
+
+# ---------------- Gated DeltaNet-2 (host pointers, reference names) ----------------
+
+class _State:
+    """A state from jt_gdn2_state_alloc (64-byte aligned host memory)."""
+
+    def __init__(self, S):
+        S = _c(S, np.float32)
+        self.dk, self.dv = S.shape
+        self.p = _vp()
+        rc = lib().jt_gdn2_state_alloc(C.byref(self.p), self.dk, self.dv)
+        if rc != JT_OK:
+            raise RuntimeError(f"jt_gdn2_state_alloc rc={rc}")
+        C.memmove(self.p, S.ctypes.data, S.nbytes)
+
+    def read(self):
+        a = np.empty((self.dk, self.dv), np.float32)
+        C.memmove(a.ctypes.data, self.p, a.nbytes)
+        return a
+
+    def __del__(self):
+        if getattr(self, "p", None):
+            lib().jt_gdn2_state_free(self.p)
+
+
+def gdn2_l2norm(x, eps=1e-6):
+    x = _c(x, np.float32).ravel()
+    y = np.full_like(x, np.nan)
+    return lib().jt_gdn2_l2norm(x.ctypes.data, y.ctypes.data, x.size, eps), y
+
+
+def gdn2_decode_step(S, q, k, v, b, w, alpha):
+    """jt_gdn2_decode_step on a copy of S [dk][dv]; returns (rc, S', o)."""
+    st = _State(S)
+    f = lambda a: _c(a, np.float32).ravel()  # noqa: E731
+    ins = [f(a) for a in (q, k, v, b, w, alpha)]
+    o = np.full(st.dv, np.nan, np.float32)
+    need = 2 * st.dk + 2 * st.dv
+    scratch = np.zeros(need, np.float32)
+    rc = lib().jt_gdn2_decode_step(st.p, o.ctypes.data, *[a.ctypes.data for a in ins],
+                                   st.dk, st.dv, scratch.ctypes.data, need)
+    return rc, st.read(), o
+
+
+def gdn2_prefill_chunk(S, Q, K, V, B, W, A):
+    """jt_gdn2_prefill_chunk16/32 (C = rows of Q) on a copy of S; returns
+    (rc, S', Out)."""
+    st = _State(S)
+    Cn = Q.shape[0]
+    f = lambda a: _c(a, np.float32)  # noqa: E731
+    ins = [f(a) for a in (Q, K, V, B, W, A)]
+    Out = np.full((Cn, st.dv), np.nan, np.float32)
+    need = 4 * Cn * st.dk + 2 * Cn * st.dv + Cn * Cn + st.dk
+    scratch = np.zeros(need, np.float32)
+    fn = lib().jt_gdn2_prefill_chunk16 if Cn == 16 else lib().jt_gdn2_prefill_chunk32
+    rc = fn(st.p, Out.ctypes.data, *[a.ctypes.data for a in ins], st.dk, st.dv,
+            scratch.ctypes.data, need)
+    return rc, st.read(), Out
+
+
+def gdn2_decode_device(S, O, q, k, v, b, w, alpha, stream=None):
+    """jt_hip_gdn2_decode on torch tensors: S [H][dk][dv] in place,
+    O [H][dv], q/k/b/alpha [H][dk], v/w [H][dv]. Returns rc."""
+    H, dk, dv = S.shape
+    return lib().jt_hip_gdn2_decode(*[t.data_ptr() for t in (S, O, q, k, v, b, w, alpha)], H,
+                                    dk, dv, _stream(stream))
+
+
+def gdn2_prefill_device(S, Out, Q, K, V, B, W, A, C_, ws=None, stream=None):
+    """jt_hip_gdn2_prefill on torch tensors: S [H][dk][dv] in place,
+    Q/K/B/A [H][T][dk], V/W/Out [H][T][dv], chunks of C_ (16 or 32).
+    Returns (rc, ws)."""
+    import torch
+    H, dk, dv = S.shape
+    T = Q.shape[1]
+    nb = lib().jt_hip_gdn2_prefill_ws_bytes(H, C_, dk)
+    if ws is None:
+        ws = torch.empty(nb, dtype=torch.uint8, device=S.device)
+    rc = lib().jt_hip_gdn2_prefill(*[t.data_ptr() for t in (S, Out, Q, K, V, B, W, A)], H, T,
+                                   C_, dk, dv, ws.data_ptr(), ws.numel(), _stream(stream))
+    return rc, ws
 
 
 def moe_fwd_batch(X, Wgate, Wg, Wu, Wd, Wg_s, Wu_s, Wd_s, k, cap_factor, unchecked=False,

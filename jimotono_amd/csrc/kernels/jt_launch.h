@@ -179,6 +179,21 @@ size_t jtk_bwd_ws_layout(int T, int n, int h, int E, int k, int S, jtk_bwd_ws *w
 int jtk_bwd_batch(const jtk_bwd_io *io, int T, int n, int h, int E, int k, int S, int validate,
                   const jtk_bwd_ws *w, uint32_t *err, hipStream_t s);
 
+/* gdn2.hip: Gated DeltaNet-2 decode step and prefill chunk over H heads.
+ * Decode: S [H][dk][dv], O [H][dv], q/k/b/alpha [H][dk], v/w [H][dv].
+ * Prefill: head h's rows of Q/K/B/A start at h*hk, of V/W/Out at h*hv. */
+int jtk_gdn2_decode(float *S, float *O, const float *q, const float *k, const float *v,
+                    const float *b, const float *w, const float *alpha, int H, int dk, int dv,
+                    uint32_t *err, hipStream_t s);
+size_t jtk_gdn2_chunk_ws_bytes(int H, int C, int dk);
+/* T tokens per head (T % C == 0) in T/C chunks; a head with a bad input
+ * value anywhere keeps its S and Out (EF_NONFINITE_INPUT). */
+int jtk_gdn2_prefill(float *S, float *Out, const float *Q, const float *K, const float *V,
+                     const float *B, const float *W, const float *A, int64_t hk, int64_t hv,
+                     int H, int T, int C, int dk, int dv, float *ws, uint32_t *err,
+                     hipStream_t s);
+int jtk_gdn2_l2norm(const float *x, float *y, int rows, int n, float eps, hipStream_t s);
+
 #ifdef __cplusplus
 }
 #endif

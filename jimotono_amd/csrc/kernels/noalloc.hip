@@ -48,6 +48,7 @@ extern "C" int jtk_preload_quant(void);
 extern "C" int jtk_preload_route(void);
 extern "C" int jtk_preload_router(void);
 extern "C" int jtk_preload_bwd(void);
+extern "C" int jtk_preload_gdn2(void);
 
 extern "C" int jtk_preload(void) {
     int e = jtk_preload_gemm_i8();
@@ -56,6 +57,7 @@ extern "C" int jtk_preload(void) {
     if (!e) e = jtk_preload_route();
     if (!e) e = jtk_preload_router();
     if (!e) e = jtk_preload_bwd();
+    if (!e) e = jtk_preload_gdn2();
     if (!e) {
         hipFuncAttributes a;
         e = (int)hipFuncGetAttributes(&a, (const void *)k_scratch_zero);

@@ -1419,3 +1419,173 @@ out:
     free(dxe);
     return rc;
 }
+
+/* ===================== GDN-2 ===================== */
+
+static int gdn2_dims_ok(int dk, int dv) {
+    return dk > 0 && dv > 0 && dk <= 1024 && dv <= 1024;
+}
+
+int or_gdn2_l2norm(const float *x, float *y, int n, float eps) {
+    if (!x || !y || n <= 0 || n > 1024 || !(eps > 0.0f)) return RC_INVAL;
+    double ss = 0.0;
+    for (int i = 0; i < n; i++) ss = ss + (double)x[i] * (double)x[i];
+    const double nrm = sqrt(ss);
+    if (nrm < (double)eps) {
+        for (int i = 0; i < n; i++) y[i] = 0.0f;
+        return RC_OK;
+    }
+    const float inv = (float)(1.0 / nrm);
+    for (int i = 0; i < n; i++) y[i] = x[i] * inv;
+    return RC_OK;
+}
+
+/* the inputs of a decode step / prefill chunk are finite and alpha in [0,1] */
+static int gdn2_inputs_ok(const float *q, const float *k, const float *b,
+                          const float *alpha, size_t nk, const float *v,
+                          const float *w, size_t nv) {
+    if (!all_finite_f(q, nk) || !all_finite_f(k, nk) || !all_finite_f(b, nk) ||
+        !all_finite_f(alpha, nk) || !all_finite_f(v, nv) || !all_finite_f(w, nv))
+        return 0;
+    for (size_t i = 0; i < nk; i++)
+        if (!(alpha[i] >= 0.0f && alpha[i] <= 1.0f)) return 0;
+    return 1;
+}
+
+int or_gdn2_decode_step(float *S, float *o, const float *q, const float *k,
+                        const float *v, const float *b, const float *w,
+                        const float *alpha, int dk, int dv) {
+    if (!S || !o || !q || !k || !v || !b || !w || !alpha) return RC_INVAL;
+    if (!gdn2_dims_ok(dk, dv)) return RC_INVAL;
+    if (!gdn2_inputs_ok(q, k, b, alpha, (size_t)dk, v, w, (size_t)dv)) return RC_INVAL;
+    float *buf = malloc((2 * (size_t)dk + 2 * (size_t)dv) * sizeof(float));
+    if (!buf) return RC_NOMEM;
+    float *qn = buf, *kn = qn + dk, *c = kn + dk, *vw = c + dv;
+    or_gdn2_l2norm(q, qn, dk, 1e-6f);
+    or_gdn2_l2norm(k, kn, dk, 1e-6f);
+    /* pass 1 (one sweep of S): decay each row, then c += (b*kn)_i * row */
+    for (int j = 0; j < dv; j++) c[j] = 0.0f;
+    for (int i = 0; i < dk; i++) {
+        float *row = S + (size_t)i * dv;
+        const float ke = b[i] * kn[i];
+        for (int j = 0; j < dv; j++) row[j] = row[j] * alpha[i];
+        for (int j = 0; j < dv; j++) c[j] = c[j] + ke * row[j];
+    }
+    for (int j = 0; j < dv; j++) vw[j] = w[j] * v[j];
+    /* pass 2: erase, write, read out */
+    for (int j = 0; j < dv; j++) o[j] = 0.0f;
+    for (int i = 0; i < dk; i++) {
+        float *row = S + (size_t)i * dv;
+        for (int j = 0; j < dv; j++) row[j] = row[j] - kn[i] * c[j];
+        for (int j = 0; j < dv; j++) row[j] = row[j] + kn[i] * vw[j];
+        for (int j = 0; j < dv; j++) o[j] = o[j] + qn[i] * row[j];
+    }
+    free(buf);
+    return RC_OK;
+}
+
+/* sum over i of (x[i]*d[i])*y[i] in four chains over i % 4 for
+ * i < dk & ~3, the tail into chain 0, then (s0+s1)+(s2+s3)
+ * (src/gdn2.c:584-599, 702-713) */
+static float gdn2_dot3(const float *x, const float *d, const float *y, int dk) {
+    float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    int i = 0;
+    for (; i + 3 < dk; i += 4)
+        for (int l = 0; l < 4; l++) s[l] = s[l] + (x[i + l] * d[i + l]) * y[i + l];
+    for (; i < dk; i++) s[0] = s[0] + (x[i] * d[i]) * y[i];
+    return (s[0] + s[1]) + (s[2] + s[3]);
+}
+
+int or_gdn2_prefill_chunk(float *S, float *Out, const float *Q,
+                          const float *K, const float *V, const float *B,
+                          const float *W, const float *Alpha, int dk, int dv,
+                          int C) {
+    if (!S || !Out || !Q || !K || !V || !B || !W || !Alpha) return RC_INVAL;
+    if ((C != 16 && C != 32) || !gdn2_dims_ok(dk, dv)) return RC_INVAL;
+    const size_t Ck = (size_t)C * dk, Cv = (size_t)C * dv;
+    if (!gdn2_inputs_ok(Q, K, B, Alpha, Ck, V, W, Cv)) return RC_INVAL;
+    float *buf = malloc((4 * Ck + 2 * Cv + (size_t)C * C + 2 * (size_t)dk) * sizeof(float));
+    if (!buf) return RC_NOMEM;
+    float *Qn = buf, *Kn = Qn + Ck, *KE = Kn + Ck, *Wg = KE + Ck;
+    float *U = Wg + Ck, *G = U + Cv, *LP = G + Cv, *cum = LP + (size_t)C * C;
+    float *cf = cum + dk;
+    for (int t = 0; t < C; t++) {
+        or_gdn2_l2norm(Q + (size_t)t * dk, Qn + (size_t)t * dk, dk, 1e-6f);
+        or_gdn2_l2norm(K + (size_t)t * dk, Kn + (size_t)t * dk, dk, 1e-6f);
+    }
+    for (size_t n = 0; n < Ck; n++) KE[n] = B[n] * Kn[n];
+    for (size_t n = 0; n < Cv; n++) U[n] = W[n] * V[n];
+    /* L[t][s] (t > s) = (ke_t * cum(t,s)) . k_s, cum(t,s) = alpha_{s+1..t} */
+    for (int s = 0; s < C; s++) {
+        for (int i = 0; i < dk; i++) cum[i] = 1.0f;
+        for (int t = s + 1; t < C; t++) {
+            for (int i = 0; i < dk; i++) cum[i] = cum[i] * Alpha[(size_t)t * dk + i];
+            LP[(size_t)t * C + s] =
+                gdn2_dot3(KE + (size_t)t * dk, cum, Kn + (size_t)s * dk, dk);
+        }
+    }
+    /* G_t = u_t - sum_i (ke_t * cumfwd(t))[i] S[i], cumfwd(t) = alpha_{0..t} */
+    for (int i = 0; i < dk; i++) cum[i] = 1.0f;
+    for (int t = 0; t < C; t++) {
+        float *g = G + (size_t)t * dv;
+        for (int i = 0; i < dk; i++) cum[i] = cum[i] * Alpha[(size_t)t * dk + i];
+        for (int j = 0; j < dv; j++) g[j] = U[(size_t)t * dv + j];
+        for (int i = 0; i < dk; i++) {
+            const float wi = KE[(size_t)t * dk + i] * cum[i];
+            for (int j = 0; j < dv; j++) g[j] = g[j] - wi * S[(size_t)i * dv + j];
+        }
+    }
+    /* (I + L) E = G by forward substitution, in place */
+    for (int t = 0; t < C; t++)
+        for (int s = 0; s < t; s++) {
+            const float l = LP[(size_t)t * C + s];
+            for (int j = 0; j < dv; j++)
+                G[(size_t)t * dv + j] = G[(size_t)t * dv + j] - l * G[(size_t)s * dv + j];
+        }
+    /* P[t][s] (s <= t) = (q_t * cum(t,s)) . k_s */
+    for (int s = 0; s < C; s++) {
+        for (int i = 0; i < dk; i++) cum[i] = 1.0f;
+        for (int t = s; t < C; t++) {
+            if (t != s)
+                for (int i = 0; i < dk; i++) cum[i] = cum[i] * Alpha[(size_t)t * dk + i];
+            LP[(size_t)t * C + s] =
+                gdn2_dot3(Qn + (size_t)t * dk, cum, Kn + (size_t)s * dk, dk);
+        }
+    }
+    /* Out_t = sum_i (q_t * cumfwd(t))[i] S[i] + sum_{s <= t} P[t][s] E_s */
+    for (int i = 0; i < dk; i++) cum[i] = 1.0f;
+    for (int t = 0; t < C; t++) {
+        float *ot = Out + (size_t)t * dv;
+        for (int i = 0; i < dk; i++) cum[i] = cum[i] * Alpha[(size_t)t * dk + i];
+        for (int j = 0; j < dv; j++) ot[j] = 0.0f;
+        for (int i = 0; i < dk; i++) {
+            const float wi = Qn[(size_t)t * dk + i] * cum[i];
+            for (int j = 0; j < dv; j++) ot[j] = ot[j] + wi * S[(size_t)i * dv + j];
+        }
+        for (int s = 0; s <= t; s++) {
+            const float p = LP[(size_t)t * C + s];
+            for (int j = 0; j < dv; j++) ot[j] = ot[j] + p * G[(size_t)s * dv + j];
+        }
+    }
+    /* S <- cumfwd(C-1) * S + sum_s (k_s * suffix_s) E_s^T, suffix_s =
+     * alpha_{s+1..C-1} accumulated from the end */
+    for (int i = 0; i < dk; i++) cum[i] = 1.0f;
+    for (int s = C - 1; s >= 0; s--)
+        for (int i = 0; i < dk; i++) {
+            Wg[(size_t)s * dk + i] = Kn[(size_t)s * dk + i] * cum[i];
+            cum[i] = cum[i] * Alpha[(size_t)s * dk + i];
+        }
+    for (int i = 0; i < dk; i++) cf[i] = 1.0f;
+    for (int t = 0; t < C; t++)
+        for (int i = 0; i < dk; i++) cf[i] = cf[i] * Alpha[(size_t)t * dk + i];
+    for (int i = 0; i < dk; i++) {
+        float *row = S + (size_t)i * dv;
+        for (int j = 0; j < dv; j++) row[j] = row[j] * cf[i];
+        for (int s = 0; s < C; s++) {
+            const float wv = Wg[(size_t)s * dk + i];
+            for (int j = 0; j < dv; j++) row[j] = row[j] + wv * G[(size_t)s * dv + j];
+        }
+    }
+    free(buf);
+    return RC_OK;
+}

@@ -153,6 +153,25 @@ int or_moe_bwd_batch(const float *dY, const float *X, const float *Wgate,
                      float *dWg_s, float *dWu_s, float *dWd_s, float *dLogits,
                      int T, int n, int h, int E, int k, int S, int validate);
 
+/* ---------- GDN-2 linear attention (src/gdn2.c) ----------
+ * State S [dk][dv] fp32 row-major; q, k, b, alpha [dk]; v, w [dv].
+ * Returns 0 or 2 (EINVAL cases: dims outside 1..1024, non-finite inputs,
+ * alpha outside [0,1]); on 2 nothing is written. */
+/* y = x * (float)(1/sqrt(sum x^2 in fp64, i ascending)); y = 0 when the
+ * norm is below eps. src/gdn2.c:219-250. */
+int or_gdn2_l2norm(const float *x, float *y, int n, float eps);
+/* One decode step (src/gdn2.c:252-405): S <- S*alpha (rows), c = (b*kn)^T S,
+ * S <- S - kn c^T + kn (w*v)^T, o = S^T qn, fp32 in the reference's order. */
+int or_gdn2_decode_step(float *S, float *o, const float *q, const float *k,
+                        const float *v, const float *b, const float *w,
+                        const float *alpha, int dk, int dv);
+/* One prefill chunk of C = 16 or 32 tokens in the WY form
+ * (src/gdn2.c:474-842): Q, K, B, Alpha [C][dk]; V, W, Out [C][dv]. */
+int or_gdn2_prefill_chunk(float *S, float *Out, const float *Q,
+                          const float *K, const float *V, const float *B,
+                          const float *W, const float *Alpha, int dk, int dv,
+                          int C);
+
 /* ---------- prepared quantised layer (MI355X fast path) ---------- */
 typedef struct or_moe_q {
     int n, h, E, k, S, hs, group;

@@ -139,6 +139,9 @@ class Oracle:
                                  _f32p]
         L.or_residual_add.argtypes = [_f32p, _f32p, _f32p, C.c_size_t]
         L.or_moe_bwd_batch.argtypes = [C.c_void_p] * 28 + [C.c_int] * 7
+        L.or_gdn2_l2norm.argtypes = [_f32p, _f32p, C.c_int, C.c_float]
+        L.or_gdn2_decode_step.argtypes = [_f32p] * 8 + [C.c_int] * 2
+        L.or_gdn2_prefill_chunk.argtypes = [_f32p] * 8 + [C.c_int] * 3
 
     # ---- W8A8 ----
     def quant_rows(self, X):
@@ -330,6 +333,31 @@ class Oracle:
                                       X.size)
         return rc, Y
 
+    def gdn2_l2norm(self, x, eps=1e-6):
+        x = _c(x, np.float32).ravel()
+        y = np.full_like(x, np.nan)
+        return self.lib.or_gdn2_l2norm(x, y, x.size, eps), y
+
+    def gdn2_decode_step(self, S, q, k, v, b, w, alpha):
+        """One step on a copy of S; returns rc, S', o."""
+        S = np.array(S, np.float32, order="C", copy=True)
+        dk, dv = S.shape
+        o = np.full(dv, np.nan, np.float32)
+        f = lambda a: _c(a, np.float32).ravel()  # noqa: E731
+        rc = self.lib.or_gdn2_decode_step(S, o, f(q), f(k), f(v), f(b), f(w), f(alpha), dk, dv)
+        return rc, S, o
+
+    def gdn2_prefill_chunk(self, S, Q, K, V, B, W, A):
+        """One chunk (C = rows of Q) on a copy of S; returns rc, S', Out."""
+        S = np.array(S, np.float32, order="C", copy=True)
+        dk, dv = S.shape
+        C_ = Q.shape[0]
+        Out = np.full((C_, dv), np.nan, np.float32)
+        f = lambda a: _c(a, np.float32)  # noqa: E731
+        rc = self.lib.or_gdn2_prefill_chunk(S, Out, f(Q), f(K), f(V), f(B), f(W), f(A), dk, dv,
+                                            C_)
+        return rc, S, Out
+
     def moe_bwd_batch(self, *args, validate=1, **kw):
         """or_moe_bwd_batch; arguments as bwd_batch_call."""
         return bwd_batch_call(self.lib.or_moe_bwd_batch, np.int64, *args,
@@ -439,6 +467,14 @@ class RefLib:
             C.c_void_p] * 5
         for fn in (L.jt_moe_bwd_batch, L.jt_moe_bwd_batch_unchecked):
             fn.argtypes = [C.c_void_p] * 28 + [C.c_int] * 6
+        L.jt_gdn2_l2norm.argtypes = [_f32p, _f32p, C.c_int, C.c_float]
+        L.jt_gdn2_state_alloc.argtypes = [C.POINTER(C.c_void_p), C.c_int, C.c_int]
+        L.jt_gdn2_state_free.argtypes = [C.c_void_p]
+        L.jt_gdn2_state_free.restype = None
+        L.jt_gdn2_decode_step.argtypes = [C.c_void_p] + [_f32p] * 7 + [C.c_int] * 2 + [
+            _f32p, C.c_size_t]
+        for fn in (L.jt_gdn2_prefill_chunk16, L.jt_gdn2_prefill_chunk32):
+            fn.argtypes = [C.c_void_p] + [_f32p] * 7 + [C.c_int] * 2 + [_f32p, C.c_size_t]
 
     def quant_rows(self, X):
         X = _c(X, np.float32)
@@ -575,6 +611,48 @@ class RefLib:
                     perm=perm[: kept.value].astype(np.int64), off=off.astype(np.int64),
                     drop=drop, Ysel=Ysel, **cache)
 
+
+    def gdn2_l2norm(self, x, eps=1e-6):
+        x = _c(x, np.float32).ravel()
+        y = np.full_like(x, np.nan)
+        return self.lib.jt_gdn2_l2norm(x, y, x.size, eps), y
+
+    def _gdn2_state(self, S):
+        """S copied into a state of the reference's own allocator (64-byte
+        aligned, as jt_gdn2_decode_step requires)."""
+        dk, dv = S.shape
+        p = C.c_void_p()
+        assert self.lib.jt_gdn2_state_alloc(C.byref(p), dk, dv) == 0
+        C.memmove(p, _c(S, np.float32).ctypes.data, S.size * 4)
+        return p
+
+    def _gdn2_take(self, p, dk, dv):
+        out = np.ctypeslib.as_array((C.c_float * (dk * dv)).from_address(p.value)).copy()
+        self.lib.jt_gdn2_state_free(p)
+        return out.reshape(dk, dv)
+
+    def gdn2_decode_step(self, S, q, k, v, b, w, alpha):
+        dk, dv = S.shape
+        p = self._gdn2_state(S)
+        o = np.full(dv, np.nan, np.float32)
+        need = 2 * dk + 2 * dv
+        scratch = np.zeros(need, np.float32)
+        f = lambda a: _c(a, np.float32).ravel()  # noqa: E731
+        rc = self.lib.jt_gdn2_decode_step(p, o, f(q), f(k), f(v), f(b), f(w), f(alpha), dk, dv,
+                                          scratch, need)
+        return rc, self._gdn2_take(p, dk, dv), o
+
+    def gdn2_prefill_chunk(self, S, Q, K, V, B, W, A):
+        dk, dv = S.shape
+        C_ = Q.shape[0]
+        p = self._gdn2_state(S)
+        Out = np.full((C_, dv), np.nan, np.float32)
+        need = 4 * C_ * dk + 2 * C_ * dv + C_ * C_ + dk
+        scratch = np.zeros(need, np.float32)
+        fn = self.lib.jt_gdn2_prefill_chunk16 if C_ == 16 else self.lib.jt_gdn2_prefill_chunk32
+        f = lambda a: _c(a, np.float32)  # noqa: E731
+        rc = fn(p, Out, f(Q), f(K), f(V), f(B), f(W), f(A), dk, dv, scratch, need)
+        return rc, self._gdn2_take(p, dk, dv), Out
 
     def moe_bwd_batch(self, *args, validate=1, **kw):
         """jt_moe_bwd_batch / _unchecked; arguments as bwd_batch_call."""

@@ -175,3 +175,51 @@ def ref_bwd_inputs(case):
     W = [np.array([f(0.3) * lpat(i, r, salt) for i in range(E * h * n)], f).reshape(E, h, n)
          for r, salt in ((0, 59), (1, 60), (2, 61))]
     return (X, dY, Wgate, *W, None, None, None, k, 1.25)
+
+
+def gdn2_decode_inputs(dk, dv, seed):
+    """The inputs of the reference's GDN-2 decode test
+    (bench/kernel/gdn2.c:95-157, test_numeric_case): S0, q, k, v, b, w,
+    alpha in the test's float32 arithmetic."""
+    f = np.float32
+    q = np.array([lpat(i, 0, seed) + f(0.37) for i in range(dk)], f)
+    k = np.array([lpat(i, 1, seed + 1) - f(0.23) for i in range(dk)], f)
+    b = np.array([f(0.5) + f(0.1) * lpat(i, 2, seed) for i in range(dk)], f)
+    a = np.array([f(0.9) + f(0.05) * lpat(i, 3, seed) for i in range(dk)], f)
+    v = np.array([lpat(0, j, seed + 2) + f(0.11) for j in range(dv)], f)
+    w = np.array([f(0.6) + f(0.1) * lpat(1, j, seed) for j in range(dv)], f)
+    S = np.array([[f(0.25) * lpat(i, j, seed + 3) for j in range(dv)] for i in range(dk)], f)
+    return S, q, k, v, b, w, a
+
+
+def gdn2_prefill_inputs(C, dk, dv, seed):
+    """The inputs of the reference's prefill equivalence test
+    (bench/kernel/gdn2.c:522-580): S0, Q, K, V, B, W, A."""
+    f = np.float32
+    Q = np.array([[lpat(t, i, seed) + f(0.37) for i in range(dk)] for t in range(C)], f)
+    K = np.array([[lpat(t, i, seed + 1) - f(0.23) for i in range(dk)] for t in range(C)], f)
+    B = np.array([[f(0.5) + f(0.1) * lpat(t, i, seed + 2) for i in range(dk)] for t in range(C)], f)
+    A = np.array([[f(0.9) + f(0.05) * lpat(t, i, seed + 3) for i in range(dk)] for t in range(C)],
+                 f)
+    V = np.array([[lpat(t, j, seed + 4) + f(0.11) for j in range(dv)] for t in range(C)], f)
+    W = np.array([[f(0.6) + f(0.1) * lpat(t, j, seed + 5) for j in range(dv)] for t in range(C)], f)
+    S = np.array([f(0.25) * lpat(i, 0, seed + 6) for i in range(dk * dv)], f).reshape(dk, dv)
+    return S, Q, K, V, B, W, A
+
+
+def gdn2_boundary_inputs():
+    """The reference's prefill boundary test (bench/kernel/gdn2.c:623-668):
+    alpha in {0, 1, 0.9}, a zero q row and a zero k row; C=16, dk=dv=8."""
+    f = np.float32
+    C, dk, dv = 16, 8, 8
+    Q = np.array([[lpat(t, i, 21) + f(0.37) for i in range(dk)] for t in range(C)], f)
+    K = np.array([[lpat(t, i, 22) - f(0.23) for i in range(dk)] for t in range(C)], f)
+    B = np.full((C, dk), 0.5, f)
+    A = np.array([[0.0 if t % 3 == 0 else (1.0 if t % 3 == 1 else 0.9) for _ in range(dk)]
+                  for t in range(C)], f)
+    V = np.array([[lpat(t, j, 23) + f(0.11) for j in range(dv)] for t in range(C)], f)
+    W = np.full((C, dv), 0.6, f)
+    Q[3] = 0.0
+    K[5] = 0.0
+    S = np.array([f(0.25) * lpat(i, 0, 24) for i in range(dk * dv)], f).reshape(dk, dv)
+    return S, Q, K, V, B, W, A

@@ -37,6 +37,11 @@ Cases (key prefixes in the .npz):
                  inputs, forward outputs and every backward output
   bwdrnd_*       jt_moe_bwd_batch outputs of gen.bwd_case(*BWD_RND) (drops, two
                  shared experts, n not a multiple of 4)
+  gdn2dec_{dk}x{dv}s{seed}_{S,o}  jt_gdn2_decode_step on the reference test's
+                 inputs (gen.gdn2_decode_inputs, bench/kernel/gdn2.c:850-860)
+  gdn2pf{C}_{dk}x{dv}s{seed}_{S,Out,Sseq,Oseq}  jt_gdn2_prefill_chunk{C} and C
+                 sequential jt_gdn2_decode_step calls on gen.gdn2_prefill_inputs;
+                 gdn2pfb_* the same on gen.gdn2_boundary_inputs
 """
 import os
 import sys
@@ -49,7 +54,8 @@ sys.path.insert(0, ROOT)
 
 from oracle.pyoracle import RefLib  # noqa: E402
 sys.path.insert(0, HERE)
-from gen import (accuracy_case, bwd_args, bwd_case, lpat_lut_inputs, ref_bwd_inputs,  # noqa: E402
+from gen import (accuracy_case, bwd_args, bwd_case, gdn2_boundary_inputs,  # noqa: E402
+                 gdn2_decode_inputs, gdn2_prefill_inputs, lpat_lut_inputs, ref_bwd_inputs,
                  shared_case)
 
 OUT = os.path.join(HERE, "ref_vectors.npz")
@@ -255,6 +261,28 @@ def main():
     for key, v in b.items():
         if key != "rc":
             g["bwdrnd_" + key] = v
+
+    # ---- GDN-2 decode and prefill chunks (the reference tests' inputs) ----
+    for dk, dv, seed in ((4, 8, 1), (5, 7, 2), (2, 3, 3), (8, 8, 4), (128, 128, 5)):
+        S, q, k, v, b, w, a = gdn2_decode_inputs(dk, dv, seed)
+        rc, S1, o = R.gdn2_decode_step(S, q, k, v, b, w, a)
+        assert rc == 0
+        g[f"gdn2dec_{dk}x{dv}s{seed}_S"], g[f"gdn2dec_{dk}x{dv}s{seed}_o"] = S1, o
+
+    def prefill_case(key, S, Q, K, V, B, W, A):
+        rc, S1, Out = R.gdn2_prefill_chunk(S, Q, K, V, B, W, A)
+        assert rc == 0
+        Ss, Os = S, []
+        for t in range(Q.shape[0]):
+            rc, Ss, o = R.gdn2_decode_step(Ss, Q[t], K[t], V[t], B[t], W[t], A[t])
+            assert rc == 0
+            Os.append(o)
+        g.update({key + "_S": S1, key + "_Out": Out, key + "_Sseq": Ss,
+                  key + "_Oseq": np.array(Os, np.float32)})
+    for C, dk, dv, seed in ((16, 8, 8, 11), (16, 16, 16, 12), (32, 8, 16, 13), (32, 16, 8, 14),
+                            (32, 128, 128, 15)):
+        prefill_case(f"gdn2pf{C}_{dk}x{dv}s{seed}", *gdn2_prefill_inputs(C, dk, dv, seed))
+    prefill_case("gdn2pfb", *gdn2_boundary_inputs())
 
     np.savez_compressed(OUT, **g)
     print(f"wrote {OUT}: {len(g)} arrays, {os.path.getsize(OUT)} bytes")
