@@ -17,8 +17,10 @@ The JSON line carries, beside the contract fields:
                   host, or the oracle restatement when _ref is absent;
   sub          -- the other benchmark shapes: W8A8 GEMM 64x1024x1024,
                   shared-expert decode M in {1,4,16}, routed decode T=16,
-                  the full decode layer at T=16 and the E=512 stress
-                  grouped GEMM.
+                  the full decode layer at T=16, the E=512 stress
+                  grouped GEMM, the batched MoE backward (training and
+                  layer shapes), the GDN-2 decode step and prefill, and the
+                  INT8 attention projection.
 """
 import argparse
 import json
@@ -504,6 +506,87 @@ def sub_benchmarks(np, torch, api, stream):
     # --- batched backward (fp32, bit-exact to the reference's) ---
     for name, shape in BWD_SHAPES.items():
         res[name] = bwd_bench(np, torch, api, stream, *shape)
+    # --- Gated DeltaNet-2 and the INT8 attention projections ---
+    res.update(gdn2_bench(np, torch, api, stream))
+    res.update(proj_bench(np, torch, api, stream))
+    return res
+
+
+def gdn2_bench(np, torch, api, stream):
+    """GDN-2 decode: one token for 64 sequences x 8 heads of 128x128 states
+    (the 1B configuration's d_model 1024 in 8 heads); each step reads and
+    writes every state once. Prefill: T=4096 tokens of 8 heads in chunks of
+    32. States stay in HBM."""
+    res = {}
+    H, dk, dv = 512, 128, 128
+    g = torch.Generator(device="cuda").manual_seed(41)
+    rn = lambda *s: torch.randn(*s, generator=g, device="cuda")  # noqa: E731
+    S = rn(H, dk, dv) * 0.3
+    q, k, b = rn(H, dk), rn(H, dk), torch.rand(H, dk, generator=g, device="cuda")
+    a = torch.rand(H, dk, generator=g, device="cuda") * 0.1 + 0.9
+    v, w = rn(H, dv), torch.rand(H, dv, generator=g, device="cuda")
+    O = torch.empty(H, dv, device="cuda")
+    _, ev = time_fn(torch, lambda: api.gdn2_decode_device(S, O, q, k, v, b, w, a, stream), 50,
+                    5, stream)
+    assert api.sync_errors(stream) == 0
+    nbytes = H * (2 * dk * dv * 4 + 4 * dk * 4 + 3 * dv * 4)
+    res["gdn2_decode_H512"] = {"us_per_step": ev * 1e3, "heads": H, "dk": dk, "dv": dv,
+                               "state_bytes_rw": nbytes, "gbps": nbytes / (ev / 1e3) / 1e9,
+                               "hbm_frac": nbytes / (ev / 1e3) / HBM_PEAK}
+    del S, O
+    H, T, C = 8, 4096, 32
+    S = rn(H, dk, dv) * 0.3
+    Q, K, B = rn(H, T, dk), rn(H, T, dk), torch.rand(H, T, dk, generator=g, device="cuda")
+    A = torch.rand(H, T, dk, generator=g, device="cuda") * 0.1 + 0.9
+    V, W = rn(H, T, dv), torch.rand(H, T, dv, generator=g, device="cuda")
+    Out = torch.empty(H, T, dv, device="cuda")
+    ws = [None]
+
+    def pstep():
+        rc, ws[0] = api.gdn2_prefill_device(S, Out, Q, K, V, B, W, A, C, ws=ws[0], stream=stream)
+        assert rc == 0
+    _, ev = time_fn(torch, pstep, 3, 1, stream)
+    assert api.sync_errors(stream) == 0
+    # fp32 work of the WY form per chunk and head (multiplies and adds):
+    # B, Out and the state update 3 x 2 C dk dv, the solve and P terms C^2 dv
+    flops = H * (T // C) * (6.0 * C * dk * dv + 2.0 * C * C * dv)
+    res["gdn2_prefill_T4096_H8"] = {"ms": ev, "tokens_per_s": H * T / (ev / 1e3),
+                                    "heads": H, "T": T, "chunk": C, "dk": dk, "dv": dv,
+                                    "gflops": flops / (ev / 1e3) / 1e9}
+    del S, Q, K, B, A, V, W, Out, ws
+    torch.cuda.empty_cache()
+    return res
+
+
+def proj_bench(np, torch, api, stream):
+    """The INT8 attention projection: fp32 activations quantised per token
+    inside the call, fused q/k/v weights [3072][1024] (per-channel int8),
+    at M = 1 and 16 (decode, 40 rotating weight copies so the weights come
+    from HBM) and M = 4096 (prefill)."""
+    res = {}
+    N, K = 3072, 1024
+    copies = 40
+    Ws = [api.W8A8(W=torch.randn(N, K, device="cuda") / 32) for _ in range(copies)]
+    wbytes = N * K + 4 * N
+    for M in (1, 16, 4096):
+        X = torch.randn(M, K, device="cuda")
+        out = torch.empty(M, N, device="cuda")
+        ws = [Ws[0].gemm_f32(X, out, stream=stream)]
+        it = [0]
+
+        def step():
+            ws[0] = Ws[it[0] % copies].gemm_f32(X, out, ws=ws[0], stream=stream)
+            it[0] += 1
+        _, ev = time_fn(torch, step, 4 * copies if M <= 16 else 20, copies if M <= 16 else 3,
+                        stream)
+        assert api.sync_errors(stream) == 0
+        r = {"us_per_call": ev * 1e3, "tops": 2.0 * M * N * K / (ev / 1e3) / 1e12,
+             "gbps": (wbytes + 4 * M * K + 4 * M * N) / (ev / 1e3) / 1e9}
+        r["hbm_frac"] = r["gbps"] * 1e9 / HBM_PEAK
+        r["mfma_frac"] = r["tops"] * 1e12 / INT8_PEAK
+        res[f"attn_proj_int8_M{M}"] = r
+    del Ws
+    torch.cuda.empty_cache()
     return res
 
 

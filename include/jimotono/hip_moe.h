@@ -80,6 +80,16 @@ int jt_hip_w8a8_gemm(const jt_hip_w8a8 *W, const int8_t *dAq,
 /* Copy out the quantised weights in the reference layout: Bq [K][N] int8
  * and sB [N] fp32 (host pointers; for tests). */
 int jt_hip_w8a8_export(const jt_hip_w8a8 *W, int8_t *Bq_kn, float *sB);
+/* The per-token INT8 projection of fp32 activations (the mixed-precision
+ * design's attention projections, reference AGENTS.MD:43-51): dC [M][N] =
+ * the GEMM above of dX [M][K] fp32 quantised per row with
+ * jt_w8a8_quant_per_channel's formula inside the call, bit-identical to
+ * jt_hip_quant_rows followed by jt_hip_w8a8_gemm. M <= 16 quantises in the
+ * GEMM's own blocks (no workspace; K % 4 == 0, K <= 4096, dX 16-byte
+ * aligned); larger M uses d_ws of jt_hip_w8a8_gemm_f32_ws_bytes(W, M) bytes. */
+size_t jt_hip_w8a8_gemm_f32_ws_bytes(const jt_hip_w8a8 *W, int M);
+int jt_hip_w8a8_gemm_f32(const jt_hip_w8a8 *W, const float *dX, float *dC,
+                         int M, void *d_ws, size_t ws_bytes, void *stream);
 void jt_hip_w8a8_free(jt_hip_w8a8 *W);
 
 /* ---- one W8A8 SwiGLU expert (the shared-expert block) ----

@@ -105,7 +105,9 @@ _PROTOS = {
     "jt_gdn2_prefill_chunk16": [_vp] * 8 + [_i, _i, _vp, _sz],
     "jt_gdn2_prefill_chunk32": [_vp] * 8 + [_i, _i, _vp, _sz],
     "jt_hip_gdn2_decode": [_vp] * 8 + [_i] * 3 + [_vp],
-    "jt_hip_gdn2_prefill_ws_bytes": ([_i] * 3, _sz),
+    "jt_hip_w8a8_gemm_f32_ws_bytes": ([_vp, _i], _sz),
+    "jt_hip_w8a8_gemm_f32": [_vp, _vp, _vp, _i, _vp, _sz, _vp],
+    "jt_hip_gdn2_prefill_ws_bytes": ([_i] * 4, _sz),
     "jt_hip_gdn2_prefill": [_vp] * 8 + [_i] * 5 + [_vp, _sz, _vp],
 }
 
@@ -413,8 +415,8 @@ def gdn2_prefill_device(S, Out, Q, K, V, B, W, A, C_, ws=None, stream=None):
     import torch
     H, dk, dv = S.shape
     T = Q.shape[1]
-    nb = lib().jt_hip_gdn2_prefill_ws_bytes(H, C_, dk)
-    if ws is None:
+    nb = lib().jt_hip_gdn2_prefill_ws_bytes(H, T, C_, dk)
+    if ws is None or ws.numel() < nb:
         ws = torch.empty(nb, dtype=torch.uint8, device=S.device)
     rc = lib().jt_hip_gdn2_prefill(*[t.data_ptr() for t in (S, Out, Q, K, V, B, W, A)], H, T,
                                    C_, dk, dv, ws.data_ptr(), ws.numel(), _stream(stream))
@@ -524,6 +526,19 @@ class W8A8:
     def gemm(self, Aq, sA, out, stream=None):
         _check(lib().jt_hip_w8a8_gemm(self.h, _ptr(Aq), _ptr(sA), _ptr(out), Aq.shape[0],
                                       _stream(stream)), "jt_hip_w8a8_gemm")
+
+    def gemm_f32(self, X, out, ws=None, stream=None):
+        """out [M][N] = the per-token INT8 projection of fp32 X [M][K]
+        (jt_hip_w8a8_gemm_f32); returns the workspace it used (M > 16)."""
+        import torch
+        M = X.shape[0]
+        nb = lib().jt_hip_w8a8_gemm_f32_ws_bytes(self.h, M)
+        if nb and (ws is None or ws.numel() < nb):
+            ws = torch.empty(nb, dtype=torch.uint8, device=X.device)
+        _check(lib().jt_hip_w8a8_gemm_f32(self.h, _ptr(X), _ptr(out), M,
+                                          _ptr(ws) if nb else None, nb, _stream(stream)),
+               "jt_hip_w8a8_gemm_f32")
+        return ws
 
     def export(self):
         Bq = np.zeros((self.K, self.N), np.int8)

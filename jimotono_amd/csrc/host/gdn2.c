@@ -148,7 +148,7 @@ static int prefill_chunk(float *S, float *Out, const float *Q, const float *K, c
     const size_t sb = (size_t)dk * dv * 4, kb = (size_t)C * dk * 4, vb = (size_t)C * dv * 4;
     stage_t st[9] = {{S, sb, NULL}, {Q, kb, NULL}, {K, kb, NULL},   {B, kb, NULL},
                      {A, kb, NULL}, {V, vb, NULL}, {W, vb, NULL},   {NULL, vb, NULL},
-                     {NULL, jtk_gdn2_chunk_ws_bytes(1, C, dk), NULL}};
+                     {NULL, jtk_gdn2_prefill_ws_bytes(1, C, C, dk), NULL}};
     int rc = stage_in(rt, st, 9, JT_SLOT_A);
     if (rc != JT_OK) return rc;
     if (jtk_gdn2_prefill(st[0].dev, st[7].dev, st[1].dev, st[2].dev, st[5].dev, st[3].dev,
@@ -191,9 +191,10 @@ int jt_hip_gdn2_decode(float *dS, float *dO, const float *dq, const float *dk_,
                : JT_OK;
 }
 
-size_t jt_hip_gdn2_prefill_ws_bytes(int H, int C, int dk) {
-    if (H <= 0 || (C != 16 && C != 32) || dk <= 0 || dk > JT_GDN2_MAX_D) return 0;
-    return jtk_gdn2_chunk_ws_bytes(H, C, dk);
+size_t jt_hip_gdn2_prefill_ws_bytes(int H, int T, int C, int dk) {
+    if (H <= 0 || (C != 16 && C != 32) || T <= 0 || T % C || dk <= 0 || dk > JT_GDN2_MAX_D)
+        return 0;
+    return jtk_gdn2_prefill_ws_bytes(H, T, C, dk);
 }
 
 int jt_hip_gdn2_prefill(float *dS, float *dOut, const float *dQ, const float *dK,
@@ -204,7 +205,7 @@ int jt_hip_gdn2_prefill(float *dS, float *dOut, const float *dQ, const float *dK
         FAIL(JT_ERR_INVAL, EINVAL);
     if (!dims_ok(dk, dv) || (C != 16 && C != 32) || T <= 0 || T % C) FAIL(JT_ERR_INVAL, EINVAL);
     if ((int64_t)T * (dk > dv ? dk : dv) > INT32_MAX) FAIL(JT_ERR_INVAL, EINVAL);
-    if (ws_bytes < jtk_gdn2_chunk_ws_bytes(H, C, dk) || ((uintptr_t)d_ws & 15u))
+    if (ws_bytes < jtk_gdn2_prefill_ws_bytes(H, T, C, dk) || ((uintptr_t)d_ws & 15u))
         FAIL(JT_ERR_INVAL, EINVAL);
     jt_rt *rt = jt_rt_get();
     if (!rt) return JT_ERR_IO;

@@ -361,6 +361,38 @@ int jt_hip_w8a8_gemm(const jt_hip_w8a8 *W, const int8_t *dAq, const float *dsA, 
     return JT_OK;
 }
 
+size_t jt_hip_w8a8_gemm_f32_ws_bytes(const jt_hip_w8a8 *W, int M) {
+    if (!W || M < 0) return 0;
+    if (M <= 16) return 0;
+    return jt_round_up((size_t)M * W->Kp, 256) + (size_t)M * sizeof(float);
+}
+
+int jt_hip_w8a8_gemm_f32(const jt_hip_w8a8 *W, const float *dX, float *dC, int M, void *d_ws,
+                         size_t ws_bytes, void *stream) {
+    if (!W || !dX || !dC || M < 0) FAIL(JT_ERR_INVAL, EINVAL);
+    jt_rt *rt = jt_rt_get();
+    if (!rt) return JT_ERR_IO;
+    if (M == 0) return JT_OK;
+    hipStream_t s = (hipStream_t)stream;
+    if (M <= 16) {
+        if (W->K % 4 || W->K > 4096 || ((uintptr_t)dX & 15u)) FAIL(JT_ERR_INVAL, EINVAL);
+        return jtk_w8a8_gemm_xq(dX, W->K, W->K, W->P, W->sB, M, W->N, W->Np, W->Kp, dC, W->N, 0,
+                                rt->d_err, s)
+                   ? jt_rt_err(hipErrorLaunchFailure)
+                   : JT_OK;
+    }
+    if (!d_ws || ws_bytes < jt_hip_w8a8_gemm_f32_ws_bytes(W, M) || ((uintptr_t)d_ws & 255u))
+        FAIL(JT_ERR_INVAL, EINVAL);
+    /* codes at row stride Kp: the columns K..Kp-1 meet zero weight codes */
+    int8_t *Xq = (int8_t *)d_ws;
+    float *sx = (float *)((char *)d_ws + jt_round_up((size_t)M * W->Kp, 256));
+    if (jtk_quant_rows(dX, M, W->K, Xq, W->Kp, sx, NULL, rt->d_err, s) ||
+        jtk_w8a8_gemm(Xq, W->Kp, sx, W->P, W->sB, M, W->N, W->Np, W->Kp, dC, W->N, 0, rt->d_err,
+                      s))
+        return jt_rt_err(hipErrorLaunchFailure);
+    return JT_OK;
+}
+
 int jt_hip_w8a8_export(const jt_hip_w8a8 *W, int8_t *Bq_kn, float *sB) {
     if (!W || !Bq_kn || !sB) FAIL(JT_ERR_INVAL, EINVAL);
     jt_rt *rt = jt_rt_get();

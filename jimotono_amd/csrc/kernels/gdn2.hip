@@ -14,13 +14,15 @@
 //                       src/gdn2.c:219-250), then per column: decay and the
 //                       erase coefficient (pass 1), erase + write + read-out
 //                       (pass 2), src/gdn2.c:333-405.
-//  k_gdn2_chunk_prep  : per head of a C-token chunk: checks, norms, ke, vw,
-//                       forward decay products, the strictly lower L and
-//                       the lower P (src/gdn2.c:537-714), the row weights
-//                       of the state update (:768-788).
-//  k_gdn2_chunk_cols  : per (head, 64 columns): B, the forward substitution,
-//                       Out and the state update (:614-680, 716-842) with
-//                       the chunk's C rows of a column in registers.
+//  k_gdn2_check       : a prefill's inputs, per head, before any chunk.
+//  k_gdn2_prep        : per (chunk, head), all chunks at once: everything
+//                       that does not depend on the state -- norms, ke, the
+//                       decay products, the strictly lower L and the lower
+//                       P (src/gdn2.c:537-714), the row weights of the state
+//                       update (:768-788).
+//  k_gdn2_cols        : per (head, 256/C columns), every chunk in order in
+//                       one launch: B, the forward substitution, Out and the
+//                       state update (:614-680, 716-842).
 #include "jt_dev.h"
 #include "jt_launch.h"
 
@@ -30,9 +32,18 @@ constexpr float GDN2_EPS = 1e-6f;
 
 // 1 / ||x|| as the reference rounds it: fp64 sum of squares in index order,
 // fp64 sqrt and divide, then float; *zero when the norm is below eps.
+// The loads go out 16 at a time ahead of the ordered sum.
 __device__ __forceinline__ float inv_norm(const float *x, int n, bool *zero) {
     double ss = 0.0;
-    for (int i = 0; i < n; i++) ss = ss + (double)x[i] * (double)x[i];
+    int i = 0;
+    for (; i + 16 <= n; i += 16) {
+        float v[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) v[u] = x[i + u];
+#pragma unroll
+        for (int u = 0; u < 16; u++) ss = ss + (double)v[u] * (double)v[u];
+    }
+    for (; i < n; i++) ss = ss + (double)x[i] * (double)x[i];
     const double nrm = sqrt(ss);
     *zero = nrm < (double)GDN2_EPS;
     return *zero ? 0.0f : (float)(1.0 / nrm);
@@ -50,8 +61,11 @@ __device__ __forceinline__ bool bad_alpha(const float *a, int n, int tid, int nt
     return bad;
 }
 
-// LDS: qn, kn, ke, al [dk] (dk <= 1024). Pass 1 writes the decayed column
-// back and pass 2 re-reads it (the same thread, so from cache).
+// LDS: qn, kn, ke, al [dk] (dk <= 1024). One thread per column (blockDim
+// = dv rounded up to 64, at most 256). Both passes read the column in
+// chunks of 32 rows, all 32 loads issued before the chunk's ordered
+// arithmetic; pass 2 re-reads the column (from cache) and recomputes the
+// decayed value, which is the same product as pass 1's.
 __global__ __launch_bounds__(256) void k_gdn2_decode(float *__restrict__ S, float *__restrict__ O,
                                                      const float *__restrict__ q,
                                                      const float *__restrict__ k,
@@ -63,67 +77,75 @@ __global__ __launch_bounds__(256) void k_gdn2_decode(float *__restrict__ S, floa
     __shared__ float qn[1024], kn[1024], ke[1024], al[1024];
     __shared__ float invs[2];
     __shared__ int zeros[2];
-    const int h = blockIdx.x, tid = threadIdx.x;
+    const int h = blockIdx.x, tid = threadIdx.x, nt = blockDim.x;
     const float *qh = q + (int64_t)h * dk, *kh = k + (int64_t)h * dk;
     const float *bh = b + (int64_t)h * dk, *ah = alpha + (int64_t)h * dk;
     const float *vh = v + (int64_t)h * dv, *wh = w + (int64_t)h * dv;
     float *Sh = S + (int64_t)h * dk * dv, *Oh = O + (int64_t)h * dv;
-    bool bad = bad_vec(qh, dk, tid, 256) || bad_vec(kh, dk, tid, 256) ||
-               bad_vec(bh, dk, tid, 256) || bad_vec(ah, dk, tid, 256) ||
-               bad_alpha(ah, dk, tid, 256) || bad_vec(vh, dv, tid, 256) ||
-               bad_vec(wh, dv, tid, 256);
+    bool bad = bad_vec(qh, dk, tid, nt) || bad_vec(kh, dk, tid, nt) || bad_vec(bh, dk, tid, nt) ||
+               bad_vec(ah, dk, tid, nt) || bad_alpha(ah, dk, tid, nt) ||
+               bad_vec(vh, dv, tid, nt) || bad_vec(wh, dv, tid, nt);
     if (__syncthreads_or(bad)) {  // fail-closed: this head's S and o untouched
         if (tid == 0) raise_err(err, EF_NONFINITE_INPUT);
         return;
     }
-    if (tid == 0 || tid == 64) {  // two waves, one norm each
+    for (int i = tid; i < dk; i += nt) {  // raw q, k into LDS for the norms
+        qn[i] = qh[i];
+        kn[i] = kh[i];
+        al[i] = ah[i];
+    }
+    __syncthreads();
+    const int kt = nt > 64 ? 64 : 1;  // the k norm on a second wave when there is one
+    if (tid == 0 || tid == kt) {
         bool z;
-        const float iv = inv_norm(tid ? kh : qh, dk, &z);
+        const float iv = inv_norm(tid ? kn : qn, dk, &z);
         invs[tid ? 1 : 0] = iv;
         zeros[tid ? 1 : 0] = z;
     }
     __syncthreads();
-    for (int i = tid; i < dk; i += 256) {
-        const float qi = zeros[0] ? 0.0f : qh[i] * invs[0];
-        const float ki = zeros[1] ? 0.0f : kh[i] * invs[1];
+    for (int i = tid; i < dk; i += nt) {
+        const float qi = zeros[0] ? 0.0f : qn[i] * invs[0];
+        const float ki = zeros[1] ? 0.0f : kn[i] * invs[1];
         qn[i] = qi;
         kn[i] = ki;
         ke[i] = bh[i] * ki;
-        al[i] = ah[i];
     }
     __syncthreads();
-    for (int j = tid; j < dv; j += 256) {
-        float *col = Sh + j;
-        float c = 0.0f;
-#pragma unroll 8
-        for (int i = 0; i < dk; i++) {
-            const float s = col[(int64_t)i * dv] * al[i];
-            col[(int64_t)i * dv] = s;
-            c = c + ke[i] * s;
-        }
+    for (int j = tid; j < dv; j += nt) {
+        const float *col = Sh + j;
+        float c = 0.0f, o = 0.0f;
         const float vw = wh[j] * vh[j];
-        float o = 0.0f;
-#pragma unroll 8
-        for (int i = 0; i < dk; i++) {
-            float r = col[(int64_t)i * dv] - kn[i] * c;
-            r = r + kn[i] * vw;
-            col[(int64_t)i * dv] = r;
-            o = o + qn[i] * r;
+        const int dk32 = dk & ~31;
+        for (int i0 = 0; i0 < dk32; i0 += 32) {
+            float x[32];
+#pragma unroll
+            for (int u = 0; u < 32; u++) x[u] = col[(int64_t)(i0 + u) * dv];
+#pragma unroll
+            for (int u = 0; u < 32; u++) c = c + ke[i0 + u] * (x[u] * al[i0 + u]);
         }
+        for (int i = dk32; i < dk; i++) c = c + ke[i] * (col[(int64_t)i * dv] * al[i]);
+        auto upd = [&](int i, float xv) {
+            float r = xv * al[i] - kn[i] * c;
+            r = r + kn[i] * vw;
+            Sh[(int64_t)i * dv + j] = r;
+            o = o + qn[i] * r;
+        };
+        for (int i0 = 0; i0 < dk32; i0 += 32) {
+            float x[32];
+#pragma unroll
+            for (int u = 0; u < 32; u++) x[u] = col[(int64_t)(i0 + u) * dv];
+#pragma unroll
+            for (int u = 0; u < 32; u++) upd(i0 + u, x[u]);
+        }
+        for (int i = dk32; i < dk; i++) upd(i, col[(int64_t)i * dv]);
         Oh[j] = o;
     }
 }
 
-// Per-head chunk workspace (floats): Qn, Kn, KE, CF (forward decay
-// products alpha_0..t), WI = KE*CF, QI = Qn*CF, WG (row weights of the
-// state update) [C][dk] each; L, P [C][C].
-__host__ __device__ constexpr int64_t chunk_ws_floats(int C, int dk) {
-    return 7LL * C * dk + 2LL * C * C;
-}
-
-// flag[h] = 1 when head h's inputs (nk values of each dk-wide array from
+// flag[h] |= 1 when head h's inputs (nk values of each dk-wide array from
 // h*hk, nv of each dv-wide one from h*hv) hold a non-finite value or an
 // alpha outside [0,1]; the later kernels leave such a head as it was.
+// blockIdx.y = head, blockIdx.x strides over the values; flag zeroed before.
 __global__ __launch_bounds__(256) void k_gdn2_check(const float *__restrict__ Q,
                                                     const float *__restrict__ K,
                                                     const float *__restrict__ B,
@@ -132,150 +154,297 @@ __global__ __launch_bounds__(256) void k_gdn2_check(const float *__restrict__ Q,
                                                     const float *__restrict__ W, int64_t hk,
                                                     int64_t hv, int nk, int nv,
                                                     int *__restrict__ flag, uint32_t *err) {
-    const int h = blockIdx.x, tid = threadIdx.x;
-    bool bad = bad_vec(Q + h * hk, nk, tid, 256) || bad_vec(K + h * hk, nk, tid, 256) ||
-               bad_vec(B + h * hk, nk, tid, 256) || bad_vec(A + h * hk, nk, tid, 256) ||
-               bad_alpha(A + h * hk, nk, tid, 256) || bad_vec(V + h * hv, nv, tid, 256) ||
-               bad_vec(W + h * hv, nv, tid, 256);
-    bad = __syncthreads_or(bad);
-    if (tid == 0) {
-        flag[h] = bad ? 1 : 0;
-        if (bad) raise_err(err, EF_NONFINITE_INPUT);
+    const int h = blockIdx.y;
+    const int i0 = blockIdx.x * 256 + threadIdx.x, st = gridDim.x * 256;
+    const float *q = Q + h * hk, *k = K + h * hk, *b = B + h * hk, *a = A + h * hk;
+    const float *v = V + h * hv, *w = W + h * hv;
+    bool bad = false;
+    for (int i = i0; i < nk; i += st)
+        bad |= !isfinite(q[i]) || !isfinite(k[i]) || !isfinite(b[i]) ||
+               !(a[i] >= 0.0f && a[i] <= 1.0f);
+    for (int i = i0; i < nv; i += st) bad |= !isfinite(v[i]) || !isfinite(w[i]);
+    bad = wave_or_i(bad);
+    if (bad && (threadIdx.x & 63) == 0) {
+        atomicOr(&flag[h], 1);
+        raise_err(err, EF_NONFINITE_INPUT);
     }
 }
 
-// (x*cum)*y summed over i in four chains (i % 4 for i < dk & ~3, the tail
-// into chain 0), then (s0+s1)+(s2+s3) (src/gdn2.c:584-599, 702-713); cum =
-// alpha_{s+1} * ... * alpha_t in that order (1 when t == s).
-__device__ __forceinline__ void dots_ts(const float *KEt, const float *Qt, const float *Ks,
-                                        const float *A, int dk, int s, int t, bool want_l,
-                                        float *l_out, float *p_out) {
-    float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f}, ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    const int dk4 = dk & ~3;
-    for (int i = 0; i < dk; i++) {
-        float cum = 1.0f;
-        for (int r = s + 1; r <= t; r++) cum = cum * A[(int64_t)r * dk + i];
-        const int ch = i < dk4 ? (i & 3) : 0;
-        if (want_l) ls[ch] = ls[ch] + (KEt[i] * cum) * Ks[i];
-        ps[ch] = ps[ch] + (Qt[i] * cum) * Ks[i];
-    }
-    *l_out = (ls[0] + ls[1]) + (ls[2] + ls[3]);
-    *p_out = (ps[0] + ps[1]) + (ps[2] + ps[3]);
+// Record of one (head, chunk) in the prefill workspace (floats): CF
+// (forward decay products alpha_0..t), WI = ke*CF, QI = q*CF, WG (row
+// weights of the state update) [C][dk]; L, P [C][C]; and, when the chunk's
+// operands do not fit in LDS, Qn, Kn, KE [C][dk].
+__host__ __device__ constexpr int64_t chunk_rec_floats(int C, int dk) {
+    return 7LL * C * dk + 2LL * C * C;
 }
 
-// Head h's chunk rows start at X + h*hk (dk-wide arrays) / h*hv (dv-wide).
-__global__ __launch_bounds__(256) void k_gdn2_chunk_prep(
-    const float *__restrict__ Q, const float *__restrict__ K, const float *__restrict__ B,
-    const float *__restrict__ A, int64_t hk, int C, int dk, const int *__restrict__ flag,
-    float *__restrict__ ws) {
+// Everything of a chunk that does not depend on the state: one block per
+// (chunk, head), all chunks of a prefill at once. Norms, ke, the decay
+// products and the WY matrices: L[t][s] = (ke_t*cum(t,s)).k_s (t > s),
+// P[t][s] = (q_t*cum(t,s)).k_s (t >= s), cum(t,s) = alpha_{s+1}*...*alpha_t
+// in that order, each a sum in four chains over i % 4 (the tail
+// i >= dk & ~3 into chain 0), then (c0+c1)+(c2+c3) (src/gdn2.c:537-714,
+// 768-788). CL: the chunk's operands live in LDS (C*dk <= CHUNK_LDS),
+// rows at stride dk + 4 so lanes on different rows fall on distinct banks;
+// the decay products are formed once per (s, i) in t order. Otherwise
+// thread (t, s, chain) forms its own products.
+constexpr int CHUNK_LDS = 4096;
+template <bool CL>
+__global__ __launch_bounds__(256) void k_gdn2_prep(const float *__restrict__ Q,
+                                                   const float *__restrict__ K,
+                                                   const float *__restrict__ B,
+                                                   const float *__restrict__ A, int64_t hk,
+                                                   int C, int dk, const int *__restrict__ flag,
+                                                   float *__restrict__ rec) {
     __shared__ float invs[64];
     __shared__ int zeros[64];
-    const int h = blockIdx.x, tid = threadIdx.x;
-    const int64_t Ck = (int64_t)C * dk;
+    __shared__ float part[2][CL ? 2 : 32][32][4];  // [L/P][s (of the pair)][t][chain]
+    constexpr int NL = CL ? CHUNK_LDS + 4 * 32 : 1;
+    __shared__ float a_l[NL], q_l[NL], k_l[NL], e_l[NL];
+    __shared__ float term_l[2][2][CL ? NL : 1];  // [L/P][s of the pair][t][i]
+    const int c = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lk = dk + 4;
     if (flag[h]) return;
-    const float *Qh = Q + h * hk, *Kh = K + h * hk, *Bh = B + h * hk, *Ah = A + h * hk;
-    float *wsh = ws + (int64_t)h * chunk_ws_floats(C, dk);
-    float *Qn = wsh, *Kn = Qn + Ck, *KE = Kn + Ck, *CF = KE + Ck, *WI = CF + Ck, *QI = WI + Ck;
-    float *WG = QI + Ck, *L = WG + Ck, *P = L + (int64_t)C * C;
+    const int64_t Ck = (int64_t)C * dk;
+    const int64_t at0 = h * hk + c * Ck;
+    const float *Qh = Q + at0, *Kh = K + at0, *Bh = B + at0, *Ah = A + at0;
+    float *r = rec + ((int64_t)h * gridDim.x + c) * chunk_rec_floats(C, dk);
+    float *CF = r, *WI = CF + Ck, *QI = WI + Ck, *WG = QI + Ck;
+    float *L = WG + Ck, *P = L + (int64_t)C * C, *Qn = P + (int64_t)C * C, *Kn = Qn + Ck;
+    float *KE = Kn + Ck;
+    if (CL) {  // raw rows into LDS for the norms
+        for (int64_t n = tid; n < Ck; n += 256) {
+            const int t = (int)(n / dk), i = (int)(n % dk);
+            q_l[t * lk + i] = Qh[n];
+            k_l[t * lk + i] = Kh[n];
+            a_l[t * lk + i] = Ah[n];
+        }
+        __syncthreads();
+    }
     if (tid < 2 * C) {  // one row norm per thread
         const int t = tid % C;
         bool z;
-        invs[tid] = inv_norm((tid < C ? Qh : Kh) + (int64_t)t * dk, dk, &z);
+        const float *row = CL ? (tid < C ? q_l : k_l) + t * lk : (tid < C ? Qh : Kh) + (int64_t)t * dk;
+        invs[tid] = inv_norm(row, dk, &z);
         zeros[tid] = z;
     }
     __syncthreads();
     for (int64_t n = tid; n < Ck; n += 256) {
-        const int t = (int)(n / dk);
-        const float qv = zeros[t] ? 0.0f : Qh[n] * invs[t];
-        const float kv = zeros[C + t] ? 0.0f : Kh[n] * invs[C + t];
-        Qn[n] = qv;
-        Kn[n] = kv;
-        KE[n] = Bh[n] * kv;
+        const int t = (int)(n / dk), i = (int)(n % dk), l = t * lk + i;
+        const float qv = zeros[t] ? 0.0f : (CL ? q_l[l] : Qh[n]) * invs[t];
+        const float kv = zeros[C + t] ? 0.0f : (CL ? k_l[l] : Kh[n]) * invs[C + t];
+        const float ev = Bh[n] * kv;
+        if (CL) {
+            q_l[l] = qv;
+            k_l[l] = kv;
+            e_l[l] = ev;
+        } else {
+            Qn[n] = qv;
+            Kn[n] = kv;
+            KE[n] = ev;
+        }
     }
     __syncthreads();
+    const float *Ab = CL ? a_l : Ah, *Eb = CL ? e_l : KE, *Qb = CL ? q_l : Qn;
+    const float *Kb = CL ? k_l : Kn;
+    const int ld = CL ? lk : dk;  // row stride of those operands
     for (int i = tid; i < dk; i += 256) {
         float cf = 1.0f;  // alpha_0 * ... * alpha_t, t ascending
         for (int t = 0; t < C; t++) {
-            cf = cf * Ah[(int64_t)t * dk + i];
+            cf = cf * Ab[t * ld + i];
             CF[(int64_t)t * dk + i] = cf;
-            WI[(int64_t)t * dk + i] = KE[(int64_t)t * dk + i] * cf;
-            QI[(int64_t)t * dk + i] = Qn[(int64_t)t * dk + i] * cf;
+            WI[(int64_t)t * dk + i] = Eb[t * ld + i] * cf;
+            QI[(int64_t)t * dk + i] = Qb[t * ld + i] * cf;
         }
         float sf = 1.0f;  // alpha_{s+1} * ..., accumulated from the end
         for (int s = C - 1; s >= 0; s--) {
-            WG[(int64_t)s * dk + i] = Kn[(int64_t)s * dk + i] * sf;
-            sf = sf * Ah[(int64_t)s * dk + i];
+            WG[(int64_t)s * dk + i] = Kb[s * ld + i] * sf;
+            sf = sf * Ab[s * ld + i];
         }
     }
-    __syncthreads();
-    for (int pr = tid; pr < C * C; pr += 256) {
-        const int t = pr / C, s = pr % C;
-        if (s > t) continue;
-        float l, p;
-        dots_ts(KE + (int64_t)t * dk, Qn + (int64_t)t * dk, Kn + (int64_t)s * dk, Ah, dk, s, t,
-                s < t, &l, &p);
-        L[pr] = s < t ? l : 0.0f;
-        P[pr] = p;
+    const int dk4 = dk & ~3;
+    if (CL) {
+        // two s at a time: thread (s, i) walks t upward forming cum(t,s)[i]
+        // and the two terms of every (t, s) chain element into LDS; then
+        // thread (t, s, chain) sums its chain in i order
+        for (int s0 = 0; s0 < C; s0 += 2) {
+            for (int idx = tid; idx < 2 * dk; idx += 256) {
+                const int sl = idx / dk, i = idx % dk, s = s0 + sl;
+                const float ks = Kb[s * ld + i];
+                float cu = 1.0f;
+                for (int t = s; t < C; t++) {
+                    if (t > s) cu = cu * Ab[t * ld + i];
+                    term_l[0][sl][t * lk + i] = (Eb[t * ld + i] * cu) * ks;
+                    term_l[1][sl][t * lk + i] = (Qb[t * ld + i] * cu) * ks;
+                }
+            }
+            __syncthreads();
+            for (int job = tid; job < 2 * C * 4; job += 256) {
+                const int ch = job & 3, t = (job >> 2) % C, sl = job / (4 * C), s = s0 + sl;
+                if (s > t) continue;
+                const float *tl = term_l[0][sl] + t * lk, *tp = term_l[1][sl] + t * lk;
+                float lsum = 0.0f, psum = 0.0f;
+                for (int i = ch; i < dk4; i += 4) {
+                    lsum = lsum + tl[i];
+                    psum = psum + tp[i];
+                }
+                if (ch == 0)
+                    for (int i = dk4; i < dk; i++) {
+                        lsum = lsum + tl[i];
+                        psum = psum + tp[i];
+                    }
+                part[0][sl][t][ch] = lsum;
+                part[1][sl][t][ch] = psum;
+            }
+            __syncthreads();
+            for (int pr = tid; pr < 2 * C; pr += 256) {
+                const int t = pr % C, sl = pr / C, s = s0 + sl;
+                const float *pl = part[0][sl][t], *pp = part[1][sl][t];
+                L[t * C + s] = s < t ? (pl[0] + pl[1]) + (pl[2] + pl[3]) : 0.0f;
+                P[t * C + s] = s <= t ? (pp[0] + pp[1]) + (pp[2] + pp[3]) : 0.0f;
+            }
+        }
+    } else {
+        for (int job = tid; job < 4 * C * C; job += 256) {
+            const int ch = job & 3, pr = job >> 2, t = pr / C, s = pr % C;
+            if (s > t) continue;
+            const float *ks = Kb + s * ld, *qt = Qb + t * ld, *et = Eb + t * ld;
+            float lsum = 0.0f, psum = 0.0f;
+            auto term = [&](int i) {
+                float cu = 1.0f;
+                for (int rr = s + 1; rr <= t; rr++) cu = cu * Ab[rr * ld + i];
+                lsum = lsum + (et[i] * cu) * ks[i];
+                psum = psum + (qt[i] * cu) * ks[i];
+            };
+            for (int i = ch; i < dk4; i += 4) term(i);
+            if (ch == 0)
+                for (int i = dk4; i < dk; i++) term(i);
+            part[0][s][t][ch] = lsum;
+            part[1][s][t][ch] = psum;
+        }
+        __syncthreads();
+        for (int pr = tid; pr < C * C; pr += 256) {
+            const int t = pr / C, s = pr % C;
+            const float *pl = part[0][s][t], *pp = part[1][s][t];
+            L[pr] = s < t ? (pl[0] + pl[1]) + (pl[2] + pl[3]) : 0.0f;
+            P[pr] = s <= t ? (pp[0] + pp[1]) + (pp[2] + pp[3]) : 0.0f;
+        }
     }
 }
 
-template <int C>
-__global__ __launch_bounds__(64) void k_gdn2_chunk_cols(
-    float *__restrict__ S, float *__restrict__ Out, const float *__restrict__ V,
-    const float *__restrict__ W, int64_t hv, int dk, int dv, const int *__restrict__ flag,
-    const float *__restrict__ ws) {
-    const int h = blockIdx.x, j = blockIdx.y * 64 + threadIdx.x;
+// The state recurrence over all chunks, in order, in one launch: one block
+// per (head, NC = 256/C columns) -- the columns of S never mix. Per chunk,
+// phase 1 thread (t, column) runs the chains over i of
+// B_t = vw_t - sum_i WI[t][i] S[i] and Out_t = sum_i QI[t][i] S[i]; phase 2
+// the forward substitution (I + L) E = B per column with the column's C
+// values in registers; phase 3 Out_t += sum_{s<=t} P[t][s] E_s; phase 4
+// thread (i, column) S[i] <- CF[C-1][i] S[i] + sum_s WG[s][i] E_s
+// (src/gdn2.c:614-680, 716-842). CL: each chunk's record is staged in LDS
+// and the block's S tile stays in LDS from the first chunk to the last.
+template <int C, bool CL>
+__global__ __launch_bounds__(256) void k_gdn2_cols(float *__restrict__ S, float *__restrict__ Out,
+                                                   const float *__restrict__ V,
+                                                   const float *__restrict__ W, int64_t hv,
+                                                   int nch, int dk, int dv,
+                                                   const int *__restrict__ flag,
+                                                   const float *__restrict__ rec) {
+    constexpr int NC = 256 / C;
+    constexpr int NL = CL ? CHUNK_LDS + 4 * 32 : 1;
+    __shared__ float G[C][NC], Ob[C][NC];
+    // the S tile: dk*NC <= CHUNK_LDS*NC/C values when C*dk <= CHUNK_LDS
+    __shared__ float wi_l[NL], qi_l[NL], wg_l[NL], s_l[CL ? CHUNK_LDS * NC / C : 1];
+    __shared__ float lp_l[CL ? 2 * C * C : 1], cf_l[CL ? 1024 : 1];
+    const int h = blockIdx.x, j0 = blockIdx.y * NC, tid = threadIdx.x, lk = dk + 4;
+    if (flag[h]) return;  // a rejected head keeps its S and Out
     const int64_t Ck = (int64_t)C * dk;
-    const float *wsh = ws + (int64_t)h * chunk_ws_floats(C, dk);
-    const float *CF = wsh + 3 * Ck, *WI = CF + Ck, *QI = WI + Ck, *WG = QI + Ck;
-    const float *L = WG + Ck, *P = L + C * C;
-    if (flag[h] || j >= dv) return;  // a rejected head keeps its S and Out
-    float *col = S + (int64_t)h * dk * dv + j;
-    const float *Vh = V + h * hv, *Wh = W + h * hv;
-    float g[C], o[C];
-#pragma unroll
-    for (int t = 0; t < C; t++) {
-        g[t] = Wh[(int64_t)t * dv + j] * Vh[(int64_t)t * dv + j];  // vw_t
-        o[t] = 0.0f;
-    }
-    // B_t = vw_t - sum_i WI[t][i] S[i], Out_t = sum_i QI[t][i] S[i] (i ascending)
-    for (int i = 0; i < dk; i++) {
-        const float sv = col[(int64_t)i * dv];
-#pragma unroll
-        for (int t = 0; t < C; t++) {
-            g[t] = g[t] - WI[(int64_t)t * dk + i] * sv;
-            o[t] = o[t] + QI[(int64_t)t * dk + i] * sv;
+    float *Sh = S + (int64_t)h * dk * dv;
+    const int ncol = min(NC, dv - j0);
+    const int t = tid / NC, jj = tid % NC, j = j0 + jj;
+    const bool live = jj < ncol;
+    const int ld = CL ? lk : dk;
+    if (CL) {
+        for (int n = tid; n < dk * NC; n += 256) {
+            const int i = n / NC, cc = n % NC;
+            s_l[n] = cc < ncol ? Sh[(int64_t)i * dv + j0 + cc] : 0.0f;
         }
     }
-    // (I + L) E = B
+    for (int c = 0; c < nch; c++) {
+        const float *r = rec + ((int64_t)h * nch + c) * chunk_rec_floats(C, dk);
+        const float *CF = r, *WI = CF + Ck, *QI = WI + Ck, *WG = QI + Ck;
+        const float *L = WG + Ck, *P = L + C * C;
+        if (CL) {
+            for (int64_t n = tid; n < Ck; n += 256) {
+                const int tt = (int)(n / dk), i = (int)(n % dk);
+                wi_l[tt * lk + i] = WI[n];
+                qi_l[tt * lk + i] = QI[n];
+                wg_l[tt * lk + i] = WG[n];
+            }
+            for (int n = tid; n < 2 * C * C; n += 256) lp_l[n] = L[n];  // L then P
+            for (int i = tid; i < dk; i += 256) cf_l[i] = CF[(int64_t)(C - 1) * dk + i];
+            __syncthreads();
+        }
+        const float *wi_b = CL ? wi_l : WI, *qi_b = CL ? qi_l : QI, *wg_b = CL ? wg_l : WG;
+        const float *L_b = CL ? lp_l : L, *P_b = CL ? lp_l + C * C : P;
+        const int64_t vo = h * hv + ((int64_t)c * C + t) * dv + j;
+        if (live) {
+            float g = W[vo] * V[vo];  // vw_t
+            float o = 0.0f;
+            const float *wi = wi_b + t * ld, *qi = qi_b + t * ld;
+#pragma unroll 8
+            for (int i = 0; i < dk; i++) {
+                const float sv = CL ? s_l[i * NC + jj] : Sh[(int64_t)i * dv + j];
+                g = g - wi[i] * sv;
+                o = o + qi[i] * sv;
+            }
+            G[t][jj] = g;
+            Ob[t][jj] = o;
+        }
+        __syncthreads();
+        if (tid < ncol) {
+            float g[C];
 #pragma unroll
-    for (int t = 1; t < C; t++)
+            for (int tt = 0; tt < C; tt++) g[tt] = G[tt][tid];
 #pragma unroll
-        for (int s = 0; s < t; s++) g[t] = g[t] - L[t * C + s] * g[s];
-    float *Oh = Out + h * hv + j;
+            for (int tt = 1; tt < C; tt++)
 #pragma unroll
-    for (int t = 0; t < C; t++) {
-        float ot = o[t];
+                for (int s = 0; s < tt; s++) g[tt] = g[tt] - L_b[tt * C + s] * g[s];
 #pragma unroll
-        for (int s = 0; s <= t; s++) ot = ot + P[t * C + s] * g[s];
-        Oh[(int64_t)t * dv] = ot;
+            for (int tt = 0; tt < C; tt++) G[tt][tid] = g[tt];
+        }
+        __syncthreads();
+        if (live) {
+            float o = Ob[t][jj];
+            for (int s = 0; s <= t; s++) o = o + P_b[t * C + s] * G[s][jj];
+            Out[vo] = o;
+        }
+        for (int idx = tid; idx < dk * NC; idx += 256) {
+            const int i = idx / NC, cc = idx % NC;
+            if (cc >= ncol) continue;
+            float *sp = Sh + (int64_t)i * dv + j0 + cc;
+            float rv = (CL ? s_l[idx] : *sp) * (CL ? cf_l[i] : CF[(int64_t)(C - 1) * dk + i]);
+#pragma unroll 8
+            for (int s = 0; s < C; s++) rv = rv + wg_b[s * ld + i] * G[s][cc];
+            if (CL)
+                s_l[idx] = rv;
+            else
+                *sp = rv;
+        }
+        __syncthreads();
     }
-    // S <- CF[C-1] * S + sum_s WG[s] E_s
-    for (int i = 0; i < dk; i++) {
-        float r = col[(int64_t)i * dv] * CF[(int64_t)(C - 1) * dk + i];
-#pragma unroll
-        for (int s = 0; s < C; s++) r = r + WG[(int64_t)s * dk + i] * g[s];
-        col[(int64_t)i * dv] = r;
+    if (CL) {
+        for (int n = tid; n < dk * NC; n += 256) {
+            const int i = n / NC, cc = n % NC;
+            if (cc < ncol) Sh[(int64_t)i * dv + j0 + cc] = s_l[n];
+        }
     }
 }
 
 }  // namespace
 
-// Workspace of jtk_gdn2_prefill: H flag words (padded to 64 floats) and the
-// per-head chunk area.
-extern "C" size_t jtk_gdn2_chunk_ws_bytes(int H, int C, int dk) {
+// Workspace of jtk_gdn2_prefill: H flag words (padded to 64 floats) and one
+// record per (head, chunk).
+extern "C" size_t jtk_gdn2_prefill_ws_bytes(int H, int T, int C, int dk) {
     const int64_t flags = ((int64_t)H + 63) / 64 * 64;
-    return (size_t)(flags + (int64_t)H * chunk_ws_floats(C, dk)) * sizeof(float);
+    return (size_t)(flags + (int64_t)H * (T / C) * chunk_rec_floats(C, dk)) * sizeof(float);
 }
 
 // H heads, one decode step each. dk, dv in 1..1024.
@@ -284,39 +453,54 @@ extern "C" int jtk_gdn2_decode(float *S, float *O, const float *q, const float *
                                const float *alpha, int H, int dk, int dv, uint32_t *err,
                                hipStream_t s) {
     if (H <= 0 || dk <= 0 || dv <= 0 || dk > 1024 || dv > 1024) return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_gdn2_decode, dim3((unsigned)H), dim3(256), 0, s, S, O, q, k, v, b, w,
+    const unsigned nt = (unsigned)(dv >= 256 ? 256 : (dv + 63) / 64 * 64);
+    hipLaunchKernelGGL(k_gdn2_decode, dim3((unsigned)H), dim3(nt), 0, s, S, O, q, k, v, b, w,
                        alpha, dk, dv, err);
     return (int)hipGetLastError();
 }
 
-// H heads, T tokens each in T/C chunks of C (16 or 32), in order: head h's
-// rows of the dk-wide inputs start at h*hk, of V, W and Out at h*hv; all
-// of a head's T tokens are checked first, and a head with a bad value keeps
-// its S and Out. ws of jtk_gdn2_chunk_ws_bytes(H, C, dk).
+// H heads, T tokens each in T/C chunks of C (16 or 32): head h's rows of
+// the dk-wide inputs start at h*hk, of V, W and Out at h*hv. All of a
+// head's T tokens are checked first (a head with a bad value keeps its S
+// and Out), every chunk's state-independent part is prepared in one
+// launch, then one launch runs the chunks' state updates in order. ws of
+// jtk_gdn2_prefill_ws_bytes(H, T, C, dk).
 extern "C" int jtk_gdn2_prefill(float *S, float *Out, const float *Q, const float *K,
                                 const float *V, const float *B, const float *W,
                                 const float *A, int64_t hk, int64_t hv, int H, int T, int C,
                                 int dk, int dv, float *ws, uint32_t *err, hipStream_t s) {
-    if (H <= 0 || (C != 16 && C != 32) || T <= 0 || T % C || dk <= 0 || dv <= 0 ||
+    if (H <= 0 || H > 65535 || (C != 16 && C != 32) || T <= 0 || T % C || dk <= 0 || dv <= 0 ||
         dk > 1024 || dv > 1024 || (int64_t)T * (dk > dv ? dk : dv) > INT32_MAX)
         return (int)hipErrorInvalidValue;
+    const int nch = T / C;
     int *flag = (int *)ws;
-    float *cw = ws + ((int64_t)H + 63) / 64 * 64;
-    hipLaunchKernelGGL(k_gdn2_check, dim3((unsigned)H), dim3(256), 0, s, Q, K, B, A, V, W, hk,
-                       hv, T * dk, T * dv, flag, err);
-    const dim3 grid((unsigned)H, (unsigned)((dv + 63) / 64));
-    for (int c0 = 0; c0 < T; c0 += C) {
-        const int64_t ok = (int64_t)c0 * dk, ov = (int64_t)c0 * dv;
-        hipLaunchKernelGGL(k_gdn2_chunk_prep, dim3((unsigned)H), dim3(256), 0, s, Q + ok, K + ok,
-                           B + ok, A + ok, hk, C, dk, flag, cw);
-        if (C == 16)
-            hipLaunchKernelGGL(k_gdn2_chunk_cols<16>, grid, dim3(64), 0, s, S, Out + ov, V + ov,
-                               W + ov, hv, dk, dv, flag, cw);
-        else
-            hipLaunchKernelGGL(k_gdn2_chunk_cols<32>, grid, dim3(64), 0, s, S, Out + ov, V + ov,
-                               W + ov, hv, dk, dv, flag, cw);
-    }
-    return (int)hipGetLastError();
+    float *rec = ws + ((int64_t)H + 63) / 64 * 64;
+    int le = jtk_zero_u32((uint32_t *)flag, H, s);
+    const int64_t most = (int64_t)T * (dk > dv ? dk : dv);
+    const unsigned nb = (unsigned)((most + 255) / 256 < 64 ? (most + 255) / 256 : 64);
+    hipLaunchKernelGGL(k_gdn2_check, dim3(nb, (unsigned)H), dim3(256), 0, s, Q, K, B, A, V, W,
+                       hk, hv, T * dk, T * dv, flag, err);
+    const bool cl = (int64_t)C * dk <= CHUNK_LDS;
+    if (cl)
+        hipLaunchKernelGGL(k_gdn2_prep<true>, dim3((unsigned)nch, (unsigned)H), dim3(256), 0, s,
+                           Q, K, B, A, hk, C, dk, flag, rec);
+    else
+        hipLaunchKernelGGL(k_gdn2_prep<false>, dim3((unsigned)nch, (unsigned)H), dim3(256), 0, s,
+                           Q, K, B, A, hk, C, dk, flag, rec);
+    const dim3 grid((unsigned)H, (unsigned)((dv + 256 / C - 1) / (256 / C)));
+    if (C == 16 && cl)
+        hipLaunchKernelGGL((k_gdn2_cols<16, true>), grid, dim3(256), 0, s, S, Out, V, W, hv, nch,
+                           dk, dv, flag, rec);
+    else if (C == 16)
+        hipLaunchKernelGGL((k_gdn2_cols<16, false>), grid, dim3(256), 0, s, S, Out, V, W, hv, nch,
+                           dk, dv, flag, rec);
+    else if (cl)
+        hipLaunchKernelGGL((k_gdn2_cols<32, true>), grid, dim3(256), 0, s, S, Out, V, W, hv, nch,
+                           dk, dv, flag, rec);
+    else
+        hipLaunchKernelGGL((k_gdn2_cols<32, false>), grid, dim3(256), 0, s, S, Out, V, W, hv, nch,
+                           dk, dv, flag, rec);
+    return le | (int)hipGetLastError();
 }
 
 // y = x / ||x|| (the reference's l2norm) for R rows of n.

@@ -185,7 +185,7 @@ int jtk_bwd_batch(const jtk_bwd_io *io, int T, int n, int h, int E, int k, int S
 int jtk_gdn2_decode(float *S, float *O, const float *q, const float *k, const float *v,
                     const float *b, const float *w, const float *alpha, int H, int dk, int dv,
                     uint32_t *err, hipStream_t s);
-size_t jtk_gdn2_chunk_ws_bytes(int H, int C, int dk);
+size_t jtk_gdn2_prefill_ws_bytes(int H, int T, int C, int dk);
 /* T tokens per head (T % C == 0) in T/C chunks; a head with a bad input
  * value anywhere keeps its S and Out (EF_NONFINITE_INPUT). */
 int jtk_gdn2_prefill(float *S, float *Out, const float *Q, const float *K, const float *V,

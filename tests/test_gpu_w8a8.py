@@ -202,6 +202,30 @@ def test_device_prepare_from_fp32(jt, orc, torch_cuda):
     assert np.array_equal(bits(out.cpu().numpy()), bits(C2))
 
 
+@pytest.mark.parametrize("N,K", [(4096, 1024), (200, 100), (130, 64)])
+def test_device_projection_fp32_activations(jt, orc, torch_cuda, N, K):
+    """The per-token INT8 projection (jt_hip_w8a8_gemm_f32): fp32 rows
+    quantised inside the call, bit-identical to quant_rows + the GEMM, for
+    the in-block quantiser (M <= 16) and the workspace path (M > 16); K not
+    a multiple of 64 meets the zero-padded weight panels."""
+    torch = torch_cuda
+    announce(f"device w8a8 projection N={N} K={K}")
+    rng = np.random.default_rng(N + K)
+    Wf = (rng.standard_normal((N, K)) / np.sqrt(K)).astype(np.float32)
+    W = jt.W8A8(W=torch.from_numpy(Wf).cuda())
+    _, Qw, sw = orc.quant_rows(Wf)
+    ws = None
+    for M in (1, 5, 16, 17, 64, 300):
+        X = rng.standard_normal((M, K)).astype(np.float32)
+        X[0, : K // 2] *= 50.0
+        out = torch.full((M, N), np.nan, device="cuda")
+        ws = W.gemm_f32(torch.from_numpy(X).cuda(), out, ws=ws)
+        assert jt.sync_errors() == 0
+        _, Qx, sx = orc.quant_rows(X)
+        rc, C2, _ = orc.w8a8_gemm(Qx, sx, Qw.T.copy(), sw)
+        assert rc == 0 and np.array_equal(bits(out.cpu().numpy()), bits(C2)), M
+
+
 def test_fail_closed(jt):
     announce("w8a8 fail-closed cases")
     Aq = np.ones((4, 16), np.int8)
