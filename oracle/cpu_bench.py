@@ -18,6 +18,7 @@ int32 accumulators.
 """
 from __future__ import annotations
 
+import ctypes
 import os
 import time
 
@@ -201,11 +202,89 @@ def bwd_batch(R, seconds, T, n, h, E, k, S, max_tokens=None, seed=3):
             "tokens_per_s": tok / med}
 
 
+def gdn2_decode(R, seconds, H=512, dk=128, dv=128, sample=64, seed=7):
+    """jt_gdn2_decode_step of the reference on `sample` of the H heads (one
+    call per head, states 64-byte aligned); the heads are independent, so
+    the time scales to H."""
+    rng = np.random.default_rng(seed)
+    L = R.lib
+    states = []
+    for _ in range(sample):
+        p = ctypes.c_void_p()
+        assert L.jt_gdn2_state_alloc(ctypes.byref(p), dk, dv) == 0
+        S = (rng.standard_normal(dk * dv) * 0.3).astype(np.float32)
+        ctypes.memmove(p, S.ctypes.data, S.nbytes)
+        states.append(p)
+    vec = lambda n, lo=None: (rng.uniform(lo, 1.0, n) if lo is not None  # noqa: E731
+                              else rng.standard_normal(n)).astype(np.float32)
+    q, k, b, a = vec(dk), vec(dk), vec(dk, 0.0), vec(dk, 0.9)
+    v, w, o = vec(dv), vec(dv, 0.0), np.zeros(dv, np.float32)
+    scratch = np.zeros(2 * dk + 2 * dv, np.float32)
+
+    def run():
+        for p in states:
+            L.jt_gdn2_decode_step(p, o, q, k, v, b, w, a, dk, dv, scratch, scratch.size)
+    med, mad, nt = trials(run, seconds)
+    for p in states:
+        L.jt_gdn2_state_free(p)
+    return {"heads_timed": sample, "us_per_head": med / sample * 1e6,
+            "us_per_step_all_heads": med / sample * H * 1e6, "trials": nt,
+            "gbps": H * 2 * dk * dv * 4 / (med / sample * H) / 1e9}
+
+
+def gdn2_prefill(R, seconds, T=4096, C=32, dk=128, dv=128, H=8, chunks=8, seed=8):
+    """jt_gdn2_prefill_chunk32 of the reference on `chunks` consecutive
+    chunks of one head; chunks cost the same, so tokens/s carries to T and
+    H heads."""
+    rng = np.random.default_rng(seed)
+    L = R.lib
+    p = ctypes.c_void_p()
+    assert L.jt_gdn2_state_alloc(ctypes.byref(p), dk, dv) == 0
+    f = lambda *sh: rng.standard_normal(sh).astype(np.float32)  # noqa: E731
+    Q, K = f(chunks, C, dk), f(chunks, C, dk)
+    B = rng.uniform(0, 1, (chunks, C, dk)).astype(np.float32)
+    A = rng.uniform(0.9, 1, (chunks, C, dk)).astype(np.float32)
+    V, W = f(chunks, C, dv), rng.uniform(0, 1, (chunks, C, dv)).astype(np.float32)
+    Out = np.zeros((C, dv), np.float32)
+    need = 4 * C * dk + 2 * C * dv + C * C + dk
+    scratch = np.zeros(need, np.float32)
+
+    def run():
+        for c in range(chunks):
+            L.jt_gdn2_prefill_chunk32(p, Out, Q[c], K[c], V[c], B[c], W[c], A[c], dk, dv,
+                                      scratch, need)
+    med, mad, nt = trials(run, seconds, min_trials=1)
+    L.jt_gdn2_state_free(p)
+    per_tok = med / (chunks * C)
+    return {"chunks_timed": chunks, "ms_per_chunk": med / chunks * 1e3, "trials": nt,
+            "tokens_per_s_one_head": 1.0 / per_tok, "tokens_per_s": 1.0 / per_tok / H}
+
+
+def attn_proj(R, seconds, M, N=3072, K=1024, sample=16, seed=9):
+    """The INT8 projection of M fp32 rows: per row jt_w8a8_quant_per_channel
+    and jt_w8a8_gemm_per_channel (its sA is one float per call), weights
+    quantised once; `sample` rows timed when M is larger."""
+    rng = np.random.default_rng(seed)
+    W = (rng.standard_normal((N, K)) / 32).astype(np.float32)
+    _, qw, sw = R.quant_rows(W)
+    Bq = np.ascontiguousarray(qw.T)
+    m = min(M, sample)
+    X = rng.standard_normal((m, K)).astype(np.float32)
+
+    def run():
+        _, Xq, sx = R.quant_rows(X)
+        for r in range(m):
+            R.gemm_per_channel(Xq[r:r + 1], Bq, float(sx[r]), sw)
+    med, mad, nt = trials(run, seconds)
+    return {"rows_timed": m, "us_per_call": med / m * M * 1e6, "trials": nt}
+
+
 def decode_and_stress(seconds):
     """The W8A8 GEMM 64x1024x1024, the shared-expert decode at 1, 4 and 16
     rows, the routed decode at 16 tokens, a token sample of the E=512
-    stress shape and the batched backward (training shape; a token sample of
-    the layer shape), on one pinned core, for the default reference build
+    stress shape, the batched backward (training shape; a token sample of
+    the layer shape), the GDN-2 decode step and prefill and the INT8
+    attention projection, on one pinned core, for the default reference build
     and (for the W8A8 shapes) its VNNI form when the host can run one."""
     if not ref_available():
         return {"error": "oracle/_ref not built"}
@@ -231,5 +310,9 @@ def decode_and_stress(seconds):
                 res["moe_bwd_T512_train"] = bwd_batch(R, seconds, 512, 64, 32, 8, 2, 1)
                 res["moe_bwd_T4096_layer"] = bwd_batch(R, seconds, 4096, 1024, 256, 64, 8, 1,
                                                        max_tokens=512)
+                res["gdn2_decode_H512"] = gdn2_decode(R, seconds)
+                res["gdn2_prefill_T4096_H8"] = gdn2_prefill(R, seconds)
+            for m in (1, 16, 4096):
+                res[f"attn_proj_int8_M{m}"] = attn_proj(R, seconds, m)
             out[name] = res
     return out
