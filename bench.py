@@ -53,6 +53,10 @@ def parse():
                    help="run only the full decode-layer sub-benchmark (T=16, router, "
                         "two shared and 256 routed experts) and print its JSON line; "
                         "the workload of the decode kernel-trace profile")
+    p.add_argument("--only", choices=["w8a8_64", "shared_decode", "routed_decode", "stress",
+                                      "bwd", "gdn2", "proj"],
+                   help="run one of the other shapes' benchmarks alone and print its JSON "
+                        "(the workloads of their kernel-trace profiles)")
     p.add_argument("--copy-probe", action="store_true",
                    help="also run a plain 256 MiB device copy (the reference kernel "
                         "for scaling HBM byte counters)")
@@ -110,6 +114,9 @@ def main():
     if args.decode_only:
         print(json.dumps({"decode_layer_T16": decode_layer(torch, api, stream, args.steps,
                                                            args.warmup)}), flush=True)
+        return
+    if args.only:
+        print(json.dumps(sub_benchmarks(np, torch, api, stream, only=args.only)), flush=True)
         return
 
     # ---------------- main workload: full layer prefill ----------------
@@ -403,9 +410,32 @@ def decode_layer(torch, api, stream, steps, warmup):
             "hbm_frac": wbytes / (ev / 1e3) / HBM_PEAK}
 
 
-def sub_benchmarks(np, torch, api, stream):
+def sub_benchmarks(np, torch, api, stream, only=None):
     res = {}
-    # --- W8A8 GEMM 64x1024x1024 (per-row activation scales) ---
+    want = lambda name: only is None or only == name  # noqa: E731
+    if want("w8a8_64"):
+        res.update(w8a8_64_bench(np, torch, api, stream))
+    if want("shared_decode"):
+        res.update(shared_decode_bench(np, torch, api, stream))
+    if want("routed_decode"):
+        res.update(routed_decode_bench(np, torch, api, stream))
+    if only is None:
+        res["decode_layer_T16"] = decode_layer(torch, api, stream, 10, 2)
+    if want("stress"):
+        res.update(stress_bench(np, torch, api, stream))
+    if want("bwd"):
+        for name, shape in BWD_SHAPES.items():
+            res[name] = bwd_bench(np, torch, api, stream, *shape)
+    if want("gdn2"):
+        res.update(gdn2_bench(np, torch, api, stream))
+    if want("proj"):
+        res.update(proj_bench(np, torch, api, stream))
+    return res
+
+
+def w8a8_64_bench(np, torch, api, stream):
+    """W8A8 GEMM 64x1024x1024 with per-row activation scales."""
+    res = {}
     M, N, K = 64, 1024, 1024
     g = torch.Generator(device="cuda").manual_seed(5)
     Bq = torch.randint(-127, 128, (K, N), generator=g, device="cuda", dtype=torch.int8)
@@ -420,8 +450,13 @@ def sub_benchmarks(np, torch, api, stream):
                                      "gbps": (M * K + N * K + 4 * (M + N) + 4 * M * N)
                                      / (ev / 1e3) / 1e9}
     del Wq
-    # --- shared-expert decode, M in {1,4,16}; 40 rotating weight copies
-    # (> 256 MB MALL) so every call streams its weights from HBM ---
+    return res
+
+
+def shared_decode_bench(np, torch, api, stream):
+    """Shared-expert decode, M in {1,4,16}; 40 rotating weight copies
+    (> 256 MB MALL) so every call streams its weights from HBM."""
+    res = {}
     n, hs = 1024, 2816
     copies = 40
     Fs = []
@@ -445,7 +480,12 @@ def sub_benchmarks(np, torch, api, stream):
                                       "hbm_frac": (wbytes + 8 * m * n) / (ev / 1e3) / HBM_PEAK}
     del Fs
     torch.cuda.empty_cache()
-    # --- routed decode: T=16, E=256, d=1024, f=256, k=8, Zipf(1.1) ---
+    return res
+
+
+def routed_decode_bench(np, torch, api, stream):
+    """Routed decode: T=16, E=256, d=1024, f=256, k=8, Zipf(1.1) ids given."""
+    res = {}
     n, h, E, k, T = 1024, 256, 256, 8, 16
     rng = np.random.default_rng(16)
     p = 1.0 / np.arange(1, E + 1) ** 1.1
@@ -476,9 +516,13 @@ def sub_benchmarks(np, torch, api, stream):
                                 "hbm_frac": rbytes / (ev / 1e3) / HBM_PEAK}
     del layers
     torch.cuda.empty_cache()
-    # --- full decode layer: router, two shared and the routed experts ---
-    res["decode_layer_T16"] = decode_layer(torch, api, stream, 10, 2)
-    # --- stress prefill: T=16384, d=2048, E=512, f=512, k=8, Zipf(1.1) ---
+    return res
+
+
+def stress_bench(np, torch, api, stream):
+    """Stress prefill: T=16384, d=2048, E=512, f=512, k=8, Zipf(1.1) ids."""
+    res = {}
+    rng = np.random.default_rng(1616)
     n, h, E, k, T = 2048, 512, 512, 8, 16384
     ids = np.stack([rng.choice(E, k, replace=False, p=(1.0 / np.arange(1, E + 1) ** 1.1)
                                / (1.0 / np.arange(1, E + 1) ** 1.1).sum())
@@ -503,12 +547,6 @@ def sub_benchmarks(np, torch, api, stream):
                                   "stages_ms": {s: v / cnt for s, v in st.items()}}
     del Ls
     torch.cuda.empty_cache()
-    # --- batched backward (fp32, bit-exact to the reference's) ---
-    for name, shape in BWD_SHAPES.items():
-        res[name] = bwd_bench(np, torch, api, stream, *shape)
-    # --- Gated DeltaNet-2 and the INT8 attention projections ---
-    res.update(gdn2_bench(np, torch, api, stream))
-    res.update(proj_bench(np, torch, api, stream))
     return res
 
 

@@ -17,9 +17,11 @@
  * on that stream. Arguments are validated on the host before anything is
  * enqueued (JT_ERR_INVAL, nothing written). Data-dependent failures found by
  * the kernels (a non-finite activation, an overflowing epilogue) raise bits in
- * the library's device error word (one per process, shared by every stream)
- * instead of a partial result being trusted; jt_hip_sync_errors() waits for
- * a stream and returns (and clears) the bits raised so far by any stream.
+ * the device error word of the stream the call was made on (each stream has
+ * its own word, so one caller never reads another stream's bits; past 63
+ * distinct streams the rest share one word) instead of a partial result
+ * being trusted; jt_hip_sync_errors() waits for a stream and returns (and
+ * clears) the bits raised so far by calls on that stream.
  *
  * Formats of a prepared layer (built on the GPU from fp32 weights):
  *  - shared experts: int8 codes, one fp32 scale per output channel (the
@@ -48,7 +50,7 @@ extern "C" {
  * every other entry point with device 0). */
 int jt_hip_init(int device);
 /* Wait for `stream` (NULL: for the whole device), then read and clear the
- * library's device error word.
+ * device error word of `stream` (NULL: of the null stream).
  * *out_flags gets the raised JT_HIP_EF_* bits (0 = clean). Returns JT_OK, or
  * JT_ERR_IO on a HIP failure. */
 int jt_hip_sync_errors(void *stream, uint32_t *out_flags);
@@ -99,9 +101,16 @@ void jt_hip_w8a8_free(jt_hip_w8a8 *W);
 typedef struct jt_hip_ffn jt_hip_ffn;
 int jt_hip_ffn_prepare(const float *dWg, const float *dWu, const float *dWd,
                        int n, int h, jt_hip_ffn **out);
-/* dY [T][n] = the expert output for dX [T][n] (fp32). */
+/* dY [T][n] = the expert output for dX [T][n] (fp32). The expert's own
+ * workspace grows to the largest T seen: a call with more rows than reserved
+ * waits for the whole device, frees and reallocates before it enqueues
+ * anything (jt_hip_ffn_reserve does that ahead of time). */
 int jt_hip_ffn_fwd(jt_hip_ffn *F, const float *dX, float *dY, int T,
                    void *stream);
+/* Size the expert's own workspace for T rows now (synchronous; T > 0), so
+ * that later jt_hip_ffn_fwd calls of at most T rows neither allocate nor
+ * synchronise (for serving loops and HIP graph capture). */
+int jt_hip_ffn_reserve(jt_hip_ffn *F, int T);
 /* jt_hip_ffn_fwd that allocates nothing. No counterpart in the reference:
  * it is for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).

@@ -78,6 +78,7 @@ _PROTOS = {
     "jt_hip_ffn_prepare": [_vp, _vp, _vp, _i, _i, C.POINTER(_vp)],
     "jt_hip_ffn_fwd": [_vp, _vp, _vp, _i, _vp],
     "jt_hip_ffn_fwd_noalloc": [_vp, _vp, _vp, _i, _vp],
+    "jt_hip_ffn_reserve": [_vp, _i],
     "jt_hip_ffn_free": ([_vp], None),
     "jt_hip_moe_prepare": [C.POINTER(_Desc)] + [_vp] * 7 + [C.POINTER(_vp)],
     "jt_hip_moe_fwd": [_vp, _vp, _vp, _i, _vp],
@@ -565,6 +566,10 @@ class FFN:
     def fwd(self, X, Y, stream=None):
         _check(lib().jt_hip_ffn_fwd(self.h, _ptr(X), _ptr(Y), X.shape[0], _stream(stream)),
                "jt_hip_ffn_fwd")
+
+    def reserve(self, T):
+        """jt_hip_ffn_reserve: size the own workspace for T rows now."""
+        _check(lib().jt_hip_ffn_reserve(self.h, T), "jt_hip_ffn_reserve")
 
     def fwd_noalloc(self, X, Y, stream=None):
         """jt_hip_ffn_fwd_noalloc: the same forward on the library's fixed

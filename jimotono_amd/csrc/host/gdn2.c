@@ -125,7 +125,7 @@ int jt_gdn2_decode_step(float *S, float *out_o, const float *q, const float *k,
     int rc = stage_in(rt, st, 8, JT_SLOT_A);
     if (rc != JT_OK) return rc;
     if (jtk_gdn2_decode(st[0].dev, st[7].dev, st[1].dev, st[2].dev, st[5].dev, st[3].dev,
-                        st[6].dev, st[4].dev, 1, dk, dv, rt->d_err, rt->stream) != 0)
+                        st[6].dev, st[4].dev, 1, dk, dv, jt_rt_errw(rt, rt->stream), rt->stream) != 0)
         return jt_rt_err(hipErrorLaunchFailure);
     uint32_t f = 0;
     if ((rc = jt_rt_flags(rt, rt->stream, &f)) != JT_OK) return rc;
@@ -152,7 +152,7 @@ static int prefill_chunk(float *S, float *Out, const float *Q, const float *K, c
     int rc = stage_in(rt, st, 9, JT_SLOT_A);
     if (rc != JT_OK) return rc;
     if (jtk_gdn2_prefill(st[0].dev, st[7].dev, st[1].dev, st[2].dev, st[5].dev, st[3].dev,
-                         st[6].dev, st[4].dev, 0, 0, 1, C, C, dk, dv, st[8].dev, rt->d_err,
+                         st[6].dev, st[4].dev, 0, 0, 1, C, C, dk, dv, st[8].dev, jt_rt_errw(rt, rt->stream),
                          rt->stream) != 0)
         return jt_rt_err(hipErrorLaunchFailure);
     uint32_t f = 0;
@@ -185,7 +185,7 @@ int jt_hip_gdn2_decode(float *dS, float *dO, const float *dq, const float *dk_,
     if (!dims_ok(dk, dv)) FAIL(JT_ERR_INVAL, EINVAL);
     jt_rt *rt = jt_rt_get();
     if (!rt) return JT_ERR_IO;
-    return jtk_gdn2_decode(dS, dO, dq, dk_, dv_, db, dw, dalpha, H, dk, dv, rt->d_err,
+    return jtk_gdn2_decode(dS, dO, dq, dk_, dv_, db, dw, dalpha, H, dk, dv, jt_rt_errw(rt, (hipStream_t)stream),
                            (hipStream_t)stream)
                ? jt_rt_err(hipErrorLaunchFailure)
                : JT_OK;
@@ -210,7 +210,7 @@ int jt_hip_gdn2_prefill(float *dS, float *dOut, const float *dQ, const float *dK
     jt_rt *rt = jt_rt_get();
     if (!rt) return JT_ERR_IO;
     return jtk_gdn2_prefill(dS, dOut, dQ, dK, dV, dB, dW, dA, (int64_t)T * dk, (int64_t)T * dv,
-                            H, T, C, dk, dv, (float *)d_ws, rt->d_err, (hipStream_t)stream)
+                            H, T, C, dk, dv, (float *)d_ws, jt_rt_errw(rt, (hipStream_t)stream), (hipStream_t)stream)
                ? jt_rt_err(hipErrorLaunchFailure)
                : JT_OK;
 }

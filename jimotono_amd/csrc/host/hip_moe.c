@@ -107,13 +107,13 @@ static int ffn_prepare_on(jt_rt *rt, const float *dWg, const float *dWu, const f
     rc = jt_rt_err(e);
     if (rc == JT_OK) {
         /* gate/up rows are output channels, K = n contiguous */
-        jtk_quant_weight_rows(dWg, n, 1, h, n, qg, sg, rt->d_err, rt->stream);
-        jtk_quant_weight_rows(dWu, n, 1, h, n, qu, su, rt->d_err, rt->stream);
+        jtk_quant_weight_rows(dWg, n, 1, h, n, qg, sg, jt_rt_errw(rt, rt->stream), rt->stream);
+        jtk_quant_weight_rows(dWu, n, 1, h, n, qu, su, jt_rt_errw(rt, rt->stream), rt->stream);
         jtk_interleave_rows(qg, qu, h, n, qgu, rt->stream);
         jtk_interleave_rows(sg, su, h, (int64_t)sizeof(float), F->gu_s, rt->stream);
         jtk_pack_i8(qgu, 2 * h, n, 0, F->Np_gu, F->Kpn, F->gu_P, rt->stream);
         /* down: Wd [h][n] is B[K=h][N=n]; output channel j is column j */
-        jtk_quant_weight_rows(dWd, 1, n, n, h, qd, F->d_s, rt->d_err, rt->stream);
+        jtk_quant_weight_rows(dWd, 1, n, n, h, qd, F->d_s, jt_rt_errw(rt, rt->stream), rt->stream);
         jtk_pack_i8(qd, n, h, 0, F->Np_d, F->Kph, F->d_P, rt->stream);
         uint32_t f = 0;
         rc = jt_rt_flags(rt, rt->stream, &f);
@@ -186,22 +186,22 @@ static ffn_ws ffn_own_ws(const jt_hip_ffn *F) {
 }
 
 /* Expert on already-quantised activations Xq [T][Kpn] (zero K padding). */
-static int ffn_run_q(jt_rt *rt, const jt_hip_ffn *F, const ffn_ws *ws, const int8_t *Xq,
-                     const float *sx, int T, float *dY, hipStream_t s, hipEvent_t *ev) {
-    if (ev) (void)hipEventRecord(ev[0], s);
-    int e = jtk_w8a8_gemm(Xq, F->Kpn, sx, F->gu_P, F->gu_s, T, 2 * F->h, F->Np_gu, F->Kpn,
-                          ws->S, F->h, 1, rt->d_err, s);
-    if (ev) (void)hipEventRecord(ev[1], s);
+static int ffn_run_q(const jt_hip_ffn *F, const ffn_ws *ws, const int8_t *Xq, const float *sx,
+                     int T, float *dY, uint32_t *err, hipStream_t s, hipEvent_t *ev) {
+    /* with profiling events the gate/up stage is the kernel's own duration */
+    int e = jtk_w8a8_gemm_ev(Xq, F->Kpn, sx, F->gu_P, F->gu_s, T, 2 * F->h, F->Np_gu, F->Kpn,
+                             ws->S, F->h, 1, err, s, ev ? ev[0] : NULL,
+                             ev ? ev[1] : NULL);
     /* up to 16 rows the down projection quantises the hidden rows itself
      * (timed with the down stage) */
     const int f = T <= 16 ? jtk_w8a8_gemm_xq(ws->S, F->h, F->h, F->d_P, F->d_s, T, F->n,
-                                             F->Np_d, F->Kph, dY, F->n, 0, rt->d_err, s)
+                                             F->Np_d, F->Kph, dY, F->n, 0, err, s)
                           : (int)hipErrorInvalidValue;
     if (f == (int)hipErrorInvalidValue) {
-        e |= jtk_quant_rows(ws->S, T, F->h, ws->Sq, F->Kph, ws->ss, NULL, rt->d_err, s);
+        e |= jtk_quant_rows(ws->S, T, F->h, ws->Sq, F->Kph, ws->ss, NULL, err, s);
         if (ev) (void)hipEventRecord(ev[2], s);
         e |= jtk_w8a8_gemm(ws->Sq, F->Kph, ws->ss, F->d_P, F->d_s, T, F->n, F->Np_d, F->Kph, dY,
-                           F->n, 0, rt->d_err, s);
+                           F->n, 0, err, s);
     } else {
         if (ev) (void)hipEventRecord(ev[2], s);
         e |= f;
@@ -210,27 +210,27 @@ static int ffn_run_q(jt_rt *rt, const jt_hip_ffn *F, const ffn_ws *ws, const int
 }
 
 /* The expert on fp32 rows dX with the workspace ws (T > 0). */
-static int ffn_fwd_on(jt_rt *rt, const jt_hip_ffn *F, const ffn_ws *ws, const float *dX,
-                      float *dY, int T, hipStream_t s) {
+static int ffn_fwd_on(const jt_hip_ffn *F, const ffn_ws *ws, const float *dX, float *dY,
+                      int T, uint32_t *err, hipStream_t s) {
     if (T <= 16) {
         /* decode: both GEMMs quantise their rows themselves (two launches) */
         int e = jtk_w8a8_gemm_xq(dX, F->n, F->n, F->gu_P, F->gu_s, T, 2 * F->h, F->Np_gu,
-                                 F->Kpn, ws->S, F->h, 1, rt->d_err, s);
+                                 F->Kpn, ws->S, F->h, 1, err, s);
         if (e != (int)hipErrorInvalidValue) {
             if (e) return jt_rt_err(hipErrorLaunchFailure);
             e = jtk_w8a8_gemm_xq(ws->S, F->h, F->h, F->d_P, F->d_s, T, F->n, F->Np_d, F->Kph,
-                                 dY, F->n, 0, rt->d_err, s);
+                                 dY, F->n, 0, err, s);
             if (e == (int)hipErrorInvalidValue) {
-                e = jtk_quant_rows(ws->S, T, F->h, ws->Sq, F->Kph, ws->ss, NULL, rt->d_err, s);
+                e = jtk_quant_rows(ws->S, T, F->h, ws->Sq, F->Kph, ws->ss, NULL, err, s);
                 e |= jtk_w8a8_gemm(ws->Sq, F->Kph, ws->ss, F->d_P, F->d_s, T, F->n, F->Np_d,
-                                   F->Kph, dY, F->n, 0, rt->d_err, s);
+                                   F->Kph, dY, F->n, 0, err, s);
             }
             return e ? jt_rt_err(hipErrorLaunchFailure) : JT_OK;
         }
     }
-    if (jtk_quant_rows(dX, T, F->n, ws->Xq, F->Kpn, ws->sx, NULL, rt->d_err, s))
+    if (jtk_quant_rows(dX, T, F->n, ws->Xq, F->Kpn, ws->sx, NULL, err, s))
         return jt_rt_err(hipErrorLaunchFailure);
-    return ffn_run_q(rt, F, ws, ws->Xq, ws->sx, T, dY, s, NULL);
+    return ffn_run_q(F, ws, ws->Xq, ws->sx, T, dY, err, s, NULL);
 }
 
 int jt_hip_ffn_fwd(jt_hip_ffn *F, const float *dX, float *dY, int T, void *stream) {
@@ -241,7 +241,14 @@ int jt_hip_ffn_fwd(jt_hip_ffn *F, const float *dX, float *dY, int T, void *strea
     int rc = ffn_reserve(F, T, 1);
     if (rc != JT_OK) return rc;
     const ffn_ws ws = ffn_own_ws(F);
-    return ffn_fwd_on(rt, F, &ws, dX, dY, T, (hipStream_t)stream); /* NULL: the null stream */
+    const hipStream_t s = (hipStream_t)stream; /* NULL: the null stream */
+    return ffn_fwd_on(F, &ws, dX, dY, T, jt_rt_errw(rt, s), s);
+}
+
+int jt_hip_ffn_reserve(jt_hip_ffn *F, int T) {
+    if (!F || T <= 0) FAIL(JT_ERR_INVAL, EINVAL);
+    if (!jt_rt_get()) return JT_ERR_IO;
+    return ffn_reserve(F, T, 1);
 }
 
 /* Byte offsets of the workspace of a T-row forward inside one buffer, each
@@ -278,7 +285,7 @@ int jt_hip_ffn_fwd_noalloc(jt_hip_ffn *F, const float *dX, float *dY, int T, voi
     if (F->Kpn > F->n) e |= jtk_scratch_zero((uint32_t *)ws.Xq, (int64_t)T * F->Kpn / 4, s);
     if (F->Kph > F->h) e |= jtk_scratch_zero((uint32_t *)ws.Sq, (int64_t)T * F->Kph / 4, s);
     if (e) return jt_rt_err(hipErrorLaunchFailure);
-    return ffn_fwd_on(rt, F, &ws, dX, dY, T, s);
+    return ffn_fwd_on(F, &ws, dX, dY, T, jt_rt_errw(rt, s), s);
 }
 
 /* ======================= MoE layer ======================= */
@@ -497,20 +504,20 @@ int jt_hip_moe_prepare(const jt_hip_moe_desc *desc, const float *dWgate, const f
                            hipMemcpyDeviceToDevice, rt->stream);
     rc = jt_rt_err(e);
     if (rc == JT_OK) {
-        jtk_check_finite(dWgate ? L->Wgate : NULL, dWgate ? (int64_t)E * n : 0, rt->d_err,
+        jtk_check_finite(dWgate ? L->Wgate : NULL, dWgate ? (int64_t)E * n : 0, jt_rt_errw(rt, rt->stream),
                          rt->stream);
         if (L->fast_router) {
-            jtk_router_codes(L->Wgate, E, n, wh_rm, wl_rm, NULL, L->winfo, rt->d_err,
+            jtk_router_codes(L->Wgate, E, n, wh_rm, wl_rm, NULL, L->winfo, jt_rt_errw(rt, rt->stream),
                              rt->stream);
             jtk_pack_i8(wh_rm, E, n, 0, Ep, n, L->rWh, rt->stream);
             jtk_pack_i8(wl_rm, E, n, 0, Ep, n, L->rWl, rt->stream);
         }
         /* routed gate/up: rows of Wg/Wu [E][h][n] are channels, K = n */
         jtk_pack_lowbit(dWg, dWu, (int64_t)h * n, n, 1, E, 2 * h, n, 2, L->gu_P, L->gu_S,
-                        NULL, NULL, rt->d_err, rt->stream);
+                        NULL, NULL, jt_rt_errw(rt, rt->stream), rt->stream);
         /* routed down: Wd [E][h][n] is B[K=h][N=n]; channel j = column j */
         jtk_pack_lowbit(dWd, NULL, (int64_t)h * n, 1, n, E, n, h, 4, L->dn_P, L->dn_S, NULL,
-                        NULL, rt->d_err, rt->stream);
+                        NULL, jt_rt_errw(rt, rt->stream), rt->stream);
         uint32_t f = 0;
         rc = jt_rt_flags(rt, rt->stream, &f);
         if (rc == JT_OK) rc = jt_rt_flags_to_rc(f);
@@ -587,7 +594,7 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
     hipStream_t s = (hipStream_t)stream; /* NULL: the HIP null stream */
     const int n = d->n, h = d->h, E = d->n_experts, k = d->topk, S = d->n_shared;
     const int Tk = T * k;
-    uint32_t *err = rt->d_err;
+    uint32_t *err = jt_rt_errw(rt, s);
     int slot = 0, rc = prof_begin(L, &slot);
     if (rc != JT_OK) return rc;
     int le = 0;
@@ -617,7 +624,7 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
         for (int i = 0; i < L->nside; i++) le |= (int)hipStreamWaitEvent(L->side[i], L->ev_fork, 0);
         for (int e = 0; e < S; e++) { /* launch errors are collected; the join still happens */
             const ffn_ws ws = ffn_own_ws(L->sh[e]);
-            le |= ffn_run_q(rt, L->sh[e], &ws, L->Xq, L->sx, T, L->Ys + (size_t)e * T * n,
+            le |= ffn_run_q(L->sh[e], &ws, L->Xq, L->sx, T, L->Ys + (size_t)e * T * n, err,
                             L->side[e % L->nside], NULL);
         }
         for (int i = 0; i < L->nside; i++) le |= (int)hipEventRecord(L->ev_join[i], L->side[i]);
@@ -707,7 +714,7 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
         for (int e = 0; e < S; e++) {
             hipEvent_t *ev = L->prof ? &L->ev[slot][ST_N + 1 + 3 * e] : NULL;
             const ffn_ws ws = ffn_own_ws(L->sh[e]);
-            rc = ffn_run_q(rt, L->sh[e], &ws, L->Xq, L->sx, T, L->Ys + (size_t)e * T * n, s, ev);
+            rc = ffn_run_q(L->sh[e], &ws, L->Xq, L->sx, T, L->Ys + (size_t)e * T * n, err, s, ev);
             if (rc != JT_OK) return rc;
         }
     }

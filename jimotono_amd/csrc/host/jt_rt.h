@@ -44,7 +44,7 @@ typedef struct jt_rt {
     int ready;
     int device;
     hipStream_t stream;
-    uint32_t *d_err;     /* device error word */
+    uint32_t *d_err;     /* device error words, one per stream (JT_ERR_WORDS) */
     uint32_t *d_scratch; /* small device scratch (reductions) */
     void *slot[JT_NSLOTS];
     size_t slot_bytes[JT_NSLOTS];
@@ -57,7 +57,14 @@ jt_rt *jt_rt_get(void);
 int jt_rt_err(hipError_t e);
 /* Grow-only device buffer of slot `s` with at least `bytes` bytes. */
 void *jt_rt_buf(jt_rt *rt, int s, size_t bytes, int *rc);
-/* Synchronise `stream`, read and clear the device error word. */
+/* The device error word of `stream`: each stream the library has launched
+ * on gets its own word (the null stream included), so callers on different
+ * streams never see each other's error bits. Past JT_ERR_WORDS - 1 distinct
+ * streams the rest share the last word. */
+#define JT_ERR_WORDS 64
+#define JT_ERR_STRIDE 16 /* words between two streams' error words (64 B) */
+uint32_t *jt_rt_errw(jt_rt *rt, hipStream_t stream);
+/* Synchronise `stream`, read and clear that stream's device error word. */
 int jt_rt_flags(jt_rt *rt, hipStream_t stream, uint32_t *flags);
 /* Map error bits to the reference's return/errno convention
  * (non-finite input or bad code -> EINVAL, computed overflow -> ERANGE). */

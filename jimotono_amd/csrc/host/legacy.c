@@ -56,7 +56,7 @@ int jt_gemm_mat_f32(const float *A, const float *B, float *C, int M, int N, int 
     if (!dA || !dB || !dC) return rc;
     if ((rc = jt_rt_h2d(rt, dA, A, (size_t)M * K * 4)) != JT_OK) return rc;
     if ((rc = jt_rt_h2d(rt, dB, B, (size_t)K * N * 4)) != JT_OK) return rc;
-    LAUNCHED(jtk_gemm_f32(dA, dB, dC, M, N, K, rt->d_err, rt->stream));
+    LAUNCHED(jtk_gemm_f32(dA, dB, dC, M, N, K, jt_rt_errw(rt, rt->stream), rt->stream));
     if ((rc = finish(rt)) != JT_OK) return rc;
     return jt_rt_d2h(rt, C, dC, (size_t)M * N * 4);
 }
@@ -109,7 +109,7 @@ int jt_lowbit_fakequant(const float *w, float *fq, size_t n, int bits) {
     float *dws = jt_rt_buf(rt, JT_SLOT_B, 4, &rc);
     if (!dW || !dws) return rc;
     if ((rc = jt_rt_h2d(rt, dW, w, n * 4)) != JT_OK) return rc;
-    LAUNCHED(jtk_lowbit_fq_cols(dW, (int)n, 1, bits, dws, rt->d_err, rt->stream));
+    LAUNCHED(jtk_lowbit_fq_cols(dW, (int)n, 1, bits, dws, jt_rt_errw(rt, rt->stream), rt->stream));
     if ((rc = finish(rt)) != JT_OK) return rc;
     return jt_rt_d2h(rt, fq, dW, n * 4);
 }
@@ -128,7 +128,7 @@ int jt_lowbit_col_to_idx(const float *col, size_t k, int bits, uint8_t *idx,
     uint8_t *didx = jt_rt_buf(rt, JT_SLOT_C, (size_t)bits * (k / 4), &rc);
     if (!dc || !dws || !didx) return rc;
     if ((rc = jt_rt_h2d(rt, dc, col, k * 4)) != JT_OK) return rc;
-    LAUNCHED(jtk_col_to_idx(dc, (int)k, 1, bits, dws, didx, rt->d_err, rt->stream));
+    LAUNCHED(jtk_col_to_idx(dc, (int)k, 1, bits, dws, didx, jt_rt_errw(rt, rt->stream), rt->stream));
     if ((rc = finish(rt)) != JT_OK) return rc;
     float ws = 0.0f;
     if ((rc = jt_rt_d2h(rt, idx, didx, (size_t)bits * (k / 4))) != JT_OK) return rc;
@@ -155,10 +155,10 @@ int jt_dev_lowbit_gemm_lut(jt_rt *rt, const float *dX, const float *dW, float *d
     uint8_t *idx = jt_rt_buf(rt, JT_SLOT_O, (size_t)h * bits * ng, &rc);
     float *ws = jt_rt_buf(rt, JT_SLOT_P, (size_t)h * 4, &rc);
     if (!qlut || !sc || !bi || !rs || !idx || !ws) return rc;
-    LAUNCHED(jtk_tmac_ctor(dX, me, k, qlut, sc, bi, rt->d_err, rt->stream));
+    LAUNCHED(jtk_tmac_ctor(dX, me, k, qlut, sc, bi, jt_rt_errw(rt, rt->stream), rt->stream));
     LAUNCHED(jtk_rowsum_f64(dX, me, k, rs, rt->stream));
-    LAUNCHED(jtk_col_to_idx(dW, k, h, bits, ws, idx, rt->d_err, rt->stream));
-    LAUNCHED(jtk_tmac_gemm(qlut, sc, bi, rs, idx, ws, me, h, k, bits, dY, rt->d_err,
+    LAUNCHED(jtk_col_to_idx(dW, k, h, bits, ws, idx, jt_rt_errw(rt, rt->stream), rt->stream));
+    LAUNCHED(jtk_tmac_gemm(qlut, sc, bi, rs, idx, ws, me, h, k, bits, dY, jt_rt_errw(rt, rt->stream),
                            rt->stream));
     return JT_OK;
 }
@@ -182,8 +182,8 @@ int jt_lowbit_gemm_lut(const float *X, const float *W, float *Y, int me, int h, 
     if (k % 32 == 0) {
         /* the reference rejects non-finite inputs in the table build and the
          * column conversion before writing Y */
-        jtk_check_finite(dX, (int64_t)me * k, rt->d_err, rt->stream);
-        jtk_check_finite(dW, (int64_t)k * h, rt->d_err, rt->stream);
+        jtk_check_finite(dX, (int64_t)me * k, jt_rt_errw(rt, rt->stream), rt->stream);
+        jtk_check_finite(dW, (int64_t)k * h, jt_rt_errw(rt, rt->stream), rt->stream);
         if ((rc = finish(rt)) != JT_OK) return rc;
     }
     if ((rc = jt_dev_lowbit_gemm_lut(rt, dX, dW, dY, me, h, k, bits)) != JT_OK) return rc;
@@ -242,7 +242,7 @@ int jt_tmac_lut_ctor(const float *act, size_t n, size_t k, int8_t *qlut, float *
     float *db = jt_rt_buf(rt, JT_SLOT_D, n * nb * 4, &rc);
     if (!dA || !dq || !ds || !db) return rc;
     if ((rc = jt_rt_h2d(rt, dA, act, n * k * 4)) != JT_OK) return rc;
-    LAUNCHED(jtk_tmac_ctor(dA, (int64_t)n, (int64_t)k, dq, ds, db, rt->d_err, rt->stream));
+    LAUNCHED(jtk_tmac_ctor(dA, (int64_t)n, (int64_t)k, dq, ds, db, jt_rt_errw(rt, rt->stream), rt->stream));
     if ((rc = finish(rt)) != JT_OK) return rc;
     if ((rc = jt_rt_d2h(rt, qlut, dq, n * (k / 4) * 8)) != JT_OK) return rc;
     if ((rc = jt_rt_d2h(rt, scales, ds, n * nb * 4)) != JT_OK) return rc;
@@ -278,7 +278,7 @@ int jt_tmac_lookup_accum(const int8_t *qlut, const uint8_t *idx, const float *sc
     if ((rc = jt_rt_h2d(rt, ds, scales, nblocks * 4)) != JT_OK) return rc;
     if ((rc = jt_rt_h2d(rt, db, biases, nblocks * 4)) != JT_OK) return rc;
     LAUNCHED(jtk_tmac_lookup1(dq, di, ds, db, (int64_t)ngroups, (int64_t)nblocks, bits,
-                              w_scale, dout, rt->d_err, rt->stream));
+                              w_scale, dout, jt_rt_errw(rt, rt->stream), rt->stream));
     if ((rc = finish(rt)) != JT_OK) return rc;
     float o = 0.0f;
     if ((rc = jt_rt_d2h(rt, &o, dout, 4)) != JT_OK) return rc;
@@ -307,9 +307,9 @@ int jt_routing_topk(const float *logits, size_t n, size_t k, size_t *out_ids,
     /* one wavefront holds rows up to the layer's limits (moe_layer.h:52-53);
      * longer rows or larger k take the block kernel */
     if (n <= JT_MOE_MAX_EXPERTS && k <= JT_MOE_MAX_TOPK) {
-        LAUNCHED(jtk_topk(dl, 1, (int)n, (int)k, di, di64, dw, rt->d_err, rt->stream));
+        LAUNCHED(jtk_topk(dl, 1, (int)n, (int)k, di, di64, dw, jt_rt_errw(rt, rt->stream), rt->stream));
     } else {
-        LAUNCHED(jtk_topk_block(dl, (int64_t)n, (int64_t)k, di64, dw, rt->d_err, rt->stream));
+        LAUNCHED(jtk_topk_block(dl, (int64_t)n, (int64_t)k, di64, dw, jt_rt_errw(rt, rt->stream), rt->stream));
     }
     if ((rc = finish(rt)) != JT_OK) return rc;
     int64_t *tmp = malloc(k * 8);
@@ -366,7 +366,7 @@ int jt_moe_batch_sort(const size_t *ids, int T, int k, int E, float cap_factor, 
     free(h32);
     if (rc != JT_OK) return rc;
     LAUNCHED(jtk_sort(dids, (int)Tk, E, cap, rank, cnt, tot, doff, doff64, dperm, dperm64,
-                      ddrop, rt->d_err, rt->stream));
+                      ddrop, jt_rt_errw(rt, rt->stream), rt->stream));
     if ((rc = finish(rt)) != JT_OK) return rc;
     int64_t kept = 0;
     if ((rc = jt_rt_d2h(rt, &kept, doff64 + E, 8)) != JT_OK) return rc;

@@ -80,7 +80,7 @@ int jt_hip_moe_bwd_batch(const float *dY, const float *X, const float *Wgate, co
                            drop,  dX,      dWgate, dWg,  dWu,   dWd,     dWg_s, dWu_s,
                            dWd_s, dLogits};
     int le = jtk_bwd_batch(&io, T, n, h, n_experts, topk, n_shared, validate != 0, &w,
-                           rt->d_err, (hipStream_t)stream);
+                           jt_rt_errw(rt, (hipStream_t)stream), (hipStream_t)stream);
     return le ? jt_rt_err(hipErrorLaunchFailure) : JT_OK;
 }
 

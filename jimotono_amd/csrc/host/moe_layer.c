@@ -75,15 +75,15 @@ static int w8a8_pc(jt_rt *rt, w8_ws *w, const float *A, const float *Brow, float
     }
     const int Kp = (int)jt_round_up((size_t)K, 64), Np = (int)jt_round_up((size_t)N, 128);
     hipStream_t s = rt->stream;
-    int le = jtk_quant_tensor(A, (int64_t)M * K, w->Bq, w->sA1, rt->d_scratch, rt->d_err, s);
+    int le = jtk_quant_tensor(A, (int64_t)M * K, w->Bq, w->sA1, rt->d_scratch, jt_rt_errw(rt, s), s);
     /* re-stride the activation codes to the padded GEMM layout */
     le |= (int)hipMemsetAsync(w->Aq, 0, (size_t)M * Kp, s);
     le |= (int)hipMemcpy2DAsync(w->Aq, (size_t)Kp, w->Bq, (size_t)K, (size_t)K, (size_t)M,
                                 hipMemcpyDeviceToDevice, s);
     le |= jtk_bcast_f32(w->sA, M, w->sA1, s);
-    le |= jtk_quant_weight_rows(Brow, K, 1, N, K, w->Bq, w->sB, rt->d_err, s);
+    le |= jtk_quant_weight_rows(Brow, K, 1, N, K, w->Bq, w->sB, jt_rt_errw(rt, s), s);
     le |= jtk_pack_i8(w->Bq, N, K, 0, Np, Kp, w->P, s);
-    le |= jtk_w8a8_gemm(w->Aq, Kp, w->sA, w->P, w->sB, M, N, Np, Kp, C, N, 0, rt->d_err, s);
+    le |= jtk_w8a8_gemm(w->Aq, Kp, w->sA, w->P, w->sB, M, N, Np, Kp, C, N, 0, jt_rt_errw(rt, s), s);
     return le ? jt_rt_err(hipErrorLaunchFailure) : JT_OK;
 }
 
@@ -97,15 +97,15 @@ static int w8a8_pt(jt_rt *rt, w8_ws *w, const float *A, const float *Bkn, float 
     }
     const int Kp = (int)jt_round_up((size_t)K, 64), Np = (int)jt_round_up((size_t)N, 128);
     hipStream_t s = rt->stream;
-    int le = jtk_quant_tensor(A, (int64_t)M * K, w->Bq, w->sA1, rt->d_scratch, rt->d_err, s);
+    int le = jtk_quant_tensor(A, (int64_t)M * K, w->Bq, w->sA1, rt->d_scratch, jt_rt_errw(rt, s), s);
     le |= (int)hipMemsetAsync(w->Aq, 0, (size_t)M * Kp, s);
     le |= (int)hipMemcpy2DAsync(w->Aq, (size_t)Kp, w->Bq, (size_t)K, (size_t)K, (size_t)M,
                                 hipMemcpyDeviceToDevice, s);
     le |= jtk_bcast_f32(w->sA, M, w->sA1, s);
-    le |= jtk_quant_tensor(Bkn, (int64_t)K * N, w->Bq, w->sB1, rt->d_scratch + 1, rt->d_err, s);
+    le |= jtk_quant_tensor(Bkn, (int64_t)K * N, w->Bq, w->sB1, rt->d_scratch + 1, jt_rt_errw(rt, s), s);
     le |= jtk_bcast_f32(w->sB, Np, w->sB1, s);
     le |= jtk_pack_i8(w->Bq, N, K, 1, Np, Kp, w->P, s);
-    le |= jtk_w8a8_gemm(w->Aq, Kp, w->sA, w->P, w->sB, M, N, Np, Kp, C, N, 0, rt->d_err, s);
+    le |= jtk_w8a8_gemm(w->Aq, Kp, w->sA, w->P, w->sB, M, N, Np, Kp, C, N, 0, jt_rt_errw(rt, s), s);
     return le ? jt_rt_err(hipErrorLaunchFailure) : JT_OK;
 }
 
@@ -138,7 +138,7 @@ static int fwd_batch(const float *X, const float *Wgate, const float *Wg, const 
     jt_rt *rt = jt_rt_get();
     if (!rt) return JT_ERR_IO;
     hipStream_t s = rt->stream;
-    uint32_t *err = rt->d_err;
+    uint32_t *err = jt_rt_errw(rt, s);
     const size_t Tk = (size_t)T * k, nh = (size_t)n * h, Tn = (size_t)T * n;
     const size_t NB = (Tk + 255) / 256;
     const int Kpmax = (int)jt_round_up((size_t)(n > h ? n : h), 64);

@@ -9,12 +9,19 @@
 #include "jt_rt.h"
 
 #include <errno.h>
+#include <pthread.h>
 #include <string.h>
 
 #include "jimotono/hip_moe.h"
 
 static jt_rt g_rt;
 static int g_req_device = 0;
+
+/* stream -> error word: slot i (0 .. JT_ERR_WORDS - 2) belongs to
+ * g_err_stream[i]; the last slot is shared by streams past the table */
+static pthread_mutex_t g_err_mu = PTHREAD_MUTEX_INITIALIZER;
+static hipStream_t g_err_stream[JT_ERR_WORDS - 1];
+static int g_err_used;
 
 int jt_rt_err(hipError_t e) {
     if (e == hipSuccess) return JT_OK;
@@ -43,9 +50,9 @@ jt_rt *jt_rt_get(void) {
      * preparation are ordered after work the caller queued on the null
      * stream (torch's default stream, for one) */
     if (hipStreamCreateWithFlags(&g_rt.stream, hipStreamDefault) != hipSuccess ||
-        hipMalloc((void **)&g_rt.d_err, 256) != hipSuccess ||
+        hipMalloc((void **)&g_rt.d_err, JT_ERR_WORDS * JT_ERR_STRIDE * 4) != hipSuccess ||
         hipMalloc((void **)&g_rt.d_scratch, 4096) != hipSuccess ||
-        hipMemset(g_rt.d_err, 0, 256) != hipSuccess) {
+        hipMemset(g_rt.d_err, 0, JT_ERR_WORDS * JT_ERR_STRIDE * 4) != hipSuccess) {
         errno = EIO;
         return NULL;
     }
@@ -98,11 +105,20 @@ void *jt_rt_buf(jt_rt *rt, int s, size_t bytes, int *rc) {
     return rt->slot[s];
 }
 
+uint32_t *jt_rt_errw(jt_rt *rt, hipStream_t stream) {
+    pthread_mutex_lock(&g_err_mu);
+    int i = 0;
+    while (i < g_err_used && g_err_stream[i] != stream) i++;
+    if (i == g_err_used && g_err_used < JT_ERR_WORDS - 1) g_err_stream[g_err_used++] = stream;
+    pthread_mutex_unlock(&g_err_mu);
+    return rt->d_err + (size_t)i * JT_ERR_STRIDE;
+}
+
 int jt_rt_flags(jt_rt *rt, hipStream_t stream, uint32_t *flags) {
-    uint32_t f = 0;
+    uint32_t f = 0, *w = jt_rt_errw(rt, stream);
     hipError_t e = hipStreamSynchronize(stream);
-    if (e == hipSuccess) e = hipMemcpy(&f, rt->d_err, sizeof(f), hipMemcpyDeviceToHost);
-    if (e == hipSuccess && f != 0) e = hipMemset(rt->d_err, 0, sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMemcpy(&f, w, sizeof(f), hipMemcpyDeviceToHost);
+    if (e == hipSuccess && f != 0) e = hipMemset(w, 0, sizeof(uint32_t));
     if (e != hipSuccess) return jt_rt_err(e);
     *flags = f;
     return JT_OK;

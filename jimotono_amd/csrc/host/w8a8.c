@@ -52,7 +52,7 @@ int jt_w8a8_quant_per_tensor(const float *src, size_t n, int8_t *dst, float *out
     float *ds = jt_rt_buf(rt, JT_SLOT_C, sizeof(float), &rc);
     if (!dx || !dq || !ds) return rc;
     if ((rc = jt_rt_h2d(rt, dx, src, n * sizeof(float))) != JT_OK) return rc;
-    if (jtk_quant_tensor(dx, (int64_t)n, dq, ds, rt->d_scratch, rt->d_err, rt->stream))
+    if (jtk_quant_tensor(dx, (int64_t)n, dq, ds, rt->d_scratch, jt_rt_errw(rt, rt->stream), rt->stream))
         return jt_rt_err(hipErrorLaunchFailure);
     uint32_t f = 0;
     if ((rc = jt_rt_flags(rt, rt->stream, &f)) != JT_OK) return rc;
@@ -78,8 +78,8 @@ int jt_w8a8_quant_per_channel(const float *src, size_t rows, size_t cols, int8_t
     if (!dx || !dq || !ds) return rc;
     if ((rc = jt_rt_h2d(rt, dx, src, n * sizeof(float))) != JT_OK) return rc;
     /* the reference checks the whole array before any row (src/w8a8.c:803-811) */
-    jtk_check_finite(dx, (int64_t)n, rt->d_err, rt->stream);
-    if (jtk_quant_rows(dx, (int64_t)rows, (int)cols, dq, (int64_t)cols, ds, NULL, rt->d_err,
+    jtk_check_finite(dx, (int64_t)n, jt_rt_errw(rt, rt->stream), rt->stream);
+    if (jtk_quant_rows(dx, (int64_t)rows, (int)cols, dq, (int64_t)cols, ds, NULL, jt_rt_errw(rt, rt->stream),
                        rt->stream))
         return jt_rt_err(hipErrorLaunchFailure);
     uint32_t f = 0;
@@ -102,7 +102,7 @@ static int dequant_common(const int8_t *src, const float *scales, size_t rows, s
     if ((rc = jt_rt_h2d(rt, dq, src, n)) != JT_OK) return rc;
     if ((rc = jt_rt_h2d(rt, ds, scales, (per_row ? rows : 1) * sizeof(float))) != JT_OK)
         return rc;
-    if (jtk_dequant(dq, ds, (int64_t)rows, (int64_t)cols, per_row, dd, rt->d_err, rt->stream))
+    if (jtk_dequant(dq, ds, (int64_t)rows, (int64_t)cols, per_row, dd, jt_rt_errw(rt, rt->stream), rt->stream))
         return jt_rt_err(hipErrorLaunchFailure);
     uint32_t f = 0;
     if ((rc = jt_rt_flags(rt, rt->stream, &f)) != JT_OK) return rc;
@@ -134,7 +134,7 @@ static int fakequant_common(const float *src, size_t rows, size_t cols, float *d
     float *dd = jt_rt_buf(rt, JT_SLOT_B, n * sizeof(float), &rc);
     if (!dx || !dd) return rc;
     if ((rc = jt_rt_h2d(rt, dx, src, n * sizeof(float))) != JT_OK) return rc;
-    if (jtk_fakequant(dx, (int64_t)rows, (int64_t)cols, dd, rt->d_scratch, rt->d_err,
+    if (jtk_fakequant(dx, (int64_t)rows, (int64_t)cols, dd, rt->d_scratch, jt_rt_errw(rt, rt->stream),
                       rt->stream))
         return jt_rt_err(hipErrorLaunchFailure);
     uint32_t f = 0;
@@ -196,13 +196,13 @@ static int gemm_host(const int8_t *Aq, const int8_t *Bq, float sA, const float *
     free(hs);
     if (e != hipSuccess) return jt_rt_err(e);
     /* -128 codes are rejected before anything is computed (src/w8a8.c:979-999) */
-    jtk_check_q(dA, (int64_t)M * Kp, rt->d_err, rt->stream);
-    jtk_check_q(dB, (int64_t)K * N, rt->d_err, rt->stream);
+    jtk_check_q(dA, (int64_t)M * Kp, jt_rt_errw(rt, rt->stream), rt->stream);
+    jtk_check_q(dB, (int64_t)K * N, jt_rt_errw(rt, rt->stream), rt->stream);
     uint32_t f = 0;
     if ((rc = jt_rt_flags(rt, rt->stream, &f)) != JT_OK) return rc;
     if ((rc = jt_rt_flags_to_rc(f)) != JT_OK) return rc;
     if (jtk_pack_i8(dB, N, K, 1, Np, Kp, dP, rt->stream) ||
-        jtk_w8a8_gemm(dA, Kp, dsA, dP, dsB, M, N, Np, Kp, dC, N, 0, rt->d_err, rt->stream))
+        jtk_w8a8_gemm(dA, Kp, dsA, dP, dsB, M, N, Np, Kp, dC, N, 0, jt_rt_errw(rt, rt->stream), rt->stream))
         return jt_rt_err(hipErrorLaunchFailure);
     if ((rc = jt_rt_flags(rt, rt->stream, &f)) != JT_OK) return rc;
     if ((rc = jt_rt_flags_to_rc(f)) != JT_OK) return rc;
@@ -260,7 +260,7 @@ int jt_hip_quant_rows(const float *dX, int rows, int cols, int8_t *dXq, float *d
     if (!rt) return JT_ERR_IO;
     if (rows == 0) return JT_OK;
     hipStream_t s = (hipStream_t)stream; /* NULL: the HIP null stream */
-    if (jtk_quant_rows(dX, rows, cols, dXq, cols, dscale, NULL, rt->d_err, s))
+    if (jtk_quant_rows(dX, rows, cols, dXq, cols, dscale, NULL, jt_rt_errw(rt, s), s))
         return jt_rt_err(hipErrorLaunchFailure);
     return JT_OK;
 }
@@ -304,7 +304,7 @@ int jt_hip_w8a8_prepare(const float *dW, int N, int K, jt_hip_w8a8 **out) {
         jt_hip_w8a8_free(W);
         return jt_rt_err(e);
     }
-    jtk_quant_weight_rows(dW, K, 1, N, K, tmp, W->sB, rt->d_err, rt->stream);
+    jtk_quant_weight_rows(dW, K, 1, N, K, tmp, W->sB, jt_rt_errw(rt, rt->stream), rt->stream);
     jtk_pack_i8(tmp, N, K, 0, W->Np, W->Kp, W->P, rt->stream);
     uint32_t f = 0;
     rc = jt_rt_flags(rt, rt->stream, &f);
@@ -334,7 +334,7 @@ int jt_hip_w8a8_prepare_kn(const int8_t *dBq, const float *dsB, int N, int K,
         jt_hip_w8a8_free(W);
         return jt_rt_err(e);
     }
-    jtk_check_q(dBq, (int64_t)N * K, rt->d_err, rt->stream);
+    jtk_check_q(dBq, (int64_t)N * K, jt_rt_errw(rt, rt->stream), rt->stream);
     jtk_pack_i8(dBq, N, K, 1, W->Np, W->Kp, W->P, rt->stream);
     uint32_t f = 0;
     rc = jt_rt_flags(rt, rt->stream, &f);
@@ -356,7 +356,7 @@ int jt_hip_w8a8_gemm(const jt_hip_w8a8 *W, const int8_t *dAq, const float *dsA, 
     if (M == 0) return JT_OK;
     hipStream_t s = (hipStream_t)stream; /* NULL: the HIP null stream */
     if (jtk_w8a8_gemm(dAq, W->K, dsA, W->P, W->sB, M, W->N, W->Np, W->Kp, dC, W->N, 0,
-                      rt->d_err, s))
+                      jt_rt_errw(rt, s), s))
         return jt_rt_err(hipErrorLaunchFailure);
     return JT_OK;
 }
@@ -377,7 +377,7 @@ int jt_hip_w8a8_gemm_f32(const jt_hip_w8a8 *W, const float *dX, float *dC, int M
     if (M <= 16) {
         if (W->K % 4 || W->K > 4096 || ((uintptr_t)dX & 15u)) FAIL(JT_ERR_INVAL, EINVAL);
         return jtk_w8a8_gemm_xq(dX, W->K, W->K, W->P, W->sB, M, W->N, W->Np, W->Kp, dC, W->N, 0,
-                                rt->d_err, s)
+                                jt_rt_errw(rt, s), s)
                    ? jt_rt_err(hipErrorLaunchFailure)
                    : JT_OK;
     }
@@ -386,8 +386,8 @@ int jt_hip_w8a8_gemm_f32(const jt_hip_w8a8 *W, const float *dX, float *dC, int M
     /* codes at row stride Kp: the columns K..Kp-1 meet zero weight codes */
     int8_t *Xq = (int8_t *)d_ws;
     float *sx = (float *)((char *)d_ws + jt_round_up((size_t)M * W->Kp, 256));
-    if (jtk_quant_rows(dX, M, W->K, Xq, W->Kp, sx, NULL, rt->d_err, s) ||
-        jtk_w8a8_gemm(Xq, W->Kp, sx, W->P, W->sB, M, W->N, W->Np, W->Kp, dC, W->N, 0, rt->d_err,
+    if (jtk_quant_rows(dX, M, W->K, Xq, W->Kp, sx, NULL, jt_rt_errw(rt, s), s) ||
+        jtk_w8a8_gemm(Xq, W->Kp, sx, W->P, W->sB, M, W->N, W->Np, W->Kp, dC, W->N, 0, jt_rt_errw(rt, s),
                       s))
         return jt_rt_err(hipErrorLaunchFailure);
     return JT_OK;

@@ -379,10 +379,12 @@ extern "C" int jtk_w8a8_gemm_xq(const float *X, int ldx, int K, const int8_t *Wp
     return (int)e;
 }
 
-extern "C" int jtk_w8a8_gemm(const int8_t *A, int lda, const float *sA, const int8_t *Wp,
-                             const float *sB, int M, int N, int Np, int Kp, float *C,
-                             int ldc, int swiglu, uint32_t *err, hipStream_t s) {
+extern "C" int jtk_w8a8_gemm_ev(const int8_t *A, int lda, const float *sA, const int8_t *Wp,
+                                const float *sB, int M, int N, int Np, int Kp, float *C,
+                                int ldc, int swiglu, uint32_t *err, hipStream_t s,
+                                hipEvent_t e0, hipEvent_t e1) {
     if (M <= 0) return 0;
+    if (M <= 64 && e0) (void)hipEventRecord(e0, s);
     if (M <= 16) {
         if (swiglu)
             hipLaunchKernelGGL((k_w8a8_skinny<EPI_SWIGLU, 2, 0>), dim3((unsigned)(Np / 32)),
@@ -410,19 +412,28 @@ extern "C" int jtk_w8a8_gemm(const int8_t *A, int lda, const float *sA, const in
         hipError_t e;
         if (swiglu) {
             e = n256 ? launch_w8a8_tile<EPI_SWIGLU, 128, 256, 2, 4, 1, 3, 4>(
-                           A, lda, sA, Wp, sB, M, N, Np, Kp, C, ldc, err, s)
+                           A, lda, sA, Wp, sB, M, N, Np, Kp, C, ldc, err, s, e0, e1)
                      : launch_w8a8_tile<EPI_SWIGLU, 128, 128, 2, 2, 2, 2, 4>(
-                           A, lda, sA, Wp, sB, M, N, Np, Kp, C, ldc, err, s);
+                           A, lda, sA, Wp, sB, M, N, Np, Kp, C, ldc, err, s, e0, e1);
         } else if (!n256 || mt128 * (Np / 128) <= 512) {
-            e = launch_w8a8_tile<EPI_PLAIN, 128, 128, 2, 2, 2, 3, 4>(A, lda, sA, Wp, sB, M, N, Np,
-                                                                     Kp, C, ldc, err, s);
+            e = launch_w8a8_tile<EPI_PLAIN, 128, 128, 2, 2, 2, 3, 4>(
+                A, lda, sA, Wp, sB, M, N, Np, Kp, C, ldc, err, s, e0, e1);
         } else {
-            e = launch_w8a8_tile<EPI_PLAIN, 128, 256, 2, 4, 1, 3, 4>(A, lda, sA, Wp, sB, M, N, Np,
-                                                                     Kp, C, ldc, err, s);
+            e = launch_w8a8_tile<EPI_PLAIN, 128, 256, 2, 4, 1, 3, 4>(
+                A, lda, sA, Wp, sB, M, N, Np, Kp, C, ldc, err, s, e0, e1);
         }
         return (int)e;
     }
-    return (int)hipGetLastError();
+    const hipError_t e = hipGetLastError();
+    if (e1) (void)hipEventRecord(e1, s);
+    return (int)e;
+}
+
+extern "C" int jtk_w8a8_gemm(const int8_t *A, int lda, const float *sA, const int8_t *Wp,
+                             const float *sB, int M, int N, int Np, int Kp, float *C,
+                             int ldc, int swiglu, uint32_t *err, hipStream_t s) {
+    return jtk_w8a8_gemm_ev(A, lda, sA, Wp, sB, M, N, Np, Kp, C, ldc, swiglu, err, s, nullptr,
+                            nullptr);
 }
 
 // ===================== grouped low-bit GEMM =====================

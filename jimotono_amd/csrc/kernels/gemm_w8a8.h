@@ -18,6 +18,7 @@
 // group) so the concurrently resident blocks of an XCD share A rows and W
 // columns in its L2.
 #pragma once
+#include <hip/hip_ext.h>
 #include "jt_dev.h"
 
 enum { EPI_PLAIN = 0, EPI_SWIGLU = 1, EPI_SCATTER = 2 };
@@ -332,11 +333,15 @@ __global__ __launch_bounds__(64 * WGM * WGN * KS) void k_w8a8_tile(
                                                   s_cs + wn, M, N, C, ldc, err, s_tab);
 }
 
-// Host-side launch of one configuration (dynamic LDS = NST stages).
+// Host-side launch of one configuration (dynamic LDS = NST stages). Non-null
+// events e0 / e1 take the timestamps of the kernel's own start and end
+// (hipExtLaunchKernelGGL), so their elapsed time is the kernel's duration
+// with no marker packet around it.
 template <int EPI, int BM, int BN, int WGM, int WGN, int KS, int NST, int GM>
 inline hipError_t launch_w8a8_tile(const int8_t *A, int lda, const float *sA, const int8_t *Wp,
                                    const float *sB, int M, int N, int Np, int Kp, float *C,
-                                   int ldc, uint32_t *err, hipStream_t s) {
+                                   int ldc, uint32_t *err, hipStream_t s,
+                                   hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr) {
     auto kern = k_w8a8_tile<EPI, BM, BN, WGM, WGN, KS, NST, GM>;
     constexpr int lds = NST * (BM + BN) / 16 * KS * 1024;
     // dynamic LDS above 64 KiB must be enabled per device, once
@@ -352,7 +357,7 @@ inline hipError_t launch_w8a8_tile(const int8_t *A, int lda, const float *sA, co
         attr_set[dev] = true;
     }
     const int mt = (M + BM - 1) / BM, nt = Np / BN;
-    hipLaunchKernelGGL(kern, dim3((unsigned)(mt * nt)), dim3(64 * WGM * WGN * KS), lds, s, A,
-                       lda, sA, Wp, sB, M, N, Kp, C, ldc, err, mt, nt);
+    hipExtLaunchKernelGGL(kern, dim3((unsigned)(mt * nt)), dim3(64 * WGM * WGN * KS), lds, s,
+                          e0, e1, 0, A, lda, sA, Wp, sB, M, N, Kp, C, ldc, err, mt, nt);
     return hipGetLastError();
 }

@@ -52,6 +52,12 @@ int jtk_quant_weight_rows(const float *W, int64_t ld_n, int64_t ld_k, int N, int
 int jtk_w8a8_gemm(const int8_t *A, int lda, const float *sA, const int8_t *Wp,
                   const float *sB, int M, int N, int Np, int Kp, float *C, int ldc,
                   int swiglu, uint32_t *err, hipStream_t s);
+/* jtk_w8a8_gemm with events for its duration: above 64 rows e0 / e1 carry
+ * the tile kernel's own start and end timestamps; up to 64 rows they are
+ * recorded before and after the launch. Either may be NULL. */
+int jtk_w8a8_gemm_ev(const int8_t *A, int lda, const float *sA, const int8_t *Wp,
+                     const float *sB, int M, int N, int Np, int Kp, float *C, int ldc,
+                     int swiglu, uint32_t *err, hipStream_t s, hipEvent_t e0, hipEvent_t e1);
 /* M <= 16 on fp32 activations X [M][ldx] (K valid columns): each block
  * quantises the rows itself with the row quantiser's arithmetic.
  * hipErrorInvalidValue (nothing launched) unless K % 4 == 0, K <= 4096

@@ -254,3 +254,30 @@ def test_gdn2_decode_full_size(jt, orc, torch_cuda, H, dk, dv):
     for h in range(H):
         rc, Sh, oh = orc.gdn2_decode_step(S[h], q[h], k[h], v[h], b[h], w[h], a[h])
         assert same(S1[h], Sh) and same(O1[h], oh), h
+
+
+def test_error_words_are_per_stream(jt, orc, torch_cuda):
+    """A rejected head on one stream sets that stream's error word only: a
+    clean call on a second stream reads zero, and reading a word clears it."""
+    torch = torch_cuda
+    H, dk, dv = 4, 16, 16
+    announce("error words per stream (jt_hip_gdn2_decode on two streams)")
+    rng = np.random.default_rng(21)
+    S = (rng.standard_normal((H, dk, dv)) * 0.3).astype(np.float32)
+    q, k, b = (rng.standard_normal((H, dk)).astype(np.float32) for _ in range(3))
+    a = rng.uniform(0, 1, (H, dk)).astype(np.float32)
+    v, w = (rng.standard_normal((H, dv)).astype(np.float32) for _ in range(2))
+    a_bad = a.copy()
+    a_bad[1, 2] = np.nan
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    torch.cuda.synchronize()
+    d1 = [_t(torch, x) for x in (S, q, k, v, b, w, a_bad)]
+    d2 = [_t(torch, x) for x in (S, q, k, v, b, w, a)]
+    o1, o2 = torch.empty(H, dv, device="cuda"), torch.empty(H, dv, device="cuda")
+    torch.cuda.synchronize()
+    assert jt.gdn2_decode_device(d1[0], o1, *d1[1:], stream=s1) == 0
+    assert jt.gdn2_decode_device(d2[0], o2, *d2[1:], stream=s2) == 0
+    assert jt.sync_errors(s2) == 0
+    assert jt.sync_errors(s1) & jt.EF_NONFINITE_INPUT
+    assert jt.sync_errors(s1) == 0
+    assert jt.sync_errors() == 0

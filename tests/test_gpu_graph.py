@@ -53,7 +53,7 @@ def test_layer_graph_replays(jt, torch_cuda, T):
         gr.replay()
         torch.cuda.synchronize()
         assert torch.equal(Y, y_eager), f"replay {rep} differs from the eager forward"
-    assert jt.sync_errors() == 0
+    assert jt.sync_errors(stream) == 0 and jt.sync_errors() == 0
 
 
 def test_ffn_graph_replays(jt, torch_cuda):
@@ -86,4 +86,4 @@ def test_ffn_graph_replays(jt, torch_cuda):
         gr.replay()
         torch.cuda.synchronize()
         assert torch.equal(Y, y_eager), f"replay {rep} differs from the eager forward"
-    assert jt.sync_errors() == 0
+    assert jt.sync_errors(stream) == 0 and jt.sync_errors() == 0

@@ -269,6 +269,28 @@ def test_ffn_shared_expert_parity(jt, orc, torch_cuda, M):
     close(dY.cpu().numpy(), Y2)
 
 
+def test_ffn_reserve_then_grow(jt, orc, torch_cuda):
+    """jt_hip_ffn_reserve sizes the workspace ahead; forwards at and below
+    the reserved rows, and one above it (which grows the workspace), all
+    match the oracle."""
+    torch = torch_cuda
+    n, h = 256, 128
+    announce(f"ffn reserve n={n} h={h}")
+    rng = np.random.default_rng(77)
+    Wg, Wu = ((rng.standard_normal((h, n)) / 16).astype(np.float32) for _ in range(2))
+    Wd = (rng.standard_normal((h, n)) / 11).astype(np.float32)
+    F = jt.FFN(dev(torch, Wg), dev(torch, Wu), dev(torch, Wd))
+    F.reserve(64)
+    for M in (64, 20, 150):
+        X = rng.standard_normal((M, n)).astype(np.float32)
+        dY = torch.zeros((M, n), dtype=torch.float32, device="cuda")
+        F.fwd(dev(torch, X), dY)
+        assert jt.sync_errors() == 0
+        rc, Y2 = orc.ffn_fwd(Wg, Wu, Wd, X)
+        assert rc == 0
+        close(dY.cpu().numpy(), Y2)
+
+
 @pytest.mark.parametrize("n,h,M", [(256, 128, 3), (768, 3072, 16), (4096, 64, 2)],
                          ids=["n256", "h3072", "n4096_fallback"])
 def test_ffn_decode_widths(jt, orc, torch_cuda, n, h, M):
