@@ -54,7 +54,7 @@ def parse():
                         "two shared and 256 routed experts) and print its JSON line; "
                         "the workload of the decode kernel-trace profile")
     p.add_argument("--only", choices=["w8a8_64", "shared_decode", "routed_decode", "stress",
-                                      "bwd", "gdn2", "proj"],
+                                      "bwd", "gdn2", "proj", "vendor"],
                    help="run one of the other shapes' benchmarks alone and print its JSON "
                         "(the workloads of their kernel-trace profiles)")
     p.add_argument("--copy-probe", action="store_true",
@@ -430,6 +430,36 @@ def sub_benchmarks(np, torch, api, stream, only=None):
         res.update(gdn2_bench(np, torch, api, stream))
     if want("proj"):
         res.update(proj_bench(np, torch, api, stream))
+    if want("vendor"):
+        res.update(vendor_bench(np, torch, api, stream))
+    return res
+
+
+def vendor_bench(np, torch, api, stream):
+    """The shared experts' two prefill GEMM shapes through this library's
+    W8A8 GEMM (int8 MFMA, fp32 output with the per-row x per-channel scale
+    epilogue) and through torch._int_mm (the vendor int8 GEMM library, int32
+    output, no epilogue), same int8 operands, timed alike: a reference point
+    for the int8 main loop on these shapes."""
+    res = {}
+    for M, N, K in ((4096, 5632, 1024), (4096, 1024, 2816)):
+        g = torch.Generator(device="cuda").manual_seed(N + K)
+        A = torch.randint(-127, 128, (M, K), generator=g, device="cuda", dtype=torch.int8)
+        Bkn = torch.randint(-127, 128, (K, N), generator=g, device="cuda", dtype=torch.int8)
+        sA = torch.rand(M, generator=g, device="cuda") * 9e-3 + 1e-3
+        sB = torch.rand(N, generator=g, device="cuda") * 9e-3 + 1e-3
+        Wq = api.W8A8(Bq_kn=Bkn, sB=sB)
+        C = torch.empty(M, N, device="cuda")
+        _, ours = time_fn(torch, lambda: Wq.gemm(A, sA, C, stream), 50, 5, stream)
+        Bt = Bkn.t().contiguous().t()  # column-major B, the library's preferred layout
+        _, ven = time_fn(torch, lambda: torch._int_mm(A, Bt), 50, 5, stream)
+        ops = 2.0 * M * N * K
+        res[f"int8_gemm_{M}x{N}x{K}"] = {
+            "ours_us": ours * 1e3, "ours_tops": ops / (ours / 1e3) / 1e12,
+            "vendor_int_mm_us": ven * 1e3, "vendor_tops": ops / (ven / 1e3) / 1e12,
+            "ours_over_vendor_time": ours / ven}
+        del Wq, A, Bkn, Bt, C
+    torch.cuda.empty_cache()
     return res
 
 
