@@ -175,12 +175,19 @@ def main():
 
     # algorithmic work per stage launch
     ops = {
-        "shared_gateup": 2.0 * T * (2 * hs) * n,   # per shared expert launch
+        "shared_gateup": 2.0 * T * (2 * hs) * n,   # per shared expert
         "shared_down": 2.0 * T * n * hs,
         "routed_gateup": 2.0 * T * k * (2 * h) * n,
         "routed_down": 2.0 * T * k * n * h,
     }
-    launches = {"shared_gateup": S, "shared_down": S, "routed_gateup": 1, "routed_down": 1}
+    # the library runs the S shared gate/ups as one GEMM (gate/up panels
+    # concatenated along N) when S >= 2, T > 64 and 2 * hs fills whole
+    # 128-channel panels with S * 2 * hs a multiple of 256
+    fused = S >= 2 and T > 64 and (2 * hs) % 128 == 0 and (S * 2 * hs) % 256 == 0
+    launches = {"shared_gateup": 1 if fused else S, "shared_down": S, "routed_gateup": 1,
+                "routed_down": 1}
+    per_expert = {"shared_gateup": S, "shared_down": S, "routed_gateup": 1, "routed_down": 1}
+    ops = {st: v * per_expert[st] / launches[st] for st, v in ops.items()}  # per launch
     per_launch = {s: stages[s] / (count * launches.get(s, 1)) for s in stages}
     dom = max(ops, key=lambda s: stages[s])
     dom_ms = per_launch[dom]

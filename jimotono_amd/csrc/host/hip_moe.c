@@ -342,6 +342,14 @@ struct jt_hip_moe {
     int32_t *rnc;   /* [T] candidate counts */
     int8_t *Sqr;
     int last_T;
+    /* the shared experts' gate/ups as one GEMM (S >= 2, 2*h_shared a
+     * multiple of 128, more than 64 tokens): gate/up panels and scales
+     * concatenated along N, hidden rows [S][T][h_shared], their codes
+     * [S][T][Kph] and scales [S][T] */
+    int sh_fused;
+    int8_t *sgu_P;
+    float *sgu_s, *sS, *sss;
+    int8_t *sSq;
     /* shared experts run on a side stream forked after the input quantiser
      * and joined before the combine; expert e uses side[e % nside] */
     int nside;
@@ -350,6 +358,7 @@ struct jt_hip_moe {
     /* profiling: ring of per-forward event sets */
     int prof;
     hipEvent_t ev[PROF_RING][ST_N + 1 + 3 * JT_MOE_MAX_SHARED];
+    int ev_fused[PROF_RING]; /* the forward in this slot ran the fused shared path */
     int ev_ready;
     int ring_head, ring_count;
     double acc_ms[ST_N];
@@ -361,7 +370,8 @@ void jt_hip_moe_free(jt_hip_moe *L) {
     void *p[] = {L->Wgate, L->gu_P, L->gu_S, L->dn_P,  L->dn_S, L->Xq,   L->sx,
                  L->logits, L->w,  L->Sr,   L->ssr,  L->Ye,   L->Ys,   L->ids,
                  L->rank,  L->cnt, L->tot,  L->off,  L->perm, L->tiles, L->ntiles,
-                 L->Sqr,   L->Xl,  L->rWh,  L->rWl,  L->xinfo, L->winfo, L->approx, L->rcand, L->rnc};
+                 L->Sqr,   L->Xl,  L->rWh,  L->rWl,  L->xinfo, L->winfo, L->approx, L->rcand, L->rnc,
+                 L->sgu_P, L->sgu_s, L->sS,  L->sSq,  L->sss};
     (void)hipDeviceSynchronize();
     for (size_t i = 0; i < sizeof(p) / sizeof(p[0]); i++) (void)hipFree(p[i]);
     for (int s = 0; s < JT_MOE_MAX_SHARED; s++) jt_hip_ffn_free(L->sh[s]);
@@ -458,8 +468,33 @@ static int moe_alloc(const jt_hip_moe_desc *dp, int has_gate, jt_hip_moe **out) 
  * weights are in place. */
 static int moe_finish(jt_hip_moe *L) {
     int rc = JT_OK;
-    for (int s = 0; s < L->d.n_shared && rc == JT_OK; s++)
-        rc = ffn_reserve(L->sh[s], L->d.max_tokens, 0);
+    const int S = L->d.n_shared, T = L->d.max_tokens;
+    const jt_hip_ffn *F0 = S > 0 ? L->sh[0] : NULL;
+    /* the fused shared gate/up needs whole 256-channel tiles, no padding
+     * channels inside an expert's block, and more than 64 tokens to run */
+    L->sh_fused = S >= 2 && T > 64 && F0->Np_gu == 2 * F0->h && (S * F0->Np_gu) % 256 == 0;
+    if (L->sh_fused) {
+        const size_t gub = (size_t)F0->Np_gu * F0->Kpn, gus = (size_t)F0->Np_gu * sizeof(float);
+        hipError_t e = hipMalloc((void **)&L->sgu_P, gub * S);
+        if (e == hipSuccess) e = hipMalloc((void **)&L->sgu_s, gus * S);
+        if (e == hipSuccess) e = hipMalloc((void **)&L->sS, (size_t)S * T * F0->h * 4);
+        if (e == hipSuccess) e = hipMalloc((void **)&L->sSq, (size_t)S * T * F0->Kph);
+        if (e == hipSuccess) e = hipMalloc((void **)&L->sss, (size_t)S * T * 4);
+        /* K padding of the hidden codes stays zero (the quantiser writes
+         * only the h valid columns) */
+        if (e == hipSuccess) e = hipMemset(L->sSq, 0, (size_t)S * T * F0->Kph);
+        for (int s = 0; s < S && e == hipSuccess; s++) {
+            e = hipMemcpy(L->sgu_P + gub * s, L->sh[s]->gu_P, gub, hipMemcpyDeviceToDevice);
+            if (e == hipSuccess)
+                e = hipMemcpy((uint8_t *)L->sgu_s + gus * s, L->sh[s]->gu_s, gus,
+                              hipMemcpyDeviceToDevice);
+        }
+        if (e == hipSuccess) e = hipDeviceSynchronize(); /* before any stream uses them */
+        rc = jt_rt_err(e);
+    }
+    /* an expert's own workspace then serves only forwards of <= 64 tokens */
+    for (int s = 0; s < S && rc == JT_OK; s++)
+        rc = ffn_reserve(L->sh[s], L->sh_fused ? 64 : T, 0);
     if (rc == JT_OK && L->d.n_shared > 0) {
         const int ns = L->d.n_shared < MOE_SIDE ? L->d.n_shared : MOE_SIDE;
         hipError_t e = hipEventCreateWithFlags(&L->ev_fork, hipEventDisableTiming);
@@ -555,9 +590,10 @@ static void prof_drain_one(jt_hip_moe *L) {
     if (hipEventElapsedTime(&ms, (a), (b)) == hipSuccess) L->acc_ms[st] += ms
     for (int i = ST_QUANT_X; i < ST_R_DOWN; i++) ADD(i, ev[i], ev[i + 1]);
     ADD(ST_R_DOWN, ev[ST_R_DOWN], S > 0 ? ev[ST_N + 1] : ev[ST_COMBINE]);
-    for (int e = 0; e < S; e++) {
+    for (int e = 0; e < (L->ev_fused[slot] ? 1 : S); e++) { /* fused: one set of marks */
         hipEvent_t *x = &ev[ST_N + 1 + 3 * e];
-        hipEvent_t end = (e + 1 < S) ? ev[ST_N + 1 + 3 * (e + 1)] : ev[ST_COMBINE];
+        hipEvent_t end = (e + 1 < S && !L->ev_fused[slot]) ? ev[ST_N + 1 + 3 * (e + 1)]
+                                                          : ev[ST_COMBINE];
         ADD(ST_S_GATEUP, x[0], x[1]);
         ADD(ST_S_QUANT, x[1], x[2]);
         ADD(ST_S_DOWN, x[2], end);
@@ -581,6 +617,29 @@ static int prof_begin(jt_hip_moe *L, int *slot) {
     L->ring_head = (L->ring_head + 1) % PROF_RING;
     L->ring_count++;
     return JT_OK;
+}
+
+/* The shared experts of a forward of T > 64 tokens with the fused gate/up:
+ * one SwiGLU GEMM over all S experts (hidden rows into S planes of T x h),
+ * one row quantiser over the S*T hidden rows, then each expert's down
+ * projection into its Ys slot. ev (profiling, may be NULL): the gate/up
+ * kernel's own start/end, then the end of the quantiser. */
+static int shared_fused(jt_hip_moe *L, int T, uint32_t *err, hipStream_t s, hipEvent_t *ev) {
+    const int S = L->d.n_shared, n = L->d.n;
+    const jt_hip_ffn *F0 = L->sh[0];
+    const int h = F0->h;
+    int e = jtk_w8a8_swiglu_planes(L->Xq, F0->Kpn, L->sx, L->sgu_P, L->sgu_s, T, S * F0->Np_gu,
+                                   F0->Kpn, L->sS, h, h, (int64_t)T * h, err, s,
+                                   ev ? ev[0] : NULL, ev ? ev[1] : NULL);
+    e |= jtk_quant_rows(L->sS, (int64_t)S * T, h, L->sSq, F0->Kph, L->sss, NULL, err, s);
+    if (ev) (void)hipEventRecord(ev[2], s);
+    for (int x = 0; x < S; x++) {
+        const jt_hip_ffn *F = L->sh[x];
+        e |= jtk_w8a8_gemm(L->sSq + (size_t)x * T * F->Kph, F->Kph, L->sss + (size_t)x * T,
+                           F->d_P, F->d_s, T, n, F->Np_d, F->Kph, L->Ys + (size_t)x * T * n, n, 0,
+                           err, s);
+    }
+    return e ? jt_rt_err(hipErrorLaunchFailure) : JT_OK;
 }
 
 static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
@@ -619,14 +678,19 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
      * more than the overlap gains (measured: 80 -> 70 us per decode layer
      * in stream order), so they run in order there too. */
     const int fork = S > 0 && !L->prof && T > 16;
+    const int fused = L->sh_fused && T > 64;
+    if (L->prof) L->ev_fused[slot] = fused;
     if (fork) {
         le |= (int)hipEventRecord(L->ev_fork, s);
         for (int i = 0; i < L->nside; i++) le |= (int)hipStreamWaitEvent(L->side[i], L->ev_fork, 0);
-        for (int e = 0; e < S; e++) { /* launch errors are collected; the join still happens */
-            const ffn_ws ws = ffn_own_ws(L->sh[e]);
-            le |= ffn_run_q(L->sh[e], &ws, L->Xq, L->sx, T, L->Ys + (size_t)e * T * n, err,
-                            L->side[e % L->nside], NULL);
-        }
+        if (fused) /* launch errors are collected; the join still happens */
+            le |= shared_fused(L, T, err, L->side[0], NULL);
+        else
+            for (int e = 0; e < S; e++) {
+                const ffn_ws ws = ffn_own_ws(L->sh[e]);
+                le |= ffn_run_q(L->sh[e], &ws, L->Xq, L->sx, T, L->Ys + (size_t)e * T * n, err,
+                                L->side[e % L->nside], NULL);
+            }
         for (int i = 0; i < L->nside; i++) le |= (int)hipEventRecord(L->ev_join[i], L->side[i]);
     }
     /* 16-row tiles when experts average at most 16 rows; the single-launch
@@ -710,6 +774,9 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
     }
     if (fork) {
         for (int i = 0; i < L->nside; i++) le |= (int)hipStreamWaitEvent(s, L->ev_join[i], 0);
+    } else if (fused) {
+        rc = shared_fused(L, T, err, s, L->prof ? &L->ev[slot][ST_N + 1] : NULL);
+        if (rc != JT_OK) return rc;
     } else {
         for (int e = 0; e < S; e++) {
             hipEvent_t *ev = L->prof ? &L->ev[slot][ST_N + 1 + 3 * e] : NULL;

@@ -429,6 +429,16 @@ extern "C" int jtk_w8a8_gemm_ev(const int8_t *A, int lda, const float *sA, const
     return (int)e;
 }
 
+extern "C" int jtk_w8a8_swiglu_planes(const int8_t *A, int lda, const float *sA,
+                                      const int8_t *Wp, const float *sB, int M, int N, int Kp,
+                                      float *C, int ldc, int hpl, int64_t plane, uint32_t *err,
+                                      hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
+    if (M <= 64 || N % 256 || hpl <= 0 || hpl % 16 || (N / 2) % hpl)
+        return (int)hipErrorInvalidValue;
+    return (int)launch_w8a8_tile<EPI_SWIGLU, 128, 256, 2, 4, 1, 3, 4>(
+        A, lda, sA, Wp, sB, M, N, N, Kp, C, ldc, err, s, e0, e1, hpl, plane);
+}
+
 extern "C" int jtk_w8a8_gemm(const int8_t *A, int lda, const float *sA, const int8_t *Wp,
                              const float *sB, int M, int N, int Np, int Kp, float *C,
                              int ldc, int swiglu, uint32_t *err, hipStream_t s) {

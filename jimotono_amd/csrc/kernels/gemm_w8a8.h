@@ -100,11 +100,15 @@ __device__ __forceinline__ void tile_coords(int lin, int mtiles, int ntiles, int
 //   EPI_PLAIN : C[row][col] = (float)((double)acc * ((double)sA[row] * sB[col]))
 //   EPI_SWIGLU: channels packed [gate 16][up 16] per 32 (tile 2jj gate, 2jj+1
 //               up); C[row][hidden] = silu(g) * u in fp64, rounded to float.
+//               With hpl > 0 the hidden columns are hpl-wide planes (one per
+//               expert whose gate/up panels are concatenated along N):
+//               hidden x goes to C[(x / hpl) * plane + row * ldc + x % hpl].
 template <int EPI, int TM, int TN, int HALF>
 __device__ __forceinline__ void w8a8_epilogue(const v4i (&acc)[TM][TN], int part, int r0, int c0,
                                               int lane, const float *rs, const float *cs,
                                               int M, int N, float *__restrict__ C, int ldc,
-                                              uint32_t *err, const double *exp_tab) {
+                                              int hpl, int64_t plane, uint32_t *err,
+                                              const double *exp_tab) {
     const int lr = (lane >> 4) * 4, lc = lane & 15;
     // The scales (rs: this wave tile's rows, cs: its columns) and the exp
     // table were copied to LDS with the first stage, so the epilogue issues
@@ -121,6 +125,14 @@ __device__ __forceinline__ void w8a8_epilogue(const v4i (&acc)[TM][TN], int part
     const bool full = r0 + 16 * TM <= M && c0 + 16 * TN <= N;
     uint32_t bad = 0, badmid = 0;
     if (EPI == EPI_SWIGLU) {
+        // pointer shift of each 16-wide hidden block into its plane
+        // (wave-uniform; hpl is a multiple of 16)
+        int64_t pofs[TN / 2];
+#pragma unroll
+        for (int jj = 0; jj < TN / 2; jj++) {
+            const int x0 = c0 / 2 + jj * 16;
+            pofs[jj] = hpl > 0 ? (int64_t)(x0 / hpl) * plane + (x0 % hpl) - x0 : 0;
+        }
         // A non-finite g or u (the only way silu_mul fails) shows as a
         // maximum of the sign-cleared bit patterns at or above that of +inf.
         uint32_t mx = 0;
@@ -141,7 +153,7 @@ __device__ __forceinline__ void w8a8_epilogue(const v4i (&acc)[TM][TN], int part
                 for (int r = 0; r < 4; r++) {
                     float *crow = C + (int64_t)(r0 + i * 16 + lr + r) * ldc + c0 / 2 + lc;
 #pragma unroll
-                    for (int jj = 0; jj < TN / 2; jj++) one(i, r, jj, crow + jj * 16);
+                    for (int jj = 0; jj < TN / 2; jj++) one(i, r, jj, crow + jj * 16 + pofs[jj]);
                 }
             }
         } else {
@@ -154,7 +166,8 @@ __device__ __forceinline__ void w8a8_epilogue(const v4i (&acc)[TM][TN], int part
                     float *crow = C + (int64_t)row * ldc + c0 / 2 + lc;
 #pragma unroll
                     for (int jj = 0; jj < TN / 2; jj++)
-                        if (row < M && c0 + (2 * jj + 1) * 16 + lc < N) one(i, r, jj, crow + jj * 16);
+                        if (row < M && c0 + (2 * jj + 1) * 16 + lc < N)
+                            one(i, r, jj, crow + jj * 16 + pofs[jj]);
                 }
             }
         }
@@ -206,7 +219,8 @@ template <int EPI, int BM, int BN, int WGM, int WGN, int KS, int NST, int GM>
 __global__ __launch_bounds__(64 * WGM * WGN * KS) void k_w8a8_tile(
     const int8_t *__restrict__ A, int lda, const float *__restrict__ sA,
     const int8_t *__restrict__ Wp, const float *__restrict__ sB, int M, int N, int Kp,
-    float *__restrict__ C, int ldc, uint32_t *err, int mtiles, int ntiles) {
+    float *__restrict__ C, int ldc, int hpl, int64_t plane, uint32_t *err, int mtiles,
+    int ntiles) {
     constexpr int NWG = WGM * WGN;  // waves per k-group
     constexpr int WTM = BM / WGM, WTN = BN / WGN;
     constexpr int TM = WTM / 16, TN = WTN / 16;
@@ -330,7 +344,8 @@ __global__ __launch_bounds__(64 * WGM * WGN * KS) void k_w8a8_tile(
     }
     if (EPI == EPI_SWIGLU) exp_tab_stage(s_tab, lane, tabv);
     w8a8_epilogue<EPI, TM, TN, KS == 2 ? TE : 0>(acc, kg, m0 + wm, n0 + wn, lane, s_rs + wm,
-                                                  s_cs + wn, M, N, C, ldc, err, s_tab);
+                                                  s_cs + wn, M, N, C, ldc, hpl, plane, err,
+                                                  s_tab);
 }
 
 // Host-side launch of one configuration (dynamic LDS = NST stages). Non-null
@@ -341,7 +356,8 @@ template <int EPI, int BM, int BN, int WGM, int WGN, int KS, int NST, int GM>
 inline hipError_t launch_w8a8_tile(const int8_t *A, int lda, const float *sA, const int8_t *Wp,
                                    const float *sB, int M, int N, int Np, int Kp, float *C,
                                    int ldc, uint32_t *err, hipStream_t s,
-                                   hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr) {
+                                   hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr,
+                                   int hpl = 0, int64_t plane = 0) {
     auto kern = k_w8a8_tile<EPI, BM, BN, WGM, WGN, KS, NST, GM>;
     constexpr int lds = NST * (BM + BN) / 16 * KS * 1024;
     // dynamic LDS above 64 KiB must be enabled per device, once
@@ -358,6 +374,7 @@ inline hipError_t launch_w8a8_tile(const int8_t *A, int lda, const float *sA, co
     }
     const int mt = (M + BM - 1) / BM, nt = Np / BN;
     hipExtLaunchKernelGGL(kern, dim3((unsigned)(mt * nt)), dim3(64 * WGM * WGN * KS), lds, s,
-                          e0, e1, 0, A, lda, sA, Wp, sB, M, N, Kp, C, ldc, err, mt, nt);
+                          e0, e1, 0, A, lda, sA, Wp, sB, M, N, Kp, C, ldc, hpl, plane, err, mt,
+                          nt);
     return hipGetLastError();
 }

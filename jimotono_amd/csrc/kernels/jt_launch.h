@@ -58,6 +58,15 @@ int jtk_w8a8_gemm(const int8_t *A, int lda, const float *sA, const int8_t *Wp,
 int jtk_w8a8_gemm_ev(const int8_t *A, int lda, const float *sA, const int8_t *Wp,
                      const float *sB, int M, int N, int Np, int Kp, float *C, int ldc,
                      int swiglu, uint32_t *err, hipStream_t s, hipEvent_t e0, hipEvent_t e1);
+/* The SwiGLU GEMM of several experts whose interleaved gate/up panels are
+ * concatenated along N (each expert 2*hpl channels, N % 256 == 0): hidden
+ * column x of row m goes to C[(x / hpl) * plane + m * ldc + x % hpl], one
+ * plane per expert. M > 64 only (128 x 256 tiles); hipErrorInvalidValue
+ * (nothing launched) otherwise. e0 / e1 as in jtk_w8a8_gemm_ev. */
+int jtk_w8a8_swiglu_planes(const int8_t *A, int lda, const float *sA, const int8_t *Wp,
+                           const float *sB, int M, int N, int Kp, float *C, int ldc, int hpl,
+                           int64_t plane, uint32_t *err, hipStream_t s, hipEvent_t e0,
+                           hipEvent_t e1);
 /* M <= 16 on fp32 activations X [M][ldx] (K valid columns): each block
  * quantises the rows itself with the row quantiser's arithmetic.
  * hipErrorInvalidValue (nothing launched) unless K % 4 == 0, K <= 4096

@@ -81,6 +81,10 @@ def check_hidden(jt, L, o, T, k, n, h, max_frac=0.01):
 CASES = [
     # n, h, E, k, S, hs, T
     (128, 64, 8, 2, 2, 64, 37),
+    # the shared experts' gate/ups as one GEMM (S >= 2, T > 64, whole
+    # 256-channel tiles over the concatenated gate/up panels)
+    (256, 128, 16, 4, 2, 128, 100),
+    (128, 64, 8, 2, 4, 64, 130),
     (256, 128, 16, 4, 1, 192, 200),
     (128, 64, 32, 8, 0, 64, 16),
     (256, 64, 64, 8, 2, 128, 1),
