@@ -339,8 +339,11 @@ __global__ __launch_bounds__(256) void k_gdn2_prep(const float *__restrict__ Q,
 // values in registers; phase 3 Out_t += sum_{s<=t} P[t][s] E_s; phase 4
 // thread (i, column) S[i] <- CF[C-1][i] S[i] + sum_s WG[s][i] E_s
 // (src/gdn2.c:614-680, 716-842). CL: each chunk's record is staged in LDS
-// and the block's S tile stays in LDS from the first chunk to the last.
-template <int C, bool CL>
+// and the block's S tile stays in LDS from the first chunk to the last;
+// with dk % 4 == 0 the next chunk's record (and the thread's v*w value)
+// is loaded into registers with 16-byte loads while the current chunk
+// computes, so a chunk does not wait on its record's memory latency.
+template <int C, bool CL, bool PF>
 __global__ __launch_bounds__(256) void k_gdn2_cols(float *__restrict__ S, float *__restrict__ Out,
                                                    const float *__restrict__ V,
                                                    const float *__restrict__ W, int64_t hv,
@@ -351,8 +354,9 @@ __global__ __launch_bounds__(256) void k_gdn2_cols(float *__restrict__ S, float 
     constexpr int NL = CL ? CHUNK_LDS + 4 * 32 : 1;
     __shared__ float G[C][NC], Ob[C][NC];
     // the S tile: dk*NC <= CHUNK_LDS*NC/C values when C*dk <= CHUNK_LDS
-    __shared__ float wi_l[NL], qi_l[NL], wg_l[NL], s_l[CL ? CHUNK_LDS * NC / C : 1];
-    __shared__ float lp_l[CL ? 2 * C * C : 1], cf_l[CL ? 1024 : 1];
+    __shared__ __attribute__((aligned(16))) float wi_l[NL], qi_l[NL], wg_l[NL];
+    __shared__ float s_l[CL ? CHUNK_LDS * NC / C : 1];
+    __shared__ __attribute__((aligned(16))) float lp_l[CL ? 2 * C * C : 1], cf_l[CL ? 1024 : 1];
     const int h = blockIdx.x, j0 = blockIdx.y * NC, tid = threadIdx.x, lk = dk + 4;
     if (flag[h]) return;  // a rejected head keeps its S and Out
     const int64_t Ck = (int64_t)C * dk;
@@ -367,11 +371,64 @@ __global__ __launch_bounds__(256) void k_gdn2_cols(float *__restrict__ S, float 
             s_l[n] = cc < ncol ? Sh[(int64_t)i * dv + j0 + cc] : 0.0f;
         }
     }
+    // register prefetch of a chunk's record (PF: CL and dk % 4 == 0): thread
+    // tid's float4 f = tid + 256u (u < 4) of WI, QI and WG [C][dk], of L and
+    // P, and of CF's last row; indices past an array are clamped to its last
+    // element (loaded, never stored), so every register is always written
+    constexpr bool pf = PF;
+    static_assert(!PF || (CL && CHUNK_LDS / 4 / 256 == 4 && 2 * C * C / 4 <= 512),
+                  "the prefetch holds 4 float4 of each [C][dk] array and 2 of L, P");
+    const int n4 = (int)(Ck / 4), nlp = C * C / 2;
+    float4 wi0, wi1, wi2, wi3, qi0, qi1, qi2, qi3, wg0, wg1, wg2, wg3, lp0, lp1, cf4;
+    float pvw = 0.0f;
+#define GDN2_PF(cc)                                                                           \
+    do {                                                                                      \
+        const float4 *r4 =                                                                    \
+            (const float4 *)(rec + ((int64_t)h * nch + (cc)) * chunk_rec_floats(C, dk));      \
+        int f_ = min(tid, n4 - 1);                                                            \
+        wi0 = r4[n4 + f_], qi0 = r4[2 * n4 + f_], wg0 = r4[3 * n4 + f_];                      \
+        f_ = min(tid + 256, n4 - 1);                                                          \
+        wi1 = r4[n4 + f_], qi1 = r4[2 * n4 + f_], wg1 = r4[3 * n4 + f_];                      \
+        f_ = min(tid + 512, n4 - 1);                                                          \
+        wi2 = r4[n4 + f_], qi2 = r4[2 * n4 + f_], wg2 = r4[3 * n4 + f_];                      \
+        f_ = min(tid + 768, n4 - 1);                                                          \
+        wi3 = r4[n4 + f_], qi3 = r4[2 * n4 + f_], wg3 = r4[3 * n4 + f_];                      \
+        lp0 = r4[4 * n4 + min(tid, nlp - 1)];                                                 \
+        lp1 = r4[4 * n4 + min(tid + 256, nlp - 1)];                                           \
+        cf4 = r4[(C - 1) * dk / 4 + min(tid, dk / 4 - 1)];                                    \
+        if (live) {                                                                           \
+            const int64_t vq = h * hv + ((int64_t)(cc) * C + t) * dv + j;                     \
+            pvw = W[vq] * V[vq];                                                              \
+        }                                                                                     \
+    } while (0)
+#define GDN2_PF_PUT(u, a, b, g)                                                               \
+    do {                                                                                      \
+        const int f_ = tid + 256 * (u);                                                       \
+        if (f_ < n4) {                                                                        \
+            const int at_ = (4 * f_ / dk) * lk + 4 * f_ % dk;                                 \
+            *(float4 *)(wi_l + at_) = a;                                                      \
+            *(float4 *)(qi_l + at_) = b;                                                      \
+            *(float4 *)(wg_l + at_) = g;                                                      \
+        }                                                                                     \
+    } while (0)
+    if constexpr (pf) GDN2_PF(0);
     for (int c = 0; c < nch; c++) {
         const float *r = rec + ((int64_t)h * nch + c) * chunk_rec_floats(C, dk);
         const float *CF = r, *WI = CF + Ck, *QI = WI + Ck, *WG = QI + Ck;
         const float *L = WG + Ck, *P = L + C * C;
-        if (CL) {
+        float vw0 = 0.0f;
+        if constexpr (pf) {
+            GDN2_PF_PUT(0, wi0, qi0, wg0);
+            GDN2_PF_PUT(1, wi1, qi1, wg1);
+            GDN2_PF_PUT(2, wi2, qi2, wg2);
+            GDN2_PF_PUT(3, wi3, qi3, wg3);
+            if (tid < nlp) *(float4 *)(lp_l + 4 * tid) = lp0;  // L then P
+            if (tid + 256 < nlp) *(float4 *)(lp_l + 4 * (tid + 256)) = lp1;
+            if (tid < dk / 4) *(float4 *)(cf_l + 4 * tid) = cf4;
+            vw0 = pvw;
+            __syncthreads();
+            if (c + 1 < nch) GDN2_PF(c + 1);  // in flight through this chunk's phases
+        } else if (CL) {
             for (int64_t n = tid; n < Ck; n += 256) {
                 const int tt = (int)(n / dk), i = (int)(n % dk);
                 wi_l[tt * lk + i] = WI[n];
@@ -386,7 +443,7 @@ __global__ __launch_bounds__(256) void k_gdn2_cols(float *__restrict__ S, float 
         const float *L_b = CL ? lp_l : L, *P_b = CL ? lp_l + C * C : P;
         const int64_t vo = h * hv + ((int64_t)c * C + t) * dv + j;
         if (live) {
-            float g = W[vo] * V[vo];  // vw_t
+            float g = pf ? vw0 : W[vo] * V[vo];  // vw_t
             float o = 0.0f;
             const float *wi = wi_b + t * ld, *qi = qi_b + t * ld;
 #pragma unroll 8
@@ -437,6 +494,8 @@ __global__ __launch_bounds__(256) void k_gdn2_cols(float *__restrict__ S, float 
         }
     }
 }
+#undef GDN2_PF
+#undef GDN2_PF_PUT
 
 }  // namespace
 
@@ -488,18 +547,25 @@ extern "C" int jtk_gdn2_prefill(float *S, float *Out, const float *Q, const floa
         hipLaunchKernelGGL(k_gdn2_prep<false>, dim3((unsigned)nch, (unsigned)H), dim3(256), 0, s,
                            Q, K, B, A, hk, C, dk, flag, rec);
     const dim3 grid((unsigned)H, (unsigned)((dv + 256 / C - 1) / (256 / C)));
-    if (C == 16 && cl)
-        hipLaunchKernelGGL((k_gdn2_cols<16, true>), grid, dim3(256), 0, s, S, Out, V, W, hv, nch,
-                           dk, dv, flag, rec);
+    const bool v4 = dk % 4 == 0;  // the record prefetch with 16-byte loads
+    if (C == 16 && cl && v4)
+        hipLaunchKernelGGL((k_gdn2_cols<16, true, true>), grid, dim3(256), 0, s, S, Out, V, W, hv,
+                           nch, dk, dv, flag, rec);
+    else if (C == 32 && cl && v4)
+        hipLaunchKernelGGL((k_gdn2_cols<32, true, true>), grid, dim3(256), 0, s, S, Out, V, W, hv,
+                           nch, dk, dv, flag, rec);
+    else if (C == 16 && cl)
+        hipLaunchKernelGGL((k_gdn2_cols<16, true, false>), grid, dim3(256), 0, s, S, Out, V, W,
+                           hv, nch, dk, dv, flag, rec);
     else if (C == 16)
-        hipLaunchKernelGGL((k_gdn2_cols<16, false>), grid, dim3(256), 0, s, S, Out, V, W, hv, nch,
-                           dk, dv, flag, rec);
+        hipLaunchKernelGGL((k_gdn2_cols<16, false, false>), grid, dim3(256), 0, s, S, Out, V, W,
+                           hv, nch, dk, dv, flag, rec);
     else if (cl)
-        hipLaunchKernelGGL((k_gdn2_cols<32, true>), grid, dim3(256), 0, s, S, Out, V, W, hv, nch,
-                           dk, dv, flag, rec);
+        hipLaunchKernelGGL((k_gdn2_cols<32, true, false>), grid, dim3(256), 0, s, S, Out, V, W,
+                           hv, nch, dk, dv, flag, rec);
     else
-        hipLaunchKernelGGL((k_gdn2_cols<32, false>), grid, dim3(256), 0, s, S, Out, V, W, hv, nch,
-                           dk, dv, flag, rec);
+        hipLaunchKernelGGL((k_gdn2_cols<32, false, false>), grid, dim3(256), 0, s, S, Out, V, W,
+                           hv, nch, dk, dv, flag, rec);
     return le | (int)hipGetLastError();
 }
 
