@@ -342,13 +342,13 @@ struct jt_hip_moe {
     int32_t *rnc;   /* [T] candidate counts */
     int8_t *Sqr;
     int last_T;
-    /* the shared experts' gate/ups as one GEMM (S >= 2, 2*h_shared a
-     * multiple of 128, more than 64 tokens): gate/up panels and scales
-     * concatenated along N, hidden rows [S][T][h_shared], their codes
-     * [S][T][Kph] and scales [S][T] */
-    int sh_fused;
-    int8_t *sgu_P;
-    float *sgu_s, *sS, *sss;
+    /* the shared experts as batched GEMMs (S >= 2, 2*h_shared a multiple of
+     * 128): gate/up panels and scales concatenated along N, down panels and
+     * scales back to back, hidden rows [S][T][h_shared]; for more than 64
+     * tokens also their codes [S][T][Kph] and scales [S][T] */
+    int sh_cat;
+    int8_t *sgu_P, *sd_P;
+    float *sgu_s, *sd_s, *sS, *sss;
     int8_t *sSq;
     /* shared experts run on a side stream forked after the input quantiser
      * and joined before the combine; expert e uses side[e % nside] */
@@ -371,7 +371,7 @@ void jt_hip_moe_free(jt_hip_moe *L) {
                  L->logits, L->w,  L->Sr,   L->ssr,  L->Ye,   L->Ys,   L->ids,
                  L->rank,  L->cnt, L->tot,  L->off,  L->perm, L->tiles, L->ntiles,
                  L->Sqr,   L->Xl,  L->rWh,  L->rWl,  L->xinfo, L->winfo, L->approx, L->rcand, L->rnc,
-                 L->sgu_P, L->sgu_s, L->sS,  L->sSq,  L->sss};
+                 L->sgu_P, L->sgu_s, L->sS,  L->sSq,  L->sss,  L->sd_P,  L->sd_s};
     (void)hipDeviceSynchronize();
     for (size_t i = 0; i < sizeof(p) / sizeof(p[0]); i++) (void)hipFree(p[i]);
     for (int s = 0; s < JT_MOE_MAX_SHARED; s++) jt_hip_ffn_free(L->sh[s]);
@@ -470,31 +470,40 @@ static int moe_finish(jt_hip_moe *L) {
     int rc = JT_OK;
     const int S = L->d.n_shared, T = L->d.max_tokens;
     const jt_hip_ffn *F0 = S > 0 ? L->sh[0] : NULL;
-    /* the fused shared gate/up needs whole 256-channel tiles, no padding
-     * channels inside an expert's block, and more than 64 tokens to run */
-    L->sh_fused = S >= 2 && T > 64 && F0->Np_gu == 2 * F0->h && (S * F0->Np_gu) % 256 == 0;
-    if (L->sh_fused) {
+    /* batched shared experts: whole 256-channel gate/up tiles over the
+     * concatenated panels and no padding channels inside an expert's block */
+    L->sh_cat = S >= 2 && F0->Np_gu == 2 * F0->h && (S * F0->Np_gu) % 256 == 0;
+    if (L->sh_cat) {
         const size_t gub = (size_t)F0->Np_gu * F0->Kpn, gus = (size_t)F0->Np_gu * sizeof(float);
+        const size_t db = (size_t)F0->Np_d * F0->Kph, ds = (size_t)F0->Np_d * sizeof(float);
         hipError_t e = hipMalloc((void **)&L->sgu_P, gub * S);
         if (e == hipSuccess) e = hipMalloc((void **)&L->sgu_s, gus * S);
+        if (e == hipSuccess) e = hipMalloc((void **)&L->sd_P, db * S);
+        if (e == hipSuccess) e = hipMalloc((void **)&L->sd_s, ds * S);
         if (e == hipSuccess) e = hipMalloc((void **)&L->sS, (size_t)S * T * F0->h * 4);
-        if (e == hipSuccess) e = hipMalloc((void **)&L->sSq, (size_t)S * T * F0->Kph);
-        if (e == hipSuccess) e = hipMalloc((void **)&L->sss, (size_t)S * T * 4);
-        /* K padding of the hidden codes stays zero (the quantiser writes
-         * only the h valid columns) */
-        if (e == hipSuccess) e = hipMemset(L->sSq, 0, (size_t)S * T * F0->Kph);
+        if (T > 64) {
+            if (e == hipSuccess) e = hipMalloc((void **)&L->sSq, (size_t)S * T * F0->Kph);
+            if (e == hipSuccess) e = hipMalloc((void **)&L->sss, (size_t)S * T * 4);
+            /* K padding of the hidden codes stays zero (the quantiser writes
+             * only the h valid columns) */
+            if (e == hipSuccess) e = hipMemset(L->sSq, 0, (size_t)S * T * F0->Kph);
+        }
         for (int s = 0; s < S && e == hipSuccess; s++) {
-            e = hipMemcpy(L->sgu_P + gub * s, L->sh[s]->gu_P, gub, hipMemcpyDeviceToDevice);
+            const jt_hip_ffn *F = L->sh[s];
+            e = hipMemcpy(L->sgu_P + gub * s, F->gu_P, gub, hipMemcpyDeviceToDevice);
             if (e == hipSuccess)
-                e = hipMemcpy((uint8_t *)L->sgu_s + gus * s, L->sh[s]->gu_s, gus,
+                e = hipMemcpy((uint8_t *)L->sgu_s + gus * s, F->gu_s, gus,
                               hipMemcpyDeviceToDevice);
+            if (e == hipSuccess) e = hipMemcpy(L->sd_P + db * s, F->d_P, db, hipMemcpyDeviceToDevice);
+            if (e == hipSuccess)
+                e = hipMemcpy((uint8_t *)L->sd_s + ds * s, F->d_s, ds, hipMemcpyDeviceToDevice);
         }
         if (e == hipSuccess) e = hipDeviceSynchronize(); /* before any stream uses them */
         rc = jt_rt_err(e);
     }
     /* an expert's own workspace then serves only forwards of <= 64 tokens */
     for (int s = 0; s < S && rc == JT_OK; s++)
-        rc = ffn_reserve(L->sh[s], L->sh_fused ? 64 : T, 0);
+        rc = ffn_reserve(L->sh[s], L->sh_cat ? 64 : T, 0);
     if (rc == JT_OK && L->d.n_shared > 0) {
         const int ns = L->d.n_shared < MOE_SIDE ? L->d.n_shared : MOE_SIDE;
         hipError_t e = hipEventCreateWithFlags(&L->ev_fork, hipEventDisableTiming);
@@ -642,6 +651,28 @@ static int shared_fused(jt_hip_moe *L, int T, uint32_t *err, hipStream_t s, hipE
     return e ? jt_rt_err(hipErrorLaunchFailure) : JT_OK;
 }
 
+/* The shared experts of a forward of T <= 16 tokens, batched: one skinny
+ * SwiGLU GEMM over the concatenated gate/up panels (hidden rows into S
+ * planes of T x h), then one launch of the S down projections, each block
+ * quantising its expert's hidden rows itself. ev as in shared_fused. */
+static int shared_fused16(jt_hip_moe *L, int T, uint32_t *err, hipStream_t s, hipEvent_t *ev) {
+    const int S = L->d.n_shared, n = L->d.n;
+    const jt_hip_ffn *F0 = L->sh[0];
+    const int h = F0->h;
+    if (ev) (void)hipEventRecord(ev[0], s);
+    int e = jtk_w8a8_skinny_swiglu_planes(L->Xq, F0->Kpn, L->sx, L->sgu_P, L->sgu_s, T,
+                                          S * F0->Np_gu, F0->Kpn, L->sS, h, h, (int64_t)T * h,
+                                          err, s);
+    if (ev) {
+        (void)hipEventRecord(ev[1], s);
+        (void)hipEventRecord(ev[2], s);
+    }
+    e |= jtk_w8a8_gemm_xq_batch(L->sS, h, h, (int64_t)T * h, L->sd_P, (int64_t)F0->Np_d * F0->Kph,
+                                L->sd_s, F0->Np_d, T, n, F0->Np_d, F0->Kph, L->Ys, n,
+                                (int64_t)T * n, S, err, s);
+    return e ? jt_rt_err(hipErrorLaunchFailure) : JT_OK;
+}
+
 static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
                        const float *d_w, const float *dR, float *dY, int T, void *stream) {
     const jt_hip_moe_desc *d = &L->d;
@@ -678,8 +709,8 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
      * more than the overlap gains (measured: 80 -> 70 us per decode layer
      * in stream order), so they run in order there too. */
     const int fork = S > 0 && !L->prof && T > 16;
-    const int fused = L->sh_fused && T > 64;
-    if (L->prof) L->ev_fused[slot] = fused;
+    const int fused = L->sh_cat && T > 64, fused16 = L->sh_cat && T <= 16;
+    if (L->prof) L->ev_fused[slot] = fused || fused16;
     if (fork) {
         le |= (int)hipEventRecord(L->ev_fork, s);
         for (int i = 0; i < L->nside; i++) le |= (int)hipStreamWaitEvent(L->side[i], L->ev_fork, 0);
@@ -774,8 +805,9 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
     }
     if (fork) {
         for (int i = 0; i < L->nside; i++) le |= (int)hipStreamWaitEvent(s, L->ev_join[i], 0);
-    } else if (fused) {
-        rc = shared_fused(L, T, err, s, L->prof ? &L->ev[slot][ST_N + 1] : NULL);
+    } else if (fused || fused16) {
+        hipEvent_t *ev = L->prof ? &L->ev[slot][ST_N + 1] : NULL;
+        rc = fused ? shared_fused(L, T, err, s, ev) : shared_fused16(L, T, err, s, ev);
         if (rc != JT_OK) return rc;
     } else {
         for (int e = 0; e < S; e++) {

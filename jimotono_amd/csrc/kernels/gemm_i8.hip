@@ -41,11 +41,30 @@
 // there, so a decode-sized expert needs no separate quantiser launch. The
 // rows are re-quantised by every block; at M <= 16 that is at most 16 * K
 // floats read from L2 per block.
+//
+// SkBatch (all zero for one GEMM): blockIdx.y selects one of gridDim.y
+// GEMMs whose A (bytes), weight panels (bytes), sB and C (floats) lie at
+// fixed strides (the shared experts' down projections in one launch), and
+// hpl > 0 sends SwiGLU hidden column x to C[(x / hpl) * plane + m * ldc +
+// x % hpl] (the shared experts' gate/ups over concatenated panels).
+struct SkBatch {
+    int hpl;
+    int64_t plane, bsA, bsW;
+    int bsB;
+    int64_t bsC;
+};
+
 template <int EPI, int NP, int QV>  // QV > 0: QA with K <= 256 * QV
 __global__ __launch_bounds__(64 * SK_WAVES) void k_w8a8_skinny(
     const void *__restrict__ Ain, int lda, const float *__restrict__ sAin,
     const int8_t *__restrict__ Wp, const float *__restrict__ sB, int M, int N, int Kp, int K,
-    float *__restrict__ C, int ldc, uint32_t *err) {
+    float *__restrict__ C, int ldc, uint32_t *err, SkBatch bt) {
+    if (blockIdx.y) {  // the blockIdx.y-th GEMM of a batch
+        Ain = (const int8_t *)Ain + blockIdx.y * bt.bsA;
+        Wp += blockIdx.y * bt.bsW;
+        sB += (int64_t)blockIdx.y * bt.bsB;
+        C += blockIdx.y * bt.bsC;
+    }
     __shared__ v4i red[SK_WAVES][NP][64];
     extern __shared__ __attribute__((aligned(16))) int8_t sk_aq[];  // QA: [16][Kp + 16]
     __shared__ float sk_sa[16];
@@ -209,7 +228,9 @@ __global__ __launch_bounds__(64 * SK_WAVES) void k_w8a8_skinny(
             bad |= (!isfinite(g)) || (!isfinite(u));
             float sv;
             badmid |= !silu_mul(g, u, &sv);
-            C[(int64_t)m * ldc + blockIdx.x * 16 + lc] = sv;
+            const int x0 = blockIdx.x * 16;  // this block's first hidden column
+            const int64_t at = bt.hpl > 0 ? (int64_t)(x0 / bt.hpl) * bt.plane + x0 % bt.hpl : x0;
+            C[(int64_t)m * ldc + at + lc] = sv;
         }
     }
     if (bad) raise_err(err, EF_RANGE);
@@ -327,7 +348,8 @@ __global__ __launch_bounds__(64 * R64_WAVES) void k_w8a8_rows64(
 template <int QV>
 static hipError_t launch_skinny_xq(const float *X, int ldx, int K, const int8_t *Wp,
                                    const float *sB, int M, int N, int Np, int Kp, float *C,
-                                   int ldc, int swiglu, uint32_t *err, hipStream_t s) {
+                                   int ldc, int swiglu, uint32_t *err, hipStream_t s,
+                                   unsigned nb = 1, SkBatch bt = SkBatch{}) {
     const size_t lds = (size_t)16 * (Kp + 16);
     static std::atomic<bool> attr_set[64];  // set once per device; a repeat is harmless
     int dev = 0;
@@ -349,13 +371,13 @@ static hipError_t launch_skinny_xq(const float *X, int ldx, int K, const int8_t 
         if constexpr (QV <= 12)
             hipLaunchKernelGGL((k_w8a8_skinny<EPI_SWIGLU, 2, QV>), dim3((unsigned)(Np / 32)),
                                dim3(64 * SK_WAVES), lds, s, (const void *)X, ldx,
-                               (const float *)NULL, Wp, sB, M, N, Kp, K, C, ldc, err);
+                               (const float *)NULL, Wp, sB, M, N, Kp, K, C, ldc, err, SkBatch{});
         else
             return hipErrorInvalidValue;
     } else
-        hipLaunchKernelGGL((k_w8a8_skinny<EPI_PLAIN, 1, QV>), dim3((unsigned)(Np / 16)),
+        hipLaunchKernelGGL((k_w8a8_skinny<EPI_PLAIN, 1, QV>), dim3((unsigned)(Np / 16), nb),
                            dim3(64 * SK_WAVES), lds, s, (const void *)X, ldx, (const float *)NULL,
-                           Wp, sB, M, N, Kp, K, C, ldc, err);
+                           Wp, sB, M, N, Kp, K, C, ldc, err, bt);
     return hipGetLastError();
 }
 
@@ -389,11 +411,11 @@ extern "C" int jtk_w8a8_gemm_ev(const int8_t *A, int lda, const float *sA, const
         if (swiglu)
             hipLaunchKernelGGL((k_w8a8_skinny<EPI_SWIGLU, 2, 0>), dim3((unsigned)(Np / 32)),
                                dim3(64 * SK_WAVES), 0, s, (const void *)A, lda, sA, Wp, sB, M, N,
-                               Kp, Kp, C, ldc, err);
+                               Kp, Kp, C, ldc, err, SkBatch{});
         else
             hipLaunchKernelGGL((k_w8a8_skinny<EPI_PLAIN, 1, 0>), dim3((unsigned)(Np / 16)),
                                dim3(64 * SK_WAVES), 0, s, (const void *)A, lda, sA, Wp, sB, M, N,
-                               Kp, Kp, C, ldc, err);
+                               Kp, Kp, C, ldc, err, SkBatch{});
     } else if (M <= 64) {  // measured: 1.7-2.5x faster than the 128-row tiles
         if (swiglu)
             hipLaunchKernelGGL((k_w8a8_rows64<EPI_SWIGLU, 2>), dim3((unsigned)(Np / 32)),
@@ -437,6 +459,47 @@ extern "C" int jtk_w8a8_swiglu_planes(const int8_t *A, int lda, const float *sA,
         return (int)hipErrorInvalidValue;
     return (int)launch_w8a8_tile<EPI_SWIGLU, 128, 256, 2, 4, 1, 3, 4>(
         A, lda, sA, Wp, sB, M, N, N, Kp, C, ldc, err, s, e0, e1, hpl, plane);
+}
+
+extern "C" int jtk_w8a8_skinny_swiglu_planes(const int8_t *A, int lda, const float *sA,
+                                             const int8_t *Wp, const float *sB, int M, int N,
+                                             int Kp, float *C, int ldc, int hpl, int64_t plane,
+                                             uint32_t *err, hipStream_t s) {
+    if (M <= 0 || M > 16 || N % 32 || hpl <= 0 || hpl % 16 || (N / 2) % hpl)
+        return (int)hipErrorInvalidValue;
+    SkBatch bt{};
+    bt.hpl = hpl;
+    bt.plane = plane;
+    hipLaunchKernelGGL((k_w8a8_skinny<EPI_SWIGLU, 2, 0>), dim3((unsigned)(N / 32)),
+                       dim3(64 * SK_WAVES), 0, s, (const void *)A, lda, sA, Wp, sB, M, N, Kp, Kp,
+                       C, ldc, err, bt);
+    return (int)hipGetLastError();
+}
+
+extern "C" int jtk_w8a8_gemm_xq_batch(const float *X, int ldx, int K, int64_t sX,
+                                      const int8_t *Wp, int64_t sW, const float *sB, int ssB,
+                                      int M, int N, int Np, int Kp, float *C, int ldc,
+                                      int64_t sC, int nb, uint32_t *err, hipStream_t s) {
+    if (M <= 0 || nb <= 0) return 0;
+    if (M > 16 || K <= 0 || K > Kp || Kp % 64 || K % 4 || K > 4096 || ldx % 4 || sX % 4 ||
+        ((uintptr_t)X & 15) || (size_t)16 * (Kp + 16) > 96 * 1024 || nb > 65535)
+        return (int)hipErrorInvalidValue;
+    SkBatch bt{};
+    bt.bsA = sX * (int64_t)sizeof(float);
+    bt.bsW = sW;
+    bt.bsB = ssB;
+    bt.bsC = sC;
+    const int nv = (K + 255) / 256;
+    hipError_t e;
+    if (nv <= 4)
+        e = launch_skinny_xq<4>(X, ldx, K, Wp, sB, M, N, Np, Kp, C, ldc, 0, err, s, nb, bt);
+    else if (nv <= 8)
+        e = launch_skinny_xq<8>(X, ldx, K, Wp, sB, M, N, Np, Kp, C, ldc, 0, err, s, nb, bt);
+    else if (nv <= 12)
+        e = launch_skinny_xq<12>(X, ldx, K, Wp, sB, M, N, Np, Kp, C, ldc, 0, err, s, nb, bt);
+    else
+        e = launch_skinny_xq<16>(X, ldx, K, Wp, sB, M, N, Np, Kp, C, ldc, 0, err, s, nb, bt);
+    return (int)e;
 }
 
 extern "C" int jtk_w8a8_gemm(const int8_t *A, int lda, const float *sA, const int8_t *Wp,

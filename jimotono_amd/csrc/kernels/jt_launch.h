@@ -67,6 +67,18 @@ int jtk_w8a8_swiglu_planes(const int8_t *A, int lda, const float *sA, const int8
                            const float *sB, int M, int N, int Kp, float *C, int ldc, int hpl,
                            int64_t plane, uint32_t *err, hipStream_t s, hipEvent_t e0,
                            hipEvent_t e1);
+/* The skinny SwiGLU GEMM (M <= 16) over concatenated gate/up panels with
+ * the hidden columns sent to hpl-wide planes, as jtk_w8a8_swiglu_planes. */
+int jtk_w8a8_skinny_swiglu_planes(const int8_t *A, int lda, const float *sA, const int8_t *Wp,
+                                  const float *sB, int M, int N, int Kp, float *C, int ldc,
+                                  int hpl, int64_t plane, uint32_t *err, hipStream_t s);
+/* nb plain jtk_w8a8_gemm_xq GEMMs in one launch: GEMM b reads X + b*sX
+ * (floats), weight panels Wp + b*sW (bytes), sB + b*ssB and writes
+ * C + b*sC (floats). hipErrorInvalidValue under jtk_w8a8_gemm_xq's limits
+ * or when sX is not a multiple of 4. */
+int jtk_w8a8_gemm_xq_batch(const float *X, int ldx, int K, int64_t sX, const int8_t *Wp,
+                           int64_t sW, const float *sB, int ssB, int M, int N, int Np, int Kp,
+                           float *C, int ldc, int64_t sC, int nb, uint32_t *err, hipStream_t s);
 /* M <= 16 on fp32 activations X [M][ldx] (K valid columns): each block
  * quantises the rows itself with the row quantiser's arithmetic.
  * hipErrorInvalidValue (nothing launched) unless K % 4 == 0, K <= 4096
