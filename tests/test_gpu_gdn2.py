@@ -93,7 +93,7 @@ def test_gdn2_decode_golden(jt, gold, dk, dv, seed):
 
 
 @pytest.mark.parametrize("dk,dv", [(1, 1), (7, 33), (128, 128), (130, 256), (1024, 8),
-                                   (8, 1024), (256, 64)])
+                                   (8, 1024), (256, 64), (64, 40), (128, 300), (64, 1024)])
 def test_gdn2_decode_vs_oracle(jt, orc, dk, dv):
     announce(f"gdn2 decode {dk}x{dv}")
     rng = np.random.default_rng(dk * 7 + dv)
