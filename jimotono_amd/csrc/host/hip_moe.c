@@ -642,12 +642,10 @@ static int shared_fused(jt_hip_moe *L, int T, uint32_t *err, hipStream_t s, hipE
                                    ev ? ev[0] : NULL, ev ? ev[1] : NULL);
     e |= jtk_quant_rows(L->sS, (int64_t)S * T, h, L->sSq, F0->Kph, L->sss, NULL, err, s);
     if (ev) (void)hipEventRecord(ev[2], s);
-    for (int x = 0; x < S; x++) {
-        const jt_hip_ffn *F = L->sh[x];
-        e |= jtk_w8a8_gemm(L->sSq + (size_t)x * T * F->Kph, F->Kph, L->sss + (size_t)x * T,
-                           F->d_P, F->d_s, T, n, F->Np_d, F->Kph, L->Ys + (size_t)x * T * n, n, 0,
-                           err, s);
-    }
+    /* every expert's down projection in one launch */
+    e |= jtk_w8a8_gemm_batch(L->sSq, F0->Kph, (int64_t)T * F0->Kph, L->sss, T, L->sd_P,
+                             (int64_t)F0->Np_d * F0->Kph, L->sd_s, F0->Np_d, T, n, F0->Np_d,
+                             F0->Kph, L->Ys, n, (int64_t)T * n, S, err, s, NULL, NULL);
     return e ? jt_rt_err(hipErrorLaunchFailure) : JT_OK;
 }
 

@@ -215,12 +215,27 @@ __device__ __forceinline__ void w8a8_epilogue(const v4i (&acc)[TM][TN], int part
 }
 #undef sa
 
+// Strides of a batch of GEMMs in one launch (blockIdx.y = GEMM b): A and the
+// weight panels in bytes, sA, sB and C in floats. All zero for one GEMM.
+struct TileBatch {
+    int64_t bsA, bsW;
+    int bsSA, bsB;
+    int64_t bsC;
+};
+
 template <int EPI, int BM, int BN, int WGM, int WGN, int KS, int NST, int GM>
 __global__ __launch_bounds__(64 * WGM * WGN * KS) void k_w8a8_tile(
     const int8_t *__restrict__ A, int lda, const float *__restrict__ sA,
     const int8_t *__restrict__ Wp, const float *__restrict__ sB, int M, int N, int Kp,
     float *__restrict__ C, int ldc, int hpl, int64_t plane, uint32_t *err, int mtiles,
-    int ntiles) {
+    int ntiles, TileBatch bt) {
+    if (blockIdx.y) {  // GEMM blockIdx.y of a batch
+        A += blockIdx.y * bt.bsA;
+        Wp += blockIdx.y * bt.bsW;
+        sA += (int64_t)blockIdx.y * bt.bsSA;
+        sB += (int64_t)blockIdx.y * bt.bsB;
+        C += blockIdx.y * bt.bsC;
+    }
     constexpr int NWG = WGM * WGN;  // waves per k-group
     constexpr int WTM = BM / WGM, WTN = BN / WGN;
     constexpr int TM = WTM / 16, TN = WTN / 16;
@@ -357,7 +372,8 @@ inline hipError_t launch_w8a8_tile(const int8_t *A, int lda, const float *sA, co
                                    const float *sB, int M, int N, int Np, int Kp, float *C,
                                    int ldc, uint32_t *err, hipStream_t s,
                                    hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr,
-                                   int hpl = 0, int64_t plane = 0) {
+                                   int hpl = 0, int64_t plane = 0, unsigned nb = 1,
+                                   TileBatch bt = TileBatch{}) {
     auto kern = k_w8a8_tile<EPI, BM, BN, WGM, WGN, KS, NST, GM>;
     constexpr int lds = NST * (BM + BN) / 16 * KS * 1024;
     // dynamic LDS above 64 KiB must be enabled per device, once
@@ -373,8 +389,8 @@ inline hipError_t launch_w8a8_tile(const int8_t *A, int lda, const float *sA, co
         attr_set[dev] = true;
     }
     const int mt = (M + BM - 1) / BM, nt = Np / BN;
-    hipExtLaunchKernelGGL(kern, dim3((unsigned)(mt * nt)), dim3(64 * WGM * WGN * KS), lds, s,
-                          e0, e1, 0, A, lda, sA, Wp, sB, M, N, Kp, C, ldc, hpl, plane, err, mt,
-                          nt);
+    hipExtLaunchKernelGGL(kern, dim3((unsigned)(mt * nt), nb), dim3(64 * WGM * WGN * KS), lds,
+                          s, e0, e1, 0, A, lda, sA, Wp, sB, M, N, Kp, C, ldc, hpl, plane, err, mt,
+                          nt, bt);
     return hipGetLastError();
 }

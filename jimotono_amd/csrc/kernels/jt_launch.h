@@ -67,6 +67,14 @@ int jtk_w8a8_swiglu_planes(const int8_t *A, int lda, const float *sA, const int8
                            const float *sB, int M, int N, int Kp, float *C, int ldc, int hpl,
                            int64_t plane, uint32_t *err, hipStream_t s, hipEvent_t e0,
                            hipEvent_t e1);
+/* nb plain W8A8 GEMMs of M > 64 rows in one launch (128 x 128 tiles with a
+ * k-split; blockIdx.y = GEMM b): GEMM b reads A + b*sAq (bytes), sA + b*ssA,
+ * panels Wp + b*sW (bytes), sB + b*ssB and writes C + b*sC (floats).
+ * hipErrorInvalidValue (nothing launched) for M <= 64 or Np % 128 != 0. */
+int jtk_w8a8_gemm_batch(const int8_t *A, int lda, int64_t sAq, const float *sA, int ssA,
+                        const int8_t *Wp, int64_t sW, const float *sB, int ssB, int M, int N,
+                        int Np, int Kp, float *C, int ldc, int64_t sC, int nb, uint32_t *err,
+                        hipStream_t s, hipEvent_t e0, hipEvent_t e1);
 /* The skinny SwiGLU GEMM (M <= 16) over concatenated gate/up panels with
  * the hidden columns sent to hpl-wide planes, as jtk_w8a8_swiglu_planes. */
 int jtk_w8a8_skinny_swiglu_planes(const int8_t *A, int lda, const float *sA, const int8_t *Wp,
