@@ -330,6 +330,7 @@ struct jt_hip_moe {
     int8_t *Xq;
     float *sx, *logits, *w, *Sr, *ssr, *Ye, *Ys;
     int32_t *ids, *rank, *cnt, *tot, *off, *perm, *tiles, *ntiles;
+    uint32_t *route_done; /* decode launch's block counter (zero between launches) */
     const int32_t *cur_ids; /* ids / weights of the last forward (caller's */
     const float *cur_w;     /* arrays after jt_hip_moe_fwd_routed) */
     /* router on the int8 matrix cores with exact verification (E <= 256,
@@ -371,7 +372,8 @@ void jt_hip_moe_free(jt_hip_moe *L) {
                  L->logits, L->w,  L->Sr,   L->ssr,  L->Ye,   L->Ys,   L->ids,
                  L->rank,  L->cnt, L->tot,  L->off,  L->perm, L->tiles, L->ntiles,
                  L->Sqr,   L->Xl,  L->rWh,  L->rWl,  L->xinfo, L->winfo, L->approx, L->rcand, L->rnc,
-                 L->sgu_P, L->sgu_s, L->sS,  L->sSq,  L->sss,  L->sd_P,  L->sd_s};
+                 L->sgu_P, L->sgu_s, L->sS,  L->sSq,  L->sss,  L->sd_P,  L->sd_s,
+                 L->route_done};
     (void)hipDeviceSynchronize();
     for (size_t i = 0; i < sizeof(p) / sizeof(p[0]); i++) (void)hipFree(p[i]);
     for (int s = 0; s < JT_MOE_MAX_SHARED; s++) jt_hip_ffn_free(L->sh[s]);
@@ -438,6 +440,8 @@ static int moe_alloc(const jt_hip_moe_desc *dp, int has_gate, jt_hip_moe **out) 
     ALLOC(L->perm, (size_t)Tk * 4);
     ALLOC(L->tiles, (size_t)(Tk / 16 + E + 1) * 16); /* int4 descriptors */
     ALLOC(L->ntiles, 4);
+    ALLOC(L->route_done, 64);
+    if (e == hipSuccess) e = hipMemset(L->route_done, 0, 64);
     ALLOC(L->Sr, (size_t)Tk * h * 4);
     ALLOC(L->Sqr, (size_t)Tk * h);
     ALLOC(L->ssr, (size_t)Tk * 4);
@@ -726,6 +730,14 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
      * sort up to 1024 pairs */
     const int R = Tk <= 16 * E ? 16 : 64;
     const int max_tiles = Tk / R + E;
+    /* Decode with the shared experts concatenated: top-k, the pair sort and
+     * the shared gate/up blocks share one launch, the routed FFN and the
+     * shared down blocks another (three launches fewer; with profiling each
+     * stage keeps its own). T <= 16 and k <= 64 keep Tk <= 1024. */
+    const jt_hip_ffn *F0 = S > 0 ? L->sh[0] : NULL;
+    const int merge16 = !L->prof && small && fused16 && R == 16 && h == 256 &&
+                        n % 256 == 0 && n <= 1024 && E <= 1024 && k <= 64 && F0->h % 16 == 0 &&
+                        F0->Kph <= 3072 && F0->Np_d >= n;
     prof_mark(L, slot, ST_ROUTER, s);
     const int32_t *ids = L->ids;
     const float *w = L->w;
@@ -735,7 +747,13 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
         prof_mark(L, slot, ST_TOPK, s);
     } else if (small) {
         prof_mark(L, slot, ST_TOPK, s);
-        le |= jtk_topk(L->logits, T, E, k, L->ids, NULL, L->w, err, s);
+        if (merge16) /* top-k, the pair sort and the shared gate/ups */
+            le |= jtk_decode_route_shared_gu(
+                L->logits, T, E, k, L->ids, L->w, R, L->off, L->perm, L->tiles, L->ntiles,
+                L->route_done, L->Xq, F0->Kpn, L->sx, L->sgu_P, L->sgu_s, S * F0->Np_gu,
+                F0->Kpn, L->sS, F0->h, F0->h, (int64_t)T * F0->h, err, s);
+        else
+            le |= jtk_topk(L->logits, T, E, k, L->ids, NULL, L->w, err, s);
     } else if (fast) {
         le |= jtk_router_approx(L->Xq, L->Xl, n, L->xinfo, L->rWh, L->rWl, L->winfo, T, E,
                                 L->approx, s);
@@ -750,7 +768,9 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
     L->cur_ids = ids;
     L->cur_w = w;
     prof_mark(L, slot, ST_SORT, s);
-    if (Tk <= 1024 && E <= 4096) {
+    if (merge16) {
+        /* sorted in the top-k launch */
+    } else if (Tk <= 1024 && E <= 4096) {
         le |= jtk_sort_small(ids, Tk, E, (int64_t)Tk, R, L->off, NULL, L->perm, NULL, NULL,
                              L->tiles, L->ntiles, err, s);
         prof_mark(L, slot, ST_TILES, s);
@@ -772,10 +792,18 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
     if (R == 16 && h == 256 && n % 256 == 0 && n <= 1024) {
         /* 16-row tiles: gate/up, SwiGLU, row codes and down in one launch
          * (the three stages are timed as one, under routed_gateup) */
-        le |= jtk_routed_ffn16(L->Xq, L->sx, L->perm, L->tiles, L->ntiles, max_tiles, k,
-                               L->gu_P, L->gu_S, L->gu_pstride, L->gu_sstride, L->dn_P, L->dn_S,
-                               L->dn_pstride, L->dn_sstride, n, h, L->Ye, L->Sqr, L->ssr, err,
-                               s);
+        if (merge16)
+            le |= jtk_decode_ffn16_shared_down(
+                L->Xq, L->sx, L->perm, L->tiles, L->ntiles, max_tiles, k, L->gu_P, L->gu_S,
+                L->gu_pstride, L->gu_sstride, L->dn_P, L->dn_S, L->dn_pstride, L->dn_sstride, n,
+                h, L->Ye, L->Sqr, L->ssr, L->sS, F0->h, F0->h, (int64_t)T * F0->h, T, L->sd_P,
+                (int64_t)F0->Np_d * F0->Kph, L->sd_s, F0->Np_d, F0->Np_d, F0->Kph, L->Ys, n,
+                (int64_t)T * n, S, err, s);
+        else
+            le |= jtk_routed_ffn16(L->Xq, L->sx, L->perm, L->tiles, L->ntiles, max_tiles, k,
+                                   L->gu_P, L->gu_S, L->gu_pstride, L->gu_sstride, L->dn_P,
+                                   L->dn_S, L->dn_pstride, L->dn_sstride, n, h, L->Ye, L->Sqr,
+                                   L->ssr, err, s);
         prof_mark(L, slot, ST_R_QUANT, s);
         prof_mark(L, slot, ST_R_DOWN, s);
     } else {
@@ -803,6 +831,8 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
     }
     if (fork) {
         for (int i = 0; i < L->nside; i++) le |= (int)hipStreamWaitEvent(s, L->ev_join[i], 0);
+    } else if (merge16) {
+        /* the shared experts ran in the top-k and routed FFN launches */
     } else if (fused || fused16) {
         hipEvent_t *ev = L->prof ? &L->ev[slot][ST_N + 1] : NULL;
         rc = fused ? shared_fused(L, T, err, s, ev) : shared_fused16(L, T, err, s, ev);

@@ -195,6 +195,14 @@ static int bwd_host(const float *dY, const float *X, const float *Wgate, const f
     }
     if (rc == JT_OK && dLogits) rc = jt_rt_d2h(rt, dLogits, o_dL, (size_t)T * E * 4);
     (void)hipStreamSynchronize(s);
+    if (rc != JT_OK) {
+        /* a failed call reports its own code: flags raised by work it had
+         * already queued are dropped, not left for the stream's next call */
+        const int saved = errno;
+        uint32_t dropped = 0;
+        (void)jt_rt_flags(rt, s, &dropped);
+        errno = saved;
+    }
     for (int i = 0; i < a.n; i++) (void)hipFree(a.p[i]);
     return rc;
 }

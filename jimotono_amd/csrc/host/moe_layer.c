@@ -250,6 +250,7 @@ static int fwd_batch(const float *X, const float *Wgate, const float *Wg, const 
         } else if (w8a8_on) {
             rc = w8a8_pc(rt, &w8, Xe, wg, Ge, Me, h, n);
             if (rc == JT_OK) rc = w8a8_pc(rt, &w8, Xe, wu, Ue, Me, h, n);
+            if (rc != JT_OK) break; /* nothing more runs on the unfilled rows */
         } else {
             le |= jtk_transpose_f32(wg, Wt1, h, n, s);
             le |= jtk_transpose_f32(wu, Wt2, h, n, s);
@@ -282,6 +283,7 @@ static int fwd_batch(const float *X, const float *Wgate, const float *Wg, const 
         if (w8a8_on) {
             rc = w8a8_pc(rt, &w8, dX, wg, Ge, T, h, n);
             if (rc == JT_OK) rc = w8a8_pc(rt, &w8, dX, wu, Ue, T, h, n);
+            if (rc != JT_OK) break; /* nothing more runs on the unfilled rows */
         } else {
             le |= jtk_transpose_f32(wg, Wt1, h, n, s);
             le |= jtk_transpose_f32(wu, Wt2, h, n, s);
@@ -301,7 +303,7 @@ static int fwd_batch(const float *X, const float *Wgate, const float *Wg, const 
         }
     }
     /* combine (src/moe_layer.c:1443-1463, 1549-1574) */
-    le |= jtk_combine(w, Ysel, drop, Ys, S, T, k, n, NULL, dY, err, s);
+    if (rc == JT_OK) le |= jtk_combine(w, Ysel, drop, Ys, S, T, k, n, NULL, dY, err, s);
     if (rc == JT_OK && le) rc = jt_rt_err(hipErrorLaunchFailure);
     if (rc != JT_OK) goto out;
     if ((rc = jt_rt_flags(rt, s, &f)) != JT_OK) goto out;
@@ -325,6 +327,14 @@ static int fwd_batch(const float *X, const float *Wgate, const float *Wg, const 
     }
 out:
     (void)hipStreamSynchronize(s);
+    if (rc != JT_OK) {
+        /* a failed call reports its own code: flags raised by work it had
+         * already queued are dropped, not left for the stream's next call */
+        const int saved = errno;
+        uint32_t dropped = 0;
+        (void)jt_rt_flags(rt, s, &dropped);
+        errno = saved;
+    }
     afree(&a);
     free(hoff);
     return rc;

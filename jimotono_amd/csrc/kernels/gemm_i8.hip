@@ -18,6 +18,8 @@
 
 #include "gemm_w8a8.h"
 #include "jt_launch.h"
+#include "topk_dev.h"
+#include "sort_dev.h"
 
 // Output fragment layout of v_mfma_i32_16x16x64_i8 (4 int32 per lane):
 // element r of lane l is row 4*(l/16)+r, column l%16 of the 16x16 tile.
@@ -54,16 +56,18 @@ struct SkBatch {
     int64_t bsC;
 };
 
+// One block's work, for block (bx, by) of the grid: k_w8a8_skinny below, and
+// the decode launches that run these blocks beside other work.
 template <int EPI, int NP, int QV>  // QV > 0: QA with K <= 256 * QV
-__global__ __launch_bounds__(64 * SK_WAVES) void k_w8a8_skinny(
-    const void *__restrict__ Ain, int lda, const float *__restrict__ sAin,
+__device__ __forceinline__ void w8a8_skinny_block(
+    int bx, int by, const void *__restrict__ Ain, int lda, const float *__restrict__ sAin,
     const int8_t *__restrict__ Wp, const float *__restrict__ sB, int M, int N, int Kp, int K,
     float *__restrict__ C, int ldc, uint32_t *err, SkBatch bt) {
-    if (blockIdx.y) {  // the blockIdx.y-th GEMM of a batch
-        Ain = (const int8_t *)Ain + blockIdx.y * bt.bsA;
-        Wp += blockIdx.y * bt.bsW;
-        sB += (int64_t)blockIdx.y * bt.bsB;
-        C += blockIdx.y * bt.bsC;
+    if (by) {  // the by-th GEMM of a batch
+        Ain = (const int8_t *)Ain + by * bt.bsA;
+        Wp += by * bt.bsW;
+        sB += (int64_t)by * bt.bsB;
+        C += by * bt.bsC;
     }
     __shared__ v4i red[SK_WAVES][NP][64];
     extern __shared__ __attribute__((aligned(16))) int8_t sk_aq[];  // QA: [16][Kp + 16]
@@ -75,7 +79,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) void k_w8a8_skinny(
     // matters because v_mfma ignores EXEC (an exec-masked MFMA still runs)
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int KB = Kp / 64;
-    const int p0 = blockIdx.x * NP;
+    const int p0 = bx * NP;
     const int row = lane & 15, kc = lane >> 4;
     const int astr = Kp + 16;
     const int8_t *arow = QA ? sk_aq + row * astr + kc * 16
@@ -157,7 +161,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) void k_w8a8_skinny(
             }
             if (lane == 0) sk_sa[wave] = qp.scale_f;
         }
-        if (flags && lane == 0 && blockIdx.x == 0) raise_err(err, flags);
+        if (flags && lane == 0 && bx == 0) raise_err(err, flags);
         __syncthreads();
     }
     for (int kb0 = wave; kb0 < KB; kb0 += SK_WAVES * SK_UNROLL) {
@@ -228,13 +232,22 @@ __global__ __launch_bounds__(64 * SK_WAVES) void k_w8a8_skinny(
             bad |= (!isfinite(g)) || (!isfinite(u));
             float sv;
             badmid |= !silu_mul(g, u, &sv);
-            const int x0 = blockIdx.x * 16;  // this block's first hidden column
+            const int x0 = bx * 16;  // this block's first hidden column
             const int64_t at = bt.hpl > 0 ? (int64_t)(x0 / bt.hpl) * bt.plane + x0 % bt.hpl : x0;
             C[(int64_t)m * ldc + at + lc] = sv;
         }
     }
     if (bad) raise_err(err, EF_RANGE);
     if (badmid) raise_err(err, EF_NONFINITE_MID);
+}
+
+template <int EPI, int NP, int QV>
+__global__ __launch_bounds__(64 * SK_WAVES) void k_w8a8_skinny(
+    const void *__restrict__ Ain, int lda, const float *__restrict__ sAin,
+    const int8_t *__restrict__ Wp, const float *__restrict__ sB, int M, int N, int Kp, int K,
+    float *__restrict__ C, int ldc, uint32_t *err, SkBatch bt) {
+    w8a8_skinny_block<EPI, NP, QV>((int)blockIdx.x, (int)blockIdx.y, Ain, lda, sAin, Wp, sB, M,
+                                   N, Kp, K, C, ldc, err, bt);
 }
 
 // ===================== few-row GEMM (16 < M <= 64) =====================
@@ -1385,10 +1398,11 @@ static hipError_t launch_lowbit_skinny(dim3 grid, int G, hipStream_t s, const in
 #define RF_WAVES 16
 #define RF_HSTR (RF_H + 4)   // fp32 gate/up row stride (floats)
 #define RF_QSTR (RF_H + 16)  // int8 h row stride (bytes)
+#define DS_QV_MAX 12         // shared down beside the routed FFN: K <= 3072 (LDS)
 
 template <int G1>
-__global__ __launch_bounds__(64 * RF_WAVES) void k_routed_ffn16(
-    const int8_t *__restrict__ Xq, const float *__restrict__ sx,
+__device__ __forceinline__ void routed_ffn16_block(
+    int tile, const int8_t *__restrict__ Xq, const float *__restrict__ sx,
     const int32_t *__restrict__ perm, const int4 *__restrict__ tiles,
     const int32_t *__restrict__ ntiles, int topk, const uint8_t *__restrict__ guP,
     const uint16_t *__restrict__ guS, int64_t gu_pstride, int64_t gu_sstride,
@@ -1412,7 +1426,6 @@ __global__ __launch_bounds__(64 * RF_WAVES) void k_routed_ffn16(
     __shared__ float rsa[16], rsq[16];
     __shared__ int rdst[16];
     __shared__ double exp_tab[64];
-    const int tile = blockIdx.x;
     if (tile >= *ntiles) return;
     const int lane = threadIdx.x & 63;
     // the SwiGLU's exp table entry, requested before the weights so that its
@@ -1595,6 +1608,20 @@ __global__ __launch_bounds__(64 * RF_WAVES) void k_routed_ffn16(
     if (flags) raise_err(err, flags);
 }
 
+template <int G1>
+__global__ __launch_bounds__(64 * RF_WAVES) void k_routed_ffn16(
+    const int8_t *__restrict__ Xq, const float *__restrict__ sx,
+    const int32_t *__restrict__ perm, const int4 *__restrict__ tiles,
+    const int32_t *__restrict__ ntiles, int topk, const uint8_t *__restrict__ guP,
+    const uint16_t *__restrict__ guS, int64_t gu_pstride, int64_t gu_sstride,
+    const uint8_t *__restrict__ dnP, const uint16_t *__restrict__ dnS, int64_t dn_pstride,
+    int64_t dn_sstride, float *__restrict__ Ye, int8_t *__restrict__ Hq,
+    float *__restrict__ Hs, uint32_t *err) {
+    routed_ffn16_block<G1>((int)blockIdx.x, Xq, sx, perm, tiles, ntiles, topk, guP, guS,
+                           gu_pstride, gu_sstride, dnP, dnS, dn_pstride, dn_sstride, Ye, Hq, Hs,
+                           err);
+}
+
 template <int BITS, int EPI, int NST>
 static hipError_t launch_lowbit(dim3 grid, hipStream_t s, const int8_t *A, int lda,
                                 const float *sA, const int32_t *perm, const int32_t *off,
@@ -1673,6 +1700,196 @@ extern "C" int jtk_routed_ffn16(const int8_t *Xq, const float *sx, const int32_t
     }
 #undef RF_LAUNCH
     return (int)hipGetLastError();
+}
+
+// ===================== decode launches with the shared experts beside =====================
+// At decode every launch costs a 2-3 us floor and the routing kernels keep
+// a few CUs busy, so the shared experts' skinny GEMM blocks ride in the
+// launches of the routed path instead of launches of their own (same
+// blocks, same arithmetic, so the same outputs):
+//   launch 1: top-k of the T <= 16 rows (blocks 0 .. ntb-1, waves 0-3, one
+//             row each), then the pair sort and tile list in whichever of
+//             those blocks finishes last, + the shared experts' concatenated
+//             gate/up panels with the SwiGLU (blocks ntb ..; they need only
+//             the token codes);
+//   launch 2: the routed FFN of the 16-row tiles (blocks 0 .. max_tiles-1)
+//             + the shared experts' down projections (blocks max_tiles ..,
+//             expert j / nbx, channel group j % nbx), which read the hidden
+//             rows launch 1 wrote.
+// The last top-k block is found with a device counter: each top-k block
+// releases its rows' ids with an agent-scope fence and counts itself in;
+// the block that counts ntb acquires every block's ids, sorts them (as
+// k_sort_small) and returns the counter to zero for the next launch.
+static_assert(RF_WAVES == SK_WAVES, "one block size for both kinds of block");
+
+template <int EPL>
+__global__ __launch_bounds__(64 * SK_WAVES) void k_decode_route_shared_gu(
+    const float *__restrict__ logits, int T, int E, int k, int32_t *__restrict__ ids,
+    float *__restrict__ w, int ntb, int R, int32_t *__restrict__ off,
+    int32_t *__restrict__ perm, int32_t *__restrict__ tiles, int32_t *__restrict__ ntiles,
+    uint32_t *__restrict__ done, const int8_t *__restrict__ Xq, int ldx,
+    const float *__restrict__ sx, const int8_t *__restrict__ Wp, const float *__restrict__ sB,
+    int N, int Kp, float *__restrict__ C, int ldc, SkBatch bt, uint32_t *err) {
+    if ((int)blockIdx.x >= ntb) {
+        w8a8_skinny_block<EPI_SWIGLU, 2, 0>((int)blockIdx.x - ntb, 0, Xq, ldx, sx, Wp, sB, T, N,
+                                            Kp, Kp, C, ldc, err, bt);
+        return;
+    }
+    __shared__ SortSmallLds sm;
+    __shared__ int is_last;
+    const int wave = threadIdx.x >> 6, row = blockIdx.x * 4 + wave;
+    if (wave < 4 && row < T)
+        (void)topk_wave_reg<EPL>(logits + (int64_t)row * E, E, k, threadIdx.x & 63, row, ids,
+                                 NULL, w, err);
+    __syncthreads();  // this block's rows are written
+    if (threadIdx.x == 0) {
+        __threadfence();  // ... and visible to the other blocks
+        const bool last = atomicAdd(done, 1u) == (uint32_t)ntb - 1;
+        // every block's rows are visible from here on, and through the
+        // barrier below to the whole block (one fence: each costs an L2
+        // write-back and invalidate)
+        if (last) __threadfence();
+        is_last = last;
+    }
+    __syncthreads();
+    if (!is_last) return;
+    const int Tk = T * k, t = threadIdx.x;
+    int e = -1;
+    if (t < Tk) {
+        e = ids[t];
+        if (e < 0 || e >= E) {
+            raise_err(err, EF_BAD_ID);
+            e = -1;
+        }
+    }
+    sort_small_core(e, Tk, E, (int64_t)Tk, R, off, NULL, perm, NULL, NULL, tiles, ntiles, sm);
+    if (t == 0) *done = 0;  // for the next launch (the counter is this block's alone now)
+}
+
+extern "C" int jtk_decode_route_shared_gu(const float *logits, int T, int E, int k,
+                                          int32_t *ids, float *w, int R, int32_t *off,
+                                          int32_t *perm, int32_t *tiles, int32_t *ntiles,
+                                          uint32_t *done, const int8_t *Xq, int ldx,
+                                          const float *sx, const int8_t *Wp, const float *sB,
+                                          int N, int Kp, float *C, int ldc, int hpl,
+                                          int64_t plane, uint32_t *err, hipStream_t s) {
+    if (T <= 0) return 0;
+    if (T > 16 || k <= 0 || k > 64 || T * k > SORT_SMALL || topk_epl(E) == 0 || R <= 0 ||
+        !done || N <= 0 || N % 32 || hpl <= 0 || hpl % 16 || (N / 2) % hpl || Kp <= 0 || Kp % 64)
+        return (int)hipErrorInvalidValue;
+    SkBatch bt{};
+    bt.hpl = hpl;
+    bt.plane = plane;
+    const int ntb = (T + 3) / 4;
+    const dim3 grid((unsigned)(ntb + N / 32));
+    switch (topk_epl(E)) {
+#define TG_LAUNCH(P)                                                                            \
+    case P:                                                                                     \
+        hipLaunchKernelGGL(k_decode_route_shared_gu<P>, grid, dim3(64 * SK_WAVES), 0, s, logits, \
+                           T, E, k, ids, w, ntb, R, off, perm, tiles, ntiles, done, Xq, ldx, sx, \
+                           Wp, sB, N, Kp, C, ldc, bt, err);                                     \
+        break;
+        TG_LAUNCH(1)
+        TG_LAUNCH(2)
+        TG_LAUNCH(4)
+        TG_LAUNCH(8)
+        TG_LAUNCH(16)
+#undef TG_LAUNCH
+    default: return (int)hipErrorInvalidValue;
+    }
+    return (int)hipGetLastError();
+}
+
+template <int G1, int QV>
+__global__ __launch_bounds__(64 * SK_WAVES) void k_decode_ffn16_shared_down(
+    const int8_t *__restrict__ Xq, const float *__restrict__ sx,
+    const int32_t *__restrict__ perm, const int4 *__restrict__ tiles,
+    const int32_t *__restrict__ ntiles, int max_tiles, int topk,
+    const uint8_t *__restrict__ guP, const uint16_t *__restrict__ guS, int64_t gu_pstride,
+    int64_t gu_sstride, const uint8_t *__restrict__ dnP, const uint16_t *__restrict__ dnS,
+    int64_t dn_pstride, int64_t dn_sstride, float *__restrict__ Ye, int8_t *__restrict__ Hq,
+    float *__restrict__ Hs, const float *__restrict__ H, int ldh, int K, int T,
+    const int8_t *__restrict__ Wd, const float *__restrict__ sBd, int N, int Kp,
+    float *__restrict__ Ys, int ldy, SkBatch bt, int nbx, uint32_t *err) {
+    if ((int)blockIdx.x < max_tiles) {
+        routed_ffn16_block<G1>((int)blockIdx.x, Xq, sx, perm, tiles, ntiles, topk, guP, guS,
+                               gu_pstride, gu_sstride, dnP, dnS, dn_pstride, dn_sstride, Ye, Hq,
+                               Hs, err);
+        return;
+    }
+    const int j = (int)blockIdx.x - max_tiles;
+    w8a8_skinny_block<EPI_PLAIN, 1, QV>(j % nbx, j / nbx, H, ldh, NULL, Wd, sBd, T, N, Kp, K, Ys,
+                                        ldy, err, bt);
+}
+
+template <int G1, int QV>
+static hipError_t launch_ffn16_down(dim3 grid, size_t lds, hipStream_t s, const int8_t *Xq,
+                                    const float *sx, const int32_t *perm, const int4 *tiles,
+                                    const int32_t *ntiles, int max_tiles, int topk,
+                                    const uint8_t *guP, const uint16_t *guS, int64_t gu_pstride,
+                                    int64_t gu_sstride, const uint8_t *dnP, const uint16_t *dnS,
+                                    int64_t dn_pstride, int64_t dn_sstride, float *Ye, int8_t *Hq,
+                                    float *Hs, const float *H, int ldh, int K, int T,
+                                    const int8_t *Wd, const float *sBd, int N, int Kp, float *Ys,
+                                    int ldy, SkBatch bt, int nbx, uint32_t *err) {
+    auto kern = k_decode_ffn16_shared_down<G1, QV>;
+    static std::atomic<bool> attr_set[64];  // set once per device; a repeat is harmless
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    if (!attr_set[dev]) {
+        e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                16 * (256 * DS_QV_MAX + 16));
+        if (e != hipSuccess) return e;
+        attr_set[dev] = true;
+    }
+    hipLaunchKernelGGL(kern, grid, dim3(64 * SK_WAVES), lds, s, Xq, sx, perm, tiles, ntiles,
+                       max_tiles, topk, guP, guS, gu_pstride, gu_sstride, dnP, dnS, dn_pstride,
+                       dn_sstride, Ye, Hq, Hs, H, ldh, K, T, Wd, sBd, N, Kp, Ys, ldy, bt, nbx, err);
+    return hipGetLastError();
+}
+
+extern "C" int jtk_decode_ffn16_shared_down(
+    const int8_t *Xq, const float *sx, const int32_t *perm, const int32_t *tiles,
+    const int32_t *ntiles, int max_tiles, int topk, const uint8_t *guP, const uint16_t *guS,
+    int64_t gu_pstride, int64_t gu_sstride, const uint8_t *dnP, const uint16_t *dnS,
+    int64_t dn_pstride, int64_t dn_sstride, int n, int h, float *Ye, int8_t *Hq, float *Hs,
+    const float *H, int ldh, int K, int64_t sH, int T, const int8_t *Wd, int64_t sW,
+    const float *sBd, int ssB, int Np, int Kp, float *Ys, int ldy, int64_t sY, int nb,
+    uint32_t *err, hipStream_t s) {
+    if (max_tiles <= 0 || T <= 0 || nb <= 0) return (int)hipErrorInvalidValue;
+    if (h != RF_H || T > 16 || K <= 0 || K > Kp || Kp % 64 || K % 4 || Kp > 256 * DS_QV_MAX ||
+        ldh % 4 || sH % 4 || ((uintptr_t)H & 15) || Np % 16 || Np < n || nb > 65535 ||
+        (int64_t)max_tiles + (int64_t)(Np / 16) * nb > 0x7fffffff)
+        return (int)hipErrorInvalidValue;
+    SkBatch bt{};
+    bt.bsA = sH * (int64_t)sizeof(float);
+    bt.bsW = sW;
+    bt.bsB = ssB;
+    bt.bsC = sY;
+    const int nbx = Np / 16;
+    const dim3 grid((unsigned)(max_tiles + nbx * nb));
+    const size_t lds = (size_t)16 * (Kp + 16);
+    const int4 *t4 = (const int4 *)tiles;
+    const int qv = (K + 255) / 256 <= 4 ? 4 : (K + 255) / 256 <= 8 ? 8 : 12;
+#define DS_LAUNCH(G, Q)                                                                         \
+    launch_ffn16_down<G, Q>(grid, lds, s, Xq, sx, perm, t4, ntiles, max_tiles, topk, guP, guS,  \
+                            gu_pstride, gu_sstride, dnP, dnS, dn_pstride, dn_sstride, Ye, Hq,   \
+                            Hs, H, ldh, K, T, Wd, sBd, n, Kp, Ys, ldy, bt, nbx, err)
+#define DS_QV(G)                                                                                \
+    (qv == 4 ? DS_LAUNCH(G, 4) : qv == 8 ? DS_LAUNCH(G, 8) : DS_LAUNCH(G, 12))
+    hipError_t e;
+    switch (n) {
+    case 256: e = DS_QV(4); break;
+    case 512: e = DS_QV(8); break;
+    case 768: e = DS_QV(12); break;
+    case 1024: e = DS_QV(16); break;
+    default: return (int)hipErrorInvalidValue;
+    }
+#undef DS_QV
+#undef DS_LAUNCH
+    return (int)e;
 }
 
 extern "C" int jtk_lowbit_grouped(int bits, const int8_t *A, int lda, const float *sA,

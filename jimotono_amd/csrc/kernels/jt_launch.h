@@ -118,6 +118,28 @@ int jtk_routed_ffn16(const int8_t *Xq, const float *sx, const int32_t *perm,
                      int64_t gu_sstride, const uint8_t *dnP, const uint16_t *dnS,
                      int64_t dn_pstride, int64_t dn_sstride, int n, int h, float *Ye,
                      int8_t *Hq, float *Hs, uint32_t *err, hipStream_t s);
+/* decode launches that carry the shared experts' blocks: top-k of T <= 16
+ * rows (E <= 1024, k <= 64) and the pair sort / tile list (as
+ * jtk_sort_small with cap = T*k; `done` is a zeroed device word the launch
+ * leaves zeroed) beside the concatenated SwiGLU gate/up panels (as
+ * jtk_w8a8_skinny_swiglu_planes), and the routed FFN of 16-row tiles (as
+ * jtk_routed_ffn16) beside the batched down projections (as
+ * jtk_w8a8_gemm_xq_batch, Kp <= 3072); hipErrorInvalidValue for other
+ * shapes */
+int jtk_decode_route_shared_gu(const float *logits, int T, int E, int k, int32_t *ids,
+                               float *w, int R, int32_t *off, int32_t *perm, int32_t *tiles,
+                               int32_t *ntiles, uint32_t *done, const int8_t *Xq, int ldx,
+                               const float *sx, const int8_t *Wp, const float *sB, int N, int Kp,
+                               float *C, int ldc, int hpl, int64_t plane, uint32_t *err,
+                               hipStream_t s);
+int jtk_decode_ffn16_shared_down(
+    const int8_t *Xq, const float *sx, const int32_t *perm, const int32_t *tiles,
+    const int32_t *ntiles, int max_tiles, int topk, const uint8_t *guP, const uint16_t *guS,
+    int64_t gu_pstride, int64_t gu_sstride, const uint8_t *dnP, const uint16_t *dnS,
+    int64_t dn_pstride, int64_t dn_sstride, int n, int h, float *Ye, int8_t *Hq, float *Hs,
+    const float *H, int ldh, int K, int64_t sH, int T, const int8_t *Wd, int64_t sW,
+    const float *sBd, int ssB, int Np, int Kp, float *Ys, int ldy, int64_t sY, int nb,
+    uint32_t *err, hipStream_t s);
 
 /* router.hip: int8 MFMA candidates + exact fp64 verification of the gate */
 int jtk_router_codes(const float *X, int rows, int n, int8_t *qh, int8_t *ql, float *sf,

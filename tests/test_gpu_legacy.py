@@ -191,6 +191,9 @@ def test_moe_fwd_batch_w8a8_row_limit(jt, orc):
     o = orc.moe_fwd_batch(X, *W, k, 1.5, 1, 0)
     assert r["rc"] == o["rc"] == 2 and err == errno.EINVAL
     assert not r["Y"].any() and not r["ids"].any()
+    # the rejection leaves no error bits behind for the stream's next call
+    rc, ids, _ = jt.routing_topk(np.array([0.5, 2.0, 1.0], np.float32), 2)
+    assert rc == 0 and list(ids) == [1, 2]
 
 
 @pytest.mark.parametrize("n,k,mode", [(8192, 100, "normal"), (4097, 8, "normal"),
