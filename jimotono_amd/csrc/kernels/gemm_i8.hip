@@ -1735,7 +1735,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) void k_decode_route_shared_gu(
                                             Kp, Kp, C, ldc, err, bt);
         return;
     }
-    __shared__ SortSmallLds sm;
+    __shared__ __attribute__((aligned(16))) SortLds sm;
     __shared__ int is_last;
     const int wave = threadIdx.x >> 6, row = blockIdx.x * 4 + wave;
     if (wave < 4 && row < T)
@@ -1762,7 +1762,12 @@ __global__ __launch_bounds__(64 * SK_WAVES) void k_decode_route_shared_gu(
             e = -1;
         }
     }
-    sort_small_core(e, Tk, E, (int64_t)Tk, R, off, NULL, perm, NULL, NULL, tiles, ntiles, sm);
+    if (Tk <= SORTF_TK && E <= SORTF_E)  // block-uniform
+        sort_small_fast(e, Tk, E, (int64_t)Tk, R, off, NULL, perm, NULL, NULL, tiles, ntiles,
+                        sm.fast);
+    else
+        sort_small_core(e, Tk, E, (int64_t)Tk, R, off, NULL, perm, NULL, NULL, tiles, ntiles,
+                        sm.small);
     if (t == 0) *done = 0;  // for the next launch (the counter is this block's alone now)
 }
 

@@ -564,7 +564,7 @@ __global__ __launch_bounds__(1024) void k_sort_small(
     int32_t *__restrict__ off, int64_t *__restrict__ off64, int32_t *__restrict__ perm,
     int64_t *__restrict__ perm64, uint8_t *__restrict__ drop, int32_t *__restrict__ tiles,
     int32_t *__restrict__ ntiles, uint32_t *err) {
-    __shared__ __attribute__((aligned(16))) SortSmallLds sm;
+    __shared__ __attribute__((aligned(16))) SortLds sm;
     const int t = threadIdx.x;
     int e = -1;
     if (t < Tk) {
@@ -574,7 +574,10 @@ __global__ __launch_bounds__(1024) void k_sort_small(
             e = -1;
         }
     }
-    sort_small_core(e, Tk, E, cap, R, off, off64, perm, perm64, drop, tiles, ntiles, sm);
+    if (Tk <= SORTF_TK && E <= SORTF_E)  // block-uniform
+        sort_small_fast(e, Tk, E, cap, R, off, off64, perm, perm64, drop, tiles, ntiles, sm.fast);
+    else
+        sort_small_core(e, Tk, E, cap, R, off, off64, perm, perm64, drop, tiles, ntiles, sm.small);
 }
 
 extern "C" int jtk_sort_small(const int32_t *ids, int Tk, int E, int64_t cap, int R,

@@ -113,3 +113,111 @@ static __device__ void sort_small_core(int e, int Tk, int E, int64_t cap, int R,
     }
 }
 
+
+// The same sort for at most SORTF_TK pairs and SORTF_E experts, with the
+// same outputs, run by the first Tk / 64 waves of a block of at least
+// SORTF_TK threads: a pair's rank within its wave comes from one ballot per
+// bit of the expert id (the lanes whose id agrees on every bit), the
+// earlier waves' counts of its expert from LDS, and the expert offsets and
+// tile bases from one wave's scan over the experts (lane l owns experts
+// l*EPL .. l*EPL + EPL - 1). No pass over the earlier pairs and one block
+// barrier less than sort_small_core.
+#define SORTF_TK 256
+#define SORTF_E 1024
+struct SortFastLds {
+    int wcnt[SORTF_TK / 64][SORTF_E];  // pairs of expert x in wave w
+    int eoff[SORTF_E];
+};
+union SortLds {
+    SortSmallLds small;
+    SortFastLds fast;
+};
+
+__device__ __forceinline__ int wave_incl_scan_i(int x, int lane) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
+    }
+    return x;
+}
+
+static __device__ void sort_small_fast(int e, int Tk, int E, int64_t cap, int R,
+                                       int32_t *__restrict__ off, int64_t *__restrict__ off64,
+                                       int32_t *__restrict__ perm, int64_t *__restrict__ perm64,
+                                       uint8_t *__restrict__ drop, int32_t *__restrict__ tiles,
+                                       int32_t *__restrict__ ntiles, SortFastLds &sm) {
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int NW = (Tk + 63) >> 6;
+    int *flat = &sm.wcnt[0][0];
+    for (int i = t; i < NW * SORTF_E; i += blockDim.x) flat[i] = 0;
+    __syncthreads();
+    int r = 0;  // stable rank: earlier pairs with the same expert
+    if (wave < NW) {
+        uint64_t m = __ballot(e >= 0);
+        for (int b = 0; (1 << b) < E; b++) {
+            const int bit = (e >> b) & 1;
+            const uint64_t bb = __ballot(bit);
+            m &= bit ? bb : ~bb;
+        }
+        r = __popcll(m & ((1ull << lane) - 1ull));
+        if (e >= 0 && r == 0) sm.wcnt[wave][e] = __popcll(m);
+    }
+    __syncthreads();
+    if (e >= 0)
+        for (int w = 0; w < wave; w++) r += sm.wcnt[w][e];
+    if (wave == 0) {
+        // lane l: experts l*EPL .. l*EPL + EPL - 1 (EPL <= 16); their kept
+        // counts are summed here and read again from LDS below (no private
+        // array, which would live in scratch memory)
+        const int EPL = (E + 63) >> 6, x0 = lane * EPL;
+        int ks = 0, ts = 0;
+        for (int u = 0; u < EPL; u++) {
+            const int x = x0 + u;
+            int c = 0;
+            // every count is read (x <= 63 * 16 + 15 stays in the array) so
+            // the reads issue back to back; the unused ones are dropped
+#pragma unroll
+            for (int w = 0; w < SORTF_TK / 64; w++) {
+                const int v = sm.wcnt[w][x];
+                c += w < NW ? v : 0;
+            }
+            const int kc = x < E ? (int)min((int64_t)c, cap) : 0;
+            ks += kc;
+            ts += (kc + R - 1) / R;
+        }
+        const int kin = wave_incl_scan_i(ks, lane), tin = wave_incl_scan_i(ts, lane);
+        int kbase = kin - ks, tbase = tin - ts;
+        for (int u = 0; u < EPL; u++) {
+            const int x = x0 + u;
+            if (x >= E) break;
+            int c = 0;
+#pragma unroll
+            for (int w = 0; w < SORTF_TK / 64; w++) {
+                const int v = sm.wcnt[w][x];
+                c += w < NW ? v : 0;
+            }
+            const int kc = (int)min((int64_t)c, cap);
+            sm.eoff[x] = kbase;
+            off[x] = kbase;
+            if (off64) off64[x] = kbase;
+            put_tiles((int4 *)tiles, tbase, x, kbase, kc, R);
+            kbase += kc;
+            tbase += (kc + R - 1) / R;
+        }
+        if (lane == 63) {
+            off[E] = kin;
+            if (off64) off64[E] = kin;
+            *ntiles = tin;
+        }
+    }
+    __syncthreads();
+    if (e >= 0) {
+        const bool kept = r < cap;
+        if (drop) drop[t] = kept ? 0 : 1;
+        if (kept) {
+            perm[sm.eoff[e] + r] = t;
+            if (perm64) perm64[sm.eoff[e] + r] = t;
+        }
+    }
+}

@@ -102,6 +102,14 @@ CASES = [
     (512, 256, 32, 4, 0, 64, 40),
     (768, 256, 16, 2, 1, 64, 100),
     (1024, 256, 256, 8, 2, 512, 16),
+    # decode with concatenated shared experts: top-k, sort and shared gate/up
+    # in one launch, routed FFN and shared down in another; E = 300 and 520
+    # (not powers of two, up to 16 keys a lane), up to 256 pairs in the
+    # ballot-ranked sort, 320 pairs in the scanning one (k = 20)
+    (256, 256, 64, 8, 2, 128, 16),
+    (512, 256, 300, 6, 2, 256, 7),
+    (256, 256, 520, 16, 3, 128, 16),
+    (256, 256, 40, 20, 2, 128, 16),
     # three to eight shared experts in the combine, with k <= 8 and k > 8
     (256, 128, 16, 4, 3, 64, 100),
     (128, 64, 32, 12, 8, 64, 50),
