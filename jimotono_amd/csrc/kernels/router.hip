@@ -844,21 +844,46 @@ extern "C" int jtk_topk_verify(const double *approx, const double *xinfo, const 
 // token rows hit different banks) and 4 gate rows by LDS-DMA; wave w owns
 // expert 4*blockIdx.x + w and lane 4t + p runs the reference's partial p of
 // token t (element j into partial j % 4, src/moe_layer.c:67-86) as one fp64
-// chain, then (l0 + l1) + (l2 + l3) by lane shuffles. Block b < T also
-// writes token b's int8 codes and scale (the row quantiser,
-// src/w8a8.c:787-855) from the staged row. n % 256 == 0, T * (n + 4) * 4 +
+// chain, then (l0 + l1) + (l2 + l3) by lane shuffles. Blocks nb .. nb+T-1
+// (nb = the logit blocks) each write one token's int8 codes and scale (the
+// row quantiser, src/w8a8.c:787-855) from its row in memory, beside the
+// logit blocks instead of after their chains (measured 8.3 -> 6.1 us at
+// T = 16, E = 256, n = 1024). n % 256 == 0, T * (n + 4) * 4 +
 // 4 * (n + 4) * 4 bytes of LDS.
 #define RL_TMAX 16
 __global__ __launch_bounds__(256) void k_router_logits_small(
-    const float *__restrict__ X, const float *__restrict__ Wg, int T, int E, int n,
+    const float *__restrict__ X, const float *__restrict__ Wg, int T, int E, int n, int nb,
     float *__restrict__ logits, int8_t *__restrict__ Xq, float *__restrict__ sx,
     uint32_t *err) {
     extern __shared__ __attribute__((aligned(16))) float rl_smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if ((int)blockIdx.x >= nb) {  // token blockIdx.x - nb's codes (wave 0)
+        const int r = blockIdx.x - nb;
+        if (wave != 0 || r >= T) return;
+        const float *xr = X + (int64_t)r * n;
+        uint32_t mu = 0;
+        for (int c = lane; c < n; c += 64) mu = max(mu, abs_bits(xr[c]));
+        mu = wave_max_u(mu);
+        const QuantParams qp = quant_params(__builtin_bit_cast(float, mu));
+        if (mu >= 0x7f800000u || !qp.ok) {
+            if (lane == 0) raise_err(err, mu >= 0x7f800000u ? EF_NONFINITE_INPUT : EF_RANGE);
+            return;
+        }
+        if (lane == 0) sx[r] = qp.scale_f;
+        const float inv = quant_inv_f(qp.scale_d);
+        for (int c = lane * 4; c < n; c += 256) {
+            const uint32_t b0 = (uint8_t)quant_code_fast(xr[c], qp.scale_d, inv);
+            const uint32_t b1 = (uint8_t)quant_code_fast(xr[c + 1], qp.scale_d, inv);
+            const uint32_t b2 = (uint8_t)quant_code_fast(xr[c + 2], qp.scale_d, inv);
+            const uint32_t b3 = (uint8_t)quant_code_fast(xr[c + 3], qp.scale_d, inv);
+            *(uint32_t *)(Xq + (int64_t)r * n + c) = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+        }
+        return;
+    }
     const int stride = n + 4;
     float *xs = rl_smem;                  // [T][n + 4]
     float *ws = rl_smem + T * stride;     // [4][n + 4]
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int e = blockIdx.x * 4 + wave;
     const int nc = n / 256;  // 1 KiB copies per row
     for (int c = wave; c < T * nc; c += 4) {
@@ -897,27 +922,6 @@ __global__ __launch_bounds__(256) void k_router_logits_small(
         logits[(int64_t)t * E + e] = f;
     }
     if (__ballot(bad != 0) && lane == 0) raise_err(err, EF_NONFINITE_MID);
-    // token blockIdx.x's codes (wave 0)
-    if (wave != 0 || (int)blockIdx.x >= T) return;
-    const int r = blockIdx.x;
-    const float *xr = xs + r * stride;
-    uint32_t mu = 0;
-    for (int c = lane; c < n; c += 64) mu = max(mu, abs_bits(xr[c]));
-    mu = wave_max_u(mu);
-    const QuantParams qp = quant_params(__builtin_bit_cast(float, mu));
-    if (mu >= 0x7f800000u || !qp.ok) {
-        if (lane == 0) raise_err(err, mu >= 0x7f800000u ? EF_NONFINITE_INPUT : EF_RANGE);
-        return;
-    }
-    if (lane == 0) sx[r] = qp.scale_f;
-    const float inv = quant_inv_f(qp.scale_d);
-    for (int c = lane * 4; c < n; c += 256) {
-        const uint32_t b0 = (uint8_t)quant_code_fast(xr[c], qp.scale_d, inv);
-        const uint32_t b1 = (uint8_t)quant_code_fast(xr[c + 1], qp.scale_d, inv);
-        const uint32_t b2 = (uint8_t)quant_code_fast(xr[c + 2], qp.scale_d, inv);
-        const uint32_t b3 = (uint8_t)quant_code_fast(xr[c + 3], qp.scale_d, inv);
-        *(uint32_t *)(Xq + (int64_t)r * n + c) = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
-    }
 }
 
 extern "C" int jtk_router_logits_small(const float *X, const float *Wg, int T, int E, int n,
@@ -938,9 +942,9 @@ extern "C" int jtk_router_logits_small(const float *X, const float *Wg, int T, i
         if (e != hipSuccess) return (int)e;
         attr_set[dev] = true;
     }
-    const int nb = (E + 3) / 4 > T ? (E + 3) / 4 : T;
-    hipLaunchKernelGGL(k_router_logits_small, dim3((unsigned)nb), dim3(256), lds, s, X, Wg, T, E,
-                       n, logits, Xq, sx, err);
+    const int nb = (E + 3) / 4;  // logit blocks; then one block per token's codes
+    hipLaunchKernelGGL(k_router_logits_small, dim3((unsigned)(nb + T)), dim3(256), lds, s, X, Wg,
+                       T, E, n, nb, logits, Xq, sx, err);
     return (int)hipGetLastError();
 }
 
