@@ -585,10 +585,12 @@ __global__ __launch_bounds__(256, 2) void k_lowbit_grouped(
     __shared__ float rowscale[64];
     __shared__ int rowdst[64];
     const int tile = blockIdx.y;  // x walks the channel groups of a tile first
+    // descriptor and tile count in one round trip (the grid never
+    // passes the descriptor array, so the read is in bounds)
+    const int4 td = ((const int4 *)tiles)[tile];  // {expert, first sorted row, rows}
     if (tile >= *ntiles) return;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar addressing
-    const int4 td = ((const int4 *)tiles)[tile];  // {expert, first sorted row, rows}
     const int e = td.x, pos0 = td.y, nrows = td.z;
     if (tid < 64) {
         const int r = min(tid, nrows - 1);
@@ -756,10 +758,12 @@ __global__ __launch_bounds__(64 * NW) void k_lowbit_gu_q(
     __shared__ uint32_t rbad[64];
     __shared__ double exp_tab[64];
     const int tile = blockIdx.x;
+    // descriptor and tile count in one round trip (the grid never
+    // passes the descriptor array, so the read is in bounds)
+    const int4 td = ((const int4 *)tiles)[tile];  // {expert, first sorted row, rows}
     if (tile >= *ntiles) return;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int4 td = ((const int4 *)tiles)[tile];  // {expert, first sorted row, rows}
     const int e = td.x, pos0 = td.y, nrows = td.z;
     const double tabv = exp_tab_load(lane);  // staged in LDS for the SwiGLU
     if (tid < 64) {
@@ -964,10 +968,12 @@ __global__ __launch_bounds__(256, 2) void k_lowbit_grouped_res(
     __shared__ float rowscale[64];
     __shared__ int rowdst[64];
     const int tile = blockIdx.y;  // x walks the channel groups of a tile first
+    // descriptor and tile count in one round trip (the grid never
+    // passes the descriptor array, so the read is in bounds)
+    const int4 td = ((const int4 *)tiles)[tile];  // {expert, first sorted row, rows}
     if (tile >= *ntiles) return;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar addressing
-    const int4 td = ((const int4 *)tiles)[tile];  // {expert, first sorted row, rows}
     const int e = td.x, pos0 = td.y, nrows = td.z;
     if (tid < 64) {
         const int r = min(tid, nrows - 1);
@@ -1127,10 +1133,12 @@ __global__ __launch_bounds__(256) void k_lowbit_down_rr(
     __shared__ float rsc[64];
     __shared__ int rdst[64];
     const int tile = blockIdx.y;
+    // descriptor and tile count in one round trip (the grid never
+    // passes the descriptor array, so the read is in bounds)
+    const int4 td = tiles[tile];  // {expert, first sorted row, rows}
     if (tile >= *ntiles) return;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int4 td = tiles[tile];  // {expert, first sorted row, rows}
     const int e = td.x, pos0 = td.y, nrows = td.z;
     if (nrows <= 0) return;
     // row scale and destination of row `lane` (wave 0), written to LDS later
@@ -1244,6 +1252,9 @@ __global__ __launch_bounds__(1024) void k_lowbit_skinny(
     typedef typename std::conditional<BITS == 2, uint32_t, uint2>::type raw_t;
     __shared__ float4 tbuf[LS_PANELS][64];
     const int tile = blockIdx.y;  // x walks the channel groups of a tile first
+    // descriptor and tile count in one round trip (the grid never
+    // passes the descriptor array, so the read is in bounds)
+    const int4 td = tiles[tile];  // {expert, first sorted row, rows}
     if (tile >= *ntiles) return;
     const int G = K / 64;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -1253,7 +1264,6 @@ __global__ __launch_bounds__(1024) void k_lowbit_skinny(
     const int nw = blockDim.x >> 6;
     const int gpw = G < 4 ? G : 4;
     const int g0 = wave * gpw;
-    const int4 td = tiles[tile];  // {expert, first sorted row, rows}
     const int e = td.x, pos0 = td.y, nrows = td.z;
     const int pan0 = blockIdx.x * LS_PANELS;
     const uint8_t *wb = Wp + (int64_t)e * wp_stride;
@@ -1426,13 +1436,15 @@ __device__ __forceinline__ void routed_ffn16_block(
     __shared__ float rsa[16], rsq[16];
     __shared__ int rdst[16];
     __shared__ double exp_tab[64];
+    // descriptor and tile count in one round trip (the grid never
+    // passes the descriptor array, so the read is in bounds)
+    const int4 td = tiles[tile];  // {expert, first sorted row, rows}
     if (tile >= *ntiles) return;
     const int lane = threadIdx.x & 63;
     // the SwiGLU's exp table entry, requested before the weights so that its
     // wait does not wait for them
     const double tabv = exp_tab_load(lane);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int4 td = tiles[tile];  // {expert, first sorted row, rows}
     const int e = td.x, pos0 = td.y, nrows = td.z;
     if (nrows <= 0) return;
     const uint8_t *gp = guP + (int64_t)e * gu_pstride;
