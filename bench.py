@@ -93,6 +93,24 @@ def time_fn(torch, fn, steps, warmup, stream):
     return wall, e0.elapsed_time(e1) / steps
 
 
+def spread_fn(torch, fn, n, stream):
+    """Median and median absolute deviation (ms) of n single-step times, from
+    an event recorded after every step (the reference's methodology,
+    bench/common/bench_common.h:39-45). Run outside the timed region: each
+    event adds its marker to the step it closes."""
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+    torch.cuda.synchronize()
+    evs[0].record(stream)
+    for i in range(1, n + 1):
+        fn()
+        evs[i].record(stream)
+    torch.cuda.synchronize()
+    per = sorted(evs[i - 1].elapsed_time(evs[i]) for i in range(1, n + 1))
+    med = per[n // 2]
+    mad = sorted(abs(x - med) for x in per)[n // 2]
+    return med, mad
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -172,6 +190,8 @@ def main():
     L.set_profiling(False)
     assert api.sync_errors(stream) == 0
     serial_ms = sum(stages.values()) / count
+    step_med, step_mad = spread_fn(torch, step, max(args.steps, 50), stream)
+    assert api.sync_errors(stream) == 0
 
     # algorithmic work per stage launch
     ops = {
@@ -221,6 +241,8 @@ def main():
         "event_ms_per_step": ev_ms,
         "serialized_ms_per_step": serial_ms,
         "stages_ms_per_step": {s: v / count for s, v in stages.items()},
+        "step_ms_median": step_med, "step_ms_mad": step_mad,
+        "step_spread_samples": max(args.steps, 50),
     }
 
     # ---------------- PCIe-inclusive rate (never the value) ----------------
@@ -401,6 +423,7 @@ def decode_layer(torch, api, stream, steps, warmup):
         assert rc == 0
         it[0] += 1
     _, ev = time_fn(torch, step, max(steps, 8) * 4, max(warmup, 2) * 4, stream)
+    med, mad = spread_fn(torch, step, 64, stream)
     assert api.sync_errors(stream) == 0
     # weight bytes one forward reads: the shared experts, the fp32 gate and
     # the routed experts its tokens touch (counted on layer 0's routing)
@@ -412,7 +435,8 @@ def decode_layer(torch, api, stream, steps, warmup):
     wbytes = S * (3 * hs * n + 4 * (2 * hs + n)) + 4 * E * n + touched * per_expert
     del layers
     torch.cuda.empty_cache()
-    return {"us_per_layer": ev * 1e3, "tokens": T, "touched_experts": touched,
+    return {"us_per_layer": ev * 1e3, "us_median": med * 1e3, "us_mad": mad * 1e3,
+            "tokens": T, "touched_experts": touched,
             "weight_bytes": wbytes, "gbps": wbytes / (ev / 1e3) / 1e9,
             "hbm_frac": wbytes / (ev / 1e3) / HBM_PEAK}
 
