@@ -156,8 +156,11 @@ def main():
     # steps, so `value` is the layer's steady-state rate.
     step()  # first call: kernel attributes and workspaces
     torch.cuda.synchronize()
-    # single-step spread (its median is robust to the ramp)
+    # single-step spread (its median is robust to the ramp); with --serial
+    # every pass runs its stages in stream order, as the timed region does
+    L.set_profiling(args.serial)
     step_med, step_mad = spread_fn(torch, step, max(args.steps, 50), stream)
+    L.set_profiling(False)
     assert api.sync_errors(stream) == 0
     # profiled pass: every stage in order on the stream, HIP events around
     # each stage give per-kernel launch durations for the roofline
