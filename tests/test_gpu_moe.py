@@ -451,6 +451,35 @@ def test_layer_residual_nonfinite(jt, torch_cuda):
     assert jt.sync_errors() != 0
 
 
+def test_layer_decode_nonfinite_then_clean(jt, orc, torch_cuda):
+    """Decode with concatenated shared experts (the launches that carry the
+    shared experts' blocks and sort in the last top-k block): a NaN token is
+    reported, and the next clean forward of the same layer matches the
+    oracle, so a failed routing leaves the launch's block counter at zero."""
+    torch = torch_cuda
+    n, h, E, k, S, hs, T = 256, 256, 64, 8, 2, 128, 16
+    announce("layer decode non-finite then clean")
+    rng = np.random.default_rng(616)
+    W = mk_weights(rng, n, h, E, S, hs)
+    Wgate, Wg, Wu, Wd, sh = W
+    L = jt.MoE(n, h, E, k, S, hs, T, dev(torch, Wgate), dev(torch, Wg), dev(torch, Wu),
+               dev(torch, Wd), dev(torch, sh[0]), dev(torch, sh[1]), dev(torch, sh[2]))
+    Y = torch.zeros((T, n), dtype=torch.float32, device="cuda")
+    bad = rng.standard_normal((T, n)).astype(np.float32)
+    bad[3, 17] = np.nan
+    assert L.fwd(dev(torch, bad), Y) == 0
+    assert jt.sync_errors() != 0
+    X = rng.standard_normal((T, n)).astype(np.float32)
+    for _ in range(2):
+        assert L.fwd(dev(torch, X), Y) == 0
+        assert jt.sync_errors() == 0
+        o = orc.moe_q(n, h, E, k, S, hs, Wgate, Wg, Wu, Wd, *sh).fwd(X)
+        assert o["rc"] == 0
+        assert np.array_equal(L.read(jt.BUF_IDS, np.int32, (T, k)), o["ids"])
+        assert np.array_equal(L.read(jt.BUF_PERM, np.int32, (T * k,)), o["perm"])
+        close(Y.cpu().numpy(), o["Y"])
+
+
 @pytest.mark.parametrize("router", [True, False])
 def test_layer_save_load_roundtrip(jt, orc, torch_cuda, router):
     """jt_hip_moe_save / jt_hip_moe_load: the reloaded layer (no quantisation,
