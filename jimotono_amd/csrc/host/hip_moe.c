@@ -316,6 +316,9 @@ static const char *const k_stage_names[ST_N] = {
  * layer against 0.370 with one side stream per expert, which leaves fewer
  * CUs to the routed chain) */
 #define MOE_SIDE 1
+/* the fork and join events only order work on this device and the host
+ * never waits on them, so they skip the system-scope fence */
+#define JT_STREAM_EVENT_FLAGS (hipEventDisableTiming | hipEventDisableSystemFence)
 
 struct jt_hip_moe {
     jt_hip_moe_desc d;
@@ -510,11 +513,11 @@ static int moe_finish(jt_hip_moe *L) {
         rc = ffn_reserve(L->sh[s], L->sh_cat ? 64 : T, 0);
     if (rc == JT_OK && L->d.n_shared > 0) {
         const int ns = L->d.n_shared < MOE_SIDE ? L->d.n_shared : MOE_SIDE;
-        hipError_t e = hipEventCreateWithFlags(&L->ev_fork, hipEventDisableTiming);
+        hipError_t e = hipEventCreateWithFlags(&L->ev_fork, JT_STREAM_EVENT_FLAGS);
         for (int i = 0; i < ns && e == hipSuccess; i++) {
             e = hipStreamCreateWithFlags(&L->side[i], hipStreamNonBlocking);
             if (e != hipSuccess) break;
-            e = hipEventCreateWithFlags(&L->ev_join[i], hipEventDisableTiming);
+            e = hipEventCreateWithFlags(&L->ev_join[i], JT_STREAM_EVENT_FLAGS);
             if (e != hipSuccess) {
                 (void)hipStreamDestroy(L->side[i]);
                 break;
