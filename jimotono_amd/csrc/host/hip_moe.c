@@ -678,6 +678,25 @@ static int shared_fused16(jt_hip_moe *L, int T, uint32_t *err, hipStream_t s, hi
     return e ? jt_rt_err(hipErrorLaunchFailure) : JT_OK;
 }
 
+
+/* Forks the shared experts onto the side streams after what s holds so
+ * far (they read Xq and sx) and records their join events. */
+static int fork_shared(jt_hip_moe *L, int T, int fused, uint32_t *err, hipStream_t s) {
+    const int S = L->d.n_shared, n = L->d.n;
+    int le = (int)hipEventRecord(L->ev_fork, s);
+    for (int i = 0; i < L->nside; i++) le |= (int)hipStreamWaitEvent(L->side[i], L->ev_fork, 0);
+    if (fused) /* launch errors are collected; the join still happens */
+        le |= shared_fused(L, T, err, L->side[0], NULL);
+    else
+        for (int e = 0; e < S; e++) {
+            const ffn_ws ws = ffn_own_ws(L->sh[e]);
+            le |= ffn_run_q(L->sh[e], &ws, L->Xq, L->sx, T, L->Ys + (size_t)e * T * n, err,
+                            L->side[e % L->nside], NULL);
+        }
+    for (int i = 0; i < L->nside; i++) le |= (int)hipEventRecord(L->ev_join[i], L->side[i]);
+    return le;
+}
+
 static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
                        const float *d_w, const float *dR, float *dY, int T, void *stream) {
     const jt_hip_moe_desc *d = &L->d;
@@ -716,19 +735,14 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
     const int fork = S > 0 && !L->prof && T > 16;
     const int fused = L->sh_cat && T > 64, fused16 = L->sh_cat && T <= 16;
     if (L->prof) L->ev_fused[slot] = fused || fused16;
-    if (fork) {
-        le |= (int)hipEventRecord(L->ev_fork, s);
-        for (int i = 0; i < L->nside; i++) le |= (int)hipStreamWaitEvent(L->side[i], L->ev_fork, 0);
-        if (fused) /* launch errors are collected; the join still happens */
-            le |= shared_fused(L, T, err, L->side[0], NULL);
-        else
-            for (int e = 0; e < S; e++) {
-                const ffn_ws ws = ffn_own_ws(L->sh[e]);
-                le |= ffn_run_q(L->sh[e], &ws, L->Xq, L->sx, T, L->Ys + (size_t)e * T * n, err,
-                                L->side[e % L->nside], NULL);
-            }
-        for (int i = 0; i < L->nside; i++) le |= (int)hipEventRecord(L->ev_join[i], L->side[i]);
-    }
+    /* with the bound-and-verify router the fork comes after its candidate
+     * selection: the exact stage is then queued before the shared gate/up,
+     * which otherwise holds every CU's registers and leaves the exact
+     * stage (21 us alone) waiting for most of its 100 us (measured at 4096
+     * tokens: 0.319-0.325 ms per layer against 0.331-0.332 forking after
+     * the codes, 0.332-0.334 forking after the approximate logits) */
+    const int fork_late = fork && fast;
+    if (fork && !fork_late) le |= fork_shared(L, T, fused, err, s);
     /* 16-row tiles when experts average at most 16 rows; the single-launch
      * sort up to 1024 pairs */
     const int R = Tk <= 16 * E ? 16 : 64;
@@ -762,7 +776,12 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
                                 L->approx, s);
         prof_mark(L, slot, ST_TOPK, s);
         le |= jtk_topk_verify(L->approx, L->xinfo, L->winfo, dX, L->Wgate, T, E, n, k, L->rcand,
-                              L->rnc, L->ids, L->w, L->logits, err, s);
+                              L->rnc, L->ids, L->w, L->logits, err, fork_late ? 1 : 3, s);
+        if (fork_late) {
+            le |= fork_shared(L, T, fused, err, s);
+            le |= jtk_topk_verify(L->approx, L->xinfo, L->winfo, dX, L->Wgate, T, E, n, k,
+                                  L->rcand, L->rnc, L->ids, L->w, L->logits, err, 2, s);
+        }
     } else {
         le |= jtk_router_logits(dX, L->Wgate, T, E, n, L->logits, err, s);
         prof_mark(L, slot, ST_TOPK, s);

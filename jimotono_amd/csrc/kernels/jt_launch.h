@@ -151,10 +151,12 @@ int jtk_router_approx(const int8_t *Xh, const int8_t *Xl, int n, const double *x
  * codes and scales; n % 256 == 0 */
 int jtk_router_logits_small(const float *X, const float *Wg, int T, int E, int n,
                             float *logits, int8_t *Xq, float *sx, uint32_t *err, hipStream_t s);
+/* stages: bit 0 the candidate selection, bit 1 the exact logits and top-k
+ * (3: both; T <= 256 runs both in one launch, with bit 1) */
 int jtk_topk_verify(const double *approx, const double *xinfo, const double *winfo,
                     const float *X, const float *Wg, int T, int E, int n, int k, int16_t *cand,
                     int32_t *ncand, int32_t *ids, float *w, float *logits, uint32_t *err,
-                    hipStream_t s);
+                    int stages, hipStream_t s);
 
 /* route.hip */
 int jtk_router_logits(const float *X, const float *Wg, int T, int E, int n, float *logits,

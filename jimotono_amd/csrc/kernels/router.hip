@@ -789,9 +789,10 @@ __global__ __launch_bounds__(64) void k_router_topk_small(
 extern "C" int jtk_topk_verify(const double *approx, const double *xinfo, const double *winfo,
                                const float *X, const float *Wg, int T, int E, int n, int k,
                                int16_t *cand, int32_t *ncand, int32_t *ids, float *w,
-                               float *logits, uint32_t *err, hipStream_t s) {
-    if (T <= 0) return 0;
+                               float *logits, uint32_t *err, int stages, hipStream_t s) {
+    if (T <= 0 || !(stages & 3)) return 0;
     if (T <= 256 && E <= RV_EMAX && k >= 1 && k <= 64 && k <= E && n % 256 == 0) {
+        if (!(stages & 2)) return 0;  // one launch: runs with the second stage
         constexpr size_t lds_s = (size_t)(RS_CH + 16 * RS_STRIDE + RV_EMAX) * 4 + 64 * 8 +
                                  (RV_EMAX + 64) * 2;
         static std::atomic<bool> attr_small[64];
@@ -828,12 +829,14 @@ extern "C" int jtk_topk_verify(const double *approx, const double *xinfo, const 
         if (e != hipSuccess) return (int)e;
         attr_set[dev] = true;
     }
-    hipLaunchKernelGGL(k_router_select, dim3((unsigned)((T + RV_WPB - 1) / RV_WPB)),
-                       dim3(64 * RV_WPB), 0, s, approx, (const double2 *)xinfo,
-                       (const double2 *)winfo, T, E, n, k, cand, ncand, logits);
-    hipLaunchKernelGGL(k_router_exact, dim3((unsigned)((T + TPB - 1) / TPB)),
-                       dim3(64 * RX_WPB), lds, s, (const int16_t *)cand, (const int32_t *)ncand,
-                       X, Wg, T, E, n, k, ids, w, logits, err);
+    if (stages & 1)
+        hipLaunchKernelGGL(k_router_select, dim3((unsigned)((T + RV_WPB - 1) / RV_WPB)),
+                           dim3(64 * RV_WPB), 0, s, approx, (const double2 *)xinfo,
+                           (const double2 *)winfo, T, E, n, k, cand, ncand, logits);
+    if (stages & 2)
+        hipLaunchKernelGGL(k_router_exact, dim3((unsigned)((T + TPB - 1) / TPB)),
+                           dim3(64 * RX_WPB), lds, s, (const int16_t *)cand,
+                           (const int32_t *)ncand, X, Wg, T, E, n, k, ids, w, logits, err);
     return (int)hipGetLastError();
 }
 
