@@ -54,13 +54,24 @@ def parse():
                         "two shared and 256 routed experts) and print its JSON line; "
                         "the workload of the decode kernel-trace profile")
     p.add_argument("--only", choices=["w8a8_64", "shared_decode", "routed_decode", "stress",
-                                      "bwd", "gdn2", "proj", "vendor"],
+                                      "bwd", "gdn2", "proj", "vendor", "dropin"],
                    help="run one of the other shapes' benchmarks alone and print its JSON "
                         "(the workloads of their kernel-trace profiles)")
     p.add_argument("--copy-probe", action="store_true",
                    help="also run a plain 256 MiB device copy (the reference kernel "
                         "for scaling HBM byte counters)")
     return p.parse_args()
+
+
+def copy_probe(torch):
+    """Two plain device copies of 256 MiB (the kernel of known size that
+    scales the HBM byte counters FETCH_SIZE and WRITE_SIZE)."""
+    src = torch.empty(64 << 20, device="cuda", dtype=torch.float32).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
 
 
 def make_layer(torch, api, n, h, E, k, S, hs, T, seed, router=True):
@@ -129,12 +140,12 @@ def main():
     # a dedicated stream for the layer and its timing events
     stream = torch.cuda.Stream()
     torch.cuda.set_stream(stream)
-    if args.decode_only:
-        print(json.dumps({"decode_layer_T16": decode_layer(torch, api, stream, args.steps,
-                                                           args.warmup)}), flush=True)
-        return
-    if args.only:
-        print(json.dumps(sub_benchmarks(np, torch, api, stream, only=args.only)), flush=True)
+    if args.decode_only or args.only:
+        if args.copy_probe:
+            copy_probe(torch)
+        res = ({"decode_layer_T16": decode_layer(torch, api, stream, args.steps, args.warmup)}
+               if args.decode_only else sub_benchmarks(np, torch, api, stream, only=args.only))
+        print(json.dumps(res), flush=True)
         return
 
     # ---------------- main workload: full layer prefill ----------------
@@ -179,12 +190,7 @@ def main():
     torch.cuda.synchronize()
     assert api.sync_errors(stream) == 0
     if args.copy_probe:
-        src = torch.empty(64 << 20, device="cuda", dtype=torch.float32).fill_(1.0)
-        dst = torch.empty_like(src)
-        for _ in range(2):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
+        copy_probe(torch)
     # timed region: the production path (shared experts overlap the routed
     # path on side streams), or with --serial every stage in stream order
     if args.serial:
@@ -478,7 +484,53 @@ def sub_benchmarks(np, torch, api, stream, only=None):
         res.update(proj_bench(np, torch, api, stream))
     if want("vendor"):
         res.update(vendor_bench(np, torch, api, stream))
+    if want("dropin"):
+        res.update(dropin_bench(np, torch, api))
     return res
+
+
+DROPIN_MODES = {"fp32": (0, 0), "w8a8": (1, 0), "lowbit_fakequant": (0, 1),
+                "lowbit_lut": (0, 2), "w8a8_and_lowbit_fakequant": (1, 1)}
+
+
+def dropin_bench(np, torch, api):
+    """The drop-in jt_moe_fwd_batch (host pointers, the reference's own
+    layer entry) at the reference trainer's shape: T=512 tokens (seq 128 x
+    batch 4), d=64, h=32, E=8, top-2, one shared expert, cap 1.5
+    (bench/kernel/train_tinystories.c:78-81, 1141-1144), in each of the
+    process-flag modes. Every call copies X and the fp32 weights over PCIe,
+    runs the forward and copies Y, ids, weights and the sort back, as the
+    reference's callers expect; the time per call is wall clock (median of
+    the calls after two warm-up calls)."""
+    T, n, h, E, k, S = 512, 64, 32, 8, 2, 1
+    rng = np.random.default_rng(512)
+    X = rng.standard_normal((T, n)).astype(np.float32)
+    W = [(rng.standard_normal(sh) / np.sqrt(sh[-1])).astype(np.float32)
+         for sh in [(E, n), (E, h, n), (E, h, n), (E, h, n), (S, h, n), (S, h, n), (S, h, n)]]
+    lib = api.lib()
+    res = {}
+    for name, (w8, lb) in DROPIN_MODES.items():
+        assert lib.jt_w8a8_set_enabled(w8) == 0 and lib.jt_lowbit_set_mode(lb) == 0
+        try:
+            for _ in range(2):
+                assert api.moe_fwd_batch(X, *W, k, 1.5)["rc"] == 0
+            ts = []
+            for _ in range(30):
+                t0 = time.perf_counter()
+                r = api.moe_fwd_batch(X, *W, k, 1.5)
+                ts.append(time.perf_counter() - t0)
+                assert r["rc"] == 0
+        finally:
+            lib.jt_w8a8_set_enabled(0)
+            lib.jt_lowbit_set_mode(0)
+        med = float(np.median(ts))
+        res[name] = {"ms_per_call": med * 1e3, "tokens_per_s": T / med,
+                     "mad_ms": float(np.median(np.abs(np.array(ts) - med))) * 1e3}
+    pcie = 4 * (T * n + E * n + 3 * E * h * n + 3 * S * h * n) + 4 * T * n + 12 * T * k
+    return {"dropin_moe_fwd_batch_T512_train": {
+        "shape": {"tokens": T, "d_model": n, "expert_ffn": h, "experts": E, "topk": k,
+                  "shared": S, "cap_factor": 1.5},
+        "includes_pcie": True, "host_bytes_each_way_per_call": pcie, "modes": res}}
 
 
 def vendor_bench(np, torch, api, stream):

@@ -20,7 +20,11 @@
  * values or alpha outside [0,1]: JT_ERR_INVAL, S and the outputs
  * untouched). A caller that keeps states in HBM uses jt_hip_gdn2_* in
  * jimotono/hip_gdn2.h. The scratch arguments are checked for size as the
- * reference checks them; the device kernels use their own workspace.
+ * reference checks them; the device kernels use their own workspace, so the
+ * caller's scratch is left as it was (the reference leaves its normalised
+ * q and k there; their contents after a call are unspecified here). As in
+ * the reference (restrict pointers), S, the outputs and the scratch must
+ * not overlap each other or the inputs; overlap is not detected.
  */
 #include <stddef.h>
 

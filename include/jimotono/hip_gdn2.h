@@ -27,7 +27,11 @@ int jt_hip_gdn2_decode(float *dS, float *dO, const float *dq, const float *dk_,
                        const float *dv_, const float *db, const float *dw,
                        const float *dalpha, int H, int dk, int dv, void *stream);
 
-/* Workspace bytes of jt_hip_gdn2_prefill (0 for invalid arguments):
+/* Heads per prefill call: the heads are a grid dimension of its launches. */
+#define JT_HIP_GDN2_MAX_PREFILL_HEADS 65535
+
+/* Workspace bytes of jt_hip_gdn2_prefill (0 for invalid arguments, H
+ * outside 1..JT_HIP_GDN2_MAX_PREFILL_HEADS included):
  * 4*ceil(H/64)*64 + H*(T/C)*(7*C*dk + 2*C*C)*4 -- one record per (head,
  * chunk), since every chunk's state-independent part is prepared at once. */
 size_t jt_hip_gdn2_prefill_ws_bytes(int H, int T, int C, int dk);
@@ -35,7 +39,8 @@ size_t jt_hip_gdn2_prefill_ws_bytes(int H, int T, int C, int dk);
  * each chunk equal to the reference's jt_gdn2_prefill_chunk{C} on the state
  * the previous chunk left: Q, K, B, Alpha [H][T][dk]; V, W, Out [H][T][dv];
  * S [H][dk][dv] in place. A head with a bad value among its T tokens keeps
- * its S and Out. d_ws: jt_hip_gdn2_prefill_ws_bytes(H, T, C, dk) bytes,
+ * its S and Out. H in 1..JT_HIP_GDN2_MAX_PREFILL_HEADS (JT_ERR_INVAL,
+ * EINVAL otherwise). d_ws: jt_hip_gdn2_prefill_ws_bytes(H, T, C, dk) bytes,
  * 16-byte aligned, not kept between calls. */
 int jt_hip_gdn2_prefill(float *dS, float *dOut, const float *dQ,
                         const float *dK, const float *dV, const float *dB,

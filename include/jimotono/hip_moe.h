@@ -19,9 +19,12 @@
  * the kernels (a non-finite activation, an overflowing epilogue) raise bits in
  * the device error word of the stream the call was made on (each stream has
  * its own word, so one caller never reads another stream's bits; past 63
- * distinct streams the rest share one word) instead of a partial result
- * being trusted; jt_hip_sync_errors() waits for a stream and returns (and
- * clears) the bits raised so far by calls on that stream.
+ * streams in use at once the rest share one word) instead of a partial
+ * result being trusted; jt_hip_sync_errors() waits for a stream and returns
+ * (and clears) the bits raised so far by calls on that stream. The word is
+ * keyed by the stream handle: call jt_hip_stream_forget() before destroying
+ * a stream the library has run on, since HIP may hand the same handle to a
+ * later stream, which would otherwise inherit unread bits.
  *
  * Formats of a prepared layer (built on the GPU from fp32 weights):
  *  - shared experts: int8 codes, one fp32 scale per output channel (the
@@ -54,6 +57,17 @@ int jt_hip_init(int device);
  * *out_flags gets the raised JT_HIP_EF_* bits (0 = clean). Returns JT_OK, or
  * JT_ERR_IO on a HIP failure. */
 int jt_hip_sync_errors(void *stream, uint32_t *out_flags);
+/* Release `stream`'s error word: waits for the stream, clears its word
+ * (unread bits are dropped) and frees the slot for the next new stream.
+ * Call it before destroying a stream the library has launched on. A stream
+ * the library has not seen is a no-op. No reference counterpart: the
+ * reference has no streams. Returns JT_OK, or JT_ERR_IO on a HIP failure. */
+int jt_hip_stream_forget(void *stream);
+/* Number of device allocations (hipMalloc) the library has made so far in
+ * this process: a diagnostic that lets a caller check that a call allocated
+ * nothing. No reference counterpart (the reference allocates host memory
+ * only). Returns JT_OK, or JT_ERR_INVAL (EINVAL) for a NULL out. */
+int jt_hip_alloc_count(uint64_t *out);
 
 #define JT_HIP_EF_NONFINITE_INPUT 0x1u /* NaN/Inf in an activation row */
 #define JT_HIP_EF_RANGE 0x2u           /* epilogue value overflowed fp32 */

@@ -69,6 +69,8 @@ _PROTOS = {
     "jt_moe_fwd_batch_unchecked": [_vp] * 9 + [_i] * 6 + [_vp] * 7 + [_fl] + [_vp] * 5,
     "jt_hip_init": [_i],
     "jt_hip_sync_errors": [_vp, C.POINTER(C.c_uint32)],
+    "jt_hip_stream_forget": [_vp],
+    "jt_hip_alloc_count": [C.POINTER(C.c_uint64)],
     "jt_hip_quant_rows": [_vp, _i, _i, _vp, _vp, _vp],
     "jt_hip_w8a8_prepare": [_vp, _i, _i, C.POINTER(_vp)],
     "jt_hip_w8a8_prepare_kn": [_vp, _vp, _i, _i, C.POINTER(_vp)],
@@ -502,6 +504,19 @@ def sync_errors(stream=None) -> int:
     f = C.c_uint32(0)
     _check(lib().jt_hip_sync_errors(_stream(stream), C.byref(f)), "jt_hip_sync_errors")
     return f.value
+
+
+def stream_forget(stream) -> None:
+    """Release the device error word of `stream` (call before the stream is
+    destroyed; HIP may reuse its handle for a later stream)."""
+    _check(lib().jt_hip_stream_forget(_stream(stream)), "jt_hip_stream_forget")
+
+
+def alloc_count() -> int:
+    """Device allocations the library has made so far in this process."""
+    v = C.c_uint64(0)
+    _check(lib().jt_hip_alloc_count(C.byref(v)), "jt_hip_alloc_count")
+    return v.value
 
 
 def quant_rows(X, Xq, scale, stream=None):

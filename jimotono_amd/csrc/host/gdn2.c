@@ -192,7 +192,8 @@ int jt_hip_gdn2_decode(float *dS, float *dO, const float *dq, const float *dk_,
 }
 
 size_t jt_hip_gdn2_prefill_ws_bytes(int H, int T, int C, int dk) {
-    if (H <= 0 || (C != 16 && C != 32) || T <= 0 || T % C || dk <= 0 || dk > JT_GDN2_MAX_D)
+    if (H <= 0 || H > JT_HIP_GDN2_MAX_PREFILL_HEADS || (C != 16 && C != 32) || T <= 0 ||
+        T % C || dk <= 0 || dk > JT_GDN2_MAX_D)
         return 0;
     return jtk_gdn2_prefill_ws_bytes(H, T, C, dk);
 }
@@ -201,7 +202,8 @@ int jt_hip_gdn2_prefill(float *dS, float *dOut, const float *dQ, const float *dK
                         const float *dV, const float *dB, const float *dW, const float *dA,
                         int H, int T, int C, int dk, int dv, void *d_ws, size_t ws_bytes,
                         void *stream) {
-    if (!dS || !dOut || !dQ || !dK || !dV || !dB || !dW || !dA || !d_ws || H <= 0)
+    if (!dS || !dOut || !dQ || !dK || !dV || !dB || !dW || !dA || !d_ws || H <= 0 ||
+        H > JT_HIP_GDN2_MAX_PREFILL_HEADS)
         FAIL(JT_ERR_INVAL, EINVAL);
     if (!dims_ok(dk, dv) || (C != 16 && C != 32) || T <= 0 || T % C) FAIL(JT_ERR_INVAL, EINVAL);
     if ((int64_t)T * (dk > dv ? dk : dv) > INT32_MAX) FAIL(JT_ERR_INVAL, EINVAL);

@@ -37,6 +37,7 @@ enum {
     JT_SLOT_N,
     JT_SLOT_O,
     JT_SLOT_P,
+    JT_SLOT_LAYER, /* the drop-in layer forward's workspace (host/moe_layer.c) */
     JT_NSLOTS
 };
 
@@ -75,5 +76,13 @@ int jt_rt_h2d(jt_rt *rt, void *dst, const void *src, size_t bytes);
 int jt_rt_d2h(jt_rt *rt, void *dst, const void *src, size_t bytes);
 
 static inline size_t jt_round_up(size_t x, size_t m) { return (x + m - 1) / m * m; }
+
+/* Every device allocation of the host layer goes through jt_rt_malloc, which
+ * counts the successful ones (jt_hip_alloc_count reads the count), so a test
+ * can show that an entry point allocated nothing. */
+hipError_t jt_rt_malloc(void **p, size_t bytes);
+#ifndef JT_RT_NO_MALLOC_MACRO
+#define hipMalloc(p, bytes) jt_rt_malloc((void **)(p), (bytes))
+#endif
 
 #endif /* JT_RT_H */

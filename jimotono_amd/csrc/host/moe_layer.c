@@ -34,28 +34,20 @@
 int jt_dev_lowbit_gemm_lut(jt_rt *rt, const float *dX, const float *dW, float *dY, int me,
                            int h, int k, int bits);
 
-/* allocation list freed at the end of a forward */
+/* The forward's device buffers are carved out of one grow-only workspace
+ * of the runtime (slot JT_SLOT_LAYER), kept between calls: the buffer list
+ * runs once with base == NULL to size the workspace, then again to hand out
+ * the pieces, 256-byte aligned. A call of the same or a smaller shape
+ * allocates nothing. */
 typedef struct {
-    void *p[64];
-    int n;
-    hipError_t e;
+    char *base;
+    size_t off;
 } arena_t;
 
 static void *aalloc(arena_t *a, size_t bytes) {
-    void *p = NULL;
-    if (a->e != hipSuccess || a->n >= 64) {
-        if (a->e == hipSuccess) a->e = hipErrorOutOfMemory;
-        return NULL;
-    }
-    a->e = hipMalloc(&p, bytes ? bytes : 16);
-    if (a->e != hipSuccess) return NULL;
-    a->p[a->n++] = p;
+    void *p = a->base ? a->base + a->off : NULL;
+    a->off += jt_round_up(bytes ? bytes : 16, 256);
     return p;
-}
-
-static void afree(arena_t *a) {
-    for (int i = 0; i < a->n; i++) (void)hipFree(a->p[i]);
-    a->n = 0;
 }
 
 /* W8A8 expert GEMM scratch, sized for the largest call of one forward */
@@ -144,7 +136,9 @@ static int fwd_batch(const float *X, const float *Wgate, const float *Wg, const 
     const int Kpmax = (int)jt_round_up((size_t)(n > h ? n : h), 64);
     const int Npmax = (int)jt_round_up((size_t)(n > h ? n : h), 128);
     const size_t Mmax = Tk > (size_t)T ? Tk : (size_t)T;
-    arena_t a = {.n = 0, .e = hipSuccess};
+    int rc = JT_OK;
+    arena_t a = {.base = NULL, .off = 0};
+carve:; /* first pass sizes the workspace (base NULL), the second carves it */
     float *dX = aalloc(&a, Tn * 4), *dWgate = aalloc(&a, (size_t)E * n * 4);
     float *dWg = aalloc(&a, E * nh * 4), *dWu = aalloc(&a, E * nh * 4);
     float *dWd = aalloc(&a, E * nh * 4);
@@ -179,12 +173,21 @@ static int fwd_batch(const float *X, const float *Wgate, const float *Wg, const 
     w8.sB1 = aalloc(&a, 16);
     w8.sA = aalloc(&a, Mmax * 4);
     w8.sB = aalloc(&a, (size_t)Npmax * 4);
-    int rc = jt_rt_err(a.e);
+    if (!a.base) {
+        a.base = jt_rt_buf(rt, JT_SLOT_LAYER, a.off, &rc);
+        if (!a.base) return rc;
+        a.off = 0;
+        goto carve;
+    }
     int64_t *hoff = malloc(((size_t)E + 1) * 8);
-    if (rc == JT_OK && !hoff) rc = JT_ERR_NOMEM, errno = ENOMEM;
-    if (rc != JT_OK) goto out;
-#define H2D(d, h_, b) \
-    if (rc == JT_OK) rc = jt_rt_h2d(rt, (d), (h_), (b))
+    if (!hoff) {
+        errno = ENOMEM;
+        return JT_ERR_NOMEM;
+    }
+    /* inputs in stream order ahead of the kernels (no wait per copy) */
+#define H2D(d, h_, b)                                                                    \
+    if (rc == JT_OK)                                                                     \
+    rc = jt_rt_err(hipMemcpyAsync((d), (h_), (b), hipMemcpyHostToDevice, s))
     H2D(dX, X, Tn * 4);
     H2D(dWgate, Wgate, (size_t)E * n * 4);
     H2D(dWg, Wg, E * nh * 4);
@@ -335,7 +338,6 @@ out:
         (void)jt_rt_flags(rt, s, &dropped);
         errno = saved;
     }
-    afree(&a);
     free(hoff);
     return rc;
 }

@@ -6,10 +6,12 @@
  * host-pointer entry points are not reentrant: they share the staging
  * buffers and the error word of one process-wide runtime.
  */
+#define JT_RT_NO_MALLOC_MACRO /* this file defines the counting wrapper */
 #include "jt_rt.h"
 
 #include <errno.h>
 #include <pthread.h>
+#include <stdatomic.h>
 #include <string.h>
 
 #include "jimotono/hip_moe.h"
@@ -18,10 +20,30 @@ static jt_rt g_rt;
 static int g_req_device = 0;
 
 /* stream -> error word: slot i (0 .. JT_ERR_WORDS - 2) belongs to
- * g_err_stream[i]; the last slot is shared by streams past the table */
+ * g_err_stream[i] while g_err_live[i]; the last slot is shared by streams
+ * past the table. jt_hip_stream_forget frees a slot (its word cleared), and
+ * the next new stream takes the lowest free slot. */
 static pthread_mutex_t g_err_mu = PTHREAD_MUTEX_INITIALIZER;
 static hipStream_t g_err_stream[JT_ERR_WORDS - 1];
+static unsigned char g_err_live[JT_ERR_WORDS - 1];
 static int g_err_used;
+
+static atomic_ullong g_allocs; /* successful device allocations so far */
+
+hipError_t jt_rt_malloc(void **p, size_t bytes) {
+    hipError_t e = hipMalloc(p, bytes);
+    if (e == hipSuccess) atomic_fetch_add(&g_allocs, 1ull);
+    return e;
+}
+
+int jt_hip_alloc_count(uint64_t *out) {
+    if (!out) {
+        errno = EINVAL;
+        return JT_ERR_INVAL;
+    }
+    *out = (uint64_t)atomic_load(&g_allocs);
+    return JT_OK;
+}
 
 int jt_rt_err(hipError_t e) {
     if (e == hipSuccess) return JT_OK;
@@ -50,8 +72,8 @@ jt_rt *jt_rt_get(void) {
      * preparation are ordered after work the caller queued on the null
      * stream (torch's default stream, for one) */
     if (hipStreamCreateWithFlags(&g_rt.stream, hipStreamDefault) != hipSuccess ||
-        hipMalloc((void **)&g_rt.d_err, JT_ERR_WORDS * JT_ERR_STRIDE * 4) != hipSuccess ||
-        hipMalloc((void **)&g_rt.d_scratch, 4096) != hipSuccess ||
+        jt_rt_malloc((void **)&g_rt.d_err, JT_ERR_WORDS * JT_ERR_STRIDE * 4) != hipSuccess ||
+        jt_rt_malloc((void **)&g_rt.d_scratch, 4096) != hipSuccess ||
         hipMemset(g_rt.d_err, 0, JT_ERR_WORDS * JT_ERR_STRIDE * 4) != hipSuccess) {
         errno = EIO;
         return NULL;
@@ -95,7 +117,7 @@ void *jt_rt_buf(jt_rt *rt, int s, size_t bytes, int *rc) {
         rt->slot_bytes[s] = 0;
     }
     size_t want = jt_round_up(bytes, 1u << 16);
-    hipError_t e = hipMalloc(&rt->slot[s], want);
+    hipError_t e = jt_rt_malloc(&rt->slot[s], want);
     if (e != hipSuccess) {
         rt->slot[s] = NULL;
         *rc = jt_rt_err(e);
@@ -107,11 +129,48 @@ void *jt_rt_buf(jt_rt *rt, int s, size_t bytes, int *rc) {
 
 uint32_t *jt_rt_errw(jt_rt *rt, hipStream_t stream) {
     pthread_mutex_lock(&g_err_mu);
-    int i = 0;
-    while (i < g_err_used && g_err_stream[i] != stream) i++;
-    if (i == g_err_used && g_err_used < JT_ERR_WORDS - 1) g_err_stream[g_err_used++] = stream;
+    int i = 0, freed = -1;
+    while (i < g_err_used && !(g_err_live[i] && g_err_stream[i] == stream)) {
+        if (!g_err_live[i] && freed < 0) freed = i;
+        i++;
+    }
+    if (i == g_err_used) { /* a new stream: a freed slot (word already zero) first */
+        if (freed >= 0)
+            i = freed;
+        else if (g_err_used < JT_ERR_WORDS - 1)
+            g_err_used++;
+        if (i < JT_ERR_WORDS - 1) {
+            g_err_stream[i] = stream;
+            g_err_live[i] = 1;
+        }
+    }
     pthread_mutex_unlock(&g_err_mu);
     return rt->d_err + (size_t)i * JT_ERR_STRIDE;
+}
+
+int jt_hip_stream_forget(void *stream) {
+    jt_rt *rt = jt_rt_get();
+    if (!rt) return JT_ERR_IO;
+    hipStream_t st = (hipStream_t)stream;
+    pthread_mutex_lock(&g_err_mu);
+    int i = 0;
+    while (i < g_err_used && !(g_err_live[i] && g_err_stream[i] == st)) i++;
+    int rc = JT_OK;
+    if (i < g_err_used) {
+        /* the stream's queued work may still raise bits: let it finish,
+         * then clear the word so the slot's next owner starts clean */
+        const uint32_t zero = 0;
+        hipError_t e = hipStreamSynchronize(st);
+        if (e == hipSuccess)
+            e = hipMemcpy(rt->d_err + (size_t)i * JT_ERR_STRIDE, &zero, sizeof(zero),
+                          hipMemcpyHostToDevice);
+        if (e == hipSuccess)
+            g_err_live[i] = 0;
+        else
+            rc = jt_rt_err(e);
+    }
+    pthread_mutex_unlock(&g_err_mu);
+    return rc;
 }
 
 int jt_rt_flags(jt_rt *rt, hipStream_t stream, uint32_t *flags) {

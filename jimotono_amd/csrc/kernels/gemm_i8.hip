@@ -49,11 +49,17 @@
 // fixed strides (the shared experts' down projections in one launch), and
 // hpl > 0 sends SwiGLU hidden column x to C[(x / hpl) * plane + m * ldc +
 // x % hpl] (the shared experts' gate/ups over concatenated panels).
+// rt16 != 0 instead makes blockIdx.y a 16-row tile of one GEMM of up to
+// 16 * gridDim.y rows (rows 16y .. 16y+15 of A, sA and C): a GEMM of 17 to
+// 64 rows then spreads over 4 x the blocks, each with one weight panel
+// unit, and the blocks of one panel unit (x fixed) sit on one XCD when
+// gridDim.x is a multiple of 8, so the panel is fetched once per XCD.
 struct SkBatch {
     int hpl;
     int64_t plane, bsA, bsW;
     int bsB;
     int64_t bsC;
+    int rt16;
 };
 
 // One block's work, for block (bx, by) of the grid: k_w8a8_skinny below, and
@@ -63,7 +69,17 @@ __device__ __forceinline__ void w8a8_skinny_block(
     int bx, int by, const void *__restrict__ Ain, int lda, const float *__restrict__ sAin,
     const int8_t *__restrict__ Wp, const float *__restrict__ sB, int M, int N, int Kp, int K,
     float *__restrict__ C, int ldc, uint32_t *err, SkBatch bt) {
-    if (by) {  // the by-th GEMM of a batch
+    constexpr bool QA = QV > 0;
+    if (bt.rt16) {  // rows 16 by .. 16 by + 15 of one GEMM
+        const int r0 = 16 * by;
+        if (QA)
+            Ain = (const float *)Ain + (int64_t)r0 * lda;
+        else
+            Ain = (const int8_t *)Ain + (int64_t)r0 * lda;
+        if (!QA) sAin += r0;
+        C += (int64_t)r0 * ldc;
+        M = min(16, M - r0);
+    } else if (by) {  // the by-th GEMM of a batch
         Ain = (const int8_t *)Ain + by * bt.bsA;
         Wp += by * bt.bsW;
         sB += (int64_t)by * bt.bsB;
@@ -72,7 +88,6 @@ __device__ __forceinline__ void w8a8_skinny_block(
     __shared__ v4i red[SK_WAVES][NP][64];
     extern __shared__ __attribute__((aligned(16))) int8_t sk_aq[];  // QA: [16][Kp + 16]
     __shared__ float sk_sa[16];
-    constexpr bool QA = QV > 0;
     constexpr int NV = QA ? QV : 1;
     const int tid = threadIdx.x, lane = tid & 63;
     // wave-uniform in a scalar register: guards on it then branch, which
@@ -88,6 +103,19 @@ __device__ __forceinline__ void w8a8_skinny_block(
     v4i acc[NP];
 #pragma unroll
     for (int q = 0; q < NP; q++) acc[q] = (v4i){0, 0, 0, 0};
+    // wave 0's epilogue scales, requested now so that their latency hides
+    // behind the weight stream instead of following the reduction
+    // (element r of lane l: row 4*(l/16) + r, channel l%16 of each panel)
+    const int lr = (lane >> 4) * 4, lc = lane & 15;
+    float sbf[NP], saf[4];
+    if (wave == 0) {
+#pragma unroll
+        for (int q = 0; q < NP; q++) sbf[q] = sB[min((p0 + q) * 16 + lc, N - 1)];
+        if (!QA) {
+#pragma unroll
+            for (int r = 0; r < 4; r++) saf[r] = sAin[min(lr + r, M - 1)];
+        }
+    }
     v4i b0[SK_UNROLL][NP];  // QA: the first round's weights
     if (QA) {
         // the row loads go first: they are L2 hits and the quantiser needs
@@ -203,14 +231,11 @@ __device__ __forceinline__ void w8a8_skinny_block(
         for (int w = 1; w < SK_WAVES; w++) t += red[w][q][lane];
         acc[q] = t;
     }
-    // element r of lane l: row 4*(l/16) + r, channel l%16 of each panel.
-    // Scales first: loads and stores share one vmcnt on gfx9.
-    const int lr = (lane >> 4) * 4, lc = lane & 15;
     double sa[4], sb[NP];
 #pragma unroll
-    for (int r = 0; r < 4; r++) sa[r] = (double)sA[min(lr + r, M - 1)];
+    for (int r = 0; r < 4; r++) sa[r] = (double)(QA ? sA[min(lr + r, M - 1)] : saf[r]);
 #pragma unroll
-    for (int q = 0; q < NP; q++) sb[q] = (double)sB[min((p0 + q) * 16 + lc, N - 1)];
+    for (int q = 0; q < NP; q++) sb[q] = (double)sbf[q];
     uint32_t bad = 0, badmid = 0;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
@@ -429,15 +454,20 @@ extern "C" int jtk_w8a8_gemm_ev(const int8_t *A, int lda, const float *sA, const
             hipLaunchKernelGGL((k_w8a8_skinny<EPI_PLAIN, 1, 0>), dim3((unsigned)(Np / 16)),
                                dim3(64 * SK_WAVES), 0, s, (const void *)A, lda, sA, Wp, sB, M, N,
                                Kp, Kp, C, ldc, err, SkBatch{});
-    } else if (M <= 64) {  // measured: 1.7-2.5x faster than the 128-row tiles
+    } else if (M <= 64) {
+        // 16-row tiles of the skinny GEMM, one per grid row: 4x the blocks
+        // of one 64-row block per panel unit
+        SkBatch bt{};
+        bt.rt16 = 1;
+        const unsigned ty = (unsigned)((M + 15) / 16);
         if (swiglu)
-            hipLaunchKernelGGL((k_w8a8_rows64<EPI_SWIGLU, 2>), dim3((unsigned)(Np / 32)),
-                               dim3(64 * R64_WAVES), 0, s, A, lda, sA, Wp, sB, M, N, Kp, C, ldc,
-                               err);
+            hipLaunchKernelGGL((k_w8a8_skinny<EPI_SWIGLU, 2, 0>), dim3((unsigned)(Np / 32), ty),
+                               dim3(64 * SK_WAVES), 0, s, (const void *)A, lda, sA, Wp, sB, M, N,
+                               Kp, Kp, C, ldc, err, bt);
         else
-            hipLaunchKernelGGL((k_w8a8_rows64<EPI_PLAIN, 1>), dim3((unsigned)(Np / 16)),
-                               dim3(64 * R64_WAVES), 0, s, A, lda, sA, Wp, sB, M, N, Kp, C, ldc,
-                               err);
+            hipLaunchKernelGGL((k_w8a8_skinny<EPI_PLAIN, 1, 0>), dim3((unsigned)(Np / 16), ty),
+                               dim3(64 * SK_WAVES), 0, s, (const void *)A, lda, sA, Wp, sB, M, N,
+                               Kp, Kp, C, ldc, err, bt);
     } else {
         // Tile choice (measured on MI355X): few 128x128 tiles -> 8 waves per
         // block with an intra-block k-split; otherwise 128 x 256 tiles of
@@ -839,7 +869,10 @@ __global__ __launch_bounds__(64 * NW) void k_lowbit_gu_q(
     exp_tab_stage(exp_tab, lane, tabv);
     uint32_t gmx = 0;  // max |g|, |u| bits: non-finite iff >= those of +inf
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < 4; i++) {
+        // wave-uniform: a short tile's padding row groups have no SwiGLU
+        // (their pmax entries stay unset and their codes are never written)
+        if (16 * i >= nrows) continue;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const int rr = 16 * i + lr + r;
@@ -859,6 +892,7 @@ __global__ __launch_bounds__(64 * NW) void k_lowbit_gu_q(
             m = row16_allmax_u(m);  // over this wave's 16 * NJ channels of the row
             if (lc == 0) pmax[wave][rr] = m;
         }
+    }
     if (gmx >= 0x7f800000u) flags |= EF_RANGE | EF_NONFINITE_MID;
     __syncthreads();
     // ---- the row quantiser's parameters, once per row ----
@@ -879,7 +913,8 @@ __global__ __launch_bounds__(64 * NW) void k_lowbit_gu_q(
     __syncthreads();
     // ---- codes, straight to Sq [sorted row][h] ----
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < 4; i++) {
+        if (16 * i >= nrows) continue;  // wave-uniform, as above
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const int rr = 16 * i + lr + r;
@@ -894,6 +929,7 @@ __global__ __launch_bounds__(64 * NW) void k_lowbit_gu_q(
                 qrow[16 * jj] = (int8_t)q;
             }
         }
+    }
     if (flags) raise_err(err, flags);
 }
 
@@ -1733,6 +1769,9 @@ extern "C" int jtk_routed_ffn16(const int8_t *Xq, const float *sx, const int32_t
 // the block that counts ntb acquires every block's ids, sorts them (as
 // k_sort_small) and returns the counter to zero for the next launch.
 static_assert(RF_WAVES == SK_WAVES, "one block size for both kinds of block");
+// sort_small_core and its block scan assume a block of exactly SORT_SMALL
+// threads (they read every wave's partial sum and clear counts with that stride)
+static_assert(64 * SK_WAVES == SORT_SMALL, "the merged sort needs SORT_SMALL threads");
 
 template <int EPL>
 __global__ __launch_bounds__(64 * SK_WAVES) void k_decode_route_shared_gu(

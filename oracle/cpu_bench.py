@@ -279,6 +279,26 @@ def attn_proj(R, seconds, M, N=3072, K=1024, sample=16, seed=9):
     return {"rows_timed": m, "us_per_call": med / m * M * 1e6, "trials": nt}
 
 
+DROPIN_MODES = {"fp32": (0, 0), "w8a8": (1, 0), "lowbit_fakequant": (0, 1),
+                "lowbit_lut": (0, 2), "w8a8_and_lowbit_fakequant": (1, 1)}
+
+
+def dropin_layer(R, seconds, T=512, n=64, h=32, E=8, k=2, S=1, seed=512):
+    """The reference's jt_moe_fwd_batch at its trainer's shape
+    (bench/kernel/train_tinystories.c:78-81) in each flag mode, the inputs of
+    bench.py's drop-in sub-benchmark."""
+    rng = np.random.default_rng(seed)
+    X = rng.standard_normal((T, n)).astype(np.float32)
+    W = [(rng.standard_normal(sh) / np.sqrt(sh[-1])).astype(np.float32)
+         for sh in [(E, n), (E, h, n), (E, h, n), (E, h, n), (S, h, n), (S, h, n), (S, h, n)]]
+    out = {}
+    for name, (w8, lb) in DROPIN_MODES.items():
+        med, mad, nt = trials(lambda: R.moe_fwd_batch(X, *W, k, 1.5, w8, lb), seconds / 5)
+        out[name] = {"ms_per_call": med * 1e3, "mad_ms": mad * 1e3, "trials": nt,
+                     "tokens_per_s": T / med}
+    return {"modes": out}
+
+
 def decode_and_stress(seconds):
     """The W8A8 GEMM 64x1024x1024, the shared-expert decode at 1, 4 and 16
     rows, the routed decode at 16 tokens, a token sample of the E=512
@@ -310,6 +330,7 @@ def decode_and_stress(seconds):
                 res["moe_bwd_T512_train"] = bwd_batch(R, seconds, 512, 64, 32, 8, 2, 1)
                 res["moe_bwd_T4096_layer"] = bwd_batch(R, seconds, 4096, 1024, 256, 64, 8, 1,
                                                        max_tokens=512)
+                res["dropin_moe_fwd_batch_T512_train"] = dropin_layer(R, seconds)
                 res["gdn2_decode_H512"] = gdn2_decode(R, seconds)
                 res["gdn2_prefill_T4096_H8"] = gdn2_prefill(R, seconds)
             for m in (1, 16, 4096):

@@ -128,11 +128,15 @@ def test_batch_sort(jt, orc, cap, T, k, E):
     assert np.array_equal(drop, drop2) and dropped == int(drop2.sum())
 
 
+@pytest.mark.parametrize("shape", [(12, 128, 64, 8, 2, 1), (512, 256, 128, 64, 8, 1)],
+                         ids=["T12", "T512E64k8"])
 @pytest.mark.parametrize("w8,lb", [(0, 0), (1, 0), (0, 1), (0, 2), (1, 1)])
-def test_moe_fwd_batch_modes(jt, orc, w8, lb):
-    announce(f"moe_fwd_batch w8a8={w8} lowbit={lb}")
-    rng = np.random.default_rng(10 + 3 * w8 + lb)
-    T, n, h, E, k, S = 12, 128, 64, 8, 2, 1
+def test_moe_fwd_batch_modes(jt, orc, w8, lb, shape):
+    """The drop-in layer entry in all five flag modes, at a toy shape and at
+    T=512, E=64, k=8 (4096 routed pairs, capacity 1.25 drops some)."""
+    T, n, h, E, k, S = shape
+    announce(f"moe_fwd_batch w8a8={w8} lowbit={lb} T={T} n={n} h={h} E={E} k={k}")
+    rng = np.random.default_rng(10 + 3 * w8 + lb + T)
     X = rng.standard_normal((T, n)).astype(np.float32)
     W = [(rng.standard_normal(s) / 8).astype(np.float32)
          for s in [(E, n), (E, h, n), (E, h, n), (E, h, n), (S, h, n), (S, h, n), (S, h, n)]]

@@ -46,6 +46,7 @@ def check(orc, X, Wgate, k, ids, w, lg):
     bad = np.nonzero((ids != oids).any(axis=1))[0]
     assert bad.size == 0, f"tokens with other ids: {bad[:10]}"
     np.testing.assert_allclose(w, ow, rtol=1e-6, atol=0)
+    assert np.array_equal(w.view(np.uint32), ow.view(np.uint32)), "routing weights' bits"
     sel = np.take_along_axis(lg, ids.astype(np.int64), axis=1)
     osel = np.take_along_axis(olg, oids, axis=1)
     assert np.array_equal(bits(sel), bits(osel))

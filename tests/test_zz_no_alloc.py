@@ -1,23 +1,17 @@
 """jt_hip_ffn_fwd_noalloc: the W8A8 SwiGLU expert on the library's fixed
 device scratch, against jt_hip_ffn_fwd (its own buffers) on the same inputs,
-bit for bit, on two calls in a row with the second one smaller. The device's
-free memory must not change across the no-allocation calls."""
-import ctypes as C
+bit for bit, on two calls in a row with the second one smaller. The
+library's own count of device allocations (jt_hip_alloc_count, every
+hipMalloc of the library goes through it) must not move across the
+no-allocation calls. The count is per process, so other processes on the
+GPU cannot disturb it, unlike the device's free memory."""
 import errno as E
 
-import numpy as np
 import pytest
 
 from conftest import announce
 
 pytestmark = pytest.mark.gpu
-
-
-def _free_bytes():
-    hip = C.CDLL("libamdhip64.so")
-    free, total = C.c_size_t(), C.c_size_t()
-    assert hip.hipMemGetInfo(C.byref(free), C.byref(total)) == 0
-    return free.value
 
 
 @pytest.mark.parametrize("n,h,Ts", [(1024, 2816, (16, 4)), (1024, 2816, (300, 17)),
@@ -39,10 +33,10 @@ def test_noalloc_matches_ffn_fwd(jt, torch_cuda, n, h, Ts):
         torch.cuda.synchronize()
         F.fwd(X, Y_ref, stream)
         torch.cuda.synchronize()
-        free0 = _free_bytes()
+        n0 = jt.alloc_count()
         assert F.fwd_noalloc(X, Y, stream) == 0
         torch.cuda.synchronize()
-        assert _free_bytes() == free0
+        assert jt.alloc_count() == n0
         assert jt.sync_errors() == 0
         assert torch.equal(Y.view(torch.int32), Y_ref.view(torch.int32)), f"T={T} differs"
 
@@ -56,6 +50,7 @@ def test_noalloc_rejects_too_many_rows(jt, torch_cuda):
     X = torch.randn(T, n, generator=g, device="cuda")
     Y = torch.zeros(T, n, device="cuda")
     torch.cuda.synchronize()
+    n0 = jt.alloc_count()
     assert F.fwd_noalloc(X[:1110], Y[:1110]) == 0
     torch.cuda.synchronize()
     Y.zero_()
@@ -63,4 +58,5 @@ def test_noalloc_rejects_too_many_rows(jt, torch_cuda):
     assert F.fwd_noalloc(X, Y) == jt.JT_ERR_NOSUP and jt.errno() == E.E2BIG
     torch.cuda.synchronize()
     assert not Y.any()                  # nothing was enqueued
+    assert jt.alloc_count() == n0
     assert jt.sync_errors() == 0
