@@ -719,8 +719,14 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
     const int small = !d_ids && L->Wgate && T <= 16 && n % 256 == 0 &&
                       (size_t)(T + 4) * (n + 4) * 4 <= 160 * 1024;
     const int fast = !d_ids && !small && L->fast_router;
+    /* caller-routed decode without a fork: the token codes ride in the sort
+     * launch (k_quant_sort_small) */
+    const int qsort = d_ids && !L->prof && T * k <= 1024 && E <= 4096 &&
+                      !(S > 0 && T > 16);
     prof_mark(L, slot, ST_QUANT_X, s);
-    if (small) /* the codes Xq and all T x E logits (timed as quant_x) */
+    if (qsort) {
+        /* quantised with the sort below */
+    } else if (small) /* the codes Xq and all T x E logits (timed as quant_x) */
         le |= jtk_router_logits_small(dX, L->Wgate, T, E, n, L->logits, L->Xq, L->sx, err, s);
     else if (fast) /* the expert codes Xq plus the router's residual codes */
         le |= jtk_router_codes(dX, T, n, L->Xq, L->Xl, L->sx, L->xinfo, err, s);
@@ -792,6 +798,9 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
     prof_mark(L, slot, ST_SORT, s);
     if (merge16) {
         /* sorted in the top-k launch */
+    } else if (qsort) {
+        le |= jtk_quant_sort_small(dX, T, n, L->Xq, L->sx, ids, Tk, E, (int64_t)Tk, R, L->off,
+                                   NULL, L->perm, NULL, NULL, L->tiles, L->ntiles, err, s);
     } else if (Tk <= 1024 && E <= 4096) {
         le |= jtk_sort_small(ids, Tk, E, (int64_t)Tk, R, L->off, NULL, L->perm, NULL, NULL,
                              L->tiles, L->ntiles, err, s);
@@ -825,7 +834,7 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
             le |= jtk_routed_ffn16(L->Xq, L->sx, L->perm, L->tiles, L->ntiles, max_tiles, k,
                                    L->gu_P, L->gu_S, L->gu_pstride, L->gu_sstride, L->dn_P,
                                    L->dn_S, L->dn_pstride, L->dn_sstride, n, h, L->Ye, L->Sqr,
-                                   L->ssr, err, s);
+                                   L->ssr, L->Sr, err, s);
         prof_mark(L, slot, ST_R_QUANT, s);
         prof_mark(L, slot, ST_R_DOWN, s);
     } else {

@@ -275,114 +275,6 @@ __global__ __launch_bounds__(64 * SK_WAVES) void k_w8a8_skinny(
                                    N, Kp, K, C, ldc, err, bt);
 }
 
-// ===================== few-row GEMM (16 < M <= 64) =====================
-// The skinny layout for up to four 16-row MFMA tiles: one block of 8 waves
-// per NP panels (16 or 32 channels), the waves splitting K as in the
-// skinny kernel, each weight fragment feeding the four row tiles. A GEMM
-// of 64 rows then runs on N/16 blocks instead of the N/128 of 128-row
-// tiles (64 x 1024 x 1024: 64 blocks instead of 8). The 8 waves' int32
-// partial tiles are summed through LDS one row tile at a time (exact).
-#define R64_WAVES 8
-template <int EPI, int NP>
-__global__ __launch_bounds__(64 * R64_WAVES) void k_w8a8_rows64(
-    const int8_t *__restrict__ A, int lda, const float *__restrict__ sA,
-    const int8_t *__restrict__ Wp, const float *__restrict__ sB, int M, int N, int Kp,
-    float *__restrict__ C, int ldc, uint32_t *err) {
-    __shared__ v4i red[R64_WAVES][NP][64];
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int KB = Kp / 64;
-    const int p0 = blockIdx.x * NP;
-    const int row = lane & 15, kc = lane >> 4;
-    const int8_t *arow[4];
-#pragma unroll
-    for (int t = 0; t < 4; t++) arow[t] = A + (int64_t)min(16 * t + row, M - 1) * lda + kc * 16;
-    v4i acc[4][NP];
-#pragma unroll
-    for (int t = 0; t < 4; t++)
-#pragma unroll
-        for (int q = 0; q < NP; q++) acc[t][q] = (v4i){0, 0, 0, 0};
-    for (int kb0 = wave; kb0 < KB; kb0 += 2 * R64_WAVES) {
-        v4i a[2][4], b[2][NP];
-#pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const int kb = kb0 + u * R64_WAVES;
-            if (kb < KB) {  // wave-uniform: a scalar branch
-#pragma unroll
-                for (int q = 0; q < NP; q++)
-                    b[u][q] = *(const v4i *)(Wp + ((int64_t)(p0 + q) * KB + kb) * 1024 + lane * 16);
-#pragma unroll
-                for (int t = 0; t < 4; t++) a[u][t] = *(const v4i *)(arow[t] + kb * 64);
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const int kb = kb0 + u * R64_WAVES;
-            if (kb < KB) {
-#pragma unroll
-                for (int t = 0; t < 4; t++)
-#pragma unroll
-                    for (int q = 0; q < NP; q++) acc[t][q] = mfma16x16x64(a[u][t], b[u][q], acc[t][q]);
-            }
-        }
-    }
-    // rows past M hold products of the clamped row M-1 and are not stored
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-#pragma unroll
-        for (int q = 0; q < NP; q++) red[wave][q][lane] = acc[t][q];
-        __syncthreads();
-        if (wave == 0) {
-#pragma unroll
-            for (int q = 0; q < NP; q++) {
-                v4i sum = red[0][q][lane];
-#pragma unroll
-                for (int w = 1; w < R64_WAVES; w++) sum += red[w][q][lane];
-                acc[t][q] = sum;
-            }
-        }
-        __syncthreads();
-    }
-    if (wave != 0) return;
-    const int lr = (lane >> 4) * 4, lc = lane & 15;
-    // all scale loads before the first store (one vmcnt for both)
-    double sa[4][4], sb[NP];
-#pragma unroll
-    for (int t = 0; t < 4; t++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) sa[t][r] = (double)sA[min(16 * t + lr + r, M - 1)];
-#pragma unroll
-    for (int q = 0; q < NP; q++) sb[q] = (double)sB[min((p0 + q) * 16 + lc, N - 1)];
-    uint32_t bad = 0, badmid = 0;
-#pragma unroll
-    for (int t = 0; t < 4; t++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int m = 16 * t + lr + r;
-            if (m >= M) continue;
-            if (EPI == EPI_PLAIN) {
-#pragma unroll
-                for (int q = 0; q < NP; q++) {
-                    const int col = (p0 + q) * 16 + lc;
-                    const float f = (float)((double)acc[t][q][r] * (sa[t][r] * sb[q]));
-                    if (col < N) {
-                        bad |= !isfinite(f);
-                        C[(int64_t)m * ldc + col] = f;
-                    }
-                }
-            } else if ((p0 + 1) * 16 + lc < N) {  // panel p0 = gate block, p0+1 its up block
-                const float g = (float)((double)acc[t][0][r] * (sa[t][r] * sb[0]));
-                const float u = (float)((double)acc[t][NP - 1][r] * (sa[t][r] * sb[NP - 1]));
-                bad |= (!isfinite(g)) || (!isfinite(u));
-                float sv;
-                badmid |= !silu_mul(g, u, &sv);
-                C[(int64_t)m * ldc + blockIdx.x * 16 + lc] = sv;
-            }
-        }
-    if (bad) raise_err(err, EF_RANGE);
-    if (badmid) raise_err(err, EF_NONFINITE_MID);
-}
-
 template <int QV>
 static hipError_t launch_skinny_xq(const float *X, int ldx, int K, const int8_t *Wp,
                                    const float *sB, int M, int N, int Np, int Kp, float *C,
@@ -1487,46 +1379,73 @@ __device__ __forceinline__ void routed_ffn16_block(
     const uint8_t *dp = dnP + (int64_t)e * dn_pstride;
     const uint8_t *gsb = (const uint8_t *)(guS + (int64_t)e * gu_sstride);
     const uint8_t *dsb = (const uint8_t *)(dnS + (int64_t)e * dn_sstride);
-    // Requests in the order their inputs are known: the scales and raw
-    // panels need only the expert, the A rows need the permutation (scalar
-    // loads, one more round trip). Loads complete in issue order, so the
-    // weights are in by the time the A rows are.
-    for (int c = wave; c < GUS_B / 1024; c += RF_WAVES)
-        dma<16>(gsb + c * 1024 + lane * 16, (char *)gus + c * 1024);
-    for (int c = wave; c < DNS_B / 1024; c += RF_WAVES)
-        dma<16>(dsb + c * 1024 + lane * 16, (char *)dns + c * 1024);
+    // Requests in an order that lets the gate/up start while the rest of
+    // the weights stream in (a wave's vector loads complete in issue order):
+    //   1. the wave's share of the fp16 scales,
+    //   2. the raw gate/up panels of the first GA 64-K groups,
+    //   3. the wave's A row (it needs the permutation, a scalar load issued
+    //      first, whose wait the group loads above cover),
+    //   4. the raw gate/up panels of the other groups, one group at a time,
+    //   5. the raw down panels.
+    // Everything lands in registers; the scales and the A row go on to LDS
+    // once they are in, and after a barrier the gate/up of groups < GA runs
+    // while steps 4-5 are still in flight; group g >= GA waits only for its
+    // own loads. (Plain register loads, not LDS-DMA: the compiler keeps an
+    // exact count of those and waits for just the load a value needs.)
+    // Compiler barriers keep the loads of each step in their place.
+    constexpr int GA = G1 / 2;
+    static_assert(16 / RF_WAVES == 1, "one A row per wave");
+    static_assert(GUS_B / 1024 <= RF_WAVES && DNS_B / 1024 <= RF_WAVES, "one 1 KiB copy per wave");
+    const int arow = wave;
+    const int pv = perm[pos0 + min(arow, nrows - 1)];  // scalar load, waited for at step 3
+    const bool has_gs = wave < GUS_B / 1024, has_ds = wave < DNS_B / 1024;  // wave-uniform
+    uint4 gs4 = {0, 0, 0, 0}, ds4 = {0, 0, 0, 0};
+    if (has_gs) gs4 = *(const uint4 *)(gsb + wave * 1024 + lane * 16);
+    if (has_ds) ds4 = *(const uint4 *)(dsb + wave * 1024 + lane * 16);
     // raw weights into registers (wave-uniform bases and constant offsets:
     // one address register for all)
     const uint8_t *gw = gp + (int64_t)(2 * HB * wave) * G1 * 256;
     const uint8_t *dw = dp + (int64_t)(DPW * wave) * 4 * 512;
     uint32_t rg[HB][G1], ru[HB][G1];
 #pragma unroll
-    for (int j = 0; j < HB; j++)
+    for (int g = 0; g < GA; g++)
 #pragma unroll
-        for (int g = 0; g < G1; g++) {
+        for (int j = 0; j < HB; j++) {
             rg[j][g] = *(const uint32_t *)(gw + ((2 * j) * G1 + g) * 256 + lane * 4);
             ru[j][g] = *(const uint32_t *)(gw + ((2 * j + 1) * G1 + g) * 256 + lane * 4);
         }
+    asm volatile("" ::: "memory");
+    const int src = pv / topk;
+    uint4 a4 = {0, 0, 0, 0};
+    if (lane < N / 16) a4 = *(const uint4 *)(Xq + (int64_t)src * N + lane * 16);
+    const float sxv = sx[src];
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int g = GA; g < G1; g++) {
+#pragma unroll
+        for (int j = 0; j < HB; j++) {
+            rg[j][g] = *(const uint32_t *)(gw + ((2 * j) * G1 + g) * 256 + lane * 4);
+            ru[j][g] = *(const uint32_t *)(gw + ((2 * j + 1) * G1 + g) * 256 + lane * 4);
+        }
+        asm volatile("" ::: "memory");
+    }
     uint2 rd[DPW][4];
 #pragma unroll
     for (int q = 0; q < DPW; q++)
 #pragma unroll
         for (int g = 0; g < 4; g++)
             rd[q][g] = *(const uint2 *)(dw + (q * 4 + g) * 512 + lane * 8);
-    // row `wave` of A, with its token scale and Ye row
-#pragma unroll
-    for (int j = 0; j < 16 / RF_WAVES; j++) {
-        const int row = wave + RF_WAVES * j;
-        const int pv = perm[pos0 + min(row, nrows - 1)];
-        const int src = pv / topk;
-        if (lane < N / 16) dma<16>(Xq + (int64_t)src * N + lane * 16, As + row * ASTR);
-        if (lane == 0) {
-            rsa[row] = sx[src];
-            rdst[row] = pv;
-        }
+    asm volatile("" ::: "memory");
+    // steps 1 and 3 to LDS (each store waits only for its own load), then
+    // every wave's
+    if (has_gs) *(uint4 *)((char *)gus + wave * 1024 + lane * 16) = gs4;
+    if (has_ds) *(uint4 *)((char *)dns + wave * 1024 + lane * 16) = ds4;
+    if (lane < N / 16) *(uint4 *)(As + arow * ASTR + lane * 16) = a4;
+    if (lane == 0) {
+        rsa[arow] = sxv;
+        rdst[arow] = pv;
     }
-    wait_vm<0>();   // this wave's copies have landed
-    lds_barrier();  // ... and every other wave's
+    lds_barrier();
     // ---- gate/up: rows 4*(lane/16)+i, h channel 16*(HB*wave+j) + lane%16 ----
     const int r = lane & 15, kc = lane >> 4, lc = lane & 15, lr = (lane >> 4) * 4;
     float Tg[HB][4], Tu[HB][4];
@@ -1534,8 +1453,8 @@ __device__ __forceinline__ void routed_ffn16_block(
     for (int j = 0; j < HB; j++)
 #pragma unroll
         for (int i = 0; i < 4; i++) Tg[j][i] = Tu[j][i] = 0.f;
-    // one group at a time, the next A fragment read one group ahead
-    // the next group's A fragment and scales are read one group ahead
+    // one group at a time; the next group's A fragment and scales are read
+    // one group ahead
     v4i an = *(const v4i *)(As + r * ASTR + kc * 16);
     uint16_t sgn[HB], sun[HB];
 #pragma unroll
@@ -1545,6 +1464,12 @@ __device__ __forceinline__ void routed_ffn16_block(
     }
 #pragma unroll
     for (int g = 0; g < G1; g++) {
+        // group g's raw panels, pinned here: the compiler then waits for
+        // exactly their loads at this point (later groups' and the down
+        // panels' loads stay in flight), and the scheduler cannot hoist
+        // their unpacking above the last loads
+#pragma unroll
+        for (int j = 0; j < HB; j++) asm volatile("" : "+v"(rg[j][g]), "+v"(ru[j][g])::"memory");
         const v4i a = an;
         if (g + 1 < G1) an = *(const v4i *)(As + r * ASTR + (g + 1) * 64 + kc * 16);
 #pragma unroll
@@ -1619,6 +1544,11 @@ __device__ __forceinline__ void routed_ffn16_block(
         }
     }
     lds_barrier();
+    // the down panels, pinned after the SwiGLU (see the gate/up)
+#pragma unroll
+    for (int q = 0; q < DPW; q++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) asm volatile("" : "+v"(rd[q][g].x), "+v"(rd[q][g].y)::"memory");
     // ---- down: rows 4*(lane/16)+i, channel 16*(DPW*wave+q) + lane%16 ----
     float Td[DPW][4];
 #pragma unroll
@@ -1725,16 +1655,259 @@ static hipError_t launch_lowbit_res(dim3 grid, int cpb, hipStream_t s, const int
     return hipGetLastError();
 }
 
+// ============ routed FFN of 16-row tiles over 4 CUs, two launches ============
+// A decode tile (one expert, <= 16 sorted rows, f = 256) is VALU-bound on one
+// CU: unpacking its INT2/INT4 panels and folding the 64-K groups of 16-row
+// MFMA tiles take about 1600 VALU instructions per wave in the one-block
+// form above, with the tile's few real rows using a sixteenth of each MFMA.
+// Here every tile runs on four blocks in each of two launches, so four CUs
+// share that work:
+//   k_routed_gu16: block (tile, quarter) = 4 waves; wave w takes h-block
+//     hb = 4 quarter + w (gate panel 2 hb, up panel 2 hb + 1), folds every
+//     64-K group in order and applies the SwiGLU to its own elements, and
+//     writes the fp32 hidden values to S [sorted row][256];
+//   k_routed_dn16: block (tile, quarter) = 16 waves; wave w quantises hidden
+//     row w (k_quant_rows's scale and codes) into LDS, then takes down
+//     panel N/64 quarter + w (waves past N/64 only quantise).
+// The arithmetic is that of routed_ffn16_block element for element (the
+// same folds, SwiGLU and codes), so Ye, the codes and the scales are
+// identical; the fp32 hidden rows pass through memory unchanged.
+#define RA_WAVES 8  // 4 h-blocks per block, a gate and an up wave for each
+
+template <int G1>
+__global__ __launch_bounds__(64 * RA_WAVES) void k_routed_gu16(
+    const int8_t *__restrict__ Xq, const float *__restrict__ sx,
+    const int32_t *__restrict__ perm, const int4 *__restrict__ tiles,
+    const int32_t *__restrict__ ntiles, int topk, const uint8_t *__restrict__ guP,
+    const uint16_t *__restrict__ guS, int64_t gu_pstride, int64_t gu_sstride,
+    float *__restrict__ S, uint32_t *err) {
+    constexpr int N = 64 * G1;
+    constexpr int ASTR = N + 16;
+    constexpr int HQ = RF_H / 4;  // hidden channels per quarter (4 h-blocks)
+    constexpr int VSTR = HQ + 4;  // LDS row stride of the scaled gate/up values (floats)
+    static_assert(N % 256 == 0 && N <= 1024, "n = 256, 512, 768 or 1024");
+    static_assert(RA_WAVES == 2 * (RF_H / 16) / 4, "a wave per gate or up panel of a quarter");
+    __shared__ __attribute__((aligned(16))) int8_t As[16 * ASTR];
+    __shared__ __attribute__((aligned(16))) uint16_t gus[RA_WAVES][G1 * 16];
+    __shared__ __attribute__((aligned(16))) float gb[16 * VSTR];
+    __shared__ __attribute__((aligned(16))) float ub[16 * VSTR];
+    __shared__ float rsa[16];
+    __shared__ double exp_tab[64];
+    const int tile = blockIdx.x >> 2, quarter = blockIdx.x & 3;
+    const int4 td = tiles[tile];  // {expert, first sorted row, rows}; the grid stays in bounds
+    if (tile >= *ntiles) return;
+    const int lane = threadIdx.x & 63;
+    const double tabv = exp_tab_load(lane);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int e = td.x, pos0 = td.y, nrows = td.z;
+    if (nrows <= 0) return;
+    const int hl = wave >> 1;             // h-block within the quarter
+    const int hb = 4 * quarter + hl;      // h-block within the expert
+    const int pan = 2 * hb + (wave & 1);  // gate panel (even wave) or up panel (odd wave)
+    // the wave's two A rows (scalar loads of the permutation first)
+    int src[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) src[j] = perm[pos0 + min(2 * wave + j, nrows - 1)] / topk;
+    // 1. the panel's fp16 scales (G1 * 32 bytes)
+    const uint8_t *gsb =
+        (const uint8_t *)(guS + (int64_t)e * gu_sstride + (int64_t)pan * G1 * 16);
+    constexpr int SC16 = G1 * 32 / 16;  // 16-byte pieces
+    uint4 gs4 = {0, 0, 0, 0};
+    if (lane < SC16) gs4 = *(const uint4 *)(gsb + lane * 16);
+    // 2. raw panel groups, first half
+    const uint8_t *gw = guP + (int64_t)e * gu_pstride + (int64_t)pan * G1 * 256;
+    constexpr int GA = G1 / 2;
+    uint32_t rw[G1];
+#pragma unroll
+    for (int g = 0; g < GA; g++) rw[g] = *(const uint32_t *)(gw + g * 256 + lane * 4);
+    asm volatile("" ::: "memory");
+    // 3. the A rows and their token scales
+    uint4 a4[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        a4[j] = (uint4){0, 0, 0, 0};
+        if (lane < N / 16) a4[j] = *(const uint4 *)(Xq + (int64_t)src[j] * N + lane * 16);
+    }
+    float sxv = 0.0f;
+    if (lane == 0) sxv = sx[src[0]];
+    if (lane == 1) sxv = sx[src[1]];
+    asm volatile("" ::: "memory");
+    // 4. the other groups
+#pragma unroll
+    for (int g = GA; g < G1; g++) {
+        rw[g] = *(const uint32_t *)(gw + g * 256 + lane * 4);
+        asm volatile("" ::: "memory");
+    }
+    if (lane < SC16) *(uint4 *)((char *)gus[wave] + lane * 16) = gs4;
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+        if (lane < N / 16) *(uint4 *)(As + (2 * wave + j) * ASTR + lane * 16) = a4[j];
+    if (lane < 2) rsa[2 * wave + lane] = sxv;
+    lds_barrier();
+    // ---- the panel: rows 4*(lane/16)+i, channel 16*pan + lane%16 ----
+    const int r = lane & 15, kc = lane >> 4, lc = lane & 15, lr = (lane >> 4) * 4;
+    float T[4] = {0.f, 0.f, 0.f, 0.f};
+    v4i an = *(const v4i *)(As + r * ASTR + kc * 16);
+#pragma unroll
+    for (int g = 0; g < G1; g++) {
+        // group g's raw panel, pinned here (see routed_ffn16_block)
+        asm volatile("" : "+v"(rw[g])::"memory");
+        const v4i a = an;
+        if (g + 1 < G1) an = *(const v4i *)(As + r * ASTR + (g + 1) * 64 + kc * 16);
+        const float sc = f16_to_f32(gus[wave][g * 16 + lc]);
+        const v4i c = mfma16x16x64(a, unpack_int2(rw[g]), (v4i){0, 0, 0, 0});
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            T[i] = __builtin_fmaf((float)c[i], sc, T[i]);
+            asm volatile("" : "+v"(T[i]));
+        }
+    }
+    // the scaled gate (even wave) or up (odd wave) values to LDS
+    uint32_t flags = 0;
+    float *vb = (wave & 1) ? ub : gb;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int row = lr + i;
+        const float v = T[i] * rsa[row < nrows ? row : 0];
+        if (row < nrows && !isfinite(v)) flags |= EF_RANGE;
+        vb[row * VSTR + 16 * hl + lc] = v;
+    }
+    exp_tab_stage(exp_tab, lane, tabv);
+    lds_barrier();
+    // ---- SwiGLU: 16 rows x HQ hidden over the block, fp32 hidden to S ----
+#pragma unroll
+    for (int u = 0; u < 16 * HQ / (64 * RA_WAVES); u++) {
+        const int x = (wave + RA_WAVES * u) * 64 + lane;  // element of the 16 x HQ tile
+        const int row = x / HQ, hc = x % HQ;
+        if (row >= nrows) continue;
+        float sv;
+        if (!silu_mul(gb[row * VSTR + hc], ub[row * VSTR + hc], &sv, exp_tab))
+            flags |= EF_NONFINITE_MID;
+        S[(int64_t)(pos0 + row) * RF_H + HQ * quarter + hc] = sv;
+    }
+    if (flags) raise_err(err, flags);
+}
+
+template <int G1>
+__global__ __launch_bounds__(64 * RF_WAVES) void k_routed_dn16(
+    const int32_t *__restrict__ perm, const int4 *__restrict__ tiles,
+    const int32_t *__restrict__ ntiles, const float *__restrict__ S,
+    const uint8_t *__restrict__ dnP, const uint16_t *__restrict__ dnS, int64_t dn_pstride,
+    int64_t dn_sstride, float *__restrict__ Ye, int8_t *__restrict__ Hq,
+    float *__restrict__ Hs, uint32_t *err) {
+    constexpr int N = 64 * G1;
+    constexpr int PQ = N / 64;  // down panels per quarter (one per wave)
+    static_assert(PQ <= RF_WAVES, "one panel per wave");
+    __shared__ __attribute__((aligned(16))) int8_t hq[16 * RF_QSTR];
+    __shared__ float rsq[16];
+    __shared__ int rdst[16];
+    const int tile = blockIdx.x >> 2, quarter = blockIdx.x & 3;
+    const int4 td = tiles[tile];  // the grid stays in bounds
+    if (tile >= *ntiles) return;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int e = td.x, pos0 = td.y, nrows = td.z;
+    if (nrows <= 0) return;
+    const int p = PQ * quarter + wave;  // this wave's down panel (wave < PQ)
+    const bool has_p = wave < PQ;      // wave-uniform
+    // the hidden row first (its quantiser runs before the down), then the
+    // panel's raw INT4 groups and scales
+    const int row = wave;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (row < nrows) v = *(const float4 *)(S + (int64_t)(pos0 + row) * RF_H + lane * 4);
+    if (row < nrows && lane == 0) rdst[row] = perm[pos0 + row];
+    uint2 rd[4];
+    uint16_t dsc[4];
+    const uint8_t *dw = dnP + (int64_t)e * dn_pstride + (int64_t)p * 4 * 512;
+    const uint16_t *dsw = dnS + (int64_t)e * dn_sstride + (int64_t)p * 4 * 16;
+    if (has_p) {
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            rd[g] = *(const uint2 *)(dw + g * 512 + lane * 8);
+            dsc[g] = dsw[g * 16 + (lane & 15)];
+        }
+    }
+    // ---- row `wave`: k_quant_rows's scale and codes, into LDS ----
+    uint32_t flags = 0;
+    if (row < nrows) {
+        uint32_t mu = max(max(abs_bits(v.x), abs_bits(v.y)), max(abs_bits(v.z), abs_bits(v.w)));
+        mu = wave_max_u(mu);
+        const QuantParams qp = quant_params(__builtin_bit_cast(float, mu));
+        if (mu >= 0x7f800000u) {
+            flags |= EF_NONFINITE_INPUT;
+        } else if (!qp.ok) {
+            flags |= EF_RANGE;
+        } else {
+            const float inv = quant_inv_f(qp.scale_d);
+            const uint32_t b0 = (uint8_t)quant_code_fast(v.x, qp.scale_d, inv);
+            const uint32_t b1 = (uint8_t)quant_code_fast(v.y, qp.scale_d, inv);
+            const uint32_t b2 = (uint8_t)quant_code_fast(v.z, qp.scale_d, inv);
+            const uint32_t b3 = (uint8_t)quant_code_fast(v.w, qp.scale_d, inv);
+            const uint32_t wd = b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+            *(uint32_t *)(hq + row * RF_QSTR + lane * 4) = wd;
+            if (quarter == 0) {  // one copy of the codes and scale in memory
+                *(uint32_t *)(Hq + (int64_t)(pos0 + row) * RF_H + lane * 4) = wd;
+                if (lane == 0) Hs[pos0 + row] = qp.scale_f;
+            }
+            if (lane == 0) rsq[row] = qp.scale_f;
+        }
+    }
+    lds_barrier();
+    if (has_p) {
+        // ---- down: rows 4*(lane/16)+i, channel 16 p + lane%16 ----
+        const int r = lane & 15, kc = lane >> 4, lc = lane & 15, lr = (lane >> 4) * 4;
+        float Td[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int g = 0; g < RF_H / 64; g++) {
+            const v4i a = *(const v4i *)(hq + r * RF_QSTR + g * 64 + kc * 16);
+            const v4i c = mfma16x16x64(a, unpack_int4(rd[g].x, rd[g].y), (v4i){0, 0, 0, 0});
+            const float sd = f16_to_f32(dsc[g]);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                Td[i] = __builtin_fmaf((float)c[i], sd, Td[i]);
+                asm volatile("" : "+v"(Td[i]));
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int rr = lr + i;
+            if (rr >= nrows) continue;
+            const float f = Td[i] * rsq[rr];
+            if (!isfinite(f)) flags |= EF_RANGE;
+            Ye[(int64_t)rdst[rr] * N + 16 * p + lc] = f;
+        }
+    }
+    if (flags) raise_err(err, flags);
+}
+
 extern "C" int jtk_routed_ffn16(const int8_t *Xq, const float *sx, const int32_t *perm,
                                 const int32_t *tiles, const int32_t *ntiles, int max_tiles,
                                 int topk, const uint8_t *guP, const uint16_t *guS,
                                 int64_t gu_pstride, int64_t gu_sstride, const uint8_t *dnP,
                                 const uint16_t *dnS, int64_t dn_pstride, int64_t dn_sstride, int n,
-                                int h, float *Ye, int8_t *Hq, float *Hs, uint32_t *err,
+                                int h, float *Ye, int8_t *Hq, float *Hs, float *S, uint32_t *err,
                                 hipStream_t s) {
     if (max_tiles <= 0) return 0;
     if (h != RF_H) return (int)hipErrorInvalidValue;
+    if (max_tiles > (1 << 29)) return (int)hipErrorInvalidValue;
     const int4 *t4 = (const int4 *)tiles;
+    if (S) {  // four CUs per tile, two launches (S: the fp32 hidden rows)
+#define RS_LAUNCH(G)                                                                          \
+    hipLaunchKernelGGL(k_routed_gu16<G>, dim3((unsigned)(4 * max_tiles)), dim3(64 * RA_WAVES), 0, \
+                       s, Xq, sx, perm, t4, ntiles, topk, guP, guS, gu_pstride, gu_sstride, S,  \
+                       err);                                                                   \
+    hipLaunchKernelGGL(k_routed_dn16<G>, dim3((unsigned)(4 * max_tiles)), dim3(64 * RF_WAVES), 0, \
+                       s, perm, t4, ntiles, S, dnP, dnS, dn_pstride, dn_sstride, Ye, Hq, Hs, err)
+        switch (n) {
+        case 256: RS_LAUNCH(4); break;
+        case 512: RS_LAUNCH(8); break;
+        case 768: RS_LAUNCH(12); break;
+        case 1024: RS_LAUNCH(16); break;
+        default: return (int)hipErrorInvalidValue;
+        }
+#undef RS_LAUNCH
+        return (int)hipGetLastError();
+    }
 #define RF_LAUNCH(G)                                                                            \
     hipLaunchKernelGGL(k_routed_ffn16<G>, dim3((unsigned)max_tiles), dim3(64 * RF_WAVES), 0, s, Xq, sx, \
                        perm, t4, ntiles, topk, guP, guS, gu_pstride, gu_sstride, dnP, dnS,      \

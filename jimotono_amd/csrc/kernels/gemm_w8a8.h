@@ -38,6 +38,11 @@ __device__ __forceinline__ void dma<4>(const void *g, void *lds_base) {
     __builtin_amdgcn_global_load_lds(g, (lds_void *)lds_base, 4, 0, 0);
 }
 
+// The 32-bit LDS address of a __shared__ pointer.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
 // Wait until at most N vector-memory operations of this wave are in flight.
 template <int N>
 __device__ __forceinline__ void wait_vm() {

@@ -110,14 +110,16 @@ int jtk_lowbit_grouped(int bits, const int8_t *A, int lda, const float *sA,
                        int64_t wp_stride, int64_t ws_stride, int N, int K, float *out, int ldo,
                        uint32_t *err, hipStream_t s);
 
-/* the routed FFN of 16-row tiles in one launch (h = 256, n = 256..1024 in
- * steps of 256); hipErrorInvalidValue for other shapes */
+/* the routed FFN of 16-row tiles (h = 256, n = 256..1024 in steps of 256;
+ * hipErrorInvalidValue for other shapes): with S == NULL one block per tile
+ * in one launch; with S (fp32 hidden rows, [sorted row][256]) four blocks per
+ * tile in each of two launches (same results) */
 int jtk_routed_ffn16(const int8_t *Xq, const float *sx, const int32_t *perm,
                      const int32_t *tiles, const int32_t *ntiles, int max_tiles, int topk,
                      const uint8_t *guP, const uint16_t *guS, int64_t gu_pstride,
                      int64_t gu_sstride, const uint8_t *dnP, const uint16_t *dnS,
                      int64_t dn_pstride, int64_t dn_sstride, int n, int h, float *Ye,
-                     int8_t *Hq, float *Hs, uint32_t *err, hipStream_t s);
+                     int8_t *Hq, float *Hs, float *S, uint32_t *err, hipStream_t s);
 /* decode launches that carry the shared experts' blocks: top-k of T <= 16
  * rows (E <= 1024, k <= 64) and the pair sort / tile list (as
  * jtk_sort_small with cap = T*k; `done` is a zeroed device word the launch
@@ -177,6 +179,12 @@ int jtk_make_tiles(const int32_t *off, int E, int R, int32_t *tiles, int32_t *nt
 int jtk_sort_small(const int32_t *ids, int Tk, int E, int64_t cap, int R, int32_t *off,
                    int64_t *off64, int32_t *perm, int64_t *perm64, uint8_t *drop,
                    int32_t *tiles, int32_t *ntiles, uint32_t *err, hipStream_t s);
+/* the T token rows' codes (k_quant_rows) and k_sort_small's sort of the
+ * caller's ids in one launch (Tk <= 1024, E <= SORT_EMAX) */
+int jtk_quant_sort_small(const float *X, int T, int n, int8_t *Xq, float *sx,
+                         const int32_t *ids, int Tk, int E, int64_t cap, int R, int32_t *off,
+                         int64_t *off64, int32_t *perm, int64_t *perm64, uint8_t *drop,
+                         int32_t *tiles, int32_t *ntiles, uint32_t *err, hipStream_t s);
 int jtk_sort_mid(const int32_t *ids, int Tk, int E, int64_t cap, int R, int32_t *rank,
                  int32_t *cnt, int32_t *off, int64_t *off64, int32_t *perm, int64_t *perm64,
                  uint8_t *drop, int32_t *tiles, int32_t *ntiles, uint32_t *err, hipStream_t s);

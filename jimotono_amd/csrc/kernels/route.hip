@@ -17,6 +17,7 @@
 #include "jt_launch.h"
 #include "topk_dev.h"
 #include "sort_dev.h"
+#include "quant_dev.h"
 
 // ---------------- router logits ----------------
 // Block: 64 tokens x 64 experts, 256 threads in 4 groups of 64; group p
@@ -587,6 +588,51 @@ extern "C" int jtk_sort_small(const int32_t *ids, int Tk, int E, int64_t cap, in
     if (Tk > SORT_SMALL || E > SORT_EMAX) return (int)hipErrorInvalidValue;
     hipLaunchKernelGGL(k_sort_small, dim3(1), dim3(1024), 0, s, ids, Tk, E, cap, R, off, off64,
                        perm, perm64, drop, tiles, ntiles, err);
+    return (int)hipGetLastError();
+}
+
+// ------- caller-routed decode: token codes and the pair sort, one launch -------
+// Blocks 0 .. gridDim.x-2 quantise the T token rows (16 per block, one
+// wavefront per row, k_quant_rows's codes); the last block sorts the pairs
+// as k_sort_small does. The two only share the launch: the sort reads the
+// caller's ids, not the codes.
+__global__ __launch_bounds__(1024) void k_quant_sort_small(
+    const float *__restrict__ X, int T, int n, int8_t *__restrict__ Xq, float *__restrict__ sx,
+    const int32_t *__restrict__ ids, int Tk, int E, int64_t cap, int R,
+    int32_t *__restrict__ off, int64_t *__restrict__ off64, int32_t *__restrict__ perm,
+    int64_t *__restrict__ perm64, uint8_t *__restrict__ drop, int32_t *__restrict__ tiles,
+    int32_t *__restrict__ ntiles, uint32_t *err) {
+    __shared__ __attribute__((aligned(16))) SortLds sm;
+    if (blockIdx.x + 1 < gridDim.x) {
+        const int64_t r = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 6);
+        if (r < T) quant_row_wave(X, r, n, Xq, n, sx, err, threadIdx.x & 63);
+        return;
+    }
+    const int t = threadIdx.x;
+    int e = -1;
+    if (t < Tk) {
+        e = ids[t];
+        if (e < 0 || e >= E) {
+            raise_err(err, EF_BAD_ID);
+            e = -1;
+        }
+    }
+    if (Tk <= SORTF_TK && E <= SORTF_E)  // block-uniform
+        sort_small_fast(e, Tk, E, cap, R, off, off64, perm, perm64, drop, tiles, ntiles, sm.fast);
+    else
+        sort_small_core(e, Tk, E, cap, R, off, off64, perm, perm64, drop, tiles, ntiles, sm.small);
+}
+
+extern "C" int jtk_quant_sort_small(const float *X, int T, int n, int8_t *Xq, float *sx,
+                                    const int32_t *ids, int Tk, int E, int64_t cap, int R,
+                                    int32_t *off, int64_t *off64, int32_t *perm,
+                                    int64_t *perm64, uint8_t *drop, int32_t *tiles,
+                                    int32_t *ntiles, uint32_t *err, hipStream_t s) {
+    if (T <= 0 || n <= 0 || Tk > SORT_SMALL || E > SORT_EMAX || T > (1 << 24))
+        return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_quant_sort_small, dim3((unsigned)((T + 15) / 16 + 1)), dim3(1024), 0,
+                       s, X, T, n, Xq, sx, ids, Tk, E, cap, R, off, off64, perm, perm64, drop,
+                       tiles, ntiles, err);
     return (int)hipGetLastError();
 }
 

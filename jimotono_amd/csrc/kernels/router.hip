@@ -454,9 +454,6 @@ __global__ __launch_bounds__(64 * RV_WPB) void k_router_select(
 #define RX_STAGE_B (64 * RX_SL * 16 + 1024)  // 64 gate rows + the 4 token rows
 
 typedef float f4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ uint32_t lds_addr(const void *p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
-}
 
 // One stage of a wavefront: for each lane's gate row (64 rows, padded to 9
 // slots so that lanes reading their own rows hit distinct banks) and the
