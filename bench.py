@@ -573,10 +573,14 @@ def w8a8_64_bench(np, torch, api, stream):
     sA = torch.rand(M, generator=g, device="cuda") * 9e-3 + 1e-3
     Cc = torch.empty(M, N, device="cuda")
     _, ev = time_fn(torch, lambda: Wq.gemm(Aq, sA, Cc, stream), 200, 20, stream)
+    nbytes = M * K + N * K + 4 * (M + N) + 4 * M * N
     res["w8a8_gemm_64x1024x1024"] = {"us_per_call": ev * 1e3,
                                      "tops": 2 * M * N * K / (ev / 1e3) / 1e12,
-                                     "gbps": (M * K + N * K + 4 * (M + N) + 4 * M * N)
-                                     / (ev / 1e3) / 1e9}
+                                     "mfma_frac": 2 * M * N * K / (ev / 1e3) / INT8_PEAK,
+                                     "bytes": nbytes,
+                                     "gbps": nbytes / (ev / 1e3) / 1e9,
+                                     "hbm_frac": nbytes / (ev / 1e3) / HBM_PEAK,
+                                     "peak_gbps": HBM_PEAK / 1e9}
     del Wq
     return res
 
@@ -605,7 +609,8 @@ def shared_decode_bench(np, torch, api, stream):
         _, ev = time_fn(torch, fstep, 4 * copies, copies, stream)
         res[f"shared_decode_M{m}"] = {"us_per_expert": ev * 1e3,
                                       "gbps": (wbytes + 8 * m * n) / (ev / 1e3) / 1e9,
-                                      "hbm_frac": (wbytes + 8 * m * n) / (ev / 1e3) / HBM_PEAK}
+                                      "hbm_frac": (wbytes + 8 * m * n) / (ev / 1e3) / HBM_PEAK,
+                                      "peak_gbps": HBM_PEAK / 1e9}
     del Fs
     torch.cuda.empty_cache()
     return res
@@ -641,7 +646,8 @@ def routed_decode_bench(np, torch, api, stream):
     res["routed_decode_T16"] = {"us_per_layer": ev * 1e3, "touched_experts": touched,
                                 "weight_bytes": rbytes,
                                 "gbps": rbytes / (ev / 1e3) / 1e9,
-                                "hbm_frac": rbytes / (ev / 1e3) / HBM_PEAK}
+                                "hbm_frac": rbytes / (ev / 1e3) / HBM_PEAK,
+                                "peak_gbps": HBM_PEAK / 1e9}
     del layers
     torch.cuda.empty_cache()
     return res
