@@ -173,6 +173,10 @@ carve:; /* first pass sizes the workspace (base NULL), the second carves it */
     w8.sB1 = aalloc(&a, 16);
     w8.sA = aalloc(&a, Mmax * 4);
     w8.sB = aalloc(&a, (size_t)Npmax * 4);
+    /* the grouped fp32 path's tile list and shared hidden rows */
+    const int max_tiles = (int)(Tk / 16) + E + 1;
+    int32_t *tiles = aalloc(&a, (size_t)max_tiles * 16), *ntiles = aalloc(&a, 16);
+    float *Ssh = S ? aalloc(&a, (size_t)S * T * h * 4) : NULL;
     if (!a.base) {
         a.base = jt_rt_buf(rt, JT_SLOT_LAYER, a.off, &rc);
         if (!a.base) return rc;
@@ -225,15 +229,30 @@ carve:; /* first pass sizes the workspace (base NULL), the second carves it */
         rc = jt_rt_err(hipErrorLaunchFailure);
         goto out;
     }
+    /* Flags off: every expert's fp32 FFN in two grouped launches (routed, then
+     * shared), with the same arithmetic as the per-expert launches below and
+     * no wait for the expert offsets. Quantised modes keep the reference's
+     * per-expert steps (per-call weight quantisation per expert). */
+    const int grouped = !lbmode && !w8a8_on;
     uint32_t f = 0;
-    if ((rc = jt_rt_flags(rt, s, &f)) != JT_OK) goto out;
-    if ((rc = jt_rt_flags_to_rc(f)) != JT_OK) goto out;
-    if ((rc = jt_rt_d2h(rt, hoff, off64, ((size_t)E + 1) * 8)) != JT_OK) goto out;
+    if (!grouped) {
+        if ((rc = jt_rt_flags(rt, s, &f)) != JT_OK) goto out;
+        if ((rc = jt_rt_flags_to_rc(f)) != JT_OK) goto out;
+        if ((rc = jt_rt_d2h(rt, hoff, off64, ((size_t)E + 1) * 8)) != JT_OK) goto out;
+    }
     if (cache_Ysel) le |= (int)hipMemsetAsync(Ysel, 0, Tk * n * 4, s);
     if (Gsel) le |= (int)hipMemsetAsync(Gsel, 0, Tk * h * 4, s);
     if (Usel) le |= (int)hipMemsetAsync(Usel, 0, Tk * h * 4, s);
+    if (grouped) {
+        le |= jtk_make_tiles(off, E, 16, tiles, ntiles, s);
+        le |= jtk_ffn_f32(dX, T, n, h, perm, k, tiles, ntiles, max_tiles, dWg, dWu, dWd, E, Gsel,
+                          Usel, Se, Ysel, 0, err, s);
+        if (S)
+            le |= jtk_ffn_f32(dX, T, n, h, NULL, k, NULL, NULL, 0, dWgs, dWus, dWds, S, Gs, Us,
+                              Ssh, Ys, 1, err, s);
+    }
     /* per-expert forward (src/moe_layer.c:1265-1420) */
-    for (int e = 0; e < E && rc == JT_OK; e++) {
+    for (int e = 0; e < E && rc == JT_OK && !grouped; e++) {
         const int b0 = (int)hoff[e], Me = (int)(hoff[e + 1] - hoff[e]);
         if (Me == 0) continue;
         const float *wg = dWg + e * nh, *wu = dWu + e * nh, *wd = dWd + e * nh;
@@ -280,7 +299,7 @@ carve:; /* first pass sizes the workspace (base NULL), the second carves it */
     }
     if (rc == JT_OK && le) rc = jt_rt_err(hipErrorLaunchFailure);
     /* shared experts (src/moe_layer.c:1468-1560) */
-    for (int sx = 0; sx < S && rc == JT_OK; sx++) {
+    for (int sx = 0; sx < S && rc == JT_OK && !grouped; sx++) {
         const float *wg = dWgs + sx * nh, *wu = dWus + sx * nh, *wd = dWds + sx * nh;
         float *ys = Ys + (size_t)sx * Tn;
         if (w8a8_on) {
@@ -311,6 +330,7 @@ carve:; /* first pass sizes the workspace (base NULL), the second carves it */
     if (rc != JT_OK) goto out;
     if ((rc = jt_rt_flags(rt, s, &f)) != JT_OK) goto out;
     if ((rc = jt_rt_flags_to_rc(f)) != JT_OK) goto out;
+    if (grouped && (rc = jt_rt_d2h(rt, hoff, off64, ((size_t)E + 1) * 8)) != JT_OK) goto out;
     /* commit (fail-closed: nothing above wrote a host output) */
     const size_t kept = (size_t)hoff[E];
     rc = jt_rt_d2h(rt, Y, dY, Tn * 4);

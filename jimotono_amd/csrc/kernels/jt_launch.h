@@ -199,6 +199,15 @@ int jtk_scatter_rows(const float *src, int n, const int32_t *perm, int base, int
                      float *dst, hipStream_t s);
 int jtk_silu_tile(const float *G, const float *U, int64_t n, float *S, uint32_t *err,
                   hipStream_t s);
+/* the drop-in layer's expert FFN in fp32 (flags off) for every expert at
+ * once: routed (dense = 0: the R = 16 tile list over the sorted pairs, Y
+ * scattered to Y[perm[pos]]) or the nexp shared experts (dense = 1: T rows
+ * each, S and Y as [nexp][T][.]); Gc/Uc optional caches ([pair][h] or
+ * [token][nexp][h]) */
+int jtk_ffn_f32(const float *X, int T, int n, int h, const int32_t *perm, int topk,
+                const int32_t *tiles, const int32_t *ntiles, int max_tiles, const float *Wg,
+                const float *Wu, const float *Wd, int nexp, float *Gc, float *Uc, float *Sbuf,
+                float *Y, int dense, uint32_t *err, hipStream_t s);
 int jtk_zero_u32(uint32_t *p, int64_t n, hipStream_t s);
 int jtk_bcast_f32(float *dst, int64_t n, const float *src, hipStream_t s);
 

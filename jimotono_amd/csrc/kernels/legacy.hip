@@ -352,3 +352,131 @@ extern "C" int jtk_preload_legacy(void) {
     hipFuncAttributes a;
     return (int)hipFuncGetAttributes(&a, (const void *)(k_gemm_f32));
 }
+
+// ---- grouped fp32 expert FFN of the drop-in layer (flags off) ----
+// The per-expert sequence gather -> transpose -> k_gemm_f32 (gate, up) ->
+// SwiGLU -> k_gemm_f32 (down) -> scatter of src/moe_layer.c:1265-1420 (and the
+// shared experts of :1468-1560), as two launches over every expert at once:
+// a block computes 16 rows x 16 columns, the rows of one (expert, 16-row)
+// tile of the sorted pairs (or, dense, 16 token rows of shared expert
+// blockIdx.z). Every output is k_gemm_f32's k-ordered fp32 sum (one rounded
+// multiply and one rounded add per step; the transpose is a copy, so reading
+// W[j][k] directly gives the same products), and the SwiGLU is
+// k_silu_tile's, so the results are those of the per-expert launches.
+//   gate/up: G, U [row][h] (optional caches, scattered to the pair's row or
+//            to [token][S][h]), S [row][h] (sorted rows, or [s][T][h]);
+//   down:    Y [pair][n] (routed, scattered by perm) or [s][T][n] (dense).
+__global__ __launch_bounds__(256) void k_ffn_gu_f32(
+    const float *__restrict__ X, int n, int h, const int32_t *__restrict__ perm, int topk,
+    const int4 *__restrict__ tiles, const int32_t *__restrict__ ntiles, int T, int S,
+    const float *__restrict__ Wg, const float *__restrict__ Wu, float *__restrict__ Gc,
+    float *__restrict__ Uc, float *__restrict__ Sout, int dense, uint32_t *err) {
+    __shared__ float as[16][17];
+    __shared__ float bg[16][17];
+    __shared__ float bu[16][17];
+    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+    int e, pos0, nrows;
+    if (dense) {
+        e = blockIdx.z;
+        pos0 = blockIdx.y * 16;
+        nrows = min(16, T - pos0);
+    } else {
+        if ((int)blockIdx.y >= *ntiles) return;
+        const int4 td = tiles[blockIdx.y];  // {expert, first sorted row, rows}
+        e = td.x;
+        pos0 = td.y;
+        nrows = td.z;
+    }
+    const int j0 = blockIdx.x * 16;
+    const int rr = min(ty, nrows - 1);
+    const int q = dense ? pos0 + rr : perm[pos0 + rr];   // token (dense) or pair index
+    const int src = dense ? q : q / topk;                // token row of X
+    const float *xa = X + (int64_t)src * n;
+    const int64_t wo = (int64_t)e * h * n;
+    const int jb = min(j0 + ty, h - 1);  // the weight row this thread stages
+    float ag = 0.0f, au = 0.0f;
+    for (int k0 = 0; k0 < n; k0 += 16) {
+        const int ka = k0 + tx;
+        as[ty][tx] = ka < n ? xa[ka] : 0.0f;
+        bg[ty][tx] = ka < n ? Wg[wo + (int64_t)jb * n + ka] : 0.0f;
+        bu[ty][tx] = ka < n ? Wu[wo + (int64_t)jb * n + ka] : 0.0f;
+        __syncthreads();
+        const int kend = min(16, n - k0);
+        for (int kk = 0; kk < kend; kk++) {
+            ag = __fadd_rn(ag, __fmul_rn(as[ty][kk], bg[tx][kk]));
+            au = __fadd_rn(au, __fmul_rn(as[ty][kk], bu[tx][kk]));
+        }
+        __syncthreads();
+    }
+    const int j = j0 + tx;
+    if (ty >= nrows || j >= h) return;
+    uint32_t f = 0;
+    if (!isfinite(ag) || !isfinite(au)) f |= EF_NONFINITE_MID;
+    float sv;
+    if (!silu_mul(ag, au, &sv)) f |= EF_NONFINITE_MID;
+    const int64_t row = dense ? (int64_t)e * T + pos0 + ty : pos0 + ty;
+    Sout[row * h + j] = sv;
+    const int64_t crow = dense ? ((int64_t)(pos0 + ty) * S + e) : q;
+    if (Gc) Gc[crow * h + j] = ag;
+    if (Uc) Uc[crow * h + j] = au;
+    if (f) raise_err(err, f);
+}
+
+__global__ __launch_bounds__(256) void k_ffn_dn_f32(
+    const float *__restrict__ Sin, int h, int n, const int32_t *__restrict__ perm,
+    const int4 *__restrict__ tiles, const int32_t *__restrict__ ntiles, int T,
+    const float *__restrict__ Wd, float *__restrict__ Y, int dense, uint32_t *err) {
+    __shared__ float as[16][17];
+    __shared__ float bs[16][17];
+    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+    int e, pos0, nrows;
+    if (dense) {
+        e = blockIdx.z;
+        pos0 = blockIdx.y * 16;
+        nrows = min(16, T - pos0);
+    } else {
+        if ((int)blockIdx.y >= *ntiles) return;
+        const int4 td = tiles[blockIdx.y];
+        e = td.x;
+        pos0 = td.y;
+        nrows = td.z;
+    }
+    const int c0 = blockIdx.x * 16;
+    const int rr = min(ty, nrows - 1);
+    const int64_t arow = dense ? (int64_t)e * T + pos0 + rr : pos0 + rr;
+    const float *sa = Sin + arow * h;
+    const float *wd = Wd + (int64_t)e * h * n;
+    const int cb = min(c0 + tx, n - 1);
+    float acc = 0.0f;
+    for (int k0 = 0; k0 < h; k0 += 16) {
+        const int ka = k0 + tx, kb = k0 + ty;
+        as[ty][tx] = ka < h ? sa[ka] : 0.0f;
+        bs[ty][tx] = kb < h ? wd[(int64_t)kb * n + cb] : 0.0f;
+        __syncthreads();
+        const int kend = min(16, h - k0);
+        for (int kk = 0; kk < kend; kk++) acc = __fadd_rn(acc, __fmul_rn(as[ty][kk], bs[kk][tx]));
+        __syncthreads();
+    }
+    const int c = c0 + tx;
+    if (ty >= nrows || c >= n) return;
+    if (!isfinite(acc)) raise_err(err, EF_NONFINITE_MID);
+    const int64_t orow = dense ? (int64_t)e * T + pos0 + ty : perm[pos0 + ty];
+    Y[orow * n + c] = acc;
+}
+
+extern "C" int jtk_ffn_f32(const float *X, int T, int n, int h, const int32_t *perm, int topk,
+                           const int32_t *tiles, const int32_t *ntiles, int max_tiles,
+                           const float *Wg, const float *Wu, const float *Wd, int nexp,
+                           float *Gc, float *Uc, float *Sbuf, float *Y, int dense,
+                           uint32_t *err, hipStream_t s) {
+    if (T <= 0 || n <= 0 || h <= 0 || nexp <= 0) return 0;
+    const unsigned gy = dense ? (unsigned)((T + 15) / 16) : (unsigned)max_tiles;
+    const unsigned gz = dense ? (unsigned)nexp : 1u;
+    if (gy == 0 || gy > 0x7fffffffu || gz > 65535u) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_ffn_gu_f32, dim3((unsigned)((h + 15) / 16), gy, gz), dim3(256), 0, s,
+                       X, n, h, perm, topk, (const int4 *)tiles, ntiles, T, nexp, Wg, Wu, Gc,
+                       Uc, Sbuf, dense, err);
+    hipLaunchKernelGGL(k_ffn_dn_f32, dim3((unsigned)((n + 15) / 16), gy, gz), dim3(256), 0, s,
+                       Sbuf, h, n, perm, (const int4 *)tiles, ntiles, T, Wd, Y, dense, err);
+    return (int)hipGetLastError();
+}
