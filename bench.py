@@ -54,7 +54,7 @@ def parse():
                         "two shared and 256 routed experts) and print its JSON line; "
                         "the workload of the decode kernel-trace profile")
     p.add_argument("--only", choices=["w8a8_64", "shared_decode", "routed_decode", "stress",
-                                      "bwd", "gdn2", "proj", "vendor", "dropin"],
+                                      "bwd", "gdn2", "proj", "vendor", "dropin", "calib"],
                    help="run one of the other shapes' benchmarks alone and print its JSON "
                         "(the workloads of their kernel-trace profiles)")
     p.add_argument("--copy-probe", action="store_true",
@@ -486,6 +486,60 @@ def sub_benchmarks(np, torch, api, stream, only=None):
         res.update(vendor_bench(np, torch, api, stream))
     if want("dropin"):
         res.update(dropin_bench(np, torch, api))
+    if want("calib"):
+        res["calibration"] = calib_bench()
+    return res
+
+
+def calib_bench(blocks=512, iters=4000):
+    """Issue rates of this GPU from libjimotono_calib.so (calib/calib.hip):
+    the int8 MFMA rate alone, the fp32 and fp64 FMA rates alone, and how
+    much of the shorter of the two the GPU hides when MFMAs and FMAs come
+    from different waves of one SIMD (split) or from the same wave (same):
+    overlap = (t_mfma + t_valu - t_mixed) / min(t_mfma, t_valu), 1 for
+    perfect overlap and 0 when the two run one after the other. Then the
+    MFMA rate with LDS-fed operands (and a barrier per 16 MFMAs), and the
+    128x256 tile GEMM's rate with its operands in HBM or aliased into L2.
+    512 blocks of 8 waves: 4 waves per SIMD. Times per wave iteration are in
+    ns per SIMD (each SIMD runs blocks * 8 / 1024 waves)."""
+    import ctypes as C
+    Lc = C.CDLL(os.path.join(ROOT, "jimotono_amd", "libjimotono_calib.so"))
+    Lc.jt_calib_issue.argtypes = [C.c_int, C.c_int, C.c_int, C.POINTER(C.c_float)]
+    Lc.jt_calib_tile.argtypes = [C.c_int, C.POINTER(C.c_float), C.POINTER(C.c_double)]
+    t = []
+    for mode in range(9):
+        ms = C.c_float()
+        rc = Lc.jt_calib_issue(mode, blocks, iters, C.byref(ms))
+        assert rc == 0, f"jt_calib_issue({mode}) rc={rc}"
+        t.append(ms.value)
+    per_simd = iters * blocks * 8 / 1024  # wave iterations per SIMD
+    ns = lambda m: t[m] * 1e6 / per_simd  # noqa: E731
+    mfma_ops = blocks * 8 * iters * 16 * 32768.0
+    tops = lambda m, frac=1.0: mfma_ops * frac / (t[m] * 1e-3) / 1e12  # noqa: E731
+    ovl = lambda a, b, mix: (a + b - mix) / min(a, b)  # noqa: E731
+    res = {
+        "blocks": blocks, "iters": iters, "waves_per_simd": blocks * 8 // 1024,
+        "mfma_i8_16x16x64_tops": tops(0),
+        "mfma_i8_ns_each": ns(0) / 16,
+        "fp32_fma_wave64_ns_each": ns(1) / 64,
+        "fp64_fma_wave64_ns_each": ns(4) / 64,
+        "overlap_fp32_split_waves": ovl(t[0] / 2, t[1] / 2, t[2]),
+        "overlap_fp32_same_wave": ovl(t[0], t[1], t[3]),
+        "overlap_fp64_split_waves": ovl(t[0] / 2, t[4] / 2, t[5]),
+        "overlap_fp64_same_wave": ovl(t[0], t[4], t[6]),
+        "mfma_lds_fed_tops": tops(7),
+        "mfma_lds_fed_barrier_tops": tops(8),
+        "ms": dict(zip(["mfma", "fp32", "mfma_fp32_split", "mfma_fp32_same", "fp64",
+                        "mfma_fp64_split", "mfma_fp64_same", "mfma_lds", "mfma_lds_barrier"],
+                       t)),
+    }
+    tile = {}
+    for which, name in enumerate(["hbm_A_W_C", "C_aliased", "A_C_aliased", "all_in_L2"]):
+        us, tp = C.c_float(), C.c_double()
+        rc = Lc.jt_calib_tile(which, C.byref(us), C.byref(tp))
+        assert rc == 0, f"jt_calib_tile({which}) rc={rc}"
+        tile[name] = {"us": us.value, "tops": tp.value}
+    res["tile_128x256_k1024_plain"] = tile
     return res
 
 

@@ -183,3 +183,22 @@ def test_tmac_size_functions(lib):
                 rc2 = getattr(ref, name)(n, k, C.byref(o2))
                 assert (rc2, C.get_errno(), o2.value) == (rc, er, out.value), (name, n, k)
     assert fq(4, 32, None) == 2 and fp(4, 32, None) == 2
+
+
+def test_calibration_library_is_separate():
+    """bench.py's issue-rate probes (libjimotono_calib.so) load without a GPU
+    and export their two entries; the drop-in library and the package never
+    refer to them."""
+    cal = os.path.join(ROOT, "jimotono_amd", "libjimotono_calib.so")
+    if not os.path.exists(cal):
+        pytest.fail(f"{cal} not built: run `make -C jimotono_amd/csrc`")
+    L = C.CDLL(cal)
+    assert hasattr(L, "jt_calib_issue") and hasattr(L, "jt_calib_tile")
+    assert not hasattr(C.CDLL(LIB), "jt_calib_issue")
+    pkg = os.path.join(ROOT, "jimotono_amd")
+    for dp, _, fs in os.walk(pkg):
+        if os.path.basename(dp) == "calib":
+            continue
+        for f in fs:
+            if f.endswith((".py", ".c", ".h", ".hip")):
+                assert "calib" not in open(os.path.join(dp, f), errors="ignore").read(), f
