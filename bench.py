@@ -729,9 +729,24 @@ def stress_bench(np, torch, api, stream):
     Ls.set_profiling(False)
     gops = 2.0 * T * k * (2 * h * n + n * h)
     gemm_ms = (st["routed_gateup"] + st["routed_down"]) / cnt
+    # Bounds of the grouped GEMM: global max(ops / peak, bytes / HBM) with the
+    # weights of every expert, X int8 and Y fp32 once; and the per-expert
+    # attainable time sum_e max(ops_e / peak, bytes_e / HBM), bytes_e = its
+    # INT2 gate/up, INT4 down and fp16 group scales plus its gathered rows
+    # (int8 in, fp32 out), as if the experts ran one after another
+    wbytes = 2 * h * n // 4 + n * h // 2 + 2 * (2 * h * n // 64 + n * h // 64)
+    rows = np.bincount(ids.ravel(), minlength=E).astype(np.float64)
+    tot_bytes = E * wbytes + T * n + T * n * 4
+    glob_ms = max(gops / INT8_PEAK, tot_bytes / HBM_PEAK) * 1e3
+    ops_e = 2.0 * rows * 3 * h * n
+    bytes_e = np.where(rows > 0, wbytes, 0) + rows * n * 5
+    per_e_ms = float(np.maximum(ops_e / INT8_PEAK, bytes_e / HBM_PEAK).sum() * 1e3)
     res["stress_prefill_E512"] = {"ms_per_layer": ev, "grouped_gemm_ms": gemm_ms,
                                   "grouped_gemm_tops": gops / (gemm_ms / 1e3) / 1e12,
                                   "mfma_frac": gops / (gemm_ms / 1e3) / INT8_PEAK,
+                                  "bound_global_ms": glob_ms,
+                                  "bound_per_expert_ms": per_e_ms,
+                                  "expert_bytes": wbytes, "head_expert_rows": int(rows.max()),
                                   "stages_ms": {s: v / cnt for s, v in st.items()}}
     del Ls
     torch.cuda.empty_cache()

@@ -27,6 +27,8 @@
 //     top-k.
 // logits[t][e] holds the exact float logit for candidates and the float of
 // the approximation for the others.
+#include <atomic>
+
 #include "gemm_w8a8.h"
 #include "jt_launch.h"
 
@@ -178,63 +180,79 @@ extern "C" int jtk_router_codes(const float *X, int rows, int n, int8_t *qh, int
 
 // ---- 2. approximate logits ----
 // Block = 64 tokens x 64 experts, 8 waves: 4 waves of 16 tokens times 2
-// k-halves (wave group g takes the k-blocks of parity g); per 64-K block a
-// wave loads its 2 A fragments and 8 panels (hi/lo of 4 expert panels) one
-// block ahead, then runs 16 MFMAs into three int32 sums per 16x16 tile. The
-// second group's int32 sums are added to the first's through LDS (exact).
-// Two waves per SIMD instead of one hide the load latency of the k chain.
+// k-groups (group g takes the k-blocks of parity g, one per step). Per step
+// each wave copies by DMA, into an RA_NST-step LDS ring, its own 16 token
+// rows' hi and lo fragments and one of the group's 4 expert panel pairs
+// (hi and lo codes); the group's 4 token waves then read the 4 panel pairs
+// there. Only LDS-DMA copies are in flight in the loop, so each wait covers
+// exactly the stage it needs. Per step a wave runs 16 MFMAs into three
+// int32 sums per 16x16 tile; group 1's sums are added to group 0's through
+// LDS (exact), so the result does not depend on how K was split.
+#define RA_NST 3
+// per step slot and group: A hi of waves 0-3, A lo of waves 0-3, B hi of
+// panels 0-3, B lo of panels 0-3, each 64 lanes x 16 B
+#define RA_LDS (RA_NST * 2 * 16 * 1024)
+static_assert(RA_LDS >= 4 * 3 * 4 * 64 * 16, "the sums fit the ring");
 __global__ __launch_bounds__(512) void k_router_approx(
     const int8_t *__restrict__ Xh, const int8_t *__restrict__ Xl, int n,
     const double2 *__restrict__ xinfo, const int8_t *__restrict__ Wh,
     const int8_t *__restrict__ Wl, const double2 *__restrict__ winfo, int T, int E,
     double *__restrict__ approx) {
-    __shared__ v4i part[4][3][4][64];  // group 1's sums: [token wave][hh|mid|ll][j]
+    // [step slot][group][16 fragments][64 lanes x 16 B] (RA_LDS bytes of
+    // dynamic LDS); after the k-loop the same bytes hold group 1's sums
+    // [token wave][hh|mid|ll][j]
+    extern __shared__ __attribute__((aligned(1024))) int8_t ra_lds[];
+    int8_t(*ring)[2][16][1024] = (int8_t(*)[2][16][1024])ra_lds;
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: MFMA guards branch
     const int wave = wv & 3, kg = wv >> 2;
     const int t0 = blockIdx.x * 64 + wave * 16, e0 = blockIdx.y * 64;
     const int KB = n / 64;
+    const int NS = (KB + 1) / 2;  // steps of both groups (group 1 idles in an odd KB's last)
     const int r = lane & 15, kc = lane >> 4;
     const int64_t arow = (int64_t)min(t0 + r, T - 1) * n + kc * 16;
     const int pb = e0 / 16;
+    // this wave's panel pair: panel pb + wave of the group's k-block
+    const int8_t *bh_src = Wh + (int64_t)(pb + wave) * KB * 1024 + lane * 16;
+    const int8_t *bl_src = Wl + (int64_t)(pb + wave) * KB * 1024 + lane * 16;
+    auto kb_of = [&](int st) { return min(2 * st + kg, KB - 1); };  // clamped: in bounds
+    auto issue = [&](int st) {
+        const int kb = kb_of(st);
+        int8_t(*slot)[1024] = ring[st % RA_NST][kg];
+        dma<16>(Xh + arow + kb * 64, slot[wave]);
+        dma<16>(Xl + arow + kb * 64, slot[4 + wave]);
+        dma<16>(bh_src + (int64_t)kb * 1024, slot[8 + wave]);
+        dma<16>(bl_src + (int64_t)kb * 1024, slot[12 + wave]);
+    };
     // HL and LH share their scale, so one int32 sum holds both (|sum| <
     // 2 n 127^2 < 2^31 for n <= 4096)
     v4i hh[4], mid[4], ll[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) hh[j] = mid[j] = ll[j] = (v4i){0, 0, 0, 0};
-    struct Frag {
-        v4i ah, al, bh[4], bl[4];
-    };
-    auto load = [&](int kb, Frag &f) {
-        f.ah = *(const v4i *)(Xh + arow + kb * 64);
-        f.al = *(const v4i *)(Xl + arow + kb * 64);
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int64_t po = ((int64_t)(pb + j) * KB + kb) * 1024 + lane * 16;
-            f.bh[j] = *(const v4i *)(Wh + po);
-            f.bl[j] = *(const v4i *)(Wl + po);
-        }
-    };
-    auto mma = [&](const Frag &f) {
+    for (int st = 0; st < RA_NST - 1; st++)
+        if (st < NS) issue(st);
+    for (int st = 0; st < NS; st++) {
+        wait_stage<4>(min(RA_NST - 2, NS - 1 - st));  // this wave's copies of stage st
+        barrier_lds();  // ... and every other wave's; slot st - 1 is free
+        if (st + RA_NST - 1 < NS) issue(st + RA_NST - 1);
+        if (2 * st + kg < KB) {  // wave-uniform
+            const int8_t(*slot)[1024] = ring[st % RA_NST][kg];
+            const v4i ah = *(const v4i *)(slot[wave] + lane * 16);
+            const v4i al = *(const v4i *)(slot[4 + wave] + lane * 16);
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            hh[j] = mfma16x16x64(f.ah, f.bh[j], hh[j]);
-            mid[j] = mfma16x16x64(f.ah, f.bl[j], mid[j]);
-            mid[j] = mfma16x16x64(f.al, f.bh[j], mid[j]);
-            ll[j] = mfma16x16x64(f.al, f.bl[j], ll[j]);
+            for (int j = 0; j < 4; j++) {
+                const v4i bh = *(const v4i *)(slot[8 + j] + lane * 16);
+                const v4i bl = *(const v4i *)(slot[12 + j] + lane * 16);
+                hh[j] = mfma16x16x64(ah, bh, hh[j]);
+                mid[j] = mfma16x16x64(ah, bl, mid[j]);
+                mid[j] = mfma16x16x64(al, bh, mid[j]);
+                ll[j] = mfma16x16x64(al, bl, ll[j]);
+            }
         }
-    };
-    // the next k-block's fragments load while the current one is summed;
-    // this group's k-blocks are kg, kg + 2, kg + 4, ...
-    Frag fa, fb;
-    if (kg < KB) load(kg, fa);
-    for (int kb = kg; kb < KB; kb += 4) {
-        if (kb + 2 < KB) load(kb + 2, fb);
-        mma(fa);
-        if (kb + 2 >= KB) break;
-        if (kb + 4 < KB) load(kb + 4, fa);
-        mma(fb);
     }
+    v4i(*part)[3][4][64] = (v4i(*)[3][4][64])ra_lds;
+    barrier_lds();  // every wave is done with the ring
     if (kg == 1) {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -345,8 +363,20 @@ extern "C" int jtk_router_approx(const int8_t *Xh, const int8_t *Xl, int n, cons
                            approx);
         return (int)hipGetLastError();
     }
+    // dynamic LDS above 64 KiB must be enabled per device, once
+    static std::atomic<bool> attr_set[64];  // set once per device; a repeat is harmless
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= 64) return (int)hipErrorInvalidDevice;
+    if (!attr_set[dev]) {
+        e = hipFuncSetAttribute((const void *)k_router_approx,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, RA_LDS);
+        if (e != hipSuccess) return (int)e;
+        attr_set[dev] = true;
+    }
     dim3 grid((unsigned)((T + 63) / 64), (unsigned)((E + 63) / 64));
-    hipLaunchKernelGGL(k_router_approx, grid, dim3(512), 0, s, Xh, Xl, n,
+    hipLaunchKernelGGL(k_router_approx, grid, dim3(512), RA_LDS, s, Xh, Xl, n,
                        (const double2 *)xinfo, Wh, Wl, (const double2 *)winfo, T, E, approx);
     return (int)hipGetLastError();
 }
