@@ -177,10 +177,30 @@ __global__ __launch_bounds__(256) void k_gdn2_check(const float *__restrict__ Q,
     const float *q = Q + h * hk, *k = K + h * hk, *b = B + h * hk, *a = A + h * hk;
     const float *v = V + h * hv, *w = W + h * hv;
     bool bad = false;
-    for (int i = i0; i < nk; i += st)
-        bad |= !isfinite(q[i]) || !isfinite(k[i]) || !isfinite(b[i]) ||
-               !(a[i] >= 0.0f && a[i] <= 1.0f);
-    for (int i = i0; i < nv; i += st) bad |= !isfinite(v[i]) || !isfinite(w[i]);
+    const uintptr_t al = (uintptr_t)q | (uintptr_t)k | (uintptr_t)b | (uintptr_t)a |
+                         (uintptr_t)v | (uintptr_t)w;
+    if (((nk | nv) & 3) == 0 && (al & 15) == 0) {
+        // 16-byte loads, four element groups of each array per thread in flight
+        auto fin = [](float4 x) {
+            return isfinite(x.x) && isfinite(x.y) && isfinite(x.z) && isfinite(x.w);
+        };
+        auto unit = [](float4 x) {
+            return x.x >= 0.0f && x.x <= 1.0f && x.y >= 0.0f && x.y <= 1.0f && x.z >= 0.0f &&
+                   x.z <= 1.0f && x.w >= 0.0f && x.w <= 1.0f;
+        };
+        const float4 *q4 = (const float4 *)q, *k4 = (const float4 *)k, *b4 = (const float4 *)b;
+        const float4 *a4 = (const float4 *)a, *v4 = (const float4 *)v, *w4 = (const float4 *)w;
+#pragma unroll 4
+        for (int i = i0; i < nk / 4; i += st)
+            bad |= !fin(q4[i]) || !fin(k4[i]) || !fin(b4[i]) || !unit(a4[i]);
+#pragma unroll 4
+        for (int i = i0; i < nv / 4; i += st) bad |= !fin(v4[i]) || !fin(w4[i]);
+    } else {
+        for (int i = i0; i < nk; i += st)
+            bad |= !isfinite(q[i]) || !isfinite(k[i]) || !isfinite(b[i]) ||
+                   !(a[i] >= 0.0f && a[i] <= 1.0f);
+        for (int i = i0; i < nv; i += st) bad |= !isfinite(v[i]) || !isfinite(w[i]);
+    }
     bad = wave_or_i(bad);
     if (bad && (threadIdx.x & 63) == 0) {
         atomicOr(&flag[h], 1);
@@ -512,6 +532,154 @@ __global__ __launch_bounds__(256) void k_gdn2_cols(float *__restrict__ S, float 
         }
     }
 }
+// k_gdn2_cols for operands in LDS with dk % 4 == 0 (the PF case), with
+// every LDS operand read 16 bytes at a time: the S tile is held transposed
+// (column cc's dk values contiguous, stride dk + 4) and so is G (column
+// cc's C values contiguous), so phase 1 reads 4 consecutive i of WI, QI
+// and S, phases 2 and 3 4 consecutive s of L, P and G, and phase 4 (thread
+// = 4 consecutive i of one column) 4 consecutive i of WG and S per s. Each
+// value is still formed by the same operations in the same order as in
+// k_gdn2_cols (phase 1's chains in ascending i, the substitution in
+// ascending s, and so on), so the results are the same bits; only the
+// number of LDS instructions drops, which is what a chunk's phases wait on.
+// The output row sum of phase 1 stays in the thread's register until
+// phase 3 (same thread).
+template <int C>
+__global__ __launch_bounds__(256) void k_gdn2_cols4(float *__restrict__ S, float *__restrict__ Out,
+                                                    const float *__restrict__ V,
+                                                    const float *__restrict__ W, int64_t hv,
+                                                    int nch, int dk, int dv,
+                                                    const int *__restrict__ flag,
+                                                    const float *__restrict__ rec) {
+    constexpr int NC = 256 / C;
+    constexpr int NL = CHUNK_LDS + 4 * 32;
+    constexpr int SKMAX = CHUNK_LDS / C + 4;  // S column stride bound (dk <= CHUNK_LDS / C)
+    constexpr int GS = C + 4;                 // G column stride
+    __shared__ __attribute__((aligned(16))) float G[NC * GS];
+    __shared__ __attribute__((aligned(16))) float wi_l[NL], qi_l[NL], wg_l[NL];
+    __shared__ __attribute__((aligned(16))) float sT[NC * SKMAX];
+    __shared__ __attribute__((aligned(16))) float lp_l[2 * C * C], cf_l[1024];
+    const int h = blockIdx.x, j0 = blockIdx.y * NC, tid = threadIdx.x, lk = dk + 4;
+    if (flag[h]) return;  // a rejected head keeps its S and Out
+    const int64_t Ck = (int64_t)C * dk;
+    float *Sh = S + (int64_t)h * dk * dv;
+    const int ncol = min(NC, dv - j0);
+    const int t = tid / NC, jj = tid % NC, j = j0 + jj;
+    const bool live = jj < ncol;
+    const int sk = dk + 4;  // S column stride (16-byte rows, lanes of nearby columns on distinct banks)
+    for (int n = tid; n < dk * NC; n += 256) {
+        const int i = n / NC, cc = n % NC;
+        sT[cc * sk + i] = cc < ncol ? Sh[(int64_t)i * dv + j0 + cc] : 0.0f;
+    }
+    const int n4 = (int)(Ck / 4), nlp = C * C / 2;
+    float4 wi0, wi1, wi2, wi3, qi0, qi1, qi2, qi3, wg0, wg1, wg2, wg3, lp0, lp1, cf4;
+    float pvw = 0.0f;
+    GDN2_PF(0);
+    const int q4 = dk / 4;
+    for (int c = 0; c < nch; c++) {
+        GDN2_PF_PUT(0, wi0, qi0, wg0);
+        GDN2_PF_PUT(1, wi1, qi1, wg1);
+        GDN2_PF_PUT(2, wi2, qi2, wg2);
+        GDN2_PF_PUT(3, wi3, qi3, wg3);
+        if (tid < nlp) *(float4 *)(lp_l + 4 * tid) = lp0;  // L then P
+        if (tid + 256 < nlp) *(float4 *)(lp_l + 4 * (tid + 256)) = lp1;
+        if (tid < dk / 4) *(float4 *)(cf_l + 4 * tid) = cf4;
+        const float vw0 = pvw;
+        __syncthreads();
+        if (c + 1 < nch) GDN2_PF(c + 1);  // in flight through this chunk's phases
+        const int64_t vo = h * hv + ((int64_t)c * C + t) * dv + j;
+        // ---- phase 1: B_t and the first part of Out_t for column jj ----
+        float o = 0.0f;
+        if (live) {
+            float g = vw0;
+            const float4 *wi = (const float4 *)(wi_l + t * lk), *qi = (const float4 *)(qi_l + t * lk);
+            const float4 *sv = (const float4 *)(sT + jj * sk);
+#pragma unroll 4
+            for (int u = 0; u < q4; u++) {
+                const float4 w4 = wi[u], x4 = qi[u], s4 = sv[u];
+                g = g - w4.x * s4.x;
+                o = o + x4.x * s4.x;
+                g = g - w4.y * s4.y;
+                o = o + x4.y * s4.y;
+                g = g - w4.z * s4.z;
+                o = o + x4.z * s4.z;
+                g = g - w4.w * s4.w;
+                o = o + x4.w * s4.w;
+            }
+            G[jj * GS + t] = g;
+        }
+        __syncthreads();
+        // ---- phase 2: (I + L) E = B per column, E over G ----
+        if (tid < ncol) {
+            float gv[C];
+#pragma unroll
+            for (int u = 0; u < C / 4; u++) {
+                const float4 x = *(const float4 *)(G + tid * GS + 4 * u);
+                gv[4 * u] = x.x, gv[4 * u + 1] = x.y, gv[4 * u + 2] = x.z, gv[4 * u + 3] = x.w;
+            }
+#pragma unroll
+            for (int tt = 1; tt < C; tt++) {
+                const float *Lr = lp_l + tt * C;
+#pragma unroll
+                for (int u = 0; u < C / 4; u++) {
+                    if (4 * u >= tt) break;
+                    const float4 l4 = *(const float4 *)(Lr + 4 * u);
+                    gv[tt] = gv[tt] - l4.x * gv[4 * u];
+                    if (4 * u + 1 < tt) gv[tt] = gv[tt] - l4.y * gv[4 * u + 1];
+                    if (4 * u + 2 < tt) gv[tt] = gv[tt] - l4.z * gv[4 * u + 2];
+                    if (4 * u + 3 < tt) gv[tt] = gv[tt] - l4.w * gv[4 * u + 3];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < C / 4; u++)
+                *(float4 *)(G + tid * GS + 4 * u) =
+                    make_float4(gv[4 * u], gv[4 * u + 1], gv[4 * u + 2], gv[4 * u + 3]);
+        }
+        __syncthreads();
+        // ---- phase 3: Out_t += sum_{s<=t} P[t][s] E_s ----
+        if (live) {
+            const float *Pr = lp_l + C * C + t * C;
+            const float *Gc = G + jj * GS;
+            for (int u = 0; 4 * u <= t; u++) {
+                const float4 p4 = *(const float4 *)(Pr + 4 * u);
+                const float4 e4 = *(const float4 *)(Gc + 4 * u);
+                o = o + p4.x * e4.x;
+                if (4 * u + 1 <= t) o = o + p4.y * e4.y;
+                if (4 * u + 2 <= t) o = o + p4.z * e4.z;
+                if (4 * u + 3 <= t) o = o + p4.w * e4.w;
+            }
+            Out[vo] = o;
+        }
+        // ---- phase 4: S[i] <- CF[C-1][i] S[i] + sum_s WG[s][i] E_s ----
+        for (int u = tid; u < q4 * NC; u += 256) {
+            const int cc = u / q4, i4 = u % q4;
+            if (cc >= ncol) continue;
+            float4 *sp = (float4 *)(sT + cc * sk) + i4;
+            const float4 s4 = *sp, f4 = *(const float4 *)(cf_l + 4 * i4);
+            float4 rv = make_float4(s4.x * f4.x, s4.y * f4.y, s4.z * f4.z, s4.w * f4.w);
+            const float *Gc = G + cc * GS;
+#pragma unroll
+            for (int v = 0; v < C / 4; v++) {
+                const float4 e4 = *(const float4 *)(Gc + 4 * v);
+                const float ev[4] = {e4.x, e4.y, e4.z, e4.w};
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const float4 w4 = *(const float4 *)(wg_l + (4 * v + q) * lk + 4 * i4);
+                    rv.x = rv.x + w4.x * ev[q];
+                    rv.y = rv.y + w4.y * ev[q];
+                    rv.z = rv.z + w4.z * ev[q];
+                    rv.w = rv.w + w4.w * ev[q];
+                }
+            }
+            *sp = rv;
+        }
+        __syncthreads();
+    }
+    for (int n = tid; n < dk * NC; n += 256) {
+        const int i = n / NC, cc = n % NC;
+        if (cc < ncol) Sh[(int64_t)i * dv + j0 + cc] = sT[cc * sk + i];
+    }
+}
 #undef GDN2_PF
 #undef GDN2_PF_PUT
 
@@ -567,11 +735,11 @@ extern "C" int jtk_gdn2_prefill(float *S, float *Out, const float *Q, const floa
     const dim3 grid((unsigned)H, (unsigned)((dv + 256 / C - 1) / (256 / C)));
     const bool v4 = dk % 4 == 0;  // the record prefetch with 16-byte loads
     if (C == 16 && cl && v4)
-        hipLaunchKernelGGL((k_gdn2_cols<16, true, true>), grid, dim3(256), 0, s, S, Out, V, W, hv,
-                           nch, dk, dv, flag, rec);
+        hipLaunchKernelGGL((k_gdn2_cols4<16>), grid, dim3(256), 0, s, S, Out, V, W, hv, nch, dk,
+                           dv, flag, rec);
     else if (C == 32 && cl && v4)
-        hipLaunchKernelGGL((k_gdn2_cols<32, true, true>), grid, dim3(256), 0, s, S, Out, V, W, hv,
-                           nch, dk, dv, flag, rec);
+        hipLaunchKernelGGL((k_gdn2_cols4<32>), grid, dim3(256), 0, s, S, Out, V, W, hv, nch, dk,
+                           dv, flag, rec);
     else if (C == 16 && cl)
         hipLaunchKernelGGL((k_gdn2_cols<16, true, false>), grid, dim3(256), 0, s, S, Out, V, W,
                            hv, nch, dk, dv, flag, rec);
