@@ -543,15 +543,17 @@ __global__ __launch_bounds__(256) void k_gdn2_cols(float *__restrict__ S, float 
 // ascending s, and so on), so the results are the same bits; only the
 // number of LDS instructions drops, which is what a chunk's phases wait on.
 // The output row sum of phase 1 stays in the thread's register until
-// phase 3 (same thread).
-template <int C>
+// phase 3 (same thread). NC = 128 / C columns per block (half the block's
+// threads in phases 1, 3 and 4) doubles the blocks when 256 / C columns
+// per block would leave CUs idle; each column's arithmetic is unchanged.
+template <int C, int NC>
 __global__ __launch_bounds__(256) void k_gdn2_cols4(float *__restrict__ S, float *__restrict__ Out,
                                                     const float *__restrict__ V,
                                                     const float *__restrict__ W, int64_t hv,
                                                     int nch, int dk, int dv,
                                                     const int *__restrict__ flag,
                                                     const float *__restrict__ rec) {
-    constexpr int NC = 256 / C;
+    static_assert(C * NC == 256 || C * NC == 128, "256 or 128 (t, column) pairs");
     constexpr int NL = CHUNK_LDS + 4 * 32;
     constexpr int SKMAX = CHUNK_LDS / C + 4;  // S column stride bound (dk <= CHUNK_LDS / C)
     constexpr int GS = C + 4;                 // G column stride
@@ -564,8 +566,10 @@ __global__ __launch_bounds__(256) void k_gdn2_cols4(float *__restrict__ S, float
     const int64_t Ck = (int64_t)C * dk;
     float *Sh = S + (int64_t)h * dk * dv;
     const int ncol = min(NC, dv - j0);
+    // with C * NC = 128 the upper 128 threads only copy records and pass
+    // the barriers
     const int t = tid / NC, jj = tid % NC, j = j0 + jj;
-    const bool live = jj < ncol;
+    const bool live = jj < ncol && tid < C * NC;
     const int sk = dk + 4;  // S column stride (16-byte rows, lanes of nearby columns on distinct banks)
     for (int n = tid; n < dk * NC; n += 256) {
         const int i = n / NC, cc = n % NC;
@@ -734,12 +738,22 @@ extern "C" int jtk_gdn2_prefill(float *S, float *Out, const float *Q, const floa
                            Q, K, B, A, hk, C, dk, flag, rec);
     const dim3 grid((unsigned)H, (unsigned)((dv + 256 / C - 1) / (256 / C)));
     const bool v4 = dk % 4 == 0;  // the record prefetch with 16-byte loads
-    if (C == 16 && cl && v4)
-        hipLaunchKernelGGL((k_gdn2_cols4<16>), grid, dim3(256), 0, s, S, Out, V, W, hv, nch, dk,
-                           dv, flag, rec);
+    // narrow blocks (128 / C columns) when the wide ones would not fill the
+    // GPU's 256 CUs
+    const bool narrow = (int64_t)grid.x * grid.y < 256;
+    const dim3 grid_n((unsigned)H, (unsigned)((dv + 128 / C - 1) / (128 / C)));
+    if (C == 16 && cl && v4 && narrow)
+        hipLaunchKernelGGL((k_gdn2_cols4<16, 8>), grid_n, dim3(256), 0, s, S, Out, V, W, hv, nch,
+                           dk, dv, flag, rec);
+    else if (C == 32 && cl && v4 && narrow)
+        hipLaunchKernelGGL((k_gdn2_cols4<32, 4>), grid_n, dim3(256), 0, s, S, Out, V, W, hv, nch,
+                           dk, dv, flag, rec);
+    else if (C == 16 && cl && v4)
+        hipLaunchKernelGGL((k_gdn2_cols4<16, 16>), grid, dim3(256), 0, s, S, Out, V, W, hv, nch,
+                           dk, dv, flag, rec);
     else if (C == 32 && cl && v4)
-        hipLaunchKernelGGL((k_gdn2_cols4<32>), grid, dim3(256), 0, s, S, Out, V, W, hv, nch, dk,
-                           dv, flag, rec);
+        hipLaunchKernelGGL((k_gdn2_cols4<32, 8>), grid, dim3(256), 0, s, S, Out, V, W, hv, nch,
+                           dk, dv, flag, rec);
     else if (C == 16 && cl)
         hipLaunchKernelGGL((k_gdn2_cols<16, true, false>), grid, dim3(256), 0, s, S, Out, V, W,
                            hv, nch, dk, dv, flag, rec);
