@@ -377,11 +377,9 @@ __global__ __launch_bounds__(256) void k_gdn2_prep(const float *__restrict__ Q,
 // values in registers; phase 3 Out_t += sum_{s<=t} P[t][s] E_s; phase 4
 // thread (i, column) S[i] <- CF[C-1][i] S[i] + sum_s WG[s][i] E_s
 // (src/gdn2.c:614-680, 716-842). CL: each chunk's record is staged in LDS
-// and the block's S tile stays in LDS from the first chunk to the last;
-// with dk % 4 == 0 the next chunk's record (and the thread's v*w value)
-// is loaded into registers with 16-byte loads while the current chunk
-// computes, so a chunk does not wait on its record's memory latency.
-template <int C, bool CL, bool PF>
+// and the block's S tile stays in LDS from the first chunk to the last.
+// (CL with dk % 4 == 0 runs as k_gdn2_cols4 below.)
+template <int C, bool CL>
 __global__ __launch_bounds__(256) void k_gdn2_cols(float *__restrict__ S, float *__restrict__ Out,
                                                    const float *__restrict__ V,
                                                    const float *__restrict__ W, int64_t hv,
@@ -409,64 +407,11 @@ __global__ __launch_bounds__(256) void k_gdn2_cols(float *__restrict__ S, float 
             s_l[n] = cc < ncol ? Sh[(int64_t)i * dv + j0 + cc] : 0.0f;
         }
     }
-    // register prefetch of a chunk's record (PF: CL and dk % 4 == 0): thread
-    // tid's float4 f = tid + 256u (u < 4) of WI, QI and WG [C][dk], of L and
-    // P, and of CF's last row; indices past an array are clamped to its last
-    // element (loaded, never stored), so every register is always written
-    constexpr bool pf = PF;
-    static_assert(!PF || (CL && CHUNK_LDS / 4 / 256 == 4 && 2 * C * C / 4 <= 512),
-                  "the prefetch holds 4 float4 of each [C][dk] array and 2 of L, P");
-    const int n4 = (int)(Ck / 4), nlp = C * C / 2;
-    float4 wi0, wi1, wi2, wi3, qi0, qi1, qi2, qi3, wg0, wg1, wg2, wg3, lp0, lp1, cf4;
-    float pvw = 0.0f;
-#define GDN2_PF(cc)                                                                           \
-    do {                                                                                      \
-        const float4 *r4 =                                                                    \
-            (const float4 *)(rec + ((int64_t)h * nch + (cc)) * chunk_rec_floats(C, dk));      \
-        int f_ = min(tid, n4 - 1);                                                            \
-        wi0 = r4[n4 + f_], qi0 = r4[2 * n4 + f_], wg0 = r4[3 * n4 + f_];                      \
-        f_ = min(tid + 256, n4 - 1);                                                          \
-        wi1 = r4[n4 + f_], qi1 = r4[2 * n4 + f_], wg1 = r4[3 * n4 + f_];                      \
-        f_ = min(tid + 512, n4 - 1);                                                          \
-        wi2 = r4[n4 + f_], qi2 = r4[2 * n4 + f_], wg2 = r4[3 * n4 + f_];                      \
-        f_ = min(tid + 768, n4 - 1);                                                          \
-        wi3 = r4[n4 + f_], qi3 = r4[2 * n4 + f_], wg3 = r4[3 * n4 + f_];                      \
-        lp0 = r4[4 * n4 + min(tid, nlp - 1)];                                                 \
-        lp1 = r4[4 * n4 + min(tid + 256, nlp - 1)];                                           \
-        cf4 = r4[(C - 1) * dk / 4 + min(tid, dk / 4 - 1)];                                    \
-        if (live) {                                                                           \
-            const int64_t vq = h * hv + ((int64_t)(cc) * C + t) * dv + j;                     \
-            pvw = W[vq] * V[vq];                                                              \
-        }                                                                                     \
-    } while (0)
-#define GDN2_PF_PUT(u, a, b, g)                                                               \
-    do {                                                                                      \
-        const int f_ = tid + 256 * (u);                                                       \
-        if (f_ < n4) {                                                                        \
-            const int at_ = (4 * f_ / dk) * lk + 4 * f_ % dk;                                 \
-            *(float4 *)(wi_l + at_) = a;                                                      \
-            *(float4 *)(qi_l + at_) = b;                                                      \
-            *(float4 *)(wg_l + at_) = g;                                                      \
-        }                                                                                     \
-    } while (0)
-    if constexpr (pf) GDN2_PF(0);
     for (int c = 0; c < nch; c++) {
         const float *r = rec + ((int64_t)h * nch + c) * chunk_rec_floats(C, dk);
         const float *CF = r, *WI = CF + Ck, *QI = WI + Ck, *WG = QI + Ck;
         const float *L = WG + Ck, *P = L + C * C;
-        float vw0 = 0.0f;
-        if constexpr (pf) {
-            GDN2_PF_PUT(0, wi0, qi0, wg0);
-            GDN2_PF_PUT(1, wi1, qi1, wg1);
-            GDN2_PF_PUT(2, wi2, qi2, wg2);
-            GDN2_PF_PUT(3, wi3, qi3, wg3);
-            if (tid < nlp) *(float4 *)(lp_l + 4 * tid) = lp0;  // L then P
-            if (tid + 256 < nlp) *(float4 *)(lp_l + 4 * (tid + 256)) = lp1;
-            if (tid < dk / 4) *(float4 *)(cf_l + 4 * tid) = cf4;
-            vw0 = pvw;
-            __syncthreads();
-            if (c + 1 < nch) GDN2_PF(c + 1);  // in flight through this chunk's phases
-        } else if (CL) {
+        if (CL) {
             for (int64_t n = tid; n < Ck; n += 256) {
                 const int tt = (int)(n / dk), i = (int)(n % dk);
                 wi_l[tt * lk + i] = WI[n];
@@ -481,7 +426,7 @@ __global__ __launch_bounds__(256) void k_gdn2_cols(float *__restrict__ S, float 
         const float *L_b = CL ? lp_l : L, *P_b = CL ? lp_l + C * C : P;
         const int64_t vo = h * hv + ((int64_t)c * C + t) * dv + j;
         if (live) {
-            float g = pf ? vw0 : W[vo] * V[vo];  // vw_t
+            float g = W[vo] * V[vo];  // vw_t
             float o = 0.0f;
             const float *wi = wi_b + t * ld, *qi = qi_b + t * ld;
 #pragma unroll 8
@@ -532,7 +477,44 @@ __global__ __launch_bounds__(256) void k_gdn2_cols(float *__restrict__ S, float 
         }
     }
 }
-// k_gdn2_cols for operands in LDS with dk % 4 == 0 (the PF case), with
+// Register prefetch of a chunk's record for k_gdn2_cols4 (operands in LDS,
+// dk % 4 == 0): thread tid's float4 f = tid + 256u (u < 4) of WI, QI and WG
+// [C][dk], of L and P, and of CF's last row; indices past an array are
+// clamped to its last element (loaded, never stored), so every register is
+// always written. GDN2_PF_PUT stores part u of WI, QI and WG into LDS rows
+// of stride lk.
+#define GDN2_PF(cc)                                                                           \
+    do {                                                                                      \
+        const float4 *r4 =                                                                    \
+            (const float4 *)(rec + ((int64_t)h * nch + (cc)) * chunk_rec_floats(C, dk));      \
+        int f_ = min(tid, n4 - 1);                                                            \
+        wi0 = r4[n4 + f_], qi0 = r4[2 * n4 + f_], wg0 = r4[3 * n4 + f_];                      \
+        f_ = min(tid + 256, n4 - 1);                                                          \
+        wi1 = r4[n4 + f_], qi1 = r4[2 * n4 + f_], wg1 = r4[3 * n4 + f_];                      \
+        f_ = min(tid + 512, n4 - 1);                                                          \
+        wi2 = r4[n4 + f_], qi2 = r4[2 * n4 + f_], wg2 = r4[3 * n4 + f_];                      \
+        f_ = min(tid + 768, n4 - 1);                                                          \
+        wi3 = r4[n4 + f_], qi3 = r4[2 * n4 + f_], wg3 = r4[3 * n4 + f_];                      \
+        lp0 = r4[4 * n4 + min(tid, nlp - 1)];                                                 \
+        lp1 = r4[4 * n4 + min(tid + 256, nlp - 1)];                                           \
+        cf4 = r4[(C - 1) * dk / 4 + min(tid, dk / 4 - 1)];                                    \
+        if (live) {                                                                           \
+            const int64_t vq = h * hv + ((int64_t)(cc) * C + t) * dv + j;                     \
+            pvw = W[vq] * V[vq];                                                              \
+        }                                                                                     \
+    } while (0)
+#define GDN2_PF_PUT(u, a, b, g)                                                               \
+    do {                                                                                      \
+        const int f_ = tid + 256 * (u);                                                       \
+        if (f_ < n4) {                                                                        \
+            const int at_ = (4 * f_ / dk) * lk + 4 * f_ % dk;                                 \
+            *(float4 *)(wi_l + at_) = a;                                                      \
+            *(float4 *)(qi_l + at_) = b;                                                      \
+            *(float4 *)(wg_l + at_) = g;                                                      \
+        }                                                                                     \
+    } while (0)
+
+// k_gdn2_cols for operands in LDS with dk % 4 == 0, with
 // every LDS operand read 16 bytes at a time: the S tile is held transposed
 // (column cc's dk values contiguous, stride dk + 4) and so is G (column
 // cc's C values contiguous), so phase 1 reads 4 consecutive i of WI, QI
@@ -554,6 +536,8 @@ __global__ __launch_bounds__(256) void k_gdn2_cols4(float *__restrict__ S, float
                                                     const int *__restrict__ flag,
                                                     const float *__restrict__ rec) {
     static_assert(C * NC == 256 || C * NC == 128, "256 or 128 (t, column) pairs");
+    static_assert(CHUNK_LDS / 4 / 256 == 4 && 2 * C * C / 4 <= 512,
+                  "the prefetch holds 4 float4 of each [C][dk] array and 2 of L, P");
     constexpr int NL = CHUNK_LDS + 4 * 32;
     constexpr int SKMAX = CHUNK_LDS / C + 4;  // S column stride bound (dk <= CHUNK_LDS / C)
     constexpr int GS = C + 4;                 // G column stride
@@ -755,16 +739,16 @@ extern "C" int jtk_gdn2_prefill(float *S, float *Out, const float *Q, const floa
         hipLaunchKernelGGL((k_gdn2_cols4<32, 8>), grid, dim3(256), 0, s, S, Out, V, W, hv, nch,
                            dk, dv, flag, rec);
     else if (C == 16 && cl)
-        hipLaunchKernelGGL((k_gdn2_cols<16, true, false>), grid, dim3(256), 0, s, S, Out, V, W,
+        hipLaunchKernelGGL((k_gdn2_cols<16, true>), grid, dim3(256), 0, s, S, Out, V, W,
                            hv, nch, dk, dv, flag, rec);
     else if (C == 16)
-        hipLaunchKernelGGL((k_gdn2_cols<16, false, false>), grid, dim3(256), 0, s, S, Out, V, W,
+        hipLaunchKernelGGL((k_gdn2_cols<16, false>), grid, dim3(256), 0, s, S, Out, V, W,
                            hv, nch, dk, dv, flag, rec);
     else if (cl)
-        hipLaunchKernelGGL((k_gdn2_cols<32, true, false>), grid, dim3(256), 0, s, S, Out, V, W,
+        hipLaunchKernelGGL((k_gdn2_cols<32, true>), grid, dim3(256), 0, s, S, Out, V, W,
                            hv, nch, dk, dv, flag, rec);
     else
-        hipLaunchKernelGGL((k_gdn2_cols<32, false, false>), grid, dim3(256), 0, s, S, Out, V, W,
+        hipLaunchKernelGGL((k_gdn2_cols<32, false>), grid, dim3(256), 0, s, S, Out, V, W,
                            hv, nch, dk, dv, flag, rec);
     return le | (int)hipGetLastError();
 }

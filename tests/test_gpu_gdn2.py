@@ -236,6 +236,37 @@ def test_gdn2_prefill_device_heads(jt, orc, torch_cuda):
         assert same(S1[h], Sh), h
 
 
+@pytest.mark.parametrize("H,T,C_,dk,dv", [(3, 64, 16, 64, 48),     # 16-row chunks, 8-column blocks
+                                          (4, 48, 16, 32, 1024),   # 16-row chunks, 16-column blocks
+                                          (2, 64, 32, 32, 1024)])  # 32-row chunks, 8-column blocks
+def test_gdn2_prefill_device_block_widths(jt, orc, torch_cuda, H, T, C_, dk, dv):
+    """Every column-block width of the prefill's state kernel: blocks of
+    128/C columns while the grid has fewer than 256 blocks of 256/C, then
+    the wide blocks (4 heads x 1024 columns at C=16, 2 x 1024 at C=32),
+    each head's state and outputs against the oracle's chunk chain."""
+    torch = torch_cuda
+    announce(f"jt_hip_gdn2_prefill H={H} T={T} C={C_} {dk}x{dv}")
+    rng = np.random.default_rng(H * 100 + C_ + dv)
+    S = (rng.standard_normal((H, dk, dv)) * 0.3).astype(np.float32)
+    Q, K, B = (rng.standard_normal((H, T, dk)).astype(np.float32) for _ in range(3))
+    A = rng.uniform(0.5, 1, (H, T, dk)).astype(np.float32)
+    V, W = (rng.standard_normal((H, T, dv)).astype(np.float32) for _ in range(2))
+    dS = _t(torch, S)
+    dOut = torch.empty((H, T, dv), device="cuda")
+    rc, _ = jt.gdn2_prefill_device(dS, dOut, *[_t(torch, x) for x in (Q, K, V, B, W, A)], C_)
+    assert rc == 0
+    assert jt.sync_errors() == 0
+    S1, O1 = dS.cpu().numpy(), dOut.cpu().numpy()
+    for h in range(H):
+        Sh = S[h]
+        for c0 in range(0, T, C_):
+            sl = slice(c0, c0 + C_)
+            rc, Sh, Oh = orc.gdn2_prefill_chunk(Sh, Q[h, sl], K[h, sl], V[h, sl], B[h, sl],
+                                                W[h, sl], A[h, sl])
+            assert rc == 0 and same(O1[h, sl], Oh), (h, c0)
+        assert same(S1[h], Sh), h
+
+
 def test_gdn2_prefill_full_size(jt, orc, torch_cuda):
     """The prefill benchmark's shape: 8 heads x 4096 tokens of 128x128
     states in chunks of 32, every head's state and every output against the
