@@ -723,6 +723,10 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
      * launch (k_quant_sort_small) */
     const int qsort = d_ids && !L->prof && T * k <= 1024 && E <= 4096 &&
                       !(S > 0 && T > 16);
+    /* ... and with 16-row tiles of f = 256 and at most 256 pairs, inside the
+     * routed gate/up launch (one launch fewer) */
+    const int qsort_gu = qsort && Tk <= 256 && E <= 1024 && Tk <= 16 * E && h == 256 &&
+                         n % 256 == 0 && n <= 1024 && ((uintptr_t)dX & 15) == 0;
     prof_mark(L, slot, ST_QUANT_X, s);
     if (qsort) {
         /* quantised with the sort below */
@@ -798,6 +802,8 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
     prof_mark(L, slot, ST_SORT, s);
     if (merge16) {
         /* sorted in the top-k launch */
+    } else if (qsort_gu) {
+        /* sorted in the routed gate/up launch below */
     } else if (qsort) {
         le |= jtk_quant_sort_small(dX, T, n, L->Xq, L->sx, ids, Tk, E, (int64_t)Tk, R, L->off,
                                    NULL, L->perm, NULL, NULL, L->tiles, L->ntiles, err, s);
@@ -823,7 +829,13 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
     if (R == 16 && h == 256 && n % 256 == 0 && n <= 1024) {
         /* 16-row tiles: gate/up, SwiGLU, row codes and down in one launch
          * (the three stages are timed as one, under routed_gateup) */
-        if (merge16)
+        if (qsort_gu)
+            le |= jtk_routed_ffn16_sort(dX, T, L->Xq, L->sx, ids, Tk, E, L->off, L->perm,
+                                        L->tiles, L->ntiles, k, L->gu_P, L->gu_S, L->gu_pstride,
+                                        L->gu_sstride, L->dn_P, L->dn_S, L->dn_pstride,
+                                        L->dn_sstride, n, h, L->Ye, L->Sqr, L->ssr, L->Sr, err,
+                                        s);
+        else if (merge16)
             le |= jtk_decode_ffn16_shared_down(
                 L->Xq, L->sx, L->perm, L->tiles, L->ntiles, max_tiles, k, L->gu_P, L->gu_S,
                 L->gu_pstride, L->gu_sstride, L->dn_P, L->dn_S, L->dn_pstride, L->dn_sstride, n,

@@ -20,6 +20,7 @@
 #include "jt_launch.h"
 #include "topk_dev.h"
 #include "sort_dev.h"
+#include "quant_dev.h"
 
 // Output fragment layout of v_mfma_i32_16x16x64_i8 (4 int32 per lane):
 // element r of lane l is row 4*(l/16)+r, column l%16 of the 16x16 tile.
@@ -1683,13 +1684,122 @@ static hipError_t launch_lowbit_res(dim3 grid, int cpb, hipStream_t s, const int
 // identical; the fp32 hidden rows pass through memory unchanged.
 #define RA_WAVES 8  // 4 h-blocks per block, a gate and an up wave for each
 
-template <int G1>
+// ---- caller-routed decode: the pair sort inside the gate/up launch ----
+// With SORT, k_routed_gu16 also does k_quant_sort_small's work (Tk <=
+// SORTF_TK pairs, E <= SORTF_E experts, no drops, 16-row tiles), so the
+// routed FFN of a caller-routed decode takes two launches instead of three:
+//   blocks 0 .. 4 mt - 1 (mt bounds the tile count): (tile, quarter) as
+//     without SORT, except that each block ranks the Tk pairs in LDS itself
+//     (tile_of_sort, sort_small_fast's ranks and tile list), which gives its
+//     tile's descriptor and rows with no round trip through memory, and that
+//     its waves quantise their two token rows from X into LDS (the codes and
+//     scales of quant_row_wave);
+//   block 4 mt: sort_small_fast with its outputs in memory (off, perm,
+//     tiles, ntiles), which the down launch and the combine read;
+//   blocks 4 mt + 1 ..: the token codes Xq and scales sx, one row a wave.
+// Every block ranks the same ids the same way, so the tiles the gate/up
+// blocks take are the tiles the down launch reads.
+struct GuSort {
+    const float *X;
+    const int32_t *ids;
+    int8_t *Xq;
+    float *sx;
+    int32_t *off, *perm, *tiles, *ntiles;
+    int T, Tk, E, mt;
+};
+struct TileSortLds {
+    int wcnt[SORTF_TK / 64][SORTF_E];  // pairs of expert x in wave w
+    int4 td;       // {expert, first sorted row, rows, first rank within the expert}
+    int nt;        // tiles in the list
+    int rows[16];  // the tile's pairs, in sorted order
+};
+union GuSortLds {
+    TileSortLds tile;
+    SortFastLds fast;
+};
+
+// Tile `tile` of the R-row tile list that sort_small_fast builds (cap = Tk,
+// so nothing is dropped) for pair t's expert e (-1 for none), into sm.td,
+// sm.nt and sm.rows: the same ballot ranks, wave counts and expert scan,
+// with only the tile's own entries kept. Ends with a block barrier.
+static __device__ void tile_of_sort(int e, int Tk, int E, int R, int tile, TileSortLds &sm) {
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int NW = (Tk + 63) >> 6;
+    int *flat = &sm.wcnt[0][0];
+    for (int i = t; i < NW * SORTF_E; i += blockDim.x) flat[i] = 0;
+    if (t == 0) {
+        sm.td = make_int4(0, 0, 0, 0);
+        sm.nt = 0;
+    }
+    __syncthreads();
+    int r = 0;  // stable rank: earlier pairs with the same expert
+    if (wave < NW) {
+        uint64_t m = __ballot(e >= 0);
+        for (int b = 0; (1 << b) < E; b++) {
+            const int bit = (e >> b) & 1;
+            const uint64_t bb = __ballot(bit);
+            m &= bit ? bb : ~bb;
+        }
+        r = __popcll(m & ((1ull << lane) - 1ull));
+        if (e >= 0 && r == 0) sm.wcnt[wave][e] = __popcll(m);
+    }
+    __syncthreads();
+    if (e >= 0)
+        for (int w = 0; w < wave; w++) r += sm.wcnt[w][e];
+    if (wave == 0) {
+        // lane l: experts l*EPL .. l*EPL + EPL - 1 (EPL <= 16; x stays below
+        // SORTF_E, and experts past E count zero)
+        const int EPL = (E + 63) >> 6, x0 = lane * EPL;
+        int ks = 0, ts = 0;
+        for (int u = 0; u < EPL; u++) {
+            const int x = x0 + u;
+            int c = 0;
+#pragma unroll
+            for (int w = 0; w < SORTF_TK / 64; w++) {
+                const int v = sm.wcnt[w][x];
+                c += w < NW ? v : 0;
+            }
+            c = x < E ? c : 0;
+            ks += c;
+            ts += (c + R - 1) / R;
+        }
+        const int kin = wave_incl_scan_i(ks, lane), tin = wave_incl_scan_i(ts, lane);
+        int kbase = kin - ks, tbase = tin - ts;
+        if (tile >= tbase && tile < tin) {  // one lane: its experts hold the tile
+            for (int u = 0; u < EPL; u++) {
+                const int x = x0 + u;
+                int c = 0;
+#pragma unroll
+                for (int w = 0; w < SORTF_TK / 64; w++) {
+                    const int v = sm.wcnt[w][x];
+                    c += w < NW ? v : 0;
+                }
+                c = x < E ? c : 0;
+                const int nt = (c + R - 1) / R;
+                if (tile < tbase + nt) {
+                    const int j = tile - tbase;
+                    sm.td = make_int4(x, kbase + j * R, min(R, c - j * R), j * R);
+                    break;
+                }
+                kbase += c;
+                tbase += nt;
+            }
+        }
+        if (lane == 63) sm.nt = tin;
+    }
+    __syncthreads();
+    const int4 td = sm.td;
+    if (e >= 0 && e == td.x && r >= td.w && r < td.w + td.z) sm.rows[r - td.w] = t;
+    __syncthreads();
+}
+
+template <int G1, bool SORT>
 __global__ __launch_bounds__(64 * RA_WAVES) void k_routed_gu16(
     const int8_t *__restrict__ Xq, const float *__restrict__ sx,
     const int32_t *__restrict__ perm, const int4 *__restrict__ tiles,
     const int32_t *__restrict__ ntiles, int topk, const uint8_t *__restrict__ guP,
     const uint16_t *__restrict__ guS, int64_t gu_pstride, int64_t gu_sstride,
-    float *__restrict__ S, uint32_t *err) {
+    float *__restrict__ S, uint32_t *err, GuSort gs) {
     constexpr int N = 64 * G1;
     constexpr int ASTR = N + 16;
     constexpr int HQ = RF_H / 4;  // hidden channels per quarter (4 h-blocks)
@@ -1702,21 +1812,56 @@ __global__ __launch_bounds__(64 * RA_WAVES) void k_routed_gu16(
     __shared__ __attribute__((aligned(16))) float ub[16 * VSTR];
     __shared__ float rsa[16];
     __shared__ double exp_tab[64];
-    const int tile = blockIdx.x >> 2, quarter = blockIdx.x & 3;
-    const int4 td = tiles[tile];  // {expert, first sorted row, rows}; the grid stays in bounds
-    if (tile >= *ntiles) return;
     const int lane = threadIdx.x & 63;
-    const double tabv = exp_tab_load(lane);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int tile = blockIdx.x >> 2, quarter = blockIdx.x & 3;
+    int4 td;  // {expert, first sorted row, rows}
+    int src[2];  // the wave's two A rows (token indices)
+    if constexpr (SORT) {
+        __shared__ __attribute__((aligned(16))) GuSortLds sl;
+        if ((int)blockIdx.x >= 4 * gs.mt) {
+            if ((int)blockIdx.x == 4 * gs.mt) {  // the sort, into memory
+                const int t = threadIdx.x;
+                int pe = -1;
+                if (t < gs.Tk) {
+                    pe = gs.ids[t];
+                    if (pe < 0 || pe >= gs.E) {
+                        raise_err(err, EF_BAD_ID);
+                        pe = -1;
+                    }
+                }
+                sort_small_fast(pe, gs.Tk, gs.E, (int64_t)gs.Tk, 16, gs.off, NULL, gs.perm, NULL,
+                                NULL, gs.tiles, gs.ntiles, sl.fast);
+            } else {  // token codes, one row a wave
+                const int64_t r = (int64_t)((int)blockIdx.x - 4 * gs.mt - 1) * RA_WAVES + wave;
+                if (r < gs.T) quant_row_wave(gs.X, r, N, gs.Xq, N, gs.sx, err, lane);
+            }
+            return;
+        }
+        int pe = -1;
+        if ((int)threadIdx.x < gs.Tk) {
+            pe = gs.ids[threadIdx.x];
+            if (pe < 0 || pe >= gs.E) pe = -1;  // reported by the sort block
+        }
+        tile_of_sort(pe, gs.Tk, gs.E, 16, tile, sl.tile);
+        if (tile >= sl.tile.nt) return;
+        td = sl.tile.td;
+        if (td.z <= 0) return;
+#pragma unroll
+        for (int j = 0; j < 2; j++) src[j] = sl.tile.rows[min(2 * wave + j, td.z - 1)] / topk;
+    } else {
+        td = tiles[tile];  // the grid stays in bounds
+        if (tile >= *ntiles) return;
+        if (td.z <= 0) return;
+        // scalar loads of the permutation first
+#pragma unroll
+        for (int j = 0; j < 2; j++) src[j] = perm[td.y + min(2 * wave + j, td.z - 1)] / topk;
+    }
+    const double tabv = exp_tab_load(lane);
     const int e = td.x, pos0 = td.y, nrows = td.z;
-    if (nrows <= 0) return;
     const int hl = wave >> 1;             // h-block within the quarter
     const int hb = 4 * quarter + hl;      // h-block within the expert
     const int pan = 2 * hb + (wave & 1);  // gate panel (even wave) or up panel (odd wave)
-    // the wave's two A rows (scalar loads of the permutation first)
-    int src[2];
-#pragma unroll
-    for (int j = 0; j < 2; j++) src[j] = perm[pos0 + min(2 * wave + j, nrows - 1)] / topk;
     // 1. the panel's fp16 scales (G1 * 32 bytes)
     const uint8_t *gsb =
         (const uint8_t *)(guS + (int64_t)e * gu_sstride + (int64_t)pan * G1 * 16);
@@ -1730,16 +1875,27 @@ __global__ __launch_bounds__(64 * RA_WAVES) void k_routed_gu16(
 #pragma unroll
     for (int g = 0; g < GA; g++) rw[g] = *(const uint32_t *)(gw + g * 256 + lane * 4);
     asm volatile("" ::: "memory");
-    // 3. the A rows and their token scales
+    // 3. the A rows and their token scales (with SORT the fp32 rows, G1/4
+    //    float4 a lane each, quantised below)
+    constexpr int XV = SORT ? G1 / 4 : 1;
     uint4 a4[2];
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-        a4[j] = (uint4){0, 0, 0, 0};
-        if (lane < N / 16) a4[j] = *(const uint4 *)(Xq + (int64_t)src[j] * N + lane * 16);
-    }
+    float4 xv[2][XV];
     float sxv = 0.0f;
-    if (lane == 0) sxv = sx[src[0]];
-    if (lane == 1) sxv = sx[src[1]];
+    if constexpr (SORT) {
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int i = 0; i < XV; i++)
+                xv[j][i] = *(const float4 *)(gs.X + (int64_t)src[j] * N + (lane + 64 * i) * 4);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            a4[j] = (uint4){0, 0, 0, 0};
+            if (lane < N / 16) a4[j] = *(const uint4 *)(Xq + (int64_t)src[j] * N + lane * 16);
+        }
+        if (lane == 0) sxv = sx[src[0]];
+        if (lane == 1) sxv = sx[src[1]];
+    }
     asm volatile("" ::: "memory");
     // 4. the other groups
 #pragma unroll
@@ -1748,9 +1904,46 @@ __global__ __launch_bounds__(64 * RA_WAVES) void k_routed_gu16(
         asm volatile("" ::: "memory");
     }
     if (lane < SC16) *(uint4 *)((char *)gus[wave] + lane * 16) = gs4;
+    if constexpr (SORT) {
+        // quant_row_wave's codes and scale for each row (a row that is not
+        // finite or out of range gets zero codes here; the row's quantiser
+        // block reports it)
 #pragma unroll
-    for (int j = 0; j < 2; j++)
-        if (lane < N / 16) *(uint4 *)(As + (2 * wave + j) * ASTR + lane * 16) = a4[j];
+        for (int j = 0; j < 2; j++) {
+            uint32_t mu = 0;
+#pragma unroll
+            for (int i = 0; i < XV; i++) {
+                mu = max(mu, max(abs_bits(xv[j][i].x), abs_bits(xv[j][i].y)));
+                mu = max(mu, max(abs_bits(xv[j][i].z), abs_bits(xv[j][i].w)));
+            }
+            mu = wave_max_u(mu);
+            const QuantParams qp = quant_params(__builtin_bit_cast(float, mu));
+            const bool good = mu < 0x7f800000u && qp.ok;
+            const float inv = quant_inv_f(qp.scale_d);
+#pragma unroll
+            for (int i = 0; i < XV; i++) {
+                const float4 u = xv[j][i];
+                bool f = false;
+                uint32_t b0 = (uint8_t)quant_code_try(u.x, inv, f);
+                uint32_t b1 = (uint8_t)quant_code_try(u.y, inv, f);
+                uint32_t b2 = (uint8_t)quant_code_try(u.z, inv, f);
+                uint32_t b3 = (uint8_t)quant_code_try(u.w, inv, f);
+                if (f && good) {  // rare: the exact quotients
+                    b0 = (uint8_t)quant_code_call(u.x, qp.scale_d);
+                    b1 = (uint8_t)quant_code_call(u.y, qp.scale_d);
+                    b2 = (uint8_t)quant_code_call(u.z, qp.scale_d);
+                    b3 = (uint8_t)quant_code_call(u.w, qp.scale_d);
+                }
+                const uint32_t wd = good ? b0 | (b1 << 8) | (b2 << 16) | (b3 << 24) : 0u;
+                *(uint32_t *)(As + (2 * wave + j) * ASTR + (lane + 64 * i) * 4) = wd;
+            }
+            if (lane == j) sxv = good ? qp.scale_f : 0.0f;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+            if (lane < N / 16) *(uint4 *)(As + (2 * wave + j) * ASTR + lane * 16) = a4[j];
+    }
     if (lane < 2) rsa[2 * wave + lane] = sxv;
     lds_barrier();
     // ---- the panel: rows 4*(lane/16)+i, channel 16*pan + lane%16 ----
@@ -1902,9 +2095,9 @@ extern "C" int jtk_routed_ffn16(const int8_t *Xq, const float *sx, const int32_t
     const int4 *t4 = (const int4 *)tiles;
     if (S) {  // four CUs per tile, two launches (S: the fp32 hidden rows)
 #define RS_LAUNCH(G)                                                                          \
-    hipLaunchKernelGGL(k_routed_gu16<G>, dim3((unsigned)(4 * max_tiles)), dim3(64 * RA_WAVES), 0, \
-                       s, Xq, sx, perm, t4, ntiles, topk, guP, guS, gu_pstride, gu_sstride, S,  \
-                       err);                                                                   \
+    hipLaunchKernelGGL((k_routed_gu16<G, false>), dim3((unsigned)(4 * max_tiles)),           \
+                       dim3(64 * RA_WAVES), 0, s, Xq, sx, perm, t4, ntiles, topk, guP, guS,     \
+                       gu_pstride, gu_sstride, S, err, GuSort{});                              \
     hipLaunchKernelGGL(k_routed_dn16<G>, dim3((unsigned)(4 * max_tiles)), dim3(64 * RF_WAVES), 0, \
                        s, perm, t4, ntiles, S, dnP, dnS, dn_pstride, dn_sstride, Ye, Hq, Hs, err)
         switch (n) {
@@ -1929,6 +2122,47 @@ extern "C" int jtk_routed_ffn16(const int8_t *Xq, const float *sx, const int32_t
     default: return (int)hipErrorInvalidValue;
     }
 #undef RF_LAUNCH
+    return (int)hipGetLastError();
+}
+
+// The caller-routed decode's routed FFN from the caller's ids: the token
+// codes, the pair sort and the gate/up in one launch (k_routed_gu16 with
+// SORT), the down in a second; the outputs are those of
+// jtk_quant_sort_small (cap = Tk, R = 16, no drop flags) followed by
+// jtk_routed_ffn16 with S. Needs Tk <= SORTF_TK, E <= SORTF_E, h = 256,
+// n in {256, 512, 768, 1024} and a 16-byte aligned X; anything else returns
+// hipErrorInvalidValue before launching.
+extern "C" int jtk_routed_ffn16_sort(const float *X, int T, int8_t *Xq, float *sx,
+                                     const int32_t *ids, int Tk, int E, int32_t *off,
+                                     int32_t *perm, int32_t *tiles, int32_t *ntiles, int topk,
+                                     const uint8_t *guP, const uint16_t *guS,
+                                     int64_t gu_pstride, int64_t gu_sstride,
+                                     const uint8_t *dnP, const uint16_t *dnS,
+                                     int64_t dn_pstride, int64_t dn_sstride, int n, int h,
+                                     float *Ye, int8_t *Hq, float *Hs, float *S, uint32_t *err,
+                                     hipStream_t s) {
+    if (T <= 0 || Tk <= 0 || Tk > SORTF_TK || E <= 0 || E > SORTF_E || topk <= 0 ||
+        Tk != T * topk || h != RF_H || ((uintptr_t)X & 15) != 0 || !S)
+        return (int)hipErrorInvalidValue;
+    // tiles: at most Tk / 16 + the experts that hold a pair
+    const int mt = Tk / 16 + (E < Tk ? E : Tk);
+    GuSort gs{X, ids, Xq, sx, off, perm, tiles, ntiles, T, Tk, E, mt};
+    const dim3 grid((unsigned)(4 * mt + 1 + (T + RA_WAVES - 1) / RA_WAVES));
+    const int4 *t4 = (const int4 *)tiles;
+#define RSS_LAUNCH(G)                                                                         \
+    hipLaunchKernelGGL((k_routed_gu16<G, true>), grid, dim3(64 * RA_WAVES), 0, s, nullptr,     \
+                       nullptr, nullptr, nullptr, nullptr, topk, guP, guS, gu_pstride,         \
+                       gu_sstride, S, err, gs);                                                \
+    hipLaunchKernelGGL(k_routed_dn16<G>, dim3((unsigned)(4 * mt)), dim3(64 * RF_WAVES), 0, s, \
+                       perm, t4, ntiles, S, dnP, dnS, dn_pstride, dn_sstride, Ye, Hq, Hs, err)
+    switch (n) {
+    case 256: RSS_LAUNCH(4); break;
+    case 512: RSS_LAUNCH(8); break;
+    case 768: RSS_LAUNCH(12); break;
+    case 1024: RSS_LAUNCH(16); break;
+    default: return (int)hipErrorInvalidValue;
+    }
+#undef RSS_LAUNCH
     return (int)hipGetLastError();
 }
 

@@ -120,6 +120,19 @@ int jtk_routed_ffn16(const int8_t *Xq, const float *sx, const int32_t *perm,
                      int64_t gu_sstride, const uint8_t *dnP, const uint16_t *dnS,
                      int64_t dn_pstride, int64_t dn_sstride, int n, int h, float *Ye,
                      int8_t *Hq, float *Hs, float *S, uint32_t *err, hipStream_t s);
+/* the caller-routed decode's routed FFN from the caller's ids: the outputs
+ * of jtk_quant_sort_small (cap = T*topk, R = 16, no drop flags) and then of
+ * jtk_routed_ffn16 with S, in two launches (the token codes and the sort
+ * ride in the gate/up launch); Tk = T*topk <= 256, E <= 1024, h = 256, n =
+ * 256..1024 in steps of 256, X 16-byte aligned, else hipErrorInvalidValue
+ * before any launch */
+int jtk_routed_ffn16_sort(const float *X, int T, int8_t *Xq, float *sx, const int32_t *ids,
+                          int Tk, int E, int32_t *off, int32_t *perm, int32_t *tiles,
+                          int32_t *ntiles, int topk, const uint8_t *guP, const uint16_t *guS,
+                          int64_t gu_pstride, int64_t gu_sstride, const uint8_t *dnP,
+                          const uint16_t *dnS, int64_t dn_pstride, int64_t dn_sstride, int n,
+                          int h, float *Ye, int8_t *Hq, float *Hs, float *S, uint32_t *err,
+                          hipStream_t s);
 /* decode launches that carry the shared experts' blocks: top-k of T <= 16
  * rows (E <= 1024, k <= 64) and the pair sort / tile list (as
  * jtk_sort_small with cap = T*k; `done` is a zeroed device word the launch

@@ -197,6 +197,65 @@ def test_layer_decode_fused_zipf(jt, orc, torch_cuda, T):
     close(Y, o["Y"])
 
 
+@pytest.mark.parametrize("n,E,k,S,T", [(256, 64, 8, 0, 16), (512, 256, 8, 2, 16),
+                                         (768, 40, 4, 1, 5), (1024, 64, 16, 0, 16),
+                                         (256, 1000, 16, 0, 16), (256, 100, 2, 2, 1),
+                                         (512, 8, 2, 0, 3)],
+                         ids=["n256E64", "n512S2", "n768E40", "n1024Tk256", "n256E1000Tk256",
+                              "n256T1S2", "n512E8"])
+def test_layer_decode_routed_sort_in_gateup(jt, orc, torch_cuda, n, E, k, S, T):
+    """Caller-routed decode with 16-row tiles of f = 256 and at most 256
+    pairs: the token codes and the pair sort run inside the routed gate/up
+    launch. The sort (offsets, permutation), the token codes and scales, the
+    hidden codes, Ye and Y against the oracle, at every model width, with
+    and without shared experts (which read the token codes), up to 256 pairs
+    and 1024 experts, and with experts holding more than 16 pairs."""
+    torch = torch_cuda
+    h, hs = 256, 128
+    announce(f"moe layer decode routed, sort in the gate/up launch: n={n} E={E} k={k} S={S} T={T}")
+    rng = np.random.default_rng(7 * n + E + T)
+    W = mk_weights(rng, n, h, E, S, hs)
+    X = rng.standard_normal((T, n)).astype(np.float32)
+    ids, w = zipf_ids(rng, T, k, E)
+    L, Y = run_layer(jt, torch, n, h, E, k, S, hs, T, W, X, ids, w)
+    o = orc.moe_q(n, h, E, k, S, hs, None, W[1], W[2], W[3], *W[4]).fwd(X, ids, w)
+    assert o["rc"] == 0
+    perm = read_buf(torch, L, jt.BUF_PERM, np.int32, (T * k,))
+    off = read_buf(torch, L, jt.BUF_OFF, np.int32, (E + 1,))
+    assert np.array_equal(off, o["off"]) and np.array_equal(perm, o["perm"])
+    Xq = read_buf(torch, L, jt.BUF_XQ, np.int8, (T, n))
+    sx = read_buf(torch, L, jt.BUF_XSCALE, np.float32, (T,))
+    _, oXq, osx = orc.quant_rows(X)
+    assert np.array_equal(Xq, oXq) and np.array_equal(sx.view(np.uint32), osx.view(np.uint32))
+    check_hidden(jt, L, o, T, k, n, h)
+    Ye = read_buf(torch, L, jt.BUF_YE, np.float32, (T * k, n))
+    close(Ye, o["Ye"])
+    close(Y, o["Y"])
+
+
+def test_layer_decode_routed_bad_id(jt, torch_cuda):
+    """An expert id outside 0..E-1 among the caller's ids (the sort inside
+    the routed gate/up launch) fails the call with the bad-id flag, and the
+    next call with good ids succeeds."""
+    torch = torch_cuda
+    n, h, E, k, S, hs, T = 256, 256, 32, 4, 0, 64, 8
+    announce("moe layer decode routed, bad expert id")
+    rng = np.random.default_rng(99)
+    W = mk_weights(rng, n, h, E, S, hs)
+    Wgate, Wg, Wu, Wd, sh = W
+    L = jt.MoE(n, h, E, k, S, hs, T, dev(torch, Wgate), dev(torch, Wg), dev(torch, Wu),
+               dev(torch, Wd), None, None, None)
+    X = dev(torch, rng.standard_normal((T, n)).astype(np.float32))
+    ids, w = zipf_ids(rng, T, k, E)
+    bad = ids.copy()
+    bad[3, 1] = E
+    Y = torch.zeros((T, n), dtype=torch.float32, device="cuda")
+    rc = L.fwd_routed(X, dev(torch, bad), dev(torch, w), Y)
+    assert rc == 0 and jt.sync_errors() & jt.EF_BAD_ID
+    assert L.fwd_routed(X, dev(torch, ids), dev(torch, w), Y) == 0
+    assert jt.sync_errors() == 0
+
+
 @pytest.mark.parametrize("T", [16, 700])
 def test_layer_stress_widths_zipf(jt, orc, torch_cuda, T):
     """The stress shape's widths (d=2048, f=512, k=8; 128 of its 512 experts
