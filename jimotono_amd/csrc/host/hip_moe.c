@@ -756,7 +756,8 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
     /* 16-row tiles when experts average at most 16 rows; the single-launch
      * sort up to 1024 pairs */
     const int R = Tk <= 16 * E ? 16 : 64;
-    const int max_tiles = Tk / R + E;
+    /* tiles: at most Tk / R plus one per expert that holds a pair */
+    const int max_tiles = Tk / R + (E < Tk ? E : Tk);
     /* Decode with the shared experts concatenated: top-k, the pair sort and
      * the shared gate/up blocks share one launch, the routed FFN and the
      * shared down blocks another (three launches fewer; with profiling each
