@@ -1882,11 +1882,15 @@ __global__ __launch_bounds__(64 * RA_WAVES) void k_routed_gu16(
     float4 xv[2][XV];
     float sxv = 0.0f;
     if constexpr (SORT) {
+        // only the tile's real rows (a decode tile holds one or two): the
+        // padding rows' codes are zero and their outputs are never stored
 #pragma unroll
         for (int j = 0; j < 2; j++)
 #pragma unroll
             for (int i = 0; i < XV; i++)
-                xv[j][i] = *(const float4 *)(gs.X + (int64_t)src[j] * N + (lane + 64 * i) * 4);
+                xv[j][i] = 2 * wave + j < nrows
+                               ? *(const float4 *)(gs.X + (int64_t)src[j] * N + (lane + 64 * i) * 4)
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
     } else {
 #pragma unroll
         for (int j = 0; j < 2; j++) {
