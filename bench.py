@@ -104,6 +104,35 @@ def time_fn(torch, fn, steps, warmup, stream):
     return wall, e0.elapsed_time(e1) / steps
 
 
+def time_graph(torch, fn, calls, reps, stream):
+    """Device time per call (ms) of `calls` back-to-back calls of fn captured
+    into one HIP graph: the replay launches every kernel with no host work
+    between them, so a call that is shorter than its host-side enqueue
+    (ctypes, argument checks, the launch API) is timed by its kernels and the
+    gaps between them alone. fn must only launch kernels (no allocation, no
+    synchronisation); median over reps replays."""
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for _ in range(calls):
+            fn()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        g.replay()  # warm
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            e0.record(stream)
+            g.replay()
+            e1.record(stream)
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1) / calls)
+    del g
+    return sorted(ts)[len(ts) // 2]
+
+
 def spread_fn(torch, fn, n, stream):
     """Median and median absolute deviation (ms) of n single-step times, from
     an event recorded after every step (the reference's methodology,
@@ -445,6 +474,7 @@ def decode_layer(torch, api, stream, steps, warmup):
     # the spread pass first: it also brings the clocks up before the timing
     med, mad = spread_fn(torch, step, 64, stream)
     _, ev = time_fn(torch, step, max(steps, 8) * 4, max(warmup, 2) * 4, stream)
+    gr = time_graph(torch, step, 16, 5, stream)  # four passes over the 4 copies
     assert api.sync_errors(stream) == 0
     # weight bytes one forward reads: the shared experts, the fp32 gate and
     # the routed experts its tokens touch (counted on layer 0's routing)
@@ -459,7 +489,8 @@ def decode_layer(torch, api, stream, steps, warmup):
     return {"us_per_layer": ev * 1e3, "us_median": med * 1e3, "us_mad": mad * 1e3,
             "tokens": T, "touched_experts": touched,
             "weight_bytes": wbytes, "gbps": wbytes / (ev / 1e3) / 1e9,
-            "hbm_frac": wbytes / (ev / 1e3) / HBM_PEAK}
+            "hbm_frac": wbytes / (ev / 1e3) / HBM_PEAK,
+            "graph_us_per_layer": gr * 1e3, "graph_hbm_frac": wbytes / (gr / 1e3) / HBM_PEAK}
 
 
 def sub_benchmarks(np, torch, api, stream, only=None):
@@ -626,15 +657,19 @@ def w8a8_64_bench(np, torch, api, stream):
     Aq = torch.randint(-127, 128, (M, K), generator=g, device="cuda", dtype=torch.int8)
     sA = torch.rand(M, generator=g, device="cuda") * 9e-3 + 1e-3
     Cc = torch.empty(M, N, device="cuda")
-    _, ev = time_fn(torch, lambda: Wq.gemm(Aq, sA, Cc, stream), 200, 20, stream)
+    wall, ev = time_fn(torch, lambda: Wq.gemm(Aq, sA, Cc, stream), 200, 20, stream)
+    gr = time_graph(torch, lambda: Wq.gemm(Aq, sA, Cc, stream), 200, 5, stream)
     nbytes = M * K + N * K + 4 * (M + N) + 4 * M * N
     res["w8a8_gemm_64x1024x1024"] = {"us_per_call": ev * 1e3,
+                                     "host_us_per_call": wall * 1e3,
                                      "tops": 2 * M * N * K / (ev / 1e3) / 1e12,
                                      "mfma_frac": 2 * M * N * K / (ev / 1e3) / INT8_PEAK,
                                      "bytes": nbytes,
                                      "gbps": nbytes / (ev / 1e3) / 1e9,
                                      "hbm_frac": nbytes / (ev / 1e3) / HBM_PEAK,
-                                     "peak_gbps": HBM_PEAK / 1e9}
+                                     "peak_gbps": HBM_PEAK / 1e9,
+                                     "graph_us_per_call": gr * 1e3,
+                                     "graph_hbm_frac": nbytes / (gr / 1e3) / HBM_PEAK}
     del Wq
     return res
 
@@ -661,10 +696,14 @@ def shared_decode_bench(np, torch, api, stream):
             Fs[it[0] % copies].fwd(Xd, Yd, stream)
             it[0] += 1
         _, ev = time_fn(torch, fstep, 4 * copies, copies, stream)
+        gr = time_graph(torch, fstep, copies, 5, stream)  # one call per copy
         res[f"shared_decode_M{m}"] = {"us_per_expert": ev * 1e3,
                                       "gbps": (wbytes + 8 * m * n) / (ev / 1e3) / 1e9,
                                       "hbm_frac": (wbytes + 8 * m * n) / (ev / 1e3) / HBM_PEAK,
-                                      "peak_gbps": HBM_PEAK / 1e9}
+                                      "peak_gbps": HBM_PEAK / 1e9,
+                                      "graph_us_per_expert": gr * 1e3,
+                                      "graph_hbm_frac": (wbytes + 8 * m * n) / (gr / 1e3)
+                                      / HBM_PEAK}
     del Fs
     torch.cuda.empty_cache()
     return res
@@ -696,12 +735,15 @@ def routed_decode_bench(np, torch, api, stream):
         assert rc == 0
         it[0] += 1
     _, ev = time_fn(torch, rstep, 40, 8, stream)
+    gr = time_graph(torch, rstep, 40, 5, stream)  # five passes over the 8 layers
     rbytes = touched * (2 * h * n // 4 + n * h // 2 + 2 * (2 * h * n // 64 + n * h // 64))
     res["routed_decode_T16"] = {"us_per_layer": ev * 1e3, "touched_experts": touched,
                                 "weight_bytes": rbytes,
                                 "gbps": rbytes / (ev / 1e3) / 1e9,
                                 "hbm_frac": rbytes / (ev / 1e3) / HBM_PEAK,
-                                "peak_gbps": HBM_PEAK / 1e9}
+                                "peak_gbps": HBM_PEAK / 1e9,
+                                "graph_us_per_layer": gr * 1e3,
+                                "graph_hbm_frac": rbytes / (gr / 1e3) / HBM_PEAK}
     del layers
     torch.cuda.empty_cache()
     return res
