@@ -202,12 +202,13 @@ def test_device_prepare_from_fp32(jt, orc, torch_cuda):
     assert np.array_equal(bits(out.cpu().numpy()), bits(C2))
 
 
-@pytest.mark.parametrize("N,K", [(4096, 1024), (200, 100), (130, 64)])
+@pytest.mark.parametrize("N,K", [(4096, 1024), (200, 100), (130, 64), (300, 4096)])
 def test_device_projection_fp32_activations(jt, orc, torch_cuda, N, K):
     """The per-token INT8 projection (jt_hip_w8a8_gemm_f32): fp32 rows
     quantised inside the call, bit-identical to quant_rows + the GEMM, for
     the in-block quantiser (M <= 16) and the workspace path (M > 16); K not
-    a multiple of 64 meets the zero-padded weight panels."""
+    a multiple of 64 meets the zero-padded weight panels, K = 4096 the
+    in-block quantiser's longest rows."""
     torch = torch_cuda
     announce(f"device w8a8 projection N={N} K={K}")
     rng = np.random.default_rng(N + K)
@@ -215,7 +216,7 @@ def test_device_projection_fp32_activations(jt, orc, torch_cuda, N, K):
     W = jt.W8A8(W=torch.from_numpy(Wf).cuda())
     _, Qw, sw = orc.quant_rows(Wf)
     ws = None
-    for M in (1, 5, 16, 17, 64, 300):
+    for M in (1, 2, 3, 4, 5, 16, 17, 64, 300):
         X = rng.standard_normal((M, K)).astype(np.float32)
         X[0, : K // 2] *= 50.0
         out = torch.full((M, N), np.nan, device="cuda")
