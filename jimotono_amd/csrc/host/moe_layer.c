@@ -164,7 +164,10 @@ carve:; /* first pass sizes the workspace (base NULL), the second carves it */
     float *Gs = (S && cache_Gs) ? aalloc(&a, (size_t)T * S * h * 4) : NULL;
     float *Us = (S && cache_Us) ? aalloc(&a, (size_t)T * S * h * 4) : NULL;
     float *Wt1 = aalloc(&a, nh * 4), *Wt2 = aalloc(&a, nh * 4);
-    float *dY = aalloc(&a, Tn * 4), *wsbuf = aalloc(&a, (size_t)(n > h ? n : h) * 4);
+    float *dY = aalloc(&a, Tn * 4);
+    /* the batched fake-quant's maxima: a row of every gate/up matrix, or a
+     * column of every down matrix */
+    float *fqws = lbmode == 1 ? aalloc(&a, (size_t)E * (n > h ? n : h) * 4) : NULL;
     w8_ws w8 = {0};
     w8.Aq = aalloc(&a, Mmax * Kpmax);
     w8.Bq = aalloc(&a, (Mmax > (size_t)Npmax ? Mmax : (size_t)Npmax) * Kpmax);
@@ -229,13 +232,19 @@ carve:; /* first pass sizes the workspace (base NULL), the second carves it */
         rc = jt_rt_err(hipErrorLaunchFailure);
         goto out;
     }
-    /* Flags off: every expert's fp32 FFN in two grouped launches (routed, then
-     * shared), with the same arithmetic as the per-expert launches below and
-     * no wait for the expert offsets. Quantised modes keep the reference's
-     * per-expert steps (per-call weight quantisation per expert). */
-    const int grouped = !lbmode && !w8a8_on;
+    /* The routed experts' fp32 FFN in two grouped launches over every expert,
+     * with the same arithmetic as the per-expert launches below and no wait
+     * for the expert offsets: with the flags off, and in the low-bit
+     * fake-quant mode after every touched expert's weights are fake-quantised
+     * in place (their per-call device copies; per gate/up row at 2 bits, per
+     * down column at 4, as the per-expert steps do). The shared experts'
+     * fp32 FFN likewise in two launches unless W8A8 is on. W8A8 and the
+     * T-MAC LUT mode keep the reference's per-expert steps (per-call
+     * quantisation of each expert's weights and activations). */
+    const int rgrouped = lbmode == 0 ? !w8a8_on : lbmode == 1;
+    const int sgrouped = !w8a8_on;
     uint32_t f = 0;
-    if (!grouped) {
+    if (!rgrouped) {
         if ((rc = jt_rt_flags(rt, s, &f)) != JT_OK) goto out;
         if ((rc = jt_rt_flags_to_rc(f)) != JT_OK) goto out;
         if ((rc = jt_rt_d2h(rt, hoff, off64, ((size_t)E + 1) * 8)) != JT_OK) goto out;
@@ -243,16 +252,22 @@ carve:; /* first pass sizes the workspace (base NULL), the second carves it */
     if (cache_Ysel) le |= (int)hipMemsetAsync(Ysel, 0, Tk * n * 4, s);
     if (Gsel) le |= (int)hipMemsetAsync(Gsel, 0, Tk * h * 4, s);
     if (Usel) le |= (int)hipMemsetAsync(Usel, 0, Tk * h * 4, s);
-    if (grouped) {
+    if (rgrouped) {
         le |= jtk_make_tiles(off, E, 16, tiles, ntiles, s);
+        if (lbmode == 1) { /* src/moe_layer.c:1301-1365, lowbit.c:118-139 */
+            le |= jtk_lowbit_fq_rows(dWg, (int64_t)E * h, n, off, h, 2, fqws, err, s);
+            le |= jtk_lowbit_fq_rows(dWu, (int64_t)E * h, n, off, h, 2, fqws, err, s);
+            le |= jtk_lowbit_fq_cols_batch(dWd, E, h, n, off, 4, fqws, err, s);
+        }
         le |= jtk_ffn_f32(dX, T, n, h, perm, k, tiles, ntiles, max_tiles, dWg, dWu, dWd, E, Gsel,
                           Usel, Se, Ysel, 0, err, s);
-        if (S)
-            le |= jtk_ffn_f32(dX, T, n, h, NULL, k, NULL, NULL, 0, dWgs, dWus, dWds, S, Gs, Us,
-                              Ssh, Ys, 1, err, s);
     }
-    /* per-expert forward (src/moe_layer.c:1265-1420) */
-    for (int e = 0; e < E && rc == JT_OK && !grouped; e++) {
+    if (sgrouped && S)
+        le |= jtk_ffn_f32(dX, T, n, h, NULL, k, NULL, NULL, 0, dWgs, dWus, dWds, S, Gs, Us, Ssh,
+                          Ys, 1, err, s);
+    /* per-expert forward (src/moe_layer.c:1265-1420): the T-MAC LUT mode
+     * (lbmode 2) or W8A8 */
+    for (int e = 0; e < E && rc == JT_OK && !rgrouped; e++) {
         const int b0 = (int)hoff[e], Me = (int)(hoff[e + 1] - hoff[e]);
         if (Me == 0) continue;
         const float *wg = dWg + e * nh, *wu = dWu + e * nh, *wd = dWd + e * nh;
@@ -260,58 +275,31 @@ carve:; /* first pass sizes the workspace (base NULL), the second carves it */
         if (lbmode != 0) {
             le |= jtk_transpose_f32(wg, Wt1, h, n, s);
             le |= jtk_transpose_f32(wu, Wt2, h, n, s);
-            if (lbmode == 1) {
-                le |= jtk_lowbit_fq_cols(Wt1, n, h, 2, wsbuf, err, s);
-                le |= jtk_lowbit_fq_cols(Wt2, n, h, 2, wsbuf, err, s);
-                le |= jtk_gemm_f32(Xe, Wt1, Ge, Me, h, n, err, s);
-                le |= jtk_gemm_f32(Xe, Wt2, Ue, Me, h, n, err, s);
-            } else {
-                rc = jt_dev_lowbit_gemm_lut(rt, Xe, Wt1, Ge, Me, h, n, 2);
-                if (rc == JT_OK) rc = jt_dev_lowbit_gemm_lut(rt, Xe, Wt2, Ue, Me, h, n, 2);
-            }
-        } else if (w8a8_on) {
+            rc = jt_dev_lowbit_gemm_lut(rt, Xe, Wt1, Ge, Me, h, n, 2);
+            if (rc == JT_OK) rc = jt_dev_lowbit_gemm_lut(rt, Xe, Wt2, Ue, Me, h, n, 2);
+        } else {
             rc = w8a8_pc(rt, &w8, Xe, wg, Ge, Me, h, n);
             if (rc == JT_OK) rc = w8a8_pc(rt, &w8, Xe, wu, Ue, Me, h, n);
-            if (rc != JT_OK) break; /* nothing more runs on the unfilled rows */
-        } else {
-            le |= jtk_transpose_f32(wg, Wt1, h, n, s);
-            le |= jtk_transpose_f32(wu, Wt2, h, n, s);
-            le |= jtk_gemm_f32(Xe, Wt1, Ge, Me, h, n, err, s);
-            le |= jtk_gemm_f32(Xe, Wt2, Ue, Me, h, n, err, s);
         }
+        if (rc != JT_OK) break; /* nothing more runs on the unfilled rows */
         le |= jtk_silu_tile(Ge, Ue, (int64_t)Me * h, Se, err, s);
-        if (lbmode != 0) {
-            if (lbmode == 1) {
-                le |= (int)hipMemcpyAsync(Wt1, wd, nh * 4, hipMemcpyDeviceToDevice, s);
-                le |= jtk_lowbit_fq_cols(Wt1, h, n, 4, wsbuf, err, s);
-                le |= jtk_gemm_f32(Se, Wt1, Ye, Me, n, h, err, s);
-            } else if (rc == JT_OK) {
-                rc = jt_dev_lowbit_gemm_lut(rt, Se, wd, Ye, Me, n, h, 4);
-            }
-        } else if (w8a8_on) {
-            if (rc == JT_OK) rc = w8a8_pt(rt, &w8, Se, wd, Ye, Me, n, h);
-        } else {
-            le |= jtk_gemm_f32(Se, wd, Ye, Me, n, h, err, s);
-        }
+        if (lbmode != 0)
+            rc = jt_dev_lowbit_gemm_lut(rt, Se, wd, Ye, Me, n, h, 4);
+        else
+            rc = w8a8_pt(rt, &w8, Se, wd, Ye, Me, n, h);
+        if (rc != JT_OK) break;
         le |= jtk_scatter_rows(Ye, n, perm, b0, Me, Ysel, s);
         if (Gsel) le |= jtk_scatter_rows(Ge, h, perm, b0, Me, Gsel, s);
         if (Usel) le |= jtk_scatter_rows(Ue, h, perm, b0, Me, Usel, s);
     }
     if (rc == JT_OK && le) rc = jt_rt_err(hipErrorLaunchFailure);
-    /* shared experts (src/moe_layer.c:1468-1560) */
-    for (int sx = 0; sx < S && rc == JT_OK && !grouped; sx++) {
+    /* shared experts with W8A8 on (src/moe_layer.c:1468-1560) */
+    for (int sx = 0; sx < S && rc == JT_OK && !sgrouped; sx++) {
         const float *wg = dWgs + sx * nh, *wu = dWus + sx * nh, *wd = dWds + sx * nh;
         float *ys = Ys + (size_t)sx * Tn;
-        if (w8a8_on) {
-            rc = w8a8_pc(rt, &w8, dX, wg, Ge, T, h, n);
-            if (rc == JT_OK) rc = w8a8_pc(rt, &w8, dX, wu, Ue, T, h, n);
-            if (rc != JT_OK) break; /* nothing more runs on the unfilled rows */
-        } else {
-            le |= jtk_transpose_f32(wg, Wt1, h, n, s);
-            le |= jtk_transpose_f32(wu, Wt2, h, n, s);
-            le |= jtk_gemm_f32(dX, Wt1, Ge, T, h, n, err, s);
-            le |= jtk_gemm_f32(dX, Wt2, Ue, T, h, n, err, s);
-        }
+        rc = w8a8_pc(rt, &w8, dX, wg, Ge, T, h, n);
+        if (rc == JT_OK) rc = w8a8_pc(rt, &w8, dX, wu, Ue, T, h, n);
+        if (rc != JT_OK) break; /* nothing more runs on the unfilled rows */
         if (Gs) le |= (int)hipMemcpy2DAsync(Gs + (size_t)sx * h, (size_t)S * h * 4, Ge,
                                            (size_t)h * 4, (size_t)h * 4, (size_t)T,
                                            hipMemcpyDeviceToDevice, s);
@@ -319,10 +307,7 @@ carve:; /* first pass sizes the workspace (base NULL), the second carves it */
                                            (size_t)h * 4, (size_t)h * 4, (size_t)T,
                                            hipMemcpyDeviceToDevice, s);
         le |= jtk_silu_tile(Ge, Ue, (int64_t)T * h, Se, err, s);
-        if (rc == JT_OK) {
-            if (w8a8_on) rc = w8a8_pt(rt, &w8, Se, wd, ys, T, n, h);
-            else le |= jtk_gemm_f32(Se, wd, ys, T, n, h, err, s);
-        }
+        rc = w8a8_pt(rt, &w8, Se, wd, ys, T, n, h);
     }
     /* combine (src/moe_layer.c:1443-1463, 1549-1574) */
     if (rc == JT_OK) le |= jtk_combine(w, Ysel, drop, Ys, S, T, k, n, NULL, dY, err, s);
@@ -330,7 +315,7 @@ carve:; /* first pass sizes the workspace (base NULL), the second carves it */
     if (rc != JT_OK) goto out;
     if ((rc = jt_rt_flags(rt, s, &f)) != JT_OK) goto out;
     if ((rc = jt_rt_flags_to_rc(f)) != JT_OK) goto out;
-    if (grouped && (rc = jt_rt_d2h(rt, hoff, off64, ((size_t)E + 1) * 8)) != JT_OK) goto out;
+    if (rgrouped && (rc = jt_rt_d2h(rt, hoff, off64, ((size_t)E + 1) * 8)) != JT_OK) goto out;
     /* commit (fail-closed: nothing above wrote a host output) */
     const size_t kept = (size_t)hoff[E];
     rc = jt_rt_d2h(rt, Y, dY, Tn * 4);

@@ -243,6 +243,15 @@ int jtk_gemm_f64acc(const float *A, const float *B, float *C, int M, int N, int 
                     hipStream_t s);
 int jtk_lowbit_fq_cols(float *W, int k, int h, int bits, float *ws, uint32_t *err,
                        hipStream_t s);
+/* the same fake-quant per row of W [rows][cols] (ws: rows floats), and per
+ * column of each of nb matrices [k][h] stored back to back (ws: nb * h
+ * floats; nb <= 65535); with the expert offsets off (E + 1 entries; rpe
+ * rows, or one matrix, per expert) the experts that hold no pair are left
+ * as they are */
+int jtk_lowbit_fq_rows(float *W, int64_t rows, int cols, const int32_t *off, int rpe, int bits,
+                       float *ws, uint32_t *err, hipStream_t s);
+int jtk_lowbit_fq_cols_batch(float *W, int nb, int k, int h, const int32_t *off, int bits,
+                             float *ws, uint32_t *err, hipStream_t s);
 
 /* moe_bwd.hip: batched MoE backward on the forward's permutation.
  * Device pointers in the reference's argument order (ids, perm, off as

@@ -346,6 +346,127 @@ extern "C" int jtk_lowbit_fq_cols(float *W, int k, int h, int bits, float *ws, u
     return (int)hipGetLastError();
 }
 
+// ---- fake-quant of every expert's weights at once ----
+// The low-bit fake-quant mode of the drop-in layer quantises, per call, each
+// routed expert's gate/up matrix per row (a column of the transposed matrix
+// that the per-expert sequence hands to jtk_lowbit_fq_cols) and its down
+// matrix per column. These two entry points do that for all experts in two
+// launches each, with k_col_maxabs's maximum and k_lowbit_fq_cols's value
+// formula, so every weight comes out as the per-expert sequence's. With the
+// expert offsets off, experts that hold no pair are skipped, as the
+// per-expert sequence skips them (their weights are neither quantised nor
+// checked).
+// Rows of W [rows][cols], one wavefront per row; rpe rows per expert.
+__global__ __launch_bounds__(256) void k_row_maxabs(const float *__restrict__ W, int64_t rows,
+                                                    int cols, const int32_t *__restrict__ off,
+                                                    int rpe, float *__restrict__ ws,
+                                                    uint32_t *err) {
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    if (off && off[r / rpe + 1] == off[r / rpe]) return;
+    const float *w = W + r * cols;
+    float m = 0.0f;
+    int bad = 0;
+    for (int t = lane; t < cols; t += 64) {
+        const float v = w[t];
+        bad |= !isfinite(v);
+        m = fmaxf(m, fabsf(v));
+    }
+    m = wave_max_f(m);
+    bad = wave_or_i(bad);
+    if (lane == 0) {
+        ws[r] = m;
+        if (bad) raise_err(err, EF_NONFINITE_INPUT);
+    }
+}
+
+__global__ __launch_bounds__(256) void k_lowbit_fq_rows(float *__restrict__ W, int64_t rows,
+                                                        int cols, const int32_t *__restrict__ off,
+                                                        int rpe, int bits,
+                                                        const float *__restrict__ ws) {
+    const int64_t id = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (id >= rows * cols) return;
+    const int64_t r = id / cols;
+    if (off && off[r / rpe + 1] == off[r / rpe]) return;
+    const double maxa = (double)ws[r];
+    if (maxa == 0.0) {
+        W[id] = 0.0f;
+        return;
+    }
+    const double nn = (double)((1 << bits) - 1);
+    const int l = lowbit_code((double)W[id], maxa, bits);
+    W[id] = (float)(((2.0 * (double)l - nn) / nn) * maxa);
+}
+
+// every row of W [rows][cols] (ws: rows floats)
+extern "C" int jtk_lowbit_fq_rows(float *W, int64_t rows, int cols, const int32_t *off, int rpe,
+                                  int bits, float *ws, uint32_t *err, hipStream_t s) {
+    if (rows <= 0 || cols <= 0) return 0;
+    if (off && rpe <= 0) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_row_maxabs, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, W, rows,
+                       cols, off, rpe, ws, err);
+    const int64_t th = rows * cols;
+    hipLaunchKernelGGL(k_lowbit_fq_rows, dim3((unsigned)((th + 255) / 256)), dim3(256), 0, s, W,
+                       rows, cols, off, rpe, bits, ws);
+    return (int)hipGetLastError();
+}
+
+// every column of each of nb matrices [k][h] stored back to back (ws: nb * h
+// floats); blockIdx.y is the matrix
+__global__ __launch_bounds__(256) void k_col_maxabs_b(const float *__restrict__ W, int k, int h,
+                                                      const int32_t *__restrict__ off,
+                                                      float *__restrict__ ws, uint32_t *err) {
+    const int j = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (j >= h) return;
+    if (off && off[blockIdx.y + 1] == off[blockIdx.y]) return;
+    const float *w = W + (int64_t)blockIdx.y * k * h;
+    float m = 0.0f;
+    int bad = 0;
+    for (int t = lane; t < k; t += 64) {
+        const float v = w[(int64_t)t * h + j];
+        bad |= !isfinite(v);
+        m = fmaxf(m, fabsf(v));
+    }
+    m = wave_max_f(m);
+    bad = wave_or_i(bad);
+    if (lane == 0) {
+        ws[(int64_t)blockIdx.y * h + j] = m;
+        if (bad) raise_err(err, EF_NONFINITE_INPUT);
+    }
+}
+
+__global__ __launch_bounds__(256) void k_lowbit_fq_cols_b(float *__restrict__ W, int k, int h,
+                                                          const int32_t *__restrict__ off,
+                                                          int bits,
+                                                          const float *__restrict__ ws) {
+    const int64_t id = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (id >= (int64_t)k * h) return;
+    if (off && off[blockIdx.y + 1] == off[blockIdx.y]) return;
+    float *w = W + (int64_t)blockIdx.y * k * h;
+    const double maxa = (double)ws[(int64_t)blockIdx.y * h + id % h];
+    if (maxa == 0.0) {
+        w[id] = 0.0f;
+        return;
+    }
+    const double nn = (double)((1 << bits) - 1);
+    const int l = lowbit_code((double)w[id], maxa, bits);
+    w[id] = (float)(((2.0 * (double)l - nn) / nn) * maxa);
+}
+
+extern "C" int jtk_lowbit_fq_cols_batch(float *W, int nb, int k, int h, const int32_t *off,
+                                        int bits, float *ws, uint32_t *err, hipStream_t s) {
+    if (nb <= 0 || k <= 0 || h <= 0) return 0;
+    if (nb > 65535) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_col_maxabs_b, dim3((unsigned)((h + 3) / 4), (unsigned)nb), dim3(256), 0,
+                       s, W, k, h, off, ws, err);
+    const int64_t th = (int64_t)k * h;
+    hipLaunchKernelGGL(k_lowbit_fq_cols_b, dim3((unsigned)((th + 255) / 256), (unsigned)nb),
+                       dim3(256), 0, s, W, k, h, off, bits, ws);
+    return (int)hipGetLastError();
+}
+
 // Load this file's code object now: the runtime otherwise loads it, and
 // allocates device memory for it, at the first launch of one of its kernels.
 extern "C" int jtk_preload_legacy(void) {
