@@ -178,6 +178,16 @@ carve:; /* first pass sizes the workspace (base NULL), the second carves it */
     w8.sB = aalloc(&a, (size_t)Npmax * 4);
     /* the grouped fp32 path's tile list and shared hidden rows */
     const int max_tiles = (int)(Tk / 16) + E + 1;
+    /* W8A8: every routed expert's steps in a few launches over the tile list
+     * (the launches' grids hold up to 65535 tiles and experts; beyond, the
+     * per-expert steps below): the weights' codes, panels, column scales and
+     * the experts' per-tensor maxima */
+    const int w8b = !lbmode && w8a8_on && max_tiles <= 65535;
+    const int Np16 = (int)jt_round_up((size_t)(n > h ? n : h), 16);
+    int8_t *wq = w8b ? aalloc(&a, (size_t)E * nh) : NULL;
+    int8_t *wpan = w8b ? aalloc(&a, (size_t)E * Np16 * Kpmax) : NULL;
+    float *wsb = w8b ? aalloc(&a, (size_t)E * Np16 * 4) : NULL;
+    uint32_t *wamax = w8b ? aalloc(&a, (size_t)E * 4) : NULL;
     int32_t *tiles = aalloc(&a, (size_t)max_tiles * 16), *ntiles = aalloc(&a, 16);
     float *Ssh = S ? aalloc(&a, (size_t)S * T * h * 4) : NULL;
     if (!a.base) {
@@ -265,9 +275,40 @@ carve:; /* first pass sizes the workspace (base NULL), the second carves it */
     if (sgrouped && S)
         le |= jtk_ffn_f32(dX, T, n, h, NULL, k, NULL, NULL, 0, dWgs, dWus, dWds, S, Gs, Us, Ssh,
                           Ys, 1, err, s);
+    if (w8b && rc == JT_OK) {
+        /* src/moe_layer.c:1265-1420 with the W8A8 steps of :185-274 for
+         * every expert at once: the reference's M <= 4096 limit first */
+        for (int e = 0; e < E; e++)
+            if (hoff[e + 1] - hoff[e] > JT_BWD_MAX_WIDE) {
+                errno = EINVAL;
+                rc = JT_ERR_INVAL;
+                goto out;
+            }
+        const int kept = (int)hoff[E];
+        const int Kpn = (int)jt_round_up((size_t)n, 64), Kph = (int)jt_round_up((size_t)h, 64);
+        const int Nph = (int)jt_round_up((size_t)h, 16), Npn = (int)jt_round_up((size_t)n, 16);
+        uint32_t *ew = err;
+        le |= jtk_make_tiles(off, E, 16, tiles, ntiles, s);
+        le |= jtk_gather_rows(dX, n, perm, 0, k, kept, Xe, s);
+        le |= jtk_quant_tiles(Xe, n, tiles, ntiles, max_tiles, wamax, E, w8.Aq, Kpn, w8.sA, ew, s);
+        le |= jtk_w8a8_weights_e(dWg, E, h, n, 0, off, wq, Nph, Kpn, wpan, wsb, NULL, ew, s);
+        le |= jtk_w8a8_gemm_tiles(w8.Aq, Kpn, w8.sA, wpan, (int64_t)Nph * Kpn, wsb, h, h, Nph,
+                                  Kpn, n, Ge, h, tiles, ntiles, max_tiles, ew, s);
+        le |= jtk_w8a8_weights_e(dWu, E, h, n, 0, off, wq, Nph, Kpn, wpan, wsb, NULL, ew, s);
+        le |= jtk_w8a8_gemm_tiles(w8.Aq, Kpn, w8.sA, wpan, (int64_t)Nph * Kpn, wsb, h, h, Nph,
+                                  Kpn, n, Ue, h, tiles, ntiles, max_tiles, ew, s);
+        le |= jtk_silu_tile(Ge, Ue, (int64_t)kept * h, Se, ew, s);
+        le |= jtk_quant_tiles(Se, h, tiles, ntiles, max_tiles, wamax, E, w8.Aq, Kph, w8.sA, ew, s);
+        le |= jtk_w8a8_weights_e(dWd, E, n, h, 1, off, wq, Npn, Kph, wpan, wsb, wamax, ew, s);
+        le |= jtk_w8a8_gemm_tiles(w8.Aq, Kph, w8.sA, wpan, (int64_t)Npn * Kph, wsb, Npn, n, Npn,
+                                  Kph, h, Ye, n, tiles, ntiles, max_tiles, ew, s);
+        le |= jtk_scatter_rows(Ye, n, perm, 0, kept, Ysel, s);
+        if (Gsel) le |= jtk_scatter_rows(Ge, h, perm, 0, kept, Gsel, s);
+        if (Usel) le |= jtk_scatter_rows(Ue, h, perm, 0, kept, Usel, s);
+    }
     /* per-expert forward (src/moe_layer.c:1265-1420): the T-MAC LUT mode
-     * (lbmode 2) or W8A8 */
-    for (int e = 0; e < E && rc == JT_OK && !rgrouped; e++) {
+     * (lbmode 2), and W8A8 beyond the batched launches' limits */
+    for (int e = 0; e < E && rc == JT_OK && !rgrouped && !w8b; e++) {
         const int b0 = (int)hoff[e], Me = (int)(hoff[e + 1] - hoff[e]);
         if (Me == 0) continue;
         const float *wg = dWg + e * nh, *wu = dWu + e * nh, *wd = dWd + e * nh;

@@ -276,6 +276,40 @@ __global__ __launch_bounds__(64 * SK_WAVES) void k_w8a8_skinny(
                                    N, Kp, K, C, ldc, err, bt);
 }
 
+// Every expert's W8A8 GEMM of the drop-in layer in one launch: block
+// (16-channel panel bx, tile blockIdx.y of the 16-row tile list) runs the
+// skinny kernel's block on the tile's rows of A (codes [row][lda], row scales
+// sA) with its expert's panels P + e pstride and column scales
+// sB + e sbstride, into C [row][ldc]. Same block, same sums and epilogue as
+// the per-expert launches, so the same outputs.
+__global__ __launch_bounds__(64 * SK_WAVES) void k_w8a8_skinny_tiles(
+    const int8_t *__restrict__ A, int lda, const float *__restrict__ sA,
+    const int8_t *__restrict__ P, int64_t pstride, const float *__restrict__ sB,
+    int64_t sbstride, int N, int Kp, int K, float *__restrict__ C, int ldc,
+    const int4 *__restrict__ tiles, const int32_t *__restrict__ ntiles, uint32_t *err) {
+    if ((int)blockIdx.y >= *ntiles) return;  // block-uniform
+    const int4 td = tiles[blockIdx.y];        // {expert, first row, rows}
+    w8a8_skinny_block<EPI_PLAIN, 1, 0>((int)blockIdx.x, 0, A + (int64_t)td.y * lda, lda,
+                                       sA + td.y, P + (int64_t)td.x * pstride,
+                                       sB + (int64_t)td.x * sbstride, td.z, N, Kp, K,
+                                       C + (int64_t)td.y * ldc, ldc, err, SkBatch{});
+}
+
+extern "C" int jtk_w8a8_gemm_tiles(const int8_t *A, int lda, const float *sA, const int8_t *P,
+                                   int64_t pstride, const float *sB, int64_t sbstride, int N,
+                                   int Np, int Kp, int K, float *C, int ldc, const int32_t *tiles,
+                                   const int32_t *ntiles, int max_tiles, uint32_t *err,
+                                   hipStream_t s) {
+    if (max_tiles <= 0) return 0;
+    if (N <= 0 || Np < N || Np % 16 || Kp % 64 || K <= 0 || K > Kp || lda < Kp ||
+        max_tiles > 65535)
+        return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_w8a8_skinny_tiles, dim3((unsigned)(Np / 16), (unsigned)max_tiles),
+                       dim3(64 * SK_WAVES), 0, s, A, lda, sA, P, pstride, sB, sbstride, N, Kp, K,
+                       C, ldc, (const int4 *)tiles, ntiles, err);
+    return (int)hipGetLastError();
+}
+
 template <int QV>
 static hipError_t launch_skinny_xq(const float *X, int ldx, int K, const int8_t *Wp,
                                    const float *sB, int M, int N, int Np, int Kp, float *C,

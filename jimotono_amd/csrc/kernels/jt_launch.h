@@ -47,6 +47,25 @@ int jtk_interleave_rows(const void *A, const void *B, int h, int64_t row_bytes, 
                         hipStream_t s);
 int jtk_quant_weight_rows(const float *W, int64_t ld_n, int64_t ld_k, int N, int K,
                           int8_t *Q, float *scale, uint32_t *err, hipStream_t s);
+/* W8A8 quantisation of every expert at once (experts with off[e + 1] ==
+ * off[e] skipped): the rows of A [row][cols] listed by the 16-row tile
+ * list, per tensor per expert (amax: nexp words, zeroed here) into Q
+ * [row][Kp] and sA [row]; and each expert's weights W [E][N][K] per output
+ * row (kn = 0; sBc [E][N]) or W [E][K][N] per tensor (kn = 1; sBc [E][Np],
+ * amax: E words) through the codes Q [E][N*K] into the panels P [E][Np*Kp] */
+int jtk_quant_tiles(const float *A, int cols, const int32_t *tiles, const int32_t *ntiles,
+                    int max_tiles, uint32_t *amax, int nexp, int8_t *Q, int Kp, float *sA,
+                    uint32_t *err, hipStream_t s);
+int jtk_w8a8_weights_e(const float *W, int E, int N, int K, int kn, const int32_t *off,
+                       int8_t *Q, int Np, int Kp, int8_t *P, float *sBc, uint32_t *amax,
+                       uint32_t *err, hipStream_t s);
+/* every expert's W8A8 GEMM over the 16-row tile list: C [row][ldc] = A
+ * [row][lda] (codes, row scales sA) x the tile's expert's panels
+ * P + e pstride (column scales sB + e sbstride) */
+int jtk_w8a8_gemm_tiles(const int8_t *A, int lda, const float *sA, const int8_t *P,
+                        int64_t pstride, const float *sB, int64_t sbstride, int N, int Np,
+                        int Kp, int K, float *C, int ldc, const int32_t *tiles,
+                        const int32_t *ntiles, int max_tiles, uint32_t *err, hipStream_t s);
 
 /* gemm_i8.hip */
 int jtk_w8a8_gemm(const int8_t *A, int lda, const float *sA, const int8_t *Wp,

@@ -487,6 +487,223 @@ extern "C" int jtk_quant_weight_rows(const float *W, int64_t ld_n, int64_t ld_k,
     return (int)hipGetLastError();
 }
 
+// ---- W8A8 quantisation of every expert at once (the drop-in layer) ----
+// The reference's W8A8 expert steps (src/moe_layer.c:185-274) quantise, per
+// call and per expert, the expert's gathered activation rows per tensor (one
+// scale over its rows) and its weights per output row (gate/up) or per
+// tensor (down). These kernels do that for all experts in a few launches
+// with k_absmax/k_quant_tensor's and k_quant_weight_rows's arithmetic.
+// Experts that hold no pair (off[e + 1] == off[e]) are skipped, as the
+// per-expert steps skip them: their weights are neither quantised nor
+// checked. Activation rows come in the sorted order, one 16-row tile list
+// entry {expert, first row, rows} per block.
+
+// max|x| of each expert's rows of A [row][cols] into amax[expert] (float
+// bits; amax zeroed before)
+__global__ __launch_bounds__(256) void k_absmax_tiles(const float *__restrict__ A, int cols,
+                                                      const int4 *__restrict__ tiles,
+                                                      const int32_t *__restrict__ ntiles,
+                                                      uint32_t *amax, uint32_t *err) {
+    if ((int)blockIdx.x >= *ntiles) return;
+    const int4 td = tiles[blockIdx.x];
+    const float *a = A + (int64_t)td.y * cols;
+    const int64_t n = (int64_t)td.z * cols;
+    float m = 0.0f;
+    int bad = 0;
+    for (int64_t i = threadIdx.x; i < n; i += 256) {
+        const float v = a[i];
+        bad |= !isfinite(v);
+        m = fmaxf(m, fabsf(v));
+    }
+    m = wave_max_f(m);
+    bad = wave_or_i(bad);
+    if ((threadIdx.x & 63) == 0) {
+        atomicMax(amax + td.x, __float_as_uint(m));
+        if (bad) raise_err(err, EF_NONFINITE_INPUT);
+    }
+}
+
+// codes of each tile's rows with their expert's per-tensor scale, into Q
+// [row][Kp] (K padding zero) and the row scales sA [row]
+__global__ __launch_bounds__(256) void k_quant_tiles(const float *__restrict__ A, int cols,
+                                                     const int4 *__restrict__ tiles,
+                                                     const int32_t *__restrict__ ntiles,
+                                                     const uint32_t *__restrict__ amax,
+                                                     int8_t *__restrict__ Q, int Kp,
+                                                     float *__restrict__ sA, uint32_t *err) {
+    if ((int)blockIdx.x >= *ntiles) return;
+    const int4 td = tiles[blockIdx.x];
+    const QuantParams p = quant_params(__uint_as_float(amax[td.x]));
+    if (!p.ok) {
+        if (threadIdx.x == 0) raise_err(err, EF_RANGE);
+        return;
+    }
+    const int64_t n = (int64_t)td.z * Kp;
+    for (int64_t i = threadIdx.x; i < n; i += 256) {
+        const int64_t r = i / Kp;
+        const int c = (int)(i % Kp);
+        const int64_t row = td.y + r;
+        Q[row * Kp + c] = c < cols ? (int8_t)quant_code(A[row * cols + c], p.scale_d) : 0;
+    }
+    if (threadIdx.x < td.z) sA[td.y + threadIdx.x] = p.scale_f;
+}
+
+extern "C" int jtk_quant_tiles(const float *A, int cols, const int32_t *tiles,
+                               const int32_t *ntiles, int max_tiles, uint32_t *amax, int nexp,
+                               int8_t *Q, int Kp, float *sA, uint32_t *err, hipStream_t s) {
+    if (max_tiles <= 0) return 0;
+    if (cols <= 0 || Kp < cols || nexp <= 0) return (int)hipErrorInvalidValue;
+    int e = (int)hipMemsetAsync(amax, 0, (size_t)nexp * sizeof(uint32_t), s);
+    hipLaunchKernelGGL(k_absmax_tiles, dim3((unsigned)max_tiles), dim3(256), 0, s, A, cols,
+                       (const int4 *)tiles, ntiles, amax, err);
+    hipLaunchKernelGGL(k_quant_tiles, dim3((unsigned)max_tiles), dim3(256), 0, s, A, cols,
+                       (const int4 *)tiles, ntiles, amax, Q, Kp, sA, err);
+    return e ? e : (int)hipGetLastError();
+}
+
+// Per-row weight codes of every expert's matrix W [E][N][K] (k_quant_weight_rows's
+// arithmetic), one wavefront per row, into Q [E][N][K] and scale [E][N].
+__global__ __launch_bounds__(256) void k_quant_weight_rows_e(const float *__restrict__ W,
+                                                             int64_t rows, int N, int K,
+                                                             const int32_t *__restrict__ off,
+                                                             int8_t *__restrict__ Q,
+                                                             float *__restrict__ scale,
+                                                             uint32_t *err) {
+    const int lane = threadIdx.x & 63;
+    const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (n >= rows) return;
+    const int64_t ex = n / N;
+    if (off[ex + 1] == off[ex]) return;
+    const float *w = W + n * K;
+    float m = 0.0f;
+    int bad = 0;
+    for (int k = lane; k < K; k += 64) {
+        const float v = w[k];
+        bad |= !isfinite(v);
+        m = fmaxf(m, fabsf(v));
+    }
+    m = wave_max_f(m);
+    bad = wave_or_i(bad);
+    const QuantParams p = quant_params(m);
+    if (bad || !p.ok) {
+        if (lane == 0) raise_err(err, bad ? EF_NONFINITE_INPUT : EF_RANGE);
+        return;
+    }
+    if (lane == 0) scale[n] = p.scale_f;
+    for (int k = lane; k < K; k += 64) Q[n * K + k] = (int8_t)quant_code(w[k], p.scale_d);
+}
+
+// Per-tensor codes of every expert's matrix W [E][nel] (k_absmax /
+// k_quant_tensor's arithmetic): blockIdx.y is the expert. The scale is also
+// broadcast to sBc [E][Np] (the GEMM's per-column scales).
+__global__ __launch_bounds__(256) void k_absmax_mats(const float *__restrict__ W, int64_t nel,
+                                                     const int32_t *__restrict__ off,
+                                                     uint32_t *amax, uint32_t *err) {
+    const int e = blockIdx.y;
+    if (off[e + 1] == off[e]) return;
+    const float *w = W + (int64_t)e * nel;
+    float m = 0.0f;
+    int bad = 0;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nel;
+         i += (int64_t)gridDim.x * 256) {
+        const float v = w[i];
+        bad |= !isfinite(v);
+        m = fmaxf(m, fabsf(v));
+    }
+    m = wave_max_f(m);
+    bad = wave_or_i(bad);
+    if ((threadIdx.x & 63) == 0) {
+        atomicMax(amax + e, __float_as_uint(m));
+        if (bad) raise_err(err, EF_NONFINITE_INPUT);
+    }
+}
+
+__global__ __launch_bounds__(256) void k_quant_mats(const float *__restrict__ W, int64_t nel,
+                                                    const int32_t *__restrict__ off,
+                                                    const uint32_t *__restrict__ amax,
+                                                    int8_t *__restrict__ Q,
+                                                    float *__restrict__ sBc, int Np,
+                                                    uint32_t *err) {
+    const int e = blockIdx.y;
+    if (off[e + 1] == off[e]) return;
+    const QuantParams p = quant_params(__uint_as_float(amax[e]));
+    if (!p.ok) {
+        if (blockIdx.x == 0 && threadIdx.x == 0) raise_err(err, EF_RANGE);
+        return;
+    }
+    if (blockIdx.x == 0)
+        for (int c = threadIdx.x; c < Np; c += 256) sBc[(int64_t)e * Np + c] = p.scale_f;
+    const float *w = W + (int64_t)e * nel;
+    int8_t *q = Q + (int64_t)e * nel;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < nel;
+         i += (int64_t)gridDim.x * 256)
+        q[i] = (int8_t)quant_code(w[i], p.scale_d);
+}
+
+// The MFMA panels of every expert's codes (k_pack_i8 with blockIdx.y the
+// expert): Q [E][N][K] (kn = 0) or [E][K][N] (kn = 1) -> P [E][Np * Kp].
+__global__ __launch_bounds__(256) void k_pack_i8_e(const int8_t *__restrict__ Q, int N, int K,
+                                                   int kn, int Np, int Kp,
+                                                   const int32_t *__restrict__ off,
+                                                   int8_t *__restrict__ P) {
+    const int e = blockIdx.y;
+    if (off[e + 1] == off[e]) return;
+    const int64_t slot = (int64_t)blockIdx.x * 256 + threadIdx.x;  // 16-byte slot
+    const int kblocks = Kp / 64;
+    const int64_t nslots = (int64_t)(Np / 16) * kblocks * 64;
+    if (slot >= nslots) return;
+    const int8_t *q = Q + (int64_t)e * N * K;
+    const int lane = (int)(slot & 63);
+    const int64_t pk = slot >> 6;
+    const int kb = (int)(pk % kblocks);
+    const int pn = (int)(pk / kblocks);
+    const int c = lane & 15, kc = lane >> 4;
+    const int nn = pn * 16 + c;
+    const int k0 = kb * 64 + kc * 16;
+    union {
+        int8_t b[16];
+        v4i v;
+    } u;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const int k = k0 + j;
+        int8_t v = 0;
+        if (nn < N && k < K) v = kn ? q[(int64_t)k * N + nn] : q[(int64_t)nn * K + k];
+        u.b[j] = v;
+    }
+    *(v4i *)(P + (int64_t)e * Np * Kp + slot * 16) = u.v;
+}
+
+// Every touched expert's weights as the W8A8 GEMM's panels: per output row
+// (kn = 0, W [E][N][K]) or per tensor (kn = 1, W [E][K][N], amax: E words),
+// codes through Q [E][N*K], panels into P [E][Np*Kp], per-column scales
+// into sBc [E][Np] (per tensor: the expert's scale in every column).
+extern "C" int jtk_w8a8_weights_e(const float *W, int E, int N, int K, int kn,
+                                  const int32_t *off, int8_t *Q, int Np, int Kp, int8_t *P,
+                                  float *sBc, uint32_t *amax, uint32_t *err, hipStream_t s) {
+    if (E <= 0 || N <= 0 || K <= 0) return 0;
+    if (E > 65535 || Np < N || Kp < K || Np % 16 || Kp % 64) return (int)hipErrorInvalidValue;
+    int e = 0;
+    if (!kn) {
+        const int64_t rows = (int64_t)E * N;
+        hipLaunchKernelGGL(k_quant_weight_rows_e, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+                           s, W, rows, N, K, off, Q, sBc, err);
+        // sBc [E][N] here; the GEMM reads it with stride N per expert
+    } else {
+        const int64_t nel = (int64_t)N * K;
+        e = (int)hipMemsetAsync(amax, 0, (size_t)E * sizeof(uint32_t), s);
+        const unsigned gx = grid_for(nel) > 64 ? 64 : grid_for(nel);
+        hipLaunchKernelGGL(k_absmax_mats, dim3(gx, (unsigned)E), dim3(256), 0, s, W, nel, off,
+                           amax, err);
+        hipLaunchKernelGGL(k_quant_mats, dim3(gx, (unsigned)E), dim3(256), 0, s, W, nel, off,
+                           amax, Q, sBc, Np, err);
+    }
+    const int64_t nslots = (int64_t)(Np / 16) * (Kp / 64) * 64;
+    hipLaunchKernelGGL(k_pack_i8_e, dim3((unsigned)((nslots + 255) / 256), (unsigned)E),
+                       dim3(256), 0, s, Q, N, K, kn, Np, Kp, off, P);
+    return e ? e : (int)hipGetLastError();
+}
+
 // Load this file's code object now: the runtime otherwise loads it, and
 // allocates device memory for it, at the first launch of one of its kernels.
 extern "C" int jtk_preload_quant(void) {
