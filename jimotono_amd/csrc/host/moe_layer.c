@@ -136,6 +136,7 @@ static int fwd_batch(const float *X, const float *Wgate, const float *Wg, const 
     const int Kpmax = (int)jt_round_up((size_t)(n > h ? n : h), 64);
     const int Npmax = (int)jt_round_up((size_t)(n > h ? n : h), 128);
     const size_t Mmax = Tk > (size_t)T ? Tk : (size_t)T;
+    const int32_t soff_h[2] = {0, T}; /* the shared experts' rows as one expert's */
     int rc = JT_OK;
     arena_t a = {.base = NULL, .off = 0};
 carve:; /* first pass sizes the workspace (base NULL), the second carves it */
@@ -188,6 +189,18 @@ carve:; /* first pass sizes the workspace (base NULL), the second carves it */
     int8_t *wpan = w8b ? aalloc(&a, (size_t)E * Np16 * Kpmax) : NULL;
     float *wsb = w8b ? aalloc(&a, (size_t)E * Np16 * 4) : NULL;
     uint32_t *wamax = w8b ? aalloc(&a, (size_t)E * 4) : NULL;
+    /* the shared experts' W8A8 steps likewise (T <= 4096 rows): the token
+     * rows' codes once, their tile list as one expert's */
+    const int w8s = w8a8_on && S > 0 && T <= JT_BWD_MAX_WIDE;
+    const int mts = T / 16 + 2;
+    int8_t *sxq = w8s ? aalloc(&a, (size_t)T * Kpmax) : NULL;
+    float *sxa = w8s ? aalloc(&a, (size_t)T * 4) : NULL;
+    int32_t *soff = w8s ? aalloc(&a, 16) : NULL;
+    int32_t *stiles = w8s ? aalloc(&a, (size_t)mts * 16) : NULL, *snt = w8s ? aalloc(&a, 16) : NULL;
+    int8_t *wq_s = w8s ? aalloc(&a, nh) : NULL;
+    int8_t *wpan_s = w8s ? aalloc(&a, (size_t)Np16 * Kpmax) : NULL;
+    float *wsb_s = w8s ? aalloc(&a, (size_t)Np16 * 4) : NULL;
+    uint32_t *wamax_s = w8s ? aalloc(&a, 16) : NULL;
     int32_t *tiles = aalloc(&a, (size_t)max_tiles * 16), *ntiles = aalloc(&a, 16);
     float *Ssh = S ? aalloc(&a, (size_t)S * T * h * 4) : NULL;
     if (!a.base) {
@@ -335,7 +348,37 @@ carve:; /* first pass sizes the workspace (base NULL), the second carves it */
     }
     if (rc == JT_OK && le) rc = jt_rt_err(hipErrorLaunchFailure);
     /* shared experts with W8A8 on (src/moe_layer.c:1468-1560) */
-    for (int sx = 0; sx < S && rc == JT_OK && !sgrouped; sx++) {
+    if (w8s && rc == JT_OK) {
+        const int Kpn = (int)jt_round_up((size_t)n, 64), Kph = (int)jt_round_up((size_t)h, 64);
+        const int Nph = (int)jt_round_up((size_t)h, 16), Npn = (int)jt_round_up((size_t)n, 16);
+        le |= (int)hipMemcpyAsync(soff, soff_h, sizeof(soff_h), hipMemcpyHostToDevice, s);
+        le |= jtk_make_tiles(soff, 1, 16, stiles, snt, s);
+        le |= jtk_quant_tiles(dX, n, stiles, snt, mts, wamax_s, 1, sxq, Kpn, sxa, err, s);
+        for (int sx = 0; sx < S; sx++) {
+            const float *wg = dWgs + sx * nh, *wu = dWus + sx * nh, *wd = dWds + sx * nh;
+            le |= jtk_w8a8_weights_e(wg, 1, h, n, 0, soff, wq_s, Nph, Kpn, wpan_s, wsb_s, NULL,
+                                     err, s);
+            le |= jtk_w8a8_gemm_tiles(sxq, Kpn, sxa, wpan_s, 0, wsb_s, 0, h, Nph, Kpn, n, Ge, h,
+                                      stiles, snt, mts, err, s);
+            le |= jtk_w8a8_weights_e(wu, 1, h, n, 0, soff, wq_s, Nph, Kpn, wpan_s, wsb_s, NULL,
+                                     err, s);
+            le |= jtk_w8a8_gemm_tiles(sxq, Kpn, sxa, wpan_s, 0, wsb_s, 0, h, Nph, Kpn, n, Ue, h,
+                                      stiles, snt, mts, err, s);
+            if (Gs) le |= (int)hipMemcpy2DAsync(Gs + (size_t)sx * h, (size_t)S * h * 4, Ge,
+                                               (size_t)h * 4, (size_t)h * 4, (size_t)T,
+                                               hipMemcpyDeviceToDevice, s);
+            if (Us) le |= (int)hipMemcpy2DAsync(Us + (size_t)sx * h, (size_t)S * h * 4, Ue,
+                                               (size_t)h * 4, (size_t)h * 4, (size_t)T,
+                                               hipMemcpyDeviceToDevice, s);
+            le |= jtk_silu_tile(Ge, Ue, (int64_t)T * h, Se, err, s);
+            le |= jtk_quant_tiles(Se, h, stiles, snt, mts, wamax_s, 1, w8.Aq, Kph, w8.sA, err, s);
+            le |= jtk_w8a8_weights_e(wd, 1, n, h, 1, soff, wq_s, Npn, Kph, wpan_s, wsb_s, wamax_s,
+                                     err, s);
+            le |= jtk_w8a8_gemm_tiles(w8.Aq, Kph, w8.sA, wpan_s, 0, wsb_s, 0, n, Npn, Kph, h,
+                                      Ys + (size_t)sx * Tn, n, stiles, snt, mts, err, s);
+        }
+    }
+    for (int sx = 0; sx < S && rc == JT_OK && !sgrouped && !w8s; sx++) {
         const float *wg = dWgs + sx * nh, *wu = dWus + sx * nh, *wd = dWds + sx * nh;
         float *ys = Ys + (size_t)sx * Tn;
         rc = w8a8_pc(rt, &w8, dX, wg, Ge, T, h, n);

@@ -128,12 +128,15 @@ def test_batch_sort(jt, orc, cap, T, k, E):
     assert np.array_equal(drop, drop2) and dropped == int(drop2.sum())
 
 
-@pytest.mark.parametrize("shape", [(12, 128, 64, 8, 2, 1), (512, 256, 128, 64, 8, 1)],
-                         ids=["T12", "T512E64k8"])
+@pytest.mark.parametrize("shape", [(12, 128, 64, 8, 2, 1), (512, 256, 128, 64, 8, 1),
+                                   (100, 128, 96, 16, 4, 3)],
+                         ids=["T12", "T512E64k8", "T100h96S3"])
 @pytest.mark.parametrize("w8,lb", [(0, 0), (1, 0), (0, 1), (0, 2), (1, 1)])
 def test_moe_fwd_batch_modes(jt, orc, w8, lb, shape):
-    """The drop-in layer entry in all five flag modes, at a toy shape and at
-    T=512, E=64, k=8 (4096 routed pairs, capacity 1.25 drops some)."""
+    """The drop-in layer entry in all five flag modes, at a toy shape, at
+    T=512, E=64, k=8 (4096 routed pairs, capacity 1.25 drops some), and
+    with three shared experts and h = 96 (not a multiple of 64: the W8A8
+    steps' padded panels)."""
     T, n, h, E, k, S = shape
     announce(f"moe_fwd_batch w8a8={w8} lowbit={lb} T={T} n={n} h={h} E={E} k={k}")
     rng = np.random.default_rng(10 + 3 * w8 + lb + T)
