@@ -189,6 +189,18 @@ carve:; /* first pass sizes the workspace (base NULL), the second carves it */
     int8_t *wpan = w8b ? aalloc(&a, (size_t)E * Np16 * Kpmax) : NULL;
     float *wsb = w8b ? aalloc(&a, (size_t)E * Np16 * 4) : NULL;
     uint32_t *wamax = w8b ? aalloc(&a, (size_t)E * 4) : NULL;
+    /* T-MAC LUT mode: every routed expert's lookup GEMMs in a few launches
+     * when both reductions are multiples of 32 (else the per-expert steps,
+     * whose fp64 fallback takes the other widths): the rows' tables, scales,
+     * biases and sums, the experts' bit-plane indices and column maxima */
+    const int lutb = lbmode == 2 && n % 32 == 0 && h % 32 == 0 && E <= 65535;
+    const size_t nhmax = (size_t)(n > h ? n : h);
+    int8_t *lq = lutb ? aalloc(&a, Mmax * nhmax * 2) : NULL;
+    float *lsc = lutb ? aalloc(&a, Mmax * (nhmax / 32) * 4) : NULL;
+    float *lbi = lutb ? aalloc(&a, Mmax * (nhmax / 32) * 4) : NULL;
+    double *lrs = lutb ? aalloc(&a, Mmax * 8) : NULL;
+    uint8_t *lidx = lutb ? aalloc(&a, (size_t)E * nh) : NULL;
+    float *lws = lutb ? aalloc(&a, (size_t)E * nhmax * 4) : NULL;
     /* the shared experts' W8A8 steps likewise (T <= 4096 rows): the token
      * rows' codes once, their tile list as one expert's */
     const int w8s = w8a8_on && S > 0 && T <= JT_BWD_MAX_WIDE;
@@ -319,9 +331,32 @@ carve:; /* first pass sizes the workspace (base NULL), the second carves it */
         if (Gsel) le |= jtk_scatter_rows(Ge, h, perm, 0, kept, Gsel, s);
         if (Usel) le |= jtk_scatter_rows(Ue, h, perm, 0, kept, Usel, s);
     }
+    if (lutb && rc == JT_OK) {
+        /* src/moe_layer.c:1265-1420 with jt_lowbit_gemm_lut (lowbit.c:158-267)
+         * for every expert at once */
+        const int kept = (int)hoff[E];
+        le |= jtk_gather_rows(dX, n, perm, 0, k, kept, Xe, s);
+        le |= jtk_tmac_ctor(Xe, kept, n, lq, lsc, lbi, err, s);
+        le |= jtk_rowsum_f64(Xe, kept, n, lrs, s);
+        /* gate/up: column j of the transposed [n][h] matrix is row j of W */
+        le |= jtk_col_to_idx_e(dWg, E, n, h, (int64_t)nh, 1, n, off, 2, lws, lidx, err, s);
+        le |= jtk_tmac_gemm_e(lq, lsc, lbi, lrs, lidx, lws, off, E, kept, h, n, 2, Ge, err, s);
+        le |= jtk_col_to_idx_e(dWu, E, n, h, (int64_t)nh, 1, n, off, 2, lws, lidx, err, s);
+        le |= jtk_tmac_gemm_e(lq, lsc, lbi, lrs, lidx, lws, off, E, kept, h, n, 2, Ue, err, s);
+        le |= jtk_silu_tile(Ge, Ue, (int64_t)kept * h, Se, err, s);
+        le |= jtk_tmac_ctor(Se, kept, h, lq, lsc, lbi, err, s);
+        le |= jtk_rowsum_f64(Se, kept, h, lrs, s);
+        /* down: W [h][n] as [k = h][n] */
+        le |= jtk_col_to_idx_e(dWd, E, h, n, (int64_t)nh, n, 1, off, 4, lws, lidx, err, s);
+        le |= jtk_tmac_gemm_e(lq, lsc, lbi, lrs, lidx, lws, off, E, kept, n, h, 4, Ye, err, s);
+        le |= jtk_scatter_rows(Ye, n, perm, 0, kept, Ysel, s);
+        if (Gsel) le |= jtk_scatter_rows(Ge, h, perm, 0, kept, Gsel, s);
+        if (Usel) le |= jtk_scatter_rows(Ue, h, perm, 0, kept, Usel, s);
+    }
     /* per-expert forward (src/moe_layer.c:1265-1420): the T-MAC LUT mode
-     * (lbmode 2), and W8A8 beyond the batched launches' limits */
-    for (int e = 0; e < E && rc == JT_OK && !rgrouped && !w8b; e++) {
+     * (lbmode 2) with other widths, and W8A8 beyond the batched launches'
+     * limits */
+    for (int e = 0; e < E && rc == JT_OK && !rgrouped && !w8b && !lutb; e++) {
         const int b0 = (int)hoff[e], Me = (int)(hoff[e + 1] - hoff[e]);
         if (Me == 0) continue;
         const float *wg = dWg + e * nh, *wu = dWu + e * nh, *wd = dWd + e * nh;

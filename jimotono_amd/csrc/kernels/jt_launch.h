@@ -271,6 +271,17 @@ int jtk_lowbit_fq_rows(float *W, int64_t rows, int cols, const int32_t *off, int
                        float *ws, uint32_t *err, hipStream_t s);
 int jtk_lowbit_fq_cols_batch(float *W, int nb, int k, int h, const int32_t *off, int bits,
                              float *ws, uint32_t *err, hipStream_t s);
+/* the T-MAC LUT GEMM of every expert: the bit-plane indices and maxima of
+ * the columns of each touched expert's matrix (element t of column j at
+ * W[e estride + t tstride + j jstride]; idx [E][h][bits][k/4], ws [E][h]),
+ * and the lookup GEMM of the sorted rows < off[E] with their experts'
+ * columns (k % 32 == 0) */
+int jtk_col_to_idx_e(const float *W, int E, int k, int h, int64_t estride, int64_t tstride,
+                     int64_t jstride, const int32_t *off, int bits, float *ws, uint8_t *idx,
+                     uint32_t *err, hipStream_t s);
+int jtk_tmac_gemm_e(const int8_t *qlut, const float *sc, const float *bi, const double *rowsum,
+                    const uint8_t *idx, const float *ws, const int32_t *off, int E, int rows,
+                    int h, int k, int bits, float *Y, uint32_t *err, hipStream_t s);
 
 /* moe_bwd.hip: batched MoE backward on the forward's permutation.
  * Device pointers in the reference's argument order (ids, perm, off as

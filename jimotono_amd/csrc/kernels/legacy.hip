@@ -467,6 +467,124 @@ extern "C" int jtk_lowbit_fq_cols_batch(float *W, int nb, int k, int h, const in
     return (int)hipGetLastError();
 }
 
+// ---- the T-MAC LUT GEMM of every expert at once (drop-in layer, mode 2) ----
+// jt_dev_lowbit_gemm_lut's steps for all experts: the activation tables and
+// row sums are per row, so they run over every sorted row in one launch
+// each; the weights' bit-plane indices and column maxima come from a strided
+// view of each expert's matrix (element t of column j of expert e at
+// W[e estride + t tstride + j jstride]: the rows of a [h][n] matrix for the
+// transposed gate/up, the columns of [h][n] for the down); the lookup GEMM
+// finds each row's expert from the offsets. Same arithmetic per element as
+// k_col_maxabs, k_col_to_idx and k_tmac_gemm. Experts that hold no pair are
+// skipped (neither indexed nor checked).
+__global__ __launch_bounds__(256) void k_col_maxabs_s(const float *__restrict__ W, int k, int h,
+                                                      int64_t estride, int64_t tstride,
+                                                      int64_t jstride,
+                                                      const int32_t *__restrict__ off,
+                                                      float *__restrict__ ws, uint32_t *err) {
+    const int j = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int e = blockIdx.y;
+    const int lane = threadIdx.x & 63;
+    if (j >= h || off[e + 1] == off[e]) return;
+    const float *w = W + (int64_t)e * estride + (int64_t)j * jstride;
+    float m = 0.0f;
+    int bad = 0;
+    for (int t = lane; t < k; t += 64) {
+        const float v = w[(int64_t)t * tstride];
+        bad |= !isfinite(v);
+        m = fmaxf(m, fabsf(v));
+    }
+    m = wave_max_f(m);
+    bad = wave_or_i(bad);
+    if (lane == 0) {
+        ws[(int64_t)e * h + j] = m;
+        if (bad) raise_err(err, EF_NONFINITE_INPUT);
+    }
+}
+
+__global__ __launch_bounds__(256) void k_col_to_idx_s(const float *__restrict__ W, int k, int h,
+                                                      int64_t estride, int64_t tstride,
+                                                      int64_t jstride,
+                                                      const int32_t *__restrict__ off, int bits,
+                                                      const float *__restrict__ ws,
+                                                      uint8_t *__restrict__ idx) {
+    const int64_t ng = k / 4;
+    const int64_t id = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int e = blockIdx.y;
+    if (id >= (int64_t)h * ng || off[e + 1] == off[e]) return;
+    const int j = (int)(id / ng);
+    const int64_t g = id % ng;
+    const double maxa = (double)ws[(int64_t)e * h + j];
+    const float *w = W + (int64_t)e * estride + (int64_t)j * jstride;
+    int li[4];
+    for (int q = 0; q < 4; q++) li[q] = lowbit_code((double)w[(g * 4 + q) * tstride], maxa, bits);
+    uint8_t *dst = idx + ((int64_t)e * h + j) * bits * ng;
+    for (int b = 0; b < bits; b++) {
+        unsigned p = 0;
+        for (int q = 0; q < 4; q++)
+            if ((li[q] >> b) & 1) p |= 1u << q;
+        dst[(int64_t)b * ng + g] = (uint8_t)p;
+    }
+}
+
+extern "C" int jtk_col_to_idx_e(const float *W, int E, int k, int h, int64_t estride,
+                                int64_t tstride, int64_t jstride, const int32_t *off, int bits,
+                                float *ws, uint8_t *idx, uint32_t *err, hipStream_t s) {
+    if (E <= 0 || k <= 0 || h <= 0) return 0;
+    if (E > 65535 || k % 4) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_col_maxabs_s, dim3((unsigned)((h + 3) / 4), (unsigned)E), dim3(256), 0,
+                       s, W, k, h, estride, tstride, jstride, off, ws, err);
+    const int64_t th = (int64_t)h * (k / 4);
+    hipLaunchKernelGGL(k_col_to_idx_s, dim3((unsigned)((th + 255) / 256), (unsigned)E),
+                       dim3(256), 0, s, W, k, h, estride, tstride, jstride, off, bits, ws, idx);
+    return (int)hipGetLastError();
+}
+
+// Y [row][h] for every sorted row (rows < off[E]); the row's expert e is
+// the one with off[e] <= row < off[e + 1]
+__global__ __launch_bounds__(256) void k_tmac_gemm_e(const int8_t *__restrict__ qlut,
+                                                     const float *__restrict__ sc,
+                                                     const float *__restrict__ bi,
+                                                     const double *__restrict__ rowsum,
+                                                     const uint8_t *__restrict__ idx,
+                                                     const float *__restrict__ ws,
+                                                     const int32_t *__restrict__ off, int E,
+                                                     int rows, int h, int k, int bits,
+                                                     float *__restrict__ Y, uint32_t *err) {
+    const int64_t id = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (id >= (int64_t)rows * h) return;
+    const int m = (int)(id / h), j = (int)(id % h);
+    int lo = 0, hi = E;  // the last e with off[e] <= m (off[0] = 0 <= m)
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (off[mid] <= m) lo = mid;
+        else hi = mid;
+    }
+    const int e = lo;
+    const int64_t ng = k / 4, nb = k / 32;
+    const int64_t col = (int64_t)e * h + j;
+    float o = 0.0f;
+    if (!tmac_dot(qlut + (int64_t)m * ng * 8, idx + col * bits * ng, sc + (int64_t)m * nb,
+                  bi + (int64_t)m * nb, ng, nb, bits, ws[col], &o)) {
+        raise_err(err, EF_RANGE);
+        return;
+    }
+    const double n1 = (double)((1 << bits) - 1);
+    Y[id] = (float)((2.0 * (double)o - n1 * (double)ws[col] * rowsum[m]) / n1);
+}
+
+extern "C" int jtk_tmac_gemm_e(const int8_t *qlut, const float *sc, const float *bi,
+                               const double *rowsum, const uint8_t *idx, const float *ws,
+                               const int32_t *off, int E, int rows, int h, int k, int bits,
+                               float *Y, uint32_t *err, hipStream_t s) {
+    if (rows <= 0) return 0;
+    if (E <= 0 || h <= 0 || k % 32) return (int)hipErrorInvalidValue;
+    const int64_t th = (int64_t)rows * h;
+    hipLaunchKernelGGL(k_tmac_gemm_e, dim3((unsigned)((th + 255) / 256)), dim3(256), 0, s, qlut,
+                       sc, bi, rowsum, idx, ws, off, E, rows, h, k, bits, Y, err);
+    return (int)hipGetLastError();
+}
+
 // Load this file's code object now: the runtime otherwise loads it, and
 // allocates device memory for it, at the first launch of one of its kernels.
 extern "C" int jtk_preload_legacy(void) {
