@@ -49,6 +49,8 @@ typedef struct jt_rt {
     uint32_t *d_scratch; /* small device scratch (reductions) */
     void *slot[JT_NSLOTS];
     size_t slot_bytes[JT_NSLOTS];
+    void *hslot[2]; /* pinned host staging (jt_rt_hbuf) */
+    size_t hslot_bytes[2];
 } jt_rt;
 
 /* Initialise on first use (device 0 unless jt_hip_init chose another).
@@ -70,6 +72,11 @@ int jt_rt_flags(jt_rt *rt, hipStream_t stream, uint32_t *flags);
 /* Map error bits to the reference's return/errno convention
  * (non-finite input or bad code -> EINVAL, computed overflow -> ERANGE). */
 int jt_rt_flags_to_rc(uint32_t flags);
+
+/* Grow-only pinned host buffer `s` (0 or 1) of at least `bytes` bytes, for
+ * host inputs and outputs staged through one copy or one wait: a grown
+ * buffer replaces the old one after the library stream has drained. */
+void *jt_rt_hbuf(jt_rt *rt, int s, size_t bytes, int *rc);
 
 /* host<->device copies on the library stream (synchronous) */
 int jt_rt_h2d(jt_rt *rt, void *dst, const void *src, size_t bytes);

@@ -226,22 +226,30 @@ carve:; /* first pass sizes the workspace (base NULL), the second carves it */
         errno = ENOMEM;
         return JT_ERR_NOMEM;
     }
-    /* inputs in stream order ahead of the kernels (no wait per copy) */
-#define H2D(d, h_, b)                                                                    \
-    if (rc == JT_OK)                                                                     \
-    rc = jt_rt_err(hipMemcpyAsync((d), (h_), (b), hipMemcpyHostToDevice, s))
-    H2D(dX, X, Tn * 4);
-    H2D(dWgate, Wgate, (size_t)E * n * 4);
-    H2D(dWg, Wg, E * nh * 4);
-    H2D(dWu, Wu, E * nh * 4);
-    H2D(dWd, Wd, E * nh * 4);
-    if (S) {
-        H2D(dWgs, Wg_s, S * nh * 4);
-        H2D(dWus, Wu_s, S * nh * 4);
-        H2D(dWds, Wd_s, S * nh * 4);
+    /* The inputs sit at the front of the workspace, in this order: they are
+     * gathered into pinned staging at the same offsets and go over in one
+     * copy, queued ahead of the kernels (the staging is rewritten only by a
+     * later call, after this one has waited for its stream). */
+    {
+        const size_t in_bytes =
+            (size_t)((char *)(S ? dWds + S * nh : dWd + E * nh) - (char *)dX);
+        char *stin = jt_rt_hbuf(rt, 0, in_bytes, &rc);
+        if (!stin) goto out;
+#define STAGE_IN(d, h_, b) memcpy(stin + ((char *)(d) - (char *)dX), (h_), (b))
+        STAGE_IN(dX, X, Tn * 4);
+        STAGE_IN(dWgate, Wgate, (size_t)E * n * 4);
+        STAGE_IN(dWg, Wg, E * nh * 4);
+        STAGE_IN(dWu, Wu, E * nh * 4);
+        STAGE_IN(dWd, Wd, E * nh * 4);
+        if (S) {
+            STAGE_IN(dWgs, Wg_s, S * nh * 4);
+            STAGE_IN(dWus, Wu_s, S * nh * 4);
+            STAGE_IN(dWds, Wd_s, S * nh * 4);
+        }
+#undef STAGE_IN
+        rc = jt_rt_err(hipMemcpyAsync(dX, stin, in_bytes, hipMemcpyHostToDevice, s));
+        if (rc != JT_OK) goto out;
     }
-#undef H2D
-    if (rc != JT_OK) goto out;
     int le = 0;
     if (validate) { /* src/moe_layer.c:1074-1096 */
         le |= jtk_check_finite(dX, (int64_t)Tn, err, s);
@@ -432,22 +440,51 @@ carve:; /* first pass sizes the workspace (base NULL), the second carves it */
     if (rc == JT_OK) le |= jtk_combine(w, Ysel, drop, Ys, S, T, k, n, NULL, dY, err, s);
     if (rc == JT_OK && le) rc = jt_rt_err(hipErrorLaunchFailure);
     if (rc != JT_OK) goto out;
+    /* The outputs go to pinned staging in copies queued behind the kernels;
+     * one wait (the error word's read) covers them all, and only then are
+     * the caller's buffers written (fail-closed: a failed call writes no
+     * host output). */
+    struct {
+        void *dst;
+        const void *src;
+        size_t bytes, at;
+    } oc[12];
+    int no = 0;
+    size_t ob = 0;
+#define STAGE_OUT(d, sp, b)                                                                \
+    if (d) {                                                                               \
+        oc[no].dst = (void *)(d);                                                          \
+        oc[no].src = (sp);                                                                 \
+        oc[no].bytes = (b);                                                                \
+        oc[no].at = ob;                                                                    \
+        ob += jt_round_up((size_t)(b) + 1, 256);                                           \
+        no++;                                                                              \
+    }
+    STAGE_OUT(hoff, off64, ((size_t)E + 1) * 8); /* first: the kept count */
+    STAGE_OUT(Y, dY, Tn * 4);
+    STAGE_OUT(out_ids, ids64, Tk * 8);
+    STAGE_OUT(out_weights, w, Tk * 4);
+    STAGE_OUT(out_perm, perm64, Tk * 8); /* the kept entries are handed over */
+    STAGE_OUT(out_drop, drop, Tk);
+    STAGE_OUT(cache_Ysel, Ysel, Tk * n * 4);
+    STAGE_OUT(cache_Gsel, Gsel, Tk * h * 4);
+    STAGE_OUT(cache_Usel, Usel, Tk * h * 4);
+    if (Gs) STAGE_OUT(cache_Gs, Gs, (size_t)T * S * h * 4);
+    if (Us) STAGE_OUT(cache_Us, Us, (size_t)T * S * h * 4);
+#undef STAGE_OUT
+    char *stout = jt_rt_hbuf(rt, 1, ob, &rc);
+    if (!stout) goto out;
+    for (int i = 0; i < no && rc == JT_OK; i++)
+        rc = jt_rt_err(hipMemcpyAsync(stout + oc[i].at, oc[i].src, oc[i].bytes,
+                                      hipMemcpyDeviceToHost, s));
+    if (rc != JT_OK) goto out;
     if ((rc = jt_rt_flags(rt, s, &f)) != JT_OK) goto out;
     if ((rc = jt_rt_flags_to_rc(f)) != JT_OK) goto out;
-    if (rgrouped && (rc = jt_rt_d2h(rt, hoff, off64, ((size_t)E + 1) * 8)) != JT_OK) goto out;
-    /* commit (fail-closed: nothing above wrote a host output) */
+    memcpy(hoff, stout, ((size_t)E + 1) * 8);
     const size_t kept = (size_t)hoff[E];
-    rc = jt_rt_d2h(rt, Y, dY, Tn * 4);
-    if (rc == JT_OK) rc = jt_rt_d2h(rt, out_ids, ids64, Tk * 8);
-    if (rc == JT_OK) rc = jt_rt_d2h(rt, out_weights, w, Tk * 4);
-    if (rc == JT_OK && out_perm) rc = jt_rt_d2h(rt, out_perm, perm64, kept * 8);
-    if (rc == JT_OK && out_off) memcpy(out_off, hoff, ((size_t)E + 1) * 8);
-    if (rc == JT_OK && out_drop) rc = jt_rt_d2h(rt, out_drop, drop, Tk);
-    if (rc == JT_OK && cache_Ysel) rc = jt_rt_d2h(rt, cache_Ysel, Ysel, Tk * n * 4);
-    if (rc == JT_OK && cache_Gsel) rc = jt_rt_d2h(rt, cache_Gsel, Gsel, Tk * h * 4);
-    if (rc == JT_OK && cache_Usel) rc = jt_rt_d2h(rt, cache_Usel, Usel, Tk * h * 4);
-    if (rc == JT_OK && cache_Gs && Gs) rc = jt_rt_d2h(rt, cache_Gs, Gs, (size_t)T * S * h * 4);
-    if (rc == JT_OK && cache_Us && Us) rc = jt_rt_d2h(rt, cache_Us, Us, (size_t)T * S * h * 4);
+    for (int i = 1; i < no; i++)
+        memcpy(oc[i].dst, stout + oc[i].at, oc[i].dst == out_perm ? kept * 8 : oc[i].bytes);
+    if (out_off) memcpy(out_off, hoff, ((size_t)E + 1) * 8);
     if (rc == JT_OK) {
         if (out_kept) *out_kept = kept;
         if (out_dropped) *out_dropped = Tk - kept;

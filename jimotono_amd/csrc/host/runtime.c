@@ -127,6 +127,26 @@ void *jt_rt_buf(jt_rt *rt, int s, size_t bytes, int *rc) {
     return rt->slot[s];
 }
 
+void *jt_rt_hbuf(jt_rt *rt, int s, size_t bytes, int *rc) {
+    if (bytes == 0) bytes = 16;
+    if (rt->hslot_bytes[s] >= bytes) return rt->hslot[s];
+    if (rt->hslot[s]) {
+        (void)hipStreamSynchronize(rt->stream);
+        (void)hipHostFree(rt->hslot[s]);
+        rt->hslot[s] = NULL;
+        rt->hslot_bytes[s] = 0;
+    }
+    const size_t want = jt_round_up(bytes, 1u << 16);
+    const hipError_t e = hipHostMalloc(&rt->hslot[s], want, hipHostMallocDefault);
+    if (e != hipSuccess) {
+        rt->hslot[s] = NULL;
+        *rc = jt_rt_err(e);
+        return NULL;
+    }
+    rt->hslot_bytes[s] = want;
+    return rt->hslot[s];
+}
+
 uint32_t *jt_rt_errw(jt_rt *rt, hipStream_t stream) {
     pthread_mutex_lock(&g_err_mu);
     int i = 0, freed = -1;
