@@ -230,12 +230,18 @@ carve:; /* first pass sizes the workspace (base NULL), the second carves it */
      * gathered into pinned staging at the same offsets and go over in one
      * copy, queued ahead of the kernels (the staging is rewritten only by a
      * later call, after this one has waited for its stream). */
+    const size_t in_bytes = (size_t)((char *)(S ? dWds + S * nh : dWd + E * nh) - (char *)dX);
     {
-        const size_t in_bytes =
-            (size_t)((char *)(S ? dWds + S * nh : dWd + E * nh) - (char *)dX);
         char *stin = jt_rt_hbuf(rt, 0, in_bytes, &rc);
         if (!stin) goto out;
-#define STAGE_IN(d, h_, b) memcpy(stin + ((char *)(d) - (char *)dX), (h_), (b))
+        size_t at = 0; /* the alignment gaps are zero, so one check covers the region */
+#define STAGE_IN(d, h_, b)                                                                 \
+    do {                                                                                   \
+        const size_t o_ = (size_t)((char *)(d) - (char *)dX);                              \
+        memset(stin + at, 0, o_ - at);                                                     \
+        memcpy(stin + o_, (h_), (b));                                                      \
+        at = o_ + (b);                                                                     \
+    } while (0)
         STAGE_IN(dX, X, Tn * 4);
         STAGE_IN(dWgate, Wgate, (size_t)E * n * 4);
         STAGE_IN(dWg, Wg, E * nh * 4);
@@ -251,18 +257,8 @@ carve:; /* first pass sizes the workspace (base NULL), the second carves it */
         if (rc != JT_OK) goto out;
     }
     int le = 0;
-    if (validate) { /* src/moe_layer.c:1074-1096 */
-        le |= jtk_check_finite(dX, (int64_t)Tn, err, s);
-        le |= jtk_check_finite(dWgate, (int64_t)E * n, err, s);
-        le |= jtk_check_finite(dWg, (int64_t)(E * nh), err, s);
-        le |= jtk_check_finite(dWu, (int64_t)(E * nh), err, s);
-        le |= jtk_check_finite(dWd, (int64_t)(E * nh), err, s);
-        if (S) {
-            le |= jtk_check_finite(dWgs, (int64_t)(S * nh), err, s);
-            le |= jtk_check_finite(dWus, (int64_t)(S * nh), err, s);
-            le |= jtk_check_finite(dWds, (int64_t)(S * nh), err, s);
-        }
-    }
+    if (validate) /* src/moe_layer.c:1074-1096: every input, in one launch */
+        le |= jtk_check_finite(dX, (int64_t)(in_bytes / 4), err, s);
     /* gate logits + top-k (src/moe_layer.c:1114-1156) */
     le |= jtk_router_logits(dX, dWgate, T, E, n, logits, err, s);
     le |= jtk_topk(logits, T, E, k, ids, ids64, w, err, s);

@@ -162,6 +162,29 @@ def test_moe_fwd_batch_modes(jt, orc, w8, lb, shape):
     assert np.array_equal(bits(r["Y"]), bits(ru["Y"]))
 
 
+@pytest.mark.parametrize("which", range(8))
+def test_moe_fwd_batch_rejects_nonfinite(jt, which):
+    """A non-finite value in any one of the eight inputs (X, the gate, the
+    routed and the shared experts' matrices) fails the checked entry with
+    EINVAL and writes no output (src/moe_layer.c:1074-1096); the next call
+    with clean inputs succeeds."""
+    import errno as E_
+    T, n, h, E, k, S = 40, 64, 32, 8, 2, 1
+    announce(f"moe_fwd_batch rejects a non-finite input {which}")
+    rng = np.random.default_rng(700 + which)
+    X = rng.standard_normal((T, n)).astype(np.float32)
+    W = [(rng.standard_normal(s) / 8).astype(np.float32)
+         for s in [(E, n), (E, h, n), (E, h, n), (E, h, n), (S, h, n), (S, h, n), (S, h, n)]]
+    args = [X] + W
+    bad = [a.copy() for a in args]
+    flat = bad[which].reshape(-1)
+    flat[rng.integers(flat.size)] = np.nan if which % 2 else np.inf
+    r = jt.moe_fwd_batch(*bad, k, 1.25)
+    assert r["rc"] == jt.JT_ERR_INVAL and jt.errno() == E_.EINVAL
+    assert not r["Y"].any() and not r["w"].any() and not r["off"].any()
+    assert jt.moe_fwd_batch(*args, k, 1.25)["rc"] == 0
+
+
 def test_moe_fwd_batch_known_answer(jt):
     """bench/kernel/test_moe_layer.c:146-189 through the batched entry."""
     announce("moe_fwd_batch known answer")
