@@ -611,11 +611,28 @@ def dropin_bench(np, torch, api):
         med = float(np.median(ts))
         res[name] = {"ms_per_call": med * 1e3, "tokens_per_s": T / med,
                      "mad_ms": float(np.median(np.abs(np.array(ts) - med))) * 1e3}
+    # the trainer's backward through the drop-in jt_moe_bwd_batch (flags off:
+    # the forward's caches and sort, a random upstream gradient)
+    f = api.moe_fwd_batch(X, *W, k, 1.5, caches=True)
+    assert f["rc"] == 0
+    dY = rng.standard_normal((T, n)).astype(np.float32)
+    bargs = [dY, X, *W, f["ids"], f["w"], f["Gsel"], f["Usel"], f["Ysel"], f["Gs"], f["Us"],
+             f["perm"], f["off"], f["drop"], k]
+    for _ in range(2):
+        assert api.moe_bwd_batch(*bargs)["rc"] == 0
+    ts = []
+    for _ in range(30):
+        t0 = time.perf_counter()
+        assert api.moe_bwd_batch(*bargs)["rc"] == 0
+        ts.append(time.perf_counter() - t0)
+    bmed = float(np.median(ts))
     pcie = 4 * (T * n + E * n + 3 * E * h * n + 3 * S * h * n) + 4 * T * n + 12 * T * k
     return {"dropin_moe_fwd_batch_T512_train": {
         "shape": {"tokens": T, "d_model": n, "expert_ffn": h, "experts": E, "topk": k,
                   "shared": S, "cap_factor": 1.5},
-        "includes_pcie": True, "host_bytes_each_way_per_call": pcie, "modes": res}}
+        "includes_pcie": True, "host_bytes_each_way_per_call": pcie, "modes": res,
+        "bwd_ms_per_call": bmed * 1e3,
+        "bwd_mad_ms": float(np.median(np.abs(np.array(ts) - bmed))) * 1e3}}
 
 
 def vendor_bench(np, torch, api, stream):

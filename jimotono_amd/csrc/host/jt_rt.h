@@ -38,6 +38,7 @@ enum {
     JT_SLOT_O,
     JT_SLOT_P,
     JT_SLOT_LAYER, /* the drop-in layer forward's workspace (host/moe_layer.c) */
+    JT_SLOT_BWD,   /* the drop-in batched backward's workspace (host/moe_bwd.c) */
     JT_NSLOTS
 };
 

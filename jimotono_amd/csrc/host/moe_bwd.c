@@ -84,23 +84,18 @@ int jt_hip_moe_bwd_batch(const float *dY, const float *X, const float *Wgate, co
     return le ? jt_rt_err(hipErrorLaunchFailure) : JT_OK;
 }
 
-/* device allocations of one host-pointer call */
+/* The host-pointer call's device buffers are carved out of one grow-only
+ * workspace kept between calls (sized in a first pass with a NULL base),
+ * 256-byte aligned; a call of the same or a smaller shape allocates
+ * nothing. */
 typedef struct {
-    void *p[40];
-    int n;
-    hipError_t e;
+    char *base;
+    size_t off;
 } bwd_arena;
 
 static void *balloc(bwd_arena *a, size_t bytes) {
-    void *p = NULL;
-    if (a->e != hipSuccess) return NULL;
-    if (a->n >= 40) {
-        a->e = hipErrorOutOfMemory;
-        return NULL;
-    }
-    a->e = hipMalloc(&p, bytes ? bytes : 256);
-    if (a->e != hipSuccess) return NULL;
-    a->p[a->n++] = p;
+    void *p = a->base ? a->base + a->off : NULL;
+    a->off += jt_round_up(bytes ? bytes : 16, 256);
     return p;
 }
 
@@ -126,9 +121,13 @@ static int bwd_host(const float *dY, const float *X, const float *Wgate, const f
     jt_rt *rt = jt_rt_get();
     if (!rt) return JT_ERR_IO;
     hipStream_t s = rt->stream;
-    bwd_arena a = {.n = 0, .e = hipSuccess};
+    int rc = JT_OK;
     const size_t wsb = jtk_bwd_ws_layout(T, n, h, E, k, S, NULL, NULL);
     const size_t sh = (size_t)T * S * h * 4;
+    bwd_arena a = {.base = NULL, .off = 0};
+carve:;
+    /* the inputs first, then the outputs, each group contiguous: one staged
+     * copy each way */
     float *d_dY = balloc(&a, Tn * 4), *d_X = balloc(&a, Tn * 4);
     float *d_Wgate = balloc(&a, (size_t)E * n * 4);
     float *d_Wg = balloc(&a, E * nh * 4), *d_Wu = balloc(&a, E * nh * 4);
@@ -148,52 +147,87 @@ static int bwd_host(const float *dY, const float *X, const float *Wgate, const f
     float *o_dWgs = S ? balloc(&a, S * nh * 4) : NULL, *o_dWus = S ? balloc(&a, S * nh * 4) : NULL;
     float *o_dWds = S ? balloc(&a, S * nh * 4) : NULL;
     float *o_dL = dLogits ? balloc(&a, (size_t)T * E * 4) : NULL;
+    char *o_end = (char *)balloc(&a, 0);
     void *ws = balloc(&a, wsb);
-    int rc = jt_rt_err(a.e);
-#define H2D(d, h_, b) \
-    if (rc == JT_OK) rc = jt_rt_h2d(rt, (d), (h_), (b))
-    H2D(d_dY, dY, Tn * 4);
-    H2D(d_X, X, Tn * 4);
-    H2D(d_Wgate, Wgate, (size_t)E * n * 4);
-    H2D(d_Wg, Wg, E * nh * 4);
-    H2D(d_Wu, Wu, E * nh * 4);
-    H2D(d_Wd, Wd, E * nh * 4);
-    if (S) {
-        H2D(d_Wgs, Wg_s, S * nh * 4);
-        H2D(d_Wus, Wu_s, S * nh * 4);
-        H2D(d_Wds, Wd_s, S * nh * 4);
-        H2D(d_Gs, Gs, sh);
-        H2D(d_Us, Us, sh);
+    if (!a.base) {
+        a.base = jt_rt_buf(rt, JT_SLOT_BWD, a.off, &rc);
+        if (!a.base) return rc;
+        a.off = 0;
+        goto carve;
     }
-    H2D(d_ids, ids, Tk * 8);
-    H2D(d_w, weights, Tk * 4);
-    H2D(d_G, Gsel, Tk * h * 4);
-    H2D(d_U, Usel, Tk * h * 4);
-    H2D(d_Y, Ysel, Tk * n * 4);
-    H2D(d_perm, perm, kept * 8);
-    H2D(d_off, off, ((size_t)E + 1) * 8);
-    H2D(d_drop, drop, Tk);
-#undef H2D
+    /* inputs: gathered into pinned staging at their workspace offsets (gaps
+     * zeroed), one copy queued ahead of the kernels */
+    {
+        const size_t in_bytes = (size_t)((char *)o_dX - (char *)d_dY);
+        char *stin = jt_rt_hbuf(rt, 0, in_bytes, &rc);
+        if (!stin) return rc;
+        size_t at = 0;
+#define STAGE_IN(d, h_, b)                                                                 \
+    do {                                                                                   \
+        if (d) {                                                                           \
+            const size_t o_ = (size_t)((char *)(d) - (char *)d_dY);                        \
+            memset(stin + at, 0, o_ - at);                                                 \
+            memcpy(stin + o_, (h_), (b));                                                  \
+            at = o_ + (b);                                                                 \
+        }                                                                                  \
+    } while (0)
+        STAGE_IN(d_dY, dY, Tn * 4);
+        STAGE_IN(d_X, X, Tn * 4);
+        STAGE_IN(d_Wgate, Wgate, (size_t)E * n * 4);
+        STAGE_IN(d_Wg, Wg, E * nh * 4);
+        STAGE_IN(d_Wu, Wu, E * nh * 4);
+        STAGE_IN(d_Wd, Wd, E * nh * 4);
+        if (S) {
+            STAGE_IN(d_Wgs, Wg_s, S * nh * 4);
+            STAGE_IN(d_Wus, Wu_s, S * nh * 4);
+            STAGE_IN(d_Wds, Wd_s, S * nh * 4);
+        }
+        STAGE_IN(d_ids, ids, Tk * 8);
+        STAGE_IN(d_w, weights, Tk * 4);
+        STAGE_IN(d_G, Gsel, Tk * h * 4);
+        STAGE_IN(d_U, Usel, Tk * h * 4);
+        STAGE_IN(d_Y, Ysel, Tk * n * 4);
+        if (S) {
+            STAGE_IN(d_Gs, Gs, sh);
+            STAGE_IN(d_Us, Us, sh);
+        }
+        STAGE_IN(d_perm, perm, kept * 8);
+        STAGE_IN(d_off, off, ((size_t)E + 1) * 8);
+        STAGE_IN(d_drop, drop, Tk);
+#undef STAGE_IN
+        memset(stin + at, 0, in_bytes - at);
+        rc = jt_rt_err(hipMemcpyAsync(d_dY, stin, in_bytes, hipMemcpyHostToDevice, s));
+    }
     if (rc == JT_OK)
         rc = jt_hip_moe_bwd_batch(d_dY, d_X, d_Wgate, d_Wg, d_Wu, d_Wd, d_Wgs, d_Wus, d_Wds,
                                   d_ids, d_w, d_G, d_U, d_Y, d_Gs, d_Us, d_perm, d_off, d_drop,
                                   o_dX, o_dWgate, o_dWg, o_dWu, o_dWd, o_dWgs, o_dWus, o_dWds,
                                   o_dL, T, n, h, E, k, S, validate, ws, wsb, s);
+    /* outputs: one copy into pinned staging behind the kernels, one wait (the
+     * error word's read), then the caller's buffers (fail-closed: a failed
+     * call writes no host output) */
+    const size_t out_bytes = (size_t)(o_end - (char *)o_dX);
+    char *stout = rc == JT_OK ? jt_rt_hbuf(rt, 1, out_bytes, &rc) : NULL;
+    if (rc == JT_OK)
+        rc = jt_rt_err(hipMemcpyAsync(stout, o_dX, out_bytes, hipMemcpyDeviceToHost, s));
     uint32_t f = 0;
     if (rc == JT_OK) rc = jt_rt_flags(rt, s, &f);
     if (rc == JT_OK) rc = jt_rt_flags_to_rc(f);
-    /* commit (fail-closed: nothing above wrote a host output) */
-    if (rc == JT_OK) rc = jt_rt_d2h(rt, dX, o_dX, Tn * 4);
-    if (rc == JT_OK) rc = jt_rt_d2h(rt, dWgate, o_dWgate, (size_t)E * n * 4);
-    if (rc == JT_OK) rc = jt_rt_d2h(rt, dWg, o_dWg, E * nh * 4);
-    if (rc == JT_OK) rc = jt_rt_d2h(rt, dWu, o_dWu, E * nh * 4);
-    if (rc == JT_OK) rc = jt_rt_d2h(rt, dWd, o_dWd, E * nh * 4);
-    if (rc == JT_OK && S) {
-        rc = jt_rt_d2h(rt, dWg_s, o_dWgs, S * nh * 4);
-        if (rc == JT_OK) rc = jt_rt_d2h(rt, dWu_s, o_dWus, S * nh * 4);
-        if (rc == JT_OK) rc = jt_rt_d2h(rt, dWd_s, o_dWds, S * nh * 4);
+    if (rc == JT_OK) {
+#define TAKE(h_, d, b) memcpy((h_), stout + ((char *)(d) - (char *)o_dX), (b))
+        TAKE(dX, o_dX, Tn * 4);
+        TAKE(dWgate, o_dWgate, (size_t)E * n * 4);
+        TAKE(dWg, o_dWg, E * nh * 4);
+        TAKE(dWu, o_dWu, E * nh * 4);
+        TAKE(dWd, o_dWd, E * nh * 4);
+        if (S) {
+            TAKE(dWg_s, o_dWgs, S * nh * 4);
+            TAKE(dWu_s, o_dWus, S * nh * 4);
+            TAKE(dWd_s, o_dWds, S * nh * 4);
+        }
+        if (dLogits) TAKE(dLogits, o_dL, (size_t)T * E * 4);
+#undef TAKE
     }
-    if (rc == JT_OK && dLogits) rc = jt_rt_d2h(rt, dLogits, o_dL, (size_t)T * E * 4);
     (void)hipStreamSynchronize(s);
     if (rc != JT_OK) {
         /* a failed call reports its own code: flags raised by work it had
@@ -203,7 +237,6 @@ static int bwd_host(const float *dY, const float *X, const float *Wgate, const f
         (void)jt_rt_flags(rt, s, &dropped);
         errno = saved;
     }
-    for (int i = 0; i < a.n; i++) (void)hipFree(a.p[i]);
     return rc;
 }
 
