@@ -723,11 +723,15 @@ __global__ __launch_bounds__(64 * NW) void k_lowbit_gu_q(
     __shared__ float rinv[64];
     __shared__ uint32_t rbad[64];
     __shared__ double exp_tab[64];
-    const int tile = blockIdx.x;
-    // descriptor and tile count in one round trip (the grid never
-    // passes the descriptor array, so the read is in bounds)
+    // blocks go to the 8 XCDs round-robin by index: block b takes tile
+    // (b % 8) * C + b / 8, C an eighth of the tile count, so each XCD works
+    // through a contiguous run of the expert-ordered tile list and the tiles
+    // of one expert read its weights through one L2
+    const int nt = *ntiles;
+    const int chunk = (nt + 7) >> 3, tl = (int)(blockIdx.x >> 3);
+    const int tile = (int)(blockIdx.x & 7) * chunk + tl;
+    if (tl >= chunk || tile >= nt) return;
     const int4 td = ((const int4 *)tiles)[tile];  // {expert, first sorted row, rows}
-    if (tile >= *ntiles) return;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int e = td.x, pos0 = td.y, nrows = td.z;
@@ -888,8 +892,10 @@ static hipError_t launch_gu_q(int lds, int max_tiles, hipStream_t s, const int8_
         if (e != hipSuccess) return e;
         attr_set[dev] = true;
     }
-    hipLaunchKernelGGL(kern, dim3((unsigned)max_tiles), dim3(64 * NW), lds, s, A, lda, sA, perm,
-                       topk, tiles, ntiles, Wp, Ws, wp_stride, ws_stride, K, Sq, ss, h, err);
+    // 8 XCD runs of ceil(max_tiles / 8) tiles
+    hipLaunchKernelGGL(kern, dim3(8u * (unsigned)((max_tiles + 7) / 8)), dim3(64 * NW), lds, s, A,
+                       lda, sA, perm, topk, tiles, ntiles, Wp, Ws, wp_stride, ws_stride, K, Sq, ss,
+                       h, err);
     return hipGetLastError();
 }
 
@@ -1092,23 +1098,29 @@ __global__ __launch_bounds__(256, 2) void k_lowbit_grouped_res(
 // waits once: no per-group ring, so each block pays one memory latency.
 // The fold T = fmaf((float)acc_g, scale_g, T) runs in ascending g, the
 // arithmetic of k_lowbit_grouped_res, so the outputs are identical.
+// Blocks go to the 8 XCDs round-robin by their index: block b works on
+// channel block (b / 8) % ncb of tile (b % 8) * C + (b / 8) / ncb, where C is
+// an eighth of the tile count, so each XCD takes a contiguous run of the
+// expert-ordered tile list and the tiles of one expert read its weights
+// through one L2.
 template <int G, int CPW>
 __global__ __launch_bounds__(256) void k_lowbit_down_rr(
     const int8_t *__restrict__ A, int lda, const float *__restrict__ sA,
     const int32_t *__restrict__ perm, const int4 *__restrict__ tiles,
     const int32_t *__restrict__ ntiles, const uint8_t *__restrict__ Wp,
     const uint16_t *__restrict__ Ws, int64_t wp_stride, int64_t ws_stride,
-    float *__restrict__ out, int ldo, uint32_t *err) {
+    float *__restrict__ out, int ldo, uint32_t *err, int ncb) {
     static_assert((CPW * G * 32) % 256 == 0, "scale copies of 256 bytes");
     __shared__ __attribute__((aligned(1024))) int8_t atile[G * 4 * 1024];  // [g][panel][64 x 16 B]
     __shared__ __attribute__((aligned(16))) uint16_t scl[4][CPW * G * 16];   // per wave [q][g][16]
     __shared__ float rsc[64];
     __shared__ int rdst[64];
-    const int tile = blockIdx.y;
-    // descriptor and tile count in one round trip (the grid never
-    // passes the descriptor array, so the read is in bounds)
+    const int nt = *ntiles;
+    const int chunk = (nt + 7) >> 3, sq = (int)(blockIdx.x >> 3);
+    const int tl = sq / ncb, cblk = sq - tl * ncb;
+    const int tile = (int)(blockIdx.x & 7) * chunk + tl;
+    if (tl >= chunk || tile >= nt) return;
     const int4 td = tiles[tile];  // {expert, first sorted row, rows}
-    if (tile >= *ntiles) return;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int e = td.x, pos0 = td.y, nrows = td.z;
@@ -1121,7 +1133,7 @@ __global__ __launch_bounds__(256) void k_lowbit_down_rr(
         my_sa = sA[r];
         my_dst = perm[r];
     }
-    const int pan0 = (blockIdx.x * 4 + wave) * CPW;
+    const int pan0 = (cblk * 4 + wave) * CPW;
     const uint8_t *wb = Wp + (int64_t)e * wp_stride + (int64_t)pan0 * G * 512;
     uint2 rw[CPW][G];
 #pragma unroll
@@ -2432,14 +2444,17 @@ extern "C" int jtk_lowbit_grouped(int bits, const int8_t *A, int lda, const floa
         // layer at K = 256: 4 panels 0.3525 ms against 2 panels 0.3577; the
         // fewer, longer blocks leave more room to the shared experts)
         const int4 *t4 = (const int4 *)tiles;
+        const int ncb = N / 256;
+        // 8 XCD runs of ceil(max_tiles / 8) tiles x ncb channel blocks
+        const unsigned grid = 8u * (unsigned)(((max_tiles + 7) / 8) * ncb);
         if (K == 256)
-            hipLaunchKernelGGL((k_lowbit_down_rr<4, 4>), dim3((unsigned)(N / 256), (unsigned)max_tiles),
-                               dim3(256), 0, s, A, lda, sA, perm, t4, ntiles, Wp, Ws, wp_stride,
-                               ws_stride, out, ldo, err);
+            hipLaunchKernelGGL((k_lowbit_down_rr<4, 4>), dim3(grid), dim3(256), 0, s, A, lda, sA,
+                               perm, t4, ntiles, Wp, Ws, wp_stride, ws_stride, out, ldo, err,
+                               ncb);
         else
-            hipLaunchKernelGGL((k_lowbit_down_rr<8, 4>), dim3((unsigned)(N / 256), (unsigned)max_tiles),
-                               dim3(256), 0, s, A, lda, sA, perm, t4, ntiles, Wp, Ws, wp_stride,
-                               ws_stride, out, ldo, err);
+            hipLaunchKernelGGL((k_lowbit_down_rr<8, 4>), dim3(grid), dim3(256), 0, s, A, lda, sA,
+                               perm, t4, ntiles, Wp, Ws, wp_stride, ws_stride, out, ldo, err,
+                               ncb);
         return (int)hipGetLastError();
     }
     if (bits == 4 && K <= LBR_KMAX && N % 128 == 0) {

@@ -732,19 +732,11 @@ __global__ __launch_bounds__(1024) void k_sort_mid_place(
             if (off64) off64[E] = ktot;
         }
         if (tiles) {
-            // every expert's whole R-row tiles first, then the partial
-            // ones, so that the blocks dispatched last are the short tiles
-            const int nf = kc / R, np = kc % R ? 1 : 0;
-            int ftot, ptot;
-            const int fbase = block_excl_scan_1024(nf, wsum, &ftot);
-            const int pbase = block_excl_scan_1024(np, wsum, &ptot);
-            if (t < E) {
-                for (int j = 0; j < nf; j++)
-                    ((int4 *)tiles)[fbase + j] = make_int4(t, kbase + j * R, R, 0);
-                if (np)
-                    ((int4 *)tiles)[ftot + pbase] = make_int4(t, kbase + nf * R, kc - nf * R, 0);
-            }
-            if (t == 0) *ntiles = ftot + ptot;
+            const int nt = (kc + R - 1) / R;
+            int ttot;
+            const int tbase = block_excl_scan_1024(nt, wsum, &ttot);
+            if (t < E) put_tiles((int4 *)tiles, tbase, t, kbase, kc, R);
+            if (t == 0) *ntiles = ttot;
         }
     }
     __syncthreads();
