@@ -12,11 +12,15 @@
 // global -> LDS with global_load_lds_dwordx4 into a ring of NST stages filled
 // NST-1 stages ahead; a wave waits only for its own copies of the stage it
 // is about to use and the workgroup then meets at a fence-less barrier.
-// Tile order: when the tile count is a multiple of 8 the blocks are dealt to
-// the 8 XCDs in contiguous chunks, and inside a chunk tiles walk GM
-// row-tiles at a time (all column tiles of a GM-row group before the next
-// group) so the concurrently resident blocks of an XCD share A rows and W
-// columns in its L2.
+// Tile order: blocks are dealt to the 8 XCDs round-robin (block b on XCD
+// b % 8). The tile grid is cut into 8 / cp row parts x cp column parts, one
+// an XCD, with cp in {1, 2, 4, 8} chosen so that an XCD's share of the A rows
+// plus its share of the weight columns is smallest (the gate/up of both
+// shared experts, 32 x 44 tiles at K = 1024: 2 x 4; their down, 32 x 4 tiles
+// at K = 2816: 8 x 1); when no cut divides the grid the tiles go in order.
+// Inside an XCD's share the tiles walk GM row-tiles at a time (all column
+// tiles of a GM-row group before the next group) so its concurrently
+// resident blocks share A rows and W columns in its L2.
 #pragma once
 #include <hip/hip_ext.h>
 #include "jt_dev.h"
@@ -262,10 +266,30 @@ __global__ __launch_bounds__(64 * WGM * WGN * KS) void k_w8a8_tile(
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wg = wave % NWG, kg = wave / NWG;
     const int total = mtiles * ntiles;
-    int pid = blockIdx.x;
-    if ((total & 7) == 0) pid = (pid & 7) * (total >> 3) + (pid >> 3);
+    const int pid = blockIdx.x;
     int mt, nt;
-    tile_coords<GM>(pid, mtiles, ntiles, mt, nt);
+    // the XCD split (8 / cp row parts x cp column parts) whose share of the
+    // A rows and weight columns is smallest
+    int cp = 0;
+    int64_t best = INT64_MAX;
+#pragma unroll
+    for (int c = 1; c <= 8; c *= 2) {
+        const int rp = 8 / c;
+        const int64_t cost = (int64_t)mtiles * BM / rp + (int64_t)ntiles * BN / c;
+        if (mtiles % rp == 0 && ntiles % c == 0 && cost < best) {
+            best = cost;
+            cp = c;
+        }
+    }
+    if (cp) {
+        const int x8 = pid & 7, sm = mtiles / (8 / cp), sn = ntiles / cp;
+        int lm, ln;
+        tile_coords<GM>(pid >> 3, sm, sn, lm, ln);
+        mt = (x8 / cp) * sm + lm;
+        nt = (x8 % cp) * sn + ln;
+    } else {
+        tile_coords<GM>(pid, mtiles, ntiles, mt, nt);
+    }
     const int m0 = mt * BM, n0 = nt * BN;
     const int wm = (wg / WGN) * WTM, wn = (wg % WGN) * WTN;
     const int KB = Kp / 64;
