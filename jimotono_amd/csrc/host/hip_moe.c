@@ -719,6 +719,12 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
     const int small = !d_ids && L->Wgate && T <= 16 && n % 256 == 0 &&
                       (size_t)(T + 4) * (n + 4) * 4 <= 160 * 1024;
     const int fast = !d_ids && !small && L->fast_router;
+    /* the router's codes, bounds and candidates as one launch (16 tokens a
+     * block against every expert), where the exact stage reads candidate
+     * lists (above 256 tokens; up to 256 the verify launch selects from the
+     * bounds in memory itself) */
+    const int front = fast && T > 256 && E % 16 == 0 && k <= 64 &&
+                      (n == 256 || n == 512 || n == 1024) && ((uintptr_t)dX & 15) == 0;
     /* caller-routed decode without a fork: the token codes ride in the sort
      * launch (k_quant_sort_small) */
     const int qsort = d_ids && !L->prof && T * k <= 1024 && E <= 4096 &&
@@ -732,6 +738,9 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
         /* quantised with the sort below */
     } else if (small) /* the codes Xq and all T x E logits (timed as quant_x) */
         le |= jtk_router_logits_small(dX, L->Wgate, T, E, n, L->logits, L->Xq, L->sx, err, s);
+    else if (front) /* codes, approximate logits and candidates in one launch */
+        le |= jtk_router_front(dX, T, n, L->Xq, L->sx, L->xinfo, L->rWh, L->rWl, L->winfo, E, k,
+                               L->rcand, L->rnc, L->logits, err, s);
     else if (fast) /* the expert codes Xq plus the router's residual codes */
         le |= jtk_router_codes(dX, T, n, L->Xq, L->Xl, L->sx, L->xinfo, err, s);
     else
@@ -783,11 +792,16 @@ static int moe_forward(jt_hip_moe *L, const float *dX, const int32_t *d_ids,
         else
             le |= jtk_topk(L->logits, T, E, k, L->ids, NULL, L->w, err, s);
     } else if (fast) {
-        le |= jtk_router_approx(L->Xq, L->Xl, n, L->xinfo, L->rWh, L->rWl, L->winfo, T, E,
-                                L->approx, s);
+        if (!front)
+            le |= jtk_router_approx(L->Xq, L->Xl, n, L->xinfo, L->rWh, L->rWl, L->winfo, T, E,
+                                    L->approx, s);
         prof_mark(L, slot, ST_TOPK, s);
-        le |= jtk_topk_verify(L->approx, L->xinfo, L->winfo, dX, L->Wgate, T, E, n, k, L->rcand,
-                              L->rnc, L->ids, L->w, L->logits, err, fork_late ? 1 : 3, s);
+        /* stage 1 (the candidates) ran in the front launch */
+        const int st1 = front ? 0 : 1;
+        if (st1 || !fork_late)
+            le |= jtk_topk_verify(L->approx, L->xinfo, L->winfo, dX, L->Wgate, T, E, n, k,
+                                  L->rcand, L->rnc, L->ids, L->w, L->logits, err,
+                                  fork_late ? st1 : st1 | 2, s);
         if (fork_late) {
             le |= fork_shared(L, T, fused, err, s);
             le |= jtk_topk_verify(L->approx, L->xinfo, L->winfo, dX, L->Wgate, T, E, n, k,

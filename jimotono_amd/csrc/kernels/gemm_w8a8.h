@@ -265,7 +265,6 @@ __global__ __launch_bounds__(64 * WGM * WGN * KS) void k_w8a8_tile(
     // matters because v_mfma ignores EXEC (an exec-masked MFMA still runs)
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wg = wave % NWG, kg = wave / NWG;
-    const int total = mtiles * ntiles;
     const int pid = blockIdx.x;
     int mt, nt;
     // the XCD split (8 / cp row parts x cp column parts) whose share of the

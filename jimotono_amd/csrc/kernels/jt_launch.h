@@ -181,6 +181,15 @@ int jtk_router_codes(const float *X, int rows, int n, int8_t *qh, int8_t *ql, fl
 int jtk_router_approx(const int8_t *Xh, const int8_t *Xl, int n, const double *xinfo,
                       const int8_t *Wh, const int8_t *Wl, const double *winfo, int T, int E,
                       double *approx, hipStream_t s);
+/* jtk_router_codes, jtk_router_approx and the candidate selection of
+ * jtk_topk_verify (stage 1) in one launch, for E <= 256 with E % 16 == 0 and
+ * n in {256, 512, 1024}: writes qh, sf, info, the candidate lists and the
+ * non-candidates' logits as those three do (the residual codes and the
+ * approximate logits stay on chip). hipErrorInvalidValue (nothing launched)
+ * for another shape. */
+int jtk_router_front(const float *X, int T, int n, int8_t *qh, float *sf, double *info,
+                     const int8_t *Wh, const int8_t *Wl, const double *winfo, int E, int k,
+                     int16_t *cand, int32_t *ncand, float *logits, uint32_t *err, hipStream_t s);
 /* T <= 16: every logit exact in fp64 (all T x E), plus the tokens' int8
  * codes and scales; n % 256 == 0 */
 int jtk_router_logits_small(const float *X, const float *Wg, int T, int E, int n,

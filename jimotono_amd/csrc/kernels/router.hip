@@ -47,6 +47,94 @@ __device__ __forceinline__ uint32_t router_lo_code(float v, int q, double sd, do
     return (uint32_t)(uint8_t)(int8_t)(int)t;
 }
 
+// The codes of one row held whole in registers (n % 4 == 0, n <= 256 RC,
+// x 16-byte aligned), by one wavefront: put(c, hi, lo) receives the 4 codes
+// of float4 c as two words. On success *info = {s, l1} and *scale =
+// (float)s (all lanes); false (error raised) for a row the quantiser
+// rejects, whose codes are then not put.
+template <int RC, typename Put>
+__device__ __forceinline__ bool router_row_regs(const float *__restrict__ x, int n, int lane,
+                                                uint32_t *err, double2 *info, float *scale,
+                                                Put put) {
+    const float4 *x4 = (const float4 *)x;
+    const int n4 = n >> 2;
+    float4 v[RC];
+    float m = 0.0f;
+    double l1 = 0.0;
+    int bad = 0;
+#pragma unroll
+    for (int i = 0; i < RC; i++) {
+        const int c = lane + 64 * i;
+        v[i] = c < n4 ? x4[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int i = 0; i < RC; i++) {
+        if (64 * i < n4) {  // wave-uniform; constant indices keep v[] in registers
+            bad |= (!isfinite(v[i].x)) || (!isfinite(v[i].y)) || (!isfinite(v[i].z)) ||
+                   (!isfinite(v[i].w));
+            m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)),
+                               fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+            l1 += (fabs((double)v[i].x) + fabs((double)v[i].y)) +
+                  (fabs((double)v[i].z) + fabs((double)v[i].w));
+        }
+    }
+    m = wave_max_f(m);
+    bad = wave_or_i(bad);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) l1 += __shfl_xor(l1, o, 64);
+    const QuantParams p = quant_params(m);
+    if (bad || !p.ok) {
+        if (lane == 0) raise_err(err, bad ? EF_NONFINITE_INPUT : EF_RANGE);
+        return false;
+    }
+    *info = make_double2(p.scale_d, l1);
+    *scale = p.scale_f;
+    const float inv = quant_inv_f(p.scale_d);
+    const double inv_lo = p.scale_d != 0.0 ? 254.0 / p.scale_d : 0.0;
+    uint32_t fmask = 0;  // bit i: a code of v[i] needs the exact quotient
+#pragma unroll
+    for (int i = 0; i < RC; i++) {
+        const int c = lane + 64 * i;
+        if (64 * i < n4 && c < n4) {
+            bool f = false;
+            const int q0 = quant_code_try(v[i].x, inv, f);
+            const int q1 = quant_code_try(v[i].y, inv, f);
+            const int q2 = quant_code_try(v[i].z, inv, f);
+            const int q3 = quant_code_try(v[i].w, inv, f);
+            fmask |= (uint32_t)f << i;
+            put(c,
+                (uint32_t)(uint8_t)q0 | ((uint32_t)(uint8_t)q1 << 8) |
+                    ((uint32_t)(uint8_t)q2 << 16) | ((uint32_t)(uint8_t)q3 << 24),
+                router_lo_code(v[i].x, q0, p.scale_d, inv_lo) |
+                    (router_lo_code(v[i].y, q1, p.scale_d, inv_lo) << 8) |
+                    (router_lo_code(v[i].z, q2, p.scale_d, inv_lo) << 16) |
+                    (router_lo_code(v[i].w, q3, p.scale_d, inv_lo) << 24));
+        }
+    }
+    // rare: put those words again, exactly, picking v[j] out of the
+    // registers with selects (a dynamic index would spill v[] to scratch)
+    while (fmask) {
+        const int j = __builtin_ctz(fmask);
+        fmask &= fmask - 1;
+        float4 u = v[0];
+#pragma unroll
+        for (int i = 1; i < RC; i++)
+            if (i == j) u = v[i];
+        const int q0 = quant_code(u.x, p.scale_d);
+        const int q1 = quant_code(u.y, p.scale_d);
+        const int q2 = quant_code(u.z, p.scale_d);
+        const int q3 = quant_code(u.w, p.scale_d);
+        put(lane + 64 * j,
+            (uint32_t)(uint8_t)q0 | ((uint32_t)(uint8_t)q1 << 8) | ((uint32_t)(uint8_t)q2 << 16) |
+                ((uint32_t)(uint8_t)q3 << 24),
+            router_lo_code(u.x, q0, p.scale_d, inv_lo) |
+                (router_lo_code(u.y, q1, p.scale_d, inv_lo) << 8) |
+                (router_lo_code(u.z, q2, p.scale_d, inv_lo) << 16) |
+                (router_lo_code(u.w, q3, p.scale_d, inv_lo) << 24));
+    }
+    return true;
+}
+
 template <int RC_REG>
 __global__ __launch_bounds__(256) void k_router_codes(const float *__restrict__ X, int rows,
                                                       int n, int8_t *__restrict__ qh,
@@ -64,81 +152,18 @@ __global__ __launch_bounds__(256) void k_router_codes(const float *__restrict__ 
     const bool vec = (n & 3) == 0 && ((uintptr_t)x & 15) == 0 &&
                      (((uintptr_t)qh | (uintptr_t)ql) & 3) == 0;
     if (vec && n <= 64 * 4 * RC_REG) {
-        const float4 *x4 = (const float4 *)x;
-        const int n4 = n >> 2;
-        float4 v[RC_REG];
-#pragma unroll
-        for (int i = 0; i < RC_REG; i++) {
-            const int c = lane + 64 * i;
-            v[i] = c < n4 ? x4[c] : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-#pragma unroll
-        for (int i = 0; i < RC_REG; i++) {
-            if (64 * i < n4) {  // wave-uniform; constant indices keep v[] in registers
-                bad |= (!isfinite(v[i].x)) || (!isfinite(v[i].y)) || (!isfinite(v[i].z)) ||
-                       (!isfinite(v[i].w));
-                m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)),
-                                   fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
-                l1 += (fabs((double)v[i].x) + fabs((double)v[i].y)) +
-                      (fabs((double)v[i].z) + fabs((double)v[i].w));
-            }
-        }
-        m = wave_max_f(m);
-        bad = wave_or_i(bad);
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) l1 += __shfl_xor(l1, o, 64);
-        const QuantParams p = quant_params(m);
-        if (bad || !p.ok) {
-            if (lane == 0) raise_err(err, bad ? EF_NONFINITE_INPUT : EF_RANGE);
-            return;
-        }
-        if (lane == 0) {
-            if (sf) sf[r] = p.scale_f;
-            info[r] = make_double2(p.scale_d, l1);
-        }
-        const float inv = quant_inv_f(p.scale_d);
-        const double inv_lo = p.scale_d != 0.0 ? 254.0 / p.scale_d : 0.0;
         uint32_t *qh4 = (uint32_t *)(qh + (int64_t)r * n);
         uint32_t *ql4 = (uint32_t *)(ql + (int64_t)r * n);
-        uint32_t fmask = 0;  // bit i: a code of v[i] needs the exact quotient
-#pragma unroll
-        for (int i = 0; i < RC_REG; i++) {
-            const int c = lane + 64 * i;
-            if (64 * i < n4 && c < n4) {
-                bool f = false;
-                const int q0 = quant_code_try(v[i].x, inv, f);
-                const int q1 = quant_code_try(v[i].y, inv, f);
-                const int q2 = quant_code_try(v[i].z, inv, f);
-                const int q3 = quant_code_try(v[i].w, inv, f);
-                fmask |= (uint32_t)f << i;
-                qh4[c] = (uint32_t)(uint8_t)q0 | ((uint32_t)(uint8_t)q1 << 8) |
-                         ((uint32_t)(uint8_t)q2 << 16) | ((uint32_t)(uint8_t)q3 << 24);
-                ql4[c] = router_lo_code(v[i].x, q0, p.scale_d, inv_lo) |
-                         (router_lo_code(v[i].y, q1, p.scale_d, inv_lo) << 8) |
-                         (router_lo_code(v[i].z, q2, p.scale_d, inv_lo) << 16) |
-                         (router_lo_code(v[i].w, q3, p.scale_d, inv_lo) << 24);
-            }
-        }
-        // rare: rewrite those words exactly, picking v[j] out of the
-        // registers with selects (a dynamic index would spill v[] to scratch)
-        while (fmask) {
-            const int j = __builtin_ctz(fmask);
-            fmask &= fmask - 1;
-            float4 u = v[0];
-#pragma unroll
-            for (int i = 1; i < RC_REG; i++)
-                if (i == j) u = v[i];
-            const int q0 = quant_code(u.x, p.scale_d);
-            const int q1 = quant_code(u.y, p.scale_d);
-            const int q2 = quant_code(u.z, p.scale_d);
-            const int q3 = quant_code(u.w, p.scale_d);
-            const int c = lane + 64 * j;
-            qh4[c] = (uint32_t)(uint8_t)q0 | ((uint32_t)(uint8_t)q1 << 8) |
-                     ((uint32_t)(uint8_t)q2 << 16) | ((uint32_t)(uint8_t)q3 << 24);
-            ql4[c] = router_lo_code(u.x, q0, p.scale_d, inv_lo) |
-                     (router_lo_code(u.y, q1, p.scale_d, inv_lo) << 8) |
-                     (router_lo_code(u.z, q2, p.scale_d, inv_lo) << 16) |
-                     (router_lo_code(u.w, q3, p.scale_d, inv_lo) << 24);
+        double2 inf;
+        float scl;
+        if (router_row_regs<RC_REG>(x, n, lane, err, &inf, &scl,
+                                    [&](int c, uint32_t h, uint32_t l) {
+                                        qh4[c] = h;
+                                        ql4[c] = l;
+                                    }) &&
+            lane == 0) {
+            if (sf) sf[r] = scl;
+            info[r] = inf;
         }
         return;
     }
@@ -418,13 +443,13 @@ __device__ __forceinline__ float float_rd(double d) {
 // The candidates of token t into cand[0..nc) (ascending expert order) and
 // the float of the approximation into the logits of the others; returns nc
 // (wave-uniform). Called by one whole wavefront.
-__device__ __forceinline__ int select_token(const double *__restrict__ approx,
-                                            const double2 *__restrict__ xinfo,
-                                            const double2 *__restrict__ winfo, int t, int E,
-                                            int n, int k, int lane, int16_t *cand,
-                                            float *__restrict__ logits) {
+// select_token on one row: ap = the token's E approximate logits (global
+// memory or LDS), {sx, l1x} its row info, cand / lg its rows of the candidate
+// list and of the logits.
+__device__ __forceinline__ int select_row(const double *ap_row, double sx, double l1x,
+                                          const double2 *__restrict__ winfo, int E, int n,
+                                          int k, int lane, int16_t *cand, float *lg) {
     constexpr int EPL = RV_EMAX / 64;
-    const double sx = xinfo[t].x, l1x = xinfo[t].y;
     const double ux = sx * (1.0 / 508.0);
     double ap[EPL], hi[EPL];
     uint32_t kmax = 0;  // below every real key
@@ -434,7 +459,7 @@ __device__ __forceinline__ int select_token(const double *__restrict__ approx,
         ap[j] = 0.0;
         hi[j] = -__builtin_inf();
         if (e < E) {
-            const double a = approx[(int64_t)t * E + e];
+            const double a = ap_row[e];
             const double sw = winfo[e].x, l1w = winfo[e].y;
             const double uw = sw * (1.0 / 508.0);
             double m = uw * l1x + ux * l1w + 3.0 * n * ux * uw;
@@ -460,10 +485,18 @@ __device__ __forceinline__ int select_token(const double *__restrict__ approx,
         const bool c = e < E && hi[j] >= cut;
         const uint64_t mask = __ballot(c);
         if (c) cand[nc + __popcll(mask & ((1ull << lane) - 1ull))] = (int16_t)e;
-        else if (e < E) logits[(int64_t)t * E + e] = (float)ap[j];
+        else if (e < E) lg[e] = (float)ap[j];
         nc += __popcll(mask);
     }
     return nc;
+}
+__device__ __forceinline__ int select_token(const double *__restrict__ approx,
+                                            const double2 *__restrict__ xinfo,
+                                            const double2 *__restrict__ winfo, int t, int E,
+                                            int n, int k, int lane, int16_t *cand,
+                                            float *__restrict__ logits) {
+    return select_row(approx + (int64_t)t * E, xinfo[t].x, xinfo[t].y, winfo, E, n, k, lane,
+                      cand, logits + (int64_t)t * E);
 }
 
 __global__ __launch_bounds__(64 * RV_WPB) void k_router_select(
@@ -476,6 +509,162 @@ __global__ __launch_bounds__(64 * RV_WPB) void k_router_select(
     const int nc =
         select_token(approx, xinfo, winfo, t, E, n, k, lane, cand + (int64_t)t * E, logits);
     if (lane == 0) ncand[t] = nc;
+}
+
+// ---- 1-3 in one launch: codes, approximate logits and candidates ----
+// Block = RF_TOK = 16 tokens x every expert (E <= 256, E % 16 == 0, n = 64 KB
+// with KB <= 16), 16 waves. Wave w writes the codes of token row w as
+// k_router_codes does (qh, the row scale and {s, l1}; the residual codes ql
+// stay in LDS), the block's hi and lo code rows go to LDS (row stride n + 16
+// bytes: the 16 rows of an MFMA fragment hit distinct banks), and wave w
+// then runs k_router_approx's four int32 products for expert panel w
+// against all 16 tokens, the panel's codes read straight into registers
+// four k-blocks ahead (the 2 x 256 KB of expert codes stay in L2). The
+// approximate logits, formed as k_router_approx forms them, go to LDS, and
+// wave w runs k_router_select's candidate selection for token w from there.
+// Outputs are those of the three launches it replaces, except that the
+// residual codes and the approximate logits never reach memory.
+#define RF_TOK 16
+template <int KB>
+__global__ __launch_bounds__(64 * RF_TOK) void k_router_front(
+    const float *__restrict__ X, int T, int8_t *__restrict__ qh, float *__restrict__ sf,
+    double2 *__restrict__ xinfo, const int8_t *__restrict__ Wh, const int8_t *__restrict__ Wl,
+    const double2 *__restrict__ winfo, int E, int k, int16_t *__restrict__ cand,
+    int32_t *__restrict__ ncand, float *__restrict__ logits, uint32_t *err) {
+    constexpr int n = 64 * KB, AS = n + 16;
+    extern __shared__ __attribute__((aligned(16))) int8_t rf_smem[];
+    int8_t *ah_s = rf_smem;                               // [16][AS]
+    int8_t *al_s = rf_smem + RF_TOK * AS;                 // [16][AS]
+    double *ap_s = (double *)(rf_smem + 2 * RF_TOK * AS);  // [16][E]
+    __shared__ double2 xi_s[RF_TOK];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: MFMA guards branch
+    const int t0 = blockIdx.x * RF_TOK;
+    // ---- codes of token row `wave` ----
+    {
+        const int tl = wave, t = t0 + tl;
+        uint32_t *hs = (uint32_t *)(ah_s + tl * AS), *ls = (uint32_t *)(al_s + tl * AS);
+        double2 inf = make_double2(0.0, 0.0);
+        float scl = 0.0f;
+        bool ok = false;
+        if (t < T) {
+            uint32_t *qg = (uint32_t *)(qh + (int64_t)t * n);
+            ok = router_row_regs<(KB + 3) / 4>(X + (int64_t)t * n, n, lane, err, &inf, &scl,
+                                               [&](int c, uint32_t h, uint32_t l) {
+                                                   qg[c] = h;
+                                                   hs[c] = h;
+                                                   ls[c] = l;
+                                               });
+        }
+        if (!ok) {  // a rejected row (error raised) or past T: zero codes
+            for (int c = lane; c < n / 4; c += 64) hs[c] = ls[c] = 0u;
+            inf = make_double2(0.0, 0.0);
+        }
+        if (lane == 0) {
+            xi_s[tl] = inf;
+            if (ok) {
+                xinfo[t] = inf;
+                if (sf) sf[t] = scl;
+            }
+        }
+    }
+    __syncthreads();
+    // ---- approximate logits of expert panel `wave` ----
+    const int lr = (lane >> 4) * 4, lc = lane & 15;
+    if (16 * wave < E) {  // wave-uniform
+        const int r = lane & 15, kc = lane >> 4;
+        const int8_t *bh = Wh + (int64_t)wave * KB * 1024 + lane * 16;
+        const int8_t *bl = Wl + (int64_t)wave * KB * 1024 + lane * 16;
+        v4i hh = {0, 0, 0, 0}, mid = {0, 0, 0, 0}, ll = {0, 0, 0, 0};
+        constexpr int D = KB < 4 ? KB : 4;  // k-blocks of expert codes in flight
+        v4i b[D][2];                        // [slot][hi, lo]
+#pragma unroll
+        for (int d = 0; d < D; d++) {
+            b[d][0] = *(const v4i *)(bh + (int64_t)d * 1024);
+            b[d][1] = *(const v4i *)(bl + (int64_t)d * 1024);
+        }
+#pragma unroll
+        for (int kb = 0; kb < KB; kb++) {
+            const v4i a_h = *(const v4i *)(ah_s + r * AS + kb * 64 + kc * 16);
+            const v4i a_l = *(const v4i *)(al_s + r * AS + kb * 64 + kc * 16);
+            v4i(&c)[2] = b[kb % D];
+            hh = mfma16x16x64(a_h, c[0], hh);
+            mid = mfma16x16x64(a_h, c[1], mid);
+            mid = mfma16x16x64(a_l, c[0], mid);
+            ll = mfma16x16x64(a_l, c[1], ll);
+            if (kb + D < KB) {
+                c[0] = *(const v4i *)(bh + (int64_t)(kb + D) * 1024);
+                c[1] = *(const v4i *)(bl + (int64_t)(kb + D) * 1024);
+            }
+        }
+        const int e = 16 * wave + lc;
+        const double sw = winfo[e].x;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int tl = lr + q;
+            const double v =
+                (double)hh[q] + (double)mid[q] / 254.0 + (double)ll[q] / 64516.0;
+            ap_s[tl * E + e] = xi_s[tl].x * sw * v;
+        }
+    }
+    __syncthreads();
+    // ---- candidates of token `wave` ----
+    const int t = t0 + wave;
+    if (t < T) {  // wave-uniform
+        const int nc = select_row(ap_s + wave * E, xi_s[wave].x, xi_s[wave].y, winfo, E,
+                                  64 * KB, k, lane, cand + (int64_t)t * E,
+                                  logits + (int64_t)t * E);
+        if (lane == 0) ncand[t] = nc;
+    }
+}
+
+template <int KB>
+static hipError_t launch_router_front(const float *X, int T, int8_t *qh, float *sf,
+                                      double *xinfo, const int8_t *Wh, const int8_t *Wl,
+                                      const double *winfo, int E, int k, int16_t *cand,
+                                      int32_t *ncand, float *logits, uint32_t *err,
+                                      hipStream_t s) {
+    auto kern = k_router_front<KB>;
+    const int lds = 2 * RF_TOK * (64 * KB + 16) + RF_TOK * E * 8;
+    // dynamic LDS above 64 KiB must be enabled per device, once
+    static std::atomic<bool> attr_set[64];  // set once per device; a repeat is harmless
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    if (!attr_set[dev]) {
+        e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                2 * RF_TOK * (64 * KB + 16) + RF_TOK * 256 * 8);
+        if (e != hipSuccess) return e;
+        attr_set[dev] = true;
+    }
+    hipLaunchKernelGGL(kern, dim3((unsigned)((T + RF_TOK - 1) / RF_TOK)), dim3(64 * RF_TOK), lds, s,
+                       X, T,
+                       qh, sf, (double2 *)xinfo, Wh, Wl, (const double2 *)winfo, E, k, cand,
+                       ncand, logits, err);
+    return hipGetLastError();
+}
+
+extern "C" int jtk_router_front(const float *X, int T, int n, int8_t *qh, float *sf,
+                                double *xinfo, const int8_t *Wh, const int8_t *Wl,
+                                const double *winfo, int E, int k, int16_t *cand, int32_t *ncand,
+                                float *logits, uint32_t *err, hipStream_t s) {
+    if (T <= 0 || E <= 0 || E > 256 || E % 16 || k < 1 || k > E || ((uintptr_t)X & 15) ||
+        ((uintptr_t)qh & 3))
+        return (int)hipErrorInvalidValue;
+    switch (n) {
+        case 1024:
+            return (int)launch_router_front<16>(X, T, qh, sf, xinfo, Wh, Wl, winfo, E, k, cand,
+                                                ncand, logits, err, s);
+        case 512:
+            return (int)launch_router_front<8>(X, T, qh, sf, xinfo, Wh, Wl, winfo, E, k, cand,
+                                               ncand, logits, err, s);
+        case 256:
+            return (int)launch_router_front<4>(X, T, qh, sf, xinfo, Wh, Wl, winfo, E, k, cand,
+                                               ncand, logits, err, s);
+        default:
+            return (int)hipErrorInvalidValue;
+    }
 }
 
 // ---- 4. exact logits of the candidates, top-k, softmax ----

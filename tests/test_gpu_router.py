@@ -101,6 +101,22 @@ def test_router_adversarial(jt, orc, torch_cuda, E, k):
     assert list(ids[0]) == list(range(k))
 
 
+@pytest.mark.parametrize("E,k,n", [(64, 8, 256), (256, 8, 1024), (32, 1, 512), (48, 40, 256)],
+                         ids=["E64k8d256", "E256k8d1024", "E32k1d512", "E48k40d256"])
+def test_router_front_adversarial(jt, orc, torch_cuda, E, k, n):
+    """More than 256 tokens with E % 16 == 0 take the one-launch front (codes,
+    int8 bounds and candidates of 16 tokens a block against every expert);
+    333 tokens leave a partial last block, and the adversarial rows (zero,
+    tiny, tied, one-hot) sit in the first block."""
+    T = 333
+    announce(f"router front adversarial E={E} k={k} d={n}")
+    rng = np.random.default_rng(E * 1000 + k * 10 + n)
+    Wgate, X = adversarial(rng, T, n, E)
+    ids, w, lg = route(jt, torch_cuda, X, Wgate, k)
+    check(orc, X, Wgate, k, ids, w, lg)
+    assert list(ids[0]) == list(range(k))
+
+
 @pytest.mark.parametrize("n", [128, 384, 2048])
 def test_router_widths(jt, orc, torch_cuda, n):
     T, E, k = 67, 128, 8
