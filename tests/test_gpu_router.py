@@ -6,7 +6,9 @@ Up to 16 tokens (d % 256 == 0) the layer evaluates the reference's fp64
 sum for every expert in one launch. Otherwise, for E <= 256 and d % 64 == 0
 it bounds every logit with int8 matrix products and evaluates the fp64 sum
 only for the experts the bounds cannot rule out; other shapes take the fp64
-router for every expert. Both must give the reference's ids exactly (including ties, which
+router for every expert. Above 256 tokens with E % 16 == 0 and d in
+{256, 512, 1024}, the codes, bounds and candidate selection run as one
+launch of 16 tokens a block. All of them must give the reference's ids exactly (including ties, which
 go to the lower expert index), the selected logits bit for bit, and the
 softmax weights within rtol 1e-6 (device exp versus glibc's).
 """
