@@ -834,7 +834,15 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ w,
 // adds, and only then loads the next). The sums run in the same order.
 #define CMB_SMAX 8
 // SN: shared rows loaded per thread, S itself when S <= 2, else CMB_SMAX
-// (rows past S - 1 then repeat the last one and are not summed)
+// (rows past S - 1 then repeat the last one and are not summed).
+// The expert and shared rows are read once, so their loads are non-temporal
+// (measured at 4096 tokens, d = 1024, top-8 and two shared rows: 32.3
+// against 34.5 us for the plain loads, 185 MB a launch).
+typedef float cmb_f4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 cmb_ld(const float *p) {
+    const cmb_f4 v = __builtin_nontemporal_load((const cmb_f4 *)p);
+    return make_float4(v.x, v.y, v.z, v.w);
+}
 template <int K, int SN, bool DROP>
 __global__ __launch_bounds__(256) void k_combine_k(const float *__restrict__ w,
                                                    const float *__restrict__ Ye,
@@ -854,14 +862,14 @@ __global__ __launch_bounds__(256) void k_combine_k(const float *__restrict__ w,
 #pragma unroll
     for (int p = 0; p < K; p++) {
         wv[p] = w[q0 + p];
-        yv[p] = *(const float4 *)(Ye + (q0 + p) * n + j);
+        yv[p] = cmb_ld(Ye + (q0 + p) * n + j);
         if (DROP) dr[p] = drop[q0 + p];
     }
     float4 ys[SN > 0 ? SN : 1];
     if (S > 0) {  // kernel-uniform
 #pragma unroll
         for (int s = 0; s < SN; s++)
-            ys[s] = *(const float4 *)(Ys + ((int64_t)min(s, S - 1) * T + t) * n + j);
+            ys[s] = cmb_ld(Ys + ((int64_t)min(s, S - 1) * T + t) * n + j);
     }
     double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
 #pragma unroll
